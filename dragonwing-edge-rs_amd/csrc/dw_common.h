@@ -1,0 +1,188 @@
+// Internal declarations shared by the HIP kernels and the C++ host runtime.
+// Nothing here crosses the C ABI (include/dw_hip.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include <string>
+
+namespace dw {
+
+// ----------------------------------------------------------------------------
+// Error plumbing: every C-ABI function converts a thrown dw::Error into a
+// status code plus a thread-local message.
+// ----------------------------------------------------------------------------
+struct Error {
+  int code;
+  std::string msg;
+};
+[[noreturn]] void fail(int code, const std::string& msg);
+void hip_check(hipError_t e, const char* what);
+#define DW_HIP(call) ::dw::hip_check((call), #call)
+
+// Element types (match DW_DTYPE_* in dw_hip.h).
+enum Dtype : int { F32 = 0, F16 = 1, I8 = 2, U8 = 3, I32 = 4 };
+__host__ __device__ inline int dtype_size(int dt) {
+  return dt == F32 || dt == I32 ? 4 : dt == F16 ? 2 : 1;
+}
+
+// Activations (match DW_ACT_*).
+enum Act : int { ACT_NONE = 0, ACT_RELU = 1, ACT_SILU = 2 };
+
+// Implicit-GEMM epilogues.
+enum Epi : int {
+  EPI_QU8 = 0,      // u8 out: rint((acc+bias)*M[c]) + zp, clamp [0,255], LUT, residual QLinearAdd
+  EPI_QS8_REF = 1,  // s8 out: clamp(acc*scale) then round half away; optional ReLU
+  EPI_I32 = 2,      // raw int32 accumulator
+  EPI_F16 = 3       // f16 out with the CPU runtime's rounding points
+};
+
+// A channel-strided NHWC view: element (pixel p, channel c) lives at
+// base + (p * pix_stride + c_off + c) * esize.  Concat/split outputs are
+// views into one buffer, so no copy kernels are needed for them.
+struct View {
+  void* base = nullptr;
+  int pix_stride = 0;  // elements between consecutive pixels
+  int c_off = 0;       // first channel
+};
+
+// Convolution geometry (NHWC, HWIO weights).
+struct ConvGeom {
+  int n, h, w, cin, cout, kh, kw, sh, sw, pt, pl, ho, wo;
+};
+
+// Arguments of the MFMA implicit-GEMM convolution (int8 and fp16).
+struct IgemmArgs {
+  const uint8_t* x;
+  const uint8_t* wpk;  // packed weights [ksteps][cout_pad][64 bytes]
+  void* y;
+  const void* res;     // residual (EPI_QU8: u8, EPI_F16: f16) or null
+  int n, h, w, cin, cout, kh, kw, sh, sw, pt, pl, ho, wo;
+  int m;        // n*ho*wo output pixels
+  int ksteps;   // ceil(kh*kw*cin*esize / 64)
+  int cout_pad; // rows per k-step in wpk
+  int x_pix_stride, x_c_off;
+  int y_pix_stride, y_c_off;
+  int r_pix_stride, r_c_off;
+  int epi, act;
+  uint32_t xpad;  // padded-input byte pattern (int8 domain after xor)
+  uint32_t xxor;  // 0x80808080 when the input is u8, else 0
+  const int* bias_i;     // EPI_QU8: bias + (128 - x_zp) * sum_k w[k][c]
+  const float* mscale;   // EPI_QU8: per-channel multiplier
+  float tscale;          // EPI_QS8_REF: per-tensor requant scale
+  int y_zp;
+  const uint8_t* lut;    // EPI_QU8 activation table or null
+  float ra, rb;          // residual add: rint((a-za)*ra + (b-zb)*rb) + zy
+  int za, zb, zy;
+  const uint16_t* bias_h;  // EPI_F16 bias (f16 bits) or null
+  int tiles_p;             // number of pixel tiles (grid remap)
+};
+
+// Arguments of the direct convolution with the reference accumulation order.
+struct DirectArgs {
+  const void* x;
+  const float* wf;  // HWIO weights as f32 (exact copies of the f16 weights)
+  void* y;
+  int n, h, w, cin, cout, kh, kw, sh, sw, pt, pl, ho, wo;
+  int m;
+  int x_pix_stride, x_c_off, y_pix_stride, y_c_off;
+  int in_kind;   // 0 f32, 1 f16, 2 u8 dequantized to f16 ((q-zp)*scale)
+  int out_kind;  // 0 f32, 1 f16, 2 u8 (QuantizeLinear of the f16 result)
+  int act;
+  const float* bias_f;     // f32 bias (out f32)
+  const uint16_t* bias_h;  // f16 bias (out f16/u8)
+  float in_scale; int in_zp;
+  float out_scale; int out_zp;
+  const uint8_t* lut;      // out u8: optional table applied after quantization
+  int groups_oc;           // number of 8-wide output-channel groups
+};
+
+// Depthwise convolution (channel multiplier 1).
+struct DwArgs {
+  const void* x;
+  const void* wt;   // [kh][kw][c], same element type as x
+  const void* bias; // [c] or null
+  void* y;
+  int n, h, w, c, kh, kw, sh, sw, pt, pl, ho, wo;
+  int act;
+  int x_pix_stride, x_c_off, y_pix_stride, y_c_off;
+};
+
+// ---------------------------------------------------------------------------
+// Kernel launchers (defined in the .hip files).  All enqueue on `st`.
+// ---------------------------------------------------------------------------
+// Packs HWIO weights (esize 1 or 2) into [ksteps][cout_pad][64B] rows.
+void launch_pack_weights(hipStream_t st, const void* w_hwio, void* wpk, int K, int cout,
+                         int cout_pad, int ksteps, int esize);
+// bias_out[c] = (bias ? bias[c] : 0) + corr * sum_k w[k][c]   (int64 checked on host)
+void launch_qconv_bias(hipStream_t st, const int8_t* w_hwio, const int* bias, int* bias_out, int K,
+                       int cout, int corr);
+// Implicit-GEMM convolution; selects a tile shape for the problem.
+void launch_igemm(hipStream_t st, const IgemmArgs& a, int esize);
+// Returns the tile name chosen for a problem (for launch descriptions).
+const char* igemm_tile_name(const IgemmArgs& a, int esize);
+// Channel-tile width used for `cout` output channels; packed weights must
+// hold a multiple of it (cout_pad).
+int igemm_channel_tile(int cout);
+
+void launch_direct_conv(hipStream_t st, const DirectArgs& a);
+void launch_dwconv(hipStream_t st, const DwArgs& a, int dtype);
+
+// Elementwise glue (count elements, contiguous).
+enum EwOp : int {
+  EW_RELU = 0, EW_ADD, EW_MUL, EW_SIGMOID, EW_SILU, EW_BIAS_ADD,
+  EW_REQUANT_I32_I8, EW_QUANT_F32_I8, EW_DEQUANT_I8_F32, EW_ADD_I8, EW_RELU_I8,
+  EW_QUANT_LINEAR_F16_U8, EW_DEQUANT_LINEAR_U8_F16, EW_QADD_U8, EW_LUT_U8,
+  EW_F32_TO_F16, EW_F16_TO_F32
+};
+struct EwArgs {
+  int op;
+  int dtype;  // F32 or F16 for float ops
+  const void* a;
+  const void* b;
+  void* y;
+  size_t count;
+  int c;  // bias channels
+  float s0, s1, s2;
+  int z0, z1, z2;
+  const uint8_t* lut;
+};
+void launch_elementwise(hipStream_t st, const EwArgs& a);
+
+// Strided-view versions used by the graph runtime (pixels x channels).
+struct Ew2Args {
+  int op;
+  int dtype;
+  View a, b, y;
+  int pixels, channels;
+  float s0, s1, s2;
+  int z0, z1, z2;
+  const uint8_t* lut;
+};
+void launch_elementwise2d(hipStream_t st, const Ew2Args& a);
+
+// Max pool, padded windows, NHWC views.  dtype F32/F16/U8/I8.
+struct PoolArgs {
+  View x, y;
+  int n, h, w, c, kh, kw, sh, sw, pt, pl, ho, wo;
+};
+void launch_maxpool(hipStream_t st, const PoolArgs& a, int dtype);
+// SPPF cascade: y1 = pool(x), y2 = pool(y1), y3 = pool(y2) for a k x k,
+// stride 1, pad k/2 pool, in one launch (windows of k, 2k-1, 3k-2).
+void launch_maxpool_cascade3(hipStream_t st, const PoolArgs& a, View y2, View y3, int dtype);
+// Nearest resize with the reference's index rule.
+struct ResizeArgs {
+  View x, y;
+  int n, h, w, c, ho, wo;
+};
+void launch_resize_nearest(hipStream_t st, const ResizeArgs& a, int dtype);
+// Channel copy between views (concat/split when aliasing is impossible).
+void launch_copy_channels(hipStream_t st, View src, View dst, int pixels, int channels, int esize);
+// Per-tensor min/max of an f32 view (calibration).  out: [min, max] floats,
+// must be initialised to (+inf, -inf) by the caller (done by launch_minmax_init).
+void launch_minmax_init(hipStream_t st, float* out);
+void launch_minmax(hipStream_t st, View x, int pixels, int channels, float* out);
+
+}  // namespace dw

@@ -1,0 +1,730 @@
+// Graph IR and the compiler passes of dragonwing-onnx, restated in C++:
+//   fold_batchnorm          crates/dragonwing-onnx/src/graph.rs:521-690
+//   convert_nchw_to_nhwc    crates/dragonwing-onnx/src/graph.rs:248-290
+//   apply_fusion_passes     crates/dragonwing-onnx/src/fusion.rs:126-190 (SiLU)
+//   convert_to_f16          crates/dragonwing-onnx/src/runtime.rs:800-811
+//   quantize_qdq            QDQ-folded u8 graph (QLinearConv etc.); the
+//                           reference's quantizer (quantize.rs:73-368) emits
+//                           symmetric s8 with one averaged requant scale,
+//                           this pass emits the ONNX per-channel form.
+// Host-only code: no device work happens here.
+#include "graph.h"
+
+#include <math.h>
+#include <string.h>
+
+#include <algorithm>
+#include <exception>
+#include <functional>
+#include <numeric>
+#include <set>
+#include <sstream>
+
+#include "backend.h"
+
+namespace dw {
+
+TensorInfo& GraphIR::tensor(const std::string& name) {
+  auto it = t.find(name);
+  if (it == t.end()) fail(DW_ERR_RUNTIME, "unknown tensor '" + name + "'");
+  return it->second;
+}
+const TensorInfo& GraphIR::tensor(const std::string& name) const {
+  auto it = t.find(name);
+  if (it == t.end()) fail(DW_ERR_RUNTIME, "unknown tensor '" + name + "'");
+  return it->second;
+}
+std::vector<int> GraphIR::consumers(const std::string& name) const {
+  std::vector<int> r;
+  for (size_t i = 0; i < ops.size(); ++i)
+    for (auto& in : ops[i].in)
+      if (in == name) {
+        r.push_back((int)i);
+        break;
+      }
+  return r;
+}
+int GraphIR::producer(const std::string& name) const {
+  for (size_t i = 0; i < ops.size(); ++i)
+    for (auto& o : ops[i].out)
+      if (o == name) return (int)i;
+  return -1;
+}
+bool GraphIR::is_output(const std::string& name) const {
+  return std::find(outputs.begin(), outputs.end(), name) != outputs.end();
+}
+
+void build_silu_lut(uint8_t lut[256], float sx, int zx, float sy, int zy) {
+  for (int q = 0; q < 256; ++q) {
+    const float v = (float)(q - zx) * sx;
+    const float s = 1.0f / (1.0f + expf(-v));
+    const float a = v * s;
+    float r = nearbyintf(a / sy) + (float)zy;
+    r = r < 0.0f ? 0.0f : (r > 255.0f ? 255.0f : r);
+    lut[q] = (uint8_t)r;
+  }
+}
+
+namespace {
+
+std::vector<float> as_f32(const TensorInfo& ti) {
+  if (ti.dtype != DW_DTYPE_F32) fail(DW_ERR_UNSUPPORTED, "expected an f32 initializer");
+  std::vector<float> v(ti.data.size() / 4);
+  memcpy(v.data(), ti.data.data(), v.size() * 4);
+  return v;
+}
+void set_f32(TensorInfo& ti, const std::vector<float>& v) {
+  ti.data.resize(v.size() * 4);
+  memcpy(ti.data.data(), v.data(), ti.data.size());
+  ti.dtype = DW_DTYPE_F32;
+  ti.is_init = true;
+}
+
+uint16_t f16_from_f32(float v) { return f16_bits_from_f32(v); }
+
+}  // namespace
+
+// F16::from_f32 (dtype.rs:164-222): IEEE round to nearest even.
+uint16_t f16_bits_from_f32(float v) {
+  uint32_t bits;
+  memcpy(&bits, &v, 4);
+  const uint32_t sign = (bits >> 16) & 0x8000u;
+  const int32_t e = (int32_t)((bits >> 23) & 0xFF);
+  const uint32_t m = bits & 0x7FFFFFu;
+  if (e == 255) return (uint16_t)(sign | (m ? 0x7E00u | std::min<uint32_t>(m >> 13, 0x1FF) : 0x7C00u));
+  const int32_t ne = e - 112;
+  if (ne >= 31) return (uint16_t)(sign | 0x7C00u);
+  if (ne <= 0) {
+    if (ne < -10) return (uint16_t)sign;
+    const int32_t sh = 1 - ne;
+    const uint32_t mh = m | 0x800000u;
+    const uint32_t q = mh >> (13 + sh);
+    const uint32_t rb = (mh >> (12 + sh)) & 1u;
+    const uint32_t st = (mh & ((1u << (12 + sh)) - 1u)) != 0;
+    return (uint16_t)(sign | (q + (rb & (st | (q & 1u)))));
+  }
+  const uint32_t q = m >> 13;
+  const uint32_t rb = (m >> 12) & 1u;
+  const uint32_t st = (m & 0xFFFu) != 0;
+  const uint32_t r = q + (rb & (st | (q & 1u)));
+  if (r >= 0x400u) {
+    if (ne + 1 >= 31) return (uint16_t)(sign | 0x7C00u);
+    return (uint16_t)(sign | ((uint32_t)(ne + 1) << 10));
+  }
+  return (uint16_t)(sign | ((uint32_t)ne << 10) | r);
+}
+
+namespace {
+
+std::string jesc(const std::string& s) {
+  std::string o;
+  for (char c : s) {
+    if (c == '"' || c == '\\') o += '\\';
+    o += c;
+  }
+  return o;
+}
+
+std::string fstr(float f) {
+  char b[64];
+  snprintf(b, sizeof b, "%.9g", (double)f);
+  return b;
+}
+
+// --------------------------------------------------------------------------
+// fold_batchnorm (graph.rs:521-690): Conv -> BatchNormalization(scale, B,
+// mean, var) with the conv output used only by the BN.  In f64:
+//   w' = (f32)(w * g / sqrt(var + eps)),  b' = (f32)((b - mean) * sf + beta)
+// The conv takes the BN's output name; a bias "<W>_bias_folded" is added
+// when the conv had none (graph.rs:630-664).
+// --------------------------------------------------------------------------
+int fold_batchnorm(GraphIR& g) {
+  int folded = 0;
+  for (size_t i = 0; i < g.ops.size(); ++i) {
+    OpNode& bn = g.ops[i];
+    if (bn.type != "BatchNormalization") continue;
+    const int pi = g.producer(bn.in[0]);
+    if (pi < 0) continue;
+    OpNode& conv = g.ops[pi];
+    if (conv.type != "Conv" || g.consumers(bn.in[0]).size() != 1) continue;
+    TensorInfo& W = g.tensor(conv.in[1]);
+    if (!W.is_init || W.dims.size() != 4) continue;
+    const auto gam = as_f32(g.tensor(bn.in[1]));
+    const auto beta = as_f32(g.tensor(bn.in[2]));
+    const auto mean = as_f32(g.tensor(bn.in[3]));
+    const auto var = as_f32(g.tensor(bn.in[4]));
+    const float eps = bn.p.epsilon;
+    auto w = as_f32(W);
+    const size_t co = (size_t)W.dims[0];
+    const size_t per = w.size() / co;
+    std::vector<float> oldb;
+    const bool has_b = conv.in.size() > 2 && !conv.in[2].empty();
+    if (has_b) oldb = as_f32(g.tensor(conv.in[2]));
+    std::vector<float> nb(co);
+    for (size_t c = 0; c < co; ++c) {
+      const double std_inv = 1.0 / sqrt((double)var[c] + (double)eps);
+      const double sf = (double)gam[c] * std_inv;
+      for (size_t k = 0; k < per; ++k) w[c * per + k] = (float)((double)w[c * per + k] * sf);
+      const double ob = has_b ? (double)oldb[c] : 0.0;
+      nb[c] = (float)((ob - (double)mean[c]) * sf + (double)beta[c]);
+    }
+    set_f32(W, w);
+    std::string bname = has_b ? conv.in[2] : conv.in[1] + "_bias_folded";
+    TensorInfo& B = g.t[bname];
+    B.dims = {(int64_t)co};
+    set_f32(B, nb);
+    if (has_b)
+      conv.in[2] = bname;
+    else
+      conv.in.resize(3), conv.in[2] = bname;
+    g.t.erase(conv.out[0]);
+    conv.out[0] = bn.out[0];
+    g.ops.erase(g.ops.begin() + i);
+    --i;
+    ++folded;
+  }
+  return folded;
+}
+
+// --------------------------------------------------------------------------
+// convert_nchw_to_nhwc (graph.rs:248-290): conv weights [Co,Ci,kh,kw] ->
+// [kh,kw,Ci,Co] (perm [2,3,1,0]); every other 4-D shape [N,C,H,W] ->
+// [N,H,W,C].  The reference leaves Concat/Split axes in NCHW numbering; here
+// they are renumbered (1 -> 3, 2 -> 1, 3 -> 2) so channel concats stay
+// channel concats on NHWC data.
+// --------------------------------------------------------------------------
+void convert_nchw_to_nhwc(GraphIR& g) {
+  std::set<std::string> weights;
+  for (auto& op : g.ops)
+    if (op.type == "Conv" && op.in.size() >= 2 && g.has(op.in[1]) && g.tensor(op.in[1]).is_init)
+      weights.insert(op.in[1]);
+  for (auto& wn : weights) {
+    TensorInfo& W = g.tensor(wn);
+    if (W.dims.size() != 4) continue;
+    const int64_t co = W.dims[0], ci = W.dims[1], kh = W.dims[2], kw = W.dims[3];
+    const int es = dtype_size(W.dtype);
+    std::vector<uint8_t> out(W.data.size());
+    for (int64_t o = 0; o < co; ++o)
+      for (int64_t i = 0; i < ci; ++i)
+        for (int64_t y = 0; y < kh; ++y)
+          for (int64_t x = 0; x < kw; ++x) {
+            const int64_t src = ((o * ci + i) * kh + y) * kw + x;
+            const int64_t dst = ((y * kw + x) * ci + i) * co + o;
+            memcpy(&out[dst * es], &W.data[src * es], es);
+          }
+    W.data.swap(out);
+    W.dims = {kh, kw, ci, co};
+  }
+  for (auto& kv : g.t) {
+    if (weights.count(kv.first) || kv.second.dims.size() != 4) continue;
+    auto& d = kv.second.dims;
+    d = {d[0], d[2], d[3], d[1]};
+  }
+  static const int remap[4] = {0, 3, 1, 2};
+  for (auto& op : g.ops)
+    if ((op.p.kind == DW_OP_CONCAT || op.p.kind == DW_OP_SPLIT) && op.p.axis >= 0 && op.p.axis < 4)
+      op.p.axis = remap[op.p.axis];
+}
+
+// --------------------------------------------------------------------------
+// apply_fusion_passes, SiLU pattern (fusion.rs:126-190): Sigmoid(x) = s and
+// Mul(x, s) = y (either operand order), s used only by that Mul, become
+// CompiledOp{op_type "SiLU", params None, inputs [x], outputs [y]}.
+// --------------------------------------------------------------------------
+int fuse_silu(GraphIR& g) {
+  int fused = 0;
+  for (size_t i = 0; i < g.ops.size(); ++i) {
+    if (g.ops[i].type != "Sigmoid") continue;
+    const std::string x = g.ops[i].in[0], s = g.ops[i].out[0];
+    auto cs = g.consumers(s);
+    if (cs.size() != 1 || g.is_output(s)) continue;
+    OpNode& mul = g.ops[cs[0]];
+    if (mul.type != "Mul" || mul.in.size() != 2) continue;
+    if (!((mul.in[0] == x && mul.in[1] == s) || (mul.in[0] == s && mul.in[1] == x))) continue;
+    OpNode silu;
+    silu.name = mul.name.empty() ? g.ops[i].name + "_silu" : mul.name;
+    silu.type = "SiLU";
+    silu.in = {x};
+    silu.out = mul.out;
+    silu.p.kind = DW_OP_NONE;
+    const int mi = cs[0];
+    g.ops[mi] = silu;
+    g.t.erase(s);
+    g.ops.erase(g.ops.begin() + i);
+    --i;
+    ++fused;
+  }
+  return fused;
+}
+
+void convert_to_f16(GraphIR& g) {
+  if (g.dtype != DW_GRAPH_F32) fail(DW_ERR_RUNTIME, "convert_to_f16 needs an F32 graph");
+  for (auto& kv : g.t) {
+    TensorInfo& ti = kv.second;
+    if (ti.dtype != DW_DTYPE_F32) continue;
+    if (ti.is_init) {
+      std::vector<uint8_t> out(ti.data.size() / 2);
+      for (size_t i = 0; i < ti.data.size() / 4; ++i) {
+        float f;
+        memcpy(&f, &ti.data[i * 4], 4);
+        const uint16_t h = f16_from_f32(f);
+        memcpy(&out[i * 2], &h, 2);
+      }
+      ti.data.swap(out);
+    }
+    ti.dtype = DW_DTYPE_F16;
+  }
+  g.dtype = DW_GRAPH_F16;
+}
+
+// --------------------------------------------------------------------------
+// QDQ quantizer.  Input: an F32 NHWC graph with calibrated ranges on its
+// activations.  Output (DW_GRAPH_QU8):
+//  * activations u8 with zero point 128 and the reference's symmetric
+//    calibration scale absmax / 127 (QuantScale::from_range,
+//    crates/dragonwing-core/src/quantization.rs:85-89);
+//  * tensors joined by Concat / Split / MaxPool / Resize share one scale
+//    (these ops then move bytes only);
+//  * Conv -> QLinearConv with s8 weights quantized per output channel
+//    (PerChannelScale::from_weights + quantize_weights_per_channel,
+//    quantize.rs:344-368: q = clamp(round(w * (1/s)))), int32 bias
+//    rint(b / (x_scale * w_scale[c])), and M[c] = x_scale*w_scale[c]/y_scale;
+//  * SiLU after a conv -> QLinearLUT on the conv's u8 pre-activation;
+//  * Add -> QLinearAdd;
+//  * convs named in keep_f16 stay fp16 (f16 weights): a u8 input gets a
+//    DequantizeLinear, an f16 result consumed by u8 ops gets a
+//    QuantizeLinear (then the SiLU table).
+// --------------------------------------------------------------------------
+struct UF {
+  std::map<std::string, std::string> parent;
+  std::string find(const std::string& a) {
+    auto it = parent.find(a);
+    if (it == parent.end() || it->second == a) return a;
+    std::string r = find(it->second);
+    parent[a] = r;
+    return r;
+  }
+  void join(const std::string& a, const std::string& b) {
+    std::string ra = find(a), rb = find(b);
+    if (ra != rb) parent[ra] = rb;
+  }
+};
+
+float sym_scale(float mn, float mx) {
+  const float a = fmaxf(fabsf(mn), fabsf(mx));
+  return a > 0.0f ? a / 127.0f : 1.0f;
+}
+
+void quantize_qdq(GraphIR& g, const std::set<std::string>& keep_f16) {
+  if (g.dtype != DW_GRAPH_F32) fail(DW_ERR_RUNTIME, "quantize_qdq needs an F32 graph");
+  fuse_silu(g);
+  // --- shared-scale groups
+  UF uf;
+  for (auto& op : g.ops) {
+    if (op.type == "Concat" || op.type == "Split" || op.type == "MaxPool" || op.type == "Resize") {
+      for (auto& i : op.in)
+        if (!g.tensor(i).is_init)
+          for (auto& o : op.out) uf.join(i, o);
+    }
+  }
+  // Tensors that stay f16: graph inputs, outputs of kept convs (and of f16
+  // concats of those).
+  std::set<std::string> f16t(g.inputs.begin(), g.inputs.end());
+  for (auto& in : g.inputs) g.tensor(in).dtype = DW_DTYPE_F16;
+  for (auto& op : g.ops) {
+    if (op.type == "Conv" && keep_f16.count(op.name)) f16t.insert(op.out[0]);
+    if (op.type == "Concat") {
+      bool all = true;
+      for (auto& i : op.in) all = all && f16t.count(i);
+      if (all) f16t.insert(op.out[0]);
+    }
+  }
+  // group ranges
+  std::map<std::string, std::pair<float, float>> grange;
+  for (auto& kv : g.t) {
+    const TensorInfo& ti = kv.second;
+    if (ti.is_init || !ti.has_range) continue;
+    const std::string r = uf.find(kv.first);
+    auto it = grange.find(r);
+    if (it == grange.end())
+      grange[r] = {ti.rmin, ti.rmax};
+    else
+      it->second = {std::min(it->second.first, ti.rmin), std::max(it->second.second, ti.rmax)};
+  }
+  auto qscale = [&](const std::string& name) -> float {
+    auto it = grange.find(uf.find(name));
+    if (it == grange.end()) fail(DW_ERR_RUNTIME, "no calibration range for '" + name + "'");
+    return sym_scale(it->second.first, it->second.second);
+  };
+  auto make_u8 = [&](const std::string& name) {
+    TensorInfo& ti = g.tensor(name);
+    ti.dtype = DW_DTYPE_U8;
+    ti.has_q = true;
+    ti.scale = qscale(name);
+    ti.zp = 128;
+  };
+
+  std::vector<OpNode> out;
+  std::map<std::string, std::string> as_u8, as_f16;  // converted twins
+  auto add_tensor_like = [&](const std::string& src, const std::string& name, int dtype) {
+    TensorInfo ti;
+    ti.dims = g.tensor(src).dims;
+    ti.dtype = dtype;
+    g.t[name] = ti;
+  };
+  // u8 view of tensor x (x is f16): QuantizeLinear with x's own range.
+  auto need_u8 = [&](const std::string& x) -> std::string {
+    if (!f16t.count(x)) return x;
+    auto it = as_u8.find(x);
+    if (it != as_u8.end()) return it->second;
+    const std::string q = x + "_q";
+    add_tensor_like(x, q, DW_DTYPE_U8);
+    TensorInfo& tq = g.tensor(q);
+    tq.has_q = true;
+    tq.scale = qscale(x);
+    tq.zp = 128;
+    OpNode op;
+    op.name = x + "_quantize";
+    op.type = "QuantizeLinear";
+    op.in = {x};
+    op.out = {q};
+    op.p.kind = DW_OP_QUANTIZE_LINEAR;
+    out.push_back(op);
+    as_u8[x] = q;
+    return q;
+  };
+  auto need_f16 = [&](const std::string& x) -> std::string {
+    if (f16t.count(x)) return x;
+    auto it = as_f16.find(x);
+    if (it != as_f16.end()) return it->second;
+    const std::string d = x + "_dq";
+    add_tensor_like(x, d, DW_DTYPE_F16);
+    OpNode op;
+    op.name = x + "_dequantize";
+    op.type = "DequantizeLinear";
+    op.in = {x};
+    op.out = {d};
+    op.p.kind = DW_OP_DEQUANTIZE_LINEAR;
+    out.push_back(op);
+    as_f16[x] = d;
+    return d;
+  };
+
+  for (size_t oi = 0; oi < g.ops.size(); ++oi) {
+    OpNode op = g.ops[oi];
+    if (op.type == "Conv") {
+      TensorInfo& W = g.tensor(op.in[1]);
+      if (W.dims.size() != 4) fail(DW_ERR_UNSUPPORTED, "quantize: conv weight must be 4-D (HWIO)");
+      const bool keep = keep_f16.count(op.name) != 0;
+      if (keep) {
+        op.in[0] = need_f16(op.in[0]);
+        // weights / bias -> f16
+        for (size_t k = 1; k < op.in.size(); ++k) {
+          if (op.in[k].empty()) continue;
+          TensorInfo& ti = g.tensor(op.in[k]);
+          if (ti.dtype == DW_DTYPE_F32) {
+            std::vector<uint8_t> h(ti.data.size() / 2);
+            for (size_t e = 0; e < ti.data.size() / 4; ++e) {
+              float f;
+              memcpy(&f, &ti.data[e * 4], 4);
+              const uint16_t b = f16_from_f32(f);
+              memcpy(&h[e * 2], &b, 2);
+            }
+            ti.data.swap(h);
+            ti.dtype = DW_DTYPE_F16;
+          }
+        }
+        g.tensor(op.out[0]).dtype = DW_DTYPE_F16;
+        out.push_back(op);
+        continue;
+      }
+      const std::string x = need_u8(op.in[0]);
+      const TensorInfo& X = g.tensor(x);
+      const int64_t kh = W.dims[0], kw = W.dims[1], ci = W.dims[2], co = W.dims[3];
+      auto w = as_f32(W);
+      std::vector<float> ws(co);
+      std::vector<int8_t> wq(w.size());
+      for (int64_t c = 0; c < co; ++c) {
+        float am = 0.0f;
+        for (int64_t k = 0; k < kh * kw * ci; ++k) am = fmaxf(am, fabsf(w[k * co + c]));
+        ws[c] = am > 0.0f ? am / 127.0f : 1.0f;
+        const float inv = 1.0f / ws[c];
+        for (int64_t k = 0; k < kh * kw * ci; ++k) {
+          float r = roundf(w[k * co + c] * inv);
+          r = r < -128.0f ? -128.0f : (r > 127.0f ? 127.0f : r);
+          wq[k * co + c] = (int8_t)r;
+        }
+      }
+      W.data.assign((const uint8_t*)wq.data(), (const uint8_t*)wq.data() + wq.size());
+      W.dtype = DW_DTYPE_I8;
+      W.ch_scales = ws;
+      if (op.in.size() > 2 && !op.in[2].empty()) {
+        TensorInfo& Bt = g.tensor(op.in[2]);
+        auto b = as_f32(Bt);
+        std::vector<int32_t> bq(co);
+        for (int64_t c = 0; c < co; ++c) {
+          const double s = (double)(X.scale * ws[c]);
+          double r = nearbyint((double)b[c] / s);
+          r = std::min(std::max(r, -2147483648.0), 2147483647.0);
+          bq[c] = (int32_t)r;
+        }
+        Bt.data.assign((const uint8_t*)bq.data(), (const uint8_t*)bq.data() + bq.size() * 4);
+        Bt.dtype = DW_DTYPE_I32;
+      }
+      op.type = "QLinearConv";
+      op.p.kind = DW_OP_QLINEAR_CONV;
+      op.in[0] = x;
+      make_u8(op.out[0]);
+      out.push_back(op);
+      continue;
+    }
+    if (op.type == "SiLU") {
+      const std::string x = need_u8(op.in[0]);
+      make_u8(op.out[0]);
+      op.type = "QLinearLUT";
+      op.p.kind = DW_OP_QLINEAR_LUT;
+      op.p.act = DW_ACT_SILU;
+      op.in = {x};
+      out.push_back(op);
+      continue;
+    }
+    if (op.type == "Add") {
+      op.in = {need_u8(op.in[0]), need_u8(op.in[1])};
+      make_u8(op.out[0]);
+      op.type = "QLinearAdd";
+      op.p.kind = DW_OP_QLINEAR_ADD;
+      out.push_back(op);
+      continue;
+    }
+    if (op.type == "Concat" && f16t.count(op.out[0])) {
+      g.tensor(op.out[0]).dtype = DW_DTYPE_F16;
+      out.push_back(op);  // f16 concat of fp16 results
+      continue;
+    }
+    if (op.type == "Concat" || op.type == "Split" || op.type == "MaxPool" || op.type == "Resize") {
+      for (auto& i : op.in)
+        if (!g.tensor(i).is_init) i = need_u8(i);
+      for (auto& o : op.out) make_u8(o);
+      out.push_back(op);
+      continue;
+    }
+    fail(DW_ERR_UNSUPPORTED, "quantize_qdq: op type '" + op.type + "' is not supported");
+  }
+  g.ops.swap(out);
+  // graph outputs that ended up u8 stay u8 (the caller dequantizes);
+  g.dtype = DW_GRAPH_QU8;
+}
+
+std::string to_json(const GraphIR& g) {
+  std::ostringstream o;
+  o << "{\"dtype\":" << g.dtype << ",\"inputs\":[";
+  for (size_t i = 0; i < g.inputs.size(); ++i) o << (i ? "," : "") << '"' << jesc(g.inputs[i]) << '"';
+  o << "],\"outputs\":[";
+  for (size_t i = 0; i < g.outputs.size(); ++i) o << (i ? "," : "") << '"' << jesc(g.outputs[i]) << '"';
+  o << "],\"tensors\":{";
+  bool first = true;
+  for (auto& kv : g.t) {
+    const TensorInfo& ti = kv.second;
+    o << (first ? "" : ",") << '"' << jesc(kv.first) << "\":{\"dims\":[";
+    first = false;
+    for (size_t i = 0; i < ti.dims.size(); ++i) o << (i ? "," : "") << ti.dims[i];
+    o << "],\"dtype\":" << ti.dtype << ",\"init\":" << (ti.is_init ? "true" : "false");
+    if (ti.has_q) o << ",\"scale\":" << fstr(ti.scale) << ",\"zp\":" << ti.zp;
+    if (!ti.ch_scales.empty()) {
+      o << ",\"ch_scales\":[";
+      for (size_t i = 0; i < ti.ch_scales.size(); ++i) o << (i ? "," : "") << fstr(ti.ch_scales[i]);
+      o << "]";
+    }
+    if (ti.has_range) o << ",\"range\":[" << fstr(ti.rmin) << "," << fstr(ti.rmax) << "]";
+    o << "}";
+  }
+  o << "},\"ops\":[";
+  for (size_t i = 0; i < g.ops.size(); ++i) {
+    const OpNode& op = g.ops[i];
+    const dw_op_params& p = op.p;
+    o << (i ? "," : "") << "{\"name\":\"" << jesc(op.name) << "\",\"type\":\"" << jesc(op.type)
+      << "\",\"inputs\":[";
+    for (size_t k = 0; k < op.in.size(); ++k) o << (k ? "," : "") << '"' << jesc(op.in[k]) << '"';
+    o << "],\"outputs\":[";
+    for (size_t k = 0; k < op.out.size(); ++k) o << (k ? "," : "") << '"' << jesc(op.out[k]) << '"';
+    o << "],\"kind\":" << p.kind << ",\"kernel_shape\":[" << p.kernel_shape[0] << ","
+      << p.kernel_shape[1] << "],\"strides\":[" << p.strides[0] << "," << p.strides[1]
+      << "],\"pads\":[" << p.pads[0] << "," << p.pads[1] << "," << p.pads[2] << "," << p.pads[3]
+      << "],\"dilations\":[" << p.dilations[0] << "," << p.dilations[1] << "],\"group\":" << p.group
+      << ",\"axis\":" << p.axis << ",\"split_sizes\":[";
+    for (int k = 0; k < p.num_splits && k < 8; ++k) o << (k ? "," : "") << p.split_sizes[k];
+    o << "],\"out_h\":" << p.out_h << ",\"out_w\":" << p.out_w << ",\"mode_nearest\":" << p.mode_nearest
+      << ",\"scale\":" << fstr(p.scale) << ",\"scale_a_over_out\":" << fstr(p.scale_a_over_out)
+      << ",\"scale_b_over_out\":" << fstr(p.scale_b_over_out) << ",\"has_relu\":" << p.has_relu
+      << ",\"epsilon\":" << fstr(p.epsilon) << ",\"act\":" << p.act << "}";
+  }
+  o << "]}";
+  return o.str();
+}
+
+}  // namespace
+}  // namespace dw
+
+#define API_BEGIN try {
+#define API_END                           \
+  }                                       \
+  catch (const dw::Error& e) {            \
+    dw::set_last_error(e.msg);            \
+    return e.code;                        \
+  }                                       \
+  catch (const std::exception& e) {       \
+    dw::set_last_error(e.what());         \
+    return DW_ERR_BACKEND;                \
+  }                                       \
+  return DW_OK;
+
+static dw::GraphIR& G(dw_graph* g) {
+  if (!g) dw::fail(DW_ERR_INVALID, "null graph");
+  g->g.json.clear();
+  return g->g;
+}
+
+extern "C" {
+
+int dw_graph_create(int dtype, dw_graph** out) {
+  API_BEGIN
+  if (!out) dw::fail(DW_ERR_INVALID, "null out");
+  if (dtype != DW_GRAPH_F32 && dtype != DW_GRAPH_F16 && dtype != DW_GRAPH_QU8)
+    dw::fail(DW_ERR_UNSUPPORTED, "graph dtype");
+  dw_graph* g = new dw_graph();
+  g->g.dtype = dtype;
+  *out = g;
+  API_END
+}
+
+void dw_graph_destroy(dw_graph* g) { delete g; }
+
+int dw_graph_add_tensor(dw_graph* gh, const char* name, const int64_t* dims, int rank, int dtype) {
+  API_BEGIN
+  dw::GraphIR& g = G(gh);
+  if (!name || !*name) dw::fail(DW_ERR_INVALID, "tensor needs a name");
+  if (rank < 0 || rank > 4) dw::fail(DW_ERR_UNSUPPORTED, "rank > 4");
+  if (dtype < 0 || dtype > DW_DTYPE_I32) dw::fail(DW_ERR_INVALID, "tensor dtype");
+  dw::TensorInfo ti;
+  for (int i = 0; i < rank; ++i) {
+    if (dims[i] <= 0) dw::fail(DW_ERR_INVALID, std::string("non-positive dim in ") + name);
+    ti.dims.push_back(dims[i]);
+  }
+  ti.dtype = dtype;
+  g.t[name] = ti;
+  API_END
+}
+
+int dw_graph_set_initializer(dw_graph* gh, const char* name, const void* data, size_t len) {
+  API_BEGIN
+  dw::GraphIR& g = G(gh);
+  dw::TensorInfo& ti = g.tensor(name);
+  const size_t want = (size_t)ti.numel() * dw::dtype_size(ti.dtype);
+  if (len != want)
+    dw::fail(DW_ERR_INVALID, std::string("initializer size mismatch for ") + name + ": expected " +
+                                 std::to_string(want) + ", got " + std::to_string(len));
+  ti.data.assign((const uint8_t*)data, (const uint8_t*)data + len);
+  ti.is_init = true;
+  API_END
+}
+
+int dw_graph_add_op(dw_graph* gh, const char* name, const char* op_type, const char* const* inputs,
+                    int num_inputs, const char* const* outputs, int num_outputs,
+                    const dw_op_params* params) {
+  API_BEGIN
+  dw::GraphIR& g = G(gh);
+  if (!op_type) dw::fail(DW_ERR_INVALID, "null op_type");
+  dw::OpNode op;
+  op.name = name ? name : "";
+  op.type = op_type;
+  for (int i = 0; i < num_inputs; ++i) {
+    std::string s = inputs[i] ? inputs[i] : "";
+    if (!s.empty() && !g.has(s)) dw::fail(DW_ERR_RUNTIME, "op " + op.name + ": unknown input " + s);
+    op.in.push_back(s);
+  }
+  for (int i = 0; i < num_outputs; ++i) {
+    std::string s = outputs[i] ? outputs[i] : "";
+    if (!g.has(s)) dw::fail(DW_ERR_RUNTIME, "op " + op.name + ": undeclared output " + s);
+    op.out.push_back(s);
+  }
+  if (params) op.p = *params;
+  g.ops.push_back(op);
+  API_END
+}
+
+int dw_graph_set_io(dw_graph* gh, const char* const* inputs, int num_inputs, const char* const* outputs,
+                    int num_outputs) {
+  API_BEGIN
+  dw::GraphIR& g = G(gh);
+  g.inputs.clear();
+  g.outputs.clear();
+  for (int i = 0; i < num_inputs; ++i) {
+    g.tensor(inputs[i]);
+    g.inputs.push_back(inputs[i]);
+  }
+  for (int i = 0; i < num_outputs; ++i) {
+    g.tensor(outputs[i]);
+    g.outputs.push_back(outputs[i]);
+  }
+  API_END
+}
+
+int dw_graph_fold_batchnorm(dw_graph* gh) {
+  API_BEGIN
+  dw::fold_batchnorm(G(gh));
+  API_END
+}
+
+int dw_graph_convert_nchw_to_nhwc(dw_graph* gh) {
+  API_BEGIN
+  dw::convert_nchw_to_nhwc(G(gh));
+  API_END
+}
+
+int dw_graph_apply_fusion_passes(dw_graph* gh, int* num_fused) {
+  API_BEGIN
+  int n = dw::fuse_silu(G(gh));
+  if (num_fused) *num_fused = n;
+  API_END
+}
+
+int dw_graph_convert_to_f16(dw_graph* gh) {
+  API_BEGIN
+  dw::convert_to_f16(G(gh));
+  API_END
+}
+
+int dw_graph_set_activation_range(dw_graph* gh, const char* name, float min_v, float max_v) {
+  API_BEGIN
+  dw::TensorInfo& ti = G(gh).tensor(name);
+  if (!(min_v <= max_v)) dw::fail(DW_ERR_INVALID, "range: min > max");
+  ti.has_range = true;
+  ti.rmin = min_v;
+  ti.rmax = max_v;
+  API_END
+}
+
+int dw_graph_quantize_qdq(dw_graph* gh, const char* const* keep_f16_ops, int num_keep) {
+  API_BEGIN
+  std::set<std::string> keep;
+  for (int i = 0; i < num_keep; ++i) keep.insert(keep_f16_ops[i]);
+  dw::quantize_qdq(G(gh), keep);
+  API_END
+}
+
+const char* dw_graph_to_json(dw_graph* gh) {
+  if (!gh) return "";
+  if (gh->g.json.empty()) gh->g.json = dw::to_json(gh->g);
+  return gh->g.json.c_str();
+}
+
+int dw_graph_get_initializer(dw_graph* gh, const char* name, const void** data, size_t* len) {
+  API_BEGIN
+  if (!gh) dw::fail(DW_ERR_INVALID, "null graph");
+  const dw::TensorInfo& ti = gh->g.tensor(name);
+  if (data) *data = ti.is_init ? ti.data.data() : nullptr;
+  if (len) *len = ti.is_init ? ti.data.size() : 0;
+  API_END
+}
+
+}  // extern "C"

@@ -1,0 +1,1123 @@
+// HipGraphRuntime: VulkanGraphRuntime's API
+// (crates/dragonwing-onnx/src/vulkan_runtime.rs:115-469, :2113-2141) on the
+// HIP backend.  At creation the graph is lowered once:
+//
+//  1. fusion groups — Conv(+bias) with its activation (Relu, Sigmoid*Mul,
+//     SiLU) and a following residual Add; QLinearConv with its activation
+//     table and QLinearAdd; DequantizeLinear -> fp16 Conv and fp16 Conv ->
+//     QuantizeLinear -> table for the fp16 layers of a u8 graph; three
+//     cascaded SPPF max pools.  Intermediates inside a group never touch
+//     memory.
+//  2. placement — a Concat's inputs are written straight into channel
+//     slices of the concat buffer, and Split outputs are channel slices of
+//     their input, so neither op moves data (a copy is emitted only when a
+//     tensor cannot be placed).
+//  3. allocation of every remaining root tensor, weight packing for the
+//     MFMA kernels, per-channel requant tables.
+//  4. a launch list replayed by run(); optionally captured once into a HIP
+//     graph (the analogue of OpsRecorder's single command buffer).
+//
+// Every op runs on the GPU; an op without a kernel is an error at creation.
+#include <math.h>
+#include <string.h>
+
+#include <algorithm>
+#include <exception>
+#include <functional>
+#include <map>
+#include <set>
+#include <sstream>
+
+#include "backend.h"
+#include "graph.h"
+
+namespace dw {
+
+struct RtTensor {
+  int dtype = 0;
+  int64_t n = 1, h = 1, w = 1, c = 1;
+  bool rank4 = false;
+  bool materialized = true;
+  std::string parent;  // storage parent ("" = own storage)
+  int c_off = 0;       // channel offset inside parent
+  void* base = nullptr;
+  int pix_stride = 0;
+  int abs_off = 0;
+  float scale = 1.0f;
+  int zp = 0;
+  int64_t pixels() const { return n * h * w; }
+  View view() const { return {base, pix_stride, abs_off}; }
+  size_t bytes() const { return (size_t)(n * h * w * c) * dtype_size(dtype); }
+};
+
+struct Launch {
+  std::string kernel;
+  std::string op;
+  double work = 0;   // algorithmic ops (MAC = 2)
+  double bytes = 0;  // algorithmic bytes moved
+  std::function<void(hipStream_t)> fn;
+};
+
+struct Group {
+  std::string kind;  // conv, qconv, pool3, pool, resize, concat, split, ew, noop
+  std::vector<int> ops;
+  // conv / qconv fusion details
+  int act = ACT_NONE;
+  std::string in, out, res;  // input, final output, residual tensors
+  int in_kind = 0;           // direct conv input: 0 f32, 1 f16, 2 u8 dequant
+  float in_scale = 1; int in_zp = 0;
+  int out_kind = 0;          // direct conv output: 0 f32, 1 f16, 2 u8 quant
+  std::string pre;           // QLinearConv output (pre-table) tensor
+  bool lut = false;
+  std::string lut_out;       // tensor after the table (QLinearLUT output)
+  int conv = -1;             // index of the conv op
+};
+
+struct Runtime {
+  Backend* be = nullptr;
+  GraphIR g;
+  std::map<std::string, RtTensor> ts;
+  std::vector<void*> allocs;
+  std::vector<Launch> launches;
+  std::vector<std::string> info;
+  bool capture = false;
+  hipGraph_t hgraph = nullptr;
+  hipGraphExec_t hexec = nullptr;
+  bool stats = false;
+  float* stats_dev = nullptr;
+  std::vector<std::string> stats_names;
+
+  ~Runtime() {
+    if (be) (void)hipSetDevice(be->device);
+    if (be && be->stream) (void)hipStreamSynchronize(be->stream);
+    if (hexec) (void)hipGraphExecDestroy(hexec);
+    if (hgraph) (void)hipGraphDestroy(hgraph);
+    for (void* p : allocs) (void)hipFree(p);
+  }
+
+  void* dalloc(size_t bytes) {
+    void* p = nullptr;
+    DW_HIP(hipMalloc(&p, std::max<size_t>(bytes, 256)));
+    allocs.push_back(p);
+    return p;
+  }
+  void* upload(const void* src, size_t bytes) {
+    void* p = dalloc(bytes);
+    DW_HIP(hipMemcpy(p, src, bytes, hipMemcpyHostToDevice));
+    return p;
+  }
+
+  RtTensor& T(const std::string& n) {
+    auto it = ts.find(n);
+    if (it == ts.end()) fail(DW_ERR_RUNTIME, "runtime: unknown tensor '" + n + "'");
+    return it->second;
+  }
+
+  void build(Backend* b, const GraphIR& graph, bool stats_mode);
+  void lower(std::vector<Group>& groups);
+  void place(const std::vector<Group>& groups);
+  void allocate();
+  void emit(const Group& gr);
+  void emit_conv(const Group& gr);
+  void emit_qconv(const Group& gr);
+  void emit_ew(const OpNode& op);
+  void run();
+};
+
+namespace {
+
+bool is_float_graph(int dt) { return dt == DW_GRAPH_F32 || dt == DW_GRAPH_F16; }
+
+}  // namespace
+
+void Runtime::build(Backend* b, const GraphIR& graph, bool stats_mode) {
+  be = b;
+  g = graph;
+  stats = stats_mode;
+  for (auto& kv : g.t) {
+    RtTensor r;
+    const TensorInfo& ti = kv.second;
+    r.dtype = ti.dtype;
+    if (ti.dims.size() == 4) {
+      r.rank4 = true;
+      r.n = ti.dims[0]; r.h = ti.dims[1]; r.w = ti.dims[2]; r.c = ti.dims[3];
+    } else {
+      r.c = ti.numel();
+    }
+    r.scale = ti.scale;
+    r.zp = ti.zp;
+    ts[kv.first] = r;
+  }
+  for (auto& op : g.ops) {
+    if (op.type == "BatchNormalization")
+      fail(DW_ERR_UNSUPPORTED, "BatchNormalization must be folded (dw_graph_fold_batchnorm) first");
+    for (auto& o : op.out)
+      if (!T(o).rank4) fail(DW_ERR_UNSUPPORTED, "runtime: activations must be 4-D NHWC (" + o + ")");
+  }
+  std::vector<Group> groups;
+  lower(groups);
+  place(groups);
+  allocate();
+  if (stats) {
+    for (auto& kv : ts)
+      if (kv.second.rank4 && !g.t[kv.first].is_init && kv.second.dtype == F32) stats_names.push_back(kv.first);
+    stats_dev = (float*)dalloc(stats_names.size() * 2 * sizeof(float));
+  }
+  for (auto& gr : groups) {
+    emit(gr);
+    if (!stats) continue;
+    // calibration: min/max of every f32 activation an op writes
+    for (int oi : gr.ops)
+      for (auto& on : g.ops[oi].out) {
+        auto it = std::find(stats_names.begin(), stats_names.end(), on);
+        if (it == stats_names.end()) continue;
+        RtTensor& y = T(on);
+        float* dst = stats_dev + 2 * (it - stats_names.begin());
+        const View v = y.view();
+        const int px = (int)y.pixels(), ch = (int)y.c;
+        Launch S;
+        S.kernel = "minmax";
+        S.op = on;
+        S.fn = [=](hipStream_t st) { launch_minmax(st, v, px, ch, dst); };
+        launches.push_back(S);
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 1. fusion groups
+// ---------------------------------------------------------------------------
+void Runtime::lower(std::vector<Group>& groups) {
+  const int nops = (int)g.ops.size();
+  std::vector<bool> used(nops, false);
+  auto single = [&](const std::string& t) -> int {
+    if (stats || g.is_output(t)) return -1;
+    auto cs = g.consumers(t);
+    return cs.size() == 1 ? cs[0] : -1;
+  };
+  auto computed_before = [&](const std::string& t, int idx) {
+    if (g.t[t].is_init) return false;
+    const int p = g.producer(t);
+    return p < idx;  // graph inputs have no producer (-1)
+  };
+  // DequantizeLinear absorbed into the fp16 conv that is its only consumer.
+  std::map<int, int> dq_into;  // conv op -> dq op
+  if (!stats) {
+    for (int i = 0; i < nops; ++i)
+      if (g.ops[i].type == "DequantizeLinear") {
+        const int c = single(g.ops[i].out[0]);
+        if (c >= 0 && g.ops[c].type == "Conv") {
+          dq_into[c] = i;
+          used[i] = true;
+        }
+      }
+  }
+
+  for (int i = 0; i < nops; ++i) {
+    if (used[i]) continue;
+    const OpNode& op = g.ops[i];
+    Group gr;
+    gr.ops = {i};
+    used[i] = true;
+    if (op.type == "Conv") {
+      const dw_op_params& p = op.p;
+      if (p.group > 1) fail(DW_ERR_UNSUPPORTED, "runtime: grouped/depthwise conv in a graph (" + op.name + ")");
+      if ((p.dilations[0] > 1) || (p.dilations[1] > 1)) fail(DW_ERR_UNSUPPORTED, "runtime: dilation != 1");
+      gr.kind = "conv";
+      gr.conv = i;
+      gr.in = op.in[0];
+      gr.out = op.out[0];
+      const int xdt = T(op.in[0]).dtype;
+      gr.in_kind = xdt == F32 ? 0 : 1;
+      auto dq = dq_into.find(i);
+      if (dq != dq_into.end()) {
+        const OpNode& d = g.ops[dq->second];
+        gr.in = d.in[0];
+        gr.in_kind = 2;
+        gr.in_scale = T(d.in[0]).scale;
+        gr.in_zp = T(d.in[0]).zp;
+        gr.ops.insert(gr.ops.begin(), dq->second);
+        T(d.out[0]).materialized = false;
+      }
+      gr.out_kind = T(op.out[0]).dtype == F32 ? 0 : 1;
+      std::string cur = op.out[0];
+      int c = single(cur);
+      if (c >= 0 && g.ops[c].type == "Relu") {
+        gr.act = ACT_RELU;
+      } else if (c >= 0 && g.ops[c].type == "SiLU") {
+        gr.act = ACT_SILU;
+      } else if (!stats && !g.is_output(cur)) {
+        auto cs = g.consumers(cur);
+        if (cs.size() == 2) {
+          int s = -1, m = -1;
+          for (int k : cs) {
+            if (g.ops[k].type == "Sigmoid") s = k;
+            if (g.ops[k].type == "Mul") m = k;
+          }
+          if (s >= 0 && m >= 0 && single(g.ops[s].out[0]) == m) {
+            const OpNode& mul = g.ops[m];
+            if ((mul.in[0] == cur && mul.in[1] == g.ops[s].out[0]) ||
+                (mul.in[1] == cur && mul.in[0] == g.ops[s].out[0])) {
+              gr.act = ACT_SILU;
+              used[s] = true;
+              gr.ops.push_back(s);
+              T(g.ops[s].out[0]).materialized = false;
+              c = m;
+            }
+          }
+        }
+      }
+      if (gr.act != ACT_NONE) {
+        used[c] = true;
+        gr.ops.push_back(c);
+        T(cur).materialized = false;
+        cur = g.ops[c].out[0];
+      }
+      // fp16 conv of a u8 graph feeding QuantizeLinear (+ table)
+      int qc = single(cur);
+      if (qc >= 0 && g.ops[qc].type == "QuantizeLinear") {
+        used[qc] = true;
+        gr.ops.push_back(qc);
+        T(cur).materialized = false;
+        cur = g.ops[qc].out[0];
+        gr.out_kind = 2;
+        int lc = single(cur);
+        if (lc >= 0 && g.ops[lc].type == "QLinearLUT") {
+          used[lc] = true;
+          gr.ops.push_back(lc);
+          gr.lut = true;
+          gr.pre = cur;
+          T(cur).materialized = false;
+          cur = g.ops[lc].out[0];
+        }
+      }
+      // residual add (f16 MFMA path only)
+      int ac = single(cur);
+      const bool mfma = g.dtype == DW_GRAPH_F16 && gr.in_kind == 1 && gr.out_kind == 1 &&
+                        (T(gr.in).c * 2) % 16 == 0 && T(gr.out).c % 4 == 0;
+      if (mfma && ac >= 0 && g.ops[ac].type == "Add") {
+        const OpNode& add = g.ops[ac];
+        const std::string other = add.in[0] == cur ? add.in[1] : add.in[0];
+        if (other != cur && computed_before(other, i) && T(other).rank4 &&
+            T(other).dtype == F16 && T(other).c == T(cur).c) {
+          used[ac] = true;
+          gr.ops.push_back(ac);
+          gr.res = other;
+          T(cur).materialized = false;
+          cur = add.out[0];
+        }
+      }
+      gr.out = cur;
+      groups.push_back(gr);
+      continue;
+    }
+    if (op.type == "QLinearConv") {
+      gr.kind = "qconv";
+      gr.conv = i;
+      gr.in = op.in[0];
+      gr.pre = op.out[0];
+      std::string cur = op.out[0];
+      int lc = single(cur);
+      if (lc >= 0 && g.ops[lc].type == "QLinearLUT") {
+        used[lc] = true;
+        gr.ops.push_back(lc);
+        gr.lut = true;
+        T(cur).materialized = false;
+        cur = g.ops[lc].out[0];
+        gr.lut_out = cur;
+      }
+      int ac = single(cur);
+      if (ac >= 0 && g.ops[ac].type == "QLinearAdd") {
+        const OpNode& add = g.ops[ac];
+        const std::string other = add.in[0] == cur ? add.in[1] : add.in[0];
+        if (other != cur && computed_before(other, i) && T(other).rank4 && T(other).c == T(cur).c) {
+          used[ac] = true;
+          gr.ops.push_back(ac);
+          gr.res = other;
+          T(cur).materialized = false;
+          cur = add.out[0];
+        }
+      }
+      gr.out = cur;
+      groups.push_back(gr);
+      continue;
+    }
+    if (op.type == "MaxPool") {
+      const dw_op_params& p = op.p;
+      const int k = p.kernel_shape[0];
+      auto cascade_ok = [&](const OpNode& o) {
+        const dw_op_params& q = o.p;
+        return o.type == "MaxPool" && q.kernel_shape[0] == k && q.kernel_shape[1] == k && q.strides[0] == 1 &&
+               q.strides[1] == 1 && q.pads[0] == k / 2 && q.pads[1] == k / 2 && q.pads[2] == k / 2 &&
+               q.pads[3] == k / 2 && (k % 2) == 1;
+      };
+      if (!stats && cascade_ok(op)) {
+        int j2 = -1, j3 = -1;
+        for (int cidx : g.consumers(op.out[0]))
+          if (!used[cidx] && cascade_ok(g.ops[cidx])) j2 = cidx;
+        if (j2 >= 0)
+          for (int cidx : g.consumers(g.ops[j2].out[0]))
+            if (!used[cidx] && cascade_ok(g.ops[cidx])) j3 = cidx;
+        if (j2 >= 0 && j3 >= 0) {
+          gr.kind = "pool3";
+          gr.ops = {i, j2, j3};
+          used[j2] = used[j3] = true;
+          groups.push_back(gr);
+          continue;
+        }
+      }
+      gr.kind = "pool";
+      groups.push_back(gr);
+      continue;
+    }
+    if (op.type == "Resize") {
+      if (!op.p.mode_nearest) fail(DW_ERR_UNSUPPORTED, "runtime: only nearest Resize is implemented");
+      gr.kind = "resize";
+    } else if (op.type == "Concat") {
+      gr.kind = "concat";
+    } else if (op.type == "Split") {
+      gr.kind = "split";
+    } else if (op.type == "Relu" || op.type == "Sigmoid" || op.type == "Mul" || op.type == "Add" ||
+               op.type == "SiLU" || op.type == "QLinearLUT" || op.type == "QLinearAdd" ||
+               op.type == "QuantizeLinear" || op.type == "DequantizeLinear") {
+      gr.kind = "ew";
+    } else {
+      fail(DW_ERR_UNSUPPORTED, "runtime: no kernel for op type '" + op.type + "' (" + op.name + ")");
+    }
+    groups.push_back(gr);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 2. placement of concat inputs and split outputs
+// ---------------------------------------------------------------------------
+void Runtime::place(const std::vector<Group>& groups) {
+  std::set<std::string> protect(g.inputs.begin(), g.inputs.end());
+  for (auto& o : g.outputs) protect.insert(o);
+  // Split outputs: slices of the input.
+  for (auto& gr : groups) {
+    if (gr.kind != "split") continue;
+    const OpNode& op = g.ops[gr.ops[0]];
+    if (op.p.axis != 3) fail(DW_ERR_UNSUPPORTED, "runtime: Split only along channels");
+    int off = 0;
+    for (size_t k = 0; k < op.out.size(); ++k) {
+      RtTensor& o = T(op.out[k]);
+      if (protect.count(op.out[k])) fail(DW_ERR_UNSUPPORTED, "runtime: split output as graph output");
+      o.parent = op.in[0];
+      o.c_off = off;
+      off += (int)o.c;
+    }
+  }
+  // Walks split parents up to the storage root; returns "" if the tensor
+  // already lives inside another concat's buffer.
+  std::set<std::string> concat_placed;
+  auto root_of = [&](std::string t, int& off) -> std::string {
+    off = 0;
+    while (!T(t).parent.empty()) {
+      if (concat_placed.count(t)) return "";
+      off += T(t).c_off;
+      t = T(t).parent;
+    }
+    return t;
+  };
+  // Concats, last first, so nested placements resolve through parents.
+  for (auto it = groups.rbegin(); it != groups.rend(); ++it) {
+    if (it->kind != "concat") continue;
+    const OpNode& op = g.ops[it->ops[0]];
+    if (op.p.axis != 3) fail(DW_ERR_UNSUPPORTED, "runtime: Concat only along channels");
+    const std::string out = op.out[0];
+    const int total = (int)T(out).c;
+    int off = 0;
+    std::map<std::string, int> want;  // root -> offset inside `out`
+    std::set<std::string> bad;
+    std::vector<std::pair<std::string, int>> ins;
+    for (auto& in : op.in) {
+      ins.push_back({in, off});
+      off += (int)T(in).c;
+    }
+    for (auto& pr : ins) {
+      int roff = 0;
+      const std::string r = root_of(pr.first, roff);
+      if (r.empty()) continue;
+      const int d = pr.second - roff;
+      if (protect.count(r) || g.t[r].is_init || !T(r).parent.empty() || r == out ||
+          T(r).dtype != T(out).dtype || d < 0 || d + T(r).c > total || (d % 16) != 0 || (total % 16) != 0 ||
+          T(r).pixels() != T(out).pixels()) {
+        bad.insert(r);
+        continue;
+      }
+      auto w = want.find(r);
+      if (w != want.end() && w->second != d) bad.insert(r);
+      want[r] = d;
+    }
+    for (auto& kv : want) {
+      if (bad.count(kv.first)) continue;
+      T(kv.first).parent = out;
+      T(kv.first).c_off = kv.second;
+      concat_placed.insert(kv.first);
+    }
+  }
+}
+
+void Runtime::allocate() {
+  // roots that need storage: graph inputs, outputs and every materialized
+  // tensor without a parent.  A placed tensor is materialized inside its
+  // root.
+  for (auto& kv : ts) {
+    RtTensor& r = kv.second;
+    if (!r.rank4 || g.t[kv.first].is_init) continue;
+    if (!r.parent.empty()) continue;
+    const bool needed = r.materialized || g.is_output(kv.first) ||
+                        std::find(g.inputs.begin(), g.inputs.end(), kv.first) != g.inputs.end();
+    if (!needed) continue;
+    // a root whose only users are fused-away intermediates still gets
+    // storage if any placed child is materialized
+    r.base = dalloc(r.bytes());
+    r.pix_stride = (int)r.c;
+    r.abs_off = 0;
+  }
+  for (auto& kv : ts) {
+    RtTensor& r = kv.second;
+    if (r.parent.empty()) continue;
+    int off = 0;
+    std::string t = kv.first;
+    while (!T(t).parent.empty()) {
+      off += T(t).c_off;
+      t = T(t).parent;
+    }
+    RtTensor& root = T(t);
+    if (!root.base) {
+      root.base = dalloc(root.bytes());
+      root.pix_stride = (int)root.c;
+    }
+    r.base = root.base;
+    r.pix_stride = root.pix_stride;
+    r.abs_off = off;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 4. launches
+// ---------------------------------------------------------------------------
+namespace {
+std::string join_names(const GraphIR& g, const std::vector<int>& ops) {
+  std::string s;
+  for (int i : ops) s += (s.empty() ? "" : "+") + g.ops[i].name;
+  return s;
+}
+}  // namespace
+
+void Runtime::emit(const Group& gr) {
+  if (gr.kind == "conv") return emit_conv(gr);
+  if (gr.kind == "qconv") return emit_qconv(gr);
+  if (gr.kind == "split") return;
+  if (gr.kind == "concat") {
+    const OpNode& op = g.ops[gr.ops[0]];
+    RtTensor& out = T(op.out[0]);
+    int off = 0;
+    for (auto& in : op.in) {
+      RtTensor& ti = T(in);
+      int roff = 0;
+      std::string t = in;
+      while (!T(t).parent.empty()) {
+        roff += T(t).c_off;
+        t = T(t).parent;
+      }
+      const bool placed = ti.base == out.base && ti.abs_off == out.abs_off + off;
+      if (!placed) {
+        View src = ti.view(), dst = out.view();
+        dst.c_off += off;
+        const int px = (int)ti.pixels(), ch = (int)ti.c, es = dtype_size(ti.dtype);
+        Launch L;
+        L.kernel = "copy_channels";
+        L.op = op.name + ":" + in;
+        L.bytes = 2.0 * px * ch * es;
+        L.fn = [=](hipStream_t st) { launch_copy_channels(st, src, dst, px, ch, es); };
+        launches.push_back(L);
+      }
+      off += (int)ti.c;
+    }
+    return;
+  }
+  if (gr.kind == "pool" || gr.kind == "pool3") {
+    const OpNode& op = g.ops[gr.ops[0]];
+    RtTensor& x = T(op.in[0]);
+    RtTensor& y = T(op.out[0]);
+    PoolArgs a{};
+    a.x = x.view();
+    a.y = y.view();
+    a.n = (int)x.n; a.h = (int)x.h; a.w = (int)x.w; a.c = (int)x.c;
+    a.kh = op.p.kernel_shape[0]; a.kw = op.p.kernel_shape[1];
+    a.sh = std::max(1, op.p.strides[0]); a.sw = std::max(1, op.p.strides[1]);
+    a.pt = op.p.pads[0]; a.pl = op.p.pads[1];
+    a.ho = (int)y.h; a.wo = (int)y.w;
+    const int dt = x.dtype;
+    Launch L;
+    L.op = join_names(g, gr.ops);
+    if (gr.kind == "pool3") {
+      View y2 = T(g.ops[gr.ops[1]].out[0]).view(), y3 = T(g.ops[gr.ops[2]].out[0]).view();
+      L.kernel = "maxpool_cascade3";
+      L.bytes = 4.0 * x.bytes();
+      L.fn = [=](hipStream_t st) { launch_maxpool_cascade3(st, a, y2, y3, dt); };
+    } else {
+      L.kernel = "maxpool";
+      L.bytes = (double)x.bytes() + y.bytes();
+      L.fn = [=](hipStream_t st) { launch_maxpool(st, a, dt); };
+    }
+    launches.push_back(L);
+    return;
+  }
+  if (gr.kind == "resize") {
+    const OpNode& op = g.ops[gr.ops[0]];
+    RtTensor& x = T(op.in[0]);
+    RtTensor& y = T(op.out[0]);
+    ResizeArgs a{};
+    a.x = x.view();
+    a.y = y.view();
+    a.n = (int)x.n; a.h = (int)x.h; a.w = (int)x.w; a.c = (int)x.c; a.ho = (int)y.h; a.wo = (int)y.w;
+    const int dt = x.dtype;
+    Launch L;
+    L.kernel = "resize_nearest";
+    L.op = op.name;
+    L.bytes = (double)x.bytes() + y.bytes();
+    L.fn = [=](hipStream_t st) { launch_resize_nearest(st, a, dt); };
+    launches.push_back(L);
+    return;
+  }
+  if (gr.kind == "ew") return emit_ew(g.ops[gr.ops[0]]);
+  fail(DW_ERR_RUNTIME, "runtime: unhandled group " + gr.kind);
+}
+
+void Runtime::emit_ew(const OpNode& op) {
+  Ew2Args e{};
+  RtTensor& a = T(op.in[0]);
+  RtTensor& y = T(op.out[0]);
+  e.a = a.view();
+  e.y = y.view();
+  e.pixels = (int)y.pixels();
+  e.channels = (int)y.c;
+  e.dtype = a.dtype;
+  double bytes = (double)a.bytes() + y.bytes();
+  if (op.in.size() > 1) {
+    RtTensor& b = T(op.in[1]);
+    if (b.pixels() != a.pixels() || b.c != a.c)
+      fail(DW_ERR_UNSUPPORTED, "runtime: broadcasting elementwise op " + op.name);
+    e.b = b.view();
+    bytes += b.bytes();
+  }
+  if (op.type == "Relu") e.op = EW_RELU;
+  else if (op.type == "Sigmoid") e.op = EW_SIGMOID;
+  else if (op.type == "Mul") e.op = EW_MUL;
+  else if (op.type == "Add") e.op = EW_ADD;
+  else if (op.type == "SiLU") e.op = EW_SILU;
+  else if (op.type == "QLinearAdd") {
+    RtTensor& b = T(op.in[1]);
+    e.op = EW_QADD_U8;
+    e.s0 = a.scale / y.scale; e.s1 = b.scale / y.scale;
+    e.z0 = a.zp; e.z1 = b.zp; e.z2 = y.zp;
+  } else if (op.type == "QLinearLUT") {
+    e.op = EW_LUT_U8;
+    uint8_t lut[256];
+    build_silu_lut(lut, a.scale, a.zp, y.scale, y.zp);
+    e.lut = (const uint8_t*)upload(lut, 256);
+  } else if (op.type == "QuantizeLinear") {
+    e.op = EW_QUANT_LINEAR_F16_U8;
+    e.s0 = y.scale; e.z0 = y.zp;
+  } else if (op.type == "DequantizeLinear") {
+    e.op = EW_DEQUANT_LINEAR_U8_F16;
+    e.s0 = a.scale; e.z0 = a.zp;
+  } else {
+    fail(DW_ERR_UNSUPPORTED, "runtime: elementwise " + op.type);
+  }
+  Launch L;
+  L.kernel = "elementwise";
+  L.op = op.name;
+  L.bytes = bytes;
+  L.fn = [=](hipStream_t st) { launch_elementwise2d(st, e); };
+  launches.push_back(L);
+}
+
+void Runtime::emit_conv(const Group& gr) {
+  const OpNode& op = g.ops[gr.conv];
+  const TensorInfo& W = g.t[op.in[1]];
+  if (W.dims.size() != 4) fail(DW_ERR_UNSUPPORTED, "runtime: conv weight must be HWIO 4-D (run convert_nchw_to_nhwc)");
+  RtTensor& x = T(gr.in);
+  RtTensor& y = T(gr.out);
+  const int kh = (int)W.dims[0], kw = (int)W.dims[1], ci = (int)W.dims[2], co = (int)W.dims[3];
+  if (ci != x.c || co != y.c) fail(DW_ERR_RUNTIME, "runtime: conv " + op.name + " channel mismatch");
+  const bool has_bias = op.in.size() > 2 && !op.in[2].empty();
+  const int pt = op.p.pads[0], pl = op.p.pads[1];
+  const int sh = std::max(1, op.p.strides[0]), sw = std::max(1, op.p.strides[1]);
+  const double macs = (double)y.pixels() * co * kh * kw * ci;
+  Launch L;
+  L.op = join_names(g, gr.ops);
+  L.work = 2.0 * macs;
+
+  const bool mfma = g.dtype == DW_GRAPH_F16 && gr.in_kind == 1 && gr.out_kind == 1 && (ci * 2) % 16 == 0 &&
+                    co % 4 == 0 && (x.pix_stride * 2) % 16 == 0 && (x.abs_off * 2) % 16 == 0 &&
+                    (y.pix_stride % 4) == 0 && (y.abs_off % 4) == 0;
+  if (mfma) {
+    IgemmArgs a{};
+    a.x = (const uint8_t*)x.base;
+    a.y = y.base;
+    a.n = (int)x.n; a.h = (int)x.h; a.w = (int)x.w; a.cin = ci; a.cout = co; a.kh = kh; a.kw = kw;
+    a.sh = sh; a.sw = sw; a.pt = pt; a.pl = pl; a.ho = (int)y.h; a.wo = (int)y.w;
+    a.m = (int)y.pixels();
+    a.ksteps = (kh * kw * ci * 2 + 63) / 64;
+    const int bc = igemm_channel_tile(co);
+    a.cout_pad = (co + bc - 1) / bc * bc;
+    a.x_pix_stride = x.pix_stride; a.x_c_off = x.abs_off;
+    a.y_pix_stride = y.pix_stride; a.y_c_off = y.abs_off;
+    void* whwio = upload(W.data.data(), W.data.size());
+    void* wpk = dalloc((size_t)a.ksteps * a.cout_pad * 64);
+    launch_pack_weights(be->stream, whwio, wpk, kh * kw * ci, co, a.cout_pad, a.ksteps, 2);
+    a.wpk = (const uint8_t*)wpk;
+    a.epi = EPI_F16;
+    a.act = gr.act;
+    if (has_bias) a.bias_h = (const uint16_t*)upload(g.t[op.in[2]].data.data(), g.t[op.in[2]].data.size());
+    if (!gr.res.empty()) {
+      RtTensor& r = T(gr.res);
+      if (r.pix_stride % 4 != 0 || r.abs_off % 4 != 0)
+        fail(DW_ERR_RUNTIME, "runtime: misaligned residual view for " + op.name);
+      a.res = r.base;
+      a.r_pix_stride = r.pix_stride;
+      a.r_c_off = r.abs_off;
+      L.bytes += r.bytes();
+    }
+    L.kernel = igemm_tile_name(a, 2);
+    L.bytes += (double)x.bytes() + W.data.size() + y.pixels() * co * 2.0;
+    L.fn = [=](hipStream_t st) { launch_igemm(st, a, 2); };
+    DW_HIP(hipStreamSynchronize(be->stream));
+    launches.push_back(L);
+    return;
+  }
+  // direct (reference accumulation order)
+  DirectArgs a{};
+  a.x = x.base;
+  a.y = y.base;
+  a.n = (int)x.n; a.h = (int)x.h; a.w = (int)x.w; a.cin = ci; a.cout = co; a.kh = kh; a.kw = kw;
+  a.sh = sh; a.sw = sw; a.pt = pt; a.pl = pl; a.ho = (int)y.h; a.wo = (int)y.w;
+  a.m = (int)y.pixels();
+  a.x_pix_stride = x.pix_stride; a.x_c_off = x.abs_off;
+  a.y_pix_stride = y.pix_stride; a.y_c_off = y.abs_off;
+  a.in_kind = gr.in_kind;
+  a.in_scale = gr.in_scale;
+  a.in_zp = gr.in_zp;
+  a.out_kind = gr.out_kind;
+  a.act = gr.act;
+  // weights as f32 (exact widening of f16 weights with the reference decode)
+  std::vector<float> wf(W.numel());
+  if (W.dtype == DW_DTYPE_F32) {
+    memcpy(wf.data(), W.data.data(), wf.size() * 4);
+  } else if (W.dtype == DW_DTYPE_F16) {
+    void* wh = upload(W.data.data(), W.data.size());
+    float* wdev = (float*)dalloc(wf.size() * 4);
+    EwArgs e{};
+    e.op = EW_F16_TO_F32; e.a = wh; e.y = wdev; e.count = wf.size();
+    launch_elementwise(be->stream, e);
+    DW_HIP(hipStreamSynchronize(be->stream));
+    a.wf = wdev;
+  } else {
+    fail(DW_ERR_UNSUPPORTED, "runtime: conv weight dtype");
+  }
+  if (!a.wf) a.wf = (const float*)upload(wf.data(), wf.size() * 4);
+  if (has_bias) {
+    const TensorInfo& B = g.t[op.in[2]];
+    if (gr.out_kind == 0)
+      a.bias_f = (const float*)upload(B.data.data(), B.data.size());
+    else
+      a.bias_h = (const uint16_t*)upload(B.data.data(), B.data.size());
+  }
+  if (gr.out_kind == 2) {
+    const RtTensor& q = T(gr.lut ? gr.pre : gr.out);
+    a.out_scale = q.scale;
+    a.out_zp = q.zp;
+    if (gr.lut) {
+      uint8_t lut[256];
+      build_silu_lut(lut, q.scale, q.zp, y.scale, y.zp);
+      a.lut = (const uint8_t*)upload(lut, 256);
+    }
+  }
+  L.kernel = "direct_conv";
+  L.bytes += (double)x.bytes() + W.numel() * 4.0 + (double)y.bytes();
+  L.fn = [=](hipStream_t st) { launch_direct_conv(st, a); };
+  launches.push_back(L);
+}
+
+void Runtime::emit_qconv(const Group& gr) {
+  const OpNode& op = g.ops[gr.conv];
+  const TensorInfo& W = g.t[op.in[1]];
+  RtTensor& x = T(gr.in);
+  RtTensor& pre = T(gr.pre);
+  RtTensor& y = T(gr.out);
+  const int kh = (int)W.dims[0], kw = (int)W.dims[1], ci = (int)W.dims[2], co = (int)W.dims[3];
+  if (x.dtype != U8 || y.dtype != U8) fail(DW_ERR_RUNTIME, "runtime: QLinearConv needs u8 tensors");
+  if (ci % 16 != 0 || co % 4 != 0)
+    fail(DW_ERR_UNSUPPORTED, "runtime: QLinearConv needs c_in % 16 == 0 and c_out % 4 == 0 (" + op.name + ")");
+  if (x.pix_stride % 16 != 0 || x.abs_off % 16 != 0 || y.pix_stride % 4 != 0 || y.abs_off % 4 != 0)
+    fail(DW_ERR_RUNTIME, "runtime: misaligned view for " + op.name);
+  IgemmArgs a{};
+  a.x = (const uint8_t*)x.base;
+  a.y = y.base;
+  a.n = (int)x.n; a.h = (int)x.h; a.w = (int)x.w; a.cin = ci; a.cout = co; a.kh = kh; a.kw = kw;
+  a.sh = std::max(1, op.p.strides[0]); a.sw = std::max(1, op.p.strides[1]);
+  a.pt = op.p.pads[0]; a.pl = op.p.pads[1]; a.ho = (int)y.h; a.wo = (int)y.w;
+  a.m = (int)y.pixels();
+  a.ksteps = (kh * kw * ci + 63) / 64;
+  const int bc = igemm_channel_tile(co);
+  a.cout_pad = (co + bc - 1) / bc * bc;
+  a.x_pix_stride = x.pix_stride; a.x_c_off = x.abs_off;
+  a.y_pix_stride = y.pix_stride; a.y_c_off = y.abs_off;
+  // weights, bias' = bias + (128 - x_zp) * sum_k w, M[c] = xs*ws[c]/ys
+  void* whwio = upload(W.data.data(), W.data.size());
+  void* wpk = dalloc((size_t)a.ksteps * a.cout_pad * 64);
+  launch_pack_weights(be->stream, whwio, wpk, kh * kw * ci, co, a.cout_pad, a.ksteps, 1);
+  std::vector<int64_t> bias(co, 0);
+  if (op.in.size() > 2 && !op.in[2].empty()) {
+    const TensorInfo& B = g.t[op.in[2]];
+    if (B.dtype != DW_DTYPE_I32) fail(DW_ERR_RUNTIME, "runtime: QLinearConv bias must be int32");
+    for (int c = 0; c < co; ++c) bias[c] = ((const int32_t*)B.data.data())[c];
+  }
+  std::vector<int32_t> bi(co);
+  std::vector<float> ms(co);
+  const int8_t* wq = (const int8_t*)W.data.data();
+  for (int c = 0; c < co; ++c) {
+    int64_t s = 0;
+    for (int k = 0; k < kh * kw * ci; ++k) s += wq[(size_t)k * co + c];
+    const int64_t v = bias[c] + (int64_t)(128 - x.zp) * s;
+    if (v < INT32_MIN || v > INT32_MAX) fail(DW_ERR_RUNTIME, "runtime: bias overflow in " + op.name);
+    bi[c] = (int32_t)v;
+    if (W.ch_scales.size() != (size_t)co) fail(DW_ERR_RUNTIME, "runtime: missing weight scales");
+    ms[c] = (x.scale * W.ch_scales[c]) / pre.scale;
+  }
+  a.wpk = (const uint8_t*)wpk;
+  a.bias_i = (const int*)upload(bi.data(), bi.size() * 4);
+  a.mscale = (const float*)upload(ms.data(), ms.size() * 4);
+  a.epi = EPI_QU8;
+  a.xxor = 0x80808080u;
+  a.xpad = (uint32_t)((x.zp ^ 0x80) & 0xff) * 0x01010101u;
+  a.y_zp = pre.zp;
+  Launch L;
+  L.op = join_names(g, gr.ops);
+  L.work = 2.0 * (double)y.pixels() * co * kh * kw * ci;
+  L.bytes = (double)x.bytes() + W.data.size() + (double)y.pixels() * co;
+  if (gr.lut) {
+    const RtTensor& lo = T(gr.lut_out);
+    uint8_t lut[256];
+    build_silu_lut(lut, pre.scale, pre.zp, lo.scale, lo.zp);
+    a.lut = (const uint8_t*)upload(lut, 256);
+  }
+  if (!gr.res.empty()) {
+    RtTensor& r = T(gr.res);
+    const RtTensor& av = T(gr.lut ? gr.lut_out : gr.pre);
+    if (r.pix_stride % 4 != 0 || r.abs_off % 4 != 0)
+      fail(DW_ERR_RUNTIME, "runtime: misaligned residual view for " + op.name);
+    a.res = r.base;
+    a.r_pix_stride = r.pix_stride;
+    a.r_c_off = r.abs_off;
+    a.ra = av.scale / y.scale;
+    a.rb = r.scale / y.scale;
+    a.za = av.zp;
+    a.zb = r.zp;
+    a.zy = y.zp;
+    L.bytes += r.bytes();
+  }
+  DW_HIP(hipStreamSynchronize(be->stream));
+  L.kernel = igemm_tile_name(a, 1);
+  L.fn = [=](hipStream_t st) { launch_igemm(st, a, 1); };
+  launches.push_back(L);
+}
+
+void Runtime::run() {
+  hipStream_t st = be->stream;
+  if (stats) {
+    for (size_t i = 0; i < stats_names.size(); ++i) launch_minmax_init(st, stats_dev + 2 * i);
+    // graph inputs are not produced by any op: record them first
+    for (auto& in : g.inputs) {
+      auto it = std::find(stats_names.begin(), stats_names.end(), in);
+      if (it != stats_names.end()) {
+        RtTensor& t = T(in);
+        launch_minmax(st, t.view(), (int)t.pixels(), (int)t.c, stats_dev + 2 * (it - stats_names.begin()));
+      }
+    }
+  }
+  if (capture && !stats) {
+    if (!hexec) {
+      DW_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+      for (auto& L : launches) L.fn(st);
+      DW_HIP(hipStreamEndCapture(st, &hgraph));
+      DW_HIP(hipGraphInstantiate(&hexec, hgraph, nullptr, nullptr, 0));
+    }
+    DW_HIP(hipGraphLaunch(hexec, st));
+    return;
+  }
+  for (auto& L : launches) L.fn(st);
+}
+
+}  // namespace dw
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+struct dw_hip_graph_runtime {
+  dw::Runtime rt;
+};
+
+#define API_BEGIN try {
+#define API_END                           \
+  }                                       \
+  catch (const dw::Error& e) {            \
+    dw::set_last_error(e.msg);            \
+    return e.code;                        \
+  }                                       \
+  catch (const std::exception& e) {       \
+    dw::set_last_error(e.what());         \
+    return DW_ERR_BACKEND;                \
+  }                                       \
+  return DW_OK;
+
+namespace {
+dw::Runtime& R(dw_hip_graph_runtime* rt) {
+  if (!rt) dw::fail(DW_ERR_INVALID, "null runtime");
+  DW_HIP(hipSetDevice(rt->rt.be->device));
+  return rt->rt;
+}
+dw::Backend* Bk(dw_hip_backend* be) {
+  if (!be) dw::fail(DW_ERR_INVALID, "null backend");
+  dw::Backend* b = reinterpret_cast<dw::Backend*>(be);
+  DW_HIP(hipSetDevice(b->device));
+  return b;
+}
+
+// F16::to_f32_soft (dtype.rs:226-263), used by get_output_f32 as the
+// reference's runtime does.
+float f16_to_f32_ref(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
+  uint32_t out;
+  if (e == 0) {
+    if (m == 0) {
+      out = sign;
+    } else {
+      uint32_t mm = m;
+      int sh = 0;
+      while ((mm & 0x400u) == 0) { mm <<= 1; ++sh; }
+      out = sign | ((uint32_t)(127 - 15 - sh) << 23) | ((mm & 0x3FFu) << 13);
+    }
+  } else if (e == 31) {
+    out = m == 0 ? (sign | 0x7F800000u) : (sign | 0x7FC00000u | (m << 13));
+  } else {
+    out = sign | ((e + 112) << 23) | (m << 13);
+  }
+  float f;
+  memcpy(&f, &out, 4);
+  return f;
+}
+}  // namespace
+
+extern "C" {
+
+int dw_hip_graph_runtime_create(dw_hip_backend* be, const dw_graph* g, dw_hip_graph_runtime** out) {
+  API_BEGIN
+  if (!g || !out) dw::fail(DW_ERR_INVALID, "null argument");
+  dw::Backend* b = Bk(be);
+  auto* rt = new dw_hip_graph_runtime();
+  try {
+    rt->rt.build(b, g->g, false);
+  } catch (...) {
+    delete rt;
+    throw;
+  }
+  *out = rt;
+  API_END
+}
+
+void dw_hip_graph_runtime_destroy(dw_hip_graph_runtime* rt) { delete rt; }
+
+int dw_hip_graph_set_input_bytes(dw_hip_graph_runtime* rth, const char* name, const void* data, size_t len) {
+  API_BEGIN
+  dw::Runtime& rt = R(rth);
+  if (!name || std::find(rt.g.inputs.begin(), rt.g.inputs.end(), std::string(name)) == rt.g.inputs.end())
+    dw::fail(DW_ERR_RUNTIME, std::string("input not found: ") + (name ? name : "(null)"));
+  dw::RtTensor& t = rt.T(name);
+  if (len != t.bytes())
+    dw::fail(DW_ERR_RUNTIME, "input size mismatch: expected " + std::to_string(t.bytes()) + ", got " +
+                                 std::to_string(len));
+  DW_HIP(hipMemcpyAsync(t.base, data, len, hipMemcpyHostToDevice, rt.be->stream));
+  DW_HIP(hipStreamSynchronize(rt.be->stream));
+  API_END
+}
+
+int dw_hip_graph_set_input_f32(dw_hip_graph_runtime* rth, const char* name, const float* data, size_t count) {
+  API_BEGIN
+  dw::Runtime& rt = R(rth);
+  if (!name || std::find(rt.g.inputs.begin(), rt.g.inputs.end(), std::string(name)) == rt.g.inputs.end())
+    dw::fail(DW_ERR_RUNTIME, std::string("input not found: ") + (name ? name : "(null)"));
+  dw::RtTensor& t = rt.T(name);
+  const size_t n = (size_t)(t.pixels() * t.c);
+  if (count != n)
+    dw::fail(DW_ERR_RUNTIME, "input size mismatch: expected " + std::to_string(n) + ", got " + std::to_string(count));
+  if (t.dtype == dw::F32) {
+    DW_HIP(hipMemcpyAsync(t.base, data, n * 4, hipMemcpyHostToDevice, rt.be->stream));
+  } else if (t.dtype == dw::F16) {
+    std::vector<uint16_t> h(n);
+    for (size_t i = 0; i < n; ++i) h[i] = dw::f16_bits_from_f32(data[i]);
+    DW_HIP(hipMemcpyAsync(t.base, h.data(), n * 2, hipMemcpyHostToDevice, rt.be->stream));
+    DW_HIP(hipStreamSynchronize(rt.be->stream));
+  } else {
+    dw::fail(DW_ERR_RUNTIME, "unsupported dtype for set_input_f32");
+  }
+  DW_HIP(hipStreamSynchronize(rt.be->stream));
+  API_END
+}
+
+int dw_hip_graph_run(dw_hip_graph_runtime* rth) {
+  API_BEGIN
+  R(rth).run();
+  API_END
+}
+
+static void download_tensor(dw::Runtime& rt, const std::string& name, std::vector<uint8_t>& out) {
+  dw::RtTensor& t = rt.T(name);
+  if (!t.base) dw::fail(DW_ERR_RUNTIME, "tensor " + name + " is not materialized");
+  DW_HIP(hipStreamSynchronize(rt.be->stream));
+  const size_t es = dw::dtype_size(t.dtype);
+  out.resize(t.bytes());
+  DW_HIP(hipMemcpy2D(out.data(), t.c * es, (const uint8_t*)t.base + (size_t)t.abs_off * es,
+                     (size_t)t.pix_stride * es, t.c * es, (size_t)t.pixels(), hipMemcpyDeviceToHost));
+}
+
+int dw_hip_graph_get_output_bytes(dw_hip_graph_runtime* rth, const char* name, void* data, size_t len) {
+  API_BEGIN
+  dw::Runtime& rt = R(rth);
+  if (!name) dw::fail(DW_ERR_INVALID, "null name");
+  std::vector<uint8_t> buf;
+  download_tensor(rt, name, buf);
+  if (len != buf.size())
+    dw::fail(DW_ERR_RUNTIME, "output size mismatch: expected " + std::to_string(buf.size()) + ", got " +
+                                 std::to_string(len));
+  memcpy(data, buf.data(), len);
+  API_END
+}
+
+int dw_hip_graph_get_output_f32(dw_hip_graph_runtime* rth, const char* name, float* data, size_t count) {
+  API_BEGIN
+  dw::Runtime& rt = R(rth);
+  if (!name) dw::fail(DW_ERR_INVALID, "null name");
+  dw::RtTensor& t = rt.T(name);
+  std::vector<uint8_t> buf;
+  download_tensor(rt, name, buf);
+  const size_t n = (size_t)(t.pixels() * t.c);
+  if (count != n) dw::fail(DW_ERR_RUNTIME, "output size mismatch");
+  if (t.dtype == dw::F32) {
+    memcpy(data, buf.data(), n * 4);
+  } else if (t.dtype == dw::F16) {
+    const uint16_t* h = (const uint16_t*)buf.data();
+    for (size_t i = 0; i < n; ++i) data[i] = f16_to_f32_ref(h[i]);
+  } else if (t.dtype == dw::U8) {
+    for (size_t i = 0; i < n; ++i) data[i] = (float)((int)buf[i] - t.zp) * t.scale;
+  } else {
+    dw::fail(DW_ERR_RUNTIME, "unsupported dtype for get_output_f32");
+  }
+  API_END
+}
+
+int dw_hip_graph_tensor_bytes(dw_hip_graph_runtime* rth, const char* name, size_t* len) {
+  API_BEGIN
+  dw::Runtime& rt = R(rth);
+  if (!name || !len) dw::fail(DW_ERR_INVALID, "null argument");
+  *len = rt.T(name).bytes();
+  API_END
+}
+
+int dw_hip_graph_enable_capture(dw_hip_graph_runtime* rth, int enable) {
+  API_BEGIN
+  dw::Runtime& rt = R(rth);
+  rt.capture = enable != 0;
+  API_END
+}
+
+int dw_hip_graph_num_launches(dw_hip_graph_runtime* rth) {
+  if (!rth) return -1;
+  return (int)rth->rt.launches.size();
+}
+
+const char* dw_hip_graph_launch_info(dw_hip_graph_runtime* rth, int index) {
+  if (!rth || index < 0 || index >= (int)rth->rt.launches.size()) return "";
+  dw::Runtime& rt = rth->rt;
+  if (rt.info.size() != rt.launches.size()) {
+    rt.info.clear();
+    for (auto& L : rt.launches) {
+      char b[64];
+      snprintf(b, sizeof b, " %.17g %.17g", L.work, L.bytes);
+      rt.info.push_back(L.kernel + " " + L.op + b);
+    }
+  }
+  return rt.info[index].c_str();
+}
+
+int dw_hip_graph_run_profiled(dw_hip_graph_runtime* rth, float* launch_ms) {
+  API_BEGIN
+  dw::Runtime& rt = R(rth);
+  if (!launch_ms) dw::fail(DW_ERR_INVALID, "null output");
+  const size_t n = rt.launches.size();
+  std::vector<hipEvent_t> ev(n + 1);
+  for (auto& e : ev) DW_HIP(hipEventCreate(&e));
+  hipStream_t st = rt.be->stream;
+  DW_HIP(hipEventRecord(ev[0], st));
+  for (size_t i = 0; i < n; ++i) {
+    rt.launches[i].fn(st);
+    DW_HIP(hipEventRecord(ev[i + 1], st));
+  }
+  DW_HIP(hipEventSynchronize(ev[n]));
+  for (size_t i = 0; i < n; ++i) DW_HIP(hipEventElapsedTime(&launch_ms[i], ev[i], ev[i + 1]));
+  for (auto& e : ev) (void)hipEventDestroy(e);
+  API_END
+}
+
+// Calibrator (crates/dragonwing-onnx/src/calibration.rs:90-260): runs the F32
+// graph on the GPU over `num_images` inputs (in batches of the graph's N),
+// records per-tensor min/max (calibration.rs:56-69) and stores the ranges in
+// the graph for dw_graph_quantize_qdq.
+int dw_hip_calibrate(dw_hip_backend* be, dw_graph* gh, const char* input_name, const float* images,
+                     size_t floats_per_image, int num_images) {
+  API_BEGIN
+  dw::Backend* b = Bk(be);
+  if (!gh || !images || !input_name) dw::fail(DW_ERR_INVALID, "null argument");
+  if (gh->g.dtype != DW_GRAPH_F32) dw::fail(DW_ERR_RUNTIME, "calibration needs the F32 graph");
+  gh->g.json.clear();
+  dw::Runtime rt;
+  rt.build(b, gh->g, true);
+  dw::RtTensor& in = rt.T(input_name);
+  const int batch = (int)in.n;
+  if (floats_per_image * batch != (size_t)(in.pixels() * in.c))
+    dw::fail(DW_ERR_INVALID, "calibration: image size does not match the graph input");
+  if (num_images <= 0 || num_images % batch != 0)
+    dw::fail(DW_ERR_INVALID, "calibration: image count must be a multiple of the graph batch");
+  std::map<std::string, std::pair<float, float>> acc;
+  std::vector<float> mm(rt.stats_names.size() * 2);
+  for (int i0 = 0; i0 < num_images; i0 += batch) {
+    DW_HIP(hipMemcpy(in.base, images + (size_t)i0 * floats_per_image, floats_per_image * batch * 4,
+                     hipMemcpyHostToDevice));
+    rt.run();
+    DW_HIP(hipStreamSynchronize(b->stream));
+    DW_HIP(hipMemcpy(mm.data(), rt.stats_dev, mm.size() * 4, hipMemcpyDeviceToHost));
+    for (size_t k = 0; k < rt.stats_names.size(); ++k) {
+      auto it = acc.find(rt.stats_names[k]);
+      if (it == acc.end())
+        acc[rt.stats_names[k]] = {mm[2 * k], mm[2 * k + 1]};
+      else
+        it->second = {std::min(it->second.first, mm[2 * k]), std::max(it->second.second, mm[2 * k + 1])};
+    }
+  }
+  for (auto& kv : acc) {
+    if (!(kv.second.first <= kv.second.second)) continue;  // never written
+    dw::TensorInfo& ti = gh->g.tensor(kv.first);
+    ti.has_range = true;
+    ti.rmin = kv.second.first;
+    ti.rmax = kv.second.second;
+  }
+  API_END
+}
+
+}  // extern "C"

@@ -1,0 +1,381 @@
+/*
+ * dw_hip.h — C ABI of the MI355X (gfx950) execution backend for
+ * dragonwing-edge-rs.
+ *
+ * Everything here is plain C: opaque handles, pointers, sizes and int status
+ * codes.  No torch or HIP types cross this boundary.  Reference citations are
+ * relative to the dragonwing-edge-rs source tree.
+ *
+ * Conventions
+ *   - Every function returning `int` returns DW_OK (0) or a negative
+ *     dw_status; the matching message is available from dw_last_error()
+ *     (thread-local, valid until the next failing call on the same thread).
+ *     This is the C form of dragonwing_core::Error::{Io,Unsupported,Backend}
+ *     (crates/dragonwing-core/src/error.rs:13-20).
+ *   - Buffers are byte spans; element types travel with the op call
+ *     (crates/dragonwing-core/src/backend.rs:21-33).
+ *   - All device work is queued on the backend's single HIP stream, in call
+ *     order.  dw_hip_download synchronizes first; dw_hip_upload is complete on
+ *     return (backend.rs:158-185).
+ *   - Tensor layouts: activations NHWC ([N][H][W][C], C fastest); conv
+ *     kernels HWIO ([kh][kw][c_in][c_out]) — the layout produced by
+ *     convert_nchw_to_nhwc (crates/dragonwing-onnx/src/graph.rs:261-276).
+ */
+#ifndef DW_HIP_H
+#define DW_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------------ */
+/* Status codes and errors                                                   */
+/* ------------------------------------------------------------------------ */
+
+typedef enum dw_status {
+  DW_OK = 0,
+  DW_ERR_BACKEND = -1,     /* Error::Backend(String): device/runtime failure */
+  DW_ERR_UNSUPPORTED = -2, /* Error::Unsupported: op/shape/dtype not handled */
+  DW_ERR_IO = -3,          /* Error::Io                                       */
+  DW_ERR_INVALID = -4,     /* size mismatch / bad argument (Error::Backend)  */
+  DW_ERR_RUNTIME = -5      /* dragonwing_onnx::Error::Runtime               */
+} dw_status;
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* dw_last_error(void);
+
+/* ------------------------------------------------------------------------ */
+/* Backend — replaces dragonwing_core::Backend for VulkanBackend             */
+/* (crates/dragonwing-core/src/backend.rs:127-199,                          */
+/*  crates/dragonwing-vulkan/src/lib.rs:246-292)                            */
+/* ------------------------------------------------------------------------ */
+
+typedef struct dw_hip_backend dw_hip_backend;
+typedef struct dw_hip_buffer dw_hip_buffer;
+
+/* BufferKind (backend.rs:89-101).  Only Storage exists. */
+#define DW_BUFFER_STORAGE 0
+
+/* Create a backend on HIP device `device` (one stream, default priority).
+ * Counterpart of VulkanBackend::new (crates/dragonwing-vulkan/src/lib.rs). */
+int dw_hip_backend_create(int device, dw_hip_backend** out);
+/* Drop: frees the stream and every internal workspace.  Buffers must be freed
+ * before their backend (backend.rs:75-79). */
+void dw_hip_backend_destroy(dw_hip_backend* be);
+/* Backend::name (backend.rs:142): "hip-gfx950". */
+const char* dw_hip_backend_name(const dw_hip_backend* be);
+
+/* Backend::alloc (backend.rs:146-156): contents unspecified; never shrinks. */
+int dw_hip_alloc(dw_hip_backend* be, size_t len_bytes, int kind, dw_hip_buffer** out);
+/* Drop for a buffer (explicit in C). NULL is ignored. */
+void dw_hip_buffer_free(dw_hip_buffer* buf);
+/* BackendBuffer::len_bytes (backend.rs:80-87). */
+size_t dw_hip_buffer_len_bytes(const dw_hip_buffer* buf);
+/* Device address of the buffer (for interop with other HIP code). */
+void* dw_hip_buffer_device_ptr(const dw_hip_buffer* buf);
+
+/* Backend::upload (backend.rs:158-173): len must equal len_bytes(dst),
+ * otherwise DW_ERR_INVALID; complete on return. */
+int dw_hip_upload(dw_hip_backend* be, dw_hip_buffer* dst, const void* src, size_t len);
+/* Backend::download (backend.rs:175-185): len must equal len_bytes(src);
+ * synchronizes the stream first. */
+int dw_hip_download(dw_hip_backend* be, const dw_hip_buffer* src, void* dst, size_t len);
+/* Backend::synchronize (backend.rs:187-198). */
+int dw_hip_synchronize(dw_hip_backend* be);
+
+/* ------------------------------------------------------------------------ */
+/* Op functions.  Free functions taking the backend, as in                   */
+/* dragonwing_vulkan::ops (crates/dragonwing-vulkan/src/ops.rs).  Buffer     */
+/* sizes are validated exactly (ops.rs:2327-2346) and ops are queued on the  */
+/* backend stream (no implicit sync).                                        */
+/* ------------------------------------------------------------------------ */
+
+/* Activation fused into an op's epilogue. */
+#define DW_ACT_NONE 0
+#define DW_ACT_RELU 1 /* ops::relu_f32 / relu_fp16 (ops.rs:189-220, 345-352) */
+#define DW_ACT_SILU 2 /* sigmoid_fp16 then mul_fp16 (ops.rs:1881, 1959)     */
+
+/* conv2d_f32_nhwc (crates/dragonwing-vulkan/src/ops.rs:1308; CPU
+ * crates/dragonwing-cpu/src/ops.rs:1356-1436).  Direct convolution with the
+ * reference's accumulation order (kh -> kw -> ic, one fused multiply-add per
+ * term), so results are bit-identical to dragonwing-cpu.  Symmetric padding. */
+int dw_hip_conv2d_f32_nhwc(dw_hip_backend* be, const dw_hip_buffer* input,
+                           const dw_hip_buffer* kernel, dw_hip_buffer* output, size_t n,
+                           size_t h_in, size_t w_in, size_t c_in, size_t c_out, size_t k_h,
+                           size_t k_w, size_t stride_h, size_t stride_w, size_t pad_h,
+                           size_t pad_w);
+
+/* Conv2d + bias + activation, fp32: CpuGraphRuntime::dispatch_conv2d with
+ * bias (crates/dragonwing-onnx/src/runtime.rs:1445-1460) followed by Relu
+ * (runtime.rs:944-1002), fused in one launch.  `bias` may be NULL.
+ * Bit-identical to the reference's op sequence. */
+int dw_hip_conv2d_bias_act_f32_nhwc(dw_hip_backend* be, const dw_hip_buffer* input,
+                                    const dw_hip_buffer* kernel, const dw_hip_buffer* bias,
+                                    dw_hip_buffer* output, size_t n, size_t h_in, size_t w_in,
+                                    size_t c_in, size_t c_out, size_t k_h, size_t k_w,
+                                    size_t stride_h, size_t stride_w, size_t pad_h,
+                                    size_t pad_w, int act);
+
+/* conv2d_fp16_nhwc (vulkan ops.rs:1385; CPU ops.rs:1442-1500, _mt
+ * :2572-2651), f16 storage (IEEE binary16 bits), then optional bias and
+ * activation with the reference's f16 rounding points (runtime.rs:1483-1498,
+ * ops.rs:1881-1967).  `exact`=1 uses the reference accumulation order
+ * (bit-identical); `exact`=0 uses the fp16 MFMA implicit-GEMM kernel
+ * (fp32 accumulation in another order: within fp16 tolerance).
+ * MFMA path requires c_in % 8 == 0 and c_out % 4 == 0. */
+int dw_hip_conv2d_bias_act_f16_nhwc(dw_hip_backend* be, const dw_hip_buffer* input,
+                                    const dw_hip_buffer* kernel, const dw_hip_buffer* bias,
+                                    dw_hip_buffer* output, size_t n, size_t h_in, size_t w_in,
+                                    size_t c_in, size_t c_out, size_t k_h, size_t k_w,
+                                    size_t stride_h, size_t stride_w, size_t pad_h,
+                                    size_t pad_w, int act, int exact);
+
+/* depthwise_conv2d_fp16_nhwc_mt (crates/dragonwing-cpu/src/ops.rs:2819-2933)
+ * with channel_multiplier 1, then bias and activation as in
+ * CpuGraphRuntime (runtime.rs:1467-1498).  kernel: [k_h][k_w][c] f16,
+ * bias: [c] f16 or NULL.  Requires c % 8 == 0. */
+int dw_hip_depthwise_conv2d_f16_nhwc(dw_hip_backend* be, const dw_hip_buffer* input,
+                                     const dw_hip_buffer* kernel, const dw_hip_buffer* bias,
+                                     dw_hip_buffer* output, size_t n, size_t h_in, size_t w_in,
+                                     size_t c, size_t k_h, size_t k_w, size_t stride_h,
+                                     size_t stride_w, size_t pad_h, size_t pad_w, int act);
+
+/* depthwise_conv2d_f32_nhwc_mt (ops.rs:2734-2815) + bias + activation. */
+int dw_hip_depthwise_conv2d_f32_nhwc(dw_hip_backend* be, const dw_hip_buffer* input,
+                                     const dw_hip_buffer* kernel, const dw_hip_buffer* bias,
+                                     dw_hip_buffer* output, size_t n, size_t h_in, size_t w_in,
+                                     size_t c, size_t k_h, size_t k_w, size_t stride_h,
+                                     size_t stride_w, size_t pad_h, size_t pad_w, int act);
+
+/* QLinearConv u8 x s8 -> u8 (ONNX QLinearConv; no counterpart in the
+ * reference, whose INT8 is symmetric s8 — it generalises
+ * conv2d_requant_relu_i8_packed, crates/dragonwing-vulkan/src/ops.rs:2294).
+ *   acc[c]  = sum (x - x_zp) * w[c] + bias[c]          (int32, exact)
+ *   y       = clamp(rint((float)acc * M[c]) + y_zp, 0, 255)
+ *   M[c]    = (x_scale * w_scales[c]) / y_scale         (f32)
+ * rint rounds half to even.  Padding uses the zero point (real 0).
+ * input u8 NHWC, kernel s8 HWIO, bias int32[c_out] device buffer or NULL,
+ * w_scales: host array of c_out floats.  Requires c_in % 16 == 0 and
+ * c_out % 4 == 0.  INT8 MFMA implicit GEMM (v_mfma_i32_16x16x64_i8). */
+int dw_hip_qlinearconv_u8s8(dw_hip_backend* be, const dw_hip_buffer* input,
+                            const dw_hip_buffer* kernel, const dw_hip_buffer* bias,
+                            dw_hip_buffer* output, size_t n, size_t h_in, size_t w_in,
+                            size_t c_in, size_t c_out, size_t k_h, size_t k_w, size_t stride_h,
+                            size_t stride_w, size_t pad_h, size_t pad_w, float x_scale,
+                            int x_zp, const float* w_scales, float y_scale, int y_zp);
+
+/* conv2d_i8_nhwc (crates/dragonwing-cpu/src/ops.rs:3086-3142): s8 x s8 ->
+ * int32 accumulator, zero padding.  Requires c_in % 16 == 0, c_out % 4 == 0. */
+int dw_hip_conv2d_i8_nhwc(dw_hip_backend* be, const dw_hip_buffer* input,
+                          const dw_hip_buffer* kernel, dw_hip_buffer* output_i32, size_t n,
+                          size_t h_in, size_t w_in, size_t c_in, size_t c_out, size_t k_h,
+                          size_t k_w, size_t stride_h, size_t stride_w, size_t pad_h,
+                          size_t pad_w);
+
+/* conv2d_requant_relu_i8_packed (crates/dragonwing-vulkan/src/ops.rs:2294-2430)
+ * with the CPU semantics it stands for: conv2d_i8_nhwc, then
+ * requantize_i32_to_i8 (ops.rs:3380-3386: clamp to [-128,127], round half
+ * away from zero), then relu_i8 when do_relu.  One per-tensor scale. */
+int dw_hip_conv2d_requant_relu_i8(dw_hip_backend* be, const dw_hip_buffer* input,
+                                  const dw_hip_buffer* kernel, dw_hip_buffer* output, size_t n,
+                                  size_t h_in, size_t w_in, size_t c_in, size_t c_out, size_t k_h,
+                                  size_t k_w, size_t stride_h, size_t stride_w, size_t pad_h,
+                                  size_t pad_w, float requant_scale, int do_relu);
+
+/* Elementwise ops.  `count` elements; all buffers exactly count*esize. */
+int dw_hip_relu_f32(dw_hip_backend* be, const dw_hip_buffer* x, dw_hip_buffer* y, size_t count);      /* ops.rs:189-220  */
+int dw_hip_relu_fp16(dw_hip_backend* be, const dw_hip_buffer* x, dw_hip_buffer* y, size_t count);     /* ops.rs:345-352  */
+int dw_hip_add_f32(dw_hip_backend* be, const dw_hip_buffer* a, const dw_hip_buffer* b, dw_hip_buffer* y, size_t count);  /* ops.rs:363-384 */
+int dw_hip_add_fp16(dw_hip_backend* be, const dw_hip_buffer* a, const dw_hip_buffer* b, dw_hip_buffer* y, size_t count); /* ops.rs:434-442 */
+int dw_hip_mul_f32(dw_hip_backend* be, const dw_hip_buffer* a, const dw_hip_buffer* b, dw_hip_buffer* y, size_t count);  /* ops.rs:1899-1919 */
+int dw_hip_mul_fp16(dw_hip_backend* be, const dw_hip_buffer* a, const dw_hip_buffer* b, dw_hip_buffer* y, size_t count); /* ops.rs:1959-1967 */
+int dw_hip_sigmoid_f32(dw_hip_backend* be, const dw_hip_buffer* x, dw_hip_buffer* y, size_t count);   /* ops.rs:1852-1870 */
+int dw_hip_sigmoid_fp16(dw_hip_backend* be, const dw_hip_buffer* x, dw_hip_buffer* y, size_t count);  /* ops.rs:1881-1888 */
+/* silu_f32 (crates/dragonwing-vulkan/src/ops.rs:2214): x * sigmoid(x). */
+int dw_hip_silu_f32(dw_hip_backend* be, const dw_hip_buffer* x, dw_hip_buffer* y, size_t count);
+/* Sigmoid then Mul in f16 with both f16 roundings (the unfused CPU pair). */
+int dw_hip_silu_fp16(dw_hip_backend* be, const dw_hip_buffer* x, dw_hip_buffer* y, size_t count);
+/* bias_add_f32_nhwc (vulkan ops.rs:2432): y[i] += bias[i % c], in place. */
+int dw_hip_bias_add_f32_nhwc(dw_hip_backend* be, dw_hip_buffer* y, const dw_hip_buffer* bias, size_t count, size_t c);
+
+/* INT8 (reference symmetric scheme, zero point 0, round half away). */
+int dw_hip_requantize_i32_to_i8(dw_hip_backend* be, const dw_hip_buffer* x_i32, dw_hip_buffer* y_i8, size_t count, float requant_scale); /* ops.rs:3380-3386 */
+int dw_hip_quantize_f32_to_i8(dw_hip_backend* be, const dw_hip_buffer* x, dw_hip_buffer* y_i8, size_t count, float scale);           /* ops.rs:3503-3525 */
+int dw_hip_dequantize_i8_to_f32(dw_hip_backend* be, const dw_hip_buffer* x_i8, dw_hip_buffer* y, size_t count, float scale);         /* ops.rs:3439-3457 */
+int dw_hip_add_i8(dw_hip_backend* be, const dw_hip_buffer* a, const dw_hip_buffer* b, dw_hip_buffer* y, size_t count, float scale_a_over_y, float scale_b_over_y); /* ops.rs:3176-3209 */
+int dw_hip_relu_i8(dw_hip_backend* be, const dw_hip_buffer* x, dw_hip_buffer* y, size_t count); /* ops.rs:3301-3320 */
+
+/* ONNX-style u8 quantization (zero point, round half to even). */
+/* QuantizeLinear: y = clamp(rint(x / scale) + zp, 0, 255), x f16. */
+int dw_hip_quantize_linear_f16_u8(dw_hip_backend* be, const dw_hip_buffer* x, dw_hip_buffer* y, size_t count, float scale, int zp);
+/* DequantizeLinear: y = f16((float)(q - zp) * scale). */
+int dw_hip_dequantize_linear_u8_f16(dw_hip_backend* be, const dw_hip_buffer* x, dw_hip_buffer* y, size_t count, float scale, int zp);
+/* QLinearAdd: y = clamp(rint((a-za)*(sa/sy) + (b-zb)*(sb/sy)) + zy, 0, 255). */
+int dw_hip_qlinear_add_u8(dw_hip_backend* be, const dw_hip_buffer* a, const dw_hip_buffer* b, dw_hip_buffer* y, size_t count,
+                          float a_scale, int a_zp, float b_scale, int b_zp, float y_scale, int y_zp);
+/* y = lut[x] for a 256-entry host table (quantized activations such as SiLU). */
+int dw_hip_lut_u8(dw_hip_backend* be, const dw_hip_buffer* x, dw_hip_buffer* y, size_t count, const uint8_t* lut256);
+
+/* Data-movement glue, NHWC.  dtype: DW_DTYPE_* element type. */
+#define DW_DTYPE_F32 0
+#define DW_DTYPE_F16 1
+#define DW_DTYPE_I8 2
+#define DW_DTYPE_U8 3
+#define DW_DTYPE_I32 4
+
+/* maxpool2d_f32_nhwc (ops.rs:1513-1552), extended with padding: padded
+ * positions never win (ONNX MaxPool; the reference ignores pads,
+ * runtime.rs:902-904).  pads = top, left, bottom, right. */
+int dw_hip_maxpool2d_nhwc(dw_hip_backend* be, int dtype, const dw_hip_buffer* x, dw_hip_buffer* y,
+                          size_t n, size_t h_in, size_t w_in, size_t c, size_t pool_h,
+                          size_t pool_w, size_t stride_h, size_t stride_w, size_t pad_t,
+                          size_t pad_l, size_t pad_b, size_t pad_r);
+/* resize_f32 Nearest (ops.rs:2320-2351): ih = clamp(round((oh+0.5)*h_in/h_out - 0.5)). */
+int dw_hip_resize_nearest_nhwc(dw_hip_backend* be, int dtype, const dw_hip_buffer* x, dw_hip_buffer* y,
+                               size_t n, size_t h_in, size_t w_in, size_t h_out, size_t w_out, size_t c);
+/* concat_fp16 / concat_f32 along axis 3 (ops.rs:2248-2299). */
+int dw_hip_concat_channels_nhwc(dw_hip_backend* be, int dtype, const dw_hip_buffer* const* inputs,
+                                const size_t* channels, size_t num_inputs, dw_hip_buffer* y,
+                                size_t pixels);
+/* split_f32 along axis 3 (ops.rs:2407-2456). */
+int dw_hip_split_channels_nhwc(dw_hip_backend* be, int dtype, const dw_hip_buffer* x,
+                               dw_hip_buffer* const* outputs, const size_t* channels,
+                               size_t num_outputs, size_t pixels);
+
+/* ------------------------------------------------------------------------ */
+/* Graph IR — the C form of dragonwing_onnx::Graph / CompiledOp / OpParams   */
+/* (crates/dragonwing-onnx/src/graph.rs:18-31, builder.rs:204-361), plus the */
+/* compiler passes that produce the graphs this backend runs.               */
+/* ------------------------------------------------------------------------ */
+
+typedef struct dw_graph dw_graph;
+
+/* OpParams discriminants (builder.rs:219-361), then this backend's
+ * quantized-ONNX extensions (no counterpart in the reference). */
+typedef enum dw_op_kind {
+  DW_OP_NONE = 0,        /* OpParams::None: op_type decides (Relu, SiLU, ...) */
+  DW_OP_CONV2D = 1,      /* OpParams::Conv2d                                  */
+  DW_OP_ADD = 2,         /* OpParams::Add                                     */
+  DW_OP_MUL = 3,         /* OpParams::Mul                                     */
+  DW_OP_SIGMOID = 4,     /* OpParams::Sigmoid                                 */
+  DW_OP_MAXPOOL = 5,     /* OpParams::MaxPool                                 */
+  DW_OP_CONCAT = 6,      /* OpParams::Concat                                  */
+  DW_OP_SPLIT = 7,       /* OpParams::Split                                   */
+  DW_OP_RESIZE = 8,      /* OpParams::Resize                                  */
+  DW_OP_BATCHNORM = 9,   /* ONNX BatchNormalization before fold_batchnorm     */
+  DW_OP_REQUANTIZE = 10, /* OpParams::Requantize                              */
+  DW_OP_ADD_QUANTIZED = 11, /* OpParams::AddQuantized                         */
+  DW_OP_QUANTIZE = 12,   /* OpParams::Quantize                                */
+  DW_OP_DEQUANTIZE = 13, /* OpParams::Dequantize                              */
+  DW_OP_CONV2D_REQUANT_RELU_I8 = 14, /* OpParams::Conv2dRequantReluI8Nhwc     */
+  /* extensions */
+  DW_OP_QLINEAR_CONV = 32,  /* QLinearConv (+ fused LUT activation, + QLinearAdd residual) */
+  DW_OP_QUANTIZE_LINEAR = 33,
+  DW_OP_DEQUANTIZE_LINEAR = 34,
+  DW_OP_QLINEAR_ADD = 35,
+  DW_OP_QLINEAR_LUT = 36    /* quantized elementwise activation by 256-entry table */
+} dw_op_kind;
+
+typedef struct dw_op_params {
+  int kind;                 /* dw_op_kind                                      */
+  int kernel_shape[2];      /* Conv2d / MaxPool: [H, W]                        */
+  int strides[2];
+  int pads[4];              /* [top, left, bottom, right]                      */
+  int dilations[2];
+  int group;
+  int axis;                 /* Concat / Split                                 */
+  int split_sizes[8];       /* Split                                          */
+  int num_splits;
+  int out_h, out_w;         /* Resize                                          */
+  int mode_nearest;         /* Resize: 1 = "nearest", 0 = "linear"            */
+  float scale;              /* Requantize/Quantize/Dequantize scale; Conv2dRequantReluI8 requant_scale */
+  float scale_a_over_out;   /* AddQuantized                                   */
+  float scale_b_over_out;
+  int has_relu;             /* Conv2dRequantReluI8Nhwc                        */
+  float epsilon;            /* BatchNormalization                             */
+  int act;                  /* QLinearLUT: DW_ACT_* the table encodes         */
+} dw_op_params;
+
+/* Graph dtypes (dragonwing_core::Dtype subset, crates/dragonwing-core/src/dtype.rs). */
+#define DW_GRAPH_F32 0
+#define DW_GRAPH_F16 1
+#define DW_GRAPH_QU8 3 /* quantized: u8 activations with zero points (QDQ-folded) */
+
+int dw_graph_create(int dtype, dw_graph** out);
+void dw_graph_destroy(dw_graph* g);
+/* Declare a tensor: name, shape (rank <= 4), element dtype (DW_DTYPE_*). */
+int dw_graph_add_tensor(dw_graph* g, const char* name, const int64_t* dims, int rank, int dtype);
+/* Attach initializer bytes to a declared tensor (weights, biases, BN params). */
+int dw_graph_set_initializer(dw_graph* g, const char* name, const void* data, size_t len);
+/* Append a CompiledOp.  Empty-string inputs are optional-absent. */
+int dw_graph_add_op(dw_graph* g, const char* name, const char* op_type, const char* const* inputs,
+                    int num_inputs, const char* const* outputs, int num_outputs,
+                    const dw_op_params* params);
+int dw_graph_set_io(dw_graph* g, const char* const* inputs, int num_inputs,
+                    const char* const* outputs, int num_outputs);
+
+/* Passes (crates/dragonwing-onnx/src/graph.rs, fusion.rs, quantize.rs). */
+int dw_graph_fold_batchnorm(dw_graph* g);         /* graph.rs:521-690 (f64 math)   */
+int dw_graph_convert_nchw_to_nhwc(dw_graph* g);   /* graph.rs:248-290              */
+int dw_graph_apply_fusion_passes(dw_graph* g, int* num_fused); /* fusion.rs:42-348 */
+int dw_graph_convert_to_f16(dw_graph* g);          /* runtime.rs:800-811: f32 initializers -> F16 RNE */
+
+/* Calibration statistics (calibration.rs:56-69) and the QDQ quantizer that
+ * turns an F32 graph into a DW_GRAPH_QU8 graph of QLinearConv ops. */
+int dw_graph_set_activation_range(dw_graph* g, const char* name, float min_v, float max_v);
+int dw_graph_quantize_qdq(dw_graph* g, const char* const* keep_f16_ops, int num_keep);
+/* Calibrator::new + feed + compute_params (calibration.rs:90-260) on the GPU:
+ * runs the F32 NHWC graph over `num_images` images (host f32, NHWC, each
+ * floats_per_image values; a multiple of the graph batch), records per-tensor
+ * min/max and stores the ranges in the graph. */
+int dw_hip_calibrate(dw_hip_backend* be, dw_graph* g, const char* input_name, const float* images,
+                     size_t floats_per_image, int num_images);
+
+/* Introspection (for oracles and tools): JSON text describing dtype, tensors,
+ * ops, params and quantization parameters.  The string stays valid until the
+ * graph is modified or destroyed. */
+const char* dw_graph_to_json(dw_graph* g);
+/* Initializer bytes of a tensor (NULL/0 if none). */
+int dw_graph_get_initializer(dw_graph* g, const char* name, const void** data, size_t* len);
+
+/* ------------------------------------------------------------------------ */
+/* Graph runtime — VulkanGraphRuntime's API                                  */
+/* (crates/dragonwing-onnx/src/vulkan_runtime.rs:115-469, :2113-2141).      */
+/* ------------------------------------------------------------------------ */
+
+typedef struct dw_hip_graph_runtime dw_hip_graph_runtime;
+
+/* VulkanGraphRuntime::new: plans device memory, packs weights, builds the
+ * launch list.  The graph is copied; it can be destroyed afterwards. */
+int dw_hip_graph_runtime_create(dw_hip_backend* be, const dw_graph* g, dw_hip_graph_runtime** out);
+void dw_hip_graph_runtime_destroy(dw_hip_graph_runtime* rt);
+/* set_input_f32 (vulkan_runtime.rs:238): converts to the graph dtype (F16 RNE). */
+int dw_hip_graph_set_input_f32(dw_hip_graph_runtime* rt, const char* name, const float* data, size_t count);
+/* set_input_bytes (vulkan_runtime.rs:2113): raw bytes in the tensor's dtype. */
+int dw_hip_graph_set_input_bytes(dw_hip_graph_runtime* rt, const char* name, const void* data, size_t len);
+/* run (vulkan_runtime.rs:359-419): enqueue every op; returns without waiting. */
+int dw_hip_graph_run(dw_hip_graph_runtime* rt);
+/* get_output_f32 (vulkan_runtime.rs:296): synchronizes, converts to f32. */
+int dw_hip_graph_get_output_f32(dw_hip_graph_runtime* rt, const char* name, float* data, size_t count);
+/* get_output_bytes (vulkan_runtime.rs:2131): synchronizes, raw bytes. */
+int dw_hip_graph_get_output_bytes(dw_hip_graph_runtime* rt, const char* name, void* data, size_t len);
+/* Byte size of a graph tensor as the runtime stores it. */
+int dw_hip_graph_tensor_bytes(dw_hip_graph_runtime* rt, const char* name, size_t* len);
+/* Capture the launch list into a HIP graph and replay it on later runs
+ * (the analogue of OpsRecorder's single command buffer, record.rs:49-679). */
+int dw_hip_graph_enable_capture(dw_hip_graph_runtime* rt, int enable);
+/* Number of kernel launches per run, and a per-launch description
+ * ("<kernel> <op name> <algorithmic ops> <bytes>"). */
+int dw_hip_graph_num_launches(dw_hip_graph_runtime* rt);
+const char* dw_hip_graph_launch_info(dw_hip_graph_runtime* rt, int index);
+/* One run with a HIP event pair around every launch; writes per-launch
+ * milliseconds (array of dw_hip_graph_num_launches floats). */
+int dw_hip_graph_run_profiled(dw_hip_graph_runtime* rt, float* launch_ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* DW_HIP_H */

@@ -1,0 +1,429 @@
+"""dragonwing-cpu oracle — TEST INFRASTRUCTURE ONLY.
+
+numpy-level access to ``oracle/dw_oracle.cpp``, the CPU restatement of the
+dragonwing-edge-rs hot-path algorithms (``crates/dragonwing-cpu/src/ops.rs``,
+``crates/dragonwing-core/src/dtype.rs``, ``crates/dragonwing-onnx/src/runtime.rs``)
+plus the ONNX quantized extensions the reference lacks.  Only ``tests/``,
+``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may use
+this package, and only as the checker or the timed CPU baseline — never as
+part of the product path.
+
+Parity status of each function is recorded in the test that pins it
+(``tests/test_oracle_*.py``).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIBPATH = HERE / "build" / "libdworacle.so"
+
+_lib = None
+
+
+def build() -> Path:
+    """Compiles the oracle with its Makefile (g++ -O3, no contraction)."""
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIBPATH
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIBPATH.exists():
+            build()
+        _lib = C.CDLL(str(LIBPATH))
+        _declare(_lib)
+    return _lib
+
+
+_P = C.c_void_p
+_Z = C.c_size_t
+_F = C.c_float
+_I = C.c_int
+
+
+def _declare(L: C.CDLL) -> None:
+    sig = {
+        "dwo_f16_from_f32": (C.c_uint16, [_F]),
+        "dwo_f16_to_f32": (_F, [C.c_uint16]),
+        "dwo_f32_to_f16_array": (None, [_P, _P, _Z]),
+        "dwo_f16_to_f32_array": (None, [_P, _P, _Z]),
+        "dwo_num_cpus": (_I, []),
+        "dwo_conv2d_f32_nhwc": (None, [_P, _P, _P] + [_Z] * 11),
+        "dwo_conv2d_f32_nhwc_mt": (None, [_P, _P, _P] + [_Z] * 11 + [_I]),
+        "dwo_conv2d_fp16_nhwc_mt": (None, [_P, _P, _P] + [_Z] * 11 + [_I]),
+        "dwo_depthwise_conv2d_f32_nhwc_mt": (None, [_P, _P, _P] + [_Z] * 11 + [_I]),
+        "dwo_depthwise_conv2d_fp16_nhwc_mt": (None, [_P, _P, _P] + [_Z] * 11 + [_I]),
+        "dwo_conv2d_i8_nhwc": (None, [_P, _P, _P] + [_Z] * 11),
+        "dwo_conv2d_i8_nhwc_rowpar": (None, [_P, _P, _P] + [_Z] * 11 + [_I]),
+        "dwo_bias_add_f32_nhwc": (None, [_P, _P, _Z, _Z]),
+        "dwo_bias_add_f16_nhwc": (None, [_P, _P, _Z, _Z]),
+        "dwo_relu_f32": (None, [_P, _P, _Z]),
+        "dwo_relu_fp16": (None, [_P, _P, _Z]),
+        "dwo_add_f32": (None, [_P, _P, _P, _Z]),
+        "dwo_add_fp16": (None, [_P, _P, _P, _Z]),
+        "dwo_mul_f32": (None, [_P, _P, _P, _Z]),
+        "dwo_mul_fp16": (None, [_P, _P, _P, _Z]),
+        "dwo_sigmoid_f32": (None, [_P, _P, _Z]),
+        "dwo_sigmoid_fp16": (None, [_P, _P, _Z]),
+        "dwo_requantize_i32_to_i8": (None, [_P, _P, _Z, _F]),
+        "dwo_quantize_f32_to_i8": (None, [_P, _P, _Z, _F]),
+        "dwo_dequantize_i8_to_f32": (None, [_P, _P, _Z, _F]),
+        "dwo_add_i8": (None, [_P, _P, _P, _Z, _F, _F]),
+        "dwo_relu_i8": (None, [_P, _P, _Z]),
+        "dwo_scale_from_range": (_F, [_F, _F]),
+        "dwo_quantize_weights_per_channel": (None, [_P, _P, _P, _Z, _Z]),
+        "dwo_maxpool2d_f32_nhwc": (None, [_P, _P] + [_Z] * 8),
+        "dwo_resize_nearest_nhwc": (None, [_P, _P] + [_Z] * 7),
+        "dwo_concat_channels": (None, [_P, _P, _P, _Z, _Z, _Z]),
+        "dwo_split_channels": (None, [_P, _P, _P, _Z, _Z, _Z]),
+        "dwo_fold_batchnorm": (None, [_P, _P, _P, _P, _P, _P, _P, _F, _Z, _Z]),
+        "dwo_qlinearconv_u8s8": (None, [_P, _P, _P, _P] + [_Z] * 11 + [_F, _I, _P, _F, _I, _I]),
+        "dwo_quantize_linear_f16_u8": (None, [_P, _P, _Z, _F, _I]),
+        "dwo_dequantize_linear_u8_f16": (None, [_P, _P, _Z, _F, _I]),
+        "dwo_qlinear_add_u8": (None, [_P, _P, _P, _Z, _F, _I, _F, _I, _F, _I]),
+        "dwo_silu_lut_u8": (None, [_P, _F, _I, _F, _I]),
+        "dwo_lut_u8": (None, [_P, _P, _Z, _P]),
+        "dwo_maxpool2d_padded_nhwc": (None, [_P, _P] + [_Z] * 13),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+def _p(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+def num_cpus() -> int:
+    return lib().dwo_num_cpus()
+
+
+def default_threads() -> int:
+    return num_cpus()
+
+
+# --- F16 -------------------------------------------------------------------
+def f16_from_f32(x) -> np.ndarray:
+    """F16::from_f32_soft bits (dtype.rs:164-222) of every element."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(x.shape, np.uint16)
+    lib().dwo_f32_to_f16_array(_p(x), _p(y), x.size)
+    return y
+
+
+def f16_to_f32(h) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    y = np.empty(h.shape, np.float32)
+    lib().dwo_f16_to_f32_array(_p(h), _p(y), h.size)
+    return y
+
+
+def out_hw(h, w, kh, kw, sh, sw, ph, pw):
+    return (h + 2 * ph - kh) // sh + 1, (w + 2 * pw - kw) // sw + 1
+
+
+# --- convolutions (NHWC input, HWIO kernel) --------------------------------
+def conv2d_f32_nhwc(x, k, stride=(1, 1), pad=(0, 0), threads=None):
+    """conv2d_f32_nhwc_mt (ops.rs:1756-1837)."""
+    x = np.ascontiguousarray(x, np.float32)
+    k = np.ascontiguousarray(k, np.float32)
+    n, h, w, ci = x.shape
+    kh, kw, ci2, co = k.shape
+    assert ci == ci2
+    ho, wo = out_hw(h, w, kh, kw, stride[0], stride[1], pad[0], pad[1])
+    y = np.empty((n, ho, wo, co), np.float32)
+    lib().dwo_conv2d_f32_nhwc_mt(_p(y), _p(x), _p(k), n, h, w, ci, co, kh, kw, stride[0], stride[1],
+                                 pad[0], pad[1], threads or default_threads())
+    return y
+
+
+def conv2d_f32_nhwc_st(x, k, stride=(1, 1), pad=(0, 0)):
+    """conv2d_f32_nhwc (ops.rs:1356-1436), single thread."""
+    x = np.ascontiguousarray(x, np.float32)
+    k = np.ascontiguousarray(k, np.float32)
+    n, h, w, ci = x.shape
+    kh, kw, _, co = k.shape
+    ho, wo = out_hw(h, w, kh, kw, stride[0], stride[1], pad[0], pad[1])
+    y = np.empty((n, ho, wo, co), np.float32)
+    lib().dwo_conv2d_f32_nhwc(_p(y), _p(x), _p(k), n, h, w, ci, co, kh, kw, stride[0], stride[1],
+                              pad[0], pad[1])
+    return y
+
+
+def conv2d_fp16_nhwc(xh, kh_, stride=(1, 1), pad=(0, 0), threads=None):
+    """conv2d_fp16_nhwc_mt (ops.rs:2572-2651) on f16 bit arrays."""
+    xh = np.ascontiguousarray(xh, np.uint16)
+    kh_ = np.ascontiguousarray(kh_, np.uint16)
+    n, h, w, ci = xh.shape
+    kh, kw, _, co = kh_.shape
+    ho, wo = out_hw(h, w, kh, kw, stride[0], stride[1], pad[0], pad[1])
+    y = np.empty((n, ho, wo, co), np.uint16)
+    lib().dwo_conv2d_fp16_nhwc_mt(_p(y), _p(xh), _p(kh_), n, h, w, ci, co, kh, kw, stride[0], stride[1],
+                                  pad[0], pad[1], threads or default_threads())
+    return y
+
+
+def depthwise_f32(x, k, stride=(1, 1), pad=(0, 0), threads=None):
+    """depthwise_conv2d_f32_nhwc_mt (ops.rs:2734-2815), kernel [kh][kw][c] (multiplier 1)."""
+    x = np.ascontiguousarray(x, np.float32)
+    k = np.ascontiguousarray(k, np.float32)
+    n, h, w, c = x.shape
+    kh, kw = k.shape[:2]
+    ho, wo = out_hw(h, w, kh, kw, stride[0], stride[1], pad[0], pad[1])
+    y = np.empty((n, ho, wo, c), np.float32)
+    lib().dwo_depthwise_conv2d_f32_nhwc_mt(_p(y), _p(x), _p(k), n, h, w, c, 1, kh, kw, stride[0],
+                                           stride[1], pad[0], pad[1], threads or default_threads())
+    return y
+
+
+def depthwise_fp16(xh, kh_, stride=(1, 1), pad=(0, 0), threads=None):
+    """depthwise_conv2d_fp16_nhwc_mt (ops.rs:2819-2933), multiplier 1."""
+    xh = np.ascontiguousarray(xh, np.uint16)
+    kh_ = np.ascontiguousarray(kh_, np.uint16)
+    n, h, w, c = xh.shape
+    kh, kw = kh_.shape[:2]
+    ho, wo = out_hw(h, w, kh, kw, stride[0], stride[1], pad[0], pad[1])
+    y = np.empty((n, ho, wo, c), np.uint16)
+    lib().dwo_depthwise_conv2d_fp16_nhwc_mt(_p(y), _p(xh), _p(kh_), n, h, w, c, 1, kh, kw, stride[0],
+                                            stride[1], pad[0], pad[1], threads or default_threads())
+    return y
+
+
+def conv2d_i8_nhwc(x, k, stride=(1, 1), pad=(0, 0), threads=1):
+    """conv2d_i8_nhwc (ops.rs:3086-3142); threads>1 uses the bit-identical row-parallel variant."""
+    x = np.ascontiguousarray(x, np.int8)
+    k = np.ascontiguousarray(k, np.int8)
+    n, h, w, ci = x.shape
+    kh, kw, _, co = k.shape
+    ho, wo = out_hw(h, w, kh, kw, stride[0], stride[1], pad[0], pad[1])
+    y = np.empty((n, ho, wo, co), np.int32)
+    if threads == 1:
+        lib().dwo_conv2d_i8_nhwc(_p(y), _p(x), _p(k), n, h, w, ci, co, kh, kw, stride[0], stride[1],
+                                 pad[0], pad[1])
+    else:
+        lib().dwo_conv2d_i8_nhwc_rowpar(_p(y), _p(x), _p(k), n, h, w, ci, co, kh, kw, stride[0],
+                                        stride[1], pad[0], pad[1], threads)
+    return y
+
+
+def qlinearconv_u8s8(x, k, bias, stride, pad, x_scale, x_zp, w_scales, y_scale, y_zp, threads=None):
+    """ONNX QLinearConv u8 x s8 -> u8 (extension; brute force by definition)."""
+    x = np.ascontiguousarray(x, np.uint8)
+    k = np.ascontiguousarray(k, np.int8)
+    ws = np.ascontiguousarray(w_scales, np.float32)
+    n, h, w, ci = x.shape
+    kh, kw, _, co = k.shape
+    ho, wo = out_hw(h, w, kh, kw, stride[0], stride[1], pad[0], pad[1])
+    y = np.empty((n, ho, wo, co), np.uint8)
+    bp = 0
+    if bias is not None:
+        bias = np.ascontiguousarray(bias, np.int32)
+        bp = _p(bias)
+    lib().dwo_qlinearconv_u8s8(_p(y), _p(x), _p(k), bp, n, h, w, ci, co, kh, kw, stride[0], stride[1],
+                               pad[0], pad[1], float(x_scale), int(x_zp), _p(ws), float(y_scale),
+                               int(y_zp), threads or default_threads())
+    return y
+
+
+# --- runtime bias passes and elementwise -----------------------------------
+def bias_add_f32(y, b):
+    y = np.ascontiguousarray(y, np.float32).copy()
+    b = np.ascontiguousarray(b, np.float32)
+    lib().dwo_bias_add_f32_nhwc(_p(y), _p(b), y.size // b.size, b.size)
+    return y
+
+
+def bias_add_f16(yh, bh):
+    yh = np.ascontiguousarray(yh, np.uint16).copy()
+    bh = np.ascontiguousarray(bh, np.uint16)
+    lib().dwo_bias_add_f16_nhwc(_p(yh), _p(bh), yh.size // bh.size, bh.size)
+    return yh
+
+
+def _unary(fn, x, dt):
+    x = np.ascontiguousarray(x, dt)
+    y = np.empty_like(x)
+    getattr(lib(), fn)(_p(y), _p(x), x.size)
+    return y
+
+
+def _binary(fn, a, b, dt):
+    a = np.ascontiguousarray(a, dt)
+    b = np.ascontiguousarray(b, dt)
+    assert a.shape == b.shape
+    y = np.empty_like(a)
+    getattr(lib(), fn)(_p(y), _p(a), _p(b), a.size)
+    return y
+
+
+def relu_f32(x): return _unary("dwo_relu_f32", x, np.float32)
+def relu_fp16(x): return _unary("dwo_relu_fp16", x, np.uint16)
+def sigmoid_f32(x): return _unary("dwo_sigmoid_f32", x, np.float32)
+def sigmoid_fp16(x): return _unary("dwo_sigmoid_fp16", x, np.uint16)
+def relu_i8(x): return _unary("dwo_relu_i8", x, np.int8)
+def add_f32(a, b): return _binary("dwo_add_f32", a, b, np.float32)
+def add_fp16(a, b): return _binary("dwo_add_fp16", a, b, np.uint16)
+def mul_f32(a, b): return _binary("dwo_mul_f32", a, b, np.float32)
+def mul_fp16(a, b): return _binary("dwo_mul_fp16", a, b, np.uint16)
+
+
+def silu_fp16(x):
+    """Sigmoid then Mul, each rounded to f16 (runtime.rs:1641-1734)."""
+    return mul_fp16(x, sigmoid_fp16(x))
+
+
+def silu_f32(x):
+    return mul_f32(x, sigmoid_f32(x))
+
+
+def requantize_i32_to_i8(x, s):
+    x = np.ascontiguousarray(x, np.int32)
+    y = np.empty(x.shape, np.int8)
+    lib().dwo_requantize_i32_to_i8(_p(y), _p(x), x.size, float(s))
+    return y
+
+
+def quantize_f32_to_i8(x, s):
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty(x.shape, np.int8)
+    lib().dwo_quantize_f32_to_i8(_p(y), _p(x), x.size, float(s))
+    return y
+
+
+def dequantize_i8_to_f32(x, s):
+    x = np.ascontiguousarray(x, np.int8)
+    y = np.empty(x.shape, np.float32)
+    lib().dwo_dequantize_i8_to_f32(_p(y), _p(x), x.size, float(s))
+    return y
+
+
+def add_i8(a, b, sa, sb):
+    a = np.ascontiguousarray(a, np.int8)
+    b = np.ascontiguousarray(b, np.int8)
+    y = np.empty(a.shape, np.int8)
+    lib().dwo_add_i8(_p(y), _p(a), _p(b), a.size, float(sa), float(sb))
+    return y
+
+
+def scale_from_range(mn, mx):
+    return float(lib().dwo_scale_from_range(float(mn), float(mx)))
+
+
+def quantize_weights_per_channel(w_rows):
+    """PerChannelScale::from_weights + quantize_weights_per_channel over rows (one row per channel)."""
+    w = np.ascontiguousarray(w_rows, np.float32)
+    c = w.shape[0]
+    q = np.empty(w.shape, np.int8)
+    s = np.empty(c, np.float32)
+    lib().dwo_quantize_weights_per_channel(_p(q), _p(s), _p(w), c, w.size // c)
+    return q, s
+
+
+def maxpool2d_f32(x, k, s):
+    x = np.ascontiguousarray(x, np.float32)
+    n, h, w, c = x.shape
+    ho, wo = (h - k[0]) // s[0] + 1, (w - k[1]) // s[1] + 1
+    y = np.empty((n, ho, wo, c), np.float32)
+    lib().dwo_maxpool2d_f32_nhwc(_p(y), _p(x), n, h, w, c, k[0], k[1], s[0], s[1])
+    return y
+
+
+def maxpool2d_padded(x, k, s, pads):
+    """pads = (top, left, bottom, right); dtype float32 / uint16 (f16 bits) / uint8."""
+    x = np.ascontiguousarray(x)
+    n, h, w, c = x.shape
+    pt, pl, pb, pr = pads
+    ho, wo = (h + pt + pb - k[0]) // s[0] + 1, (w + pl + pr - k[1]) // s[1] + 1
+    y = np.empty((n, ho, wo, c), x.dtype)
+    lib().dwo_maxpool2d_padded_nhwc(_p(y), _p(x), n, h, w, c, k[0], k[1], s[0], s[1], pt, pl, pb, pr,
+                                    x.dtype.itemsize)
+    return y
+
+
+def resize_nearest(x, ho, wo):
+    x = np.ascontiguousarray(x)
+    n, h, w, c = x.shape
+    y = np.empty((n, ho, wo, c), x.dtype)
+    lib().dwo_resize_nearest_nhwc(_p(y), _p(x), n, h, w, ho, wo, c, x.dtype.itemsize)
+    return y
+
+
+def concat_channels(xs):
+    xs = [np.ascontiguousarray(a) for a in xs]
+    pix = xs[0].size // xs[0].shape[-1]
+    chans = (C.c_size_t * len(xs))(*[a.shape[-1] for a in xs])
+    ptrs = (C.c_void_p * len(xs))(*[_p(a) for a in xs])
+    y = np.empty(xs[0].shape[:-1] + (sum(a.shape[-1] for a in xs),), xs[0].dtype)
+    lib().dwo_concat_channels(_p(y), ptrs, chans, len(xs), pix, xs[0].dtype.itemsize)
+    return y
+
+
+def split_channels(x, sizes):
+    x = np.ascontiguousarray(x)
+    pix = x.size // x.shape[-1]
+    outs = [np.empty(x.shape[:-1] + (s,), x.dtype) for s in sizes]
+    chans = (C.c_size_t * len(sizes))(*sizes)
+    ptrs = (C.c_void_p * len(sizes))(*[_p(a) for a in outs])
+    lib().dwo_split_channels(ptrs, _p(x), chans, len(sizes), pix, x.dtype.itemsize)
+    return outs
+
+
+def fold_batchnorm(w_oihw, bias, gamma, beta, mean, var, eps):
+    """fold_batchnorm arithmetic (graph.rs:597-613); returns (w', b')."""
+    w = np.ascontiguousarray(w_oihw, np.float32).copy()
+    c = w.shape[0]
+    b_out = np.empty(c, np.float32)
+    bp = 0
+    if bias is not None:
+        bias = np.ascontiguousarray(bias, np.float32)
+        bp = _p(bias)
+    arrs = [np.ascontiguousarray(a, np.float32) for a in (gamma, beta, mean, var)]
+    lib().dwo_fold_batchnorm(_p(w), _p(b_out), bp, *[_p(a) for a in arrs], float(eps), c, w.size // c)
+    return w, b_out
+
+
+# --- quantized extensions ----------------------------------------------------
+def quantize_linear_f16_u8(xh, scale, zp):
+    xh = np.ascontiguousarray(xh, np.uint16)
+    y = np.empty(xh.shape, np.uint8)
+    lib().dwo_quantize_linear_f16_u8(_p(y), _p(xh), xh.size, float(scale), int(zp))
+    return y
+
+
+def dequantize_linear_u8_f16(x, scale, zp):
+    x = np.ascontiguousarray(x, np.uint8)
+    y = np.empty(x.shape, np.uint16)
+    lib().dwo_dequantize_linear_u8_f16(_p(y), _p(x), x.size, float(scale), int(zp))
+    return y
+
+
+def qlinear_add_u8(a, b, sa, za, sb, zb, sy, zy):
+    a = np.ascontiguousarray(a, np.uint8)
+    b = np.ascontiguousarray(b, np.uint8)
+    y = np.empty(a.shape, np.uint8)
+    lib().dwo_qlinear_add_u8(_p(y), _p(a), _p(b), a.size, float(sa), int(za), float(sb), int(zb),
+                             float(sy), int(zy))
+    return y
+
+
+def silu_lut_u8(sx, zx, sy, zy):
+    lut = np.empty(256, np.uint8)
+    lib().dwo_silu_lut_u8(_p(lut), float(sx), int(zx), float(sy), int(zy))
+    return lut
+
+
+def lut_u8(x, lut):
+    x = np.ascontiguousarray(x, np.uint8)
+    lut = np.ascontiguousarray(lut, np.uint8)
+    y = np.empty(x.shape, np.uint8)
+    lib().dwo_lut_u8(_p(y), _p(x), x.size, _p(lut))
+    return y

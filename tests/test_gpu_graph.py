@@ -1,0 +1,134 @@
+"""GPU parity of the graph runtime (HipGraphRuntime) on YOLOv8n-shaped
+graphs against the oracle's CpuGraphRuntime restatement.
+
+* fp16 graph: max|gpu - ref| <= 1e-2 * max|ref| per detect output (the MFMA
+  convs accumulate in another order than the CPU);
+* f32 graph (the calibration graph): <= 1e-3 relative (only expf may differ);
+* int8 (u8 QDQ) graph: bit-exact, including the fp16 stem and head layers,
+  at a small size and at the full 640x640 batch-32 workload (checked on
+  sampled images of the batch against a batch-1 oracle run).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from oracle.cpu_graph import CpuGraph
+from dragonwing_edge_rs_amd import synth, yolo
+from dragonwing_edge_rs_amd.graph import HipGraphRuntime
+
+pytestmark = pytest.mark.gpu
+
+
+def oracle_run(g, inputs: dict):
+    cg = CpuGraph(g.to_dict(), g.initializer)
+    for k, v in inputs.items():
+        cg.set_input(k, v)
+    return cg.run()
+
+
+def rel_err(got, ref):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return float(np.max(np.abs(got - ref)) / max(np.max(np.abs(ref)), 1e-30))
+
+
+def gpu_outputs(rt, info, dtype=np.uint16):
+    return [rt.get_output_bytes(o).view(dtype).reshape(s) for o, s in zip(info["outputs"], info["out_shapes"])]
+
+
+def test_f16_graph_small_vs_oracle(backend):
+    g, info = yolo.f16_graph(batch=2, size=96)
+    x = yolo.input_images(2, 96)
+    rt = HipGraphRuntime(g, backend)
+    rt.set_input_f32(info["input"], x)
+    rt.run()
+    got = gpu_outputs(rt, info)
+    ref = oracle_run(g, {info["input"]: synth.f16_bits(x)})
+    for o, gv in zip(info["outputs"], got):
+        e = rel_err(oracle.f16_to_f32(gv), oracle.f16_to_f32(ref[o]))
+        print(f"{o}: rel err {e:.2e}")
+        assert e <= 1e-2
+
+
+def test_f32_graph_small_vs_oracle(backend):
+    g, info = yolo.build_yolov8n(batch=1, size=64)
+    g.fold_batchnorm()
+    g.convert_nchw_to_nhwc()
+    x = yolo.input_images(1, 64)
+    rt = HipGraphRuntime(g, backend)
+    rt.set_input_f32(info["input"], x)
+    rt.run()
+    ref = oracle_run(g, {info["input"]: x})
+    for o, s in zip(info["outputs"], info["out_shapes"]):
+        got = rt.get_output_bytes(o).view(np.float32).reshape(s)
+        assert rel_err(got, ref[o]) <= 1e-3
+
+
+@pytest.fixture(scope="module")
+def int8_small(backend):
+    return yolo.int8_graph(backend, batch=2, size=96, calib=yolo.calibration_images(16, 96))
+
+
+def test_int8_graph_small_bit_exact(backend, int8_small):
+    g, info = int8_small
+    x = yolo.input_images(2, 96)
+    rt = HipGraphRuntime(g, backend)
+    rt.set_input_f32(info["input"], x)
+    rt.run()
+    got = gpu_outputs(rt, info)
+    ref = oracle_run(g, {info["input"]: synth.f16_bits(x)})
+    for o, gv in zip(info["outputs"], got):
+        assert gv.shape == ref[o].shape
+        np.testing.assert_array_equal(gv, ref[o], err_msg=o)
+    # the result is not degenerate
+    assert len(np.unique(got[0])) > 100
+
+
+def test_int8_graph_capture_replays_match_eager(backend, int8_small):
+    g, info = int8_small
+    x = yolo.input_images(2, 96)
+    rt = HipGraphRuntime(g, backend)
+    rt.set_input_f32(info["input"], x)
+    rt.run()
+    eager = gpu_outputs(rt, info)
+    rt.enable_capture(True)
+    for i in range(4):
+        rt.set_input_f32(info["input"], x if i % 2 == 0 else np.zeros_like(x))
+        rt.run()
+        outs = gpu_outputs(rt, info)
+        if i % 2 == 0:
+            for a, b in zip(outs, eager):
+                np.testing.assert_array_equal(a, b)
+        backend.synchronize()
+
+
+def test_int8_graph_launch_plan(backend, int8_small):
+    g, info = int8_small
+    rt = HipGraphRuntime(g, backend)
+    ls = rt.launches()
+    kinds = {}
+    for L in ls:
+        kinds[L["kernel"].split("_")[0]] = kinds.get(L["kernel"].split("_")[0], 0) + 1
+    # 56 int8 MFMA convs (each with its table / residual fused), 7 fp16
+    # direct convs, one SPPF cascade, two resizes, no copies or elementwise.
+    assert kinds.get("igemm") == 56, kinds
+    assert kinds.get("direct") == 7 and kinds.get("maxpool") == 1 and kinds.get("resize") == 2, kinds
+    assert "copy" not in kinds and "elementwise" not in kinds, kinds
+    ms = rt.run_profiled()
+    assert len(ms) == len(ls) and np.all(ms > 0)
+
+
+def test_int8_graph_full_workload_bit_exact(backend):
+    # The headline workload: batch 32 at 640x640, calibrated on 16 images.
+    g, info = yolo.int8_graph(backend, batch=32, size=640)
+    x = yolo.input_images(32, 640)
+    rt = HipGraphRuntime(g, backend)
+    rt.set_input_f32(info["input"], x)
+    rt.run()
+    got = gpu_outputs(rt, info)
+    g1, info1 = yolo.int8_graph_from_ranges(info["ranges"], batch=1, size=640)
+    for img in (0, 31):
+        ref = oracle_run(g1, {info1["input"]: synth.f16_bits(x[img:img + 1])})
+        for o, gv in zip(info["outputs"], got):
+            np.testing.assert_array_equal(gv[img:img + 1], ref[o], err_msg=f"{o} image {img}")
+        print(f"image {img}: bit-exact on all three detect outputs", flush=True)

@@ -1,0 +1,402 @@
+"""GPU parity of the op-level C ABI against the oracle (dragonwing-cpu
+restatement), on the same seeded inputs.
+
+Bars: bit-exact for every integer path and for the fp32/fp16 kernels that
+keep the reference accumulation order; fp16 MFMA convolution within
+max|gpu - ref| <= 1e-2 * max|ref|; fp16 paths that call expf (SiLU,
+sigmoid) within the same fp16 bar (the GPU expf and glibc expf may differ
+in the last bit, which can flip an f16 rounding).
+"""
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle
+import dragonwing_edge_rs_amd as dw
+from dragonwing_edge_rs_amd import ops, synth
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def rel_err(got, ref):
+    ref = np.asarray(ref, np.float64)
+    return float(np.max(np.abs(np.asarray(got, np.float64) - ref)) / max(np.max(np.abs(ref)), 1e-30))
+
+
+def f16v(bits):
+    return oracle.f16_to_f32(bits)
+
+
+# --------------------------------------------------------------------------
+# Backend contract (backend.rs:127-199)
+# --------------------------------------------------------------------------
+def test_backend_roundtrip_and_errors(backend):
+    assert backend.name() == "hip-gfx950"
+    data = np.arange(1000, dtype=np.uint8)
+    buf = backend.from_numpy(data)
+    assert buf.len_bytes() == 1000
+    out = np.zeros_like(data)
+    backend.download(buf, out)
+    np.testing.assert_array_equal(out, data)
+    with pytest.raises(dw.HipError) as e:
+        backend.upload(buf, np.zeros(999, np.uint8))
+    assert e.value.code == -4
+    with pytest.raises(dw.HipError):
+        backend.download(buf, np.zeros(1001, np.uint8))
+    empty = backend.alloc(0)
+    backend.upload(empty, np.zeros(0, np.uint8))
+    backend.synchronize()
+
+
+# --------------------------------------------------------------------------
+# fp32 conv + bias + ReLU (the single-op fp32 workload, 1x64x56x56, 3x3)
+# --------------------------------------------------------------------------
+def run_conv_f32(be, x, k, b, stride, pad, act):
+    n, h, w, ci = x.shape
+    kh, kw, _, co = k.shape
+    ho, wo = oracle.out_hw(h, w, kh, kw, stride, stride, pad, pad)
+    bx, bk = be.from_numpy(x), be.from_numpy(k)
+    bb = be.from_numpy(b) if b is not None else None
+    by = be.alloc(n * ho * wo * co * 4)
+    ops.conv2d_bias_act_f32_nhwc(be, bx, bk, bb, by, n, h, w, ci, co, kh, kw, stride, stride, pad, pad, act)
+    return be.to_numpy(by, np.float32, (n, ho, wo, co))
+
+
+def test_conv_f32_bias_relu_full_workload_bit_exact(backend):
+    x, k, b = synth.conv_f32_case(0)
+    got = run_conv_f32(backend, x, k, b, 1, 1, ops.ACT_RELU)
+    ref = oracle.relu_f32(oracle.bias_add_f32(oracle.conv2d_f32_nhwc(x, k, (1, 1), (1, 1)), b))
+    np.testing.assert_array_equal(got, ref)
+    assert rel_err(got, ref) <= 1e-3
+
+
+@pytest.mark.parametrize("shape", [(2, 9, 7, 5, 6, 3, 2, 1), (1, 6, 5, 3, 16, 3, 2, 1),
+                                   (3, 5, 5, 4, 12, 1, 1, 0), (1, 1, 1, 8, 8, 3, 1, 1)])
+def test_conv_f32_ragged_bit_exact(backend, shape):
+    n, h, w, ci, co, k, s, p = shape
+    rng = np.random.default_rng(sum(shape))
+    x = rng.uniform(-1, 1, (n, h, w, ci)).astype(np.float32)
+    kk = rng.uniform(-1, 1, (k, k, ci, co)).astype(np.float32)
+    got = run_conv_f32(backend, x, kk, None, s, p, ops.ACT_NONE)
+    np.testing.assert_array_equal(got, oracle.conv2d_f32_nhwc(x, kk, (s, s), (p, p)))
+
+
+def test_conv_f32_plain_entry(backend):
+    x, k, _ = synth.conv_f32_case(0, c_in=16, c_out=8, h=12, w=12)
+    n, h, w, ci = x.shape
+    bx, bk, by = backend.from_numpy(x), backend.from_numpy(k), backend.alloc(n * h * w * 8 * 4)
+    ops.conv2d_f32_nhwc(backend, bx, bk, by, n, h, w, ci, 8, 3, 3, 1, 1, 1, 1)
+    np.testing.assert_array_equal(backend.to_numpy(by, np.float32, (n, h, w, 8)),
+                                  oracle.conv2d_f32_nhwc(x, k, (1, 1), (1, 1)))
+    with pytest.raises(dw.HipError):  # wrong output size is rejected, not truncated
+        ops.conv2d_f32_nhwc(backend, bx, bk, backend.alloc(4), n, h, w, ci, 8, 3, 3, 1, 1, 1, 1)
+
+
+# --------------------------------------------------------------------------
+# QLinearConv u8 x s8 -> u8 (INT8 MFMA)
+# --------------------------------------------------------------------------
+def run_qconv(be, c, stride, pad):
+    x, w = c["x"], c["w"]
+    n, h, wd, ci = x.shape
+    kh, kw, _, co = w.shape
+    ho, wo = oracle.out_hw(h, wd, kh, kw, stride, stride, pad, pad)
+    bx, bw = be.from_numpy(x), be.from_numpy(w)
+    bb = be.from_numpy(np.asarray(c["bias"], np.int32)) if c["bias"] is not None else None
+    by = be.alloc(n * ho * wo * co)
+    ops.qlinearconv_u8s8(be, bx, bw, bb, by, n, h, wd, ci, co, kh, kw, stride, stride, pad, pad,
+                         c["x_scale"], c["x_zp"], c["w_scales"], c["y_scale"], c["y_zp"])
+    return be.to_numpy(by, np.uint8, (n, ho, wo, co))
+
+
+def oracle_qconv(c, stride, pad):
+    return oracle.qlinearconv_u8s8(c["x"], c["w"], c["bias"], (stride, stride), (pad, pad), c["x_scale"],
+                                   c["x_zp"], c["w_scales"], c["y_scale"], c["y_zp"])
+
+
+def test_qlinearconv_full_workload_bit_exact(backend):
+    # batch 32, 80x80x128 -> 40x40x256, 3x3 stride 2 pad 1
+    c = synth.qlinearconv_case(1)
+    got = run_qconv(backend, c, 2, 1)
+    ref = oracle_qconv(c, 2, 1)
+    assert got.shape == (32, 40, 40, 256)
+    np.testing.assert_array_equal(got, ref)
+    # not trivially saturated: the outputs span the range
+    assert 20 < len(np.unique(ref)) and (ref == 0).mean() < 0.5 and (ref == 255).mean() < 0.5
+
+
+@pytest.mark.parametrize("geom", [(1, 7, 9, 16, 4, 3, 1, 1), (2, 9, 7, 32, 20, 3, 2, 1),
+                                  (1, 5, 8, 48, 80, 1, 1, 0), (1, 13, 11, 64, 64, 3, 2, 1),
+                                  (2, 6, 6, 128, 144, 3, 1, 1), (1, 20, 20, 256, 256, 1, 1, 0)])
+@pytest.mark.parametrize("x_zp", [128, 0, 201])
+def test_qlinearconv_shapes_bit_exact(backend, geom, x_zp):
+    n, h, w, ci, co, k, s, p = geom
+    r = synth.Rng(synth.seed_for(100 + sum(geom)))
+    c = dict(x=r.integers((n, h, w, ci), 0, 255).astype(np.uint8),
+             w=r.integers((k, k, ci, co), -127, 127).astype(np.int8),
+             bias=r.integers((co,), -4096, 4096).astype(np.int32),
+             w_scales=r.log_uniform((co,), 1e-3, 1e-2), x_scale=0.02, x_zp=x_zp, y_scale=0.05, y_zp=128)
+    np.testing.assert_array_equal(run_qconv(backend, c, s, p), oracle_qconv(c, s, p))
+
+
+def test_qlinearconv_golden_fixtures(backend):
+    cases = json.loads((GOLDEN / "qlinear_cases.json").read_text())["qlinearconv"]
+    for g in cases:
+        c = dict(x=np.array(g["x"], np.uint8).reshape(g["x_shape"]),
+                 w=np.array(g["w"], np.int8).reshape(g["w_shape"]), bias=np.array(g["bias"], np.int32),
+                 w_scales=np.array(g["w_scales"], np.float32), x_scale=g["x_scale"], x_zp=g["x_zp"],
+                 y_scale=g["y_scale"], y_zp=g["y_zp"])
+        got = run_qconv(backend, c, g["stride"][0], g["pad"][0])
+        np.testing.assert_array_equal(got.ravel(), g["y"], err_msg=g["name"])
+
+
+def test_qlinearconv_rejects_unsupported(backend):
+    x = backend.alloc(1 * 4 * 4 * 8)
+    w = backend.alloc(9 * 8 * 4)
+    y = backend.alloc(1 * 4 * 4 * 4)
+    with pytest.raises(dw.HipError) as e:  # c_in = 8 is not a multiple of 16
+        ops.qlinearconv_u8s8(backend, x, w, None, y, 1, 4, 4, 8, 4, 3, 3, 1, 1, 1, 1, 0.02, 128,
+                             np.ones(4, np.float32), 0.05, 128)
+    assert e.value.code == -2
+
+
+# --------------------------------------------------------------------------
+# Reference INT8 ops (symmetric s8)
+# --------------------------------------------------------------------------
+def test_conv2d_i8_and_requant_relu_bit_exact(backend):
+    r = synth.Rng(synth.seed_for(7))
+    n, h, w, ci, co = 2, 11, 9, 32, 24
+    x = r.integers((n, h, w, ci), -128, 127).astype(np.int8)
+    k = r.integers((3, 3, ci, co), -127, 127).astype(np.int8)
+    bx, bk = backend.from_numpy(x), backend.from_numpy(k)
+    for s in (1, 2):
+        ho, wo = oracle.out_hw(h, w, 3, 3, s, s, 1, 1)
+        acc_ref = oracle.conv2d_i8_nhwc(x, k, (s, s), (1, 1))
+        by = backend.alloc(n * ho * wo * co * 4)
+        ops.conv2d_i8_nhwc(backend, bx, bk, by, n, h, w, ci, co, 3, 3, s, s, 1, 1)
+        np.testing.assert_array_equal(backend.to_numpy(by, np.int32, acc_ref.shape), acc_ref)
+        for relu in (0, 1):
+            scale = 0.0023
+            ref = oracle.requantize_i32_to_i8(acc_ref, scale)
+            if relu:
+                ref = oracle.relu_i8(ref)
+            bq = backend.alloc(n * ho * wo * co)
+            ops.conv2d_requant_relu_i8(backend, bx, bk, bq, n, h, w, ci, co, 3, 3, s, s, 1, 1, scale, relu)
+            np.testing.assert_array_equal(backend.to_numpy(bq, np.int8, ref.shape), ref)
+
+
+def test_int8_elementwise_bit_exact(backend):
+    r = synth.Rng(synth.seed_for(8))
+    acc = r.integers((4099,), -40000, 40000).astype(np.int32)
+    a = r.integers((4099,), -128, 127).astype(np.int8)
+    b = r.integers((4099,), -128, 127).astype(np.int8)
+    f = r.uniform((4099,), -20.0, 20.0)
+    n = 4099
+    bacc, ba, bb, bf = map(backend.from_numpy, (acc, a, b, f))
+    y8 = backend.alloc(n)
+    ops.requantize_i32_to_i8(backend, bacc, y8, n, 0.0031)
+    np.testing.assert_array_equal(backend.to_numpy(y8, np.int8, n), oracle.requantize_i32_to_i8(acc, 0.0031))
+    ops.add_i8(backend, ba, bb, y8, n, 0.7, 0.45)
+    np.testing.assert_array_equal(backend.to_numpy(y8, np.int8, n), oracle.add_i8(a, b, 0.7, 0.45))
+    ops.relu_i8(backend, ba, y8, n)
+    np.testing.assert_array_equal(backend.to_numpy(y8, np.int8, n), oracle.relu_i8(a))
+    ops.quantize_f32_to_i8(backend, bf, y8, n, 0.13)
+    np.testing.assert_array_equal(backend.to_numpy(y8, np.int8, n), oracle.quantize_f32_to_i8(f, 0.13))
+    yf = backend.alloc(n * 4)
+    ops.dequantize_i8_to_f32(backend, ba, yf, n, 0.07)
+    np.testing.assert_array_equal(backend.to_numpy(yf, np.float32, n), oracle.dequantize_i8_to_f32(a, 0.07))
+
+
+def test_onnx_quant_elementwise_bit_exact(backend):
+    r = synth.Rng(synth.seed_for(9))
+    n = 5000
+    xa = r.integers((n,), 0, 255).astype(np.uint8)
+    xb = r.integers((n,), 0, 255).astype(np.uint8)
+    xh = synth.f16_bits(r.normal((n,), 0.0, 3.0))
+    ba, bb, bh = map(backend.from_numpy, (xa, xb, xh))
+    y = backend.alloc(n)
+    ops.qlinear_add_u8(backend, ba, bb, y, n, 0.031, 120, 0.017, 131, 0.04, 125)
+    np.testing.assert_array_equal(backend.to_numpy(y, np.uint8, n),
+                                  oracle.qlinear_add_u8(xa, xb, 0.031, 120, 0.017, 131, 0.04, 125))
+    ops.quantize_linear_f16_u8(backend, bh, y, n, 0.037, 128)
+    np.testing.assert_array_equal(backend.to_numpy(y, np.uint8, n), oracle.quantize_linear_f16_u8(xh, 0.037, 128))
+    yh = backend.alloc(n * 2)
+    ops.dequantize_linear_u8_f16(backend, ba, yh, n, 0.021, 128)
+    np.testing.assert_array_equal(backend.to_numpy(yh, np.uint16, n),
+                                  oracle.dequantize_linear_u8_f16(xa, 0.021, 128))
+    lut = oracle.silu_lut_u8(0.05, 128, 0.03, 128)
+    ops.lut_u8(backend, ba, y, n, lut)
+    np.testing.assert_array_equal(backend.to_numpy(y, np.uint8, n), lut[xa])
+
+
+# --------------------------------------------------------------------------
+# fp16 convolutions
+# --------------------------------------------------------------------------
+def run_conv_f16(be, xh, kh_, bh, stride, pad, act, exact):
+    n, h, w, ci = xh.shape
+    kh, kw, _, co = kh_.shape
+    ho, wo = oracle.out_hw(h, w, kh, kw, stride, stride, pad, pad)
+    bx, bk = be.from_numpy(xh), be.from_numpy(kh_)
+    bb = be.from_numpy(bh) if bh is not None else None
+    by = be.alloc(n * ho * wo * co * 2)
+    ops.conv2d_bias_act_f16_nhwc(be, bx, bk, bb, by, n, h, w, ci, co, kh, kw, stride, stride, pad, pad,
+                                 act, exact)
+    return be.to_numpy(by, np.uint16, (n, ho, wo, co))
+
+
+def oracle_conv_f16(xh, kh_, bh, stride, pad, act):
+    y = oracle.conv2d_fp16_nhwc(xh, kh_, (stride, stride), (pad, pad))
+    if bh is not None:
+        y = oracle.bias_add_f16(y, bh)
+    if act == ops.ACT_RELU:
+        y = oracle.relu_fp16(y)
+    elif act == ops.ACT_SILU:
+        y = oracle.silu_fp16(y)
+    return y
+
+
+@pytest.mark.parametrize("geom", [(2, 16, 16, 16, 32, 3, 2, 1), (1, 20, 20, 64, 64, 3, 1, 1),
+                                  (2, 10, 10, 80, 80, 3, 1, 1), (1, 12, 12, 128, 256, 1, 1, 0),
+                                  (1, 9, 7, 48, 16, 3, 1, 1), (1, 17, 9, 32, 144, 3, 2, 1)])
+@pytest.mark.parametrize("act", [ops.ACT_NONE, ops.ACT_SILU])
+def test_conv_f16_mfma_within_tolerance(backend, geom, act):
+    n, h, w, ci, co, k, s, p = geom
+    r = synth.Rng(synth.seed_for(200 + sum(geom)))
+    xh = synth.f16_bits(r.normal((n, h, w, ci), 0.0, 1.0))
+    kh_ = synth.f16_bits(r.normal((k, k, ci, co), 0.0, (1.0 / (k * k * ci)) ** 0.5))
+    bh = synth.f16_bits(r.normal((co,), 0.0, 0.1))
+    got = run_conv_f16(backend, xh, kh_, bh, s, p, act, exact=False)
+    ref = oracle_conv_f16(xh, kh_, bh, s, p, act)
+    assert rel_err(f16v(got), f16v(ref)) <= 1e-2
+
+
+@pytest.mark.parametrize("geom", [(2, 32, 32, 3, 16, 3, 2, 1), (1, 12, 12, 64, 64, 1, 1, 0),
+                                  (1, 10, 10, 80, 80, 1, 1, 0)])
+def test_conv_f16_exact_order_bit_exact(backend, geom):
+    n, h, w, ci, co, k, s, p = geom
+    r = synth.Rng(synth.seed_for(300 + sum(geom)))
+    xh = synth.f16_bits(r.uniform((n, h, w, ci), 0.0, 1.0))
+    kh_ = synth.f16_bits(r.normal((k, k, ci, co), 0.0, 0.2))
+    bh = synth.f16_bits(r.normal((co,), 0.0, 0.1))
+    got = run_conv_f16(backend, xh, kh_, bh, s, p, ops.ACT_NONE, exact=True)
+    np.testing.assert_array_equal(got, oracle_conv_f16(xh, kh_, bh, s, p, ops.ACT_NONE))
+    got = run_conv_f16(backend, xh, kh_, bh, s, p, ops.ACT_RELU, exact=True)
+    np.testing.assert_array_equal(got, oracle_conv_f16(xh, kh_, bh, s, p, ops.ACT_RELU))
+
+
+def test_conv_f16_subnormal_inputs_follow_reference_decode(backend):
+    # dragonwing-cpu widens f16 subnormals at half their IEEE value; the
+    # exact-order kernel reproduces it bit for bit.
+    xh = np.full((1, 4, 4, 8), 0x0200, np.uint16)  # subnormal
+    kh_ = np.full((1, 1, 8, 8), 0x3C00, np.uint16)  # 1.0
+    got = run_conv_f16(backend, xh, kh_, None, 1, 0, ops.ACT_NONE, exact=True)
+    np.testing.assert_array_equal(got, oracle_conv_f16(xh, kh_, None, 1, 0, ops.ACT_NONE))
+
+
+# --------------------------------------------------------------------------
+# Depthwise 3x3 fp16 + bias + SiLU (batch 32, 40x40x384)
+# --------------------------------------------------------------------------
+def test_depthwise_f16_full_workload(backend):
+    x, wt, b = synth.dwconv_case(2)
+    n, h, w, c = x.shape
+    bx, bw, bb = backend.from_numpy(x), backend.from_numpy(wt), backend.from_numpy(b)
+    by = backend.alloc(x.nbytes)
+    ops.depthwise_conv2d_f16_nhwc(backend, bx, bw, bb, by, n, h, w, c, 3, 3, 1, 1, 1, 1, ops.ACT_SILU)
+    got = backend.to_numpy(by, np.uint16, x.shape)
+    ref = oracle.silu_fp16(oracle.bias_add_f16(oracle.depthwise_fp16(x, wt, (1, 1), (1, 1)), b))
+    assert rel_err(f16v(got), f16v(ref)) <= 1e-2
+    # Everything before the expf-based activation is bit-exact:
+    ops.depthwise_conv2d_f16_nhwc(backend, bx, bw, bb, by, n, h, w, c, 3, 3, 1, 1, 1, 1, ops.ACT_NONE)
+    np.testing.assert_array_equal(backend.to_numpy(by, np.uint16, x.shape),
+                                  oracle.bias_add_f16(oracle.depthwise_fp16(x, wt, (1, 1), (1, 1)), b))
+    assert np.mean(got != ref) < 1e-3  # f16 flips from expf last-bit differences are rare
+
+
+@pytest.mark.parametrize("geom", [(1, 7, 5, 8, 2), (2, 9, 9, 16, 1), (1, 6, 6, 24, 2)])
+def test_depthwise_f32_and_f16_ragged(backend, geom):
+    n, h, w, c, s = geom
+    r = synth.Rng(synth.seed_for(400 + sum(geom)))
+    x = r.normal((n, h, w, c), 0.0, 1.0)
+    k = r.normal((3, 3, c), 0.0, 0.3)
+    ho, wo = oracle.out_hw(h, w, 3, 3, s, s, 1, 1)
+    bx, bk = backend.from_numpy(x), backend.from_numpy(k)
+    by = backend.alloc(n * ho * wo * c * 4)
+    ops.depthwise_conv2d_f32_nhwc(backend, bx, bk, None, by, n, h, w, c, 3, 3, s, s, 1, 1, ops.ACT_RELU)
+    np.testing.assert_array_equal(backend.to_numpy(by, np.float32, (n, ho, wo, c)),
+                                  oracle.relu_f32(oracle.depthwise_f32(x, k, (s, s), (1, 1))))
+    xh, kh_ = synth.f16_bits(x), synth.f16_bits(k)
+    bx, bk = backend.from_numpy(xh), backend.from_numpy(kh_)
+    by = backend.alloc(n * ho * wo * c * 2)
+    ops.depthwise_conv2d_f16_nhwc(backend, bx, bk, None, by, n, h, w, c, 3, 3, s, s, 1, 1, ops.ACT_NONE)
+    np.testing.assert_array_equal(backend.to_numpy(by, np.uint16, (n, ho, wo, c)),
+                                  oracle.depthwise_fp16(xh, kh_, (s, s), (1, 1)))
+
+
+# --------------------------------------------------------------------------
+# fp16 / fp32 elementwise and glue
+# --------------------------------------------------------------------------
+def test_float_elementwise(backend):
+    r = synth.Rng(synth.seed_for(10))
+    n = 3001
+    a32 = r.normal((n,), 0.0, 4.0)
+    b32 = r.normal((n,), 0.0, 4.0)
+    a16, b16 = synth.f16_bits(a32), synth.f16_bits(b32)
+    ba, bb, ba16, bb16 = map(backend.from_numpy, (a32, b32, a16, b16))
+    y32, y16 = backend.alloc(n * 4), backend.alloc(n * 2)
+    for fn, ref in [(ops.add_f32, oracle.add_f32), (ops.mul_f32, oracle.mul_f32)]:
+        fn(backend, ba, bb, y32, n)
+        np.testing.assert_array_equal(backend.to_numpy(y32, np.float32, n), ref(a32, b32))
+    for fn, ref in [(ops.add_fp16, oracle.add_fp16), (ops.mul_fp16, oracle.mul_fp16)]:
+        fn(backend, ba16, bb16, y16, n)
+        np.testing.assert_array_equal(backend.to_numpy(y16, np.uint16, n), ref(a16, b16))
+    ops.relu_f32(backend, ba, y32, n)
+    np.testing.assert_array_equal(backend.to_numpy(y32, np.float32, n), oracle.relu_f32(a32))
+    ops.relu_fp16(backend, ba16, y16, n)
+    np.testing.assert_array_equal(backend.to_numpy(y16, np.uint16, n), oracle.relu_fp16(a16))
+    ops.sigmoid_f32(backend, ba, y32, n)
+    np.testing.assert_allclose(backend.to_numpy(y32, np.float32, n), oracle.sigmoid_f32(a32), rtol=2e-7, atol=1e-7)
+    ops.silu_fp16(backend, ba16, y16, n)
+    assert rel_err(f16v(backend.to_numpy(y16, np.uint16, n)), f16v(oracle.silu_fp16(a16))) <= 1e-2
+    ops.sigmoid_fp16(backend, ba16, y16, n)
+    assert rel_err(f16v(backend.to_numpy(y16, np.uint16, n)), f16v(oracle.sigmoid_fp16(a16))) <= 1e-2
+
+
+def test_pool_resize_concat_split(backend):
+    r = synth.Rng(synth.seed_for(11))
+    x = synth.f16_bits(r.normal((2, 20, 20, 32), 0.0, 1.0))
+    n, h, w, c = x.shape
+    bx = backend.from_numpy(x)
+    # SPPF pool: k5 s1 p2 (padded, extension) and the reference's unpadded 2x2 s2
+    by = backend.alloc(x.nbytes)
+    ops.maxpool2d_nhwc(backend, ops.DTYPE_F16, bx, by, n, h, w, c, 5, 5, 1, 1, (2, 2, 2, 2))
+    np.testing.assert_array_equal(backend.to_numpy(by, np.uint16, x.shape),
+                                  oracle.maxpool2d_padded(x, (5, 5), (1, 1), (2, 2, 2, 2)))
+    x32 = oracle.f16_to_f32(x)
+    b32 = backend.from_numpy(x32)
+    by = backend.alloc(n * 10 * 10 * c * 4)
+    ops.maxpool2d_nhwc(backend, ops.DTYPE_F32, b32, by, n, h, w, c, 2, 2, 2, 2)
+    np.testing.assert_array_equal(backend.to_numpy(by, np.float32, (n, 10, 10, c)),
+                                  oracle.maxpool2d_f32(x32, (2, 2), (2, 2)))
+    # nearest 2x
+    by = backend.alloc(n * 40 * 40 * c * 2)
+    ops.resize_nearest_nhwc(backend, ops.DTYPE_F16, bx, by, n, h, w, 40, 40, c)
+    np.testing.assert_array_equal(backend.to_numpy(by, np.uint16, (n, 40, 40, c)), oracle.resize_nearest(x, 40, 40))
+    # concat / split along channels
+    parts = [x[..., :8].copy(), x[..., 8:24].copy(), x[..., 24:].copy()]
+    bparts = [backend.from_numpy(p) for p in parts]
+    by = backend.alloc(x.nbytes)
+    ops.concat_channels_nhwc(backend, ops.DTYPE_F16, bparts, [8, 16, 8], by, n * h * w)
+    np.testing.assert_array_equal(backend.to_numpy(by, np.uint16, x.shape), oracle.concat_channels(parts))
+    outs = [backend.alloc(p.nbytes) for p in parts]
+    ops.split_channels_nhwc(backend, ops.DTYPE_F16, bx, outs, [8, 16, 8], n * h * w)
+    for o, p, q in zip(outs, parts, oracle.split_channels(x, [8, 16, 8])):
+        np.testing.assert_array_equal(backend.to_numpy(o, np.uint16, p.shape), q)
+    # u8 padded maxpool
+    xq = r.integers((1, 9, 11, 16), 0, 255).astype(np.uint8)
+    bq = backend.from_numpy(xq)
+    by = backend.alloc(xq.nbytes)
+    ops.maxpool2d_nhwc(backend, ops.DTYPE_U8, bq, by, 1, 9, 11, 16, 5, 5, 1, 1, (2, 2, 2, 2))
+    np.testing.assert_array_equal(backend.to_numpy(by, np.uint8, xq.shape),
+                                  oracle.maxpool2d_padded(xq, (5, 5), (1, 1), (2, 2, 2, 2)))
