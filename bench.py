@@ -1,0 +1,311 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X backend on its headline workload.
+
+Default: the YOLOv8n-shaped graph, u8-quantized (QDQ-folded QLinearConv,
+fp16 stem and head 1x1s), batch 32, 640x640, on one GPU through
+HipGraphRuntime (the whole run captured once into a HIP graph).  A step is
+one run of the graph over one batch already resident in HBM; `value` is
+images/s over exactly --steps steps after --warmup untimed steps, bracketed
+by stream synchronisation.
+
+Also prints, on the same JSON line:
+  roofline     — the dominant kernel (most GPU time in one run): its
+                 algorithmic work per launch divided by its mean launch time,
+                 measured with HIP events around every launch on the backend
+                 stream, against the MI355X dense peak of its bound;
+  cpu_baseline — the oracle (dragonwing-cpu restated in C++) on a bounded
+                 sample of the same workload, timed on this host's cores.
+
+Other workloads (--workload): qlinearconv, dwconv, conv_f32, yolov8n_f16.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "images/sec YOLOv8n-shape INT8 640² b32 on 1 MI355X; conv % MFMA/HBM peak"
+PEAKS = {  # MI355X dense peaks
+    "int8": ("mfma", 5000.0, "TOP/s"),
+    "f16": ("mfma", 2500.0, "TFLOP/s"),
+    "f32": ("mfma", 157.3, "TFLOP/s"),
+    "hbm": ("hbm", 8000.0, "GB/s"),
+}
+
+
+def kernel_bound(kernel: str):
+    if kernel.startswith("igemm_i8"):
+        return PEAKS["int8"]
+    if kernel.startswith("igemm_f16"):
+        return PEAKS["f16"]
+    if kernel.startswith("direct_conv"):
+        return PEAKS["f32"]
+    return PEAKS["hbm"]
+
+
+def cpu_threads() -> int:
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
+def profile(rts, launches, iters: int):
+    """Mean per-launch milliseconds over `iters` event-bracketed runs."""
+    acc = None
+    for i in range(iters):
+        ms = rts[i % len(rts)].run_profiled().astype(np.float64)
+        acc = ms if acc is None else acc + ms
+    ms = acc / iters
+    fam = {}
+    for L, t in zip(launches, ms):
+        f = fam.setdefault(L["kernel"], {"kernel": L["kernel"], "launches": 0, "ms": 0.0, "work": 0.0,
+                                         "bytes": 0.0})
+        f["launches"] += 1
+        f["ms"] += float(t)
+        f["work"] += L["work"]
+        f["bytes"] += L["bytes"]
+    return ms, sorted(fam.values(), key=lambda f: -f["ms"])
+
+
+def roofline_of(fam):
+    bound, peak, unit = kernel_bound(fam["kernel"])
+    secs = fam["ms"] * 1e-3
+    if bound == "hbm":
+        achieved = fam["bytes"] / secs / 1e9
+    else:
+        achieved = fam["work"] / secs / 1e12
+    return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": None, "kernel": fam["kernel"],
+            "launches_per_step": fam["launches"], "mean_launch_us": round(fam["ms"] * 1e3 / fam["launches"], 2),
+            "work_per_launch": fam["work"] / fam["launches"], "bytes_per_launch": fam["bytes"] / fam["launches"]}
+
+
+# ---------------------------------------------------------------------------
+# CPU baselines (oracle, bounded samples)
+# ---------------------------------------------------------------------------
+def cpu_baseline_yolo_int8(info, x_f16, seconds: float):
+    from oracle.cpu_graph import CpuGraph
+    from dragonwing_edge_rs_amd import yolo
+
+    threads = cpu_threads()
+    g1, info1 = yolo.int8_graph_from_ranges(info["ranges"], batch=1, size=info["size"])
+    desc = g1.to_dict()
+    done, t0 = 0, time.perf_counter()
+    while True:
+        cg = CpuGraph(desc, g1.initializer, threads=threads)
+        cg.set_input(info1["input"], x_f16[done % x_f16.shape[0]][None])
+        cg.run()
+        done += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or done >= x_f16.shape[0]:
+            break
+    return {"value": round(done / el, 3), "unit": "images/s", "cores": threads, "kind": "port",
+            "sample": f"{done} of the 32 images (640x640) through the oracle's CpuGraph on the same u8 graph "
+                      f"at batch 1; int8 convs row-parallel on {threads} threads (bit-identical to the "
+                      f"single-threaded conv2d_i8_nhwc form); {el:.1f} s"}
+
+
+def cpu_baseline_yolo_f16(info, x_f16, seconds: float):
+    from oracle.cpu_graph import CpuGraph
+    from dragonwing_edge_rs_amd import yolo
+
+    threads = cpu_threads()
+    g1, info1 = yolo.f16_graph(batch=1, size=info["size"])
+    desc = g1.to_dict()
+    done, t0 = 0, time.perf_counter()
+    while True:
+        cg = CpuGraph(desc, g1.initializer, threads=threads)
+        cg.set_input(info1["input"], x_f16[done % x_f16.shape[0]][None])
+        cg.run()
+        done += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or done >= x_f16.shape[0]:
+            break
+    return {"value": round(done / el, 3), "unit": "images/s", "cores": threads, "kind": "port",
+            "sample": f"{done} of the 32 images through the oracle's CpuGraph (conv2d_fp16_nhwc_mt on "
+                      f"{threads} threads); {el:.1f} s"}
+
+
+def cpu_baseline_qconv(case, seconds: float):
+    import oracle
+
+    threads = cpu_threads()
+    done, t0 = 0, time.perf_counter()
+    while True:
+        sl = slice(done % 32, done % 32 + 1)
+        oracle.qlinearconv_u8s8(case["x"][sl], case["w"], case["bias"], (2, 2), (1, 1), case["x_scale"],
+                                case["x_zp"], case["w_scales"], case["y_scale"], case["y_zp"], threads)
+        done += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or done >= 32:
+            break
+    return {"value": round(done / el, 3), "unit": "images/s", "cores": threads, "kind": "port",
+            "sample": f"{done} of the 32 images (80x80x128 -> 40x40x256) through the oracle QLinearConv on "
+                      f"{threads} threads; {el:.1f} s"}
+
+
+def cpu_baseline_dwconv(xwb, seconds: float):
+    import oracle
+
+    x, w, b = xwb
+    threads = cpu_threads()
+    done, t0 = 0, time.perf_counter()
+    while True:
+        sl = slice(done % 32, done % 32 + 1)
+        y = oracle.depthwise_fp16(x[sl], w, (1, 1), (1, 1), threads)
+        oracle.silu_fp16(oracle.bias_add_f16(y, b))
+        done += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or done >= 32:
+            break
+    return {"value": round(done / el, 3), "unit": "images/s", "cores": threads, "kind": "port",
+            "sample": f"{done} of the 32 images through depthwise_conv2d_fp16_nhwc_mt + bias + sigmoid/mul "
+                      f"on {threads} threads; {el:.1f} s"}
+
+
+def cpu_baseline_conv_f32(xwb, seconds: float):
+    import oracle
+
+    x, w, b = xwb
+    threads = cpu_threads()
+    done, t0 = 0, time.perf_counter()
+    while True:
+        oracle.relu_f32(oracle.bias_add_f32(oracle.conv2d_f32_nhwc(x, w, (1, 1), (1, 1), threads), b))
+        done += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return {"value": round(done / el, 3), "unit": "images/s", "cores": threads, "kind": "port",
+            "sample": f"{done} runs of conv2d_f32_nhwc_mt + bias + relu on {threads} threads; {el:.1f} s"}
+
+
+# ---------------------------------------------------------------------------
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="yolov8n_int8",
+                    choices=["yolov8n_int8", "yolov8n_f16", "qlinearconv", "dwconv", "conv_f32"])
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--profile-iters", type=int, default=5)
+    ap.add_argument("--no-capture", action="store_true", help="replay launches eagerly instead of a HIP graph")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this backend runs on one GPU; --gpus {args.gpus} is not supported "
+              f"(the batch would shard data-parallel across GPUs with no exchange).", file=sys.stderr)
+        sys.exit(2)
+
+    import __graft_entry__
+
+    dw = __graft_entry__.import_pkg()
+    from dragonwing_edge_rs_amd import workloads
+    from dragonwing_edge_rs_amd.graph import HipGraphRuntime
+
+    be = dw.Backend(0)
+    wl = args.workload
+    rotate = 1
+    t_setup = time.perf_counter()
+    if wl == "yolov8n_int8":
+        g, inputs, outs, work, extra = workloads.yolov8n_int8(be)
+        config = {"workload": "YOLOv8n-shaped graph, u8 QDQ (QLinearConv, fp16 stem + head 1x1s), "
+                              "batch 32, 640x640, calibrated on 16 uniform images",
+                  "batch": 32, "size": 640, "convs": extra["convs"], "params": extra["params"]}
+        dtype = "int8"
+    elif wl == "yolov8n_f16":
+        g, inputs, outs, work, extra = workloads.yolov8n_f16()
+        config = {"workload": "YOLOv8n-shaped graph, fp16, batch 32, 640x640", "batch": 32, "size": 640,
+                  "convs": extra["convs"], "params": extra["params"]}
+        dtype = "f16"
+    elif wl == "qlinearconv":
+        g, inputs, outs, work, extra = workloads.qlinearconv()
+        config = {"workload": "QLinearConv u8xs8->u8, N=32, 80x80x128 -> 40x40x256, 3x3 s2 p1", "batch": 32}
+        dtype = "int8"
+        rotate = 8  # 8 x 39.6 MB > 256 MB Infinity Cache
+    elif wl == "dwconv":
+        g, inputs, outs, work, extra = workloads.dwconv()
+        config = {"workload": "depthwise 3x3 fp16 + bias + SiLU, N=32, C=384, 40x40", "batch": 32}
+        dtype = "f16"
+        rotate = 4  # 4 x 78.7 MB > 256 MB Infinity Cache
+    else:
+        g, inputs, outs, work, extra = workloads.conv_f32()
+        config = {"workload": "Conv2d fp32 + bias + ReLU, N=1, 64->64, 56x56, 3x3 s1 p1", "batch": 1}
+        dtype = "f32"
+    rts = [HipGraphRuntime(g, be) for _ in range(rotate)]
+    for rt in rts:
+        for k, v in inputs.items():
+            rt.set_input_bytes(k, v)
+        if not args.no_capture:
+            rt.enable_capture(True)
+    t_setup = time.perf_counter() - t_setup
+    images = work["images"]
+
+    for i in range(args.warmup):
+        rts[i % rotate].run()
+    be.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        rts[i % rotate].run()
+    be.synchronize()
+    el = time.perf_counter() - t0
+    ms_per_step = el * 1e3 / args.steps
+    value = images * args.steps / el
+
+    launches = rts[0].launches()
+    ms, fams = profile(rts, launches, args.profile_iters)
+    dom = fams[0]
+    roof = roofline_of(dom)
+    kernels = []
+    for f in fams[:8]:
+        r = roofline_of(f)
+        kernels.append({"kernel": f["kernel"], "launches": f["launches"], "ms": round(f["ms"], 4),
+                        "achieved": r["achieved"], "unit": r["unit"], "frac": r["frac"]})
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        if wl == "yolov8n_int8":
+            cpu = cpu_baseline_yolo_int8(extra, inputs[extra["input"]], args.cpu_seconds)
+        elif wl == "yolov8n_f16":
+            cpu = cpu_baseline_yolo_f16(extra, inputs[extra["input"]], args.cpu_seconds)
+        elif wl == "qlinearconv":
+            cpu = cpu_baseline_qconv(extra, args.cpu_seconds)
+        elif wl == "dwconv":
+            cpu = cpu_baseline_dwconv(extra, args.cpu_seconds)
+        else:
+            cpu = cpu_baseline_conv_f32(extra, args.cpu_seconds)
+
+    line = {
+        "metric": METRIC if wl == "yolov8n_int8" else f"images/sec {wl} on 1 MI355X",
+        "value": round(value, 2),
+        "unit": "images/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dtype,
+        "data": "synthetic (seeded LCG inputs, random-init weights with BN folded)",
+        "config": config,
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "kernels": kernels,
+        "gpu_ms_sum_of_launches": round(float(ms.sum()), 4),
+        "setup_s": round(t_setup, 1),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

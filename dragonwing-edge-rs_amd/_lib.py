@@ -95,6 +95,8 @@ SIGNATURES = {
     "dw_graph_destroy": (None, [P]),
     "dw_graph_add_tensor": (I, [P, S, P, I, I]),
     "dw_graph_set_initializer": (I, [P, S, P, Z]),
+    "dw_graph_set_quant": (I, [P, S, F, I]),
+    "dw_graph_set_channel_scales": (I, [P, S, P, Z]),
     "dw_graph_add_op": (I, [P, S, S, P, I, P, I, C.POINTER(DwOpParams)]),
     "dw_graph_set_io": (I, [P, P, I, P, I]),
     "dw_graph_fold_batchnorm": (I, [P]),

@@ -628,6 +628,28 @@ int dw_graph_set_initializer(dw_graph* gh, const char* name, const void* data, s
   API_END
 }
 
+int dw_graph_set_quant(dw_graph* gh, const char* name, float scale, int zero_point) {
+  API_BEGIN
+  dw::TensorInfo& ti = G(gh).tensor(name);
+  if (!(scale > 0.0f)) dw::fail(DW_ERR_INVALID, "scale must be > 0");
+  if (zero_point < 0 || zero_point > 255) dw::fail(DW_ERR_INVALID, "zero point must be in [0, 255]");
+  ti.has_q = true;
+  ti.scale = scale;
+  ti.zp = zero_point;
+  API_END
+}
+
+int dw_graph_set_channel_scales(dw_graph* gh, const char* name, const float* scales, size_t count) {
+  API_BEGIN
+  dw::TensorInfo& ti = G(gh).tensor(name);
+  if (ti.dims.empty() || (int64_t)count != ti.dims.back())
+    dw::fail(DW_ERR_INVALID, "channel scales must match the last (output-channel) dimension");
+  for (size_t i = 0; i < count; ++i)
+    if (!(scales[i] > 0.0f)) dw::fail(DW_ERR_INVALID, "channel scales must be > 0");
+  ti.ch_scales.assign(scales, scales + count);
+  API_END
+}
+
 int dw_graph_add_op(dw_graph* gh, const char* name, const char* op_type, const char* const* inputs,
                     int num_inputs, const char* const* outputs, int num_outputs,
                     const dw_op_params* params) {

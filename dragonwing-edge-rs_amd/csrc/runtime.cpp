@@ -219,9 +219,47 @@ void Runtime::lower(std::vector<Group>& groups) {
     Group gr;
     gr.ops = {i};
     used[i] = true;
+    if (op.type == "Conv" && op.p.group > 1) {
+      // CpuGraphRuntime::dispatch_conv2d: depthwise when group == c_in
+      // (runtime.rs:1412-1421); other groupings are an error there too.
+      if (op.p.group != T(op.in[0]).c || T(op.out[0]).c != T(op.in[0]).c)
+        fail(DW_ERR_UNSUPPORTED, "runtime: general grouped convolution (" + op.name + ")");
+      gr.kind = "dwconv";
+      gr.conv = i;
+      gr.in = op.in[0];
+      std::string cur = op.out[0];
+      int c = single(cur);
+      if (c >= 0 && (g.ops[c].type == "Relu" || g.ops[c].type == "SiLU")) {
+        gr.act = g.ops[c].type == "Relu" ? ACT_RELU : ACT_SILU;
+      } else if (!stats && !g.is_output(cur)) {
+        auto cs = g.consumers(cur);
+        if (cs.size() == 2) {
+          int s = -1, m = -1;
+          for (int k : cs) {
+            if (g.ops[k].type == "Sigmoid") s = k;
+            if (g.ops[k].type == "Mul") m = k;
+          }
+          if (s >= 0 && m >= 0 && single(g.ops[s].out[0]) == m) {
+            gr.act = ACT_SILU;
+            used[s] = true;
+            gr.ops.push_back(s);
+            T(g.ops[s].out[0]).materialized = false;
+            c = m;
+          }
+        }
+      }
+      if (gr.act != ACT_NONE) {
+        used[c] = true;
+        gr.ops.push_back(c);
+        T(cur).materialized = false;
+        cur = g.ops[c].out[0];
+      }
+      gr.out = cur;
+      groups.push_back(gr);
+      continue;
+    }
     if (op.type == "Conv") {
       const dw_op_params& p = op.p;
-      if (p.group > 1) fail(DW_ERR_UNSUPPORTED, "runtime: grouped/depthwise conv in a graph (" + op.name + ")");
       if ((p.dilations[0] > 1) || (p.dilations[1] > 1)) fail(DW_ERR_UNSUPPORTED, "runtime: dilation != 1");
       gr.kind = "conv";
       gr.conv = i;
@@ -509,6 +547,40 @@ std::string join_names(const GraphIR& g, const std::vector<int>& ops) {
 
 void Runtime::emit(const Group& gr) {
   if (gr.kind == "conv") return emit_conv(gr);
+  if (gr.kind == "dwconv") {
+    const OpNode& op = g.ops[gr.conv];
+    const TensorInfo& W = g.t[op.in[1]];
+    RtTensor& x = T(gr.in);
+    RtTensor& y = T(gr.out);
+    // weights [kh][kw][c][1] (HWIO with one output per group)
+    if (W.dims.size() != 4 || W.dims[2] != 1 || W.dims[3] != x.c)
+      fail(DW_ERR_UNSUPPORTED, "runtime: depthwise weights must be [kh,kw,1,C] after NHWC conversion");
+    if (x.c % 8 != 0 || x.pix_stride % 8 != 0 || x.abs_off % 8 != 0 || y.pix_stride % 8 != 0 ||
+        y.abs_off % 8 != 0)
+      fail(DW_ERR_UNSUPPORTED, "runtime: depthwise needs 8-channel aligned views (" + op.name + ")");
+    if (x.dtype != F16 && x.dtype != F32) fail(DW_ERR_UNSUPPORTED, "runtime: depthwise dtype");
+    DwArgs a{};
+    a.x = x.base;
+    a.y = y.base;
+    a.wt = upload(W.data.data(), W.data.size());
+    if (op.in.size() > 2 && !op.in[2].empty()) a.bias = upload(g.t[op.in[2]].data.data(), g.t[op.in[2]].data.size());
+    a.n = (int)x.n; a.h = (int)x.h; a.w = (int)x.w; a.c = (int)x.c;
+    a.kh = (int)W.dims[0]; a.kw = (int)W.dims[1];
+    a.sh = std::max(1, op.p.strides[0]); a.sw = std::max(1, op.p.strides[1]);
+    a.pt = op.p.pads[0]; a.pl = op.p.pads[1]; a.ho = (int)y.h; a.wo = (int)y.w;
+    a.act = gr.act;
+    a.x_pix_stride = x.pix_stride; a.x_c_off = x.abs_off;
+    a.y_pix_stride = y.pix_stride; a.y_c_off = y.abs_off;
+    const int dt = x.dtype;
+    Launch L;
+    L.kernel = dt == F16 ? "dwconv_f16" : "dwconv_f32";
+    L.op = join_names(g, gr.ops);
+    L.work = 2.0 * (double)y.pixels() * y.c * a.kh * a.kw;
+    L.bytes = (double)x.bytes() + (double)y.bytes() + W.data.size() + (a.bias ? y.c * dtype_size(dt) : 0);
+    L.fn = [=](hipStream_t st) { launch_dwconv(st, a, dt); };
+    launches.push_back(L);
+    return;
+  }
   if (gr.kind == "qconv") return emit_qconv(gr);
   if (gr.kind == "split") return;
   if (gr.kind == "concat") {

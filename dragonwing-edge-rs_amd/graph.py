@@ -97,6 +97,13 @@ class Graph:
         self.set_initializer(name, data)
         return name
 
+    def set_quant(self, name: str, scale: float, zero_point: int):
+        check(load().dw_graph_set_quant(self._h, name.encode(), float(scale), int(zero_point)))
+
+    def set_channel_scales(self, name: str, scales):
+        s = np.ascontiguousarray(scales, np.float32)
+        check(load().dw_graph_set_channel_scales(self._h, name.encode(), s.ctypes.data, s.size))
+
     def add_op(self, name: str, op_type: str, inputs, outputs, kind: str | None = None, **kw):
         p = _params(kind or KIND_OF_TYPE.get(op_type, "None"), **kw)
         check(load().dw_graph_add_op(self._h, name.encode(), op_type.encode(), _cstrs(inputs), len(inputs),

@@ -310,6 +310,11 @@ void dw_graph_destroy(dw_graph* g);
 int dw_graph_add_tensor(dw_graph* g, const char* name, const int64_t* dims, int rank, int dtype);
 /* Attach initializer bytes to a declared tensor (weights, biases, BN params). */
 int dw_graph_set_initializer(dw_graph* g, const char* name, const void* data, size_t len);
+/* Quantization parameters of a u8 tensor: real = (q - zero_point) * scale
+ * (the x_scale/x_zero_point inputs of an ONNX QLinearConv). */
+int dw_graph_set_quant(dw_graph* g, const char* name, float scale, int zero_point);
+/* Per-output-channel scales of an s8 weight tensor (zero point 0). */
+int dw_graph_set_channel_scales(dw_graph* g, const char* name, const float* scales, size_t count);
 /* Append a CompiledOp.  Empty-string inputs are optional-absent. */
 int dw_graph_add_op(dw_graph* g, const char* name, const char* op_type, const char* const* inputs,
                     int num_inputs, const char* const* outputs, int num_outputs,

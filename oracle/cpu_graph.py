@@ -50,7 +50,18 @@ class CpuGraph:
             b = ins[2] if len(ins) > 2 else None
             s, p = op["strides"], op["pads"]
             if op["group"] > 1:
-                raise NotImplementedError("grouped conv")
+                # dispatch_conv2d depthwise branch (runtime.rs:1412-1421, :1467-1473)
+                if op["group"] != x.shape[3]:
+                    raise NotImplementedError("grouped conv")
+                k = np.ascontiguousarray(w).reshape(w.shape[0], w.shape[1], -1)
+                if x.dtype == np.float32:
+                    y = oracle.depthwise_f32(x, k, s, (p[0], p[1]), self.threads)
+                    y = oracle.bias_add_f32(y, b) if b is not None else y
+                else:
+                    y = oracle.depthwise_fp16(x, k, s, (p[0], p[1]), self.threads)
+                    y = oracle.bias_add_f16(y, b) if b is not None else y
+                self.vals[out[0]] = y
+                return
             if x.dtype == np.float32:
                 y = oracle.conv2d_f32_nhwc(x, w, s, (p[0], p[1]), self.threads)
                 if b is not None:

@@ -132,3 +132,36 @@ def test_int8_graph_full_workload_bit_exact(backend):
         for o, gv in zip(info["outputs"], got):
             np.testing.assert_array_equal(gv[img:img + 1], ref[o], err_msg=f"{o} image {img}")
         print(f"image {img}: bit-exact on all three detect outputs", flush=True)
+
+
+def test_single_op_graphs(backend):
+    """The single-op workloads expressed as graphs: QLinearConv (bit-exact),
+    depthwise fp16 + SiLU (fp16 tolerance), fp32 conv + ReLU (bit-exact)."""
+    from dragonwing_edge_rs_amd import workloads
+
+    g, inputs, outs, work, c = workloads.qlinearconv()
+    rt = HipGraphRuntime(g, backend)
+    rt.set_input_bytes("x", inputs["x"])
+    rt.run()
+    got = rt.get_output_bytes("y").reshape(32, 40, 40, 256)
+    ref = oracle.qlinearconv_u8s8(c["x"], c["w"], c["bias"], (2, 2), (1, 1), c["x_scale"], c["x_zp"],
+                                  c["w_scales"], c["y_scale"], c["y_zp"])
+    np.testing.assert_array_equal(got, ref)
+    assert [L["kernel"].split("_")[0] for L in rt.launches()] == ["igemm"]
+
+    g, inputs, outs, work, (x, w, b) = workloads.dwconv()
+    rt = HipGraphRuntime(g, backend)
+    rt.set_input_bytes("x", inputs["x"])
+    rt.run()
+    got = rt.get_output_bytes("out").view(np.uint16).reshape(x.shape)
+    ref = oracle_run(g, {"x": x})["out"]
+    assert rel_err(oracle.f16_to_f32(got), oracle.f16_to_f32(ref)) <= 1e-2
+    assert [L["kernel"] for L in rt.launches()] == ["dwconv_f16"]
+
+    g, inputs, outs, work, (x, w, b) = workloads.conv_f32()
+    rt = HipGraphRuntime(g, backend)
+    rt.set_input_f32("x", x)
+    rt.run()
+    got = rt.get_output_bytes("out").view(np.float32).reshape(1, 56, 56, 64)
+    np.testing.assert_array_equal(got, oracle.relu_f32(oracle.bias_add_f32(oracle.conv2d_f32_nhwc(x, w, (1, 1), (1, 1)), b)))
+    assert [L["kernel"] for L in rt.launches()] == ["direct_conv"]
