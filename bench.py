@@ -200,6 +200,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-iters", type=int, default=5)
     ap.add_argument("--no-capture", action="store_true", help="replay launches eagerly instead of a HIP graph")
+    ap.add_argument("--dump-launches", default="", help="write per-launch timings (JSON lines) to this file")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this backend runs on one GPU; --gpus {args.gpus} is not supported "
@@ -263,6 +264,10 @@ def main():
 
     launches = rts[0].launches()
     ms, fams = profile(rts, launches, args.profile_iters)
+    if args.dump_launches:
+        with open(args.dump_launches, "w") as f:
+            for L, t in zip(launches, ms):
+                f.write(json.dumps(dict(L, ms=round(float(t), 5))) + "\n")
     dom = fams[0]
     roof = roofline_of(dom)
     kernels = []

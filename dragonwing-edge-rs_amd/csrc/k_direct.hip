@@ -4,12 +4,13 @@
 //       acc = fma(x, w, acc)                       (f32, single rounding)
 // (crates/dragonwing-cpu/src/ops.rs:1356-1436, :2572-2651, :2819-2933).
 //
-// direct_conv: one thread = one output pixel x 8 output channels.  A
-// wavefront covers 64 pixels of one 8-channel group, so the weight row for
-// (tap, ic) is wave-uniform and is fetched with scalar loads; inputs stream
-// per lane.  Used for fp32 convolutions, for convolutions whose c_in is not
-// a multiple of 8 (the 3-channel stem), and for the fp16 layers of the int8
-// graph that must match the CPU bit for bit.
+// direct_conv: one thread = one output pixel x a chunk of output channels
+// (up to 80).  A wavefront covers 64 pixels of one chunk, so the weight row
+// for (tap, ic) is wave-uniform and is fetched with scalar loads, and each
+// input value is read and decoded once for the whole chunk.  Used for fp32
+// convolutions, for convolutions whose c_in is not a multiple of 8 (the
+// 3-channel stem), and for the fp16 layers of the int8 graph that must match
+// the CPU bit for bit.
 //
 // dwconv: depthwise 3x3 (any k), channel multiplier 1.  One thread = one
 // pixel x 8 channels, so every load/store is a 16-byte (f16) or 32-byte
@@ -25,22 +26,73 @@ namespace {
 // relu_f32_scalar (ops.rs:208-220): x > 0 -> x, NaN -> NaN, else +0.
 __device__ __forceinline__ float relu_ref(float v) { return v > 0.0f ? v : (v != v ? v : 0.0f); }
 
-constexpr int OCG = 8;
+template <int IN_KIND>
+__device__ __forceinline__ float load1(const DirectArgs& a, size_t i) {
+  if (IN_KIND == 0) return ((const float*)a.x)[i];
+  if (IN_KIND == 1) return h2f(((const uint16_t*)a.x)[i]);
+  const int q = ((const uint8_t*)a.x)[i];
+  return round_f16((float)(q - a.in_zp) * a.in_scale);  // DequantizeLinear to f16, then read
+}
 
+// Four consecutive channels; the caller guarantees 4-element alignment.
+template <int IN_KIND>
+__device__ __forceinline__ void load4(const DirectArgs& a, size_t i, float v[4]) {
+  if (IN_KIND == 0) {
+    const float4 f = *reinterpret_cast<const float4*>((const float*)a.x + i);
+    v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+  } else if (IN_KIND == 1) {
+    const uint2 u = *reinterpret_cast<const uint2*>((const uint16_t*)a.x + i);
+    v[0] = h2f(u.x & 0xffff); v[1] = h2f(u.x >> 16); v[2] = h2f(u.y & 0xffff); v[3] = h2f(u.y >> 16);
+  } else {
+    const uint32_t u = *reinterpret_cast<const uint32_t*>((const uint8_t*)a.x + i);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = round_f16((float)((int)((u >> (8 * e)) & 0xff) - a.in_zp) * a.in_scale);
+  }
+}
+
+// One thread = one output pixel x OC output channels (OC | c_out).  The
+// workgroup first copies its weight slice [K][OC] (K = kh*kw*c_in) into
+// LDS; every lane of a wavefront then reads the same weight row (a
+// broadcast, free of bank conflicts), and each decoded input value feeds
+// OC accumulators.  Per output the FMA sequence is the reference's.
+template <int IN_KIND, int OC>
 __global__ __launch_bounds__(256) void direct_conv_kernel(const DirectArgs a) {
+  extern __shared__ float wl[];
+  const int K = a.kh * a.kw * a.cin;
+  const int oc0 = blockIdx.y * OC;
+  for (int i = threadIdx.x; i < K * OC; i += blockDim.x) {
+    const int k = i / OC, j = i - (i / OC) * OC;
+    wl[i] = a.wf[(size_t)k * a.cout + oc0 + j];
+  }
+  __syncthreads();
   const int p = blockIdx.x * blockDim.x + threadIdx.x;
-  const int oc0 = blockIdx.y * OCG;
   if (p >= a.m) return;
   const int hw = a.ho * a.wo;
   const int nn = p / hw;
   const int rem = p - nn * hw;
   const int oh = rem / a.wo;
   const int ow = rem - oh * a.wo;
-  const int nv = min(OCG, a.cout - oc0);
+  const bool vec4 = (a.cin & 3) == 0 && (a.x_pix_stride & 3) == 0 && (a.x_c_off & 3) == 0;
 
-  float acc[OCG];
+  float acc[OC];
 #pragma unroll
-  for (int j = 0; j < OCG; ++j) acc[j] = 0.0f;
+  for (int j = 0; j < OC; ++j) acc[j] = 0.0f;
+
+  auto fma_row = [&](float xv, const float* wr) {
+    if constexpr (OC % 4 == 0) {
+#pragma unroll
+      for (int j = 0; j < OC; j += 4) {
+        const float4 w4 = *reinterpret_cast<const float4*>(wr + j);
+        acc[j] = fmaf(xv, w4.x, acc[j]);
+        acc[j + 1] = fmaf(xv, w4.y, acc[j + 1]);
+        acc[j + 2] = fmaf(xv, w4.z, acc[j + 2]);
+        acc[j + 3] = fmaf(xv, w4.w, acc[j + 3]);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < OC; ++j) acc[j] = fmaf(xv, wr[j], acc[j]);
+    }
+  };
 
   for (int kh = 0; kh < a.kh; ++kh) {
     const int ih = oh * a.sh + kh - a.pt;
@@ -49,30 +101,23 @@ __global__ __launch_bounds__(256) void direct_conv_kernel(const DirectArgs a) {
       const int iw = ow * a.sw + kw - a.pl;
       if (iw < 0 || iw >= a.w) continue;
       const size_t xo = ((size_t)(nn * a.h + ih) * a.w + iw) * a.x_pix_stride + a.x_c_off;
-      const float* wrow = a.wf + ((size_t)(kh * a.kw + kw) * a.cin) * a.cout + oc0;
-      for (int ic = 0; ic < a.cin; ++ic) {
-        float xv;
-        if (a.in_kind == 0) {
-          xv = ((const float*)a.x)[xo + ic];
-        } else if (a.in_kind == 1) {
-          xv = h2f(((const uint16_t*)a.x)[xo + ic]);
-        } else {
-          const int q = ((const uint8_t*)a.x)[xo + ic];
-          xv = round_f16(((float)(q - a.in_zp) * a.in_scale));
-        }
-        const float* wr = wrow + (size_t)ic * a.cout;
-        if (nv == OCG) {
+      const float* wrow = wl + (size_t)(kh * a.kw + kw) * a.cin * OC;
+      if (vec4) {
+        for (int ic = 0; ic < a.cin; ic += 4) {
+          float xv[4];
+          load4<IN_KIND>(a, xo + ic, xv);
 #pragma unroll
-          for (int j = 0; j < OCG; ++j) acc[j] = fmaf(xv, wr[j], acc[j]);
-        } else {
-          for (int j = 0; j < nv; ++j) acc[j] = fmaf(xv, wr[j], acc[j]);
+          for (int e = 0; e < 4; ++e) fma_row(xv[e], wrow + (ic + e) * OC);
         }
+      } else {
+        for (int ic = 0; ic < a.cin; ++ic) fma_row(load1<IN_KIND>(a, xo + ic), wrow + ic * OC);
       }
     }
   }
 
   const size_t yo = (size_t)p * a.y_pix_stride + a.y_c_off + oc0;
-  for (int j = 0; j < nv; ++j) {
+#pragma unroll
+  for (int j = 0; j < OC; ++j) {
     const int oc = oc0 + j;
     if (a.out_kind == 0) {
       float v = acc[j];
@@ -193,9 +238,33 @@ __global__ __launch_bounds__(256) void dwconv_kernel(const DwArgs a) {
 }  // namespace
 
 void launch_direct_conv(hipStream_t st, const DirectArgs& a) {
-  dim3 grid((a.m + 255) / 256, (a.cout + OCG - 1) / OCG);
-  hipLaunchKernelGGL(direct_conv_kernel, grid, dim3(256), 0, st, a);
-  DW_HIP(hipGetLastError());
+  // Output-channel chunk: as wide as c_out and the 64 KB LDS weight slice
+  // allow (each decoded input feeds more FMAs), narrowed when there are too
+  // few pixels to fill the GPU.
+  const long K = (long)a.kh * a.kw * a.cin;
+  int oc = 0;
+  for (int c : {32, 16, 8, 4, 1})
+    if (a.cout % c == 0 && K * c * 4 <= 65536) { oc = c; break; }
+  if (!oc) fail(-2, "direct conv: kernel too large for the LDS weight slice");
+  const long waves = ((long)a.m + 63) / 64;
+  if (oc == 32 && waves * (a.cout / oc) < 2048 && a.cout % 16 == 0) oc = 16;
+  dim3 grid((a.m + 255) / 256, a.cout / oc);
+  const size_t lds = (size_t)K * oc * 4;
+#define DW_DC(KIND, O)                                                                         \
+  if (a.in_kind == KIND && oc == O) {                                                          \
+    hipLaunchKernelGGL((direct_conv_kernel<KIND, O>), grid, dim3(256), lds, st, a);            \
+    DW_HIP(hipGetLastError());                                                                 \
+    return;                                                                                    \
+  }
+#define DW_DC_ALL(O) DW_DC(0, O) DW_DC(1, O) DW_DC(2, O)
+  DW_DC_ALL(32)
+  DW_DC_ALL(16)
+  DW_DC_ALL(8)
+  DW_DC_ALL(4)
+  DW_DC_ALL(1)
+#undef DW_DC_ALL
+#undef DW_DC
+  fail(-2, "direct conv: no kernel for this channel count");
 }
 
 void launch_dwconv(hipStream_t st, const DwArgs& a, int dtype) {

@@ -306,6 +306,69 @@ __global__ __launch_bounds__(256) void maxpool_cascade3_kernel(const PoolArgs a,
   }
 }
 
+// SPPF cascade for planes that fit in LDS: one workgroup owns one image and
+// one 16-byte channel slice (16 u8 / 8 f16 / 4 f32 channels), keeps the
+// whole H x W plane in LDS and runs the three k x k pools as separable row
+// and column maxima, writing each result to its output view.  Max is exact,
+// so the order of comparisons does not change any value.
+typedef unsigned char u8x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+template <int ES>
+__device__ __forceinline__ uint4 vmax16(uint4 a, uint4 b) {
+  if constexpr (ES == 1) {
+    return __builtin_bit_cast(uint4, __builtin_elementwise_max(__builtin_bit_cast(u8x16, a),
+                                                               __builtin_bit_cast(u8x16, b)));
+  } else if constexpr (ES == 2) {
+    return __builtin_bit_cast(uint4, __builtin_elementwise_max(__builtin_bit_cast(f16x8, a),
+                                                               __builtin_bit_cast(f16x8, b)));
+  } else {
+    const float4 x = __builtin_bit_cast(float4, a), y = __builtin_bit_cast(float4, b);
+    return __builtin_bit_cast(uint4, make_float4(fmaxf(x.x, y.x), fmaxf(x.y, y.y), fmaxf(x.z, y.z),
+                                                 fmaxf(x.w, y.w)));
+  }
+}
+
+template <int ES>
+__global__ __launch_bounds__(256) void sppf_lds_kernel(const PoolArgs a, View y2, View y3) {
+  extern __shared__ uint4 plane[];
+  const int hw = a.h * a.w;
+  uint4* A = plane;       // current plane
+  uint4* B = plane + hw;  // row maxima
+  const int nn = blockIdx.x;
+  const int c0 = blockIdx.y * (16 / ES);
+  const int r = a.kh / 2;
+  auto gaddr = [&](const View& v, int pix) {
+    return (uint8_t*)v.base + ((size_t)(nn * hw + pix) * v.pix_stride + v.c_off + c0) * ES;
+  };
+  for (int i = threadIdx.x; i < hw; i += blockDim.x) A[i] = *reinterpret_cast<const uint4*>(gaddr(a.x, i));
+  __syncthreads();
+  const View outs[3] = {a.y, y2, y3};
+  for (int stage = 0; stage < 3; ++stage) {
+    for (int i = threadIdx.x; i < hw; i += blockDim.x) {
+      const int y = i / a.w, x = i - (i / a.w) * a.w;
+      uint4 m = A[i];
+      for (int d = 1; d <= r; ++d) {
+        if (x - d >= 0) m = vmax16<ES>(m, A[y * a.w + x - d]);
+        if (x + d < a.w) m = vmax16<ES>(m, A[y * a.w + x + d]);
+      }
+      B[i] = m;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < hw; i += blockDim.x) {
+      const int y = i / a.w, x = i - (i / a.w) * a.w;
+      uint4 m = B[i];
+      for (int d = 1; d <= r; ++d) {
+        if (y - d >= 0) m = vmax16<ES>(m, B[(y - d) * a.w + x]);
+        if (y + d < a.h) m = vmax16<ES>(m, B[(y + d) * a.w + x]);
+      }
+      A[i] = m;
+      *reinterpret_cast<uint4*>(gaddr(outs[stage], i)) = m;
+    }
+    __syncthreads();
+  }
+}
+
 // Nearest resize (resize_f32 Nearest, ops.rs:2320-2351):
 //   ih = clamp(round((oh + 0.5) * (h_in / h_out) - 0.5), 0, h_in - 1)
 // computed in f32 like the reference; `round` is half away from zero.
@@ -442,6 +505,21 @@ void launch_maxpool(hipStream_t st, const PoolArgs& a, int dtype) {
 void launch_maxpool_cascade3(hipStream_t st, const PoolArgs& a, View y2, View y3, int dtype) {
   const size_t total = (size_t)a.n * a.h * a.w * a.c;
   if (total == 0) return;
+  const int es = dtype_size(dtype);
+  const size_t lds = (size_t)2 * a.h * a.w * 16;
+  auto al16 = [&](const View& v) { return (v.pix_stride * es) % 16 == 0 && (v.c_off * es) % 16 == 0; };
+  if ((a.c * es) % 16 == 0 && lds <= 65536 && al16(a.x) && al16(a.y) && al16(y2) && al16(y3) &&
+      (dtype == U8 || dtype == F16 || dtype == F32)) {
+    const dim3 g(a.n, a.c * es / 16), b(256);
+    if (es == 1)
+      hipLaunchKernelGGL(sppf_lds_kernel<1>, g, b, lds, st, a, y2, y3);
+    else if (es == 2)
+      hipLaunchKernelGGL(sppf_lds_kernel<2>, g, b, lds, st, a, y2, y3);
+    else
+      hipLaunchKernelGGL(sppf_lds_kernel<4>, g, b, lds, st, a, y2, y3);
+    DW_HIP(hipGetLastError());
+    return;
+  }
   const dim3 g(grid_for(total)), b(256);
   switch (dtype) {
     case F32: hipLaunchKernelGGL(maxpool_cascade3_kernel<float>, g, b, 0, st, a, y2, y3); break;
