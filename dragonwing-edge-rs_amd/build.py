@@ -36,6 +36,9 @@ DEVICE = [
     f"--offload-arch={ARCH}",
     "-fno-gpu-flush-denormals-to-zero",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in ordinary VGPRs: no copies between VGPRs and AGPRs
+    # around the matrix instructions, and fewer registers per wave.
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
 ]
 
 

@@ -154,6 +154,7 @@ void require_igemm(const Geo& g, int esize) {
     dw::fail(DW_ERR_UNSUPPORTED, "MFMA conv needs c_in*esize % 16 == 0 (got c_in=" +
                                      std::to_string(g.ci) + ")");
   if (g.co % 4 != 0) dw::fail(DW_ERR_UNSUPPORTED, "MFMA conv needs c_out % 4 == 0");
+  if (g.kh * g.kw > 31) dw::fail(DW_ERR_UNSUPPORTED, "MFMA conv supports at most 31 filter taps");
 }
 
 // Packs HWIO weights into workspace slot 0 and returns the pointer.

@@ -77,7 +77,8 @@ struct IgemmArgs {
   float ra, rb;          // residual add: rint((a-za)*ra + (b-zb)*rb) + zy
   int za, zb, zy;
   const uint16_t* bias_h;  // EPI_F16 bias (f16 bits) or null
-  int tiles_p;             // number of pixel tiles (grid remap)
+  int kchunk;              // set by the launcher: k-steps per LDS weight chunk
+  int tile_bc, tile_pb;    // tile choice (channels, 16-pixel blocks per wave); 0 = heuristic
 };
 
 // Arguments of the direct convolution with the reference accumulation order.
@@ -96,7 +97,7 @@ struct DirectArgs {
   float in_scale; int in_zp;
   float out_scale; int out_zp;
   const uint8_t* lut;      // out u8: optional table applied after quantization
-  int groups_oc;           // number of 8-wide output-channel groups
+  int vec_out;             // set by the launcher: widest aligned store (16, 4 or 1 bytes)
 };
 
 // Depthwise convolution (channel multiplier 1).
@@ -126,6 +127,9 @@ const char* igemm_tile_name(const IgemmArgs& a, int esize);
 // Channel-tile width used for `cout` output channels; packed weights must
 // hold a multiple of it (cout_pad).
 int igemm_channel_tile(int cout);
+// Tile shapes launch_igemm can run for `a` (channel tile, pixel blocks per
+// wave); returns how many were written (at most `max`).
+int igemm_candidates(const IgemmArgs& a, int* bc, int* pb, int max);
 
 void launch_direct_conv(hipStream_t st, const DirectArgs& a);
 void launch_dwconv(hipStream_t st, const DwArgs& a, int dtype);

@@ -26,73 +26,69 @@ namespace {
 // relu_f32_scalar (ops.rs:208-220): x > 0 -> x, NaN -> NaN, else +0.
 __device__ __forceinline__ float relu_ref(float v) { return v > 0.0f ? v : (v != v ? v : 0.0f); }
 
+// Weights are read through the constant address space: the row for one
+// (tap, ic) is the same for every lane of a wavefront, so the compiler
+// fetches it with scalar loads and each FMA takes its weight from an SGPR
+// (no LDS traffic, no per-lane weight loads).
+typedef const __attribute__((address_space(4))) float* wrow_t;
+
+// One input element as the reference conv reads it.
 template <int IN_KIND>
-__device__ __forceinline__ float load1(const DirectArgs& a, size_t i) {
-  if (IN_KIND == 0) return ((const float*)a.x)[i];
-  if (IN_KIND == 1) return h2f(((const uint16_t*)a.x)[i]);
-  const int q = ((const uint8_t*)a.x)[i];
-  return round_f16((float)(q - a.in_zp) * a.in_scale);  // DequantizeLinear to f16, then read
+__device__ __forceinline__ float load1(const DirectArgs& a, const uint8_t* p) {
+  if (IN_KIND == 0) return *reinterpret_cast<const float*>(p);
+  if (IN_KIND == 1) return h2f(*reinterpret_cast<const uint16_t*>(p));
+  return round_f16((float)((int)*p - a.in_zp) * a.in_scale);  // DequantizeLinear to f16, then read
 }
 
-// Four consecutive channels; the caller guarantees 4-element alignment.
+// Elements per 16-byte input vector.
 template <int IN_KIND>
-__device__ __forceinline__ void load4(const DirectArgs& a, size_t i, float v[4]) {
-  if (IN_KIND == 0) {
-    const float4 f = *reinterpret_cast<const float4*>((const float*)a.x + i);
-    v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
-  } else if (IN_KIND == 1) {
-    const uint2 u = *reinterpret_cast<const uint2*>((const uint16_t*)a.x + i);
-    v[0] = h2f(u.x & 0xffff); v[1] = h2f(u.x >> 16); v[2] = h2f(u.y & 0xffff); v[3] = h2f(u.y >> 16);
-  } else {
-    const uint32_t u = *reinterpret_cast<const uint32_t*>((const uint8_t*)a.x + i);
+constexpr int vec_elems() {
+  return IN_KIND == 0 ? 4 : (IN_KIND == 1 ? 8 : 16);
+}
+
+// A 16-byte vector of consecutive input channels, decoded.
+template <int IN_KIND>
+__device__ __forceinline__ void load_vec(const DirectArgs& a, const uint8_t* p, float* v) {
+  const uint4 u = *reinterpret_cast<const uint4*>(p);
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = round_f16((float)((int)((u >> (8 * e)) & 0xff) - a.in_zp) * a.in_scale);
+  for (int i = 0; i < 4; ++i) {
+    if (IN_KIND == 0) {
+      v[i] = __builtin_bit_cast(float, w[i]);
+    } else if (IN_KIND == 1) {
+      v[2 * i] = h2f(w[i] & 0xffff);
+      v[2 * i + 1] = h2f(w[i] >> 16);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        v[4 * i + e] = round_f16((float)((int)((w[i] >> (8 * e)) & 0xff) - a.in_zp) * a.in_scale);
+    }
   }
 }
 
-// One thread = one output pixel x OC output channels (OC | c_out).  The
-// workgroup first copies its weight slice [K][OC] (K = kh*kw*c_in) into
-// LDS; every lane of a wavefront then reads the same weight row (a
-// broadcast, free of bank conflicts), and each decoded input value feeds
-// OC accumulators.  Per output the FMA sequence is the reference's.
-template <int IN_KIND, int OC>
+// One thread = one output pixel x OC consecutive output channels; all OC
+// accumulators consume each decoded input value, so the decode is paid once
+// per OC FMAs.  Per output the FMA sequence is the reference's.  VIN: the
+// input rows are 16-byte aligned and c_in is a whole number of vectors.
+template <int IN_KIND, int OC, bool VIN>
 __global__ __launch_bounds__(256) void direct_conv_kernel(const DirectArgs a) {
-  extern __shared__ float wl[];
-  const int K = a.kh * a.kw * a.cin;
-  const int oc0 = blockIdx.y * OC;
-  for (int i = threadIdx.x; i < K * OC; i += blockDim.x) {
-    const int k = i / OC, j = i - (i / OC) * OC;
-    wl[i] = a.wf[(size_t)k * a.cout + oc0 + j];
-  }
-  __syncthreads();
+  constexpr int ES = IN_KIND == 0 ? 4 : (IN_KIND == 1 ? 2 : 1);
+  constexpr int VN = vec_elems<IN_KIND>();
   const int p = blockIdx.x * blockDim.x + threadIdx.x;
   if (p >= a.m) return;
+  const int oc0 = blockIdx.y * OC;
   const int hw = a.ho * a.wo;
   const int nn = p / hw;
   const int rem = p - nn * hw;
   const int oh = rem / a.wo;
   const int ow = rem - oh * a.wo;
-  const bool vec4 = (a.cin & 3) == 0 && (a.x_pix_stride & 3) == 0 && (a.x_c_off & 3) == 0;
+  const int cin = a.cin, cout = a.cout;
+  const uint8_t* __restrict__ X = (const uint8_t*)a.x;
+  const wrow_t wbase = (wrow_t)(a.wf + oc0);
 
   float acc[OC];
 #pragma unroll
   for (int j = 0; j < OC; ++j) acc[j] = 0.0f;
-
-  auto fma_row = [&](float xv, const float* wr) {
-    if constexpr (OC % 4 == 0) {
-#pragma unroll
-      for (int j = 0; j < OC; j += 4) {
-        const float4 w4 = *reinterpret_cast<const float4*>(wr + j);
-        acc[j] = fmaf(xv, w4.x, acc[j]);
-        acc[j + 1] = fmaf(xv, w4.y, acc[j + 1]);
-        acc[j + 2] = fmaf(xv, w4.z, acc[j + 2]);
-        acc[j + 3] = fmaf(xv, w4.w, acc[j + 3]);
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < OC; ++j) acc[j] = fmaf(xv, wr[j], acc[j]);
-    }
-  };
 
   for (int kh = 0; kh < a.kh; ++kh) {
     const int ih = oh * a.sh + kh - a.pt;
@@ -100,49 +96,91 @@ __global__ __launch_bounds__(256) void direct_conv_kernel(const DirectArgs a) {
     for (int kw = 0; kw < a.kw; ++kw) {
       const int iw = ow * a.sw + kw - a.pl;
       if (iw < 0 || iw >= a.w) continue;
-      const size_t xo = ((size_t)(nn * a.h + ih) * a.w + iw) * a.x_pix_stride + a.x_c_off;
-      const float* wrow = wl + (size_t)(kh * a.kw + kw) * a.cin * OC;
-      if (vec4) {
-        for (int ic = 0; ic < a.cin; ic += 4) {
-          float xv[4];
-          load4<IN_KIND>(a, xo + ic, xv);
+      const uint8_t* xp = X + (((size_t)(nn * a.h + ih) * a.w + iw) * a.x_pix_stride + a.x_c_off) * ES;
+      const wrow_t wt = wbase + (size_t)(kh * a.kw + kw) * cin * cout;
+      if constexpr (VIN) {
+        for (int ic = 0; ic < cin; ic += VN) {
+          float xv[VN];
+          load_vec<IN_KIND>(a, xp + (size_t)ic * ES, xv);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) fma_row(xv[e], wrow + (ic + e) * OC);
+          for (int e = 0; e < VN; ++e) {
+            const wrow_t wr = wt + (size_t)(ic + e) * cout;
+#pragma unroll
+            for (int j = 0; j < OC; ++j) acc[j] = fmaf(xv[e], wr[j], acc[j]);
+          }
         }
       } else {
-        for (int ic = 0; ic < a.cin; ++ic) fma_row(load1<IN_KIND>(a, xo + ic), wrow + ic * OC);
+        for (int ic = 0; ic < cin; ++ic) {
+          const float xv = load1<IN_KIND>(a, xp + (size_t)ic * ES);
+          const wrow_t wr = wt + (size_t)ic * cout;
+#pragma unroll
+          for (int j = 0; j < OC; ++j) acc[j] = fmaf(xv, wr[j], acc[j]);
+        }
       }
     }
   }
 
+  // Epilogue: the rest of the fused group, then stores packed into 32-bit
+  // words (16- or 4-byte stores when the output view is aligned for them,
+  // else one store per element).
+  const int OES = a.out_kind == 0 ? 4 : (a.out_kind == 1 ? 2 : 1);
   const size_t yo = (size_t)p * a.y_pix_stride + a.y_c_off + oc0;
+  uint8_t* yb = (uint8_t*)a.y + yo * OES;
+  uint32_t words[(OC * 4 + 3) / 4];
 #pragma unroll
-  for (int j = 0; j < OC; ++j) {
-    const int oc = oc0 + j;
-    if (a.out_kind == 0) {
+  for (int i = 0; i < (OC * 4 + 3) / 4; ++i) words[i] = 0;
+  // (one fully unrolled loop per output type keeps each loop small enough
+  // to unroll, so acc and words stay in registers)
+  if (a.out_kind == 0) {
+#pragma unroll
+    for (int j = 0; j < OC; ++j) {
       float v = acc[j];
-      if (a.bias_f) v = v + a.bias_f[oc];
+      if (a.bias_f) v = v + a.bias_f[oc0 + j];
       if (a.act == ACT_RELU) {
         v = relu_ref(v);
       } else if (a.act == ACT_SILU) {
         const float s = 1.0f / (1.0f + expf(-v));
         v = v * s;
       }
-      ((float*)a.y)[yo + j] = v;
-    } else {
-      uint16_t hb = f2h(acc[j]);
-      if (a.bias_h) hb = f16_add_bits(hb, a.bias_h[oc]);
-      if (a.out_kind == 1) {
-        ((uint16_t*)a.y)[yo + j] = f16_act_bits(hb, a.act);
-      } else {
-        // QuantizeLinear of the stored f16 value.
-        float q = rintf(__fdiv_rn(h2f(hb), a.out_scale)) + (float)a.out_zp;
-        q = fminf(fmaxf(q, 0.0f), 255.0f);
-        int qi = (int)q;
-        if (a.lut) qi = a.lut[qi];
-        ((uint8_t*)a.y)[yo + j] = (uint8_t)qi;
-      }
+      words[j] = __builtin_bit_cast(uint32_t, v);
+      if (a.vec_out == 1) reinterpret_cast<float*>(yb)[j] = v;
     }
+  } else if (a.out_kind == 1) {
+#pragma unroll
+    for (int j = 0; j < OC; ++j) {
+      uint16_t hb = f2h(acc[j]);
+      if (a.bias_h) hb = f16_add_bits(hb, a.bias_h[oc0 + j]);
+      const uint16_t ob = f16_act_bits(hb, a.act);
+      words[j >> 1] |= (uint32_t)ob << (16 * (j & 1));
+      if (a.vec_out == 1) reinterpret_cast<uint16_t*>(yb)[j] = ob;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < OC; ++j) {
+      uint16_t hb = f2h(acc[j]);
+      if (a.bias_h) hb = f16_add_bits(hb, a.bias_h[oc0 + j]);
+      // QuantizeLinear of the stored f16 value.
+      float q = rintf(__fdiv_rn(h2f(hb), a.out_scale)) + (float)a.out_zp;
+      q = fminf(fmaxf(q, 0.0f), 255.0f);
+      int qi = (int)q;
+      if (a.lut) qi = a.lut[qi];
+      words[j >> 2] |= (uint32_t)qi << (8 * (j & 3));
+      if (a.vec_out == 1) yb[j] = (uint8_t)qi;
+    }
+  }
+  // (loops run to the f32 maximum with constant indices, so `words` stays
+  // in registers; the byte count of this output type bounds them)
+  const int nbytes = OC * OES;
+  if (a.vec_out == 16) {
+#pragma unroll
+    for (int i = 0; i < OC / 4; ++i)
+      if (16 * i < nbytes)
+        *reinterpret_cast<uint4*>(yb + 16 * i) =
+            make_uint4(words[4 * i], words[4 * i + 1], words[4 * i + 2], words[4 * i + 3]);
+  } else if (a.vec_out == 4) {
+#pragma unroll
+    for (int i = 0; i < OC; ++i)
+      if (4 * i < nbytes) *reinterpret_cast<uint32_t*>(yb + 4 * i) = words[i];
   }
 }
 
@@ -237,31 +275,53 @@ __global__ __launch_bounds__(256) void dwconv_kernel(const DwArgs a) {
 
 }  // namespace
 
-void launch_direct_conv(hipStream_t st, const DirectArgs& a) {
-  // Output-channel chunk: as wide as c_out and the 64 KB LDS weight slice
-  // allow (each decoded input feeds more FMAs), narrowed when there are too
-  // few pixels to fill the GPU.
-  const long K = (long)a.kh * a.kw * a.cin;
-  int oc = 0;
-  for (int c : {32, 16, 8, 4, 1})
-    if (a.cout % c == 0 && K * c * 4 <= 65536) { oc = c; break; }
-  if (!oc) fail(-2, "direct conv: kernel too large for the LDS weight slice");
+void launch_direct_conv(hipStream_t st, const DirectArgs& a_in) {
+  DirectArgs a = a_in;
+  const int es = a.in_kind == 0 ? 4 : (a.in_kind == 1 ? 2 : 1);
+  const int vn = 16 / es;
+  const bool vin = a.cin % vn == 0 && (a.x_pix_stride * es) % 16 == 0 && (a.x_c_off * es) % 16 == 0 &&
+                   ((uintptr_t)a.x & 15) == 0;
+  // Output channels per thread: the widest chunk of c_out that still gives
+  // about four wavefronts per CU (wide chunks pay the input decode once for
+  // more FMAs; narrow ones spread small layers over the GPU).
   const long waves = ((long)a.m + 63) / 64;
-  if (oc == 32 && waves * (a.cout / oc) < 2048 && a.cout % 16 == 0) oc = 16;
+  static const int wide[] = {80, 64, 40, 32, 16, 8, 4, 1};
+  static const int narrow[] = {16, 8, 4, 1};
+  const int* cand = vin ? wide : narrow;
+  const int ncand = vin ? 8 : 4;
+  // (chunks below 4 channels only when c_out is not a multiple of 4)
+  const int min_oc = a.cout % 4 == 0 ? 4 : 1;
+  int oc = 0;
+  for (int i = 0; i < ncand && !oc; ++i)
+    if (cand[i] >= min_oc && a.cout % cand[i] == 0 && waves * (a.cout / cand[i]) >= 1024) oc = cand[i];
+  if (!oc) oc = min_oc;  // too few pixels for any chunk: the narrowest
+  if (a.cout % oc != 0) fail(-2, "direct conv: no channel chunk for this c_out");
+  const int oes = a.out_kind == 0 ? 4 : (a.out_kind == 1 ? 2 : 1);
+  auto aligned = [&](int v) {
+    return (oc * oes) % v == 0 && (a.y_pix_stride * oes) % v == 0 && (a.y_c_off * oes) % v == 0 &&
+           ((uintptr_t)a.y % v) == 0;
+  };
+  a.vec_out = aligned(16) ? 16 : (aligned(4) ? 4 : 1);
   dim3 grid((a.m + 255) / 256, a.cout / oc);
-  const size_t lds = (size_t)K * oc * 4;
-#define DW_DC(KIND, O)                                                                         \
-  if (a.in_kind == KIND && oc == O) {                                                          \
-    hipLaunchKernelGGL((direct_conv_kernel<KIND, O>), grid, dim3(256), lds, st, a);            \
-    DW_HIP(hipGetLastError());                                                                 \
-    return;                                                                                    \
+#define DW_DC(KIND, O, V)                                                                     \
+  if (a.in_kind == KIND && oc == O && vin == V) {                                             \
+    hipLaunchKernelGGL((direct_conv_kernel<KIND, O, V>), grid, dim3(256), 0, st, a);          \
+    DW_HIP(hipGetLastError());                                                                \
+    return;                                                                                   \
   }
-#define DW_DC_ALL(O) DW_DC(0, O) DW_DC(1, O) DW_DC(2, O)
-  DW_DC_ALL(32)
-  DW_DC_ALL(16)
-  DW_DC_ALL(8)
-  DW_DC_ALL(4)
-  DW_DC_ALL(1)
+#define DW_DC_ALL(O, V) DW_DC(0, O, V) DW_DC(1, O, V) DW_DC(2, O, V)
+  DW_DC_ALL(80, true)
+  DW_DC_ALL(64, true)
+  DW_DC_ALL(40, true)
+  DW_DC_ALL(32, true)
+  DW_DC_ALL(16, true)
+  DW_DC_ALL(8, true)
+  DW_DC_ALL(4, true)
+  DW_DC_ALL(1, true)
+  DW_DC_ALL(16, false)
+  DW_DC_ALL(8, false)
+  DW_DC_ALL(4, false)
+  DW_DC_ALL(1, false)
 #undef DW_DC_ALL
 #undef DW_DC
   fail(-2, "direct conv: no kernel for this channel count");

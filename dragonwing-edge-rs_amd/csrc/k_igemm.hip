@@ -37,6 +37,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <algorithm>
 #include <type_traits>
 
 namespace dw {
@@ -53,6 +54,15 @@ __device__ __forceinline__ int swz(int row, int chunk) {
   return row * 64 + ((chunk ^ ((row >> 1) & 3)) << 4);
 }
 
+// Per-channel epilogue parameters of the workgroup's channel tile, staged
+// in LDS at the start (indexed by the channel's position in the tile).
+struct EpiLds {
+  const int* bias;         // EPI_QU8 bias' or null
+  const float* ms;         // EPI_QU8 multipliers
+  const uint8_t* lut;      // EPI_QU8 table (256 entries) or null
+  const uint16_t* bias_h;  // EPI_F16 bias or null
+};
+
 // f16 epilogue chain of CpuGraphRuntime: conv result rounded to f16, then
 // the bias pass, the activation and the residual add, each on stored f16.
 __device__ __forceinline__ uint16_t f16_chain(float acc, const uint16_t* bias_h, int ch, int act,
@@ -64,14 +74,16 @@ __device__ __forceinline__ uint16_t f16_chain(float acc, const uint16_t* bias_h,
   return hb;
 }
 
-// Epilogue for one 16x16 block: this lane holds channels ch..ch+3 of pixel p.
+// Epilogue for one 16x16 block: this lane holds channels ch..ch+3 of pixel
+// p (channel cl..cl+3 of the tile).
 template <int ESZ, typename AccT>
-__device__ __forceinline__ void epilogue4(const IgemmArgs& a, const AccT& v, int ch, int p) {
+__device__ __forceinline__ void epilogue4(const IgemmArgs& a, const EpiLds& e, const AccT& v, int ch, int cl,
+                                          int p) {
   const size_t yo = (size_t)p * a.y_pix_stride + a.y_c_off + ch;
   if constexpr (ESZ == 1) {
     if (a.epi == EPI_QU8) {
-      const int4 bi = a.bias_i ? *reinterpret_cast<const int4*>(a.bias_i + ch) : make_int4(0, 0, 0, 0);
-      const float4 ms = *reinterpret_cast<const float4*>(a.mscale + ch);
+      const int4 bi = e.bias ? *reinterpret_cast<const int4*>(e.bias + cl) : make_int4(0, 0, 0, 0);
+      const float4 ms = *reinterpret_cast<const float4*>(e.ms + cl);
       uint32_t rres = 0;
       if (a.res)
         rres = *reinterpret_cast<const uint32_t*>((const uint8_t*)a.res + (size_t)p * a.r_pix_stride +
@@ -84,7 +96,7 @@ __device__ __forceinline__ void epilogue4(const IgemmArgs& a, const AccT& v, int
         float q = rintf((float)accs[r] * mss[r]) + (float)a.y_zp;
         q = fminf(fmaxf(q, 0.0f), 255.0f);
         int qi = (int)q;
-        if (a.lut) qi = a.lut[qi];
+        if (e.lut) qi = e.lut[qi];
         if (a.res) {
           const int rb = (rres >> (8 * r)) & 0xff;
           const float f = (float)(qi - a.za) * a.ra + (float)(rb - a.zb) * a.rb;
@@ -115,56 +127,36 @@ __device__ __forceinline__ void epilogue4(const IgemmArgs& a, const AccT& v, int
       rres = *reinterpret_cast<const uint2*>((const uint16_t*)a.res + (size_t)p * a.r_pix_stride +
                                              a.r_c_off + ch);
     const bool hr = a.res != nullptr;
-    const uint32_t lo = (uint32_t)f16_chain(v[0], a.bias_h, ch + 0, a.act, hr, rres.x & 0xffff) |
-                        ((uint32_t)f16_chain(v[1], a.bias_h, ch + 1, a.act, hr, rres.x >> 16) << 16);
-    const uint32_t hi = (uint32_t)f16_chain(v[2], a.bias_h, ch + 2, a.act, hr, rres.y & 0xffff) |
-                        ((uint32_t)f16_chain(v[3], a.bias_h, ch + 3, a.act, hr, rres.y >> 16) << 16);
+    const uint32_t lo = (uint32_t)f16_chain(v[0], e.bias_h, cl + 0, a.act, hr, rres.x & 0xffff) |
+                        ((uint32_t)f16_chain(v[1], e.bias_h, cl + 1, a.act, hr, rres.x >> 16) << 16);
+    const uint32_t hi = (uint32_t)f16_chain(v[2], e.bias_h, cl + 2, a.act, hr, rres.y & 0xffff) |
+                        ((uint32_t)f16_chain(v[3], e.bias_h, cl + 3, a.act, hr, rres.y >> 16) << 16);
     *reinterpret_cast<uint2*>((uint16_t*)a.y + yo) = make_uint2(lo, hi);
   }
 }
 
-// Number of k-steps per LDS weight chunk (16 KB per buffer).
-template <int BC>
-constexpr int chunk_steps() {
-  return (16384 / (BC * 64)) > 0 ? (16384 / (BC * 64)) : 1;
-}
-
-// Bytes of LDS: two weight-chunk buffers, or the split-K partial sums.
-template <int BC, int PB, int KS>
-constexpr int smem_bytes() {
-  return (2 * chunk_steps<BC>() * BC * 64) > ((KS - 1) * (4 / KS) * 64 * (BC / 16) * PB * 16)
-             ? (2 * chunk_steps<BC>() * BC * 64)
-             : ((KS - 1) * (4 / KS) * 64 * (BC / 16) * PB * 16);
-}
-
-template <int ESZ, int BC, int PB, int KS>
+template <int ESZ, int BC, int PB, int PD>
 __global__ __launch_bounds__(256) void igemm_kernel(const IgemmArgs a) {
   constexpr int CB = BC / 16;       // 16-channel blocks (all channels of the tile per wave)
-  constexpr int KE = 64 / ESZ;      // elements per row per k-step
   constexpr int CE = 16 / ESZ;      // elements per 16-byte slice
-  constexpr int PG = 4 / KS;        // waves along pixels
   constexpr int WPIX = 16 * PB;     // pixels per wave
-  constexpr int WGPIX = PG * WPIX;  // pixels per workgroup
-  constexpr int KC = chunk_steps<BC>();
-  constexpr int ABYTES = KC * BC * 64;
-  constexpr int AQ = ABYTES / 16;         // 16-byte slices per chunk
-  constexpr int AREG = (AQ + 255) / 256;  // slices per thread
+  constexpr int WGPIX = 4 * WPIX;   // pixels per workgroup
   using acc_t = typename std::conditional<ESZ == 1, v4i, v4f>::type;
-  static_assert(BC % 16 == 0 && (KS == 1 || KS == 2 || KS == 4), "tile");
-  __shared__ __attribute__((aligned(16))) uint8_t smem[smem_bytes<BC, PB, KS>()];
+  static_assert(BC % 16 == 0 && PD >= 2, "tile");
+  // LDS: the weight chunk, fragment-major [k-step][channel block][lane][16 B],
+  // then the k-slice table (one int2 per 16-byte slice along K).
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
-  // scalars used in the k loop (kept in SGPRs)
   const uint8_t* __restrict__ X = a.x;
   const uint8_t* __restrict__ WPK = a.wpk;
   const int H = a.h, W = a.w, CIN = a.cin, KH = a.kh, KW = a.kw;
   const int XPS = a.x_pix_stride, XCO = a.x_c_off, KSTEPS = a.ksteps, COUTP = a.cout_pad;
+  const int KCH = a.kchunk;
   const uint32_t XXOR = a.xxor;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int pg = wave % PG;
-  const int ks = wave / PG;
 
   // XCD-aware tile order: workgroup b runs on XCD b % 8; give each XCD a
   // contiguous range of tiles (channel tiles of one pixel tile adjacent).
@@ -176,73 +168,101 @@ __global__ __launch_bounds__(256) void igemm_kernel(const IgemmArgs a) {
   const int ctiles = COUTP / BC;
   const int ptile = tile / ctiles;
   const int c0 = (tile - ptile * ctiles) * BC;
-  const int p0 = ptile * WGPIX + pg * WPIX;
+  const int p0 = ptile * WGPIX + wave * WPIX;
 
-  // ---- im2col state of this lane: pixels p0 + pb*16 + (lane & 15), slice lane >> 4
+  // ---- k-slice table: slice q of K (16 bytes, one filter tap) is at element
+  // offset koff from the pixel's top-left tap and belongs to tap `tap`
+  // (31 = past the end of K: always padding).  It does not depend on the
+  // pixel, so the workgroup builds it once.
+  // (the ring reads up to k-step KSTEPS + 2 * PD - 3, see the main loop)
+  int2* ktab = reinterpret_cast<int2*>(smem + KCH * (BC * 64));
+  const int nq = (KSTEPS + 2 * PD) * 4;
+  const int kelems = KH * KW * CIN;
+  for (int q = tid; q < nq; q += 256) {
+    const int e = q * CE;
+    int2 t = make_int2(0, 31);
+    if (e < kelems) {
+      const int tap = e / CIN, ci = e - (e / CIN) * CIN;
+      const int kh = tap / KW, kw = tap - (tap / KW) * KW;
+      t = make_int2((kh * W + kw) * XPS + ci, tap);
+    }
+    ktab[q] = t;
+  }
+
+  // ---- this lane's pixels p0 + pb*16 + (lane & 15): element offset of the
+  // top-left tap and the in-image bit of every tap
   const int hw_o = a.ho * a.wo;
-  int ih0[PB], iw0[PB], nb[PB];
-  bool pv[PB];
+  int pbase[PB];
+  uint32_t tmask[PB];
 #pragma unroll
   for (int pb = 0; pb < PB; ++pb) {
     const int p = p0 + pb * 16 + (lane & 15);
-    pv[pb] = p < a.m;
-    const int pp = pv[pb] ? p : 0;
+    const bool pv = p < a.m;
+    const int pp = pv ? p : 0;
     const int nn = pp / hw_o;
     const int r = pp - nn * hw_o;
     const int oh = r / a.wo;
     const int ow = r - oh * a.wo;
-    ih0[pb] = oh * a.sh - a.pt;
-    iw0[pb] = ow * a.sw - a.pl;
-    nb[pb] = nn * H;
+    const int ih0 = oh * a.sh - a.pt, iw0 = ow * a.sw - a.pl;
+    pbase[pb] = ((nn * H + ih0) * W + iw0) * XPS + XCO;
+    uint32_t m = 0;
+    for (int kh = 0; kh < KH; ++kh)
+      for (int kw = 0; kw < KW; ++kw)
+        if ((unsigned)(ih0 + kh) < (unsigned)H && (unsigned)(iw0 + kw) < (unsigned)W) m |= 1u << (kh * KW + kw);
+    tmask[pb] = pv ? m : 0u;
   }
-  int e_c = ks * KE + (lane >> 4) * CE;  // first k-step of this wave is `ks`
-  int e_kh = 0, e_kw = 0;
-#define DW_NORMALIZE()                      \
-  while (e_c >= CIN) {                      \
-    e_c -= CIN;                             \
-    if (++e_kw == KW) { e_kw = 0; ++e_kh; } \
-  }
-  DW_NORMALIZE();
 
+  // Weight chunks go to LDS with direct global->LDS loads: one 1 KB
+  // fragment per wave instruction, lane l writing bytes [16 l, 16 l + 16).
+  const int frag_lane = ((lane & 15) * 64 + (lane >> 4) * 16);  // this lane's slice in a 16-row block
+#define DW_ISSUE_A(s_first)                                                                         \
+  {                                                                                                 \
+    const int nfr_ = (min(KSTEPS, (s_first) + KCH) - (s_first)) * CB;                               \
+    for (int f = wave; f < nfr_; f += 4) {                                                          \
+      const int sl = f / CB, cb = f - (f / CB) * CB;                                                \
+      const uint8_t* src = WPK + ((size_t)((s_first) + sl) * COUTP + c0 + cb * 16) * 64 + frag_lane; \
+      __builtin_amdgcn_global_load_lds((const void*)src,                                            \
+                                       (__attribute__((address_space(3))) void*)(smem + f * 1024), \
+                                       16, 0, 0);                                                   \
+    }                                                                                               \
+  }
+  // this wave's LDS writes (and loads) have landed, then everyone's have
+#define DW_LDS_FENCE()              \
+  __builtin_amdgcn_s_waitcnt(0);    \
+  __syncthreads();
+
+  // Epilogue parameters of the channel tile, also copied to LDS (one wave
+  // each): bias' and multipliers, the activation table, or the f16 bias.
+  uint8_t* sx = smem + KCH * (BC * 64) + nq * sizeof(int2);
+  const int nvalid = min(BC, a.cout - c0);  // a multiple of 4
+  EpiLds ep{nullptr, nullptr, nullptr, nullptr};
+  if (a.epi == EPI_QU8) {
+    ep.bias = a.bias_i ? reinterpret_cast<const int*>(sx) : nullptr;
+    ep.ms = reinterpret_cast<const float*>(sx + BC * 4);
+    ep.lut = a.lut ? sx + BC * 8 : nullptr;
+  } else if (a.epi == EPI_F16 && a.bias_h) {
+    ep.bias_h = reinterpret_cast<const uint16_t*>(sx);
+  }
+
+  __syncthreads();  // the k-slice table is complete
+  // ---- im2col ring: k-step s lives in bq[s % PD], loaded PD - 1 steps
+  // ahead.  The ring holds the raw loads and their in-image flags; the xor
+  // and the pad select happen when the k-step is consumed, so nothing waits
+  // for a load before its k-step comes up.  Every k-step issues exactly PB
+  // loads, also past the last k-step (those read the pad), so the compiler's
+  // load counters stay exact and a k-step waits only for its own loads.
   const u32x4 padv = {a.xpad, a.xpad, a.xpad, a.xpad};
-#define DW_LOAD_B(dst)                                                                                  \
-  _Pragma("unroll") for (int pb = 0; pb < PB; ++pb) {                                                   \
-    const int ih = ih0[pb] + e_kh;                                                                      \
-    const int iw = iw0[pb] + e_kw;                                                                      \
-    const bool ok = pv[pb] && e_kh < KH && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W;    \
-    /* branch-free: out-of-image taps read the tensor base, then take the pad */                        \
-    const int off = ok ? ((nb[pb] + ih) * W + iw) * XPS + XCO + e_c : 0;                                \
-    u32x4 v = *reinterpret_cast<const u32x4*>(X + (size_t)off * ESZ);                                   \
-    if (ESZ == 1) v ^= XXOR;                                                                            \
-    dst[pb] = ok ? v : padv;                                                                            \
-  }
-
-  // ---- weight chunks: thread-strided 16-byte slices of [KC][BC][64 B]
-  const int nchunks = (KSTEPS + KC - 1) / KC;
-  u32x4 areg[AREG];
-#define DW_FETCH_CHUNK(c)                                                                              \
-  {                                                                                                    \
-    const int s0_ = (c) * KC;                                                                          \
-    const int nq_ = min(KC, KSTEPS - s0_) * BC * 4;                                                    \
-    _Pragma("unroll") for (int t = 0; t < AREG; ++t) {                                                 \
-      /* clamped index: every load is valid, so areg stays in registers */                            \
-      const int q = min(tid + 256 * t, nq_ - 1);                                                       \
-      const int sl = q / (BC * 4), r = q - sl * (BC * 4);                                              \
-      areg[t] = *reinterpret_cast<const u32x4*>(WPK + ((size_t)(s0_ + sl) * COUTP + c0 + (r >> 2)) * 64 + \
-                                                (r & 3) * 16);                                         \
-    }                                                                                                  \
-  }
-#define DW_STORE_CHUNK(c, buf)                                                                       \
-  {                                                                                                    \
-    const int s0_ = (c) * KC;                                                                          \
-    const int nq_ = min(KC, KSTEPS - s0_) * BC * 4;                                                    \
-    uint8_t* As_ = smem + (buf) * ABYTES;                                                              \
-    _Pragma("unroll") for (int t = 0; t < AREG; ++t) {                                                 \
-      /* same clamp as the fetch: surplus threads rewrite the last slice with its own value */         \
-      const int q = min(tid + 256 * t, nq_ - 1);                                                       \
-      const int sl = q / (BC * 4), r = q - sl * (BC * 4);                                              \
-      *reinterpret_cast<u32x4*>(As_ + sl * (BC * 64) + swz(r >> 2, r & 3)) = areg[t];                  \
-    }                                                                                                  \
+  const int2* my_tab = ktab + (lane >> 4);
+#define DW_LOAD_B(s_, dst, dok)                                                      \
+  {                                                                                  \
+    const int2 t_ = my_tab[(s_) * 4];                                                \
+    _Pragma("unroll") for (int pb = 0; pb < PB; ++pb) {                              \
+      const bool ok = (tmask[pb] >> t_.y) & 1u;                                      \
+      /* out-of-image taps read the tensor base, then take the pad */              \
+      const int off = ok ? pbase[pb] + t_.x : 0;                                     \
+      dst[pb] = *reinterpret_cast<const u32x4*>(X + (size_t)(unsigned)off * ESZ);    \
+      dok[pb] = ok;                                                                  \
+    }                                                                                \
   }
 
   acc_t acc[CB][PB];
@@ -251,78 +271,69 @@ __global__ __launch_bounds__(256) void igemm_kernel(const IgemmArgs a) {
 #pragma unroll
     for (int pb = 0; pb < PB; ++pb) acc[cb][pb] = acc_t{0, 0, 0, 0};
 
-  DW_FETCH_CHUNK(0);
-  DW_STORE_CHUNK(0, 0);
-  int my_s = ks;  // next k-step this wave computes
-  u32x4 bcur[PB], bnext[PB];
-  if (my_s < KSTEPS) {
-    DW_LOAD_B(bcur);
-  }
-  __syncthreads();
+  u32x4 bq[PD][PB];
+  bool bok[PD][PB];
+#pragma unroll
+  for (int r = 0; r < PD - 1; ++r) DW_LOAD_B(r, bq[r], bok[r]);
 
-  const int arow = lane & 15;
-  const int kslice = lane >> 4;
-  for (int c = 0; c < nchunks; ++c) {
-    const bool more = c + 1 < nchunks;
-    if (more) DW_FETCH_CHUNK(c + 1);
-    const uint8_t* As = smem + (c & 1) * ABYTES;
-    const int s1 = min(KSTEPS, (c + 1) * KC);
-    while (my_s < s1) {
-      const int nxt = my_s + KS;
-      if (nxt < KSTEPS) {
-        e_c += KS * KE;
-        DW_NORMALIZE();
-        DW_LOAD_B(bnext);
+  // All of the workgroup's start-up loads are in flight together: the first
+  // PD - 1 im2col k-steps, the first weight chunk and the epilogue data.
+  DW_ISSUE_A(0);
+  if (a.epi == EPI_QU8) {
+    if (wave == 0 && a.bias_i && lane < nvalid / 4)
+      __builtin_amdgcn_global_load_lds((const void*)(a.bias_i + c0 + lane * 4),
+                                       (__attribute__((address_space(3))) void*)sx, 16, 0, 0);
+    if (wave == 1 && lane < nvalid / 4)
+      __builtin_amdgcn_global_load_lds((const void*)(a.mscale + c0 + lane * 4),
+                                       (__attribute__((address_space(3))) void*)(sx + BC * 4), 16, 0, 0);
+    if (wave == 2 && a.lut && lane < 16)
+      __builtin_amdgcn_global_load_lds((const void*)(a.lut + lane * 16),
+                                       (__attribute__((address_space(3))) void*)(sx + BC * 8), 16, 0, 0);
+  } else if (a.epi == EPI_F16 && a.bias_h) {
+    if (wave == 0 && lane < nvalid / 2)
+      __builtin_amdgcn_global_load_lds((const void*)(a.bias_h + c0 + lane * 2),
+                                       (__attribute__((address_space(3))) void*)sx, 4, 0, 0);
+  }
+  DW_LDS_FENCE();
+
+  int next_chunk = KCH, chunk0 = 0;
+  for (int s0 = 0; s0 < KSTEPS; s0 += PD) {
+#pragma unroll
+    for (int r = 0; r < PD; ++r) {
+      const int s = s0 + r;
+      if (s < KSTEPS && s == next_chunk) {
+        __syncthreads();  // every wave is done with the previous chunk
+        chunk0 = s;
+        next_chunk = s + KCH;
+        DW_ISSUE_A(s);
+        DW_LDS_FENCE();
       }
-      const uint8_t* Arow = As + (my_s - c * KC) * (BC * 64);
+      DW_LOAD_B(s + PD - 1, bq[(r + PD - 1) % PD], bok[(r + PD - 1) % PD]);
+      if (s < KSTEPS) {
+        u32x4 bcur[PB];
 #pragma unroll
-      for (int cb = 0; cb < CB; ++cb) {
-        const v4i af = *reinterpret_cast<const v4i*>(Arow + swz(cb * 16 + arow, kslice));
+        for (int pb = 0; pb < PB; ++pb) bcur[pb] = bok[r][pb] ? (bq[r][pb] ^ XXOR) : padv;
+        const uint8_t* Af = smem + (s - chunk0) * (CB * 1024) + lane * 16;
 #pragma unroll
-        for (int pb = 0; pb < PB; ++pb) {
-          if constexpr (ESZ == 1) {
-            acc[cb][pb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, __builtin_bit_cast(v4i, bcur[pb]),
-                                                                acc[cb][pb], 0, 0, 0);
-          } else {
-            acc[cb][pb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                __builtin_bit_cast(v8h, af), __builtin_bit_cast(v8h, bcur[pb]), acc[cb][pb], 0, 0, 0);
+        for (int cb = 0; cb < CB; ++cb) {
+          const v4i af = *reinterpret_cast<const v4i*>(Af + cb * 1024);
+#pragma unroll
+          for (int pb = 0; pb < PB; ++pb) {
+            if constexpr (ESZ == 1) {
+              acc[cb][pb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, __builtin_bit_cast(v4i, bcur[pb]),
+                                                                  acc[cb][pb], 0, 0, 0);
+            } else {
+              acc[cb][pb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                  __builtin_bit_cast(v8h, af), __builtin_bit_cast(v8h, bcur[pb]), acc[cb][pb], 0, 0, 0);
+            }
           }
         }
       }
-#pragma unroll
-      for (int pb = 0; pb < PB; ++pb) bcur[pb] = bnext[pb];
-      my_s = nxt;
     }
-    if (more) DW_STORE_CHUNK(c + 1, (c + 1) & 1);
-    __syncthreads();
   }
-#undef DW_NORMALIZE
+#undef DW_ISSUE_A
+#undef DW_LDS_FENCE
 #undef DW_LOAD_B
-#undef DW_FETCH_CHUNK
-#undef DW_STORE_CHUNK
-
-  // ---- split-K: waves ks > 0 hand their partial sums to wave ks == 0
-  if constexpr (KS > 1) {
-    // (the final barrier of the k loop guarantees smem is free)
-    acc_t* red = reinterpret_cast<acc_t*>(smem);
-    if (ks > 0) {
-      acc_t* dst = red + (((ks - 1) * PG + pg) * 64 + lane) * (CB * PB);
-#pragma unroll
-      for (int cb = 0; cb < CB; ++cb)
-#pragma unroll
-        for (int pb = 0; pb < PB; ++pb) dst[cb * PB + pb] = acc[cb][pb];
-    }
-    __syncthreads();
-    if (ks > 0) return;
-#pragma unroll
-    for (int k2 = 1; k2 < KS; ++k2) {
-      const acc_t* src = red + (((k2 - 1) * PG + pg) * 64 + lane) * (CB * PB);
-#pragma unroll
-      for (int cb = 0; cb < CB; ++cb)
-#pragma unroll
-        for (int pb = 0; pb < PB; ++pb) acc[cb][pb] += src[cb * PB + pb];
-    }
-  }
 
   // ---- epilogue: lane holds channels ch..ch+3 of pixel p for every block
 #pragma unroll
@@ -332,7 +343,7 @@ __global__ __launch_bounds__(256) void igemm_kernel(const IgemmArgs a) {
 #pragma unroll
     for (int pb = 0; pb < PB; ++pb) {
       const int p = p0 + pb * 16 + (lane & 15);
-      if (p < a.m) epilogue4<ESZ>(a, acc[cb][pb], ch, p);
+      if (p < a.m) epilogue4<ESZ>(a, ep, acc[cb][pb], ch, ch - c0, p);
     }
   }
 }
@@ -366,7 +377,7 @@ __global__ void qconv_bias_kernel(const int8_t* __restrict__ w, const int* __res
 }
 
 struct TileCfg {
-  int bc, pb, ks;
+  int bc, pb, pd, kchunk;
 };
 
 int channel_tile(int cout) {
@@ -379,64 +390,69 @@ int channel_tile(int cout) {
   return 16;
 }
 
-// Split-K partial sums must fit the 64 KB of LDS a workgroup may use.
-bool splitk_fits(int bc, int pb, int ks) {
-  if (ks == 1) return true;
-  return (ks - 1) * (4 / ks) * 64 * (bc / 16) * pb * 16 <= 65536;
+// LDS for the weight chunk of one workgroup: two workgroups fit a CU.
+constexpr int kWeightLds = 65536;
+
+// Prefetch depth of the im2col ring: deeper for narrow pixel tiles, whose
+// k-steps are short, so about the same time's worth of loads is in flight.
+int ring_depth(int pb) { return pb == 4 ? 4 : (pb == 2 ? 6 : 8); }
+
+bool tile_ok(const IgemmArgs& a, int bc, int pb) {
+  const int bcs[] = {128, 96, 80, 64, 48, 32, 16};
+  bool known = false;
+  for (int b : bcs) known |= b == bc;
+  return known && (pb == 1 || pb == 2 || pb == 4) && bc <= channel_tile(a.cout) && a.cout_pad % bc == 0;
 }
 
-// Tile shape for a problem: the widest pixel tile that still yields at
-// least two workgroups per CU; otherwise split the k-steps across the four
-// waves (the deep, small-spatial layers).
+TileCfg make_tile(const IgemmArgs& a, int bc, int pb) {
+  const int kchunk = std::max(1, std::min(a.ksteps, kWeightLds / (bc * 64)));
+  return {bc, pb, ring_depth(pb), kchunk};
+}
+
+// Tile shape for a problem: an explicit choice (a.tile_bc / a.tile_pb, set
+// by the graph runtime's tuner), else the widest channel tile and the widest
+// pixel tile (16 * pb pixels per wave) that still gives about two
+// workgroups per CU.  The weight slice of the channel tile is staged in
+// chunks of at most kWeightLds bytes.
 TileCfg pick(const IgemmArgs& a) {
+  // Override for tests and tuning runs: "BC,PB" (or "PB" with the default
+  // channel tile), applied where it is a valid shape for the problem.
+  if (const char* env = getenv("DW_IGEMM_TILE")) {
+    int v0 = 0, v1 = 0;
+    const int nv = sscanf(env, "%d,%d", &v0, &v1);
+    if (nv == 2 && tile_ok(a, v0, v1)) return make_tile(a, v0, v1);
+    if (nv == 1 && tile_ok(a, channel_tile(a.cout), v0)) return make_tile(a, channel_tile(a.cout), v0);
+  }
+  if (a.tile_bc && tile_ok(a, a.tile_bc, a.tile_pb)) return make_tile(a, a.tile_bc, a.tile_pb);
   const int bc = channel_tile(a.cout);
-  // Tuning override "PB,KS" (pixel blocks per wave, k-split), e.g. "2,2".
-  static const char* env = getenv("DW_IGEMM_TILE");
-  if (env) {
-    int pb = 0, ks = 0;
-    if (sscanf(env, "%d,%d", &pb, &ks) == 2 && (pb == 1 || pb == 2 || pb == 4) &&
-        (ks == 1 || ks == 2 || ks == 4) && splitk_fits(bc, pb, ks))
-      return {bc, pb, ks};
+  const int ctiles = a.cout_pad / bc;
+  for (int pb : {4, 2, 1}) {
+    const long wgs = (long)((a.m + 64 * pb - 1) / (64 * pb)) * ctiles;
+    if (wgs >= 512) return make_tile(a, bc, pb);
   }
-  const int ctiles = (a.cout_pad + bc - 1) / bc;
-  const TileCfg opts[] = {{bc, 4, 1}, {bc, 4, 2}, {bc, 2, 2}, {bc, 4, 4}, {bc, 2, 4}, {bc, 1, 4}};
-  TileCfg best = {bc, 1, 1};
-  long best_wgs = 0;
-  for (const TileCfg& t : opts) {
-    if (!splitk_fits(t.bc, t.pb, t.ks)) continue;
-    if (t.ks > 1 && a.ksteps < 2 * t.ks) continue;
-    const int wgpix = (4 / t.ks) * 16 * t.pb;
-    const long wgs = (long)((a.m + wgpix - 1) / wgpix) * ctiles;
-    if (wgs >= 512) return t;
-    if (wgs > best_wgs) {
-      best_wgs = wgs;
-      best = t;
-    }
-  }
-  return best;
+  return make_tile(a, bc, 1);
 }
 
 template <int ESZ, int BC>
 bool launch_bc(hipStream_t st, const IgemmArgs& a, const TileCfg& t, dim3 grid) {
-#define DW_T(PB, KS)                                                                       \
-  if (t.pb == PB && t.ks == KS) {                                                          \
-    hipLaunchKernelGGL((igemm_kernel<ESZ, BC, PB, KS>), grid, dim3(256), 0, st, a);        \
+  // weight chunk + k-slice table
+  // weight chunk + k-slice table + epilogue data (bias', multipliers, table)
+  const size_t lds = (size_t)t.kchunk * BC * 64 + (size_t)(a.ksteps + 2 * t.pd) * 4 * sizeof(int2) + BC * 8 + 256;
+#define DW_T(PB, PD)                                                                       \
+  if (t.pb == PB && t.pd == PD) {                                                          \
+    hipLaunchKernelGGL((igemm_kernel<ESZ, BC, PB, PD>), grid, dim3(256), lds, st, a);      \
     return true;                                                                           \
   }
-  DW_T(4, 1)
-  DW_T(4, 2)
-  DW_T(2, 2)
   DW_T(4, 4)
-  DW_T(2, 4)
-  DW_T(1, 4)
-  DW_T(1, 1)
+  DW_T(2, 6)
+  DW_T(1, 8)
 #undef DW_T
   return false;
 }
 
 template <int ESZ>
 void launch_cfg(hipStream_t st, const IgemmArgs& a, const TileCfg& t) {
-  const int wgpix = (4 / t.ks) * 16 * t.pb;
+  const int wgpix = 64 * t.pb;
   const dim3 grid((unsigned)(((a.m + wgpix - 1) / wgpix) * (a.cout_pad / t.bc)));
   bool ok = false;
   switch (t.bc) {
@@ -455,17 +471,30 @@ void launch_cfg(hipStream_t st, const IgemmArgs& a, const TileCfg& t) {
 
 int igemm_channel_tile(int cout) { return channel_tile(cout); }
 
+int igemm_candidates(const IgemmArgs& a, int* bc, int* pb, int max) {
+  int n = 0;
+  for (int b : {128, 96, 80, 64, 48, 32, 16})
+    for (int p : {4, 2, 1})
+      if (n < max && tile_ok(a, b, p)) {
+        bc[n] = b;
+        pb[n] = p;
+        ++n;
+      }
+  return n;
+}
+
 const char* igemm_tile_name(const IgemmArgs& a, int esize) {
   static thread_local char buf[64];
   const TileCfg t = pick(a);
-  snprintf(buf, sizeof buf, "igemm_%s_c%d_p%d_k%d", esize == 1 ? "i8" : "f16", t.bc, 16 * t.pb * (4 / t.ks),
-           t.ks);
+  snprintf(buf, sizeof buf, "igemm_%s_c%d_p%d", esize == 1 ? "i8" : "f16", t.bc, 64 * t.pb);
   return buf;
 }
 
-void launch_igemm(hipStream_t st, const IgemmArgs& a, int esize) {
-  const TileCfg t = pick(a);
-  if (a.cout_pad % t.bc != 0) fail(-4, "igemm: cout_pad not a multiple of the channel tile");
+void launch_igemm(hipStream_t st, const IgemmArgs& a_in, int esize) {
+  const TileCfg t = pick(a_in);
+  if (a_in.cout_pad % t.bc != 0) fail(-4, "igemm: cout_pad not a multiple of the channel tile");
+  IgemmArgs a = a_in;
+  a.kchunk = t.kchunk;
   if (esize == 1)
     launch_cfg<1>(st, a, t);
   else

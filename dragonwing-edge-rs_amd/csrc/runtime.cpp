@@ -25,6 +25,7 @@
 #include <exception>
 #include <functional>
 #include <map>
+#include <memory>
 #include <set>
 #include <sstream>
 
@@ -56,6 +57,10 @@ struct Launch {
   double work = 0;   // algorithmic ops (MAC = 2)
   double bytes = 0;  // algorithmic bytes moved
   std::function<void(hipStream_t)> fn;
+  // implicit-GEMM launches: their arguments, shared with `fn`, so the tuner
+  // can change the tile shape after the launch list is built
+  std::shared_ptr<IgemmArgs> ig;
+  int esize = 0;
 };
 
 struct Group {
@@ -121,6 +126,8 @@ struct Runtime {
   void emit_conv(const Group& gr);
   void emit_qconv(const Group& gr);
   void emit_ew(const OpNode& op);
+  void push_igemm(Launch& L, const IgemmArgs& a, int esize);
+  void autotune();
   void run();
 };
 
@@ -182,6 +189,7 @@ void Runtime::build(Backend* b, const GraphIR& graph, bool stats_mode) {
         launches.push_back(S);
       }
   }
+  if (!stats) autotune();
 }
 
 // ---------------------------------------------------------------------------
@@ -726,7 +734,7 @@ void Runtime::emit_conv(const Group& gr) {
   L.work = 2.0 * macs;
 
   const bool mfma = g.dtype == DW_GRAPH_F16 && gr.in_kind == 1 && gr.out_kind == 1 && (ci * 2) % 16 == 0 &&
-                    co % 4 == 0 && (x.pix_stride * 2) % 16 == 0 && (x.abs_off * 2) % 16 == 0 &&
+                    co % 4 == 0 && kh * kw <= 31 && (x.pix_stride * 2) % 16 == 0 && (x.abs_off * 2) % 16 == 0 &&
                     (y.pix_stride % 4) == 0 && (y.abs_off % 4) == 0;
   if (mfma) {
     IgemmArgs a{};
@@ -756,11 +764,9 @@ void Runtime::emit_conv(const Group& gr) {
       a.r_c_off = r.abs_off;
       L.bytes += r.bytes();
     }
-    L.kernel = igemm_tile_name(a, 2);
     L.bytes += (double)x.bytes() + W.data.size() + y.pixels() * co * 2.0;
-    L.fn = [=](hipStream_t st) { launch_igemm(st, a, 2); };
     DW_HIP(hipStreamSynchronize(be->stream));
-    launches.push_back(L);
+    push_igemm(L, a, 2);
     return;
   }
   // direct (reference accumulation order)
@@ -824,8 +830,9 @@ void Runtime::emit_qconv(const Group& gr) {
   RtTensor& y = T(gr.out);
   const int kh = (int)W.dims[0], kw = (int)W.dims[1], ci = (int)W.dims[2], co = (int)W.dims[3];
   if (x.dtype != U8 || y.dtype != U8) fail(DW_ERR_RUNTIME, "runtime: QLinearConv needs u8 tensors");
-  if (ci % 16 != 0 || co % 4 != 0)
-    fail(DW_ERR_UNSUPPORTED, "runtime: QLinearConv needs c_in % 16 == 0 and c_out % 4 == 0 (" + op.name + ")");
+  if (ci % 16 != 0 || co % 4 != 0 || kh * kw > 31)
+    fail(DW_ERR_UNSUPPORTED, "runtime: QLinearConv needs c_in % 16 == 0, c_out % 4 == 0 and at most 31 taps (" +
+                                 op.name + ")");
   if (x.pix_stride % 16 != 0 || x.abs_off % 16 != 0 || y.pix_stride % 4 != 0 || y.abs_off % 4 != 0)
     fail(DW_ERR_RUNTIME, "runtime: misaligned view for " + op.name);
   IgemmArgs a{};
@@ -895,9 +902,68 @@ void Runtime::emit_qconv(const Group& gr) {
     L.bytes += r.bytes();
   }
   DW_HIP(hipStreamSynchronize(be->stream));
-  L.kernel = igemm_tile_name(a, 1);
-  L.fn = [=](hipStream_t st) { launch_igemm(st, a, 1); };
+  push_igemm(L, a, 1);
+}
+
+void Runtime::push_igemm(Launch& L, const IgemmArgs& a, int esize) {
+  auto ig = std::make_shared<IgemmArgs>(a);
+  L.ig = ig;
+  L.esize = esize;
+  L.kernel = igemm_tile_name(*ig, esize);
+  L.fn = [ig, esize](hipStream_t st) { launch_igemm(st, *ig, esize); };
   launches.push_back(L);
+}
+
+// Plan-time tuning of the implicit-GEMM tile shapes: every candidate shape
+// of every MFMA convolution is timed on the runtime's own buffers (one
+// warm-up launch, then the best of three), and the fastest is kept.  The
+// tile shape changes only the work split, never the order of the k-steps a
+// result is accumulated over, so outputs are identical for every choice.
+// The launches write only buffers the next run() rewrites.  Set
+// DW_AUTOTUNE=0 to keep the built-in heuristic (DW_IGEMM_TILE, which forces
+// a shape, also disables it).
+void Runtime::autotune() {
+  const char* env = getenv("DW_AUTOTUNE");
+  if ((env && env[0] == '0') || getenv("DW_IGEMM_TILE")) return;
+  hipStream_t st = be->stream;
+  hipEvent_t e0, e1;
+  DW_HIP(hipEventCreate(&e0));
+  DW_HIP(hipEventCreate(&e1));
+  for (auto& L : launches) {
+    if (!L.ig) continue;
+    IgemmArgs& a = *L.ig;
+    int bc[32], pb[32];
+    const int n = igemm_candidates(a, bc, pb, 32);
+    float best = 1e30f;
+    int bi = -1;
+    for (int i = 0; i < n; ++i) {
+      a.tile_bc = bc[i];
+      a.tile_pb = pb[i];
+      launch_igemm(st, a, L.esize);
+      float t_min = 1e30f;
+      for (int r = 0; r < 3; ++r) {
+        DW_HIP(hipEventRecord(e0, st));
+        launch_igemm(st, a, L.esize);
+        DW_HIP(hipEventRecord(e1, st));
+        DW_HIP(hipEventSynchronize(e1));
+        float ms = 0;
+        DW_HIP(hipEventElapsedTime(&ms, e0, e1));
+        t_min = std::min(t_min, ms);
+      }
+      if (t_min < best) {
+        best = t_min;
+        bi = i;
+      }
+    }
+    if (bi >= 0) {
+      a.tile_bc = bc[bi];
+      a.tile_pb = pb[bi];
+    }
+    L.kernel = igemm_tile_name(a, L.esize);
+  }
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  info.clear();
 }
 
 void Runtime::run() {

@@ -141,6 +141,38 @@ def test_qlinearconv_shapes_bit_exact(backend, geom, x_zp):
     np.testing.assert_array_equal(run_qconv(backend, c, s, p), oracle_qconv(c, s, p))
 
 
+def channel_tile(co):
+    for lim, bc in ((96, 128), (80, 96), (64, 80), (48, 64), (32, 48), (16, 32)):
+        if co > lim:
+            return bc
+    return 16
+
+
+def igemm_tiles(co):
+    """Every (channel tile, pixel blocks per wave) the implicit GEMM accepts
+    for c_out = co (the shapes the graph runtime's tuner chooses from)."""
+    top = channel_tile(co)
+    pad = -(-co // top) * top
+    return [(bc, pb) for bc in (128, 96, 80, 64, 48, 32, 16) if bc <= top and pad % bc == 0
+            for pb in (4, 2, 1)]
+
+
+@pytest.mark.parametrize("geom", [(2, 9, 11, 64, 256, 3, 2, 1), (1, 13, 7, 128, 80, 3, 1, 1),
+                                  (2, 10, 10, 48, 96, 1, 1, 0), (1, 6, 6, 256, 128, 3, 1, 1)])
+def test_qlinearconv_every_tile_bit_exact(backend, geom, monkeypatch):
+    # The last case has 36 k-steps, staged through LDS in several chunks.
+    n, h, w, ci, co, k, s, p = geom
+    r = synth.Rng(synth.seed_for(500 + sum(geom)))
+    c = dict(x=r.integers((n, h, w, ci), 0, 255).astype(np.uint8),
+             w=r.integers((k, k, ci, co), -127, 127).astype(np.int8),
+             bias=r.integers((co,), -4096, 4096).astype(np.int32),
+             w_scales=r.log_uniform((co,), 1e-3, 1e-2), x_scale=0.02, x_zp=128, y_scale=0.05, y_zp=128)
+    ref = oracle_qconv(c, s, p)
+    for bc, pb in igemm_tiles(co):
+        monkeypatch.setenv("DW_IGEMM_TILE", f"{bc},{pb}")
+        np.testing.assert_array_equal(run_qconv(backend, c, s, p), ref, err_msg=f"tile {bc},{pb}")
+
+
 def test_qlinearconv_golden_fixtures(backend):
     cases = json.loads((GOLDEN / "qlinear_cases.json").read_text())["qlinearconv"]
     for g in cases:
@@ -270,6 +302,25 @@ def test_conv_f16_mfma_within_tolerance(backend, geom, act):
     got = run_conv_f16(backend, xh, kh_, bh, s, p, act, exact=False)
     ref = oracle_conv_f16(xh, kh_, bh, s, p, act)
     assert rel_err(f16v(got), f16v(ref)) <= 1e-2
+
+
+def test_conv_f16_mfma_every_tile_identical(backend, monkeypatch):
+    # Tile shapes split the work differently but accumulate every output
+    # over the same k-steps in the same order: results agree bit for bit.
+    n, h, w, ci, co, k, s, p = 2, 11, 9, 64, 128, 3, 1, 1
+    r = synth.Rng(synth.seed_for(600))
+    xh = synth.f16_bits(r.normal((n, h, w, ci), 0.0, 1.0))
+    kh_ = synth.f16_bits(r.normal((k, k, ci, co), 0.0, (1.0 / (k * k * ci)) ** 0.5))
+    bh = synth.f16_bits(r.normal((co,), 0.0, 0.1))
+    ref = oracle_conv_f16(xh, kh_, bh, s, p, ops.ACT_SILU)
+    first = None
+    for bc, pb in igemm_tiles(co):
+        monkeypatch.setenv("DW_IGEMM_TILE", f"{bc},{pb}")
+        got = run_conv_f16(backend, xh, kh_, bh, s, p, ops.ACT_SILU, exact=False)
+        assert rel_err(f16v(got), f16v(ref)) <= 1e-2
+        if first is None:
+            first = got
+        np.testing.assert_array_equal(got, first, err_msg=f"tile {bc},{pb}")
 
 
 @pytest.mark.parametrize("geom", [(2, 32, 32, 3, 16, 3, 2, 1), (1, 12, 12, 64, 64, 1, 1, 0),
