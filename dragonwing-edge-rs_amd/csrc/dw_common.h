@@ -79,6 +79,7 @@ struct IgemmArgs {
   const uint16_t* bias_h;  // EPI_F16 bias (f16 bits) or null
   int kchunk;              // set by the launcher: k-steps per LDS weight chunk
   int tile_bc, tile_pb;    // tile choice (channels, 16-pixel blocks per wave); 0 = heuristic
+  int x_bytes;             // set by the launcher: bytes of the input view's buffer (< 2^31)
 };
 
 // Arguments of the direct convolution with the reference accumulation order.

@@ -1,0 +1,503 @@
+// Implicit-GEMM convolution kernel for CDNA4 matrix cores (gfx950): the
+// kernel template shared by the translation units that instantiate it.
+//
+// The convolution is the GEMM  Y[c][p] = sum_k W[k][c] * X[p][k]  with
+//   c = output channel, p = output pixel (n, oh, ow), k = (kh, kw, ci).
+// Both operands are consumed as 64-byte rows per k-step (64 int8 or 32 fp16
+// values): one wavefront instruction is v_mfma_i32_16x16x64_i8 (int8) or
+// v_mfma_f32_16x16x32_f16 (fp16), and each lane supplies a 16-byte slice of
+// one row of each operand (row = lane % 16, slice = lane / 16).
+//
+// Work split: a workgroup (4 waves) owns BC output channels x 64*PB output
+// pixels; every wave computes all BC channels of its own 16*PB pixels.
+//
+// Data movement:
+//  * weights (operand A), pre-packed as [k-step][c_out][64 B] rows, are
+//    copied to LDS with direct global->LDS loads, in fragment order (one
+//    1 KB fragment per wave instruction), in chunks of up to 64 KB (one
+//    chunk holds all of K for almost every layer);
+//  * im2col rows (operand B) go straight from the NHWC input to the MFMA
+//    source registers, through a ring of PD k-steps loaded PD - 1 steps
+//    ahead.  The per-lane address arithmetic is a lookup: a per-workgroup
+//    LDS table gives, for every 16-byte slice of K, its offset from the
+//    pixel's top-left tap and its tap number, and a per-pixel bitmask says
+//    which taps lie inside the image.  A 16-byte slice is 16 int8 / 8 fp16
+//    consecutive input channels of one tap, so c_in * esize must be a
+//    multiple of 16.  Out-of-image taps and k-steps past the end of K use
+//    buffer loads with an out-of-range offset (no memory access);
+//  * the per-channel epilogue data (bias', multipliers, activation table)
+//    are staged in LDS with the first weight chunk, so all start-up loads
+//    of a workgroup are in flight together;
+//  * workgroups are numbered so that neighbouring tiles land on the same
+//    XCD (the hardware deals workgroups round-robin over the 8 XCDs, each
+//    with its own L2), so input halos and weights are shared in L2.
+//
+// u8 inputs are mapped to s8 by xor 0x80 (x - 128); the missing
+// (128 - x_zp) * sum_k W is folded into the per-channel bias by the host, so
+// int8 results are exact.  Epilogues fuse what the reference runs as
+// separate passes: bias, the requantization with its rounding rule, a u8
+// activation table, the residual QLinearAdd, or the f16 rounding chain; all
+// stores go to channel-strided views, so concat outputs are written in place.
+// The common int8 epilogues are compiled as specialisations (EPV) so that
+// the per-value work is a straight instruction sequence.
+#pragma once
+
+#include "dw_common.h"
+#include "dw_device.h"
+
+#include <type_traits>
+
+namespace dw {
+
+// Tile shape of one launch.
+struct TileCfg {
+  int bc, pb, pd, kchunk;
+};
+
+// Epilogue specialisations.
+enum EpiVariant : int {
+  EPV_GENERIC = 0,     // any epilogue, decided at run time
+  EPV_QU8 = 1,         // requantize to u8
+  EPV_QU8_LUT = 2,     // requantize, then the activation table
+  EPV_QU8_LUT_RES = 3  // requantize, table, then the residual QLinearAdd
+};
+
+// Launch one instantiation (defined in the k_igemm_*.hip files); false if
+// no kernel exists for the shape.
+bool igemm_launch_i8_a(hipStream_t st, const IgemmArgs& a, const TileCfg& t, int epv);  // generic, QU8
+bool igemm_launch_i8_b(hipStream_t st, const IgemmArgs& a, const TileCfg& t, int epv);  // LUT variants
+bool igemm_launch_f16(hipStream_t st, const IgemmArgs& a, const TileCfg& t);
+
+namespace ig {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// LDS layout of a workgroup (bytes):
+//   [0, 256)                 activation table (u8)
+//   [256, 256 + 4 BC)        bias' (i32) or the f16 bias
+//   [256 + 4 BC, 256 + 8 BC) multipliers (f32)
+//   then the k-slice table ((ksteps + 2 PD) * 4 int2), then the weight chunk
+__host__ __device__ constexpr int lds_table_off(int bc) { return 256 + 8 * bc; }
+__host__ __device__ constexpr int lds_chunk_off(int bc, int ksteps, int pd) {
+  return lds_table_off(bc) + (ksteps + 2 * pd) * 4 * 8;
+}
+inline size_t lds_bytes(const TileCfg& t, int ksteps) {
+  return (size_t)lds_chunk_off(t.bc, ksteps, t.pd) + (size_t)t.kchunk * t.bc * 64;
+}
+
+// n / d for 0 <= n < 2^24, 0 < d < 2^24, with rd = 1.0f / d: the float
+// quotient is within 2 of the exact one; two correction steps fix it.
+__device__ __forceinline__ int div_small(int n, int d, float rd) {
+  int q = (int)((float)n * rd);
+  int r = n - q * d;
+  q += (r >= d) - (r < 0);
+  r = n - q * d;
+  q += (r >= d) - (r < 0);
+  return q;
+}
+
+// Per-channel epilogue parameters of the workgroup's channel tile, staged
+// in LDS at the start (indexed by the channel's position in the tile).
+struct EpiLds {
+  const int* bias;         // EPI_QU8 bias' or null
+  const float* ms;         // EPI_QU8 multipliers
+  const uint8_t* lut;      // EPI_QU8 table (256 entries) or null
+  const uint16_t* bias_h;  // EPI_F16 bias or null
+};
+
+// f16 epilogue chain of CpuGraphRuntime: conv result rounded to f16, then
+// the bias pass, the activation and the residual add, each on stored f16.
+__device__ __forceinline__ uint16_t f16_chain(float acc, const uint16_t* bias_h, int ch, int act,
+                                              bool has_res, uint16_t resv) {
+  uint16_t hb = f2h(acc);
+  if (bias_h) hb = f16_add_bits(hb, bias_h[ch]);
+  hb = f16_act_bits(hb, act);
+  if (has_res) hb = f16_add_bits(hb, resv);
+  return hb;
+}
+
+// QLinearConv requantization of one accumulator (bias' already added):
+// rint(acc * M) + y_zp, saturated to [0, 255] (ONNX QLinearConv, RNE).
+__device__ __forceinline__ int requant_u8(int acc, float m, float zp) {
+  const float q = rintf((float)acc * m) + zp;
+  return (int)__builtin_amdgcn_fmed3f(q, 0.0f, 255.0f);
+}
+
+// QLinearAdd of the table output a and the residual b (QuantizeLinear of
+// the sum of both dequantized operands, RNE, saturated).
+__device__ __forceinline__ int qadd_u8(int qa, int rb, const IgemmArgs& a) {
+  const float f = (float)(qa - a.za) * a.ra + (float)(rb - a.zb) * a.rb;
+  const float g = rintf(f) + (float)a.zy;
+  return (int)__builtin_amdgcn_fmed3f(g, 0.0f, 255.0f);
+}
+
+// Generic epilogue for one 16x16 block: this lane holds channels ch..ch+3
+// of pixel p (channel cl..cl+3 of the tile).
+template <int ESZ, typename AccT>
+__device__ __forceinline__ void epilogue4(const IgemmArgs& a, const EpiLds& e, const AccT& v, int ch, int cl,
+                                          int p) {
+  const size_t yo = (size_t)p * a.y_pix_stride + a.y_c_off + ch;
+  if constexpr (ESZ == 1) {
+    if (a.epi == EPI_QU8) {
+      const int4 bi = e.bias ? *reinterpret_cast<const int4*>(e.bias + cl) : make_int4(0, 0, 0, 0);
+      const float4 ms = *reinterpret_cast<const float4*>(e.ms + cl);
+      uint32_t rres = 0;
+      if (a.res)
+        rres = *reinterpret_cast<const uint32_t*>((const uint8_t*)a.res + (size_t)p * a.r_pix_stride +
+                                                  a.r_c_off + ch);
+      const int accs[4] = {v[0] + bi.x, v[1] + bi.y, v[2] + bi.z, v[3] + bi.w};
+      const float mss[4] = {ms.x, ms.y, ms.z, ms.w};
+      uint32_t out = 0;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        int qi = requant_u8(accs[r], mss[r], (float)a.y_zp);
+        if (e.lut) qi = e.lut[qi];
+        if (a.res) qi = qadd_u8(qi, (rres >> (8 * r)) & 0xff, a);
+        out |= (uint32_t)qi << (8 * r);
+      }
+      *reinterpret_cast<uint32_t*>((uint8_t*)a.y + yo) = out;
+    } else if (a.epi == EPI_QS8_REF) {
+      uint32_t out = 0;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float f = (float)v[r] * a.tscale;
+        f = fminf(fmaxf(f, -128.0f), 127.0f);
+        f = roundf(f);
+        if (a.act == ACT_RELU) f = fmaxf(f, 0.0f);
+        out |= ((uint32_t)(int)f & 0xffu) << (8 * r);
+      }
+      *reinterpret_cast<uint32_t*>((uint8_t*)a.y + yo) = out;
+    } else {  // EPI_I32
+      *reinterpret_cast<int4*>((int*)a.y + yo) = make_int4(v[0], v[1], v[2], v[3]);
+    }
+  } else {
+    uint2 rres = make_uint2(0, 0);
+    if (a.res)
+      rres = *reinterpret_cast<const uint2*>((const uint16_t*)a.res + (size_t)p * a.r_pix_stride +
+                                             a.r_c_off + ch);
+    const bool hr = a.res != nullptr;
+    const uint32_t lo = (uint32_t)f16_chain(v[0], e.bias_h, cl + 0, a.act, hr, rres.x & 0xffff) |
+                        ((uint32_t)f16_chain(v[1], e.bias_h, cl + 1, a.act, hr, rres.x >> 16) << 16);
+    const uint32_t hi = (uint32_t)f16_chain(v[2], e.bias_h, cl + 2, a.act, hr, rres.y & 0xffff) |
+                        ((uint32_t)f16_chain(v[3], e.bias_h, cl + 3, a.act, hr, rres.y >> 16) << 16);
+    *reinterpret_cast<uint2*>((uint16_t*)a.y + yo) = make_uint2(lo, hi);
+  }
+}
+
+template <int ESZ, int BC, int PB, int PD, int EPV>
+__global__ __launch_bounds__(256) void igemm_kernel(const IgemmArgs a) {
+  constexpr int CB = BC / 16;       // 16-channel blocks (all channels of the tile per wave)
+  constexpr int CE = 16 / ESZ;      // elements per 16-byte slice
+  constexpr int WPIX = 16 * PB;     // pixels per wave
+  constexpr int WGPIX = 4 * WPIX;   // pixels per workgroup
+  constexpr bool FAST = EPV != EPV_GENERIC;
+  using acc_t = typename std::conditional<ESZ == 1, v4i, v4f>::type;
+  static_assert(BC % 16 == 0 && PD >= 2, "tile");
+  static_assert(!FAST || ESZ == 1, "specialised epilogues are int8");
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+
+  const uint8_t* __restrict__ X = a.x;
+  const uint8_t* __restrict__ WPK = a.wpk;
+  const int H = a.h, W = a.w, CIN = a.cin, KH = a.kh, KW = a.kw;
+  const int XPS = a.x_pix_stride, XCO = a.x_c_off, KSTEPS = a.ksteps, COUTP = a.cout_pad;
+  const int KCH = a.kchunk;
+  const uint32_t XXOR = a.xxor;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+
+  // XCD-aware tile order: workgroup b runs on XCD b % 8; give each XCD a
+  // contiguous range of tiles (channel tiles of one pixel tile adjacent).
+  const int nwg = gridDim.x;
+  const int bid = blockIdx.x;
+  const int xcd = bid & 7, idx = bid >> 3;
+  const int base = nwg >> 3, rem = nwg & 7;
+  const int tile = xcd * base + min(xcd, rem) + idx;
+  const int ctiles = COUTP / BC;
+  const int ptile = tile / ctiles;
+  const int c0 = (tile - ptile * ctiles) * BC;
+  const int p0 = ptile * WGPIX + wave * WPIX;
+
+  uint8_t* const s_lut = smem;
+  uint8_t* const s_bias = smem + 256;
+  uint8_t* const s_ms = smem + 256 + 4 * BC;
+  int2* const ktab = reinterpret_cast<int2*>(smem + lds_table_off(BC));
+  uint8_t* const s_chunk = smem + lds_chunk_off(BC, KSTEPS, PD);
+
+  // ---- k-slice table: slice q of K (16 bytes, one filter tap) is at element
+  // offset koff from the pixel's top-left tap and belongs to tap `tap`
+  // (31 = past the end of K: always padding).  It does not depend on the
+  // pixel, so the workgroup builds it once.  (The ring reads up to k-step
+  // KSTEPS + 2 * PD - 3, see the main loop.)
+  const int nq = (KSTEPS + 2 * PD) * 4;
+  const int kelems = KH * KW * CIN;
+  {
+    const float rcin = 1.0f / (float)CIN, rkw = 1.0f / (float)KW;
+    for (int q = tid; q < nq; q += 256) {
+      const int e = q * CE;
+      int2 t = make_int2(0, 31);
+      if (e < kelems) {
+        const int tap = div_small(e, CIN, rcin);
+        const int ci = e - tap * CIN;
+        const int kh = div_small(tap, KW, rkw);
+        const int kw = tap - kh * KW;
+        t = make_int2((kh * W + kw) * XPS + ci, tap);
+      }
+      ktab[q] = t;
+    }
+  }
+
+  // ---- this lane's pixels p0 + pb*16 + (lane & 15): element offset of the
+  // top-left tap and the in-image bit of every tap
+  int pbase[PB];
+  uint32_t tmask[PB];
+  {
+    const int hw_o = a.ho * a.wo;
+    const float rhw = 1.0f / (float)hw_o, rwo = 1.0f / (float)a.wo;
+#pragma unroll
+    for (int pb = 0; pb < PB; ++pb) {
+      const int p = p0 + pb * 16 + (lane & 15);
+      const bool pv = p < a.m;
+      const int pp = pv ? p : 0;
+      const int nn = div_small(pp, hw_o, rhw);
+      const int r = pp - nn * hw_o;
+      const int oh = div_small(r, a.wo, rwo);
+      const int ow = r - oh * a.wo;
+      const int ih0 = oh * a.sh - a.pt, iw0 = ow * a.sw - a.pl;
+      pbase[pb] = ((nn * H + ih0) * W + iw0) * XPS + XCO;
+      uint32_t rows = 0, cols = 0;
+      for (int kh = 0; kh < KH; ++kh) rows |= (uint32_t)((unsigned)(ih0 + kh) < (unsigned)H) << kh;
+      for (int kw = 0; kw < KW; ++kw) cols |= (uint32_t)((unsigned)(iw0 + kw) < (unsigned)W) << kw;
+      uint32_t m = 0;
+      for (int kh = 0; kh < KH; ++kh)
+        if ((rows >> kh) & 1u) m |= cols << (kh * KW);
+      tmask[pb] = pv ? m : 0u;
+    }
+  }
+
+  // Weight chunks go to LDS with direct global->LDS loads: one 1 KB
+  // fragment per wave instruction, lane l writing bytes [16 l, 16 l + 16).
+  const int frag_lane = ((lane & 15) * 64 + (lane >> 4) * 16);  // this lane's slice in a 16-row block
+#define DW_ISSUE_A(s_first)                                                                         \
+  {                                                                                                 \
+    const int nfr_ = (min(KSTEPS, (s_first) + KCH) - (s_first)) * CB;                               \
+    for (int f = wave; f < nfr_; f += 4) {                                                          \
+      const int sl = f / CB, cb = f - (f / CB) * CB;                                                \
+      const uint8_t* src = WPK + ((size_t)((s_first) + sl) * COUTP + c0 + cb * 16) * 64 + frag_lane; \
+      __builtin_amdgcn_global_load_lds((const void*)src,                                            \
+                                       (__attribute__((address_space(3))) void*)(s_chunk + f * 1024), \
+                                       16, 0, 0);                                                   \
+    }                                                                                               \
+  }
+  // this wave's LDS writes (and loads) have landed, then everyone's have
+#define DW_LDS_FENCE()              \
+  __builtin_amdgcn_s_waitcnt(0);    \
+  __syncthreads();
+
+  // Epilogue parameters of the channel tile (one wave each): bias' and
+  // multipliers, the activation table, or the f16 bias.
+  const int nvalid = min(BC, a.cout - c0);  // a multiple of 4
+  EpiLds ep{nullptr, nullptr, nullptr, nullptr};
+  if (a.epi == EPI_QU8) {
+    ep.bias = a.bias_i ? reinterpret_cast<const int*>(s_bias) : nullptr;
+    ep.ms = reinterpret_cast<const float*>(s_ms);
+    ep.lut = a.lut ? s_lut : nullptr;
+  } else if (a.epi == EPI_F16 && a.bias_h) {
+    ep.bias_h = reinterpret_cast<const uint16_t*>(s_bias);
+  }
+
+  __syncthreads();  // the k-slice table is complete
+
+  // im2col loads are buffer loads over the input view: padding taps and
+  // k-steps past the end of K use an out-of-range offset, which returns
+  // zero without a memory access.
+  const u32x4 padv = {a.xpad, a.xpad, a.xpad, a.xpad};
+  const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc((void*)X, (short)0, a.x_bytes, 0x00020000);
+  const int2* my_tab = ktab + (lane >> 4);
+#define DW_LOAD_B(s_, dst, dok)                                                                     \
+  {                                                                                                 \
+    const int2 t_ = my_tab[(s_) * 4];                                                               \
+    _Pragma("unroll") for (int pb = 0; pb < PB; ++pb) {                                             \
+      const bool ok = (tmask[pb] >> t_.y) & 1u;                                                     \
+      const int off = ok ? (pbase[pb] + t_.x) * ESZ : (int)0x80000000;                              \
+      dst[pb] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrsrc, off, 0, 0)); \
+      dok[pb] = ok;                                                                                 \
+    }                                                                                               \
+  }
+
+  // ---- im2col ring: k-step s lives in bq[s % PD], loaded PD - 1 steps
+  // ahead.  The ring holds the raw loads and their in-image flags; the xor
+  // and the pad select happen when the k-step is consumed, so nothing waits
+  // for a load before its k-step comes up.  Every k-step issues exactly PB
+  // loads, also past the last k-step, so the compiler's load counters stay
+  // exact and a k-step waits only for its own loads.
+  u32x4 bq[PD][PB];
+  bool bok[PD][PB];
+#pragma unroll
+  for (int r = 0; r < PD - 1; ++r) DW_LOAD_B(r, bq[r], bok[r]);
+
+  // All of the workgroup's start-up loads are in flight together: the first
+  // PD - 1 im2col k-steps, the first weight chunk and the epilogue data.
+  DW_ISSUE_A(0);
+  if (a.epi == EPI_QU8) {
+    if (wave == 0 && a.bias_i && lane < nvalid / 4)
+      __builtin_amdgcn_global_load_lds((const void*)(a.bias_i + c0 + lane * 4),
+                                       (__attribute__((address_space(3))) void*)s_bias, 16, 0, 0);
+    if (wave == 1 && lane < nvalid / 4)
+      __builtin_amdgcn_global_load_lds((const void*)(a.mscale + c0 + lane * 4),
+                                       (__attribute__((address_space(3))) void*)s_ms, 16, 0, 0);
+    if (wave == 2 && a.lut && lane < 16)
+      __builtin_amdgcn_global_load_lds((const void*)(a.lut + lane * 16),
+                                       (__attribute__((address_space(3))) void*)s_lut, 16, 0, 0);
+  } else if (a.epi == EPI_F16 && a.bias_h) {
+    if (wave == 0 && lane < nvalid / 2)
+      __builtin_amdgcn_global_load_lds((const void*)(a.bias_h + c0 + lane * 2),
+                                       (__attribute__((address_space(3))) void*)s_bias, 4, 0, 0);
+  }
+  DW_LDS_FENCE();
+
+  // Accumulators; the specialised int8 epilogues start them at bias'.
+  const int cq = 4 * (lane >> 4);  // this lane's first channel within a 16-channel block
+  acc_t acc[CB][PB];
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb) {
+    acc_t init = acc_t{0, 0, 0, 0};
+    if constexpr (FAST) {
+      if (a.bias_i) init = *reinterpret_cast<const v4i*>(s_bias + 4 * (cb * 16 + cq));
+    }
+#pragma unroll
+    for (int pb = 0; pb < PB; ++pb) acc[cb][pb] = init;
+  }
+
+  int next_chunk = KCH, chunk0 = 0;
+  for (int s0 = 0; s0 < KSTEPS; s0 += PD) {
+#pragma unroll
+    for (int r = 0; r < PD; ++r) {
+      const int s = s0 + r;
+      if (s < KSTEPS && s == next_chunk) {
+        __syncthreads();  // every wave is done with the previous chunk
+        chunk0 = s;
+        next_chunk = s + KCH;
+        DW_ISSUE_A(s);
+        DW_LDS_FENCE();
+      }
+      DW_LOAD_B(s + PD - 1, bq[(r + PD - 1) % PD], bok[(r + PD - 1) % PD]);
+      if (s < KSTEPS) {
+        u32x4 bcur[PB];
+#pragma unroll
+        for (int pb = 0; pb < PB; ++pb) {
+          if constexpr (ESZ == 1)
+            bcur[pb] = bok[r][pb] ? (bq[r][pb] ^ XXOR) : padv;
+          else
+            bcur[pb] = bq[r][pb];  // f16 padding is +0, what the out-of-range load returns
+        }
+        const uint8_t* Af = s_chunk + (s - chunk0) * (CB * 1024) + lane * 16;
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) {
+          const v4i af = *reinterpret_cast<const v4i*>(Af + cb * 1024);
+#pragma unroll
+          for (int pb = 0; pb < PB; ++pb) {
+            if constexpr (ESZ == 1) {
+              acc[cb][pb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, __builtin_bit_cast(v4i, bcur[pb]),
+                                                                  acc[cb][pb], 0, 0, 0);
+            } else {
+              acc[cb][pb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                  __builtin_bit_cast(v8h, af), __builtin_bit_cast(v8h, bcur[pb]), acc[cb][pb], 0, 0, 0);
+            }
+          }
+        }
+      }
+    }
+  }
+#undef DW_ISSUE_A
+#undef DW_LDS_FENCE
+#undef DW_LOAD_B
+
+  // ---- epilogue: lane holds channels c0 + cb*16 + cq .. +3 of pixel
+  // p0 + pb*16 + (lane & 15) for every block
+  if constexpr (FAST) {
+    const bool full = c0 + BC <= a.cout;
+    const float zpf = (float)a.y_zp;
+    float4 msr[CB];
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) msr[cb] = *reinterpret_cast<const float4*>(s_ms + 4 * (cb * 16 + cq));
+#pragma unroll
+    for (int pb = 0; pb < PB; ++pb) {
+      const int p = p0 + pb * 16 + (lane & 15);
+      if (p >= a.m) continue;
+      uint8_t* yrow = (uint8_t*)a.y + (size_t)p * a.y_pix_stride + a.y_c_off + c0 + cq;
+      uint32_t rres[CB];
+      if constexpr (EPV == EPV_QU8_LUT_RES) {
+        const uint8_t* rrow = (const uint8_t*)a.res + (size_t)p * a.r_pix_stride + a.r_c_off + c0 + cq;
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb)
+          rres[cb] = (full || c0 + cb * 16 + cq < a.cout) ? *reinterpret_cast<const uint32_t*>(rrow + cb * 16) : 0u;
+      }
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) {
+        if (!full && c0 + cb * 16 + cq >= a.cout) continue;
+        const float ms4[4] = {msr[cb].x, msr[cb].y, msr[cb].z, msr[cb].w};
+        uint32_t out = 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          int qi = requant_u8(acc[cb][pb][r], ms4[r], zpf);
+          if constexpr (EPV != EPV_QU8) qi = s_lut[qi];
+          if constexpr (EPV == EPV_QU8_LUT_RES) qi = qadd_u8(qi, (rres[cb] >> (8 * r)) & 0xff, a);
+          out |= (uint32_t)qi << (8 * r);
+        }
+        *reinterpret_cast<uint32_t*>(yrow + cb * 16) = out;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+      const int ch = c0 + cb * 16 + cq;
+      if (ch >= a.cout) continue;
+#pragma unroll
+      for (int pb = 0; pb < PB; ++pb) {
+        const int p = p0 + pb * 16 + (lane & 15);
+        if (p < a.m) epilogue4<ESZ>(a, ep, acc[cb][pb], ch, ch - c0, p);
+      }
+    }
+  }
+}
+
+// Launch of the instantiation for a tile shape (the caller checked that it
+// is one of the shapes below).
+template <int ESZ, int BC, int EPV>
+bool launch_bc(hipStream_t st, const IgemmArgs& a, const TileCfg& t, dim3 grid) {
+  const size_t lds = lds_bytes(t, a.ksteps);
+#define DW_T(PB, PD)                                                                         \
+  if (t.pb == PB && t.pd == PD) {                                                            \
+    hipLaunchKernelGGL((igemm_kernel<ESZ, BC, PB, PD, EPV>), grid, dim3(256), lds, st, a);   \
+    return true;                                                                             \
+  }
+  DW_T(4, 4)
+  DW_T(2, 6)
+  DW_T(1, 8)
+#undef DW_T
+  return false;
+}
+
+template <int ESZ, int EPV>
+bool launch_tiles(hipStream_t st, const IgemmArgs& a, const TileCfg& t) {
+  const int wgpix = 64 * t.pb;
+  const dim3 grid((unsigned)(((a.m + wgpix - 1) / wgpix) * (a.cout_pad / t.bc)));
+  switch (t.bc) {
+    case 128: return launch_bc<ESZ, 128, EPV>(st, a, t, grid);
+    case 96: return launch_bc<ESZ, 96, EPV>(st, a, t, grid);
+    case 80: return launch_bc<ESZ, 80, EPV>(st, a, t, grid);
+    case 64: return launch_bc<ESZ, 64, EPV>(st, a, t, grid);
+    case 48: return launch_bc<ESZ, 48, EPV>(st, a, t, grid);
+    case 32: return launch_bc<ESZ, 32, EPV>(st, a, t, grid);
+    case 16: return launch_bc<ESZ, 16, EPV>(st, a, t, grid);
+  }
+  return false;
+}
+
+}  // namespace ig
+}  // namespace dw

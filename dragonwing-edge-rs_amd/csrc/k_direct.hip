@@ -16,15 +16,11 @@
 // pixel x 8 channels, so every load/store is a 16-byte (f16) or 32-byte
 // (f32) vector and consecutive threads walk consecutive channels (coalesced
 // NHWC).  No matrix cores: the op is HBM-bound.
-#include "dw_common.h"
-#include "dw_device.h"
+#include "direct_util.h"
 
 namespace dw {
 namespace {
 
-
-// relu_f32_scalar (ops.rs:208-220): x > 0 -> x, NaN -> NaN, else +0.
-__device__ __forceinline__ float relu_ref(float v) { return v > 0.0f ? v : (v != v ? v : 0.0f); }
 
 // Weights are read through the constant address space: the row for one
 // (tap, ic) is the same for every lane of a wavefront, so the compiler
@@ -32,39 +28,10 @@ __device__ __forceinline__ float relu_ref(float v) { return v > 0.0f ? v : (v !=
 // (no LDS traffic, no per-lane weight loads).
 typedef const __attribute__((address_space(4))) float* wrow_t;
 
-// One input element as the reference conv reads it.
-template <int IN_KIND>
-__device__ __forceinline__ float load1(const DirectArgs& a, const uint8_t* p) {
-  if (IN_KIND == 0) return *reinterpret_cast<const float*>(p);
-  if (IN_KIND == 1) return h2f(*reinterpret_cast<const uint16_t*>(p));
-  return round_f16((float)((int)*p - a.in_zp) * a.in_scale);  // DequantizeLinear to f16, then read
-}
-
-// Elements per 16-byte input vector.
-template <int IN_KIND>
-constexpr int vec_elems() {
-  return IN_KIND == 0 ? 4 : (IN_KIND == 1 ? 8 : 16);
-}
-
-// A 16-byte vector of consecutive input channels, decoded.
-template <int IN_KIND>
-__device__ __forceinline__ void load_vec(const DirectArgs& a, const uint8_t* p, float* v) {
-  const uint4 u = *reinterpret_cast<const uint4*>(p);
-  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    if (IN_KIND == 0) {
-      v[i] = __builtin_bit_cast(float, w[i]);
-    } else if (IN_KIND == 1) {
-      v[2 * i] = h2f(w[i] & 0xffff);
-      v[2 * i + 1] = h2f(w[i] >> 16);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        v[4 * i + e] = round_f16((float)((int)((w[i] >> (8 * e)) & 0xff) - a.in_zp) * a.in_scale);
-    }
-  }
-}
+using dx::load1;
+using dx::load_vec;
+using dx::relu_ref;
+using dx::vec_elems;
 
 // One thread = one output pixel x OC consecutive output channels; all OC
 // accumulators consume each decoded input value, so the decode is paid once
@@ -120,68 +87,63 @@ __global__ __launch_bounds__(256) void direct_conv_kernel(const DirectArgs a) {
     }
   }
 
-  // Epilogue: the rest of the fused group, then stores packed into 32-bit
-  // words (16- or 4-byte stores when the output view is aligned for them,
-  // else one store per element).
+  // Epilogue: the rest of the fused group, packed stores.
   const int OES = a.out_kind == 0 ? 4 : (a.out_kind == 1 ? 2 : 1);
   const size_t yo = (size_t)p * a.y_pix_stride + a.y_c_off + oc0;
-  uint8_t* yb = (uint8_t*)a.y + yo * OES;
-  uint32_t words[(OC * 4 + 3) / 4];
+  dx::store_outputs<OC>(a, acc, oc0, (uint8_t*)a.y + yo * OES);
+}
+
+// Small-kernel, few-channel case (the 3-channel stem): KH x KW x CIN known
+// at compile time.  One thread = one output pixel x OC channels.  All
+// KH*KW*CIN input values are loaded up front (out-of-image taps read a
+// clamped in-image address and are then skipped), decoded once, and fed to
+// OC FMA chains in the reference order, skipping out-of-image taps exactly
+// as the reference does.  Weights come through scalar loads (SGPR operands).
+template <int IN_KIND, int OC, int KH, int KW, int CIN>
+__global__ __launch_bounds__(256) void conv_small_kernel(const DirectArgs a) {
+  constexpr int ES = IN_KIND == 0 ? 4 : (IN_KIND == 1 ? 2 : 1);
+  constexpr int KT = KH * KW;
+  const int p = blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= a.m) return;
+  const int oc0 = blockIdx.y * OC;
+  const int hw = a.ho * a.wo;
+  const int nn = p / hw;
+  const int rem = p - nn * hw;
+  const int oh = rem / a.wo;
+  const int ow = rem - oh * a.wo;
+  const int ih0 = oh * a.sh - a.pt, iw0 = ow * a.sw - a.pl;
+  const uint8_t* __restrict__ X = (const uint8_t*)a.x;
+  float xv[KT][CIN];
+  bool ok[KT];
 #pragma unroll
-  for (int i = 0; i < (OC * 4 + 3) / 4; ++i) words[i] = 0;
-  // (one fully unrolled loop per output type keeps each loop small enough
-  // to unroll, so acc and words stay in registers)
-  if (a.out_kind == 0) {
+  for (int kh = 0; kh < KH; ++kh)
 #pragma unroll
-    for (int j = 0; j < OC; ++j) {
-      float v = acc[j];
-      if (a.bias_f) v = v + a.bias_f[oc0 + j];
-      if (a.act == ACT_RELU) {
-        v = relu_ref(v);
-      } else if (a.act == ACT_SILU) {
-        const float s = 1.0f / (1.0f + expf(-v));
-        v = v * s;
-      }
-      words[j] = __builtin_bit_cast(uint32_t, v);
-      if (a.vec_out == 1) reinterpret_cast<float*>(yb)[j] = v;
+    for (int kw = 0; kw < KW; ++kw) {
+      const int ih = ih0 + kh, iw = iw0 + kw;
+      const bool v = (unsigned)ih < (unsigned)a.h && (unsigned)iw < (unsigned)a.w;
+      ok[kh * KW + kw] = v;
+      const int ihc = min(max(ih, 0), a.h - 1), iwc = min(max(iw, 0), a.w - 1);
+      const uint8_t* xp = X + (((size_t)(nn * a.h + ihc) * a.w + iwc) * a.x_pix_stride + a.x_c_off) * ES;
+#pragma unroll
+      for (int ic = 0; ic < CIN; ++ic) xv[kh * KW + kw][ic] = load1<IN_KIND>(a, xp + ic * ES);
     }
-  } else if (a.out_kind == 1) {
+  const wrow_t wbase = (wrow_t)(a.wf + oc0);
+  float acc[OC];
 #pragma unroll
-    for (int j = 0; j < OC; ++j) {
-      uint16_t hb = f2h(acc[j]);
-      if (a.bias_h) hb = f16_add_bits(hb, a.bias_h[oc0 + j]);
-      const uint16_t ob = f16_act_bits(hb, a.act);
-      words[j >> 1] |= (uint32_t)ob << (16 * (j & 1));
-      if (a.vec_out == 1) reinterpret_cast<uint16_t*>(yb)[j] = ob;
-    }
-  } else {
+  for (int j = 0; j < OC; ++j) acc[j] = 0.0f;
 #pragma unroll
-    for (int j = 0; j < OC; ++j) {
-      uint16_t hb = f2h(acc[j]);
-      if (a.bias_h) hb = f16_add_bits(hb, a.bias_h[oc0 + j]);
-      // QuantizeLinear of the stored f16 value.
-      float q = rintf(__fdiv_rn(h2f(hb), a.out_scale)) + (float)a.out_zp;
-      q = fminf(fmaxf(q, 0.0f), 255.0f);
-      int qi = (int)q;
-      if (a.lut) qi = a.lut[qi];
-      words[j >> 2] |= (uint32_t)qi << (8 * (j & 3));
-      if (a.vec_out == 1) yb[j] = (uint8_t)qi;
+  for (int t = 0; t < KT; ++t) {
+    if (!ok[t]) continue;
+#pragma unroll
+    for (int ic = 0; ic < CIN; ++ic) {
+      const wrow_t wr = wbase + (size_t)(t * CIN + ic) * a.cout;
+#pragma unroll
+      for (int j = 0; j < OC; ++j) acc[j] = fmaf(xv[t][ic], wr[j], acc[j]);
     }
   }
-  // (loops run to the f32 maximum with constant indices, so `words` stays
-  // in registers; the byte count of this output type bounds them)
-  const int nbytes = OC * OES;
-  if (a.vec_out == 16) {
-#pragma unroll
-    for (int i = 0; i < OC / 4; ++i)
-      if (16 * i < nbytes)
-        *reinterpret_cast<uint4*>(yb + 16 * i) =
-            make_uint4(words[4 * i], words[4 * i + 1], words[4 * i + 2], words[4 * i + 3]);
-  } else if (a.vec_out == 4) {
-#pragma unroll
-    for (int i = 0; i < OC; ++i)
-      if (4 * i < nbytes) *reinterpret_cast<uint32_t*>(yb + 4 * i) = words[i];
-  }
+  const int OES = a.out_kind == 0 ? 4 : (a.out_kind == 1 ? 2 : 1);
+  const size_t yo = (size_t)p * a.y_pix_stride + a.y_c_off + oc0;
+  dx::store_outputs<OC>(a, acc, oc0, (uint8_t*)a.y + yo * OES);
 }
 
 template <int ESZ>
@@ -276,7 +238,24 @@ __global__ __launch_bounds__(256) void dwconv_kernel(const DwArgs a) {
 }  // namespace
 
 void launch_direct_conv(hipStream_t st, const DirectArgs& a_in) {
+  if (launch_conv1x1_exact(st, a_in)) return;
   DirectArgs a = a_in;
+  // the 3x3, 3-channel stem
+  if (a.kh == 3 && a.kw == 3 && a.cin == 3 && a.cout % 16 == 0 && a.in_kind <= 1) {
+    const int oes = a.out_kind == 0 ? 4 : (a.out_kind == 1 ? 2 : 1);
+    auto aligned = [&](int v) {
+      return (16 * oes) % v == 0 && (a.y_pix_stride * oes) % v == 0 && (a.y_c_off * oes) % v == 0 &&
+             ((uintptr_t)a.y % v) == 0;
+    };
+    a.vec_out = aligned(16) ? 16 : (aligned(4) ? 4 : 1);
+    const dim3 grid((a.m + 255) / 256, a.cout / 16);
+    if (a.in_kind == 0)
+      hipLaunchKernelGGL((conv_small_kernel<0, 16, 3, 3, 3>), grid, dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL((conv_small_kernel<1, 16, 3, 3, 3>), grid, dim3(256), 0, st, a);
+    DW_HIP(hipGetLastError());
+    return;
+  }
   const int es = a.in_kind == 0 ? 4 : (a.in_kind == 1 ? 2 : 1);
   const int vn = 16 / es;
   const bool vin = a.cin % vn == 0 && (a.x_pix_stride * es) % 16 == 0 && (a.x_c_off * es) % 16 == 0 &&

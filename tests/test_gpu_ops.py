@@ -337,6 +337,23 @@ def test_conv_f16_exact_order_bit_exact(backend, geom):
     np.testing.assert_array_equal(got, oracle_conv_f16(xh, kh_, bh, s, p, ops.ACT_RELU))
 
 
+@pytest.mark.parametrize("geom", [(1, 9, 7, 16, 80, 1, 1, 0), (2, 33, 31, 64, 64, 1, 1, 0),
+                                  (1, 40, 40, 80, 80, 1, 1, 0), (3, 11, 13, 32, 40, 1, 2, 0),
+                                  (1, 5, 5, 8, 4, 1, 1, 0), (8, 20, 20, 64, 20, 1, 1, 0)])
+def test_conv_f16_exact_1x1_bit_exact(backend, geom):
+    # The 1x1 exact-order kernel: ragged pixel counts, stride 2, and c_out
+    # values that select every channels-per-wave / pixels-per-lane shape.
+    n, h, w, ci, co, k, s, p = geom
+    r = synth.Rng(synth.seed_for(700 + sum(geom)))
+    xh = synth.f16_bits(r.normal((n, h, w, ci), 0.0, 1.0))
+    kh_ = synth.f16_bits(r.normal((k, k, ci, co), 0.0, 0.2))
+    bh = synth.f16_bits(r.normal((co,), 0.0, 0.1))
+    # (ReLU, not SiLU: bit-exact SiLU would need the host libm's expf)
+    for act in (ops.ACT_NONE, ops.ACT_RELU):
+        got = run_conv_f16(backend, xh, kh_, bh, s, p, act, exact=True)
+        np.testing.assert_array_equal(got, oracle_conv_f16(xh, kh_, bh, s, p, act), err_msg=f"act {act}")
+
+
 def test_conv_f16_subnormal_inputs_follow_reference_decode(backend):
     # dragonwing-cpu widens f16 subnormals at half their IEEE value; the
     # exact-order kernel reproduces it bit for bit.
