@@ -9,10 +9,13 @@ images/s over exactly --steps steps after --warmup untimed steps, bracketed
 by stream synchronisation.
 
 Also prints, on the same JSON line:
-  roofline     — the dominant kernel (most GPU time in one run): its
-                 algorithmic work per launch divided by its mean launch time,
-                 measured with HIP events around every launch on the backend
-                 stream, against the MI355X dense peak of its bound;
+  roofline     — the dominant kernel family (most GPU time in one run; the
+                 implicit-GEMM launches of all tile shapes are one family):
+                 its algorithmic work per launch divided by its mean launch
+                 time, measured with HIP events on the backend stream (each
+                 launch repeated back to back between one event pair, so the
+                 time includes the gap between dispatches), against the
+                 MI355X dense peak of its bound;
   cpu_baseline — the oracle (dragonwing-cpu restated in C++) on a bounded
                  sample of the same workload, timed on this host's cores.
 
@@ -58,17 +61,29 @@ def cpu_threads() -> int:
         return os.cpu_count() or 1
 
 
-def profile(rts, launches, iters: int):
-    """Mean per-launch milliseconds over `iters` event-bracketed runs."""
+def family(kernel: str) -> str:
+    """Kernel family of a launch name: the implicit-GEMM launches of one
+    element type are one kernel template whatever their tile shape
+    (igemm_i8_c64_p128 -> igemm_i8)."""
+    if kernel.startswith("igemm_"):
+        return "_".join(kernel.split("_")[:2])
+    return kernel
+
+
+def profile(rts, launches, iters: int, repeat: int):
+    """Per-launch milliseconds on the backend stream (each launch enqueued
+    `repeat` times back to back between one HIP event pair, averaged over
+    `iters` passes: kernel duration plus the dispatch-to-dispatch gap), and
+    per kernel family: launches, total ms, algorithmic work and bytes."""
     acc = None
     for i in range(iters):
-        ms = rts[i % len(rts)].run_profiled().astype(np.float64)
+        ms = rts[i % len(rts)].time_launches(repeat).astype(np.float64)
         acc = ms if acc is None else acc + ms
     ms = acc / iters
     fam = {}
     for L, t in zip(launches, ms):
-        f = fam.setdefault(L["kernel"], {"kernel": L["kernel"], "launches": 0, "ms": 0.0, "work": 0.0,
-                                         "bytes": 0.0})
+        k = family(L["kernel"])
+        f = fam.setdefault(k, {"kernel": k, "launches": 0, "ms": 0.0, "work": 0.0, "bytes": 0.0})
         f["launches"] += 1
         f["ms"] += float(t)
         f["work"] += L["work"]
@@ -198,9 +213,14 @@ def main():
                     choices=["yolov8n_int8", "yolov8n_f16", "qlinearconv", "dwconv", "conv_f32"])
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--profile-iters", type=int, default=5)
+    ap.add_argument("--profile-iters", type=int, default=3)
+    ap.add_argument("--profile-repeat", type=int, default=10,
+                    help="back-to-back repeats of each launch per timing pass")
     ap.add_argument("--no-capture", action="store_true", help="replay launches eagerly instead of a HIP graph")
     ap.add_argument("--dump-launches", default="", help="write per-launch timings (JSON lines) to this file")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="end with one plain 256 MiB device copy (copy_channels kernel), the known-size "
+                         "reference for scaling FETCH_SIZE / WRITE_SIZE counters of the same run")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this backend runs on one GPU; --gpus {args.gpus} is not supported "
@@ -263,7 +283,7 @@ def main():
     value = images * args.steps / el
 
     launches = rts[0].launches()
-    ms, fams = profile(rts, launches, args.profile_iters)
+    ms, fams = profile(rts, launches, args.profile_iters, args.profile_repeat)
     if args.dump_launches:
         with open(args.dump_launches, "w") as f:
             for L, t in zip(launches, ms):
@@ -309,6 +329,14 @@ def main():
         "gpu_ms_sum_of_launches": round(float(ms.sum()), 4),
         "setup_s": round(t_setup, 1),
     }
+    if args.traffic_probe:
+        from dragonwing_edge_rs_amd import ops
+
+        n = 256 << 20
+        src, dst = be.alloc(n), be.alloc(n)
+        ops.concat_channels_nhwc(be, ops.DTYPE_U8, [src], [n >> 10], dst, 1 << 10)
+        be.synchronize()
+        line["traffic_probe_bytes"] = {"read": n, "write": n}
     print(json.dumps(line), flush=True)
 
 

@@ -19,6 +19,8 @@
 //
 // Every op runs on the GPU; an op without a kernel is an error at creation.
 #include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -1115,6 +1117,49 @@ int dw_hip_graph_run(dw_hip_graph_runtime* rth) {
   API_END
 }
 
+int dw_hip_graph_run_unbatched(dw_hip_graph_runtime* rth) {
+  API_BEGIN
+  dw::Runtime& rt = R(rth);
+  const bool trace = getenv("DW_TRACE") != nullptr;
+  hipStream_t st = rt.be->stream;
+  for (size_t i = 0; i < rt.launches.size(); ++i) {
+    dw::Launch& L = rt.launches[i];
+    if (trace) fprintf(stderr, "[launch %3zu] %s (%s)\n", i, L.kernel.c_str(), L.op.c_str());
+    try {
+      L.fn(st);
+      if (trace) DW_HIP(hipStreamSynchronize(st));
+    } catch (const dw::Error& e) {
+      dw::fail(e.code, "launch[" + std::to_string(i) + "] " + L.kernel + " (" + L.op + ") failed: " + e.msg);
+    }
+  }
+  API_END
+}
+
+int dw_hip_graph_num_io(dw_hip_graph_runtime* rth, int which) {
+  if (!rth) return -1;
+  return (int)(which ? rth->rt.g.outputs.size() : rth->rt.g.inputs.size());
+}
+
+const char* dw_hip_graph_io_name(dw_hip_graph_runtime* rth, int which, int index) {
+  if (!rth) return "";
+  const auto& v = which ? rth->rt.g.outputs : rth->rt.g.inputs;
+  if (index < 0 || index >= (int)v.size()) return "";
+  return v[index].c_str();
+}
+
+int dw_hip_graph_tensor_shape(dw_hip_graph_runtime* rth, const char* name, int64_t* dims4, int* rank) {
+  API_BEGIN
+  dw::Runtime& rt = R(rth);
+  if (!name || !dims4 || !rank) dw::fail(DW_ERR_INVALID, "null argument");
+  auto it = rt.g.t.find(name);
+  if (it == rt.g.t.end()) dw::fail(DW_ERR_RUNTIME, std::string("runtime: unknown tensor '") + name + "'");
+  const auto& d = it->second.dims;
+  if (d.size() > 4) dw::fail(DW_ERR_UNSUPPORTED, "tensor rank above 4");
+  *rank = (int)d.size();
+  for (size_t i = 0; i < d.size(); ++i) dims4[i] = d[i];
+  API_END
+}
+
 static void download_tensor(dw::Runtime& rt, const std::string& name, std::vector<uint8_t>& out) {
   dw::RtTensor& t = rt.T(name);
   if (!t.base) dw::fail(DW_ERR_RUNTIME, "tensor " + name + " is not materialized");
@@ -1210,6 +1255,29 @@ int dw_hip_graph_run_profiled(dw_hip_graph_runtime* rth, float* launch_ms) {
   DW_HIP(hipEventSynchronize(ev[n]));
   for (size_t i = 0; i < n; ++i) DW_HIP(hipEventElapsedTime(&launch_ms[i], ev[i], ev[i + 1]));
   for (auto& e : ev) (void)hipEventDestroy(e);
+  API_END
+}
+
+int dw_hip_graph_time_launches(dw_hip_graph_runtime* rth, int repeat, float* launch_ms) {
+  API_BEGIN
+  dw::Runtime& rt = R(rth);
+  if (!launch_ms || repeat < 1) dw::fail(DW_ERR_INVALID, "time_launches: null output or repeat < 1");
+  const size_t n = rt.launches.size();
+  hipEvent_t e0, e1;
+  DW_HIP(hipEventCreate(&e0));
+  DW_HIP(hipEventCreate(&e1));
+  hipStream_t st = rt.be->stream;
+  for (size_t i = 0; i < n; ++i) {
+    DW_HIP(hipEventRecord(e0, st));
+    for (int r = 0; r < repeat; ++r) rt.launches[i].fn(st);
+    DW_HIP(hipEventRecord(e1, st));
+    DW_HIP(hipEventSynchronize(e1));
+    float ms = 0;
+    DW_HIP(hipEventElapsedTime(&ms, e0, e1));
+    launch_ms[i] = ms / repeat;
+  }
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
   API_END
 }
 

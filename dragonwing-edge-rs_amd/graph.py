@@ -180,6 +180,30 @@ class HipGraphRuntime:
         a = np.ascontiguousarray(data)
         check(load().dw_hip_graph_set_input_bytes(self._h, name.encode(), a.ctypes.data, a.nbytes))
 
+    def run_unbatched(self):
+        """run_unbatched (vulkan_runtime.rs:423-470): launches one by one,
+        errors name the failing launch; DW_TRACE=1 prints and syncs each."""
+        check(load().dw_hip_graph_run_unbatched(self._h))
+
+    def _io(self, which: int):
+        lib = load()
+        out = []
+        for i in range(lib.dw_hip_graph_num_io(self._h, which)):
+            name = lib.dw_hip_graph_io_name(self._h, which, i).decode()
+            dims = (C.c_int64 * 4)()
+            rank = C.c_int()
+            check(lib.dw_hip_graph_tensor_shape(self._h, name.encode(), dims, C.byref(rank)))
+            out.append((name, tuple(dims[:rank.value])))
+        return out
+
+    def inputs(self):
+        """Input tensor names and shapes (vulkan_runtime.rs:213-216)."""
+        return self._io(0)
+
+    def outputs(self):
+        """Output tensor names and shapes (vulkan_runtime.rs:218-221)."""
+        return self._io(1)
+
     def run(self):
         check(load().dw_hip_graph_run(self._h))
 
@@ -215,6 +239,15 @@ class HipGraphRuntime:
         n = load().dw_hip_graph_num_launches(self._h)
         ms = np.zeros(n, np.float32)
         check(load().dw_hip_graph_run_profiled(self._h, ms.ctypes.data))
+        return ms
+
+    def time_launches(self, repeat: int = 10) -> np.ndarray:
+        """Per-launch milliseconds: each launch enqueued `repeat` times back
+        to back between one event pair (dw_hip_graph_time_launches); the
+        kernel's duration plus the gap between consecutive dispatches."""
+        n = load().dw_hip_graph_num_launches(self._h)
+        ms = np.zeros(n, np.float32)
+        check(load().dw_hip_graph_time_launches(self._h, repeat, ms.ctypes.data))
         return ms
 
 

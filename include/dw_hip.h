@@ -125,7 +125,7 @@ int dw_hip_conv2d_bias_act_f32_nhwc(dw_hip_backend* be, const dw_hip_buffer* inp
  * ops.rs:1881-1967).  `exact`=1 uses the reference accumulation order
  * (bit-identical); `exact`=0 uses the fp16 MFMA implicit-GEMM kernel
  * (fp32 accumulation in another order: within fp16 tolerance).
- * MFMA path requires c_in % 8 == 0 and c_out % 4 == 0. */
+ * MFMA path requires c_in % 8 == 0, c_out % 4 == 0 and k_h*k_w <= 31. */
 int dw_hip_conv2d_bias_act_f16_nhwc(dw_hip_backend* be, const dw_hip_buffer* input,
                                     const dw_hip_buffer* kernel, const dw_hip_buffer* bias,
                                     dw_hip_buffer* output, size_t n, size_t h_in, size_t w_in,
@@ -158,8 +158,9 @@ int dw_hip_depthwise_conv2d_f32_nhwc(dw_hip_backend* be, const dw_hip_buffer* in
  *   M[c]    = (x_scale * w_scales[c]) / y_scale         (f32)
  * rint rounds half to even.  Padding uses the zero point (real 0).
  * input u8 NHWC, kernel s8 HWIO, bias int32[c_out] device buffer or NULL,
- * w_scales: host array of c_out floats.  Requires c_in % 16 == 0 and
- * c_out % 4 == 0.  INT8 MFMA implicit GEMM (v_mfma_i32_16x16x64_i8). */
+ * w_scales: host array of c_out floats.  Requires c_in % 16 == 0,
+ * c_out % 4 == 0 and k_h*k_w <= 31.  INT8 MFMA implicit GEMM
+ * (v_mfma_i32_16x16x64_i8). */
 int dw_hip_qlinearconv_u8s8(dw_hip_backend* be, const dw_hip_buffer* input,
                             const dw_hip_buffer* kernel, const dw_hip_buffer* bias,
                             dw_hip_buffer* output, size_t n, size_t h_in, size_t w_in,
@@ -168,7 +169,8 @@ int dw_hip_qlinearconv_u8s8(dw_hip_backend* be, const dw_hip_buffer* input,
                             int x_zp, const float* w_scales, float y_scale, int y_zp);
 
 /* conv2d_i8_nhwc (crates/dragonwing-cpu/src/ops.rs:3086-3142): s8 x s8 ->
- * int32 accumulator, zero padding.  Requires c_in % 16 == 0, c_out % 4 == 0. */
+ * int32 accumulator, zero padding.  Requires c_in % 16 == 0, c_out % 4 == 0,
+ * k_h*k_w <= 31. */
 int dw_hip_conv2d_i8_nhwc(dw_hip_backend* be, const dw_hip_buffer* input,
                           const dw_hip_buffer* kernel, dw_hip_buffer* output_i32, size_t n,
                           size_t h_in, size_t w_in, size_t c_in, size_t c_out, size_t k_h,
@@ -363,6 +365,18 @@ int dw_hip_graph_set_input_f32(dw_hip_graph_runtime* rt, const char* name, const
 int dw_hip_graph_set_input_bytes(dw_hip_graph_runtime* rt, const char* name, const void* data, size_t len);
 /* run (vulkan_runtime.rs:359-419): enqueue every op; returns without waiting. */
 int dw_hip_graph_run(dw_hip_graph_runtime* rt);
+/* run_unbatched (vulkan_runtime.rs:423-470): enqueue the launches one by one
+ * (never as a HIP graph); a failing launch is reported with its index and
+ * op names.  With the environment variable DW_TRACE set, every launch is
+ * printed to stderr and followed by a synchronize (as DRAGONWING_TRACE does). */
+int dw_hip_graph_run_unbatched(dw_hip_graph_runtime* rt);
+/* inputs() / outputs() (vulkan_runtime.rs:213-221): count and names of the
+ * graph inputs (which = 0) or outputs (which = 1); names stay valid for the
+ * runtime's lifetime.  Tensor shapes via dw_hip_graph_tensor_shape. */
+int dw_hip_graph_num_io(dw_hip_graph_runtime* rt, int which);
+const char* dw_hip_graph_io_name(dw_hip_graph_runtime* rt, int which, int index);
+/* Shape of a graph tensor (NHWC for activations): up to 4 dims. */
+int dw_hip_graph_tensor_shape(dw_hip_graph_runtime* rt, const char* name, int64_t* dims4, int* rank);
 /* get_output_f32 (vulkan_runtime.rs:296): synchronizes, converts to f32. */
 int dw_hip_graph_get_output_f32(dw_hip_graph_runtime* rt, const char* name, float* data, size_t count);
 /* get_output_bytes (vulkan_runtime.rs:2131): synchronizes, raw bytes. */
@@ -379,6 +393,13 @@ const char* dw_hip_graph_launch_info(dw_hip_graph_runtime* rt, int index);
 /* One run with a HIP event pair around every launch; writes per-launch
  * milliseconds (array of dw_hip_graph_num_launches floats). */
 int dw_hip_graph_run_profiled(dw_hip_graph_runtime* rt, float* launch_ms);
+/* Per-launch device time: every launch of one run is enqueued `repeat`
+ * times back to back between one HIP event pair, and launch_ms[i] is the
+ * elapsed time divided by `repeat`: the kernel's duration plus the gap
+ * between consecutive dispatches on the stream (the event overhead is spread
+ * over the repeats).  Every launch only reads its inputs and writes its
+ * outputs, so repeating it leaves the run's results as one run would. */
+int dw_hip_graph_time_launches(dw_hip_graph_runtime* rt, int repeat, float* launch_ms);
 
 #ifdef __cplusplus
 }

@@ -102,6 +102,25 @@ def test_int8_graph_capture_replays_match_eager(backend, int8_small):
         backend.synchronize()
 
 
+def test_run_unbatched_and_io(backend, int8_small, monkeypatch):
+    g, info = int8_small
+    rt = HipGraphRuntime(g, backend)
+    assert rt.inputs() == [(info["input"], (2, 96, 96, 3))]
+    assert [n for n, _ in rt.outputs()] == info["outputs"]
+    assert [s for _, s in rt.outputs()] == [tuple(s) for s in info["out_shapes"]]
+    x = yolo.input_images(2, 96)
+    rt.set_input_f32(info["input"], x)
+    rt.run()
+    ref = gpu_outputs(rt, info)
+    rt.set_input_f32(info["input"], np.zeros_like(x))
+    rt.run()
+    rt.set_input_f32(info["input"], x)
+    monkeypatch.setenv("DW_TRACE", "1")
+    rt.run_unbatched()
+    for a, b in zip(gpu_outputs(rt, info), ref):
+        np.testing.assert_array_equal(a, b)
+
+
 def test_int8_graph_launch_plan(backend, int8_small):
     g, info = int8_small
     rt = HipGraphRuntime(g, backend)
