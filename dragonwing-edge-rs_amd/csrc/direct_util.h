@@ -79,16 +79,32 @@ __device__ __forceinline__ void store_outputs_t(const DirectArgs& a, const float
       if (a.vec_out == 1) reinterpret_cast<float*>(yb)[j] = v;
     } else if constexpr (OUT == 1) {
       uint16_t hb = f2h(acc[j]);
-      if (a.bias_h) hb = f16_add_bits(hb, a.bias_h[oc0 + j]);
+      if (a.bias_hf)
+        hb = f2h(h2f(hb) + a.bias_hf[oc0 + j]);
+      else if (a.bias_h)
+        hb = f16_add_bits(hb, a.bias_h[oc0 + j]);
       const uint16_t ob = f16_act_bits(hb, a.act);
       words[j >> 1] |= (uint32_t)ob << (16 * (j & 1));
       if (a.vec_out == 1) reinterpret_cast<uint16_t*>(yb)[j] = ob;
     } else {
       uint16_t hb = f2h(acc[j]);
-      if (a.bias_h) hb = f16_add_bits(hb, a.bias_h[oc0 + j]);
-      // QuantizeLinear of the stored f16 value.
-      float q = rintf(__fdiv_rn(h2f(hb), a.out_scale)) + (float)a.out_zp;
-      q = fminf(fmaxf(q, 0.0f), 255.0f);
+      if (a.bias_hf)
+        hb = f2h(h2f(hb) + a.bias_hf[oc0 + j]);
+      else if (a.bias_h)
+        hb = f16_add_bits(hb, a.bias_h[oc0 + j]);
+      // QuantizeLinear of the stored f16 value: x / scale, correctly rounded
+      // (reciprocal + one FMA correction where the host proved that equal for
+      // every finite f16 x; the division otherwise).
+      const float xv = h2f(hb);
+      float d;
+      if (a.out_fast && fabsf(xv) <= 65504.0f) {
+        const float q0 = xv * a.out_rcp;
+        d = fmaf(fmaf(-q0, a.out_scale, xv), a.out_rcp, q0);
+      } else {
+        d = __fdiv_rn(xv, a.out_scale);
+      }
+      float q = rintf(d) + (float)a.out_zp;
+      q = __builtin_amdgcn_fmed3f(q, 0.0f, 255.0f);
       int qi = (int)q;
       if (a.lut) qi = a.lut[qi];
       words[j >> 2] |= (uint32_t)qi << (8 * (j & 3));

@@ -79,7 +79,10 @@ struct IgemmArgs {
   const uint16_t* bias_h;  // EPI_F16 bias (f16 bits) or null
   int kchunk;              // set by the launcher: k-steps per LDS weight chunk
   int tile_bc, tile_pb;    // tile choice (channels, 16-pixel blocks per wave); 0 = heuristic
+  int tile_tpw;            // > 0: persistent kernel, pixel tiles per workgroup (small K only)
   int x_bytes;             // set by the launcher: bytes of the input view's buffer (< 2^31)
+  float r_cin, r_kw, r_hwo, r_wo;  // set by the launcher: 1/cin, 1/kw, 1/(ho*wo), 1/wo
+  int y_bytes, r_bytes;            // set by the launcher: bytes of the output and residual views
 };
 
 // Arguments of the direct convolution with the reference accumulation order.
@@ -99,6 +102,10 @@ struct DirectArgs {
   float out_scale; int out_zp;
   const uint8_t* lut;      // out u8: optional table applied after quantization
   int vec_out;             // set by the launcher: widest aligned store (16, 4 or 1 bytes)
+  const float* bias_hf;    // optional: the f16 bias already widened with the reference decode
+  float out_rcp;           // out u8: 1 / out_scale ...
+  int out_fast;            // ... and 1 if x / out_scale may be computed as x*rcp plus one
+                           // FMA correction (checked exhaustively on the host for every f16 x)
 };
 
 // Depthwise convolution (channel multiplier 1).
@@ -130,7 +137,7 @@ const char* igemm_tile_name(const IgemmArgs& a, int esize);
 int igemm_channel_tile(int cout);
 // Tile shapes launch_igemm can run for `a` (channel tile, pixel blocks per
 // wave); returns how many were written (at most `max`).
-int igemm_candidates(const IgemmArgs& a, int* bc, int* pb, int max);
+int igemm_candidates(const IgemmArgs& a, int* bc, int* pb, int* tpw, int max);
 
 void launch_direct_conv(hipStream_t st, const DirectArgs& a);
 void launch_dwconv(hipStream_t st, const DwArgs& a, int dtype);

@@ -52,6 +52,7 @@ namespace dw {
 // Tile shape of one launch.
 struct TileCfg {
   int bc, pb, pd, kchunk;
+  int tpw;  // > 0: the persistent small-K kernel with this many pixel tiles per workgroup
 };
 
 // Epilogue specialisations.
@@ -88,15 +89,18 @@ inline size_t lds_bytes(const TileCfg& t, int ksteps) {
   return (size_t)lds_chunk_off(t.bc, ksteps, t.pd) + (size_t)t.kchunk * t.bc * 64;
 }
 
-// n / d for 0 <= n < 2^24, 0 < d < 2^24, with rd = 1.0f / d: the float
-// quotient is within 2 of the exact one; two correction steps fix it.
+// n / d for 0 <= n < 2^24 and 1 <= d < 2^23, given rd = 1.0f / d rounded to
+// nearest.  The float product n * rd is within 1 of n / d (its relative
+// error is below 2^-23, and it is exact for d <= 2), so its truncation is
+// floor(n / d) - 1, + 0 or + 1, and one remainder test corrects it.  Every
+// intermediate is an integer below 2^24 in magnitude, so the float
+// arithmetic is exact (and full rate, unlike 32-bit integer multiplies).
 __device__ __forceinline__ int div_small(int n, int d, float rd) {
-  int q = (int)((float)n * rd);
-  int r = n - q * d;
-  q += (r >= d) - (r < 0);
-  r = n - q * d;
-  q += (r >= d) - (r < 0);
-  return q;
+  const float nf = (float)n, df = (float)d;
+  float q = truncf(nf * rd);
+  const float r = fmaf(-q, df, nf);
+  q += (r < 0.0f) ? -1.0f : ((r >= df) ? 1.0f : 0.0f);
+  return (int)q;
 }
 
 // Per-channel epilogue parameters of the workgroup's channel tile, staged
@@ -187,7 +191,62 @@ __device__ __forceinline__ void epilogue4(const IgemmArgs& a, const EpiLds& e, c
   }
 }
 
-template <int ESZ, int BC, int PB, int PD, int EPV>
+// k-slice table: slice q of K (16 bytes, one filter tap) is at element
+// offset .x from the pixel's top-left tap and belongs to tap .y (31 = past
+// the end of K: always padding).  It does not depend on the pixel, so a
+// workgroup builds it once, for nq slices.
+__device__ __forceinline__ void build_ktab(int2* ktab, int nq, int ce, const IgemmArgs& a, int tid) {
+  const int kelems = a.kh * a.kw * a.cin;
+  for (int q = tid; q < nq; q += 256) {
+    const int e = q * ce;
+    int2 t = make_int2(0, 31);
+    if (e < kelems) {
+      const int tap = div_small(e, a.cin, a.r_cin);
+      const int ci = e - tap * a.cin;
+      const int kh = div_small(tap, a.kw, a.r_kw);
+      const int kw = tap - kh * a.kw;
+      t = make_int2((kh * a.w + kw) * a.x_pix_stride + ci, tap);
+    }
+    ktab[q] = t;
+  }
+}
+
+// This lane's pixels p0 + pb*16 + (lane & 15): element offset of the
+// top-left tap and the in-image bit of every tap (none for pixels past the
+// end, or for every pixel when !live).  Each pixel of the wave is
+// decomposed once (lane L takes pixel p0 + L mod 16 PB), and lanes fetch
+// their pixels' values from there.
+template <int PB>
+__device__ __forceinline__ void pixel_setup(const IgemmArgs& a, int p0, int lane, bool live, int (&pbase)[PB],
+                                            uint32_t (&tmask)[PB]) {
+  const int hw_o = a.ho * a.wo;
+  const int p = p0 + (lane & (16 * PB - 1));
+  const bool pv = live && p < a.m;
+  const int pp = pv ? p : 0;
+  const int nn = div_small(pp, hw_o, a.r_hwo);
+  const int r = pp - nn * hw_o;
+  const int oh = div_small(r, a.wo, a.r_wo);
+  const int ow = r - oh * a.wo;
+  const int ih0 = oh * a.sh - a.pt, iw0 = ow * a.sw - a.pl;
+  const int base = ((nn * a.h + ih0) * a.w + iw0) * a.x_pix_stride + a.x_c_off;
+  // filter rows [rlo, rhi) and columns [clo, chi) fall inside the image
+  const int rlo = max(0, -ih0), rhi = min(a.kh, a.h - ih0);
+  const int clo = max(0, -iw0), chi = min(a.kw, a.w - iw0);
+  const uint32_t cols = chi > clo ? (1u << chi) - (1u << clo) : 0u;
+  uint32_t m = 0;
+  for (int kh = 0; kh < a.kh; ++kh) m |= (kh >= rlo && kh < rhi) ? cols << (kh * a.kw) : 0u;
+  m = pv ? m : 0u;
+#pragma unroll
+  for (int pb = 0; pb < PB; ++pb) {
+    const int src = pb * 16 + (lane & 15);
+    pbase[pb] = __shfl(base, src);
+    tmask[pb] = (uint32_t)__shfl((int)m, src);
+  }
+}
+
+// SK: K fits in the start-up loads (ksteps <= PD - 1, and in one weight
+// chunk), so the k-loop issues no loads.
+template <int ESZ, int BC, int PB, int PD, int EPV, bool SK>
 __global__ __launch_bounds__(256) void igemm_kernel(const IgemmArgs a) {
   constexpr int CB = BC / 16;       // 16-channel blocks (all channels of the tile per wave)
   constexpr int CE = 16 / ESZ;      // elements per 16-byte slice
@@ -228,56 +287,12 @@ __global__ __launch_bounds__(256) void igemm_kernel(const IgemmArgs a) {
   int2* const ktab = reinterpret_cast<int2*>(smem + lds_table_off(BC));
   uint8_t* const s_chunk = smem + lds_chunk_off(BC, KSTEPS, PD);
 
-  // ---- k-slice table: slice q of K (16 bytes, one filter tap) is at element
-  // offset koff from the pixel's top-left tap and belongs to tap `tap`
-  // (31 = past the end of K: always padding).  It does not depend on the
-  // pixel, so the workgroup builds it once.  (The ring reads up to k-step
-  // KSTEPS + 2 * PD - 3, see the main loop.)
-  const int nq = (KSTEPS + 2 * PD) * 4;
-  const int kelems = KH * KW * CIN;
-  {
-    const float rcin = 1.0f / (float)CIN, rkw = 1.0f / (float)KW;
-    for (int q = tid; q < nq; q += 256) {
-      const int e = q * CE;
-      int2 t = make_int2(0, 31);
-      if (e < kelems) {
-        const int tap = div_small(e, CIN, rcin);
-        const int ci = e - tap * CIN;
-        const int kh = div_small(tap, KW, rkw);
-        const int kw = tap - kh * KW;
-        t = make_int2((kh * W + kw) * XPS + ci, tap);
-      }
-      ktab[q] = t;
-    }
-  }
-
-  // ---- this lane's pixels p0 + pb*16 + (lane & 15): element offset of the
-  // top-left tap and the in-image bit of every tap
+  // ---- k-slice table (the ring reads up to k-step KSTEPS + 2 * PD - 3,
+  // see the main loop) and this lane's pixels
+  build_ktab(ktab, (KSTEPS + 2 * PD) * 4, CE, a, tid);
   int pbase[PB];
   uint32_t tmask[PB];
-  {
-    const int hw_o = a.ho * a.wo;
-    const float rhw = 1.0f / (float)hw_o, rwo = 1.0f / (float)a.wo;
-#pragma unroll
-    for (int pb = 0; pb < PB; ++pb) {
-      const int p = p0 + pb * 16 + (lane & 15);
-      const bool pv = p < a.m;
-      const int pp = pv ? p : 0;
-      const int nn = div_small(pp, hw_o, rhw);
-      const int r = pp - nn * hw_o;
-      const int oh = div_small(r, a.wo, rwo);
-      const int ow = r - oh * a.wo;
-      const int ih0 = oh * a.sh - a.pt, iw0 = ow * a.sw - a.pl;
-      pbase[pb] = ((nn * H + ih0) * W + iw0) * XPS + XCO;
-      uint32_t rows = 0, cols = 0;
-      for (int kh = 0; kh < KH; ++kh) rows |= (uint32_t)((unsigned)(ih0 + kh) < (unsigned)H) << kh;
-      for (int kw = 0; kw < KW; ++kw) cols |= (uint32_t)((unsigned)(iw0 + kw) < (unsigned)W) << kw;
-      uint32_t m = 0;
-      for (int kh = 0; kh < KH; ++kh)
-        if ((rows >> kh) & 1u) m |= cols << (kh * KW);
-      tmask[pb] = pv ? m : 0u;
-    }
-  }
+  pixel_setup<PB>(a, p0, lane, true, pbase, tmask);
 
   // Weight chunks go to LDS with direct global->LDS loads: one 1 KB
   // fragment per wave instruction, lane l writing bytes [16 l, 16 l + 16).
@@ -287,7 +302,7 @@ __global__ __launch_bounds__(256) void igemm_kernel(const IgemmArgs a) {
     const int nfr_ = (min(KSTEPS, (s_first) + KCH) - (s_first)) * CB;                               \
     for (int f = wave; f < nfr_; f += 4) {                                                          \
       const int sl = f / CB, cb = f - (f / CB) * CB;                                                \
-      const uint8_t* src = WPK + ((size_t)((s_first) + sl) * COUTP + c0 + cb * 16) * 64 + frag_lane; \
+      const uint8_t* src = WPK + (((uint32_t)((s_first) + sl) * COUTP + c0 + cb * 16) * 64u + frag_lane); \
       __builtin_amdgcn_global_load_lds((const void*)src,                                            \
                                        (__attribute__((address_space(3))) void*)(s_chunk + f * 1024), \
                                        16, 0, 0);                                                   \
@@ -318,9 +333,9 @@ __global__ __launch_bounds__(256) void igemm_kernel(const IgemmArgs a) {
   const u32x4 padv = {a.xpad, a.xpad, a.xpad, a.xpad};
   const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc((void*)X, (short)0, a.x_bytes, 0x00020000);
   const int2* my_tab = ktab + (lane >> 4);
-#define DW_LOAD_B(s_, dst, dok)                                                                     \
+#define DW_LOAD_B(tab_entry, dst, dok)                                                              \
   {                                                                                                 \
-    const int2 t_ = my_tab[(s_) * 4];                                                               \
+    const int2 t_ = (tab_entry);                                                                    \
     _Pragma("unroll") for (int pb = 0; pb < PB; ++pb) {                                             \
       const bool ok = (tmask[pb] >> t_.y) & 1u;                                                     \
       const int off = ok ? (pbase[pb] + t_.x) * ESZ : (int)0x80000000;                              \
@@ -338,7 +353,10 @@ __global__ __launch_bounds__(256) void igemm_kernel(const IgemmArgs a) {
   u32x4 bq[PD][PB];
   bool bok[PD][PB];
 #pragma unroll
-  for (int r = 0; r < PD - 1; ++r) DW_LOAD_B(r, bq[r], bok[r]);
+  for (int r = 0; r < PD - 1; ++r) DW_LOAD_B(my_tab[r * 4], bq[r], bok[r]);
+  // table entry of the next k-step to load, read one k-step ahead so that a
+  // load's address never waits for an LDS read
+  int2 tnext = my_tab[(PD - 1) * 4];
 
   // All of the workgroup's start-up loads are in flight together: the first
   // PD - 1 im2col k-steps, the first weight chunk and the epilogue data.
@@ -373,46 +391,78 @@ __global__ __launch_bounds__(256) void igemm_kernel(const IgemmArgs a) {
     for (int pb = 0; pb < PB; ++pb) acc[cb][pb] = init;
   }
 
+  // Weight fragments are read FA fragments ahead of their MFMA (fragment
+  // j = k-step * CB + cb lives in afr[j % FA]), so no MFMA waits for LDS.
+  // A read ahead that falls past the current chunk reads a stale row (the
+  // row index is clamped into the chunk) and is read again once that chunk
+  // has been loaded.
+  constexpr int FA = (PB >= 4 && CB >= 2) ? 2 : CB;
+  static_assert((PD * CB) % FA == 0 && FA <= CB, "fragment ring");
+  const uint8_t* const a_lane = s_chunk + lane * 16;
+#define DW_FRAG(row_, cb_) (*reinterpret_cast<const v4i*>(a_lane + ((row_) * CB + (cb_)) * 1024))
+  v4i afr[FA];
+#pragma unroll
+  for (int i = 0; i < FA; ++i) afr[i] = DW_FRAG(0, i);
+
+  // k-step s_, held in ring slot r_ (a compile-time index): the pad select,
+  // then each weight fragment's MFMAs, with the read of fragment j + FA
+  // issued ahead of them.
+#define DW_MMA_STEP(r_, s_)                                                                          \
+  {                                                                                                  \
+    u32x4 bcur[PB];                                                                                  \
+    _Pragma("unroll") for (int pb = 0; pb < PB; ++pb) {                                              \
+      if constexpr (ESZ == 1)                                                                        \
+        bcur[pb] = bok[r_][pb] ? (bq[r_][pb] ^ XXOR) : padv;                                         \
+      else                                                                                           \
+        bcur[pb] = bq[r_][pb]; /* f16 padding is +0, what the out-of-range load returns */          \
+    }                                                                                                \
+    _Pragma("unroll") for (int cb = 0; cb < CB; ++cb) {                                              \
+      const int slot = ((r_) * CB + cb) % FA;                                                        \
+      const v4i af = afr[slot];                                                                      \
+      const int ahead_row = min((s_) + (cb + FA) / CB - chunk0, KCH - 1); /* fragment j + FA */      \
+      afr[slot] = DW_FRAG(ahead_row, (cb + FA) % CB);                                                \
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); /* this read, then the MFMAs */            \
+      __builtin_amdgcn_sched_group_barrier(0x008, PB, 0);                                            \
+      _Pragma("unroll") for (int pb = 0; pb < PB; ++pb) {                                            \
+        if constexpr (ESZ == 1) {                                                                    \
+          acc[cb][pb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, __builtin_bit_cast(v4i, bcur[pb]), \
+                                                              acc[cb][pb], 0, 0, 0);                 \
+        } else {                                                                                     \
+          acc[cb][pb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(                                      \
+              __builtin_bit_cast(v8h, af), __builtin_bit_cast(v8h, bcur[pb]), acc[cb][pb], 0, 0, 0); \
+        }                                                                                            \
+      }                                                                                              \
+    }                                                                                                \
+  }
+
   int next_chunk = KCH, chunk0 = 0;
-  for (int s0 = 0; s0 < KSTEPS; s0 += PD) {
+  if constexpr (SK) {
+    // Small K: the start-up loads brought all of it.
 #pragma unroll
-    for (int r = 0; r < PD; ++r) {
-      const int s = s0 + r;
-      if (s < KSTEPS && s == next_chunk) {
-        __syncthreads();  // every wave is done with the previous chunk
-        chunk0 = s;
-        next_chunk = s + KCH;
-        DW_ISSUE_A(s);
-        DW_LDS_FENCE();
-      }
-      DW_LOAD_B(s + PD - 1, bq[(r + PD - 1) % PD], bok[(r + PD - 1) % PD]);
-      if (s < KSTEPS) {
-        u32x4 bcur[PB];
+    for (int r = 0; r < PD - 1; ++r)
+      if (r < KSTEPS) DW_MMA_STEP(r, r);
+  } else {
+    for (int s0 = 0; s0 < KSTEPS; s0 += PD) {
 #pragma unroll
-        for (int pb = 0; pb < PB; ++pb) {
-          if constexpr (ESZ == 1)
-            bcur[pb] = bok[r][pb] ? (bq[r][pb] ^ XXOR) : padv;
-          else
-            bcur[pb] = bq[r][pb];  // f16 padding is +0, what the out-of-range load returns
+      for (int r = 0; r < PD; ++r) {
+        const int s = s0 + r;
+        if (s < KSTEPS && s == next_chunk) {
+          __syncthreads();  // every wave is done with the previous chunk
+          chunk0 = s;
+          next_chunk = s + KCH;
+          DW_ISSUE_A(s);
+          DW_LDS_FENCE();
+#pragma unroll
+          for (int i = 0; i < FA; ++i) afr[(r * CB + i) % FA] = DW_FRAG(0, i);
         }
-        const uint8_t* Af = s_chunk + (s - chunk0) * (CB * 1024) + lane * 16;
-#pragma unroll
-        for (int cb = 0; cb < CB; ++cb) {
-          const v4i af = *reinterpret_cast<const v4i*>(Af + cb * 1024);
-#pragma unroll
-          for (int pb = 0; pb < PB; ++pb) {
-            if constexpr (ESZ == 1) {
-              acc[cb][pb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, __builtin_bit_cast(v4i, bcur[pb]),
-                                                                  acc[cb][pb], 0, 0, 0);
-            } else {
-              acc[cb][pb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                  __builtin_bit_cast(v8h, af), __builtin_bit_cast(v8h, bcur[pb]), acc[cb][pb], 0, 0, 0);
-            }
-          }
-        }
+        DW_LOAD_B(tnext, bq[(r + PD - 1) % PD], bok[(r + PD - 1) % PD]);
+        tnext = my_tab[(s + PD) * 4];
+        if (s < KSTEPS) DW_MMA_STEP(r, s);
       }
     }
   }
+#undef DW_MMA_STEP
+#undef DW_FRAG
 #undef DW_ISSUE_A
 #undef DW_LDS_FENCE
 #undef DW_LOAD_B
@@ -471,10 +521,13 @@ __global__ __launch_bounds__(256) void igemm_kernel(const IgemmArgs a) {
 template <int ESZ, int BC, int EPV>
 bool launch_bc(hipStream_t st, const IgemmArgs& a, const TileCfg& t, dim3 grid) {
   const size_t lds = lds_bytes(t, a.ksteps);
-#define DW_T(PB, PD)                                                                         \
-  if (t.pb == PB && t.pd == PD) {                                                            \
-    hipLaunchKernelGGL((igemm_kernel<ESZ, BC, PB, PD, EPV>), grid, dim3(256), lds, st, a);   \
-    return true;                                                                             \
+#define DW_T(PB, PD)                                                                             \
+  if (t.pb == PB && t.pd == PD) {                                                                \
+    if (a.ksteps <= PD - 1 && a.ksteps <= t.kchunk)                                              \
+      hipLaunchKernelGGL((igemm_kernel<ESZ, BC, PB, PD, EPV, true>), grid, dim3(256), lds, st, a);  \
+    else                                                                                         \
+      hipLaunchKernelGGL((igemm_kernel<ESZ, BC, PB, PD, EPV, false>), grid, dim3(256), lds, st, a); \
+    return true;                                                                                 \
   }
   DW_T(4, 4)
   DW_T(2, 6)

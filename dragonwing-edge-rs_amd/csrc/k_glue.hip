@@ -6,6 +6,8 @@
 #include "dw_common.h"
 #include "dw_device.h"
 
+#include <type_traits>
+
 namespace dw {
 namespace {
 
@@ -379,28 +381,24 @@ __device__ __forceinline__ int nearest_index(int o, float scale, int n_in) {
   return (int)f;
 }
 
-template <int ESZ>
-__global__ __launch_bounds__(256) void resize_nearest_kernel(const ResizeArgs a) {
-  // One thread per (output pixel, 4-byte word of channels) when aligned.
-  const int words = a.c * ESZ / 4;
-  const size_t total = (size_t)a.n * a.ho * a.wo * words;
-  const float sh = (float)a.h / (float)a.ho;
-  const float sw = (float)a.w / (float)a.wo;
-  for (size_t t = blockIdx.x * (size_t)blockDim.x + threadIdx.x; t < total;
-       t += (size_t)gridDim.x * blockDim.x) {
-    const int wd = (int)(t % words);
-    const size_t p = t / words;
-    const int hw = a.ho * a.wo;
-    const int nn = (int)(p / hw);
-    const int rem = (int)(p - (size_t)nn * hw);
-    const int oh = rem / a.wo, ow = rem - (rem / a.wo) * a.wo;
-    const int ih = nearest_index(oh, sh, a.h);
-    const int iw = nearest_index(ow, sw, a.w);
-    const size_t src = ((size_t)(nn * a.h + ih) * a.w + iw) * a.x.pix_stride + a.x.c_off;
-    const size_t dst = p * a.y.pix_stride + a.y.c_off;
-    const uint32_t v = *reinterpret_cast<const uint32_t*>((const uint8_t*)a.x.base + src * ESZ + wd * 4);
-    *reinterpret_cast<uint32_t*>((uint8_t*)a.y.base + dst * ESZ + wd * 4) = v;
-  }
+// Workgroups take strips of one output row (row = n * ho + oh, so the
+// source row is uniform); threads over (output column, VB-byte word of the
+// channels).  VB = 16 when both views' rows are 16-byte aligned, else 4.
+template <int VB>
+__global__ __launch_bounds__(256) void resize_nearest_kernel(const ResizeArgs a, int esz, int strips) {
+  using V = typename std::conditional<VB == 16, uint4, uint32_t>::type;
+  const int words = a.c * esz / VB;
+  const int row = blockIdx.x / strips;
+  const int t = (blockIdx.x - row * strips) * 256 + threadIdx.x;
+  if (t >= a.wo * words) return;
+  const int nn = row / a.ho, oh = row - nn * a.ho;
+  const int ow = t / words, wd = t - ow * words;
+  const int ih = nearest_index(oh, (float)a.h / (float)a.ho, a.h);
+  const int iw = nearest_index(ow, (float)a.w / (float)a.wo, a.w);
+  const size_t src = ((size_t)(nn * a.h + ih) * a.w + iw) * a.x.pix_stride + a.x.c_off;
+  const size_t dst = ((size_t)row * a.wo + ow) * a.y.pix_stride + a.y.c_off;
+  const V v = *reinterpret_cast<const V*>((const uint8_t*)a.x.base + src * esz + (size_t)wd * VB);
+  *reinterpret_cast<V*>((uint8_t*)a.y.base + dst * esz + (size_t)wd * VB) = v;
 }
 
 __global__ __launch_bounds__(256) void copy_channels_kernel(View s, View d, int pixels, int bytes_row,
@@ -533,15 +531,20 @@ void launch_maxpool_cascade3(hipStream_t st, const PoolArgs& a, View y2, View y3
 void launch_resize_nearest(hipStream_t st, const ResizeArgs& a, int dtype) {
   const int esz = dtype_size(dtype);
   if ((a.c * esz) % 4 != 0) fail(-2, "resize: channel bytes must be a multiple of 4");
-  const size_t total = (size_t)a.n * a.ho * a.wo * (a.c * esz / 4);
-  if (total == 0) return;
-  const dim3 g(grid_for(total)), b(256);
-  if (esz == 4)
-    hipLaunchKernelGGL(resize_nearest_kernel<4>, g, b, 0, st, a);
-  else if (esz == 2)
-    hipLaunchKernelGGL(resize_nearest_kernel<2>, g, b, 0, st, a);
+  if ((size_t)a.n * a.ho * a.wo * a.c == 0) return;
+  auto aligned16 = [&](const View& v, const void* base) {
+    return ((uintptr_t)base % 16 == 0) && (v.pix_stride * esz) % 16 == 0 && (v.c_off * esz) % 16 == 0;
+  };
+  const bool v16 = (a.c * esz) % 16 == 0 && aligned16(a.x, a.x.base) && aligned16(a.y, a.y.base);
+  const int vb = v16 ? 16 : 4;
+  const int strips = (a.wo * (a.c * esz / vb) + 255) / 256;
+  const long long blocks = (long long)a.n * a.ho * strips;
+  if (blocks >= (1ll << 31)) fail(-2, "resize: output too large");
+  const dim3 g((unsigned)blocks), b(256);
+  if (v16)
+    hipLaunchKernelGGL(resize_nearest_kernel<16>, g, b, 0, st, a, esz, strips);
   else
-    hipLaunchKernelGGL(resize_nearest_kernel<1>, g, b, 0, st, a);
+    hipLaunchKernelGGL(resize_nearest_kernel<4>, g, b, 0, st, a, esz, strips);
   DW_HIP(hipGetLastError());
 }
 

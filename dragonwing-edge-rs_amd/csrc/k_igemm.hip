@@ -1,8 +1,8 @@
 // Implicit-GEMM convolution on CDNA4 matrix cores: tile selection, launch
-// dispatch and weight packing.  The kernel itself is igemm_kernel.h; its
-// instantiations live in k_igemm_i8a.hip, k_igemm_i8b.hip and
-// k_igemm_f16.hip so that they compile in parallel.
-#include "igemm_kernel.h"
+// dispatch and weight packing.  The kernels are igemm_kernel.h and, for
+// small K, the persistent igemm_sk.h; their instantiations live in the
+// k_igemm_*.hip files so that they compile in parallel.
+#include "igemm_sk.h"
 
 #include <stdio.h>
 #include <stdlib.h>
@@ -66,7 +66,21 @@ bool tile_ok(const IgemmArgs& a, int bc, int pb) {
 
 TileCfg make_tile(const IgemmArgs& a, int bc, int pb) {
   const int kchunk = std::max(1, std::min(a.ksteps, kWeightLds / (bc * 64)));
-  return {bc, pb, ring_depth(pb), kchunk};
+  return {bc, pb, ring_depth(pb), kchunk, 0};
+}
+
+// The persistent small-K kernel: all of K in at most 4 k-steps, instantiated
+// for these channel and pixel tiles.
+bool sk_ok(const IgemmArgs& a, int bc, int pb, int tpw) {
+  return tpw > 0 && a.ksteps >= 1 && a.ksteps <= 4 && (pb == 2 || pb == 4) &&
+         (bc == 128 || bc == 64 || bc == 32 || bc == 16) && tile_ok(a, bc, pb);
+}
+
+TileCfg make_sk_tile(const IgemmArgs& a, int bc, int pb, int tpw) {
+  TileCfg t = make_tile(a, bc, pb);
+  t.kchunk = a.ksteps;
+  t.tpw = tpw;
+  return t;
 }
 
 // Tile shape for a problem: an override from DW_IGEMM_TILE (tests and
@@ -77,11 +91,13 @@ TileCfg make_tile(const IgemmArgs& a, int bc, int pb) {
 // kWeightLds bytes.
 TileCfg pick(const IgemmArgs& a) {
   if (const char* env = getenv("DW_IGEMM_TILE")) {
-    int v0 = 0, v1 = 0;
-    const int nv = sscanf(env, "%d,%d", &v0, &v1);
-    if (nv == 2 && tile_ok(a, v0, v1)) return make_tile(a, v0, v1);
+    int v0 = 0, v1 = 0, v2 = 0;
+    const int nv = sscanf(env, "%d,%d,%d", &v0, &v1, &v2);
+    if (nv == 3 && sk_ok(a, v0, v1, v2)) return make_sk_tile(a, v0, v1, v2);
+    if (nv >= 2 && tile_ok(a, v0, v1)) return make_tile(a, v0, v1);
     if (nv == 1 && tile_ok(a, channel_tile(a.cout), v0)) return make_tile(a, channel_tile(a.cout), v0);
   }
+  if (a.tile_bc && sk_ok(a, a.tile_bc, a.tile_pb, a.tile_tpw)) return make_sk_tile(a, a.tile_bc, a.tile_pb, a.tile_tpw);
   if (a.tile_bc && tile_ok(a, a.tile_bc, a.tile_pb)) return make_tile(a, a.tile_bc, a.tile_pb);
   const int bc = channel_tile(a.cout);
   const int ctiles = a.cout_pad / bc;
@@ -103,22 +119,36 @@ int epilogue_variant(const IgemmArgs& a, int esize) {
 
 int igemm_channel_tile(int cout) { return channel_tile(cout); }
 
-int igemm_candidates(const IgemmArgs& a, int* bc, int* pb, int max) {
+int igemm_candidates(const IgemmArgs& a, int* bc, int* pb, int* tpw, int max) {
   int n = 0;
   for (int b : {128, 96, 80, 64, 48, 32, 16})
-    for (int p : {4, 2, 1})
+    for (int p : {4, 2, 1}) {
       if (n < max && tile_ok(a, b, p)) {
         bc[n] = b;
         pb[n] = p;
+        tpw[n] = 0;
         ++n;
       }
+      // persistent variants that still leave a workgroup for every CU
+      const long tiles = (long)((a.m + 64 * p - 1) / (64 * p)) * (a.cout_pad / std::max(b, 1));
+      for (int t : {2, 4, 8})
+        if (n < max && sk_ok(a, b, p, t) && tiles / t >= 256) {
+          bc[n] = b;
+          pb[n] = p;
+          tpw[n] = t;
+          ++n;
+        }
+    }
   return n;
 }
 
 const char* igemm_tile_name(const IgemmArgs& a, int esize) {
   static thread_local char buf[64];
   const TileCfg t = pick(a);
-  snprintf(buf, sizeof buf, "igemm_%s_c%d_p%d", esize == 1 ? "i8" : "f16", t.bc, 64 * t.pb);
+  if (t.tpw > 0)
+    snprintf(buf, sizeof buf, "igemm_%s_c%d_p%d_t%d", esize == 1 ? "i8" : "f16", t.bc, 64 * t.pb, t.tpw);
+  else
+    snprintf(buf, sizeof buf, "igemm_%s_c%d_p%d", esize == 1 ? "i8" : "f16", t.bc, 64 * t.pb);
   return buf;
 }
 
@@ -132,13 +162,32 @@ void launch_igemm(hipStream_t st, const IgemmArgs& a_in, int esize) {
   const long long xb = (long long)a.n * a.h * a.w * a.x_pix_stride * esize;
   if (xb >= (1ll << 31)) fail(-2, "igemm: input view larger than 2 GB");
   a.x_bytes = (int)xb;
-  if (ig::lds_bytes(t, a.ksteps) > 160 * 1024) fail(-2, "igemm: k-slice table does not fit LDS");
+  const size_t lds = t.tpw > 0 ? ig::sk_lds_bytes(t.bc, a.ksteps) : ig::lds_bytes(t, a.ksteps);
+  if (lds > 160 * 1024) fail(-2, "igemm: k-slice table does not fit LDS");
+  if ((long long)a.ho * a.wo >= (1ll << 23)) fail(-2, "igemm: more than 2^23 output pixels per image");
+  if ((long long)a.ksteps * a.cout_pad * 64 >= (1ll << 32)) fail(-2, "igemm: packed weights larger than 4 GB");
+  a.r_cin = 1.0f / (float)a.cin;
+  a.r_kw = 1.0f / (float)a.kw;
+  a.r_hwo = 1.0f / (float)(a.ho * a.wo);
+  a.r_wo = 1.0f / (float)a.wo;
+  // u8 output and residual views, addressed by the persistent kernel's
+  // buffer stores and loads
+  const long long yb = a.epi == EPI_QU8 ? (long long)a.m * a.y_pix_stride : 0;
+  const long long rb = a.epi == EPI_QU8 && a.res ? (long long)a.m * a.r_pix_stride : 0;
+  if (yb >= (1ll << 31) || rb >= (1ll << 31)) fail(-2, "igemm: output view larger than 2 GB");
+  a.y_bytes = (int)yb;
+  a.r_bytes = (int)rb;
+  a.tile_tpw = t.tpw;
   bool ok;
   if (esize == 1) {
     const int epv = epilogue_variant(a, esize);
-    ok = (epv == EPV_GENERIC || epv == EPV_QU8) ? igemm_launch_i8_a(st, a, t, epv) : igemm_launch_i8_b(st, a, t, epv);
+    const bool ab = epv == EPV_GENERIC || epv == EPV_QU8;
+    if (t.tpw > 0)
+      ok = ab ? igemm_launch_sk_i8_a(st, a, t, epv) : igemm_launch_sk_i8_b(st, a, t, epv);
+    else
+      ok = ab ? igemm_launch_i8_a(st, a, t, epv) : igemm_launch_i8_b(st, a, t, epv);
   } else {
-    ok = igemm_launch_f16(st, a, t);
+    ok = t.tpw > 0 ? igemm_launch_sk_f16(st, a, t) : igemm_launch_f16(st, a, t);
   }
   if (!ok) fail(-2, "igemm: no kernel for tile");
   DW_HIP(hipGetLastError());

@@ -133,9 +133,49 @@ struct Runtime {
   void run();
 };
 
+// F16::to_f32_soft (dtype.rs:226-263), used by get_output_f32 as the
+// reference's runtime does.
+float f16_to_f32_ref(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
+  uint32_t out;
+  if (e == 0) {
+    if (m == 0) {
+      out = sign;
+    } else {
+      uint32_t mm = m;
+      int sh = 0;
+      while ((mm & 0x400u) == 0) { mm <<= 1; ++sh; }
+      out = sign | ((uint32_t)(127 - 15 - sh) << 23) | ((mm & 0x3FFu) << 13);
+    }
+  } else if (e == 31) {
+    out = m == 0 ? (sign | 0x7F800000u) : (sign | 0x7FC00000u | (m << 13));
+  } else {
+    out = sign | ((e + 112) << 23) | (m << 13);
+  }
+  float f;
+  memcpy(&f, &out, 4);
+  return f;
+}
+
 namespace {
 
 bool is_float_graph(int dt) { return dt == DW_GRAPH_F32 || dt == DW_GRAPH_F16; }
+
+// Whether rint(x / s), for every finite f16 value x widened with the
+// reference decode, equals rint of the reciprocal quotient with one FMA
+// correction: q0 = x * (1/s); q = fma(fma(-q0, s, x), 1/s, q0).  Checked
+// exhaustively (65,536 inputs), so the kernels may use it bit-exactly.
+bool fast_quant_ok(float s, float rcp) {
+  for (uint32_t h = 0; h < 65536; ++h) {
+    const float x = f16_to_f32_ref((uint16_t)h);
+    if (!(fabsf(x) <= 65504.0f)) continue;  // non-finite: the kernels divide
+    const float q0 = x * rcp;
+    const float q = fmaf(fmaf(-q0, s, x), rcp, q0);
+    if (rintf(q) != rintf(x / s)) return false;
+  }
+  return true;
+}
 
 }  // namespace
 
@@ -803,15 +843,23 @@ void Runtime::emit_conv(const Group& gr) {
   if (!a.wf) a.wf = (const float*)upload(wf.data(), wf.size() * 4);
   if (has_bias) {
     const TensorInfo& B = g.t[op.in[2]];
-    if (gr.out_kind == 0)
+    if (gr.out_kind == 0) {
       a.bias_f = (const float*)upload(B.data.data(), B.data.size());
-    else
+    } else {
       a.bias_h = (const uint16_t*)upload(B.data.data(), B.data.size());
+      if (B.dtype == DW_DTYPE_F16) {  // widen once here, as every f16 operand is widened
+        std::vector<float> bf(B.data.size() / 2);
+        for (size_t i = 0; i < bf.size(); ++i) bf[i] = f16_to_f32_ref(((const uint16_t*)B.data.data())[i]);
+        a.bias_hf = (const float*)upload(bf.data(), bf.size() * 4);
+      }
+    }
   }
   if (gr.out_kind == 2) {
     const RtTensor& q = T(gr.lut ? gr.pre : gr.out);
     a.out_scale = q.scale;
     a.out_zp = q.zp;
+    a.out_rcp = 1.0f / q.scale;
+    a.out_fast = fast_quant_ok(q.scale, a.out_rcp) ? 1 : 0;
     if (gr.lut) {
       uint8_t lut[256];
       build_silu_lut(lut, q.scale, q.zp, y.scale, y.zp);
@@ -934,13 +982,14 @@ void Runtime::autotune() {
   for (auto& L : launches) {
     if (!L.ig) continue;
     IgemmArgs& a = *L.ig;
-    int bc[32], pb[32];
-    const int n = igemm_candidates(a, bc, pb, 32);
+    int bc[64], pb[64], tpw[64];
+    const int n = igemm_candidates(a, bc, pb, tpw, 64);
     float best = 1e30f;
     int bi = -1;
     for (int i = 0; i < n; ++i) {
       a.tile_bc = bc[i];
       a.tile_pb = pb[i];
+      a.tile_tpw = tpw[i];
       launch_igemm(st, a, L.esize);
       float t_min = 1e30f;
       for (int r = 0; r < 3; ++r) {
@@ -960,6 +1009,7 @@ void Runtime::autotune() {
     if (bi >= 0) {
       a.tile_bc = bc[bi];
       a.tile_pb = pb[bi];
+      a.tile_tpw = tpw[bi];
     }
     L.kernel = igemm_tile_name(a, L.esize);
   }
@@ -1029,30 +1079,7 @@ dw::Backend* Bk(dw_hip_backend* be) {
   return b;
 }
 
-// F16::to_f32_soft (dtype.rs:226-263), used by get_output_f32 as the
-// reference's runtime does.
-float f16_to_f32_ref(uint16_t h) {
-  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
-  const uint32_t e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
-  uint32_t out;
-  if (e == 0) {
-    if (m == 0) {
-      out = sign;
-    } else {
-      uint32_t mm = m;
-      int sh = 0;
-      while ((mm & 0x400u) == 0) { mm <<= 1; ++sh; }
-      out = sign | ((uint32_t)(127 - 15 - sh) << 23) | ((mm & 0x3FFu) << 13);
-    }
-  } else if (e == 31) {
-    out = m == 0 ? (sign | 0x7F800000u) : (sign | 0x7FC00000u | (m << 13));
-  } else {
-    out = sign | ((e + 112) << 23) | (m << 13);
-  }
-  float f;
-  memcpy(&f, &out, 4);
-  return f;
-}
+using dw::f16_to_f32_ref;
 }  // namespace
 
 extern "C" {

@@ -84,6 +84,23 @@ def test_int8_graph_small_bit_exact(backend, int8_small):
     assert len(np.unique(got[0])) > 100
 
 
+@pytest.mark.parametrize("tile", ["16,4,3", "32,2,1", "64,4,2", "128,2,5"])
+def test_int8_graph_persistent_tiles_bit_exact(backend, int8_small, monkeypatch, tile):
+    # Every convolution whose K fits the persistent kernel runs on it with
+    # this tile (requantize, activation table and residual epilogues).
+    monkeypatch.setenv("DW_IGEMM_TILE", tile)
+    g, info = int8_small
+    x = yolo.input_images(2, 96)
+    rt = HipGraphRuntime(g, backend)
+    if tile == "16,4,3":
+        assert any(l["kernel"].endswith("_t3") for l in rt.launches())
+    rt.set_input_f32(info["input"], x)
+    rt.run()
+    ref = oracle_run(g, {info["input"]: synth.f16_bits(x)})
+    for o, gv in zip(info["outputs"], gpu_outputs(rt, info)):
+        np.testing.assert_array_equal(gv, ref[o], err_msg=f"{o} tile {tile}")
+
+
 def test_int8_graph_capture_replays_match_eager(backend, int8_small):
     g, info = int8_small
     x = yolo.input_images(2, 96)

@@ -157,6 +157,37 @@ def igemm_tiles(co):
             for pb in (4, 2, 1)]
 
 
+def igemm_sk_tiles(co, ksteps):
+    """The persistent small-K tiles (channel tile, pixel blocks, pixel tiles
+    per workgroup) for c_out = co and a K of `ksteps` 64-byte k-steps; one
+    and three tiles per workgroup (a range that ends part-way is covered)."""
+    if not 1 <= ksteps <= 4:
+        return []
+    top = channel_tile(co)
+    pad = -(-co // top) * top
+    return [(bc, pb, t) for bc in (128, 64, 32, 16) if bc <= top and pad % bc == 0
+            for pb in (4, 2) for t in (1, 3)]
+
+
+@pytest.mark.parametrize("geom", [(2, 10, 10, 48, 96, 1, 1, 0), (1, 23, 17, 256, 128, 1, 1, 0),
+                                  (2, 19, 21, 16, 16, 3, 1, 1), (1, 33, 31, 16, 32, 3, 2, 1),
+                                  (3, 9, 13, 128, 20, 1, 1, 0)])
+def test_qlinearconv_persistent_tiles_bit_exact(backend, geom, monkeypatch):
+    # K of 1 to 4 k-steps: the persistent kernel over every tile it has.
+    n, h, w, ci, co, k, s, p = geom
+    r = synth.Rng(synth.seed_for(700 + sum(geom)))
+    c = dict(x=r.integers((n, h, w, ci), 0, 255).astype(np.uint8),
+             w=r.integers((k, k, ci, co), -127, 127).astype(np.int8),
+             bias=r.integers((co,), -4096, 4096).astype(np.int32),
+             w_scales=r.log_uniform((co,), 1e-3, 1e-2), x_scale=0.02, x_zp=131, y_scale=0.05, y_zp=120)
+    ref = oracle_qconv(c, s, p)
+    tiles = igemm_sk_tiles(co, -(-k * k * ci // 64))
+    assert tiles
+    for bc, pb, t in tiles:
+        monkeypatch.setenv("DW_IGEMM_TILE", f"{bc},{pb},{t}")
+        np.testing.assert_array_equal(run_qconv(backend, c, s, p), ref, err_msg=f"tile {bc},{pb},{t}")
+
+
 @pytest.mark.parametrize("geom", [(2, 9, 11, 64, 256, 3, 2, 1), (1, 13, 7, 128, 80, 3, 1, 1),
                                   (2, 10, 10, 48, 96, 1, 1, 0), (1, 6, 6, 256, 128, 3, 1, 1)])
 def test_qlinearconv_every_tile_bit_exact(backend, geom, monkeypatch):
@@ -323,6 +354,24 @@ def test_conv_f16_mfma_every_tile_identical(backend, monkeypatch):
         np.testing.assert_array_equal(got, first, err_msg=f"tile {bc},{pb}")
 
 
+def test_conv_f16_persistent_tiles_identical(backend, monkeypatch):
+    # 1x1 over 64 f16 channels: two k-steps, so the persistent kernel applies;
+    # it sums the same k-steps in the same order as the other tiles.
+    n, h, w, ci, co, k, s, p = 2, 13, 11, 64, 64, 1, 1, 0
+    r = synth.Rng(synth.seed_for(601))
+    xh = synth.f16_bits(r.normal((n, h, w, ci), 0.0, 1.0))
+    kh_ = synth.f16_bits(r.normal((k, k, ci, co), 0.0, (1.0 / (k * k * ci)) ** 0.5))
+    bh = synth.f16_bits(r.normal((co,), 0.0, 0.1))
+    ref = oracle_conv_f16(xh, kh_, bh, s, p, ops.ACT_SILU)
+    monkeypatch.setenv("DW_IGEMM_TILE", "64,4")
+    first = run_conv_f16(backend, xh, kh_, bh, s, p, ops.ACT_SILU, exact=False)
+    assert rel_err(f16v(first), f16v(ref)) <= 1e-2
+    for bc, pb, t in igemm_sk_tiles(co, 2):
+        monkeypatch.setenv("DW_IGEMM_TILE", f"{bc},{pb},{t}")
+        got = run_conv_f16(backend, xh, kh_, bh, s, p, ops.ACT_SILU, exact=False)
+        np.testing.assert_array_equal(got, first, err_msg=f"tile {bc},{pb},{t}")
+
+
 @pytest.mark.parametrize("geom", [(2, 32, 32, 3, 16, 3, 2, 1), (1, 12, 12, 64, 64, 1, 1, 0),
                                   (1, 10, 10, 80, 80, 1, 1, 0)])
 def test_conv_f16_exact_order_bit_exact(backend, geom):
@@ -429,6 +478,26 @@ def test_float_elementwise(backend):
     assert rel_err(f16v(backend.to_numpy(y16, np.uint16, n)), f16v(oracle.silu_fp16(a16))) <= 1e-2
     ops.sigmoid_fp16(backend, ba16, y16, n)
     assert rel_err(f16v(backend.to_numpy(y16, np.uint16, n)), f16v(oracle.sigmoid_fp16(a16))) <= 1e-2
+
+
+@pytest.mark.parametrize("case", [("u8", 32, (7, 5), (13, 11)), ("u8", 4, (20, 20), (40, 40)),
+                                  ("u8", 128, (9, 12), (4, 7)), ("f16", 8, (6, 6), (12, 12)),
+                                  ("f16", 6, (5, 9), (11, 3))])
+def test_resize_nearest_scales_and_widths(backend, case):
+    # 16-byte rows (u8 c=32/128, f16 c=8) and 4-byte rows, up and down.
+    dt, c, (h, w), (ho, wo) = case
+    r = synth.Rng(synth.seed_for(12 + c + h))
+    if dt == "u8":
+        x = r.integers((2, h, w, c), 0, 255).astype(np.uint8)
+        dtype = ops.DTYPE_U8
+    else:
+        x = synth.f16_bits(r.normal((2, h, w, c), 0.0, 1.0))
+        dtype = ops.DTYPE_F16
+    bx = backend.from_numpy(x)
+    by = backend.alloc(2 * ho * wo * c * x.itemsize)
+    ops.resize_nearest_nhwc(backend, dtype, bx, by, 2, h, w, ho, wo, c)
+    got = backend.to_numpy(by, x.dtype, (2, ho, wo, c))
+    np.testing.assert_array_equal(got, oracle.resize_nearest(x, ho, wo))
 
 
 def test_pool_resize_concat_split(backend):
