@@ -130,6 +130,20 @@ __device__ __forceinline__ int requant_u8(int acc, float m, float zp) {
   return (int)__builtin_amdgcn_fmed3f(q, 0.0f, 255.0f);
 }
 
+// The same value with fewer instructions, for the specialised epilogues.
+// With f = acc * M rounded to f32 (as above), f + 1.5 * 2^23 rounds f to an
+// integer by the current mode (nearest, ties to even: the constant is even,
+// so the parity of the sum is that of rint(f)); for |f| < 2^22 the sum is
+// exactly 1.5 * 2^23 + rint(f), and outside that range it still grows with
+// f, so clamping the sum to [1.5 * 2^23 - y_zp, 1.5 * 2^23 + 255 - y_zp]
+// saturates exactly as above.  Returns the clamped sum's bit pattern, which
+// is qbase + rint(f) + y_zp with qbase = 0x4B400000 - y_zp (lo, hi: the
+// clamp bounds as floats).
+__device__ __forceinline__ int requant_bits(int acc, float m, float lo, float hi) {
+  const float f = (float)acc * m;
+  return __builtin_bit_cast(int, __builtin_amdgcn_fmed3f(f + 12582912.0f, lo, hi));
+}
+
 // QLinearAdd of the table output a and the residual b (QuantizeLinear of
 // the sum of both dequantized operands, RNE, saturated).
 __device__ __forceinline__ int qadd_u8(int qa, int rb, const IgemmArgs& a) {
@@ -330,17 +344,16 @@ __global__ __launch_bounds__(256) void igemm_kernel(const IgemmArgs a) {
   // im2col loads are buffer loads over the input view: padding taps and
   // k-steps past the end of K use an out-of-range offset, which returns
   // zero without a memory access.
-  const u32x4 padv = {a.xpad, a.xpad, a.xpad, a.xpad};
   const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc((void*)X, (short)0, a.x_bytes, 0x00020000);
   const int2* my_tab = ktab + (lane >> 4);
-#define DW_LOAD_B(tab_entry, dst, dok)                                                              \
+#define DW_LOAD_B(tab_entry, dst, dkey)                                                              \
   {                                                                                                 \
     const int2 t_ = (tab_entry);                                                                    \
     _Pragma("unroll") for (int pb = 0; pb < PB; ++pb) {                                             \
       const bool ok = (tmask[pb] >> t_.y) & 1u;                                                     \
       const int off = ok ? (pbase[pb] + t_.x) * ESZ : (int)0x80000000;                              \
       dst[pb] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrsrc, off, 0, 0)); \
-      dok[pb] = ok;                                                                                 \
+      dkey[pb] = ok ? XXOR : a.xpad;                                                                \
     }                                                                                               \
   }
 
@@ -351,9 +364,9 @@ __global__ __launch_bounds__(256) void igemm_kernel(const IgemmArgs a) {
   // loads, also past the last k-step, so the compiler's load counters stay
   // exact and a k-step waits only for its own loads.
   u32x4 bq[PD][PB];
-  bool bok[PD][PB];
+  uint32_t bkey[PD][PB];  // xor key: u8 -> s8 for in-image taps, the pad value for padding
 #pragma unroll
-  for (int r = 0; r < PD - 1; ++r) DW_LOAD_B(my_tab[r * 4], bq[r], bok[r]);
+  for (int r = 0; r < PD - 1; ++r) DW_LOAD_B(my_tab[r * 4], bq[r], bkey[r]);
   // table entry of the next k-step to load, read one k-step ahead so that a
   // load's address never waits for an LDS read
   int2 tnext = my_tab[(PD - 1) * 4];
@@ -391,16 +404,19 @@ __global__ __launch_bounds__(256) void igemm_kernel(const IgemmArgs a) {
     for (int pb = 0; pb < PB; ++pb) acc[cb][pb] = init;
   }
 
-  // Weight fragments are read FA fragments ahead of their MFMA (fragment
-  // j = k-step * CB + cb lives in afr[j % FA]), so no MFMA waits for LDS.
+  // Weight fragments are read FA fragments ahead of their MFMA: fragment
+  // j = k-step * CB + cb lives in afr[j % (2 FA)], and its read goes to a
+  // slot no live fragment occupies, so the ring needs no register copies
+  // (PD * CB is a multiple of 2 FA, so the slots repeat every PD k-steps).
   // A read ahead that falls past the current chunk reads a stale row (the
   // row index is clamped into the chunk) and is read again once that chunk
   // has been loaded.
   constexpr int FA = (PB >= 4 && CB >= 2) ? 2 : CB;
-  static_assert((PD * CB) % FA == 0 && FA <= CB, "fragment ring");
+  constexpr int RS = 2 * FA;
+  static_assert((PD * CB) % RS == 0 && FA <= CB, "fragment ring");
   const uint8_t* const a_lane = s_chunk + lane * 16;
 #define DW_FRAG(row_, cb_) (*reinterpret_cast<const v4i*>(a_lane + ((row_) * CB + (cb_)) * 1024))
-  v4i afr[FA];
+  v4i afr[RS];
 #pragma unroll
   for (int i = 0; i < FA; ++i) afr[i] = DW_FRAG(0, i);
 
@@ -412,15 +428,15 @@ __global__ __launch_bounds__(256) void igemm_kernel(const IgemmArgs a) {
     u32x4 bcur[PB];                                                                                  \
     _Pragma("unroll") for (int pb = 0; pb < PB; ++pb) {                                              \
       if constexpr (ESZ == 1)                                                                        \
-        bcur[pb] = bok[r_][pb] ? (bq[r_][pb] ^ XXOR) : padv;                                         \
+        bcur[pb] = bq[r_][pb] ^ bkey[r_][pb];                                                        \
       else                                                                                           \
         bcur[pb] = bq[r_][pb]; /* f16 padding is +0, what the out-of-range load returns */          \
     }                                                                                                \
     _Pragma("unroll") for (int cb = 0; cb < CB; ++cb) {                                              \
-      const int slot = ((r_) * CB + cb) % FA;                                                        \
-      const v4i af = afr[slot];                                                                      \
+      const int j_ = (r_) * CB + cb;                                                                 \
+      const v4i af = afr[j_ % RS];                                                                   \
       const int ahead_row = min((s_) + (cb + FA) / CB - chunk0, KCH - 1); /* fragment j + FA */      \
-      afr[slot] = DW_FRAG(ahead_row, (cb + FA) % CB);                                                \
+      afr[(j_ + FA) % RS] = DW_FRAG(ahead_row, (cb + FA) % CB);                                      \
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); /* this read, then the MFMAs */            \
       __builtin_amdgcn_sched_group_barrier(0x008, PB, 0);                                            \
       _Pragma("unroll") for (int pb = 0; pb < PB; ++pb) {                                            \
@@ -453,9 +469,9 @@ __global__ __launch_bounds__(256) void igemm_kernel(const IgemmArgs a) {
           DW_ISSUE_A(s);
           DW_LDS_FENCE();
 #pragma unroll
-          for (int i = 0; i < FA; ++i) afr[(r * CB + i) % FA] = DW_FRAG(0, i);
+          for (int i = 0; i < FA; ++i) afr[(r * CB + i) % RS] = DW_FRAG(0, i);
         }
-        DW_LOAD_B(tnext, bq[(r + PD - 1) % PD], bok[(r + PD - 1) % PD]);
+        DW_LOAD_B(tnext, bq[(r + PD - 1) % PD], bkey[(r + PD - 1) % PD]);
         tnext = my_tab[(s + PD) * 4];
         if (s < KSTEPS) DW_MMA_STEP(r, s);
       }
@@ -471,7 +487,9 @@ __global__ __launch_bounds__(256) void igemm_kernel(const IgemmArgs a) {
   // p0 + pb*16 + (lane & 15) for every block
   if constexpr (FAST) {
     const bool full = c0 + BC <= a.cout;
-    const float zpf = (float)a.y_zp;
+    const int qbase = 0x4B400000 - a.y_zp;
+    const float qlo = 12582912.0f - (float)a.y_zp, qhi = qlo + 255.0f;
+    const __attribute__((address_space(3))) uint8_t* lut3 = (const __attribute__((address_space(3))) uint8_t*)s_lut;
     float4 msr[CB];
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) msr[cb] = *reinterpret_cast<const float4*>(s_ms + 4 * (cb * 16 + cq));
@@ -494,8 +512,12 @@ __global__ __launch_bounds__(256) void igemm_kernel(const IgemmArgs a) {
         uint32_t out = 0;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          int qi = requant_u8(acc[cb][pb][r], ms4[r], zpf);
-          if constexpr (EPV != EPV_QU8) qi = s_lut[qi];
+          const int qb = requant_bits(acc[cb][pb][r], ms4[r], qlo, qhi);
+          int qi;
+          if constexpr (EPV != EPV_QU8)
+            qi = lut3[(uint32_t)qb - (uint32_t)qbase];
+          else
+            qi = qb - qbase;
           if constexpr (EPV == EPV_QU8_LUT_RES) qi = qadd_u8(qi, (rres[cb] >> (8 * r)) & 0xff, a);
           out |= (uint32_t)qi << (8 * r);
         }

@@ -39,10 +39,15 @@ __global__ __launch_bounds__(256) void igemm_sk_kernel(const IgemmArgs a) {
   constexpr int WPIX = 16 * PB;
   constexpr int WGPIX = 4 * WPIX;
   constexpr bool FAST = EPV != EPV_GENERIC;
-  constexpr int FA = (PB >= 4 && CB >= 2 && (NS * CB) % 2 == 0) ? 2 : CB;  // fragments read ahead
+  // Weight fragments: all held in registers when there are at most 8, else
+  // read 2 ahead through a ring of 4 (NS * CB is then a multiple of 4, so
+  // the ring runs on into the next tile, whose weights are the same).
+  constexpr int NF = NS * CB;
+  constexpr bool RESIDENT = NF <= 8;
+  constexpr int FA = 2, RS = 4;
   using acc_t = typename std::conditional<ESZ == 1, v4i, v4f>::type;
   static_assert(!FAST || ESZ == 1, "specialised epilogues are int8");
-  static_assert((NS * CB) % FA == 0 && FA <= CB, "fragment ring");
+  static_assert(RESIDENT || NF % RS == 0, "fragment ring");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
   const int tid = threadIdx.x;
@@ -88,7 +93,6 @@ __global__ __launch_bounds__(256) void igemm_sk_kernel(const IgemmArgs a) {
   }
   __syncthreads();  // the k-slice table is complete
 
-  const u32x4 padv = {a.xpad, a.xpad, a.xpad, a.xpad};
   const __amdgpu_buffer_rsrc_t xrsrc =
       __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, a.x_bytes, 0x00020000);
   const int2* my_tab = ktab + (lane >> 4);
@@ -96,7 +100,7 @@ __global__ __launch_bounds__(256) void igemm_sk_kernel(const IgemmArgs a) {
   // and pixels past the end use an out-of-range offset: no memory access),
   // so the compiler's load counters stay exact.
   u32x4 bq[NS][PB];
-  bool bok[NS][PB];
+  uint32_t bkey[NS][PB];  // xor key: u8 -> s8 for in-image taps, the pad value for padding
 #define DW_SK_LOADS()                                                                                 \
   _Pragma("unroll") for (int s = 0; s < NS; ++s) {                                                    \
     const int2 t_ = my_tab[s * 4];                                                                    \
@@ -104,7 +108,7 @@ __global__ __launch_bounds__(256) void igemm_sk_kernel(const IgemmArgs a) {
       const bool ok = (tmask[pb] >> t_.y) & 1u;                                                       \
       const int off = ok ? (pbase[pb] + t_.x) * ESZ : (int)0x80000000;                                \
       bq[s][pb] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrsrc, off, 0, 0)); \
-      bok[s][pb] = ok;                                                                                \
+      bkey[s][pb] = ok ? a.xxor : a.xpad;                                                             \
     }                                                                                                 \
   }
   DW_SK_LOADS();
@@ -155,13 +159,11 @@ __global__ __launch_bounds__(256) void igemm_sk_kernel(const IgemmArgs a) {
   const __amdgpu_buffer_rsrc_t rrsrc =
       __builtin_amdgcn_make_buffer_rsrc((void*)a.res, (short)0, a.r_bytes, 0x00020000);
 
-  // Weight fragment j = k-step * CB + cb sits at s_w + j KB; the read of
-  // fragment j + FA (mod NS * CB: the weights stay, so the ring runs on into
-  // the next tile) is issued ahead of fragment j's MFMAs.
+  // Weight fragment j = k-step * CB + cb sits at s_w + j KB.
   const uint8_t* const w_lane = s_w + lane * 16;
-  v4i afr[FA];
+  v4i afr[RESIDENT ? NF : RS];
 #pragma unroll
-  for (int i = 0; i < FA; ++i) afr[i] = *reinterpret_cast<const v4i*>(w_lane + i * 1024);
+  for (int i = 0; i < (RESIDENT ? NF : FA); ++i) afr[i] = *reinterpret_cast<const v4i*>(w_lane + i * 1024);
 
   for (;;) {
     acc_t acc[CB][PB];
@@ -176,17 +178,22 @@ __global__ __launch_bounds__(256) void igemm_sk_kernel(const IgemmArgs a) {
 #pragma unroll
       for (int pb = 0; pb < PB; ++pb) {
         if constexpr (ESZ == 1)
-          bcur[pb] = bok[s][pb] ? (bq[s][pb] ^ a.xxor) : padv;
+          bcur[pb] = bq[s][pb] ^ bkey[s][pb];
         else
           bcur[pb] = bq[s][pb];  // f16 padding is +0, what the out-of-range load returns
       }
 #pragma unroll
       for (int cb = 0; cb < CB; ++cb) {
         const int j = s * CB + cb;
-        const v4i af = afr[j % FA];
-        afr[j % FA] = *reinterpret_cast<const v4i*>(w_lane + ((j + FA) % (NS * CB)) * 1024);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // this read, then the MFMAs
-        __builtin_amdgcn_sched_group_barrier(0x008, PB, 0);
+        v4i af;
+        if constexpr (RESIDENT) {
+          af = afr[j];
+        } else {
+          af = afr[j % RS];
+          afr[(j + FA) % RS] = *reinterpret_cast<const v4i*>(w_lane + ((j + FA) % NF) * 1024);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // this read, then the MFMAs
+          __builtin_amdgcn_sched_group_barrier(0x008, PB, 0);
+        }
 #pragma unroll
         for (int pb = 0; pb < PB; ++pb) {
           if constexpr (ESZ == 1) {
@@ -226,7 +233,9 @@ __global__ __launch_bounds__(256) void igemm_sk_kernel(const IgemmArgs a) {
 
     // Epilogue of this tile.
     if constexpr (FAST) {
-      const float zpf = (float)a.y_zp;
+      const int qbase = 0x4B400000 - a.y_zp;
+      const float qlo = 12582912.0f - (float)a.y_zp, qhi = qlo + 255.0f;
+      const __attribute__((address_space(3))) uint8_t* lut3 = (const __attribute__((address_space(3))) uint8_t*)s_lut;
 #pragma unroll
       for (int pb = 0; pb < PB; ++pb) {
         const int p = pc + pb * 16 + (lane & 15);
@@ -236,8 +245,12 @@ __global__ __launch_bounds__(256) void igemm_sk_kernel(const IgemmArgs a) {
           uint32_t out = 0;
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            int qi = requant_u8(acc[cb][pb][r], ms4[r], zpf);
-            if constexpr (EPV != EPV_QU8) qi = s_lut[qi];
+            const int qb = requant_bits(acc[cb][pb][r], ms4[r], qlo, qhi);
+            int qi;
+            if constexpr (EPV != EPV_QU8)
+              qi = lut3[(uint32_t)qb - (uint32_t)qbase];
+            else
+              qi = qb - qbase;
             if constexpr (EPV == EPV_QU8_LUT_RES) qi = qadd_u8(qi, (rres[cb][pb] >> (8 * r)) & 0xff, a);
             out |= (uint32_t)qi << (8 * r);
           }

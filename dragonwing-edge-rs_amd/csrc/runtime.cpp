@@ -991,10 +991,12 @@ void Runtime::autotune() {
       a.tile_pb = pb[i];
       a.tile_tpw = tpw[i];
       launch_igemm(st, a, L.esize);
+      // back-to-back launches between the events: the event overhead is
+      // spread over several kernels, so close candidates are told apart
       float t_min = 1e30f;
       for (int r = 0; r < 3; ++r) {
         DW_HIP(hipEventRecord(e0, st));
-        launch_igemm(st, a, L.esize);
+        for (int k = 0; k < 4; ++k) launch_igemm(st, a, L.esize);
         DW_HIP(hipEventRecord(e1, st));
         DW_HIP(hipEventSynchronize(e1));
         float ms = 0;

@@ -169,6 +169,34 @@ def igemm_sk_tiles(co, ksteps):
             for pb in (4, 2) for t in (1, 3)]
 
 
+@pytest.mark.parametrize("case", ["ties", "saturation"])
+@pytest.mark.parametrize("tile", ["32,4", "32,4,2"])
+def test_qlinearconv_requant_ties_and_saturation(backend, case, tile, monkeypatch):
+    # The fast epilogues round acc * M by adding 1.5 * 2^23.  "ties": M = 0.5
+    # exactly, so every odd accumulator is a tie (round half to even);
+    # "saturation": M about 2000, so |acc * M| runs far past 2^22 both ways.
+    monkeypatch.setenv("DW_IGEMM_TILE", tile)
+    r = synth.Rng(synth.seed_for(800 if case == "ties" else 801))
+    n, h, w, ci, co = 2, 9, 10, 32, 32
+    if case == "ties":
+        x = r.integers((n, h, w, ci), 118, 138).astype(np.uint8)
+        wt = r.integers((1, 1, ci, co), -3, 3).astype(np.int8)
+        c = dict(x=x, w=wt, bias=r.integers((co,), -40, 40).astype(np.int32),
+                 w_scales=np.full(co, 0.5, np.float32), x_scale=1.0, x_zp=128, y_scale=1.0, y_zp=128)
+    else:
+        x = r.integers((n, h, w, ci), 0, 255).astype(np.uint8)
+        wt = r.integers((1, 1, ci, co), -127, 127).astype(np.int8)
+        c = dict(x=x, w=wt, bias=r.integers((co,), -4096, 4096).astype(np.int32),
+                 w_scales=np.full(co, 0.25, np.float32), x_scale=0.5, x_zp=100, y_scale=6.25e-5, y_zp=3)
+    ref = oracle_qconv(c, 1, 0)
+    got = run_qconv(backend, c, 1, 0)
+    np.testing.assert_array_equal(got, ref)
+    if case == "ties":
+        assert 10 < len(np.unique(ref)) and (ref == 0).mean() < 0.2 and (ref == 255).mean() < 0.2
+    else:
+        assert (ref == 0).mean() > 0.2 and (ref == 255).mean() > 0.2
+
+
 @pytest.mark.parametrize("geom", [(2, 10, 10, 48, 96, 1, 1, 0), (1, 23, 17, 256, 128, 1, 1, 0),
                                   (2, 19, 21, 16, 16, 3, 1, 1), (1, 33, 31, 16, 32, 3, 2, 1),
                                   (3, 9, 13, 128, 20, 1, 1, 0)])
