@@ -362,7 +362,11 @@ static int dwconv_common(dw_hip_backend* be, int dtype, const dw_hip_buffer* inp
   Backend* b = B(be);
   const size_t es = dtype == DW_DTYPE_F16 ? 2 : 4;
   Geo g = geo(n, h_in, w_in, c, c, k_h, k_w, stride_h, stride_w, pad_h, pad_w);
-  if (c % 8 != 0) dw::fail(DW_ERR_UNSUPPORTED, "depthwise: c must be a multiple of 8");
+  // f16 3x3 with stride 1 or 2 runs on the sliding-window kernel (channel
+  // groups of 4); every other shape on the generic one (groups of 8)
+  const bool sliding = dtype == DW_DTYPE_F16 && k_h == 3 && k_w == 3 && (stride_w == 1 || stride_w == 2);
+  if (c % (sliding ? 4 : 8) != 0)
+    dw::fail(DW_ERR_UNSUPPORTED, sliding ? "depthwise: c must be a multiple of 4" : "depthwise: c must be a multiple of 8");
   need(input, n * h_in * w_in * c * es, "depthwise: input");
   need(kernel, k_h * k_w * c * es, "depthwise: kernel");
   need(output, n * g.ho * g.wo * c * es, "depthwise: output");

@@ -9,7 +9,16 @@ namespace dw {
 // IEEE binary16 <-> f32 (hardware conversions; f32 -> f16 rounds to nearest
 // even with subnormals, as F16::from_f32_soft does, dtype.rs:164-222).
 __device__ __forceinline__ float h2f_ieee(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
-__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+// f32 -> f16, round to nearest even, of an f32 value that has been rounded
+// to f32.  The empty asm makes the value opaque: without it the compiler
+// may fuse the conversion with the fmaf that produced the value into one
+// v_fma_mixlo_f16, which rounds the exact sum to f16 once, not to f32 and
+// then to f16 as the reference does (the two differ by an f16 ulp when the
+// f32 rounding lands on an f16 rounding midpoint).
+__device__ __forceinline__ uint16_t f2h(float f) {
+  asm("" : "+v"(f));
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
 
 // F16::to_f32_soft (crates/dragonwing-core/src/dtype.rs:226-263).  It is the
 // IEEE decode except for subnormals, which it returns at half their IEEE

@@ -146,6 +146,98 @@ __global__ __launch_bounds__(256) void conv_small_kernel(const DirectArgs a) {
   dx::store_outputs<OC>(a, acc, oc0, (uint8_t*)a.y + yo * OES);
 }
 
+// Depthwise 3x3 over f16 NHWC with a sliding window along the output row.
+// A thread owns 4 channels of SEG consecutive outputs of one row: it
+// widens its 36 weights once, keeps the 3x3 window of widened inputs in
+// registers and loads only the SW new input columns per output, so every
+// input is loaded and widened 3 times (once per output row that reads it)
+// instead of 9.  Each output is the reference's sum: taps in (kh, kw)
+// order, fmaf in f32 on the reference-widened operands; out-of-image taps
+// contribute an exact +0, which leaves the sum as the reference's skip does
+// (the running sum starts at +0 and so is never -0; weights are finite).
+template <int SW>
+__global__ __launch_bounds__(256) void dwconv3_f16_kernel(const DwArgs a, int segs) {
+  constexpr int SEG = 8, CPT = 4;
+  const int groups = a.c / CPT;
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  if (t >= a.n * a.ho * segs * groups) return;
+  const int g = t % groups;
+  int rest = t / groups;
+  const int sg = rest % segs;
+  rest /= segs;
+  const int oh = rest % a.ho;
+  const int nn = rest / a.ho;
+  const int c0 = g * CPT;
+  const int ow0 = sg * SEG;
+
+  float wv[3][3][CPT];
+#pragma unroll
+  for (int k = 0; k < 9; ++k) {
+    const uint2 r = *reinterpret_cast<const uint2*>((const uint16_t*)a.wt + (size_t)k * a.c + c0);
+    wv[k / 3][k % 3][0] = h2f(r.x & 0xffff);
+    wv[k / 3][k % 3][1] = h2f(r.x >> 16);
+    wv[k / 3][k % 3][2] = h2f(r.y & 0xffff);
+    wv[k / 3][k % 3][3] = h2f(r.y >> 16);
+  }
+  uint16_t bh[CPT] = {0, 0, 0, 0};
+  if (a.bias) {
+    const uint2 r = *reinterpret_cast<const uint2*>((const uint16_t*)a.bias + c0);
+    bh[0] = r.x & 0xffff; bh[1] = r.x >> 16; bh[2] = r.y & 0xffff; bh[3] = r.y >> 16;
+  }
+
+  const uint16_t* rowp[3];
+  bool rv[3];
+#pragma unroll
+  for (int kh = 0; kh < 3; ++kh) {
+    const int ih = oh * a.sh - a.pt + kh;
+    rv[kh] = ih >= 0 && ih < a.h;
+    rowp[kh] = (const uint16_t*)a.x + ((size_t)(nn * a.h + (rv[kh] ? ih : 0)) * a.w) * a.x_pix_stride + a.x_c_off + c0;
+  }
+  // window column q (input column iw0 + q) lives in slot q % 3
+  float xw[3][3][CPT];
+  const int iw0 = ow0 * SW - a.pl;
+#define DW_LOAD_COL(q)                                                                      \
+  {                                                                                         \
+    const int iw = iw0 + (q);                                                               \
+    const bool cv = iw >= 0 && iw < a.w;                                                    \
+    _Pragma("unroll") for (int kh = 0; kh < 3; ++kh) {                                      \
+      uint2 r = make_uint2(0, 0);                                                           \
+      if (cv && rv[kh]) r = *reinterpret_cast<const uint2*>(rowp[kh] + (size_t)iw * a.x_pix_stride); \
+      xw[kh][(q) % 3][0] = h2f(r.x & 0xffff);                                               \
+      xw[kh][(q) % 3][1] = h2f(r.x >> 16);                                                  \
+      xw[kh][(q) % 3][2] = h2f(r.y & 0xffff);                                               \
+      xw[kh][(q) % 3][3] = h2f(r.y >> 16);                                                  \
+    }                                                                                       \
+  }
+  DW_LOAD_COL(0);
+  DW_LOAD_COL(1);
+  uint16_t* const yrow = (uint16_t*)a.y + ((size_t)(nn * a.ho + oh) * a.wo) * a.y_pix_stride + a.y_c_off + c0;
+#pragma unroll
+  for (int j = 0; j < SEG; ++j) {
+    if (ow0 + j >= a.wo) break;
+    // new columns of this output: q in (SW * (j - 1) + 2, SW * j + 2]
+#pragma unroll
+    for (int q = (j == 0 ? 2 : SW * (j - 1) + 3); q <= SW * j + 2; ++q) DW_LOAD_COL(q);
+    float acc[CPT] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int kh = 0; kh < 3; ++kh)
+#pragma unroll
+      for (int kw = 0; kw < 3; ++kw)
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) acc[c] = fmaf(xw[kh][(SW * j + kw) % 3][c], wv[kh][kw][c], acc[c]);
+    uint16_t ob[CPT];
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+      uint16_t hb = f2h(acc[c]);
+      if (a.bias) hb = f16_add_bits(hb, bh[c]);
+      ob[c] = f16_act_bits(hb, a.act);
+    }
+    *reinterpret_cast<uint2*>(yrow + (size_t)(ow0 + j) * a.y_pix_stride) =
+        make_uint2((uint32_t)ob[0] | ((uint32_t)ob[1] << 16), (uint32_t)ob[2] | ((uint32_t)ob[3] << 16));
+  }
+#undef DW_LOAD_COL
+}
+
 template <int ESZ>
 __global__ __launch_bounds__(256) void dwconv_kernel(const DwArgs a) {
   constexpr int V = 8;
@@ -307,6 +399,25 @@ void launch_direct_conv(hipStream_t st, const DirectArgs& a_in) {
 }
 
 void launch_dwconv(hipStream_t st, const DwArgs& a, int dtype) {
+  // f16 3x3, stride 1 or 2: the sliding-window kernel (8-byte channel
+  // groups; the same sums, so the same results as the generic kernel)
+  const bool al8 = (uintptr_t)a.x % 8 == 0 && (uintptr_t)a.y % 8 == 0 && (uintptr_t)a.wt % 8 == 0 &&
+                   (uintptr_t)a.bias % 8 == 0 && (a.x_pix_stride * 2) % 8 == 0 && (a.x_c_off * 2) % 8 == 0 &&
+                   (a.y_pix_stride * 2) % 8 == 0 && (a.y_c_off * 2) % 8 == 0;
+  if (dtype == F16 && a.kh == 3 && a.kw == 3 && (a.sw == 1 || a.sw == 2) && a.c % 4 == 0 && al8) {
+    const int segs = (a.wo + 7) / 8;
+    const long long threads = (long long)a.n * a.ho * segs * (a.c / 4);
+    if (threads < (1ll << 31)) {
+      const dim3 g((unsigned)((threads + 255) / 256));
+      if (a.sw == 1)
+        hipLaunchKernelGGL(dwconv3_f16_kernel<1>, g, dim3(256), 0, st, a, segs);
+      else
+        hipLaunchKernelGGL(dwconv3_f16_kernel<2>, g, dim3(256), 0, st, a, segs);
+      DW_HIP(hipGetLastError());
+      return;
+    }
+  }
+  if (a.c % 8 != 0) fail(-2, "depthwise: c must be a multiple of 8 for this shape");
   const size_t total = (size_t)a.n * a.ho * a.wo * (a.c / 8);
   size_t blocks = (total + 255) / 256;
   if (blocks > 65535 * 8) blocks = 65535 * 8;

@@ -136,7 +136,8 @@ int dw_hip_conv2d_bias_act_f16_nhwc(dw_hip_backend* be, const dw_hip_buffer* inp
 /* depthwise_conv2d_fp16_nhwc_mt (crates/dragonwing-cpu/src/ops.rs:2819-2933)
  * with channel_multiplier 1, then bias and activation as in
  * CpuGraphRuntime (runtime.rs:1467-1498).  kernel: [k_h][k_w][c] f16,
- * bias: [c] f16 or NULL.  Requires c % 8 == 0. */
+ * bias: [c] f16 or NULL.  Requires c % 4 == 0 for a 3x3 kernel with
+ * stride_w 1 or 2, else c % 8 == 0. */
 int dw_hip_depthwise_conv2d_f16_nhwc(dw_hip_backend* be, const dw_hip_buffer* input,
                                      const dw_hip_buffer* kernel, const dw_hip_buffer* bias,
                                      dw_hip_buffer* output, size_t n, size_t h_in, size_t w_in,

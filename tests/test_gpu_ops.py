@@ -459,6 +459,27 @@ def test_depthwise_f16_full_workload(backend):
     assert np.mean(got != ref) < 1e-3  # f16 flips from expf last-bit differences are rare
 
 
+@pytest.mark.parametrize("geom", [(1, 5, 11, 12, 1), (2, 13, 10, 4, 2), (1, 9, 17, 20, 1), (3, 8, 19, 36, 2)])
+def test_depthwise_f16_sliding_window_shapes(backend, geom):
+    # Row lengths that end part-way through a thread's 8 outputs, channel
+    # counts that are multiples of 4 but not 8, both strides; bias and no bias.
+    n, h, w, c, s = geom
+    r = synth.Rng(synth.seed_for(420 + sum(geom)))
+    xh = synth.f16_bits(r.normal((n, h, w, c), 0.0, 1.0))
+    kh_ = synth.f16_bits(r.normal((3, 3, c), 0.0, 0.3))
+    bh = synth.f16_bits(r.normal((c,), 0.0, 0.1))
+    ho, wo = oracle.out_hw(h, w, 3, 3, s, s, 1, 1)
+    bx, bk, bb = backend.from_numpy(xh), backend.from_numpy(kh_), backend.from_numpy(bh)
+    by = backend.alloc(n * ho * wo * c * 2)
+    ops.depthwise_conv2d_f16_nhwc(backend, bx, bk, bb, by, n, h, w, c, 3, 3, s, s, 1, 1, ops.ACT_NONE)
+    np.testing.assert_array_equal(backend.to_numpy(by, np.uint16, (n, ho, wo, c)),
+                                  oracle.bias_add_f16(oracle.depthwise_fp16(xh, kh_, (s, s), (1, 1)), bh))
+    ops.depthwise_conv2d_f16_nhwc(backend, bx, bk, None, by, n, h, w, c, 3, 3, s, s, 1, 1, ops.ACT_SILU)
+    got = backend.to_numpy(by, np.uint16, (n, ho, wo, c))
+    ref = oracle.silu_fp16(oracle.depthwise_fp16(xh, kh_, (s, s), (1, 1)))
+    assert rel_err(f16v(got), f16v(ref)) <= 1e-2
+
+
 @pytest.mark.parametrize("geom", [(1, 7, 5, 8, 2), (2, 9, 9, 16, 1), (1, 6, 6, 24, 2)])
 def test_depthwise_f32_and_f16_ragged(backend, geom):
     n, h, w, c, s = geom
