@@ -117,6 +117,7 @@ struct DwArgs {
   int n, h, w, c, kh, kw, sh, sw, pt, pl, ho, wo;
   int act;
   int x_pix_stride, x_c_off, y_pix_stride, y_c_off;
+  int w_plain;  // 1: no f16 weight is subnormal (checked by whoever fills the struct)
 };
 
 // ---------------------------------------------------------------------------

@@ -26,8 +26,10 @@ __device__ __forceinline__ uint16_t f2h(float f) {
 // dragonwing-cpu widens every f16 operand through it, so kernels that must
 // reproduce the CPU results bit for bit decode with this function.
 __device__ __forceinline__ float h2f(uint16_t b) {
+  // subnormal f16 <=> nonzero |v| < 2^-14; zeros give v * 0.5 = v, and NaN
+  // fails the comparison
   const float v = h2f_ieee(b);
-  return ((b & 0x7C00u) == 0 && (b & 0x03FFu) != 0) ? v * 0.5f : v;
+  return fabsf(v) < 6.103515625e-05f ? v * 0.5f : v;
 }
 
 // f32 -> f16 -> f32: the value the next CPU op sees after an f16 store.
@@ -52,6 +54,26 @@ __device__ __forceinline__ uint16_t f16_act_bits(uint16_t hb, int act) {
     return f2h(v * h2f(s));
   }
   return hb;
+}
+
+// SiLU of an f16 value for the fp16 paths held to the fp16 tolerance: the
+// reference's steps (sigmoid in f32, rounded to f16, times x, rounded to
+// f16) with exp and the reciprocal from the hardware's exp2 and rcp, each
+// refined to about an f32 ulp: exp(-x) = 2^hi * (1 + lo ln 2) with hi + lo
+// = -x log2(e) split exactly by an fma, and one Newton step on 1 / (1 + e).
+// Operands are widened as IEEE f16 (the reference halves subnormals; a
+// subnormal x only changes an output below 2^-14 in magnitude).
+__device__ __forceinline__ uint16_t silu_f16_fast(uint16_t hb) {
+  const float x = h2f_ieee(hb);
+  const float hi = x * -1.44269502f;
+  const float lo = fmaf(x, -1.44269502f, -hi) + x * -1.92596299e-08f;
+  float e = __builtin_amdgcn_exp2f(hi);
+  e = fmaf(e, lo * 0.693147182f, e);
+  const float d = 1.0f + e;
+  float r = __builtin_amdgcn_rcpf(d);
+  r = fmaf(r, fmaf(-d, r, 1.0f), r);
+  const uint16_t s = f2h(r);
+  return f2h(x * h2f_ieee(s));
 }
 
 }  // namespace dw

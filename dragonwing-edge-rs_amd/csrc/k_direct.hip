@@ -146,18 +146,25 @@ __global__ __launch_bounds__(256) void conv_small_kernel(const DirectArgs a) {
   dx::store_outputs<OC>(a, acc, oc0, (uint8_t*)a.y + yo * OES);
 }
 
-// Depthwise 3x3 over f16 NHWC with a sliding window along the output row.
-// A thread owns 4 channels of SEG consecutive outputs of one row: it
-// widens its 36 weights once, keeps the 3x3 window of widened inputs in
-// registers and loads only the SW new input columns per output, so every
-// input is loaded and widened 3 times (once per output row that reads it)
-// instead of 9.  Each output is the reference's sum: taps in (kh, kw)
-// order, fmaf in f32 on the reference-widened operands; out-of-image taps
-// contribute an exact +0, which leaves the sum as the reference's skip does
-// (the running sum starts at +0 and so is never -0; weights are finite).
-template <int SW>
+// Depthwise 3x3 over f16 NHWC, a row segment per thread.  A thread owns 4
+// channels of SEG consecutive outputs of one row; it loads the segment's
+// SW * (SEG - 1) + 3 input columns of its 3 input rows up front (raw f16,
+// 8 bytes each), so every input is loaded 3 times (once per output row that
+// reads it) instead of 9, and all loads are in flight together.  Each output
+// is the reference's sum: taps in (kh, kw) order, fmaf in f32.  The inputs
+// enter the fma as f16 operands (v_fma_mix widens them exactly), which is
+// the reference's widening unless the value is an f16 subnormal (the
+// reference halves those): an output whose window holds one, anywhere in
+// the wave, takes the decoding path.  WPLAIN: no weight is subnormal (the
+// planner checks), so the weights enter the fma as f16 too.  Out-of-image
+// taps contribute an exact +0, which leaves the sum as the reference's skip
+// does (the running sum starts at +0 and so is never -0; weights are
+// finite).  SiLU uses silu_f16_fast (fp16 tolerance).
+template <int SW, int SEG, bool WPLAIN, bool BIAS, int ACT>
 __global__ __launch_bounds__(256) void dwconv3_f16_kernel(const DwArgs a, int segs) {
-  constexpr int SEG = 8, CPT = 4;
+  constexpr int CPT = 4;
+  constexpr int NC = SW * (SEG - 1) + 3;
+  typedef unsigned short us2 __attribute__((ext_vector_type(2)));
   const int groups = a.c / CPT;
   const int t = blockIdx.x * 256 + threadIdx.x;
   if (t >= a.n * a.ho * segs * groups) return;
@@ -170,21 +177,15 @@ __global__ __launch_bounds__(256) void dwconv3_f16_kernel(const DwArgs a, int se
   const int c0 = g * CPT;
   const int ow0 = sg * SEG;
 
-  float wv[3][3][CPT];
+  // weights and bias first: the first output needs them with its columns
+  uint2 wr[9];
 #pragma unroll
-  for (int k = 0; k < 9; ++k) {
-    const uint2 r = *reinterpret_cast<const uint2*>((const uint16_t*)a.wt + (size_t)k * a.c + c0);
-    wv[k / 3][k % 3][0] = h2f(r.x & 0xffff);
-    wv[k / 3][k % 3][1] = h2f(r.x >> 16);
-    wv[k / 3][k % 3][2] = h2f(r.y & 0xffff);
-    wv[k / 3][k % 3][3] = h2f(r.y >> 16);
-  }
-  uint16_t bh[CPT] = {0, 0, 0, 0};
-  if (a.bias) {
+  for (int k = 0; k < 9; ++k) wr[k] = *reinterpret_cast<const uint2*>((const uint16_t*)a.wt + (size_t)k * a.c + c0);
+  float bf[CPT] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (BIAS) {
     const uint2 r = *reinterpret_cast<const uint2*>((const uint16_t*)a.bias + c0);
-    bh[0] = r.x & 0xffff; bh[1] = r.x >> 16; bh[2] = r.y & 0xffff; bh[3] = r.y >> 16;
+    bf[0] = h2f(r.x & 0xffff); bf[1] = h2f(r.x >> 16); bf[2] = h2f(r.y & 0xffff); bf[3] = h2f(r.y >> 16);
   }
-
   const uint16_t* rowp[3];
   bool rv[3];
 #pragma unroll
@@ -193,49 +194,93 @@ __global__ __launch_bounds__(256) void dwconv3_f16_kernel(const DwArgs a, int se
     rv[kh] = ih >= 0 && ih < a.h;
     rowp[kh] = (const uint16_t*)a.x + ((size_t)(nn * a.h + (rv[kh] ? ih : 0)) * a.w) * a.x_pix_stride + a.x_c_off + c0;
   }
-  // window column q (input column iw0 + q) lives in slot q % 3
-  float xw[3][3][CPT];
+  // input column q of the segment is iw0 + q
   const int iw0 = ow0 * SW - a.pl;
-#define DW_LOAD_COL(q)                                                                      \
-  {                                                                                         \
-    const int iw = iw0 + (q);                                                               \
-    const bool cv = iw >= 0 && iw < a.w;                                                    \
-    _Pragma("unroll") for (int kh = 0; kh < 3; ++kh) {                                      \
-      uint2 r = make_uint2(0, 0);                                                           \
-      if (cv && rv[kh]) r = *reinterpret_cast<const uint2*>(rowp[kh] + (size_t)iw * a.x_pix_stride); \
-      xw[kh][(q) % 3][0] = h2f(r.x & 0xffff);                                               \
-      xw[kh][(q) % 3][1] = h2f(r.x >> 16);                                                  \
-      xw[kh][(q) % 3][2] = h2f(r.y & 0xffff);                                               \
-      xw[kh][(q) % 3][3] = h2f(r.y >> 16);                                                  \
-    }                                                                                       \
+  uint2 xc[NC][3];
+#pragma unroll
+  for (int q = 0; q < NC; ++q) {
+    const int iw = iw0 + q;
+    const bool cv = iw >= 0 && iw < a.w;
+#pragma unroll
+    for (int kh = 0; kh < 3; ++kh) {
+      xc[q][kh] = make_uint2(0, 0);
+      if (cv && rv[kh]) xc[q][kh] = *reinterpret_cast<const uint2*>(rowp[kh] + (size_t)iw * a.x_pix_stride);
+    }
   }
-  DW_LOAD_COL(0);
-  DW_LOAD_COL(1);
+  float wv[3][3][CPT];
+  if constexpr (!WPLAIN) {
+#pragma unroll
+    for (int k = 0; k < 9; ++k) {
+      wv[k / 3][k % 3][0] = h2f(wr[k].x & 0xffff);
+      wv[k / 3][k % 3][1] = h2f(wr[k].x >> 16);
+      wv[k / 3][k % 3][2] = h2f(wr[k].y & 0xffff);
+      wv[k / 3][k % 3][3] = h2f(wr[k].y >> 16);
+    }
+  }
+  // columns holding an f16 subnormal: |h| - 1 (mod 2^16) < 0x3ff
+  bool subc[NC];
+#pragma unroll
+  for (int q = 0; q < NC; ++q) {
+    us2 mn = {0xffff, 0xffff};
+    const us2 one = {1, 1};
+#pragma unroll
+    for (int kh = 0; kh < 3; ++kh) {
+      mn = __builtin_elementwise_min(mn, __builtin_bit_cast(us2, xc[q][kh].x & 0x7fff7fffu) - one);
+      mn = __builtin_elementwise_min(mn, __builtin_bit_cast(us2, xc[q][kh].y & 0x7fff7fffu) - one);
+    }
+    subc[q] = mn.x < 0x3ff || mn.y < 0x3ff;
+  }
+
   uint16_t* const yrow = (uint16_t*)a.y + ((size_t)(nn * a.ho + oh) * a.wo) * a.y_pix_stride + a.y_c_off + c0;
+#define DW_HALVES(r_) {(uint16_t)((r_).x & 0xffff), (uint16_t)((r_).x >> 16), (uint16_t)((r_).y & 0xffff), (uint16_t)((r_).y >> 16)}
 #pragma unroll
   for (int j = 0; j < SEG; ++j) {
-    if (ow0 + j >= a.wo) break;
-    // new columns of this output: q in (SW * (j - 1) + 2, SW * j + 2]
+    if (ow0 + j < a.wo) {
+      float acc[CPT] = {0.0f, 0.0f, 0.0f, 0.0f};
+      const bool sub = subc[SW * j] || subc[SW * j + 1] || subc[SW * j + 2];
+      if (__any(sub)) {
 #pragma unroll
-    for (int q = (j == 0 ? 2 : SW * (j - 1) + 3); q <= SW * j + 2; ++q) DW_LOAD_COL(q);
-    float acc[CPT] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int kh = 0; kh < 3; ++kh)
 #pragma unroll
-    for (int kh = 0; kh < 3; ++kh)
+          for (int kw = 0; kw < 3; ++kw) {
+            const uint16_t hv[CPT] = DW_HALVES(xc[SW * j + kw][kh]);
+            const uint16_t hw[CPT] = DW_HALVES(wr[kh * 3 + kw]);
 #pragma unroll
-      for (int kw = 0; kw < 3; ++kw)
+            for (int c = 0; c < CPT; ++c) {
+              const float wk = WPLAIN ? h2f_ieee(hw[c]) : wv[kh][kw][c];
+              acc[c] = fmaf(h2f(hv[c]), wk, acc[c]);
+            }
+          }
+      } else {
 #pragma unroll
-        for (int c = 0; c < CPT; ++c) acc[c] = fmaf(xw[kh][(SW * j + kw) % 3][c], wv[kh][kw][c], acc[c]);
-    uint16_t ob[CPT];
+        for (int kh = 0; kh < 3; ++kh)
 #pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-      uint16_t hb = f2h(acc[c]);
-      if (a.bias) hb = f16_add_bits(hb, bh[c]);
-      ob[c] = f16_act_bits(hb, a.act);
+          for (int kw = 0; kw < 3; ++kw) {
+            const uint16_t hv[CPT] = DW_HALVES(xc[SW * j + kw][kh]);
+            const uint16_t hw[CPT] = DW_HALVES(wr[kh * 3 + kw]);
+#pragma unroll
+            for (int c = 0; c < CPT; ++c) {
+              const float wk = WPLAIN ? h2f_ieee(hw[c]) : wv[kh][kw][c];
+              acc[c] = fmaf(h2f_ieee(hv[c]), wk, acc[c]);
+            }
+          }
+      }
+      uint16_t ob[CPT];
+#pragma unroll
+      for (int c = 0; c < CPT; ++c) {
+        uint16_t hb = f2h(acc[c]);
+        if constexpr (BIAS) hb = f2h(h2f(hb) + bf[c]);
+        if constexpr (ACT == ACT_SILU)
+          hb = silu_f16_fast(hb);
+        else if constexpr (ACT == ACT_RELU)
+          hb = f16_act_bits(hb, ACT_RELU);
+        ob[c] = hb;
+      }
+      *reinterpret_cast<uint2*>(yrow + (size_t)(ow0 + j) * a.y_pix_stride) =
+          make_uint2((uint32_t)ob[0] | ((uint32_t)ob[1] << 16), (uint32_t)ob[2] | ((uint32_t)ob[3] << 16));
     }
-    *reinterpret_cast<uint2*>(yrow + (size_t)(ow0 + j) * a.y_pix_stride) =
-        make_uint2((uint32_t)ob[0] | ((uint32_t)ob[1] << 16), (uint32_t)ob[2] | ((uint32_t)ob[3] << 16));
   }
-#undef DW_LOAD_COL
+#undef DW_HALVES
 }
 
 template <int ESZ>
@@ -405,14 +450,30 @@ void launch_dwconv(hipStream_t st, const DwArgs& a, int dtype) {
                    (uintptr_t)a.bias % 8 == 0 && (a.x_pix_stride * 2) % 8 == 0 && (a.x_c_off * 2) % 8 == 0 &&
                    (a.y_pix_stride * 2) % 8 == 0 && (a.y_c_off * 2) % 8 == 0;
   if (dtype == F16 && a.kh == 3 && a.kw == 3 && (a.sw == 1 || a.sw == 2) && a.c % 4 == 0 && al8) {
-    const int segs = (a.wo + 7) / 8;
+    // 8 outputs per thread at stride 1, 4 at stride 2 (10 and 9 input columns)
+    const int seg = a.sw == 1 ? 8 : 4;
+    const int segs = (a.wo + seg - 1) / seg;
     const long long threads = (long long)a.n * a.ho * segs * (a.c / 4);
     if (threads < (1ll << 31)) {
       const dim3 g((unsigned)((threads + 255) / 256));
-      if (a.sw == 1)
-        hipLaunchKernelGGL(dwconv3_f16_kernel<1>, g, dim3(256), 0, st, a, segs);
-      else
-        hipLaunchKernelGGL(dwconv3_f16_kernel<2>, g, dim3(256), 0, st, a, segs);
+      const bool bias = a.bias != nullptr;
+#define DW_DW3(SW_, SEG_, WP_, B_, ACT_)                                                          \
+  if (a.sw == SW_ && (a.w_plain != 0) == WP_ && bias == B_ && a.act == ACT_)                       \
+    hipLaunchKernelGGL((dwconv3_f16_kernel<SW_, SEG_, WP_, B_, ACT_>), g, dim3(256), 0, st, a, segs); \
+  else
+#define DW_DW3_ACTS(SW_, SEG_, WP_, B_) \
+  DW_DW3(SW_, SEG_, WP_, B_, ACT_NONE) DW_DW3(SW_, SEG_, WP_, B_, ACT_RELU) DW_DW3(SW_, SEG_, WP_, B_, ACT_SILU)
+      DW_DW3_ACTS(1, 8, true, true)
+      DW_DW3_ACTS(1, 8, true, false)
+      DW_DW3_ACTS(1, 8, false, true)
+      DW_DW3_ACTS(1, 8, false, false)
+      DW_DW3_ACTS(2, 4, true, true)
+      DW_DW3_ACTS(2, 4, true, false)
+      DW_DW3_ACTS(2, 4, false, true)
+      DW_DW3_ACTS(2, 4, false, false)
+      fail(-2, "depthwise: no kernel for this activation");
+#undef DW_DW3_ACTS
+#undef DW_DW3
       DW_HIP(hipGetLastError());
       return;
     }

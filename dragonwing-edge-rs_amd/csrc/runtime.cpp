@@ -614,6 +614,12 @@ void Runtime::emit(const Group& gr) {
     a.y = y.base;
     a.wt = upload(W.data.data(), W.data.size());
     if (op.in.size() > 2 && !op.in[2].empty()) a.bias = upload(g.t[op.in[2]].data.data(), g.t[op.in[2]].data.size());
+    if (x.dtype == F16) {
+      a.w_plain = 1;
+      const uint16_t* wh = (const uint16_t*)W.data.data();
+      for (size_t i = 0; i < W.data.size() / 2; ++i)
+        if ((wh[i] & 0x7C00u) == 0 && (wh[i] & 0x03FFu) != 0) a.w_plain = 0;
+    }
     a.n = (int)x.n; a.h = (int)x.h; a.w = (int)x.w; a.c = (int)x.c;
     a.kh = (int)W.dims[0]; a.kw = (int)W.dims[1];
     a.sh = std::max(1, op.p.strides[0]); a.sw = std::max(1, op.p.strides[1]);
