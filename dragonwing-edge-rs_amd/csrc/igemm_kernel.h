@@ -114,11 +114,13 @@ struct EpiLds {
 
 // f16 epilogue chain of CpuGraphRuntime: conv result rounded to f16, then
 // the bias pass, the activation and the residual add, each on stored f16.
+// (The MFMA sums already differ from the reference's order, so these
+// results are held to the fp16 tolerance and SiLU takes silu_f16_fast.)
 __device__ __forceinline__ uint16_t f16_chain(float acc, const uint16_t* bias_h, int ch, int act,
                                               bool has_res, uint16_t resv) {
   uint16_t hb = f2h(acc);
   if (bias_h) hb = f16_add_bits(hb, bias_h[ch]);
-  hb = f16_act_bits(hb, act);
+  hb = act == ACT_SILU ? silu_f16_fast(hb) : f16_act_bits(hb, act);
   if (has_res) hb = f16_add_bits(hb, resv);
   return hb;
 }
