@@ -73,11 +73,17 @@ def family(kernel: str) -> str:
 def profile(rts, launches, iters: int, repeat: int):
     """Per-launch milliseconds on the backend stream (each launch enqueued
     `repeat` times back to back between one HIP event pair, averaged over
-    `iters` passes: kernel duration plus the dispatch-to-dispatch gap), and
-    per kernel family: launches, total ms, algorithmic work and bytes."""
+    `iters` passes: kernel duration plus the dispatch-to-dispatch gap; with
+    several runtimes the repeats cycle through their buffer sets), and per
+    kernel family: launches, total ms, algorithmic work and bytes."""
+    from dragonwing_edge_rs_amd.graph import time_launches_rotated
+
     acc = None
     for i in range(iters):
-        ms = rts[i % len(rts)].time_launches(repeat).astype(np.float64)
+        if len(rts) > 1:
+            ms = time_launches_rotated(rts, repeat).astype(np.float64)
+        else:
+            ms = rts[0].time_launches(repeat).astype(np.float64)
         acc = ms if acc is None else acc + ms
     ms = acc / iters
     fam = {}
@@ -290,6 +296,9 @@ def main():
                 f.write(json.dumps(dict(L, ms=round(float(t), 5))) + "\n")
     dom = fams[0]
     roof = roofline_of(dom)
+    roof["timing"] = ("each launch repeated back to back between HIP events" +
+                      (", cycling through %d buffer sets (more than the Infinity Cache holds)" % rotate
+                       if rotate > 1 else ""))
     kernels = []
     for f in fams[:8]:
         r = roofline_of(f)

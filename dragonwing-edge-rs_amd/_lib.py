@@ -121,6 +121,7 @@ SIGNATURES = {
     "dw_hip_graph_launch_info": (S, [P, I]),
     "dw_hip_graph_run_profiled": (I, [P, P]),
     "dw_hip_graph_time_launches": (I, [P, I, P]),
+    "dw_hip_graph_time_launches_rotated": (I, [P, I, I, P]),
     "dw_hip_graph_run_unbatched": (I, [P]),
     "dw_hip_graph_num_io": (I, [P, I]),
     "dw_hip_graph_io_name": (S, [P, I, I]),

@@ -1316,6 +1316,35 @@ int dw_hip_graph_time_launches(dw_hip_graph_runtime* rth, int repeat, float* lau
   API_END
 }
 
+int dw_hip_graph_time_launches_rotated(dw_hip_graph_runtime* const* rths, int n_rt, int repeat, float* launch_ms) {
+  API_BEGIN
+  if (!rths || n_rt < 1 || !launch_ms || repeat < 1)
+    dw::fail(DW_ERR_INVALID, "time_launches_rotated: null argument, no runtime or repeat < 1");
+  const dw::Runtime& r0 = R(rths[0]);
+  for (int k = 1; k < n_rt; ++k) {
+    const dw::Runtime& rk = R(rths[k]);
+    if (rk.launches.size() != r0.launches.size() || rk.be != r0.be)
+      dw::fail(DW_ERR_INVALID, "time_launches_rotated: runtimes differ in launches or backend");
+  }
+  const size_t n = r0.launches.size();
+  hipEvent_t e0, e1;
+  DW_HIP(hipEventCreate(&e0));
+  DW_HIP(hipEventCreate(&e1));
+  hipStream_t st = r0.be->stream;
+  for (size_t i = 0; i < n; ++i) {
+    DW_HIP(hipEventRecord(e0, st));
+    for (int r = 0; r < repeat; ++r) R(rths[r % n_rt]).launches[i].fn(st);
+    DW_HIP(hipEventRecord(e1, st));
+    DW_HIP(hipEventSynchronize(e1));
+    float ms = 0;
+    DW_HIP(hipEventElapsedTime(&ms, e0, e1));
+    launch_ms[i] = ms / repeat;
+  }
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  API_END
+}
+
 // Calibrator (crates/dragonwing-onnx/src/calibration.rs:90-260): runs the F32
 // graph on the GPU over `num_images` inputs (in batches of the graph's N),
 // records per-tensor min/max (calibration.rs:56-69) and stores the ranges in

@@ -251,6 +251,18 @@ class HipGraphRuntime:
         return ms
 
 
+def time_launches_rotated(runtimes, repeat: int = 8) -> np.ndarray:
+    """Per-launch milliseconds with the repeats of each launch cycling
+    through ``runtimes`` (HipGraphRuntime objects of one graph on one
+    backend): dw_hip_graph_time_launches_rotated."""
+    lib = load()
+    n = lib.dw_hip_graph_num_launches(runtimes[0]._h)
+    handles = (C.c_void_p * len(runtimes))(*[rt._h for rt in runtimes])
+    ms = np.zeros(n, np.float32)
+    check(lib.dw_hip_graph_time_launches_rotated(handles, len(runtimes), repeat, ms.ctypes.data))
+    return ms
+
+
 def calibrate(backend, graph: Graph, input_name: str, images: np.ndarray):
     """Runs the F32 NHWC graph on the GPU over ``images`` ([k*N, H, W, C] f32)
     and stores per-tensor min/max ranges in ``graph``."""

@@ -401,6 +401,12 @@ int dw_hip_graph_run_profiled(dw_hip_graph_runtime* rt, float* launch_ms);
  * over the repeats).  Every launch only reads its inputs and writes its
  * outputs, so repeating it leaves the run's results as one run would. */
 int dw_hip_graph_time_launches(dw_hip_graph_runtime* rt, int repeat, float* launch_ms);
+/* As dw_hip_graph_time_launches, but the repeats of launch i cycle through
+ * n_rt runtimes built from the same graph on the same backend (repeat r
+ * runs runtime r % n_rt), so a working set larger than the Infinity Cache
+ * is timed from HBM.  No counterpart in the reference (measurement only). */
+int dw_hip_graph_time_launches_rotated(dw_hip_graph_runtime* const* rts, int n_rt, int repeat,
+                                       float* launch_ms);
 
 #ifdef __cplusplus
 }
