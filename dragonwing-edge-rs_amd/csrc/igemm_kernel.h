@@ -276,8 +276,7 @@ __global__ __launch_bounds__(256) void igemm_kernel(const IgemmArgs a) {
 
   const uint8_t* __restrict__ X = a.x;
   const uint8_t* __restrict__ WPK = a.wpk;
-  const int H = a.h, W = a.w, CIN = a.cin, KH = a.kh, KW = a.kw;
-  const int XPS = a.x_pix_stride, XCO = a.x_c_off, KSTEPS = a.ksteps, COUTP = a.cout_pad;
+  const int KSTEPS = a.ksteps, COUTP = a.cout_pad;
   const int KCH = a.kchunk;
   const uint32_t XXOR = a.xxor;
 

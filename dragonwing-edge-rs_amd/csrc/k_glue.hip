@@ -158,11 +158,6 @@ __global__ __launch_bounds__(256) void elementwise2d_kernel(const Ew2Args e) {
   }
 }
 
-template <typename T>
-__device__ __forceinline__ float ld_as_f(const T* p);
-template <>
-__device__ __forceinline__ float ld_as_f<float>(const float* p) { return *p; }
-
 // Padded max pool over one element type.  Padded taps never win (ONNX
 // MaxPool); a window with no valid tap cannot occur for pad < kernel.
 template <typename T>

@@ -160,8 +160,6 @@ float f16_to_f32_ref(uint16_t h) {
 
 namespace {
 
-bool is_float_graph(int dt) { return dt == DW_GRAPH_F32 || dt == DW_GRAPH_F16; }
-
 // Whether rint(x / s), for every finite f16 value x widened with the
 // reference decode, equals rint of the reciprocal quotient with one FMA
 // correction: q0 = x * (1/s); q = fma(fma(-q0, s, x), 1/s, q0).  Checked
