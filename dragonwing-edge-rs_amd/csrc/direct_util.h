@@ -57,8 +57,13 @@ __device__ __forceinline__ void load_vec(const DirectArgs& a, const uint8_t* p, 
 // 16 or 4 bytes at a time when the view allows (a.vec_out), else element by
 // element.  One instantiation per output type keeps each unrolled loop
 // small, so acc and words stay in registers.
-template <int OUT, int OC>
-__device__ __forceinline__ void store_outputs_t(const DirectArgs& a, const float* acc, int oc0, uint8_t* yb) {
+// FE (a.fast_epi set by the host): the f16 values are widened as IEEE f16
+// (one instruction) and the quantization rounds by adding 1.5 * 2^23 and
+// clamps with one med3 on the float (as requant_bits in igemm_kernel.h).
+// lut: the activation table (LDS or global); a.lut when null.
+template <int OUT, int OC, bool FE = false>
+__device__ __forceinline__ void store_outputs_t(const DirectArgs& a, const float* acc, int oc0, uint8_t* yb,
+                                                const uint8_t* lut = nullptr) {
   constexpr int OES = OUT == 0 ? 4 : (OUT == 1 ? 2 : 1);
   constexpr int NW = (OC * OES + 3) / 4;
   uint32_t words[NW];
@@ -80,7 +85,7 @@ __device__ __forceinline__ void store_outputs_t(const DirectArgs& a, const float
     } else if constexpr (OUT == 1) {
       uint16_t hb = f2h(acc[j]);
       if (a.bias_hf)
-        hb = f2h(h2f(hb) + a.bias_hf[oc0 + j]);
+        hb = f2h((FE ? h2f_ieee(hb) : h2f(hb)) + a.bias_hf[oc0 + j]);
       else if (a.bias_h)
         hb = f16_add_bits(hb, a.bias_h[oc0 + j]);
       const uint16_t ob = f16_act_bits(hb, a.act);
@@ -89,24 +94,35 @@ __device__ __forceinline__ void store_outputs_t(const DirectArgs& a, const float
     } else {
       uint16_t hb = f2h(acc[j]);
       if (a.bias_hf)
-        hb = f2h(h2f(hb) + a.bias_hf[oc0 + j]);
+        hb = f2h((FE ? h2f_ieee(hb) : h2f(hb)) + a.bias_hf[oc0 + j]);
       else if (a.bias_h)
         hb = f16_add_bits(hb, a.bias_h[oc0 + j]);
       // QuantizeLinear of the stored f16 value: x / scale, correctly rounded
       // (reciprocal + one FMA correction where the host proved that equal for
       // every finite f16 x; the division otherwise).
-      const float xv = h2f(hb);
-      float d;
-      if (a.out_fast && fabsf(xv) <= 65504.0f) {
+      int qi;
+      if constexpr (FE) {
+        const float xv = h2f_ieee(hb);
         const float q0 = xv * a.out_rcp;
-        d = fmaf(fmaf(-q0, a.out_scale, xv), a.out_rcp, q0);
+        const float dc = fmaf(fmaf(-q0, a.out_scale, xv), a.out_rcp, q0);
+        const float d = fabsf(xv) <= 65504.0f ? dc : q0;  // inf * rcp is the quotient too
+        const float lo = 12582912.0f - (float)a.out_zp;
+        const int qb = __builtin_bit_cast(int, __builtin_amdgcn_fmed3f(d + 12582912.0f, lo, lo + 255.0f));
+        qi = (qb - (0x4B400000 - a.out_zp)) & 0xff;  // the clamp makes it 0..255 (the mask keeps table reads in range)
       } else {
-        d = __fdiv_rn(xv, a.out_scale);
+        const float xv = h2f(hb);
+        float d;
+        if (a.out_fast && fabsf(xv) <= 65504.0f) {
+          const float q0 = xv * a.out_rcp;
+          d = fmaf(fmaf(-q0, a.out_scale, xv), a.out_rcp, q0);
+        } else {
+          d = __fdiv_rn(xv, a.out_scale);
+        }
+        float q = rintf(d) + (float)a.out_zp;
+        q = __builtin_amdgcn_fmed3f(q, 0.0f, 255.0f);
+        qi = (int)q;
       }
-      float q = rintf(d) + (float)a.out_zp;
-      q = __builtin_amdgcn_fmed3f(q, 0.0f, 255.0f);
-      int qi = (int)q;
-      if (a.lut) qi = a.lut[qi];
+      if (a.lut) qi = (lut ? lut : a.lut)[qi];
       words[j >> 2] |= (uint32_t)qi << (8 * (j & 3));
       if (a.vec_out == 1) yb[j] = (uint8_t)qi;
     }

@@ -106,6 +106,9 @@ struct DirectArgs {
   float out_rcp;           // out u8: 1 / out_scale ...
   int out_fast;            // ... and 1 if x / out_scale may be computed as x*rcp plus one
                            // FMA correction (checked exhaustively on the host for every f16 x)
+  int fast_epi;            // 1: out_fast holds, and the epilogue may widen its f16 values
+                           // as IEEE f16 (the host checked that no subnormal changes a result)
+  int x_bytes;             // set by the launcher for buffer-load paths: bytes of the input
 };
 
 // Depthwise convolution (channel multiplier 1).

@@ -99,10 +99,21 @@ __global__ __launch_bounds__(256) void direct_conv_kernel(const DirectArgs a) {
 // clamped in-image address and are then skipped), decoded once, and fed to
 // OC FMA chains in the reference order, skipping out-of-image taps exactly
 // as the reference does.  Weights come through scalar loads (SGPR operands).
-template <int IN_KIND, int OC, int KH, int KW, int CIN>
+// PAR >= 0 (f16 input, 3 channels, dense rows, even column stride): the 9
+// values of one filter row are 18 contiguous bytes at a 2-byte offset of
+// parity PAR; they come in with five 4-byte buffer loads from the 4-byte
+// boundary at or below them (15 loads per output instead of 27; a load
+// outside the buffer returns zeros, and out-of-image taps are skipped as
+// always).
+template <int IN_KIND, int OC, int KH, int KW, int CIN, bool FE, int PAR>
 __global__ __launch_bounds__(256) void conv_small_kernel(const DirectArgs a) {
+  static_assert(PAR < 0 || (IN_KIND == 1 && KW == 3 && CIN == 3), "row loads: f16, 3x3 taps of 3 channels");
   constexpr int ES = IN_KIND == 0 ? 4 : (IN_KIND == 1 ? 2 : 1);
   constexpr int KT = KH * KW;
+  // the activation table in LDS (one byte per thread)
+  __shared__ uint8_t s_lut[256];
+  if (a.lut) s_lut[threadIdx.x] = a.lut[threadIdx.x];
+  __syncthreads();
   const int p = blockIdx.x * blockDim.x + threadIdx.x;
   if (p >= a.m) return;
   const int oc0 = blockIdx.y * OC;
@@ -115,18 +126,48 @@ __global__ __launch_bounds__(256) void conv_small_kernel(const DirectArgs a) {
   const uint8_t* __restrict__ X = (const uint8_t*)a.x;
   float xv[KT][CIN];
   bool ok[KT];
+  if constexpr (PAR >= 0) {
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, a.x_bytes, 0x00020000);
 #pragma unroll
-  for (int kh = 0; kh < KH; ++kh)
+    for (int kh = 0; kh < KH; ++kh) {
+      const int ih = ih0 + kh;
+      const bool rv = (unsigned)ih < (unsigned)a.h;
+      // half index of the row's first value, less PAR: a 4-byte boundary
+      const int off = rv ? (((nn * a.h + ih) * a.w + iw0) * 3 - PAR) * 2 : (int)0x80000000;
+      // five 4-byte loads.  The row of image 0's first pixel row starts 8
+      // bytes before the buffer when iw0 < 0: each load's offset is formed
+      // here, and a negative one is sent out of range (a negative voffset
+      // plus an immediate offset is not wrapped back into range).
+      uint32_t dw[5];
 #pragma unroll
-    for (int kw = 0; kw < KW; ++kw) {
-      const int ih = ih0 + kh, iw = iw0 + kw;
-      const bool v = (unsigned)ih < (unsigned)a.h && (unsigned)iw < (unsigned)a.w;
-      ok[kh * KW + kw] = v;
-      const int ihc = min(max(ih, 0), a.h - 1), iwc = min(max(iw, 0), a.w - 1);
-      const uint8_t* xp = X + (((size_t)(nn * a.h + ihc) * a.w + iwc) * a.x_pix_stride + a.x_c_off) * ES;
+      for (int i = 0; i < 5; ++i) {
+        const int o = off + 4 * i;
+        dw[i] = __builtin_amdgcn_raw_buffer_load_b32(xr, o < 0 ? (int)0x80000000 : o, 0, 0);
+      }
 #pragma unroll
-      for (int ic = 0; ic < CIN; ++ic) xv[kh * KW + kw][ic] = load1<IN_KIND>(a, xp + ic * ES);
+      for (int kw = 0; kw < KW; ++kw) {
+        ok[kh * KW + kw] = rv && (unsigned)(iw0 + kw) < (unsigned)a.w;
+#pragma unroll
+        for (int ic = 0; ic < CIN; ++ic) {
+          const int hi = PAR + kw * 3 + ic;  // half index in the 20 loaded bytes
+          xv[kh * KW + kw][ic] = h2f((uint16_t)(dw[hi >> 1] >> (16 * (hi & 1))));
+        }
+      }
     }
+  } else {
+#pragma unroll
+    for (int kh = 0; kh < KH; ++kh)
+#pragma unroll
+      for (int kw = 0; kw < KW; ++kw) {
+        const int ih = ih0 + kh, iw = iw0 + kw;
+        const bool v = (unsigned)ih < (unsigned)a.h && (unsigned)iw < (unsigned)a.w;
+        ok[kh * KW + kw] = v;
+        const int ihc = min(max(ih, 0), a.h - 1), iwc = min(max(iw, 0), a.w - 1);
+        const uint8_t* xp = X + (((size_t)(nn * a.h + ihc) * a.w + iwc) * a.x_pix_stride + a.x_c_off) * ES;
+#pragma unroll
+        for (int ic = 0; ic < CIN; ++ic) xv[kh * KW + kw][ic] = load1<IN_KIND>(a, xp + ic * ES);
+      }
+  }
   const wrow_t wbase = (wrow_t)(a.wf + oc0);
   float acc[OC];
 #pragma unroll
@@ -141,9 +182,13 @@ __global__ __launch_bounds__(256) void conv_small_kernel(const DirectArgs a) {
       for (int j = 0; j < OC; ++j) acc[j] = fmaf(xv[t][ic], wr[j], acc[j]);
     }
   }
-  const int OES = a.out_kind == 0 ? 4 : (a.out_kind == 1 ? 2 : 1);
   const size_t yo = (size_t)p * a.y_pix_stride + a.y_c_off + oc0;
-  dx::store_outputs<OC>(a, acc, oc0, (uint8_t*)a.y + yo * OES);
+  if (a.out_kind == 0)
+    dx::store_outputs_t<0, OC>(a, acc, oc0, (uint8_t*)a.y + yo * 4);
+  else if (a.out_kind == 1)
+    dx::store_outputs_t<1, OC, FE>(a, acc, oc0, (uint8_t*)a.y + yo * 2);
+  else
+    dx::store_outputs_t<2, OC, FE>(a, acc, oc0, (uint8_t*)a.y + yo, s_lut);
 }
 
 // Depthwise 3x3 over f16 NHWC, a row segment per thread.  A thread owns 4
@@ -386,10 +431,31 @@ void launch_direct_conv(hipStream_t st, const DirectArgs& a_in) {
     };
     a.vec_out = aligned(16) ? 16 : (aligned(4) ? 4 : 1);
     const dim3 grid((a.m + 255) / 256, a.cout / 16);
+    // row loads: dense f16 rows of even width, 4-byte aligned base, even
+    // column stride (every output's first input pixel index then has the
+    // parity of the left pad, so the loads start on 4-byte boundaries)
+    const long long xb = (long long)a.n * a.h * a.w * 6;
+    const bool rows = a.in_kind == 1 && a.x_pix_stride == 3 && a.x_c_off == 0 && a.sw % 2 == 0 &&
+                      a.w % 2 == 0 && (uintptr_t)a.x % 4 == 0 && xb + 16 < (1ll << 31);
+    a.x_bytes = rows ? (int)xb : 0;
+    const int par = a.pl & 1;
+#define DW_SMALL(FE_, PAR_) \
+  hipLaunchKernelGGL((conv_small_kernel<1, 16, 3, 3, 3, FE_, PAR_>), grid, dim3(256), 0, st, a)
     if (a.in_kind == 0)
-      hipLaunchKernelGGL((conv_small_kernel<0, 16, 3, 3, 3>), grid, dim3(256), 0, st, a);
+      hipLaunchKernelGGL((conv_small_kernel<0, 16, 3, 3, 3, false, -1>), grid, dim3(256), 0, st, a);
+    else if (rows && par == 1 && a.fast_epi)
+      DW_SMALL(true, 1);
+    else if (rows && par == 1)
+      DW_SMALL(false, 1);
+    else if (rows && a.fast_epi)
+      DW_SMALL(true, 0);
+    else if (rows)
+      DW_SMALL(false, 0);
+    else if (a.fast_epi)
+      DW_SMALL(true, -1);
     else
-      hipLaunchKernelGGL((conv_small_kernel<1, 16, 3, 3, 3>), grid, dim3(256), 0, st, a);
+      DW_SMALL(false, -1);
+#undef DW_SMALL
     DW_HIP(hipGetLastError());
     return;
   }

@@ -175,6 +175,32 @@ bool fast_quant_ok(float s, float rcp) {
   return true;
 }
 
+// Whether the exact-conv epilogue may widen its f16 values as IEEE f16
+// instead of the reference decode (which halves subnormals) and use the
+// reciprocal quotient: true when no f16 subnormal can change an output.
+//  * bias pass F16(f32(y) + b): checked for every subnormal y and every
+//    channel's bias;
+//  * QuantizeLinear: a subnormal |y| < 2^-14 gives |y / s| < 0.5 either way
+//    when s >= 2^-13, so it quantizes to the zero point both ways; and the
+//    reciprocal quotient must be exact (out_fast).
+bool fast_epi_ok(const GraphIR& g, const OpNode& op, bool has_bias, int out_kind, const DirectArgs& a) {
+  if (out_kind == 2 && (!a.out_fast || !(a.out_scale >= 1.220703125e-04f))) return false;
+  if (!has_bias) return true;
+  const TensorInfo& B = g.t.at(op.in[2]);
+  if (B.dtype != DW_DTYPE_F16) return false;
+  const uint16_t* bh = (const uint16_t*)B.data.data();
+  for (size_t c = 0; c < B.data.size() / 2; ++c) {
+    const float b = f16_to_f32_ref(bh[c]);
+    for (uint32_t m = 1; m < 0x400; ++m)
+      for (uint32_t sign : {0u, 0x8000u}) {
+        const float ieee = ldexpf((float)m, -24) * (sign ? -1.0f : 1.0f);
+        const float ref = f16_to_f32_ref((uint16_t)(sign | m));
+        if (f16_bits_from_f32(ref + b) != f16_bits_from_f32(ieee + b)) return false;
+      }
+  }
+  return true;
+}
+
 }  // namespace
 
 void Runtime::build(Backend* b, const GraphIR& graph, bool stats_mode) {
@@ -870,6 +896,7 @@ void Runtime::emit_conv(const Group& gr) {
       a.lut = (const uint8_t*)upload(lut, 256);
     }
   }
+  if (gr.out_kind != 0) a.fast_epi = fast_epi_ok(g, op, has_bias, gr.out_kind, a) ? 1 : 0;
   L.kernel = "direct_conv";
   L.bytes += (double)x.bytes() + W.numel() * 4.0 + (double)y.bytes();
   L.fn = [=](hipStream_t st) { launch_direct_conv(st, a); };

@@ -401,11 +401,17 @@ def test_conv_f16_persistent_tiles_identical(backend, monkeypatch):
 
 
 @pytest.mark.parametrize("geom", [(2, 32, 32, 3, 16, 3, 2, 1), (1, 12, 12, 64, 64, 1, 1, 0),
-                                  (1, 10, 10, 80, 80, 1, 1, 0)])
+                                  (1, 10, 10, 80, 80, 1, 1, 0), (1, 17, 15, 3, 16, 3, 2, 1),
+                                  (2, 20, 22, 3, 16, 3, 2, 0), (1, 9, 12, 3, 32, 3, 2, 1),
+                                  (1, 11, 10, 3, 16, 3, 1, 1)])
 def test_conv_f16_exact_order_bit_exact(backend, geom):
+    # The 3-channel stem shapes take the row-load path (even width and
+    # column stride, either pad parity) or the per-value loads (odd width,
+    # stride 1); subnormal inputs are planted for the reference's decode.
     n, h, w, ci, co, k, s, p = geom
     r = synth.Rng(synth.seed_for(300 + sum(geom)))
     xh = synth.f16_bits(r.uniform((n, h, w, ci), 0.0, 1.0))
+    xh.ravel()[::97] = np.uint16(0x0005)
     kh_ = synth.f16_bits(r.normal((k, k, ci, co), 0.0, 0.2))
     bh = synth.f16_bits(r.normal((co,), 0.0, 0.1))
     got = run_conv_f16(backend, xh, kh_, bh, s, p, ops.ACT_NONE, exact=True)
