@@ -53,6 +53,14 @@ struct RtTensor {
   size_t bytes() const { return (size_t)(n * h * w * c) * dtype_size(dtype); }
 };
 
+// Channels [lo, hi) of every pixel of the storage root at `base`: what a
+// launch reads or writes (every activation is a channel slice of a root).
+struct Region {
+  const void* base;
+  int lo, hi;
+  bool overlaps(const Region& o) const { return base == o.base && lo < o.hi && o.lo < hi; }
+};
+
 struct Launch {
   std::string kernel;
   std::string op;
@@ -63,6 +71,14 @@ struct Launch {
   // can change the tile shape after the launch list is built
   std::shared_ptr<IgemmArgs> ig;
   int esize = 0;
+  // schedule over several streams: the storage this launch touches, its
+  // stream, the launches on other streams it waits for, and whether a
+  // later launch on another stream waits for it
+  int group = -1;
+  std::vector<Region> reads, writes;
+  int stream = 0;
+  std::vector<int> waits;
+  bool record = false;
 };
 
 struct Group {
@@ -90,6 +106,12 @@ struct Runtime {
   bool capture = false;
   hipGraph_t hgraph = nullptr;
   hipGraphExec_t hexec = nullptr;
+  // independent launches (no shared storage along any path of the launch
+  // list) go to different streams, forked from and joined back into the
+  // backend's stream; a captured graph keeps them as parallel branches
+  int nstreams = 1;
+  std::vector<hipStream_t> side;  // streams 1 .. nstreams - 1
+  std::vector<hipEvent_t> evs;    // per launch (recorded ones only), then fork
   bool stats = false;
   float* stats_dev = nullptr;
   std::vector<std::string> stats_names;
@@ -99,6 +121,12 @@ struct Runtime {
     if (be && be->stream) (void)hipStreamSynchronize(be->stream);
     if (hexec) (void)hipGraphExecDestroy(hexec);
     if (hgraph) (void)hipGraphDestroy(hgraph);
+    for (hipStream_t s : side) {
+      (void)hipStreamSynchronize(s);
+      (void)hipStreamDestroy(s);
+    }
+    for (hipEvent_t e : evs)
+      if (e) (void)hipEventDestroy(e);
     for (void* p : allocs) (void)hipFree(p);
   }
 
@@ -130,6 +158,9 @@ struct Runtime {
   void emit_ew(const OpNode& op);
   void push_igemm(Launch& L, const IgemmArgs& a, int esize);
   void autotune();
+  void tag_group(const Group& gr, size_t first, int gid);
+  void plan_streams(int n);
+  void enqueue(hipStream_t st);
   void run();
 };
 
@@ -236,8 +267,11 @@ void Runtime::build(Backend* b, const GraphIR& graph, bool stats_mode) {
       if (kv.second.rank4 && !g.t[kv.first].is_init && kv.second.dtype == F32) stats_names.push_back(kv.first);
     stats_dev = (float*)dalloc(stats_names.size() * 2 * sizeof(float));
   }
-  for (auto& gr : groups) {
+  for (size_t gi = 0; gi < groups.size(); ++gi) {
+    const Group& gr = groups[gi];
+    const size_t first = launches.size();
     emit(gr);
+    tag_group(gr, first, (int)gi);
     if (!stats) continue;
     // calibration: min/max of every f32 activation an op writes
     for (int oi : gr.ops)
@@ -256,6 +290,118 @@ void Runtime::build(Backend* b, const GraphIR& graph, bool stats_mode) {
       }
   }
   if (!stats) autotune();
+  int ns = 4;
+  if (const char* env = getenv("DW_GRAPH_STREAMS")) ns = atoi(env);
+  plan_streams(stats ? 1 : std::max(1, std::min(ns, 8)));
+}
+
+// The storage a group's launches touch: every materialized activation its
+// ops read or write, as channel ranges of their roots (a superset of what
+// each launch touches, which only adds dependencies).
+void Runtime::tag_group(const Group& gr, size_t first, int gid) {
+  std::vector<Region> rd, wr;
+  auto add = [&](std::vector<Region>& v, const std::string& name) {
+    auto it = ts.find(name);
+    if (it == ts.end() || g.t[name].is_init) return;
+    const RtTensor& r = it->second;
+    if (!r.rank4 || !r.base) return;
+    v.push_back({r.base, r.abs_off, r.abs_off + (int)r.c});
+  };
+  for (int oi : gr.ops) {
+    for (auto& n : g.ops[oi].in) add(rd, n);
+    for (auto& n : g.ops[oi].out) add(wr, n);
+  }
+  for (size_t k = first; k < launches.size(); ++k) {
+    launches[k].group = gid;
+    launches[k].reads = rd;
+    launches[k].writes = wr;
+  }
+}
+
+// Stream schedule.  Launch j depends on an earlier launch i when one writes
+// storage the other reads or writes, or when both belong to the same group
+// (launches of one group run in list order).  j continues the stream whose
+// last launch is its latest dependency; otherwise (no dependency at a
+// stream's tail) it takes the stream whose last launch is oldest.  It then
+// waits for the latest dependency on every other stream.
+void Runtime::plan_streams(int n) {
+  nstreams = n;
+  for (auto& L : launches) {
+    L.stream = 0;
+    L.waits.clear();
+    L.record = false;
+  }
+  if (n <= 1) return;
+  auto depends = [](const Launch& a, const Launch& b) {
+    if (a.group == b.group) return true;
+    for (const Region& w : a.writes) {
+      for (const Region& r : b.reads) if (w.overlaps(r)) return true;
+      for (const Region& r : b.writes) if (w.overlaps(r)) return true;
+    }
+    for (const Region& r : a.reads)
+      for (const Region& w : b.writes) if (r.overlaps(w)) return true;
+    return false;
+  };
+  std::vector<int> last(n, -1);
+  for (int j = 0; j < (int)launches.size(); ++j) {
+    Launch& J = launches[j];
+    std::vector<int> dep(n, -1);
+    for (int i = 0; i < j; ++i)
+      if (depends(launches[i], J)) dep[launches[i].stream] = i;
+    int s = -1;
+    for (int k = 0; k < n; ++k)
+      if (dep[k] >= 0 && dep[k] == last[k] && (s < 0 || dep[k] > dep[s])) s = k;
+    if (s < 0) {
+      s = 0;
+      for (int k = 1; k < n; ++k)
+        if (last[k] < last[s]) s = k;
+    }
+    for (int k = 0; k < n; ++k)
+      if (k != s && dep[k] >= 0) {
+        J.waits.push_back(dep[k]);
+        launches[dep[k]].record = true;
+      }
+    J.stream = s;
+    last[s] = j;
+  }
+  // the backend's stream joins every other stream's last launch
+  for (int k = 1; k < n; ++k)
+    if (last[k] >= 0) launches[last[k]].record = true;
+  while ((int)side.size() < n - 1) {
+    hipStream_t st = nullptr;
+    DW_HIP(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+    side.push_back(st);
+  }
+  evs.assign(launches.size() + 1, nullptr);
+  for (size_t i = 0; i <= launches.size(); ++i)
+    if (i == launches.size() || launches[i].record)
+      DW_HIP(hipEventCreateWithFlags(&evs[i], hipEventDisableTiming));
+}
+
+void Runtime::enqueue(hipStream_t st) {
+  if (nstreams <= 1 || stats) {
+    for (auto& L : launches) L.fn(st);
+    return;
+  }
+  auto sk = [&](int k) { return k == 0 ? st : side[k - 1]; };
+  hipEvent_t fork = evs.back();
+  DW_HIP(hipEventRecord(fork, st));
+  std::vector<bool> forked(nstreams, false);
+  std::vector<int> last(nstreams, -1);
+  for (size_t j = 0; j < launches.size(); ++j) {
+    const Launch& L = launches[j];
+    const hipStream_t s = sk(L.stream);
+    if (L.stream != 0 && !forked[L.stream]) {
+      DW_HIP(hipStreamWaitEvent(s, fork, 0));
+      forked[L.stream] = true;
+    }
+    for (int w : L.waits) DW_HIP(hipStreamWaitEvent(s, evs[w], 0));
+    L.fn(s);
+    if (L.record) DW_HIP(hipEventRecord(evs[j], s));
+    last[L.stream] = (int)j;
+  }
+  for (int k = 1; k < nstreams; ++k)
+    if (last[k] >= 0) DW_HIP(hipStreamWaitEvent(st, evs[last[k]], 0));
 }
 
 // ---------------------------------------------------------------------------
@@ -1067,14 +1213,14 @@ void Runtime::run() {
   if (capture && !stats) {
     if (!hexec) {
       DW_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
-      for (auto& L : launches) L.fn(st);
+      enqueue(st);
       DW_HIP(hipStreamEndCapture(st, &hgraph));
       DW_HIP(hipGraphInstantiate(&hexec, hgraph, nullptr, nullptr, 0));
     }
     DW_HIP(hipGraphLaunch(hexec, st));
     return;
   }
-  for (auto& L : launches) L.fn(st);
+  enqueue(st);
 }
 
 }  // namespace dw

@@ -151,6 +151,31 @@ def test_int8_graph_capture_replays_match_eager(backend, int8_small):
         backend.synchronize()
 
 
+def test_int8_graph_streams_match_one_stream(backend, int8_small, monkeypatch):
+    # Independent launches run on several streams (parallel branches of the
+    # captured graph); the results must equal the one-stream schedule's, on
+    # every replay, eagerly and captured.
+    g, info = int8_small
+    x = yolo.input_images(2, 96)
+    monkeypatch.setenv("DW_GRAPH_STREAMS", "1")
+    rt1 = HipGraphRuntime(g, backend)
+    monkeypatch.setenv("DW_GRAPH_STREAMS", "4")
+    rt4 = HipGraphRuntime(g, backend)
+    rt1.set_input_f32(info["input"], x)
+    rt1.run()
+    ref = gpu_outputs(rt1, info)
+    for capture in (False, True):
+        rt4.enable_capture(capture)
+        for i in range(3):
+            rt4.set_input_f32(info["input"], x if i % 2 == 0 else np.zeros_like(x))
+            rt4.run()
+            outs = gpu_outputs(rt4, info)
+            if i % 2 == 0:
+                for a, b in zip(outs, ref):
+                    np.testing.assert_array_equal(a, b)
+            backend.synchronize()
+
+
 def test_run_unbatched_and_io(backend, int8_small, monkeypatch):
     g, info = int8_small
     rt = HipGraphRuntime(g, backend)
