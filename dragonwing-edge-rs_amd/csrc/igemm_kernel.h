@@ -260,6 +260,69 @@ __device__ __forceinline__ void pixel_setup(const IgemmArgs& a, int p0, int lane
   }
 }
 
+// Epilogue of a workgroup's tile: this lane holds channels c0 + cb*16 + cq
+// .. +3 of pixel p0 + pb*16 + (lane & 15) for every block (cb, pb).  The
+// specialised int8 epilogues (EPV) take bias' from the accumulators' start
+// values and the multipliers and table from LDS.
+template <int ESZ, int BC, int PB, int EPV, typename AccT>
+__device__ __forceinline__ void igemm_store(const IgemmArgs& a, const EpiLds& ep, AccT (&acc)[BC / 16][PB], int c0,
+                                            int p0, int lane, const uint8_t* s_ms, const uint8_t* s_lut) {
+  constexpr int CB = BC / 16;
+  constexpr bool FAST = EPV != EPV_GENERIC;
+  const int cq = 4 * (lane >> 4);
+  if constexpr (FAST) {
+    const bool full = c0 + BC <= a.cout;
+    const int qbase = 0x4B400000 - a.y_zp;
+    const float qlo = 12582912.0f - (float)a.y_zp, qhi = qlo + 255.0f;
+    const __attribute__((address_space(3))) uint8_t* lut3 = (const __attribute__((address_space(3))) uint8_t*)s_lut;
+    float4 msr[CB];
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) msr[cb] = *reinterpret_cast<const float4*>(s_ms + 4 * (cb * 16 + cq));
+#pragma unroll
+    for (int pb = 0; pb < PB; ++pb) {
+      const int p = p0 + pb * 16 + (lane & 15);
+      if (p >= a.m) continue;
+      uint8_t* yrow = (uint8_t*)a.y + (size_t)p * a.y_pix_stride + a.y_c_off + c0 + cq;
+      uint32_t rres[CB];
+      if constexpr (EPV == EPV_QU8_LUT_RES) {
+        const uint8_t* rrow = (const uint8_t*)a.res + (size_t)p * a.r_pix_stride + a.r_c_off + c0 + cq;
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb)
+          rres[cb] = (full || c0 + cb * 16 + cq < a.cout) ? *reinterpret_cast<const uint32_t*>(rrow + cb * 16) : 0u;
+      }
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) {
+        if (!full && c0 + cb * 16 + cq >= a.cout) continue;
+        const float ms4[4] = {msr[cb].x, msr[cb].y, msr[cb].z, msr[cb].w};
+        uint32_t out = 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int qb = requant_bits(acc[cb][pb][r], ms4[r], qlo, qhi);
+          int qi;
+          if constexpr (EPV != EPV_QU8)
+            qi = lut3[(uint32_t)qb - (uint32_t)qbase];
+          else
+            qi = qb - qbase;
+          if constexpr (EPV == EPV_QU8_LUT_RES) qi = qadd_u8(qi, (rres[cb] >> (8 * r)) & 0xff, a);
+          out |= (uint32_t)qi << (8 * r);
+        }
+        *reinterpret_cast<uint32_t*>(yrow + cb * 16) = out;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+      const int ch = c0 + cb * 16 + cq;
+      if (ch >= a.cout) continue;
+#pragma unroll
+      for (int pb = 0; pb < PB; ++pb) {
+        const int p = p0 + pb * 16 + (lane & 15);
+        if (p < a.m) epilogue4<ESZ>(a, ep, acc[cb][pb], ch, ch - c0, p);
+      }
+    }
+  }
+}
+
 // SK: K fits in the start-up loads (ksteps <= PD - 1, and in one weight
 // chunk), so the k-loop issues no loads.
 template <int ESZ, int BC, int PB, int PD, int EPV, bool SK>
@@ -484,59 +547,7 @@ __global__ __launch_bounds__(256) void igemm_kernel(const IgemmArgs a) {
 #undef DW_LDS_FENCE
 #undef DW_LOAD_B
 
-  // ---- epilogue: lane holds channels c0 + cb*16 + cq .. +3 of pixel
-  // p0 + pb*16 + (lane & 15) for every block
-  if constexpr (FAST) {
-    const bool full = c0 + BC <= a.cout;
-    const int qbase = 0x4B400000 - a.y_zp;
-    const float qlo = 12582912.0f - (float)a.y_zp, qhi = qlo + 255.0f;
-    const __attribute__((address_space(3))) uint8_t* lut3 = (const __attribute__((address_space(3))) uint8_t*)s_lut;
-    float4 msr[CB];
-#pragma unroll
-    for (int cb = 0; cb < CB; ++cb) msr[cb] = *reinterpret_cast<const float4*>(s_ms + 4 * (cb * 16 + cq));
-#pragma unroll
-    for (int pb = 0; pb < PB; ++pb) {
-      const int p = p0 + pb * 16 + (lane & 15);
-      if (p >= a.m) continue;
-      uint8_t* yrow = (uint8_t*)a.y + (size_t)p * a.y_pix_stride + a.y_c_off + c0 + cq;
-      uint32_t rres[CB];
-      if constexpr (EPV == EPV_QU8_LUT_RES) {
-        const uint8_t* rrow = (const uint8_t*)a.res + (size_t)p * a.r_pix_stride + a.r_c_off + c0 + cq;
-#pragma unroll
-        for (int cb = 0; cb < CB; ++cb)
-          rres[cb] = (full || c0 + cb * 16 + cq < a.cout) ? *reinterpret_cast<const uint32_t*>(rrow + cb * 16) : 0u;
-      }
-#pragma unroll
-      for (int cb = 0; cb < CB; ++cb) {
-        if (!full && c0 + cb * 16 + cq >= a.cout) continue;
-        const float ms4[4] = {msr[cb].x, msr[cb].y, msr[cb].z, msr[cb].w};
-        uint32_t out = 0;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int qb = requant_bits(acc[cb][pb][r], ms4[r], qlo, qhi);
-          int qi;
-          if constexpr (EPV != EPV_QU8)
-            qi = lut3[(uint32_t)qb - (uint32_t)qbase];
-          else
-            qi = qb - qbase;
-          if constexpr (EPV == EPV_QU8_LUT_RES) qi = qadd_u8(qi, (rres[cb] >> (8 * r)) & 0xff, a);
-          out |= (uint32_t)qi << (8 * r);
-        }
-        *reinterpret_cast<uint32_t*>(yrow + cb * 16) = out;
-      }
-    }
-  } else {
-#pragma unroll
-    for (int cb = 0; cb < CB; ++cb) {
-      const int ch = c0 + cb * 16 + cq;
-      if (ch >= a.cout) continue;
-#pragma unroll
-      for (int pb = 0; pb < PB; ++pb) {
-        const int p = p0 + pb * 16 + (lane & 15);
-        if (p < a.m) epilogue4<ESZ>(a, ep, acc[cb][pb], ch, ch - c0, p);
-      }
-    }
-  }
+  igemm_store<ESZ, BC, PB, EPV>(a, ep, acc, c0, p0, lane, s_ms, s_lut);
 }
 
 // Launch of the instantiation for a tile shape (the caller checked that it

@@ -1,8 +1,10 @@
 // Implicit-GEMM convolution on CDNA4 matrix cores: tile selection, launch
-// dispatch and weight packing.  The kernels are igemm_kernel.h and, for
-// small K, the persistent igemm_sk.h; their instantiations live in the
-// k_igemm_*.hip files so that they compile in parallel.
+// dispatch and weight packing.  The kernels are igemm_kernel.h, the
+// persistent igemm_sk.h for small K and the streamed-weight igemm_stream.h
+// for long K; their instantiations live in the k_igemm_*.hip files so that
+// they compile in parallel.
 #include "igemm_sk.h"
+#include "igemm_stream.h"
 
 #include <stdio.h>
 #include <stdlib.h>
@@ -83,6 +85,18 @@ TileCfg make_sk_tile(const IgemmArgs& a, int bc, int pb, int tpw) {
   return t;
 }
 
+// The streamed-weight kernel (tpw = -1): two or more k-steps, and its
+// weight ring and k-slice table fit LDS.
+bool st_ok(const IgemmArgs& a, int bc, int pb) {
+  return tile_ok(a, bc, pb) && a.ksteps >= 2 && ig::st_lds_bytes(bc, a.ksteps, ring_depth(pb)) <= 160 * 1024;
+}
+
+TileCfg make_st_tile(const IgemmArgs& a, int bc, int pb) {
+  TileCfg t = make_tile(a, bc, pb);
+  t.tpw = -1;
+  return t;
+}
+
 // Tile shape for a problem: an override from DW_IGEMM_TILE (tests and
 // tuning runs), an explicit choice (a.tile_bc / a.tile_pb, set by the graph
 // runtime's tuner), else the widest channel tile and the widest pixel tile
@@ -94,10 +108,12 @@ TileCfg pick(const IgemmArgs& a) {
     int v0 = 0, v1 = 0, v2 = 0;
     const int nv = sscanf(env, "%d,%d,%d", &v0, &v1, &v2);
     if (nv == 3 && sk_ok(a, v0, v1, v2)) return make_sk_tile(a, v0, v1, v2);
+    if (nv == 3 && v2 < 0 && st_ok(a, v0, v1)) return make_st_tile(a, v0, v1);
     if (nv >= 2 && tile_ok(a, v0, v1)) return make_tile(a, v0, v1);
     if (nv == 1 && tile_ok(a, channel_tile(a.cout), v0)) return make_tile(a, channel_tile(a.cout), v0);
   }
   if (a.tile_bc && sk_ok(a, a.tile_bc, a.tile_pb, a.tile_tpw)) return make_sk_tile(a, a.tile_bc, a.tile_pb, a.tile_tpw);
+  if (a.tile_bc && a.tile_tpw < 0 && st_ok(a, a.tile_bc, a.tile_pb)) return make_st_tile(a, a.tile_bc, a.tile_pb);
   if (a.tile_bc && tile_ok(a, a.tile_bc, a.tile_pb)) return make_tile(a, a.tile_bc, a.tile_pb);
   const int bc = channel_tile(a.cout);
   const int ctiles = a.cout_pad / bc;
@@ -129,6 +145,12 @@ int igemm_candidates(const IgemmArgs& a, int* bc, int* pb, int* tpw, int max) {
         tpw[n] = 0;
         ++n;
       }
+      if (n < max && st_ok(a, b, p)) {
+        bc[n] = b;
+        pb[n] = p;
+        tpw[n] = -1;
+        ++n;
+      }
       // persistent variants that still leave a workgroup for every CU
       const long tiles = (long)((a.m + 64 * p - 1) / (64 * p)) * (a.cout_pad / std::max(b, 1));
       for (int t : {2, 4, 8})
@@ -147,6 +169,8 @@ const char* igemm_tile_name(const IgemmArgs& a, int esize) {
   const TileCfg t = pick(a);
   if (t.tpw > 0)
     snprintf(buf, sizeof buf, "igemm_%s_c%d_p%d_t%d", esize == 1 ? "i8" : "f16", t.bc, 64 * t.pb, t.tpw);
+  else if (t.tpw < 0)
+    snprintf(buf, sizeof buf, "igemm_%s_c%d_p%d_st", esize == 1 ? "i8" : "f16", t.bc, 64 * t.pb);
   else
     snprintf(buf, sizeof buf, "igemm_%s_c%d_p%d", esize == 1 ? "i8" : "f16", t.bc, 64 * t.pb);
   return buf;
@@ -162,7 +186,9 @@ void launch_igemm(hipStream_t st, const IgemmArgs& a_in, int esize) {
   const long long xb = (long long)a.n * a.h * a.w * a.x_pix_stride * esize;
   if (xb >= (1ll << 31)) fail(-2, "igemm: input view larger than 2 GB");
   a.x_bytes = (int)xb;
-  const size_t lds = t.tpw > 0 ? ig::sk_lds_bytes(t.bc, a.ksteps) : ig::lds_bytes(t, a.ksteps);
+  const size_t lds = t.tpw > 0   ? ig::sk_lds_bytes(t.bc, a.ksteps)
+                     : t.tpw < 0 ? ig::st_lds_bytes(t.bc, a.ksteps, t.pd)
+                                 : ig::lds_bytes(t, a.ksteps);
   if (lds > 160 * 1024) fail(-2, "igemm: k-slice table does not fit LDS");
   if ((long long)a.ho * a.wo >= (1ll << 23)) fail(-2, "igemm: more than 2^23 output pixels per image");
   if ((long long)a.ksteps * a.cout_pad * 64 >= (1ll << 32)) fail(-2, "igemm: packed weights larger than 4 GB");
@@ -184,10 +210,12 @@ void launch_igemm(hipStream_t st, const IgemmArgs& a_in, int esize) {
     const bool ab = epv == EPV_GENERIC || epv == EPV_QU8;
     if (t.tpw > 0)
       ok = ab ? igemm_launch_sk_i8_a(st, a, t, epv) : igemm_launch_sk_i8_b(st, a, t, epv);
+    else if (t.tpw < 0)
+      ok = ab ? igemm_launch_st_i8_a(st, a, t, epv) : igemm_launch_st_i8_b(st, a, t, epv);
     else
       ok = ab ? igemm_launch_i8_a(st, a, t, epv) : igemm_launch_i8_b(st, a, t, epv);
   } else {
-    ok = t.tpw > 0 ? igemm_launch_sk_f16(st, a, t) : igemm_launch_f16(st, a, t);
+    ok = t.tpw > 0 ? igemm_launch_sk_f16(st, a, t) : (t.tpw < 0 ? igemm_launch_st_f16(st, a, t) : igemm_launch_f16(st, a, t));
   }
   if (!ok) fail(-2, "igemm: no kernel for tile");
   DW_HIP(hipGetLastError());

@@ -101,6 +101,23 @@ def test_int8_graph_persistent_tiles_bit_exact(backend, int8_small, monkeypatch,
         np.testing.assert_array_equal(gv, ref[o], err_msg=f"{o} tile {tile}")
 
 
+@pytest.mark.parametrize("tile", ["128,1,-1", "64,2,-1", "32,4,-1"])
+def test_int8_graph_streamed_tiles_bit_exact(backend, int8_small, monkeypatch, tile):
+    # Every layer with two or more k-steps on the streamed-weight kernel
+    # (all four int8 epilogues: requantize, table, table + residual).
+    g, info = int8_small
+    monkeypatch.setenv("DW_IGEMM_TILE", tile)
+    x = yolo.input_images(2, 96)
+    rt = HipGraphRuntime(g, backend)
+    assert any(L["kernel"].endswith("_st") for L in rt.launches())
+    rt.set_input_f32(info["input"], x)
+    rt.run()
+    got = gpu_outputs(rt, info)
+    ref = oracle_run(g, {info["input"]: synth.f16_bits(x)})
+    for o, gv in zip(info["outputs"], got):
+        np.testing.assert_array_equal(gv, ref[o], err_msg=f"{o} tile {tile}")
+
+
 @pytest.mark.parametrize("plant_subnormal_weight", [False, True])
 @pytest.mark.parametrize("stride", [1, 2])
 def test_depthwise_graph_bit_exact(backend, plant_subnormal_weight, stride):

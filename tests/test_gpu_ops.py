@@ -232,6 +232,24 @@ def test_qlinearconv_every_tile_bit_exact(backend, geom, monkeypatch):
         np.testing.assert_array_equal(run_qconv(backend, c, s, p), ref, err_msg=f"tile {bc},{pb}")
 
 
+@pytest.mark.parametrize("geom", [(2, 9, 11, 64, 256, 3, 2, 1), (1, 13, 7, 128, 80, 3, 1, 1),
+                                  (2, 10, 10, 48, 96, 1, 1, 0), (1, 6, 6, 256, 128, 3, 1, 1),
+                                  (2, 5, 7, 272, 48, 3, 1, 1)])
+def test_qlinearconv_streamed_tiles_bit_exact(backend, geom, monkeypatch):
+    # The streamed-weight kernel over every tile: K of 2 to 37 k-steps, so
+    # the weight ring wraps several times and ends part-way through it.
+    n, h, w, ci, co, k, s, p = geom
+    r = synth.Rng(synth.seed_for(900 + sum(geom)))
+    c = dict(x=r.integers((n, h, w, ci), 0, 255).astype(np.uint8),
+             w=r.integers((k, k, ci, co), -127, 127).astype(np.int8),
+             bias=r.integers((co,), -4096, 4096).astype(np.int32),
+             w_scales=r.log_uniform((co,), 1e-3, 1e-2), x_scale=0.02, x_zp=126, y_scale=0.05, y_zp=133)
+    ref = oracle_qconv(c, s, p)
+    for bc, pb in igemm_tiles(co):
+        monkeypatch.setenv("DW_IGEMM_TILE", f"{bc},{pb},-1")
+        np.testing.assert_array_equal(run_qconv(backend, c, s, p), ref, err_msg=f"tile {bc},{pb},-1")
+
+
 def test_qlinearconv_golden_fixtures(backend):
     cases = json.loads((GOLDEN / "qlinear_cases.json").read_text())["qlinearconv"]
     for g in cases:
@@ -398,6 +416,24 @@ def test_conv_f16_persistent_tiles_identical(backend, monkeypatch):
         monkeypatch.setenv("DW_IGEMM_TILE", f"{bc},{pb},{t}")
         got = run_conv_f16(backend, xh, kh_, bh, s, p, ops.ACT_SILU, exact=False)
         np.testing.assert_array_equal(got, first, err_msg=f"tile {bc},{pb},{t}")
+
+
+def test_conv_f16_streamed_tiles_identical(backend, monkeypatch):
+    # 3x3 over 64 f16 channels: 18 k-steps.  The streamed-weight kernel sums
+    # the same k-steps in the same order as the staged one.
+    n, h, w, ci, co, k, s, p = 2, 11, 9, 64, 96, 3, 1, 1
+    r = synth.Rng(synth.seed_for(602))
+    xh = synth.f16_bits(r.normal((n, h, w, ci), 0.0, 1.0))
+    kh_ = synth.f16_bits(r.normal((k, k, ci, co), 0.0, (1.0 / (k * k * ci)) ** 0.5))
+    bh = synth.f16_bits(r.normal((co,), 0.0, 0.1))
+    ref = oracle_conv_f16(xh, kh_, bh, s, p, ops.ACT_SILU)
+    monkeypatch.setenv("DW_IGEMM_TILE", "32,4")
+    first = run_conv_f16(backend, xh, kh_, bh, s, p, ops.ACT_SILU, exact=False)
+    assert rel_err(f16v(first), f16v(ref)) <= 1e-2
+    for bc, pb in igemm_tiles(co):
+        monkeypatch.setenv("DW_IGEMM_TILE", f"{bc},{pb},-1")
+        got = run_conv_f16(backend, xh, kh_, bh, s, p, ops.ACT_SILU, exact=False)
+        np.testing.assert_array_equal(got, first, err_msg=f"tile {bc},{pb},-1")
 
 
 @pytest.mark.parametrize("geom", [(2, 32, 32, 3, 16, 3, 2, 1), (1, 12, 12, 64, 64, 1, 1, 0),
