@@ -38,7 +38,11 @@ __device__ __forceinline__ float decode_x(const DirectArgs& a, const uint4& u, i
   if constexpr (IN_KIND == 2 && NOSUB) {
     const uint32_t wd = e < 4 ? u.x : (e < 8 ? u.y : (e < 12 ? u.z : u.w));
     const int q = (int)((wd >> (8 * (e & 3))) & 0xff);
-    return h2f_ieee(f2h((float)(q - a.in_zp) * a.in_scale));
+    float v = h2f_ieee(f2h((float)(q - a.in_zp) * a.in_scale));
+    // widened once here: the FMAs then take an f32 operand (v_fma_f32)
+    // rather than each widening the f16 value again (v_fma_mix_f32)
+    asm volatile("" : "+v"(v));
+    return v;
   } else {
     return dx::decode_elem<IN_KIND>(a, u, e);
   }
