@@ -12,10 +12,11 @@
 // read it (one k-step ahead of its MFMAs).  The weight traffic overlaps the
 // MFMAs and a workgroup starts after its first two k-steps have landed.
 //
-// Every load goes to registers (no direct-to-LDS loads in the k-loop), so
-// the compiler's own waits for loads are exact: it counts loads of one kind
-// completing in order, which it cannot assume once direct-to-LDS loads are
-// in flight (it then waits for all of them).  LDS slot reuse: k-step
+// Every load goes to registers (no direct-to-LDS loads anywhere in the
+// kernel), so the compiler's own waits for loads are exact: it counts loads
+// of one kind completing in order, which it cannot assume once
+// direct-to-LDS loads are in flight (it then waits for all of them), and
+// the start-up waits only for k-steps 0 and 1 and the first im2col k-step.  LDS slot reuse: k-step
 // s + 2's slot last held k-step s - 2, whose fragments every wave read
 // before the barrier of k-step s.
 #pragma once
@@ -95,21 +96,37 @@ __global__ __launch_bounds__(256) void igemm_stream_kernel(const IgemmArgs a) {
   }
   __syncthreads();  // the k-slice table is complete
 
-  // epilogue data, straight to LDS (landed by the start-up wait below)
-  if (a.epi == EPI_QU8) {
-    if (wave == 0 && a.bias_i && lane < nvalid / 4)
-      __builtin_amdgcn_global_load_lds((const void*)(a.bias_i + c0 + lane * 4),
-                                       (__attribute__((address_space(3))) void*)s_bias, 16, 0, 0);
-    if (wave == 1 && lane < nvalid / 4)
-      __builtin_amdgcn_global_load_lds((const void*)(a.mscale + c0 + lane * 4),
-                                       (__attribute__((address_space(3))) void*)s_ms, 16, 0, 0);
-    if (wave == 2 && a.lut && lane < 16)
-      __builtin_amdgcn_global_load_lds((const void*)(a.lut + lane * 16),
-                                       (__attribute__((address_space(3))) void*)s_lut, 16, 0, 0);
-  } else if (a.epi == EPI_F16 && a.bias_h) {
-    if (wave == 0 && lane < nvalid / 2)
-      __builtin_amdgcn_global_load_lds((const void*)(a.bias_h + c0 + lane * 2),
-                                       (__attribute__((address_space(3))) void*)s_bias, 4, 0, 0);
+  // epilogue data, through registers (written to LDS below, after the
+  // start-up loads are issued): no direct-to-LDS load is in flight anywhere
+  // in this kernel, so every wait the compiler places is exact
+  // (one load site, so no wave waits for one load before issuing the next)
+  const uint8_t* epi_src = nullptr;
+  uint8_t* epi_dst = nullptr;
+  if constexpr (ESZ == 1) {
+    if (a.epi == EPI_QU8) {
+      if (wave == 0 && a.bias_i && lane < nvalid / 4) {
+        epi_src = reinterpret_cast<const uint8_t*>(a.bias_i + c0 + lane * 4);
+        epi_dst = s_bias + lane * 16;
+      } else if (wave == 1 && lane < nvalid / 4) {
+        epi_src = reinterpret_cast<const uint8_t*>(a.mscale + c0 + lane * 4);
+        epi_dst = s_ms + lane * 16;
+      } else if (wave == 2 && a.lut && lane < 16) {
+        epi_src = a.lut + lane * 16;
+        epi_dst = s_lut + lane * 16;
+      }
+    }
+  } else {
+    if (a.epi == EPI_F16 && a.bias_h && wave == 0 && lane < nvalid / 2) {
+      epi_src = reinterpret_cast<const uint8_t*>(a.bias_h + c0 + lane * 2);
+      epi_dst = s_bias + lane * 4;
+    }
+  }
+  uint4 epi_v = make_uint4(0, 0, 0, 0);
+  if (epi_src) {
+    if constexpr (ESZ == 1)
+      epi_v = *reinterpret_cast<const uint4*>(epi_src);
+    else
+      epi_v.x = *reinterpret_cast<const uint32_t*>(epi_src);
   }
 
   // ---- weights: this wave's fragments cb = wave + 4 i (i < NWV) of k-step
@@ -164,12 +181,18 @@ __global__ __launch_bounds__(256) void igemm_stream_kernel(const IgemmArgs a) {
 #pragma unroll
   for (int r = 0; r < PD - 1; ++r) DW_LOAD_B(my_tab[r * 4], bq[r], bkey[r]);
   int2 tnext = my_tab[(PD - 1) * 4];
+  if (epi_dst) {
+    if constexpr (ESZ == 1)
+      *reinterpret_cast<uint4*>(epi_dst) = epi_v;
+    else
+      *reinterpret_cast<uint32_t*>(epi_dst) = epi_v.x;
+  }
   DW_STORE_W(0, 0);
   DW_STORE_W(1, 1);
-  // the epilogue data's direct loads have landed (and with them everything
-  // issued so far), this wave's weight writes too; then everyone's
+  // this wave's LDS writes (epilogue data, k-steps 0 and 1) are done; then
+  // everyone's
   asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 
