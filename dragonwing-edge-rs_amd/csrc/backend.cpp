@@ -207,7 +207,9 @@ int dw_hip_backend_create(int device, dw_hip_backend** out) {
   API_END
 }
 
-void dw_hip_backend_destroy(dw_hip_backend* be) { delete reinterpret_cast<Backend*>(be); }
+void dw_hip_backend_destroy(dw_hip_backend* be) {
+  if (be) dw::release(reinterpret_cast<Backend*>(be));
+}
 
 const char* dw_hip_backend_name(const dw_hip_backend* be) {
   (void)be;
@@ -225,15 +227,18 @@ int dw_hip_alloc(dw_hip_backend* be, size_t len_bytes, int kind, dw_hip_buffer**
     dw::fail(DW_ERR_BACKEND, "alloc of " + std::to_string(len_bytes) + " bytes failed: " +
                                  hipGetErrorString(e));
   *out = new dw_hip_buffer{b, p, len_bytes};
+  dw::hold(b);
   API_END
 }
 
 void dw_hip_buffer_free(dw_hip_buffer* buf) {
   if (!buf) return;
-  (void)hipSetDevice(buf->be->device);
-  (void)hipStreamSynchronize(buf->be->stream);
+  Backend* b = buf->be;
+  (void)hipSetDevice(b->device);
+  (void)hipStreamSynchronize(b->stream);
   (void)hipFree(buf->ptr);
   delete buf;
+  dw::release(b);
 }
 
 size_t dw_hip_buffer_len_bytes(const dw_hip_buffer* buf) { return buf ? buf->len : 0; }

@@ -3,6 +3,8 @@
 
 #include "dw_common.h"
 
+#include <atomic>
+
 namespace dw {
 
 void set_last_error(const std::string& m);
@@ -21,9 +23,20 @@ struct Backend {
   hipStream_t stream = nullptr;
   Ws ws[kWsSlots];
 
+  // Holders: the handle itself, every buffer and every graph runtime made
+  // on it (as the reference's Arc<Backend>): destroying the handle while
+  // they live only drops its hold, and the last holder frees the device
+  // state.
+  std::atomic<int> holds{1};
+
   void* workspace(int slot, size_t bytes);
   void upload_async(void* dst, const void* src, size_t bytes);
   ~Backend();
 };
+
+inline void hold(Backend* b) { b->holds.fetch_add(1, std::memory_order_relaxed); }
+inline void release(Backend* b) {
+  if (b->holds.fetch_sub(1, std::memory_order_acq_rel) == 1) delete b;
+}
 
 }  // namespace dw

@@ -3,6 +3,7 @@
 // persistent igemm_sk.h for small K and the streamed-weight igemm_stream.h
 // for long K; their instantiations live in the k_igemm_*.hip files so that
 // they compile in parallel.
+#include "igemm_rows.h"
 #include "igemm_sk.h"
 #include "igemm_stream.h"
 
@@ -97,6 +98,26 @@ TileCfg make_st_tile(const IgemmArgs& a, int bc, int pb) {
   return t;
 }
 
+// The row-tile kernel (tpw = -2): int8 3x3, stride 1, padding 1 (same-size
+// output), whole rows of 320 output pixels per workgroup (W divides 320, and
+// the row count per tile divides H), channel tiles up to 96 (register
+// budget), the input tile within the start-up loads and LDS.
+bool rows_ok(const IgemmArgs& a, int bc) {
+  if (a.epi == EPI_F16 || a.kh != 3 || a.kw != 3 || a.sh != 1 || a.sw != 1 || a.pt != 1 || a.pl != 1) return false;
+  if (a.ho != a.h || a.wo != a.w || a.cin % 16 != 0 || a.w <= 0 || ig::kRowsPix % a.w != 0) return false;
+  const int r = ig::kRowsPix / a.w;
+  if (a.h % r != 0 || bc > 96 || !tile_ok(a, bc, 4)) return false;
+  if ((r + 2) * (a.w + 2) * (a.cin / 16) > ig::kRowsFill * 256) return false;
+  return ig::rows_lds_bytes(bc, a.ksteps, a.w, a.cin) <= 160 * 1024;
+}
+
+TileCfg make_rows_tile(const IgemmArgs& a, int bc) {
+  TileCfg t = make_tile(a, bc, 4);
+  t.kchunk = a.ksteps;
+  t.tpw = -2;
+  return t;
+}
+
 // Tile shape for a problem: an override from DW_IGEMM_TILE (tests and
 // tuning runs), an explicit choice (a.tile_bc / a.tile_pb, set by the graph
 // runtime's tuner), else the widest channel tile and the widest pixel tile
@@ -108,12 +129,14 @@ TileCfg pick(const IgemmArgs& a) {
     int v0 = 0, v1 = 0, v2 = 0;
     const int nv = sscanf(env, "%d,%d,%d", &v0, &v1, &v2);
     if (nv == 3 && sk_ok(a, v0, v1, v2)) return make_sk_tile(a, v0, v1, v2);
-    if (nv == 3 && v2 < 0 && st_ok(a, v0, v1)) return make_st_tile(a, v0, v1);
+    if (nv == 3 && v2 == -1 && st_ok(a, v0, v1)) return make_st_tile(a, v0, v1);
+    if (nv == 3 && v2 == -2 && rows_ok(a, v0)) return make_rows_tile(a, v0);
     if (nv >= 2 && tile_ok(a, v0, v1)) return make_tile(a, v0, v1);
     if (nv == 1 && tile_ok(a, channel_tile(a.cout), v0)) return make_tile(a, channel_tile(a.cout), v0);
   }
   if (a.tile_bc && sk_ok(a, a.tile_bc, a.tile_pb, a.tile_tpw)) return make_sk_tile(a, a.tile_bc, a.tile_pb, a.tile_tpw);
-  if (a.tile_bc && a.tile_tpw < 0 && st_ok(a, a.tile_bc, a.tile_pb)) return make_st_tile(a, a.tile_bc, a.tile_pb);
+  if (a.tile_bc && a.tile_tpw == -1 && st_ok(a, a.tile_bc, a.tile_pb)) return make_st_tile(a, a.tile_bc, a.tile_pb);
+  if (a.tile_bc && a.tile_tpw == -2 && rows_ok(a, a.tile_bc)) return make_rows_tile(a, a.tile_bc);
   if (a.tile_bc && tile_ok(a, a.tile_bc, a.tile_pb)) return make_tile(a, a.tile_bc, a.tile_pb);
   const int bc = channel_tile(a.cout);
   const int ctiles = a.cout_pad / bc;
@@ -151,6 +174,12 @@ int igemm_candidates(const IgemmArgs& a, int* bc, int* pb, int* tpw, int max) {
         tpw[n] = -1;
         ++n;
       }
+      if (n < max && p == 4 && rows_ok(a, b)) {
+        bc[n] = b;
+        pb[n] = p;
+        tpw[n] = -2;
+        ++n;
+      }
       // persistent variants that still leave a workgroup for every CU
       const long tiles = (long)((a.m + 64 * p - 1) / (64 * p)) * (a.cout_pad / std::max(b, 1));
       for (int t : {2, 4, 8})
@@ -169,8 +198,10 @@ const char* igemm_tile_name(const IgemmArgs& a, int esize) {
   const TileCfg t = pick(a);
   if (t.tpw > 0)
     snprintf(buf, sizeof buf, "igemm_%s_c%d_p%d_t%d", esize == 1 ? "i8" : "f16", t.bc, 64 * t.pb, t.tpw);
-  else if (t.tpw < 0)
+  else if (t.tpw == -1)
     snprintf(buf, sizeof buf, "igemm_%s_c%d_p%d_st", esize == 1 ? "i8" : "f16", t.bc, 64 * t.pb);
+  else if (t.tpw == -2)
+    snprintf(buf, sizeof buf, "igemm_%s_c%d_rows", esize == 1 ? "i8" : "f16", t.bc);
   else
     snprintf(buf, sizeof buf, "igemm_%s_c%d_p%d", esize == 1 ? "i8" : "f16", t.bc, 64 * t.pb);
   return buf;
@@ -186,9 +217,10 @@ void launch_igemm(hipStream_t st, const IgemmArgs& a_in, int esize) {
   const long long xb = (long long)a.n * a.h * a.w * a.x_pix_stride * esize;
   if (xb >= (1ll << 31)) fail(-2, "igemm: input view larger than 2 GB");
   a.x_bytes = (int)xb;
-  const size_t lds = t.tpw > 0   ? ig::sk_lds_bytes(t.bc, a.ksteps)
-                     : t.tpw < 0 ? ig::st_lds_bytes(t.bc, a.ksteps, t.pd)
-                                 : ig::lds_bytes(t, a.ksteps);
+  const size_t lds = t.tpw > 0     ? ig::sk_lds_bytes(t.bc, a.ksteps)
+                     : t.tpw == -1 ? ig::st_lds_bytes(t.bc, a.ksteps, t.pd)
+                     : t.tpw == -2 ? ig::rows_lds_bytes(t.bc, a.ksteps, a.w, a.cin)
+                                   : ig::lds_bytes(t, a.ksteps);
   if (lds > 160 * 1024) fail(-2, "igemm: k-slice table does not fit LDS");
   if ((long long)a.ho * a.wo >= (1ll << 23)) fail(-2, "igemm: more than 2^23 output pixels per image");
   if ((long long)a.ksteps * a.cout_pad * 64 >= (1ll << 32)) fail(-2, "igemm: packed weights larger than 4 GB");
@@ -210,12 +242,14 @@ void launch_igemm(hipStream_t st, const IgemmArgs& a_in, int esize) {
     const bool ab = epv == EPV_GENERIC || epv == EPV_QU8;
     if (t.tpw > 0)
       ok = ab ? igemm_launch_sk_i8_a(st, a, t, epv) : igemm_launch_sk_i8_b(st, a, t, epv);
-    else if (t.tpw < 0)
+    else if (t.tpw == -1)
       ok = ab ? igemm_launch_st_i8_a(st, a, t, epv) : igemm_launch_st_i8_b(st, a, t, epv);
+    else if (t.tpw == -2)
+      ok = ab ? igemm_launch_rows_i8_a(st, a, t, epv) : igemm_launch_rows_i8_b(st, a, t, epv);
     else
       ok = ab ? igemm_launch_i8_a(st, a, t, epv) : igemm_launch_i8_b(st, a, t, epv);
   } else {
-    ok = t.tpw > 0 ? igemm_launch_sk_f16(st, a, t) : (t.tpw < 0 ? igemm_launch_st_f16(st, a, t) : igemm_launch_f16(st, a, t));
+    ok = t.tpw > 0 ? igemm_launch_sk_f16(st, a, t) : (t.tpw == -1 ? igemm_launch_st_f16(st, a, t) : igemm_launch_f16(st, a, t));
   }
   if (!ok) fail(-2, "igemm: no kernel for tile");
   DW_HIP(hipGetLastError());

@@ -1268,17 +1268,24 @@ int dw_hip_graph_runtime_create(dw_hip_backend* be, const dw_graph* g, dw_hip_gr
   if (!g || !out) dw::fail(DW_ERR_INVALID, "null argument");
   dw::Backend* b = Bk(be);
   auto* rt = new dw_hip_graph_runtime();
+  dw::hold(b);  // released with the runtime
   try {
     rt->rt.build(b, g->g, false);
   } catch (...) {
     delete rt;
+    dw::release(b);
     throw;
   }
   *out = rt;
   API_END
 }
 
-void dw_hip_graph_runtime_destroy(dw_hip_graph_runtime* rt) { delete rt; }
+void dw_hip_graph_runtime_destroy(dw_hip_graph_runtime* rt) {
+  if (!rt) return;
+  dw::Backend* b = rt->rt.be;
+  delete rt;
+  if (b) dw::release(b);
+}
 
 int dw_hip_graph_set_input_bytes(dw_hip_graph_runtime* rth, const char* name, const void* data, size_t len) {
   API_BEGIN

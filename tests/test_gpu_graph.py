@@ -118,6 +118,23 @@ def test_int8_graph_streamed_tiles_bit_exact(backend, int8_small, monkeypatch, t
         np.testing.assert_array_equal(gv, ref[o], err_msg=f"{o} tile {tile}")
 
 
+def test_int8_graph_row_tiles_bit_exact(backend, monkeypatch):
+    # 320x320 input: the 80- and 40-wide stride-1 3x3 layers (C2f bottlenecks,
+    # P3 detect heads) take the row-tile kernel, with the table and the
+    # table + residual epilogues.
+    g, info = yolo.int8_graph(backend, batch=1, size=320, calib=yolo.calibration_images(4, 320))
+    monkeypatch.setenv("DW_IGEMM_TILE", "16,4,-2")
+    x = yolo.input_images(1, 320)
+    rt = HipGraphRuntime(g, backend)
+    assert sum(L["kernel"].endswith("_rows") for L in rt.launches()) >= 10
+    rt.set_input_f32(info["input"], x)
+    rt.run()
+    got = gpu_outputs(rt, info)
+    ref = oracle_run(g, {info["input"]: synth.f16_bits(x)})
+    for o, gv in zip(info["outputs"], got):
+        np.testing.assert_array_equal(gv, ref[o], err_msg=o)
+
+
 @pytest.mark.parametrize("plant_subnormal_weight", [False, True])
 @pytest.mark.parametrize("stride", [1, 2])
 def test_depthwise_graph_bit_exact(backend, plant_subnormal_weight, stride):

@@ -250,6 +250,27 @@ def test_qlinearconv_streamed_tiles_bit_exact(backend, geom, monkeypatch):
         np.testing.assert_array_equal(run_qconv(backend, c, s, p), ref, err_msg=f"tile {bc},{pb},-1")
 
 
+@pytest.mark.parametrize("geom", [(2, 8, 80, 64, 64, 3, 1, 1), (1, 4, 160, 16, 32, 3, 1, 1),
+                                  (2, 16, 40, 128, 96, 3, 1, 1), (1, 8, 80, 80, 80, 3, 1, 1),
+                                  (1, 2, 160, 48, 16, 3, 1, 1)])
+def test_qlinearconv_row_tiles_bit_exact(backend, geom, monkeypatch):
+    # The row-tile kernel (3x3, stride 1, whole rows of 320 pixels staged in
+    # LDS with their halo) over every channel tile it has; zero points other
+    # than 128 make the padding pattern matter.
+    n, h, w, ci, co, k, s, p = geom
+    r = synth.Rng(synth.seed_for(950 + sum(geom)))
+    c = dict(x=r.integers((n, h, w, ci), 0, 255).astype(np.uint8),
+             w=r.integers((k, k, ci, co), -127, 127).astype(np.int8),
+             bias=r.integers((co,), -4096, 4096).astype(np.int32),
+             w_scales=r.log_uniform((co,), 1e-3, 1e-2), x_scale=0.02, x_zp=119, y_scale=0.05, y_zp=140)
+    ref = oracle_qconv(c, s, p)
+    tiles = [bc for bc, pb in igemm_tiles(co) if pb == 4 and bc <= 96]
+    assert tiles
+    for bc in tiles:
+        monkeypatch.setenv("DW_IGEMM_TILE", f"{bc},4,-2")
+        np.testing.assert_array_equal(run_qconv(backend, c, s, p), ref, err_msg=f"tile {bc},4,-2")
+
+
 def test_qlinearconv_golden_fixtures(backend):
     cases = json.loads((GOLDEN / "qlinear_cases.json").read_text())["qlinearconv"]
     for g in cases:
