@@ -364,6 +364,17 @@ void Runtime::plan_streams(int n) {
     J.stream = s;
     last[s] = j;
   }
+  // one stream after all (a chain, or a single launch): no fork or join
+  bool side_used = false;
+  for (int k = 1; k < n; ++k) side_used |= last[k] >= 0;
+  if (!side_used) {
+    nstreams = 1;
+    for (auto& L : launches) {
+      L.waits.clear();
+      L.record = false;
+    }
+    return;
+  }
   // the backend's stream joins every other stream's last launch
   for (int k = 1; k < n; ++k)
     if (last[k] >= 0) launches[last[k]].record = true;
