@@ -260,18 +260,33 @@ __device__ __forceinline__ void pixel_setup(const IgemmArgs& a, int p0, int lane
   }
 }
 
+// LDS rows the int8 epilogue uses to regroup results (per wave: 16 pixels
+// x (BC + 16) bytes; the 16-byte pad puts the 64 lanes' 4-byte writes in 64
+// distinct banks).
+__host__ __device__ constexpr int xpose_row(int bc) { return bc + 16; }
+__host__ __device__ constexpr int xpose_bytes(int bc) { return 4 * 16 * xpose_row(bc); }
+
 // Epilogue of a workgroup's tile: this lane holds channels c0 + cb*16 + cq
 // .. +3 of pixel p0 + pb*16 + (lane & 15) for every block (cb, pb).  The
 // specialised int8 epilogues (EPV) take bias' from the accumulators' start
-// values and the multipliers and table from LDS.
+// values and the multipliers and table from LDS.  With xp (this wave's
+// xpose_row(BC) x 16 bytes of LDS), a pixel's u8 results are regrouped
+// there so that each lane stores 16 consecutive channels: one 16-byte store
+// per lane and 4 blocks, whole cache lines when the output rows are dense,
+// instead of a 4-byte store per lane and block (a 16-channel tile gains
+// nothing: it has one block).
 template <int ESZ, int BC, int PB, int EPV, typename AccT>
 __device__ __forceinline__ void igemm_store(const IgemmArgs& a, const EpiLds& ep, AccT (&acc)[BC / 16][PB], int c0,
-                                            int p0, int lane, const uint8_t* s_ms, const uint8_t* s_lut) {
+                                            int p0, int lane, const uint8_t* s_ms, const uint8_t* s_lut,
+                                            uint8_t* xp = nullptr) {
   constexpr int CB = BC / 16;
   constexpr bool FAST = EPV != EPV_GENERIC;
   const int cq = 4 * (lane >> 4);
   if constexpr (FAST) {
     const bool full = c0 + BC <= a.cout;
+    const bool wide = CB >= 2 && xp != nullptr && full && (a.y_pix_stride & 15) == 0 &&
+                      ((a.y_c_off + c0) & 15) == 0 && (((uintptr_t)a.y) & 15) == 0;
+    uint8_t* const xrow = wide ? xp + (lane & 15) * xpose_row(BC) : nullptr;
     const int qbase = 0x4B400000 - a.y_zp;
     const float qlo = 12582912.0f - (float)a.y_zp, qhi = qlo + 255.0f;
     const __attribute__((address_space(3))) uint8_t* lut3 = (const __attribute__((address_space(3))) uint8_t*)s_lut;
@@ -290,6 +305,7 @@ __device__ __forceinline__ void igemm_store(const IgemmArgs& a, const EpiLds& ep
         for (int cb = 0; cb < CB; ++cb)
           rres[cb] = (full || c0 + cb * 16 + cq < a.cout) ? *reinterpret_cast<const uint32_t*>(rrow + cb * 16) : 0u;
       }
+      if (wide) asm volatile("" ::: "memory");  // the previous block's reads are issued
 #pragma unroll
       for (int cb = 0; cb < CB; ++cb) {
         if (!full && c0 + cb * 16 + cq >= a.cout) continue;
@@ -306,7 +322,22 @@ __device__ __forceinline__ void igemm_store(const IgemmArgs& a, const EpiLds& ep
           if constexpr (EPV == EPV_QU8_LUT_RES) qi = qadd_u8(qi, (rres[cb] >> (8 * r)) & 0xff, a);
           out |= (uint32_t)qi << (8 * r);
         }
-        *reinterpret_cast<uint32_t*>(yrow + cb * 16) = out;
+        if (wide)
+          *reinterpret_cast<uint32_t*>(xrow + cb * 16 + cq) = out;
+        else
+          *reinterpret_cast<uint32_t*>(yrow + cb * 16) = out;
+      }
+      if (wide) {
+        // the pixel's 4 lanes wrote its BC channels; lane g now stores
+        // blocks g, g + 4, ... (one wave's LDS operations run in order)
+        asm volatile("" ::: "memory");
+        uint8_t* const ydst = yrow - cq;
+#pragma unroll
+        for (int i = 0; i < (CB + 3) / 4; ++i) {
+          const int cb = 4 * i + (lane >> 4);
+          if (cb < CB)
+            *reinterpret_cast<uint4*>(ydst + cb * 16) = *reinterpret_cast<const uint4*>(xrow + cb * 16);
+        }
       }
     }
   } else {
@@ -547,7 +578,16 @@ __global__ __launch_bounds__(256) void igemm_kernel(const IgemmArgs a) {
 #undef DW_LDS_FENCE
 #undef DW_LOAD_B
 
-  igemm_store<ESZ, BC, PB, EPV>(a, ep, acc, c0, p0, lane, s_ms, s_lut);
+  // int8 epilogue: the weight chunk's LDS, once every wave is done with it,
+  // regroups the results (when the chunk is large enough)
+  uint8_t* xp = nullptr;
+  if constexpr (FAST && BC >= 32) {
+    if (KCH * BC * 64 >= xpose_bytes(BC)) {
+      __syncthreads();
+      xp = s_chunk + wave * 16 * xpose_row(BC);
+    }
+  }
+  igemm_store<ESZ, BC, PB, EPV>(a, ep, acc, c0, p0, lane, s_ms, s_lut, xp);
 }
 
 // Launch of the instantiation for a tile shape (the caller checked that it

@@ -219,7 +219,14 @@ __global__ __launch_bounds__(256) void igemm_rows_kernel(const IgemmArgs a) {
   }
 #undef DW_READ_K
 
-  igemm_store<1, BC, PB, EPV>(a, ep, acc, c0, p0, lane, s_ms, s_lut);
+  // int8 epilogue: the input tile's LDS, once every wave is done with it,
+  // regroups the results (the tile is at least 4 rows of 42 16-byte units)
+  uint8_t* xp = nullptr;
+  if constexpr (FAST && BC >= 32) {
+    __syncthreads();
+    xp = s_x + wave * 16 * xpose_row(BC);
+  }
+  igemm_store<1, BC, PB, EPV>(a, ep, acc, c0, p0, lane, s_ms, s_lut, xp);
 }
 
 template <int EPV>

@@ -273,7 +273,15 @@ __global__ __launch_bounds__(256) void igemm_stream_kernel(const IgemmArgs a) {
 #undef DW_STORE_W
 #undef DW_LOAD_B
 
-  igemm_store<ESZ, BC, PB, EPV>(a, ep, acc, c0, p0, lane, s_ms, s_lut);
+  // int8 epilogue: the weight ring's LDS, once every wave is done with it,
+  // regroups the results
+  uint8_t* xp = nullptr;
+  if constexpr (FAST && BC >= 32) {
+    static_assert(NW * BC * 64 >= xpose_bytes(BC), "regroup area");
+    __syncthreads();
+    xp = s_ring + wave * 16 * xpose_row(BC);
+  }
+  igemm_store<ESZ, BC, PB, EPV>(a, ep, acc, c0, p0, lane, s_ms, s_lut, xp);
 }
 
 template <int ESZ, int BC, int EPV>
