@@ -3,8 +3,10 @@
 
 Default: the YOLOv8n-shaped graph, u8-quantized (QDQ-folded QLinearConv,
 fp16 stem and head 1x1s), batch 32, 640x640, on one GPU through
-HipGraphRuntime (the whole run captured once into a HIP graph).  A step is
-one run of the graph over one batch already resident in HBM; `value` is
+HipGraphRuntime (its launch list replayed on the backend's streams; --capture
+replays one HIP graph instead, which measures slower here: hipGraphLaunch
+costs more host and device time than the ~70 launches it replaces).  A step
+is one run of the graph over one batch already resident in HBM; `value` is
 images/s over exactly --steps steps after --warmup untimed steps, bracketed
 by stream synchronisation.
 
@@ -213,7 +215,8 @@ def cpu_baseline_conv_f32(xwb, seconds: float):
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=0,
+                    help="timed steps (default: 50 for the graphs, 1000 for the single-op workloads)")
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="yolov8n_int8",
                     choices=["yolov8n_int8", "yolov8n_f16", "qlinearconv", "dwconv", "conv_f32"])
@@ -222,7 +225,7 @@ def main():
     ap.add_argument("--profile-iters", type=int, default=3)
     ap.add_argument("--profile-repeat", type=int, default=10,
                     help="back-to-back repeats of each launch per timing pass")
-    ap.add_argument("--no-capture", action="store_true", help="replay launches eagerly instead of a HIP graph")
+    ap.add_argument("--capture", action="store_true", help="replay one captured HIP graph per step")
     ap.add_argument("--dump-launches", default="", help="write per-launch timings (JSON lines) to this file")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="end with one plain 256 MiB device copy (copy_channels kernel), the known-size "
@@ -233,6 +236,8 @@ def main():
               f"(the batch would shard data-parallel across GPUs with no exchange).", file=sys.stderr)
         sys.exit(2)
 
+    if args.steps <= 0:
+        args.steps = 50 if args.workload.startswith("yolov8n") else 1000
     import __graft_entry__
 
     dw = __graft_entry__.import_pkg()
@@ -272,7 +277,7 @@ def main():
     for rt in rts:
         for k, v in inputs.items():
             rt.set_input_bytes(k, v)
-        if not args.no_capture:
+        if args.capture:
             rt.enable_capture(True)
     t_setup = time.perf_counter() - t_setup
     images = work["images"]

@@ -76,4 +76,83 @@ __device__ __forceinline__ uint16_t silu_f16_fast(uint16_t hb) {
   return f2h(x * h2f_ieee(s));
 }
 
+// Two f16 values in one 32-bit register (element 0 in the low half); the
+// arithmetic operators on it are the packed f16 instructions, correctly
+// rounded with f16 subnormals kept.
+typedef _Float16 h16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint16_t pk_lo(h16x2 v) { return (uint16_t)__builtin_bit_cast(uint32_t, v); }
+__device__ __forceinline__ uint16_t pk_hi(h16x2 v) { return (uint16_t)(__builtin_bit_cast(uint32_t, v) >> 16); }
+__device__ __forceinline__ h16x2 pk_make(uint16_t lo, uint16_t hi) {
+  return __builtin_bit_cast(h16x2, (uint32_t)lo | ((uint32_t)hi << 16));
+}
+// f2h of two values (each rounded to f32 first, as f2h requires)
+__device__ __forceinline__ h16x2 pk_f2h(float a, float b) {
+  asm("" : "+v"(a));
+  asm("" : "+v"(b));
+  return h16x2{(_Float16)a, (_Float16)b};
+}
+
+// SiLU of two f16 values for the fp16-tolerance paths, fewer instructions
+// than silu_f16_fast: exp(-x) = 2^h * (1 + r) with h = -x log2(e) rounded to
+// f32 and r = -x - h ln 2 its residual (ln 2 in two parts, Cody-Waite), then
+// one rcp of 1 + exp(-x) (1 ulp); the sigmoid is rounded to f16 and the
+// product x * s of two f16 values (exact in f32, so one rounding) is one
+// packed f16 multiply.
+__device__ __forceinline__ h16x2 silu_f16_pk(h16x2 x) {
+  float r[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const float v = (float)x[i];
+    const float h = v * -1.44269502f;
+    float res = fmaf(-h, 0.693145751953125f, -v);
+    res = fmaf(-h, 1.42860677e-06f, res);
+    float e = __builtin_amdgcn_exp2f(h);
+    e = fmaf(e, res, e);
+    r[i] = __builtin_amdgcn_rcpf(1.0f + e);
+  }
+  return x * pk_f2h(r[0], r[1]);
+}
+
+// acc + (f16 half SEL of x) * (f16 half SEL of w), fused, in f32: the f16
+// values widen exactly (subnormals at their IEEE value).  One v_fma_mix per
+// product; written out because the compiler otherwise widens reused
+// operands with separate conversions.
+template <int SEL>
+__device__ __forceinline__ float fma_mix_h(uint32_t x, uint32_t w, float acc) {
+  if constexpr (SEL == 0)
+    asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel_hi:[1,1,0]" : "+v"(acc) : "v"(x), "v"(w));
+  else
+    asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel:[1,1,0] op_sel_hi:[1,1,0]" : "+v"(acc) : "v"(x), "v"(w));
+  return acc;
+}
+// (f16 half SEL of x) * (f16 half SEL of w) + 0: the first product of a
+// chain that starts at +0 (+0 + -0 is +0, as fma gives)
+template <int SEL>
+__device__ __forceinline__ float fma_mix_h0(uint32_t x, uint32_t w) {
+  float r;
+  if constexpr (SEL == 0)
+    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,1,0]" : "=v"(r) : "v"(x), "v"(w));
+  else
+    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[1,1,0] op_sel_hi:[1,1,0]" : "=v"(r) : "v"(x), "v"(w));
+  return r;
+}
+// the same with an f32 weight
+template <int SEL>
+__device__ __forceinline__ float fma_mix_hf(uint32_t x, float w, float acc) {
+  if constexpr (SEL == 0)
+    asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel_hi:[1,0,0]" : "+v"(acc) : "v"(x), "v"(w));
+  else
+    asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(acc) : "v"(x), "v"(w));
+  return acc;
+}
+template <int SEL>
+__device__ __forceinline__ float fma_mix_hf0(uint32_t x, float w) {
+  float r;
+  if constexpr (SEL == 0)
+    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(x), "v"(w));
+  else
+    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(x), "v"(w));
+  return r;
+}
+
 }  // namespace dw

@@ -524,7 +524,7 @@ def test_depthwise_f16_full_workload(backend):
 
 @pytest.mark.parametrize("geom", [(1, 5, 11, 12, 1), (2, 13, 10, 4, 2), (1, 9, 17, 20, 1), (3, 8, 19, 36, 2)])
 def test_depthwise_f16_sliding_window_shapes(backend, geom):
-    # Row lengths that end part-way through a thread's 8 outputs, channel
+    # Row lengths that end part-way through a thread's 4 outputs, channel
     # counts that are multiples of 4 but not 8, both strides; bias and no bias.
     n, h, w, c, s = geom
     r = synth.Rng(synth.seed_for(420 + sum(geom)))
