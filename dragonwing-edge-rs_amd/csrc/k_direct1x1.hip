@@ -32,17 +32,15 @@ typedef const __attribute__((address_space(4))) float* wrow_t;
 
 // Input element e of a raw 16-byte vector.  NOSUB (u8 input only): the
 // dequantized value can never be an f16 subnormal (scale >= 2^-14), so the
-// reference's subnormal decode rule is compiled out.
+// reference's subnormal decode rule is compiled out, and the value (a
+// function of the byte alone) is read from a 256-entry table in LDS that
+// the workgroup fills first: one address computation and one LDS read per
+// input instead of five conversions.
 template <int IN_KIND, bool NOSUB>
-__device__ __forceinline__ float decode_x(const DirectArgs& a, const uint4& u, int e) {
+__device__ __forceinline__ float decode_x(const DirectArgs& a, const uint4& u, int e, const float* s_deq) {
   if constexpr (IN_KIND == 2 && NOSUB) {
     const uint32_t wd = e < 4 ? u.x : (e < 8 ? u.y : (e < 12 ? u.z : u.w));
-    const int q = (int)((wd >> (8 * (e & 3))) & 0xff);
-    float v = h2f_ieee(f2h((float)(q - a.in_zp) * a.in_scale));
-    // widened once here: the FMAs then take an f32 operand (v_fma_f32)
-    // rather than each widening the f16 value again (v_fma_mix_f32)
-    asm volatile("" : "+v"(v));
-    return v;
+    return s_deq[(wd >> (8 * (e & 3))) & 0xff];
   } else {
     return dx::decode_elem<IN_KIND>(a, u, e);
   }
@@ -56,6 +54,16 @@ __global__ __launch_bounds__(64) void conv1x1_exact_kernel(const DirectArgs a) {
   const int oc0 = blockIdx.y * C;
   const int lane = threadIdx.x;
   const wrow_t wbase = (wrow_t)(a.wf + oc0);
+  // u8 -> f32 of the f16 dequantized value, (q - zp) * scale rounded to f16
+  __shared__ float s_deq[IN_KIND == 2 && NOSUB ? 256 : 1];
+  if constexpr (IN_KIND == 2 && NOSUB) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int q = lane * 4 + i;
+      s_deq[q] = h2f_ieee(f2h((float)(q - a.in_zp) * a.in_scale));
+    }
+    __syncthreads();
+  }
 
   // this lane's pixels: p = tile*64P + j*64 + lane
   const uint8_t* xp[P];
@@ -94,7 +102,7 @@ __global__ __launch_bounds__(64) void conv1x1_exact_kernel(const DirectArgs a) {
     for (int e = 0; e < VN; ++e) {
       float xv[P];
 #pragma unroll
-      for (int j = 0; j < P; ++j) xv[j] = decode_x<IN_KIND, NOSUB>(a, cur[j], e);
+      for (int j = 0; j < P; ++j) xv[j] = decode_x<IN_KIND, NOSUB>(a, cur[j], e, s_deq);
       const wrow_t wr = wbase + (size_t)(k0 + e) * cout;
 #pragma unroll
       for (int c = 0; c < C; ++c) {
