@@ -61,6 +61,45 @@ __device__ __forceinline__ void load_vec(const DirectArgs& a, const uint8_t* p, 
 // (one instruction) and the quantization rounds by adding 1.5 * 2^23 and
 // clamps with one med3 on the float (as requant_bits in igemm_kernel.h).
 // lut: the activation table (LDS or global); a.lut when null.
+//
+// u8 quantization of the IEEE value xv of a stored f16 (FE): the integer
+// rint(xv / out_scale) + zp clamped to 0..255, as its low byte.  PLAIN: the
+// host checked that xv * (1 / out_scale) rounds to the same integer for
+// every finite f16 xv, so the correction FMAs are left out.
+template <bool PLAIN>
+__device__ __forceinline__ int quant_u8_fe(const DirectArgs& a, float xv) {
+  const float q0 = xv * a.out_rcp;
+  float d = q0;
+  if constexpr (!PLAIN) {
+    const float dc = fmaf(fmaf(-q0, a.out_scale, xv), a.out_rcp, q0);
+    d = fabsf(xv) <= 65504.0f ? dc : q0;  // inf * rcp is the quotient too
+  }
+  const float lo = 12582912.0f - (float)a.out_zp;
+  const int qb = __builtin_bit_cast(int, __builtin_amdgcn_fmed3f(d + 12582912.0f, lo, lo + 255.0f));
+  return (qb - (0x4B400000 - a.out_zp)) & 0xff;  // the clamp makes it 0..255 (the mask keeps table reads in range)
+}
+
+// The u8 epilogue with FE when a.epi_pk is set (no f16 bias value is
+// subnormal): the conv results are rounded to f16 two at a time and the
+// bias pass F16(f32(y) + f32(b)) is one packed f16 add (f32 holds the sum
+// of two f16 values to 2 * 11 + 2 bits, so rounding it to f16 is the
+// correctly rounded f16 sum).
+template <int OC, bool PLAIN>
+__device__ __forceinline__ void quant_pairs_fe(const DirectArgs& a, const float* acc, int oc0, const uint8_t* lut,
+                                               uint32_t* words) {
+#pragma unroll
+  for (int j = 0; j < OC; j += 2) {
+    h16x2 p = pk_f2h(acc[j], acc[j + 1]);
+    if (a.bias_h) p = p + *reinterpret_cast<const h16x2*>(a.bias_h + oc0 + j);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      int qi = quant_u8_fe<PLAIN>(a, (float)p[i]);
+      if (a.lut) qi = lut[qi];
+      words[(j + i) >> 2] |= (uint32_t)qi << (8 * ((j + i) & 3));
+    }
+  }
+}
+
 template <int OUT, int OC, bool FE = false>
 __device__ __forceinline__ void store_outputs_t(const DirectArgs& a, const float* acc, int oc0, uint8_t* yb,
                                                 const uint8_t* lut = nullptr) {
@@ -69,6 +108,25 @@ __device__ __forceinline__ void store_outputs_t(const DirectArgs& a, const float
   uint32_t words[NW];
 #pragma unroll
   for (int i = 0; i < NW; ++i) words[i] = 0;
+  if constexpr (OUT == 2 && FE && OC % 4 == 0) {
+    if (a.epi_pk && a.vec_out != 1) {
+      const uint8_t* lt = lut ? lut : a.lut;
+      if (a.out_plain)
+        quant_pairs_fe<OC, true>(a, acc, oc0, lt, words);
+      else
+        quant_pairs_fe<OC, false>(a, acc, oc0, lt, words);
+      if (a.vec_out == 16) {
+#pragma unroll
+        for (int i = 0; i < NW / 4; ++i)
+          *reinterpret_cast<uint4*>(yb + 16 * i) =
+              make_uint4(words[4 * i], words[4 * i + 1], words[4 * i + 2], words[4 * i + 3]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < NW; ++i) *reinterpret_cast<uint32_t*>(yb + 4 * i) = words[i];
+      }
+      return;
+    }
+  }
 #pragma unroll
   for (int j = 0; j < OC; ++j) {
     if constexpr (OUT == 0) {

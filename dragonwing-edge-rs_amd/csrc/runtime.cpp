@@ -206,6 +206,37 @@ bool fast_quant_ok(float s, float rcp) {
   return true;
 }
 
+// Whether rint(x * (1/s)) equals rint(x / s) for every finite f16 value x
+// (IEEE decode) whose quotient is not clamped either way (|x / s| < 512;
+// x * (1/s) is within two ulps of x / s), so the fast epilogue may leave out
+// the FMA correction.
+bool plain_quant_ok(float s, float rcp) {
+  for (uint32_t h = 0; h < 65536; ++h) {
+    if ((h & 0x7C00u) == 0x7C00u) continue;  // inf, NaN
+    uint16_t hb = (uint16_t)h;
+    _Float16 hv;
+    memcpy(&hv, &hb, 2);
+    const float x = (float)hv;
+    if (fabsf(x / s) >= 512.0f) continue;  // clamped to 0 or 255 either way
+    if (rintf(x * rcp) != rintf(x / s)) return false;
+  }
+  return true;
+}
+
+// Whether an f16 bias holds no subnormal value (then the bias pass on f16
+// values is the IEEE f16 sum).
+bool bias_plain_f16(const GraphIR& g, const OpNode& op, bool has_bias) {
+  if (!has_bias) return true;
+  const TensorInfo& B = g.t.at(op.in[2]);
+  if (B.dtype != DW_DTYPE_F16) return false;
+  const uint16_t* bh = (const uint16_t*)B.data.data();
+  for (size_t c = 0; c < B.data.size() / 2; ++c) {
+    const uint16_t m = bh[c] & 0x7fff;
+    if (m != 0 && m < 0x400) return false;
+  }
+  return true;
+}
+
 // Whether the exact-conv epilogue may widen its f16 values as IEEE f16
 // instead of the reference decode (which halves subnormals) and use the
 // reciprocal quotient: true when no f16 subnormal can change an output.
@@ -1054,6 +1085,13 @@ void Runtime::emit_conv(const Group& gr) {
     }
   }
   if (gr.out_kind != 0) a.fast_epi = fast_epi_ok(g, op, has_bias, gr.out_kind, a) ? 1 : 0;
+  if (a.fast_epi && gr.out_kind == 2) {
+    a.epi_pk = bias_plain_f16(g, op, has_bias) ? 1 : 0;
+    a.out_plain = plain_quant_ok(a.out_scale, a.out_rcp) ? 1 : 0;
+    // test override: the quotient with the FMA correction everywhere
+    if (const char* e = getenv("DW_QUANT_CORRECTED"))
+      if (atoi(e) != 0) a.out_plain = 0;
+  }
   L.kernel = "direct_conv";
   L.bytes += (double)x.bytes() + W.numel() * 4.0 + (double)y.bytes();
   L.fn = [=](hipStream_t st) { launch_direct_conv(st, a); };

@@ -84,6 +84,22 @@ def test_int8_graph_small_bit_exact(backend, int8_small):
     assert len(np.unique(got[0])) > 100
 
 
+def test_int8_graph_corrected_quotient_bit_exact(backend, int8_small, monkeypatch):
+    # The fp16 stem's u8 epilogue divides by the output scale as a product
+    # with the reciprocal, plus an FMA correction unless the host proved the
+    # plain product exact for every f16 value; the corrected form gives the
+    # same bytes.
+    monkeypatch.setenv("DW_QUANT_CORRECTED", "1")
+    g, info = int8_small
+    x = yolo.input_images(2, 96)
+    rt = HipGraphRuntime(g, backend)
+    rt.set_input_f32(info["input"], x)
+    rt.run()
+    ref = oracle_run(g, {info["input"]: synth.f16_bits(x)})
+    for o, gv in zip(info["outputs"], gpu_outputs(rt, info)):
+        np.testing.assert_array_equal(gv, ref[o], err_msg=o)
+
+
 @pytest.mark.parametrize("tile", ["16,4,3", "32,2,1", "64,4,2", "128,2,5"])
 def test_int8_graph_persistent_tiles_bit_exact(backend, int8_small, monkeypatch, tile):
     # Every convolution whose K fits the persistent kernel runs on it with
