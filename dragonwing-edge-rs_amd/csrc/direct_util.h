@@ -79,11 +79,14 @@ __device__ __forceinline__ int quant_u8_fe(const DirectArgs& a, float xv) {
   return (qb - (0x4B400000 - a.out_zp)) & 0xff;  // the clamp makes it 0..255 (the mask keeps table reads in range)
 }
 
-// The u8 epilogue with FE when a.epi_pk is set (no f16 bias value is
-// subnormal): the conv results are rounded to f16 two at a time and the
-// bias pass F16(f32(y) + f32(b)) is one packed f16 add (f32 holds the sum
-// of two f16 values to 2 * 11 + 2 bits, so rounding it to f16 is the
-// correctly rounded f16 sum).
+// The u8 epilogue when a.epi_pk is set: the conv results are rounded to
+// f16 two at a time and the bias pass F16(f32(y) + f32(b)) is one packed
+// f16 add (f32 holds the sum of two f16 values to 2 * 11 + 2 bits, so
+// rounding it to f16 is the correctly rounded f16 sum).  Exact when neither
+// y nor b is an f16 subnormal (the reference decodes those at half value):
+// the host checked the biases, and the caller checks the results.  The sum
+// is then quantized as an IEEE value: a subnormal sum quantizes to the zero
+// point either way, since the host also checked out_scale >= 2^-13.
 template <int OC, bool PLAIN>
 __device__ __forceinline__ void quant_pairs_fe(const DirectArgs& a, const float* acc, int oc0, const uint8_t* lut,
                                                uint32_t* words) {
@@ -108,8 +111,13 @@ __device__ __forceinline__ void store_outputs_t(const DirectArgs& a, const float
   uint32_t words[NW];
 #pragma unroll
   for (int i = 0; i < NW; ++i) words[i] = 0;
-  if constexpr (OUT == 2 && FE && OC % 4 == 0) {
-    if (a.epi_pk && a.vec_out != 1) {
+  if constexpr (OUT == 2 && OC % 4 == 0) {
+    // no result that rounds to an f16 subnormal (|acc| < 2^-14) anywhere
+    // in the wave: else the wave takes the per-channel path below
+    float amin = fabsf(acc[0]);
+#pragma unroll
+    for (int j = 1; j < OC; ++j) amin = fminf(amin, fabsf(acc[j]));
+    if (a.epi_pk && a.vec_out != 1 && !__any(amin < 6.103515625e-05f)) {
       const uint8_t* lt = lut ? lut : a.lut;
       if (a.out_plain)
         quant_pairs_fe<OC, true>(a, acc, oc0, lt, words);
