@@ -111,6 +111,30 @@ __device__ __forceinline__ void store_outputs_t(const DirectArgs& a, const float
   uint32_t words[NW];
 #pragma unroll
   for (int i = 0; i < NW; ++i) words[i] = 0;
+  if constexpr (OUT == 1 && OC % 2 == 0) {
+    // f16 out, no activation: the same packed rounding and bias pass
+    float amin = fabsf(acc[0]);
+#pragma unroll
+    for (int j = 1; j < OC; ++j) amin = fminf(amin, fabsf(acc[j]));
+    if (a.epi_pk && a.act == ACT_NONE && a.vec_out != 1 && !__any(amin < 6.103515625e-05f)) {
+#pragma unroll
+      for (int j = 0; j < OC; j += 2) {
+        h16x2 p = pk_f2h(acc[j], acc[j + 1]);
+        if (a.bias_h) p = p + *reinterpret_cast<const h16x2*>(a.bias_h + oc0 + j);
+        words[j >> 1] = __builtin_bit_cast(uint32_t, p);
+      }
+      if (a.vec_out == 16) {
+#pragma unroll
+        for (int i = 0; i < NW / 4; ++i)
+          *reinterpret_cast<uint4*>(yb + 16 * i) =
+              make_uint4(words[4 * i], words[4 * i + 1], words[4 * i + 2], words[4 * i + 3]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < NW; ++i) *reinterpret_cast<uint32_t*>(yb + 4 * i) = words[i];
+      }
+      return;
+    }
+  }
   if constexpr (OUT == 2 && OC % 4 == 0) {
     // no result that rounds to an f16 subnormal (|acc| < 2^-14) anywhere
     // in the wave: else the wave takes the per-channel path below

@@ -110,7 +110,10 @@ struct DirectArgs {
   int fast_epi;            // 1: out_fast holds, and the epilogue may widen its f16 values
                            // as IEEE f16 (the host checked that no subnormal changes a result)
   int x_bytes;             // set by the launcher for buffer-load paths: bytes of the input
-  int epi_pk;              // 1 (u8 out): no f16 bias value is subnormal, out_fast holds and
+  int epi_pk;              // 1 (f16 out): no f16 bias value is subnormal, so the bias pass
+                           // may be a packed f16 add (results that round to f16 subnormals
+                           // are checked in the kernel);
+                           // 1 (u8 out): no f16 bias value is subnormal, out_fast holds and
                            // out_scale >= 2^-13, so the bias pass may be a packed f16 add
                            // and the quantization may widen as IEEE f16 (results that
                            // round to f16 subnormals are checked in the kernel)

@@ -1085,6 +1085,7 @@ void Runtime::emit_conv(const Group& gr) {
     }
   }
   if (gr.out_kind != 0) a.fast_epi = fast_epi_ok(g, op, has_bias, gr.out_kind, a) ? 1 : 0;
+  if (gr.out_kind == 1) a.epi_pk = bias_plain_f16(g, op, has_bias) ? 1 : 0;
   if (gr.out_kind == 2 && a.out_fast && a.out_scale >= 1.220703125e-04f) {
     a.epi_pk = bias_plain_f16(g, op, has_bias) ? 1 : 0;
     a.out_plain = plain_quant_ok(a.out_scale, a.out_rcp) ? 1 : 0;
