@@ -91,6 +91,11 @@ SIGNATURES = {
     "dw_hip_resize_nearest_nhwc": (I, [P, I, P, P] + [Z] * 6),
     "dw_hip_concat_channels_nhwc": (I, [P, I, PP, P, Z, P, Z]),
     "dw_hip_split_channels_nhwc": (I, [P, I, P, PP, P, Z, Z]),
+    "dw_hip_gemm_f32": (I, [P, P, P, P, Z, Z, Z]),
+    "dw_hip_gemm_fp16": (I, [P, P, P, P, Z, Z, Z]),
+    "dw_hip_gemm_i8": (I, [P, P, P, P, Z, Z, Z]),
+    "dw_hip_global_avg_pool_nhwc": (I, [P, I, P, P, Z, Z, Z, Z]),
+    "dw_hip_softmax_f32": (I, [P, P, P, Z, Z]),
     "dw_graph_create": (I, [I, PP]),
     "dw_graph_destroy": (None, [P]),
     "dw_graph_add_tensor": (I, [P, S, P, I, I]),

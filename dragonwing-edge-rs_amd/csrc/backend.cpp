@@ -6,6 +6,7 @@
 #include "backend.h"
 
 #include <math.h>
+#include <stdint.h>
 #include <string.h>
 
 #include <algorithm>
@@ -680,6 +681,72 @@ int dw_hip_split_channels_nhwc(dw_hip_backend* be, int dtype, const dw_hip_buffe
                              (int)es);
     off += channels[i];
   }
+  API_END
+}
+
+// Classifier-head ops (see dw_hip.h for the reference functions each mirrors).
+int dw_hip_gemm_f32(dw_hip_backend* be, const dw_hip_buffer* a, const dw_hip_buffer* b, dw_hip_buffer* c,
+                    size_t m, size_t n, size_t k) {
+  API_BEGIN
+  Backend* bk = B(be);
+  if (!m || !n || !k) dw::fail(DW_ERR_INVALID, "gemm_f32: zero size");
+  if (m > 65535 || n > INT32_MAX || k > INT32_MAX) dw::fail(DW_ERR_UNSUPPORTED, "gemm_f32: m > 65535 or n, k > 2^31 - 1");
+  need(a, m * k * 4, "gemm_f32: A size");
+  need(b, k * n * 4, "gemm_f32: B size");
+  need(c, m * n * 4, "gemm_f32: C size");
+  dw::launch_gemm(bk->stream, dw::F32, a->ptr, b->ptr, c->ptr, (int)m, (int)n, (int)k);
+  API_END
+}
+
+int dw_hip_gemm_fp16(dw_hip_backend* be, const dw_hip_buffer* a, const dw_hip_buffer* b, dw_hip_buffer* c,
+                     size_t m, size_t n, size_t k) {
+  API_BEGIN
+  Backend* bk = B(be);
+  if (!m || !n || !k) dw::fail(DW_ERR_INVALID, "gemm_fp16: zero size");
+  if (m > 65535 || n > INT32_MAX || k > INT32_MAX) dw::fail(DW_ERR_UNSUPPORTED, "gemm_fp16: m > 65535 or n, k > 2^31 - 1");
+  need(a, m * k * 2, "gemm_fp16: A size");
+  need(b, k * n * 2, "gemm_fp16: B size");
+  need(c, m * n * 2, "gemm_fp16: C size");
+  dw::launch_gemm(bk->stream, dw::F16, a->ptr, b->ptr, c->ptr, (int)m, (int)n, (int)k);
+  API_END
+}
+
+int dw_hip_gemm_i8(dw_hip_backend* be, const dw_hip_buffer* a, const dw_hip_buffer* b, dw_hip_buffer* c_i32,
+                   size_t m, size_t n, size_t k) {
+  API_BEGIN
+  Backend* bk = B(be);
+  if (!m || !n || !k) dw::fail(DW_ERR_INVALID, "gemm_i8: zero size");
+  if (m > 65535 || n > INT32_MAX || k > INT32_MAX) dw::fail(DW_ERR_UNSUPPORTED, "gemm_i8: m > 65535 or n, k > 2^31 - 1");
+  need(a, m * k, "gemm_i8: A size");
+  need(b, k * n, "gemm_i8: B size");
+  need(c_i32, m * n * 4, "gemm_i8: C size");
+  dw::launch_gemm(bk->stream, dw::I8, a->ptr, b->ptr, c_i32->ptr, (int)m, (int)n, (int)k);
+  API_END
+}
+
+int dw_hip_global_avg_pool_nhwc(dw_hip_backend* be, int dtype, const dw_hip_buffer* x, dw_hip_buffer* y,
+                                size_t n, size_t h, size_t w, size_t c) {
+  API_BEGIN
+  Backend* bk = B(be);
+  if (dtype != DW_DTYPE_F32 && dtype != DW_DTYPE_F16)
+    dw::fail(DW_ERR_UNSUPPORTED, "global_avg_pool: unsupported dtype");
+  if (!n || !h || !w || !c) dw::fail(DW_ERR_INVALID, "global_avg_pool: zero size");
+  if (h * w > INT32_MAX || n > 65535 || c > INT32_MAX) dw::fail(DW_ERR_UNSUPPORTED, "global_avg_pool: size");
+  const size_t es = dw::dtype_size(dtype);
+  need(x, n * h * w * c * es, "global_avg_pool: input size");
+  need(y, n * c * es, "global_avg_pool: output size");
+  dw::launch_global_avg_pool(bk->stream, dtype, x->ptr, y->ptr, (int)n, (int)(h * w), (int)c);
+  API_END
+}
+
+int dw_hip_softmax_f32(dw_hip_backend* be, const dw_hip_buffer* x, dw_hip_buffer* y, size_t rows, size_t n) {
+  API_BEGIN
+  Backend* bk = B(be);
+  if (!rows || !n) dw::fail(DW_ERR_INVALID, "softmax_f32: zero size");
+  if (rows > INT32_MAX || n > INT32_MAX) dw::fail(DW_ERR_UNSUPPORTED, "softmax_f32: size");
+  need(x, rows * n * 4, "softmax_f32: input size");
+  need(y, rows * n * 4, "softmax_f32: output size");
+  dw::launch_softmax_rows(bk->stream, (const float*)x->ptr, (float*)y->ptr, (int)rows, (int)n);
   API_END
 }
 

@@ -155,6 +155,13 @@ int igemm_candidates(const IgemmArgs& a, int* bc, int* pb, int* tpw, int max);
 void launch_direct_conv(hipStream_t st, const DirectArgs& a);
 void launch_dwconv(hipStream_t st, const DwArgs& a, int dtype);
 
+// Classifier-head ops (k_head.hip).  gemm: row-major C[m][n] = A[m][k] B[k][n]
+// (dtype F32, F16 or I8 with an int32 C); global average pool over NHWC
+// [n][hw][c] -> [n][c]; softmax over rows of n f32 values.
+void launch_gemm(hipStream_t st, int dtype, const void* a, const void* b, void* c, int m, int n, int k);
+void launch_global_avg_pool(hipStream_t st, int dtype, const void* x, void* y, int n, int hw, int c);
+void launch_softmax_rows(hipStream_t st, const float* x, float* y, int rows, int n);
+
 // Elementwise glue (count elements, contiguous).
 enum EwOp : int {
   EW_RELU = 0, EW_ADD, EW_MUL, EW_SIGMOID, EW_SILU, EW_BIAS_ADD,

@@ -1,0 +1,127 @@
+// Classifier-head ops: Gemm (f32, f16, int8) with the reference's
+// accumulation order, GlobalAveragePool and Softmax over rows.  These are
+// small ops (a classifier's last layers: batch x 1280 -> 1000, a 7 x 7
+// pool), so every output is one thread walking its sum in the reference
+// order; the loads of each step are coalesced across the threads of a row
+// of outputs.
+#include "dw_common.h"
+#include "dw_device.h"
+
+namespace dw {
+namespace {
+
+// C[i][j] = sum over p of A[i][p] * B[p][j]: thread (i, j), j across the
+// lanes (B rows coalesced, A[i][p] the same in every lane).  f32: fma chain
+// from +0 in p order (gemm_f32_naive, ops.rs:273-290).  F16: operands
+// widened with the reference decode (h2f), the same chain, f2h of the sum
+// (gemm_fp16, ops.rs:461-479).
+template <bool F16>
+__global__ __launch_bounds__(256) void gemm_exact_kernel(const void* A, const void* B, void* Cm, int m, int n,
+                                                         int k) {
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  const int i = blockIdx.y;
+  if (j >= n || i >= m) return;
+  float acc = 0.0f;
+  if constexpr (F16) {
+    const uint16_t* a = (const uint16_t*)A + (size_t)i * k;
+    const uint16_t* b = (const uint16_t*)B + j;
+    for (int p = 0; p < k; ++p) acc = fmaf(h2f(a[p]), h2f(b[(size_t)p * n]), acc);
+    ((uint16_t*)Cm)[(size_t)i * n + j] = f2h(acc);
+  } else {
+    const float* a = (const float*)A + (size_t)i * k;
+    const float* b = (const float*)B + j;
+    for (int p = 0; p < k; ++p) acc = fmaf(a[p], b[(size_t)p * n], acc);
+    ((float*)Cm)[(size_t)i * n + j] = acc;
+  }
+}
+
+// int32 sum of i8 products (gemm_i8_scalar, ops.rs:2981-2995); integer
+// addition wraps like the reference's release build, in any order.
+__global__ __launch_bounds__(256) void gemm_i8_kernel(const int8_t* A, const int8_t* B, int32_t* Cm, int m, int n,
+                                                      int k) {
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  const int i = blockIdx.y;
+  if (j >= n || i >= m) return;
+  const int8_t* a = A + (size_t)i * k;
+  const int8_t* b = B + j;
+  uint32_t acc = 0;
+  for (int p = 0; p < k; ++p) acc += (uint32_t)((int32_t)a[p] * (int32_t)b[(size_t)p * n]);
+  Cm[(size_t)i * n + j] = (int32_t)acc;
+}
+
+// NHWC global average pool (CpuGraphRuntime::dispatch_global_avg_pool,
+// onnx runtime.rs:1109-1175): thread (batch, channel) sums its h x w values
+// in row-major order in f32 and divides by h * w (correctly rounded); f16
+// widens with the reference decode and rounds the mean to f16.
+template <bool F16>
+__global__ __launch_bounds__(256) void global_avg_pool_kernel(const void* X, void* Y, int n, int hw, int c) {
+  const int ch = blockIdx.x * 256 + threadIdx.x;
+  const int b = blockIdx.y;
+  if (ch >= c || b >= n) return;
+  float sum = 0.0f;
+  const size_t base = (size_t)b * hw * c + ch;
+  if constexpr (F16) {
+    const uint16_t* x = (const uint16_t*)X + base;
+    for (int s = 0; s < hw; ++s) sum += h2f(x[(size_t)s * c]);
+    ((uint16_t*)Y)[(size_t)b * c + ch] = f2h(__fdiv_rn(sum, (float)hw));
+  } else {
+    const float* x = (const float*)X + base;
+    for (int s = 0; s < hw; ++s) sum += x[(size_t)s * c];
+    ((float*)Y)[(size_t)b * c + ch] = __fdiv_rn(sum, (float)hw);
+  }
+}
+
+// Softmax over rows of n (softmax_f32, ops.rs:1609-1638), one thread per
+// row: the max from -inf (fmaxf: a NaN operand loses, as f32::max), e =
+// exp(x - max), the sum in order, out = e * (1 / sum).  exp is the device
+// expf, so outputs agree with the host's to within a few ulps.
+__global__ __launch_bounds__(256) void softmax_rows_kernel(const float* X, float* Y, int rows, int n) {
+  const int r = blockIdx.x * 256 + threadIdx.x;
+  if (r >= rows) return;
+  const float* x = X + (size_t)r * n;
+  float* y = Y + (size_t)r * n;
+  float mx = -INFINITY;
+  for (int i = 0; i < n; ++i) mx = fmaxf(mx, x[i]);
+  float sum = 0.0f;
+  for (int i = 0; i < n; ++i) {
+    const float e = expf(x[i] - mx);
+    y[i] = e;
+    sum += e;
+  }
+  const float inv = __fdiv_rn(1.0f, sum);
+  for (int i = 0; i < n; ++i) y[i] *= inv;
+}
+
+}  // namespace
+
+void launch_gemm(hipStream_t st, int dtype, const void* a, const void* b, void* c, int m, int n, int k) {
+  const dim3 g((unsigned)((n + 255) / 256), (unsigned)m);
+  if (dtype == F32)
+    hipLaunchKernelGGL((gemm_exact_kernel<false>), g, dim3(256), 0, st, a, b, c, m, n, k);
+  else if (dtype == F16)
+    hipLaunchKernelGGL((gemm_exact_kernel<true>), g, dim3(256), 0, st, a, b, c, m, n, k);
+  else if (dtype == I8)
+    hipLaunchKernelGGL(gemm_i8_kernel, g, dim3(256), 0, st, (const int8_t*)a, (const int8_t*)b, (int32_t*)c, m, n,
+                       k);
+  else
+    fail(-2, "gemm: dtype");
+  DW_HIP(hipGetLastError());
+}
+
+void launch_global_avg_pool(hipStream_t st, int dtype, const void* x, void* y, int n, int hw, int c) {
+  const dim3 g((unsigned)((c + 255) / 256), (unsigned)n);
+  if (dtype == F32)
+    hipLaunchKernelGGL((global_avg_pool_kernel<false>), g, dim3(256), 0, st, x, y, n, hw, c);
+  else if (dtype == F16)
+    hipLaunchKernelGGL((global_avg_pool_kernel<true>), g, dim3(256), 0, st, x, y, n, hw, c);
+  else
+    fail(-2, "global average pool: dtype");
+  DW_HIP(hipGetLastError());
+}
+
+void launch_softmax_rows(hipStream_t st, const float* x, float* y, int rows, int n) {
+  hipLaunchKernelGGL(softmax_rows_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st, x, y, rows, n);
+  DW_HIP(hipGetLastError());
+}
+
+}  // namespace dw

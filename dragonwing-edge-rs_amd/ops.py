@@ -167,3 +167,24 @@ def split_channels_nhwc(be, dtype, x, outputs, channels, pixels):
     arr = (C.c_void_p * len(outputs))(*[b.handle for b in outputs])
     ch = (C.c_size_t * len(channels))(*channels)
     check(load().dw_hip_split_channels_nhwc(be.handle, dtype, x.handle, arr, ch, len(outputs), pixels))
+
+
+# Classifier-head ops (row-major; see include/dw_hip.h)
+def gemm_f32(be, a, b, c, m, n, k):
+    check(load().dw_hip_gemm_f32(be.handle, a.handle, b.handle, c.handle, m, n, k))
+
+
+def gemm_fp16(be, a, b, c, m, n, k):
+    check(load().dw_hip_gemm_fp16(be.handle, a.handle, b.handle, c.handle, m, n, k))
+
+
+def gemm_i8(be, a, b, c_i32, m, n, k):
+    check(load().dw_hip_gemm_i8(be.handle, a.handle, b.handle, c_i32.handle, m, n, k))
+
+
+def global_avg_pool_nhwc(be, dtype, x, y, n, h, w, c):
+    check(load().dw_hip_global_avg_pool_nhwc(be.handle, dtype, x.handle, y.handle, n, h, w, c))
+
+
+def softmax_f32(be, x, y, rows, n):
+    check(load().dw_hip_softmax_f32(be.handle, x.handle, y.handle, rows, n))

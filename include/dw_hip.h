@@ -248,6 +248,29 @@ int dw_hip_split_channels_nhwc(dw_hip_backend* be, int dtype, const dw_hip_buffe
                                dw_hip_buffer* const* outputs, const size_t* channels,
                                size_t num_outputs, size_t pixels);
 
+/* Classifier-head ops.  Row-major, sizes must match exactly. */
+/* gemm_f32 (dragonwing-vulkan ops.rs:437; CPU gemm_f32_naive ops.rs:273-290 and
+ * gemm_f32_mt :1659-1707): c[m][n] = a[m][k] b[k][n], fma chain over k in order. */
+int dw_hip_gemm_f32(dw_hip_backend* be, const dw_hip_buffer* a, const dw_hip_buffer* b, dw_hip_buffer* c,
+                    size_t m, size_t n, size_t k);
+/* gemm_fp16 (dragonwing-vulkan ops.rs:1184; CPU ops.rs:461-479, :1709-1749): f16 in
+ * and out, F16::to_f32 operands, f32 fma chain, F16::from_f32 of the sum. */
+int dw_hip_gemm_fp16(dw_hip_backend* be, const dw_hip_buffer* a, const dw_hip_buffer* b, dw_hip_buffer* c,
+                     size_t m, size_t n, size_t k);
+/* gemm_i8 (CPU ops.rs:2964-2995; the Vulkan gemm_i8_packed ops.rs:1723 takes
+ * pre-packed operands): i8 x i8 -> int32 sums. */
+int dw_hip_gemm_i8(dw_hip_backend* be, const dw_hip_buffer* a, const dw_hip_buffer* b, dw_hip_buffer* c_i32,
+                   size_t m, size_t n, size_t k);
+/* GlobalAveragePool, NHWC [n][h][w][c] -> [n][c] (CpuGraphRuntime::
+ * dispatch_global_avg_pool, dragonwing-onnx runtime.rs:1109-1175): f32 sum over
+ * rows then columns, divided by h*w; dtype F32 or F16. */
+int dw_hip_global_avg_pool_nhwc(dw_hip_backend* be, int dtype, const dw_hip_buffer* x, dw_hip_buffer* y,
+                                size_t n, size_t h, size_t w, size_t c);
+/* softmax_f32 over rows of n (dragonwing-vulkan ops.rs:1519; CPU ops.rs:1609-1638):
+ * max subtraction, exp, sum, multiply by 1/sum.  exp is the device's: outputs
+ * agree with the CPU to a few ulps. */
+int dw_hip_softmax_f32(dw_hip_backend* be, const dw_hip_buffer* x, dw_hip_buffer* y, size_t rows, size_t n);
+
 /* ------------------------------------------------------------------------ */
 /* Graph IR — the C form of dragonwing_onnx::Graph / CompiledOp / OpParams   */
 /* (crates/dragonwing-onnx/src/graph.rs:18-31, builder.rs:204-361), plus the */

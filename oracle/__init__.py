@@ -91,6 +91,12 @@ def _declare(L: C.CDLL) -> None:
         "dwo_silu_lut_u8": (None, [_P, _F, _I, _F, _I]),
         "dwo_lut_u8": (None, [_P, _P, _Z, _P]),
         "dwo_maxpool2d_padded_nhwc": (None, [_P, _P] + [_Z] * 13),
+        "dwo_gemm_f32": (None, [_P, _P, _P, _Z, _Z, _Z]),
+        "dwo_gemm_fp16": (None, [_P, _P, _P, _Z, _Z, _Z]),
+        "dwo_gemm_i8": (None, [_P, _P, _P, _Z, _Z, _Z]),
+        "dwo_global_avg_pool_f32": (None, [_P, _P, _Z, _Z, _Z, _Z]),
+        "dwo_global_avg_pool_fp16": (None, [_P, _P, _Z, _Z, _Z, _Z]),
+        "dwo_softmax_f32": (None, [_P, _P, _Z, _Z]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -426,4 +432,64 @@ def lut_u8(x, lut):
     lut = np.ascontiguousarray(lut, np.uint8)
     y = np.empty(x.shape, np.uint8)
     lib().dwo_lut_u8(_p(y), _p(x), x.size, _p(lut))
+    return y
+
+
+# --------------------------------------------------------------------------
+# Classifier-head ops (ops.rs:273-290, :461-479, :2981-2995, :1609-1638;
+# onnx runtime.rs:1109-1175)
+# --------------------------------------------------------------------------
+def gemm_f32(a, b):
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    (m, k), (k2, n) = a.shape, b.shape
+    assert k == k2
+    c = np.empty((m, n), np.float32)
+    lib().dwo_gemm_f32(_p(c), _p(a), _p(b), m, n, k)
+    return c
+
+
+def gemm_fp16(a, b):
+    """f16 bit patterns (uint16) in and out."""
+    a = np.ascontiguousarray(a, np.uint16)
+    b = np.ascontiguousarray(b, np.uint16)
+    (m, k), (k2, n) = a.shape, b.shape
+    assert k == k2
+    c = np.empty((m, n), np.uint16)
+    lib().dwo_gemm_fp16(_p(c), _p(a), _p(b), m, n, k)
+    return c
+
+
+def gemm_i8(a, b):
+    a = np.ascontiguousarray(a, np.int8)
+    b = np.ascontiguousarray(b, np.int8)
+    (m, k), (k2, n) = a.shape, b.shape
+    assert k == k2
+    c = np.empty((m, n), np.int32)
+    lib().dwo_gemm_i8(_p(c), _p(a), _p(b), m, n, k)
+    return c
+
+
+def global_avg_pool_f32(x):
+    x = np.ascontiguousarray(x, np.float32)
+    n, h, w, c = x.shape
+    y = np.empty((n, c), np.float32)
+    lib().dwo_global_avg_pool_f32(_p(y), _p(x), n, h, w, c)
+    return y
+
+
+def global_avg_pool_fp16(x):
+    x = np.ascontiguousarray(x, np.uint16)
+    n, h, w, c = x.shape
+    y = np.empty((n, c), np.uint16)
+    lib().dwo_global_avg_pool_fp16(_p(y), _p(x), n, h, w, c)
+    return y
+
+
+def softmax_f32(x):
+    """Softmax over the last axis."""
+    x = np.ascontiguousarray(x, np.float32)
+    n = x.shape[-1]
+    y = np.empty_like(x)
+    lib().dwo_softmax_f32(_p(y), _p(x), x.size // n, n)
     return y

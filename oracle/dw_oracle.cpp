@@ -544,6 +544,86 @@ void dwo_fold_batchnorm(float* w, float* bias_out, const float* bias_in, const f
   }
 }
 
+// ---------------------------------------------------------------------------
+// Part A.7 — classifier-head ops
+// ---------------------------------------------------------------------------
+
+// gemm_f32_naive (ops.rs:273-290; gemm_f32_mt :1659-1707 runs the same
+// per-output chain by rows): C[m][n] = A[m][k] B[k][n], acc = fma(a, b, acc)
+// over p in order from +0.
+void dwo_gemm_f32(float* c, const float* a, const float* b, size_t m, size_t n, size_t k) {
+  for (size_t i = 0; i < m; ++i)
+    for (size_t j = 0; j < n; ++j) {
+      float acc = 0.0f;
+      for (size_t p = 0; p < k; ++p) acc = fmaf(a[i * k + p], b[p * n + j], acc);
+      c[i * n + j] = acc;
+    }
+}
+
+// gemm_fp16 (ops.rs:461-479; gemm_fp16_mt :1709-1749): operands widened
+// with F16::to_f32, the same f32 chain, F16::from_f32 of the sum.
+void dwo_gemm_fp16(uint16_t* c, const uint16_t* a, const uint16_t* b, size_t m, size_t n, size_t k) {
+  for (size_t i = 0; i < m; ++i)
+    for (size_t j = 0; j < n; ++j) {
+      float acc = 0.0f;
+      for (size_t p = 0; p < k; ++p) acc = fmaf(dwo_f16_to_f32(a[i * k + p]), dwo_f16_to_f32(b[p * n + j]), acc);
+      c[i * n + j] = dwo_f16_from_f32(acc);
+    }
+}
+
+// gemm_i8_scalar (ops.rs:2981-2995): int32 sum of i8 products (wrapping, as
+// the release build's i32 addition).
+void dwo_gemm_i8(int32_t* c, const int8_t* a, const int8_t* b, size_t m, size_t n, size_t k) {
+  for (size_t i = 0; i < m; ++i)
+    for (size_t j = 0; j < n; ++j) {
+      uint32_t acc = 0;
+      for (size_t p = 0; p < k; ++p) acc += (uint32_t)((int32_t)a[i * k + p] * (int32_t)b[p * n + j]);
+      c[i * n + j] = (int32_t)acc;
+    }
+}
+
+// CpuGraphRuntime::dispatch_global_avg_pool (onnx runtime.rs:1109-1175),
+// NHWC: per (batch, channel) an f32 sum over rows then columns, divided by
+// h * w as f32; f16 widens with F16::to_f32 and stores F16::from_f32.
+void dwo_global_avg_pool_f32(float* y, const float* x, size_t n, size_t h, size_t w, size_t c) {
+  for (size_t b = 0; b < n; ++b)
+    for (size_t ch = 0; ch < c; ++ch) {
+      float sum = 0.0f;
+      for (size_t r = 0; r < h; ++r)
+        for (size_t col = 0; col < w; ++col) sum += x[((b * h + r) * w + col) * c + ch];
+      y[b * c + ch] = sum / (float)(h * w);
+    }
+}
+
+void dwo_global_avg_pool_fp16(uint16_t* y, const uint16_t* x, size_t n, size_t h, size_t w, size_t c) {
+  for (size_t b = 0; b < n; ++b)
+    for (size_t ch = 0; ch < c; ++ch) {
+      float sum = 0.0f;
+      for (size_t r = 0; r < h; ++r)
+        for (size_t col = 0; col < w; ++col) sum += dwo_f16_to_f32(x[((b * h + r) * w + col) * c + ch]);
+      y[b * c + ch] = dwo_f16_from_f32(sum / (float)(h * w));
+    }
+}
+
+// softmax_f32 (ops.rs:1609-1638) over rows of n: max by f32::max from -inf
+// (a NaN operand loses), e = exp(x - max), sum in order, out = e * (1 / sum).
+void dwo_softmax_f32(float* y, const float* x, size_t rows, size_t n) {
+  for (size_t r = 0; r < rows; ++r) {
+    const float* xi = x + r * n;
+    float* yo = y + r * n;
+    float mx = -INFINITY;
+    for (size_t i = 0; i < n; ++i) mx = fmaxf(mx, xi[i]);
+    float sum = 0.0f;
+    for (size_t i = 0; i < n; ++i) {
+      const float e = expf(xi[i] - mx);
+      yo[i] = e;
+      sum += e;
+    }
+    const float inv = 1.0f / sum;
+    for (size_t i = 0; i < n; ++i) yo[i] *= inv;
+  }
+}
+
 // ===========================================================================
 // Part B — ONNX quantized extensions (no counterpart in the reference)
 // ===========================================================================

@@ -1,0 +1,83 @@
+"""GPU parity of the classifier-head ops (Gemm f32 / f16 / int8,
+GlobalAveragePool, Softmax) against the oracle, through the C ABI.
+
+Bars: bit-exact for Gemm and GlobalAveragePool (the reference's order of
+accumulation); Softmax within 1e-5 relative (the device expf and glibc expf
+may differ in the last bits)."""
+import numpy as np
+import pytest
+
+import oracle
+import dragonwing_edge_rs_amd as dw
+from dragonwing_edge_rs_amd import ops
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("mnk", [(32, 1000, 1280), (3, 5, 7), (1, 300, 17)])
+def test_gemm_f32_bit_exact(backend, mnk):
+    m, n, k = mnk
+    r = np.random.default_rng(sum(mnk))
+    a = r.uniform(-1, 1, (m, k)).astype(np.float32)
+    b = r.uniform(-1, 1, (k, n)).astype(np.float32)
+    ba, bb, bc = backend.from_numpy(a), backend.from_numpy(b), backend.alloc(m * n * 4)
+    ops.gemm_f32(backend, ba, bb, bc, m, n, k)
+    np.testing.assert_array_equal(backend.to_numpy(bc, np.float32, (m, n)), oracle.gemm_f32(a, b))
+
+
+@pytest.mark.parametrize("mnk", [(32, 1000, 1280), (2, 70, 9)])
+def test_gemm_fp16_bit_exact(backend, mnk):
+    m, n, k = mnk
+    r = np.random.default_rng(7 + sum(mnk))
+    a = r.normal(0, 1, (m, k)).astype(np.float16).view(np.uint16)
+    b = r.normal(0, 0.1, (k, n)).astype(np.float16).view(np.uint16)
+    a.ravel()[::97] = np.uint16(0x0003)  # subnormal operands: decoded at half value
+    b.ravel()[::89] = np.uint16(0x8201)
+    ba, bb, bc = backend.from_numpy(a), backend.from_numpy(b), backend.alloc(m * n * 2)
+    ops.gemm_fp16(backend, ba, bb, bc, m, n, k)
+    np.testing.assert_array_equal(backend.to_numpy(bc, np.uint16, (m, n)), oracle.gemm_fp16(a, b))
+
+
+def test_gemm_i8_exact(backend):
+    m, n, k = 32, 1000, 1280
+    r = np.random.default_rng(11)
+    a = r.integers(-128, 128, (m, k)).astype(np.int8)
+    b = r.integers(-128, 128, (k, n)).astype(np.int8)
+    ba, bb, bc = backend.from_numpy(a), backend.from_numpy(b), backend.alloc(m * n * 4)
+    ops.gemm_i8(backend, ba, bb, bc, m, n, k)
+    got = backend.to_numpy(bc, np.int32, (m, n))
+    np.testing.assert_array_equal(got, oracle.gemm_i8(a, b))
+    np.testing.assert_array_equal(got, a.astype(np.int64) @ b.astype(np.int64))
+
+
+def test_gemm_rejects_size_mismatch(backend):
+    a, b = backend.alloc(3 * 4 * 4), backend.alloc(4 * 5 * 4)
+    with pytest.raises(dw.HipError):
+        ops.gemm_f32(backend, a, b, backend.alloc(4), 3, 5, 4)
+
+
+@pytest.mark.parametrize("shape", [(32, 7, 7, 1280), (3, 5, 9, 70)])
+def test_global_avg_pool_bit_exact(backend, shape):
+    n, h, w, c = shape
+    r = np.random.default_rng(sum(shape))
+    x = r.normal(0, 2, shape).astype(np.float32)
+    bx, by = backend.from_numpy(x), backend.alloc(n * c * 4)
+    ops.global_avg_pool_nhwc(backend, ops.DTYPE_F32, bx, by, n, h, w, c)
+    np.testing.assert_array_equal(backend.to_numpy(by, np.float32, (n, c)), oracle.global_avg_pool_f32(x))
+    xh = x.astype(np.float16).view(np.uint16)
+    xh.ravel()[::53] = np.uint16(0x0005)
+    bx, by = backend.from_numpy(xh), backend.alloc(n * c * 2)
+    ops.global_avg_pool_nhwc(backend, ops.DTYPE_F16, bx, by, n, h, w, c)
+    np.testing.assert_array_equal(backend.to_numpy(by, np.uint16, (n, c)), oracle.global_avg_pool_fp16(xh))
+
+
+@pytest.mark.parametrize("rows_n", [(32, 1000), (25600, 16), (3, 1)])
+def test_softmax_f32(backend, rows_n):
+    rows, n = rows_n
+    x = np.random.default_rng(rows + n).normal(0, 4, (rows, n)).astype(np.float32)
+    bx, by = backend.from_numpy(x), backend.alloc(x.nbytes)
+    ops.softmax_f32(backend, bx, by, rows, n)
+    got = backend.to_numpy(by, np.float32, (rows, n))
+    ref = oracle.softmax_f32(x)
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-30)
+    np.testing.assert_allclose(got.astype(np.float64).sum(axis=1), 1.0, rtol=1e-5)

@@ -84,6 +84,22 @@ def test_conv_f32_ragged_bit_exact(backend, shape):
     np.testing.assert_array_equal(got, oracle.conv2d_f32_nhwc(x, kk, (s, s), (p, p)))
 
 
+@pytest.mark.parametrize("shape", [(2, 9, 7, 32, 40, 3, 2, 1), (1, 11, 13, 16, 96, 3, 1, 1),
+                                   (3, 6, 5, 48, 33, 5, 1, 2)])
+def test_conv_f32_wide_channels_bit_exact(backend, shape):
+    # c_in a multiple of 16 (vector input loads), channel counts that are not
+    # a multiple of the per-thread channel group, pixel counts that end
+    # part-way through a wavefront, 5x5 taps; bias and ReLU.
+    n, h, w, ci, co, k, s, p = shape
+    rng = np.random.default_rng(sum(shape))
+    x = rng.uniform(-1, 1, (n, h, w, ci)).astype(np.float32)
+    kk = rng.uniform(-1, 1, (k, k, ci, co)).astype(np.float32)
+    b = rng.uniform(-0.1, 0.1, (co,)).astype(np.float32)
+    got = run_conv_f32(backend, x, kk, b, s, p, ops.ACT_RELU)
+    ref = oracle.relu_f32(oracle.bias_add_f32(oracle.conv2d_f32_nhwc(x, kk, (s, s), (p, p)), b))
+    np.testing.assert_array_equal(got, ref)
+
+
 def test_conv_f32_plain_entry(backend):
     x, k, _ = synth.conv_f32_case(0, c_in=16, c_out=8, h=12, w=12)
     n, h, w, ci = x.shape
