@@ -112,18 +112,11 @@ struct EpiLds {
   const uint16_t* bias_h;  // EPI_F16 bias or null
 };
 
-// f16 epilogue chain of CpuGraphRuntime: conv result rounded to f16, then
-// the bias pass, the activation and the residual add, each on stored f16.
-// (The MFMA sums already differ from the reference's order, so these
-// results are held to the fp16 tolerance and SiLU takes silu_f16_fast.)
-__device__ __forceinline__ uint16_t f16_chain(float acc, const uint16_t* bias_h, int ch, int act,
-                                              bool has_res, uint16_t resv) {
-  uint16_t hb = f2h(acc);
-  if (bias_h) hb = f16_add_bits(hb, bias_h[ch]);
-  hb = act == ACT_SILU ? silu_f16_fast(hb) : f16_act_bits(hb, act);
-  if (has_res) hb = f16_add_bits(hb, resv);
-  return hb;
-}
+// f16 epilogue (EPI_F16) is CpuGraphRuntime's chain: conv result rounded to
+// f16, then the bias pass, the activation and the residual add, each on
+// stored f16.  The MFMA sums already differ from the reference's order, so
+// these results are held to the fp16 tolerance, and the store runs the
+// chain two channels at a time in packed f16 (IEEE operands, silu_f16_pk).
 
 // QLinearConv requantization of one accumulator (bias' already added):
 // rint(acc * M) + y_zp, saturated to [0, 255] (ONNX QLinearConv, RNE).
@@ -198,12 +191,25 @@ __device__ __forceinline__ void epilogue4(const IgemmArgs& a, const EpiLds& e, c
     if (a.res)
       rres = *reinterpret_cast<const uint2*>((const uint16_t*)a.res + (size_t)p * a.r_pix_stride +
                                              a.r_c_off + ch);
-    const bool hr = a.res != nullptr;
-    const uint32_t lo = (uint32_t)f16_chain(v[0], e.bias_h, cl + 0, a.act, hr, rres.x & 0xffff) |
-                        ((uint32_t)f16_chain(v[1], e.bias_h, cl + 1, a.act, hr, rres.x >> 16) << 16);
-    const uint32_t hi = (uint32_t)f16_chain(v[2], e.bias_h, cl + 2, a.act, hr, rres.y & 0xffff) |
-                        ((uint32_t)f16_chain(v[3], e.bias_h, cl + 3, a.act, hr, rres.y >> 16) << 16);
-    *reinterpret_cast<uint2*>((uint16_t*)a.y + yo) = make_uint2(lo, hi);
+    // the f16 chain two channels at a time in packed f16
+    h16x2 p01 = pk_f2h(v[0], v[1]), p23 = pk_f2h(v[2], v[3]);
+    if (e.bias_h) {
+      p01 = p01 + pk_make(e.bias_h[cl], e.bias_h[cl + 1]);
+      p23 = p23 + pk_make(e.bias_h[cl + 2], e.bias_h[cl + 3]);
+    }
+    if (a.act == ACT_SILU) {
+      p01 = silu_f16_pk(p01);
+      p23 = silu_f16_pk(p23);
+    } else if (a.act != ACT_NONE) {
+      p01 = pk_make(f16_act_bits(pk_lo(p01), a.act), f16_act_bits(pk_hi(p01), a.act));
+      p23 = pk_make(f16_act_bits(pk_lo(p23), a.act), f16_act_bits(pk_hi(p23), a.act));
+    }
+    if (a.res) {
+      p01 = p01 + __builtin_bit_cast(h16x2, rres.x);
+      p23 = p23 + __builtin_bit_cast(h16x2, rres.y);
+    }
+    *reinterpret_cast<uint2*>((uint16_t*)a.y + yo) =
+        make_uint2(__builtin_bit_cast(uint32_t, p01), __builtin_bit_cast(uint32_t, p23));
   }
 }
 
