@@ -112,15 +112,19 @@ __device__ __forceinline__ void store_outputs_t(const DirectArgs& a, const float
 #pragma unroll
   for (int i = 0; i < NW; ++i) words[i] = 0;
   if constexpr (OUT == 1 && OC % 2 == 0) {
-    // f16 out, no activation: the same packed rounding and bias pass
+    // f16 out, no activation or SiLU: the same packed rounding and bias
+    // pass; SiLU (held to the fp16 tolerance, as every expf-based output)
+    // two values at a time
     float amin = fabsf(acc[0]);
 #pragma unroll
     for (int j = 1; j < OC; ++j) amin = fminf(amin, fabsf(acc[j]));
-    if (a.epi_pk && a.act == ACT_NONE && a.vec_out != 1 && !__any(amin < 6.103515625e-05f)) {
+    if (a.epi_pk && (a.act == ACT_NONE || a.act == ACT_SILU) && a.vec_out != 1 &&
+        !__any(amin < 6.103515625e-05f)) {
 #pragma unroll
       for (int j = 0; j < OC; j += 2) {
         h16x2 p = pk_f2h(acc[j], acc[j + 1]);
         if (a.bias_h) p = p + *reinterpret_cast<const h16x2*>(a.bias_h + oc0 + j);
+        if (a.act == ACT_SILU) p = silu_f16_pk(p);
         words[j >> 1] = __builtin_bit_cast(uint32_t, p);
       }
       if (a.vec_out == 16) {
