@@ -43,6 +43,10 @@ class DwOpParams(C.Structure):
         ("has_relu", I),
         ("epsilon", F),
         ("act", I),
+        ("alpha", F),
+        ("beta", F),
+        ("trans_a", I),
+        ("trans_b", I),
     ]
 
 

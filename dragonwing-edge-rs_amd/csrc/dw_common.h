@@ -159,6 +159,12 @@ void launch_dwconv(hipStream_t st, const DwArgs& a, int dtype);
 // (dtype F32, F16 or I8 with an int32 C); global average pool over NHWC
 // [n][hw][c] -> [n][c]; softmax over rows of n f32 values.
 void launch_gemm(hipStream_t st, int dtype, const void* a, const void* b, void* c, int m, int n, int k);
+// The graph runtime's Gemm (f32 / f16): trans_b takes B as [n][k] and sums
+// with separate multiply and add, as the reference's transposed path does;
+// bias (blen values, column j takes bias[j % blen]) is added after the sum
+// is stored, as the reference's bias pass.
+void launch_gemm_ex(hipStream_t st, int dtype, const void* a, const void* b, void* c, int m, int n, int k,
+                    bool trans_b, const void* bias, int blen);
 void launch_global_avg_pool(hipStream_t st, int dtype, const void* x, void* y, int n, int hw, int c);
 void launch_softmax_rows(hipStream_t st, const float* x, float* y, int rows, int n);
 

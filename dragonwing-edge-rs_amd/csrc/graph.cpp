@@ -556,7 +556,8 @@ std::string to_json(const GraphIR& g) {
     o << "],\"out_h\":" << p.out_h << ",\"out_w\":" << p.out_w << ",\"mode_nearest\":" << p.mode_nearest
       << ",\"scale\":" << fstr(p.scale) << ",\"scale_a_over_out\":" << fstr(p.scale_a_over_out)
       << ",\"scale_b_over_out\":" << fstr(p.scale_b_over_out) << ",\"has_relu\":" << p.has_relu
-      << ",\"epsilon\":" << fstr(p.epsilon) << ",\"act\":" << p.act << "}";
+      << ",\"epsilon\":" << fstr(p.epsilon) << ",\"act\":" << p.act << ",\"trans_a\":" << p.trans_a
+      << ",\"trans_b\":" << p.trans_b << "}";
   }
   o << "]}";
   return o.str();

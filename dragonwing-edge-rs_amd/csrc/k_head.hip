@@ -14,23 +14,47 @@ namespace {
 // lanes (B rows coalesced, A[i][p] the same in every lane).  f32: fma chain
 // from +0 in p order (gemm_f32_naive, ops.rs:273-290).  F16: operands
 // widened with the reference decode (h2f), the same chain, f2h of the sum
-// (gemm_fp16, ops.rs:461-479).
-template <bool F16>
+// (gemm_fp16, ops.rs:461-479).  TB (the graph runtime's transposed path,
+// onnx runtime.rs:1220-1233, :1256-1266): B is [n][k] and each step is a
+// multiply then an add, each rounded.  bias (blen values): the stored sum
+// plus bias[j % blen] (f32 add; f16: F16 of the widened sum).
+template <bool F16, bool TB>
 __global__ __launch_bounds__(256) void gemm_exact_kernel(const void* A, const void* B, void* Cm, int m, int n,
-                                                         int k) {
+                                                         int k, const void* bias, int blen) {
   const int j = blockIdx.x * 256 + threadIdx.x;
   const int i = blockIdx.y;
   if (j >= n || i >= m) return;
   float acc = 0.0f;
+  const size_t bs = TB ? 1 : (size_t)n;  // B step along p
+  const size_t b0 = TB ? (size_t)j * k : (size_t)j;
   if constexpr (F16) {
     const uint16_t* a = (const uint16_t*)A + (size_t)i * k;
-    const uint16_t* b = (const uint16_t*)B + j;
-    for (int p = 0; p < k; ++p) acc = fmaf(h2f(a[p]), h2f(b[(size_t)p * n]), acc);
-    ((uint16_t*)Cm)[(size_t)i * n + j] = f2h(acc);
+    const uint16_t* b = (const uint16_t*)B + b0;
+    for (int p = 0; p < k; ++p) {
+      if constexpr (TB) {
+        float prod = h2f(a[p]) * h2f(b[p * bs]);
+        asm("" : "+v"(prod));  // rounded product, then the add
+        acc = acc + prod;
+      } else {
+        acc = fmaf(h2f(a[p]), h2f(b[p * bs]), acc);
+      }
+    }
+    uint16_t hb = f2h(acc);
+    if (bias) hb = f16_add_bits(hb, ((const uint16_t*)bias)[j % blen]);
+    ((uint16_t*)Cm)[(size_t)i * n + j] = hb;
   } else {
     const float* a = (const float*)A + (size_t)i * k;
-    const float* b = (const float*)B + j;
-    for (int p = 0; p < k; ++p) acc = fmaf(a[p], b[(size_t)p * n], acc);
+    const float* b = (const float*)B + b0;
+    for (int p = 0; p < k; ++p) {
+      if constexpr (TB) {
+        float prod = a[p] * b[p * bs];
+        asm("" : "+v"(prod));
+        acc = acc + prod;
+      } else {
+        acc = fmaf(a[p], b[p * bs], acc);
+      }
+    }
+    if (bias) acc = acc + ((const float*)bias)[j % blen];
     ((float*)Cm)[(size_t)i * n + j] = acc;
   }
 }
@@ -94,13 +118,28 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(const float* X, float
 
 }  // namespace
 
+void launch_gemm_ex(hipStream_t st, int dtype, const void* a, const void* b, void* c, int m, int n, int k,
+                    bool trans_b, const void* bias, int blen) {
+  if (m > 65535) fail(-2, "gemm: more than 65535 rows");
+  const dim3 g((unsigned)((n + 255) / 256), (unsigned)m);
+  if (dtype == F32 && !trans_b)
+    hipLaunchKernelGGL((gemm_exact_kernel<false, false>), g, dim3(256), 0, st, a, b, c, m, n, k, bias, blen);
+  else if (dtype == F32)
+    hipLaunchKernelGGL((gemm_exact_kernel<false, true>), g, dim3(256), 0, st, a, b, c, m, n, k, bias, blen);
+  else if (dtype == F16 && !trans_b)
+    hipLaunchKernelGGL((gemm_exact_kernel<true, false>), g, dim3(256), 0, st, a, b, c, m, n, k, bias, blen);
+  else if (dtype == F16)
+    hipLaunchKernelGGL((gemm_exact_kernel<true, true>), g, dim3(256), 0, st, a, b, c, m, n, k, bias, blen);
+  else
+    fail(-2, "gemm: dtype");
+  DW_HIP(hipGetLastError());
+}
+
 void launch_gemm(hipStream_t st, int dtype, const void* a, const void* b, void* c, int m, int n, int k) {
   const dim3 g((unsigned)((n + 255) / 256), (unsigned)m);
-  if (dtype == F32)
-    hipLaunchKernelGGL((gemm_exact_kernel<false>), g, dim3(256), 0, st, a, b, c, m, n, k);
-  else if (dtype == F16)
-    hipLaunchKernelGGL((gemm_exact_kernel<true>), g, dim3(256), 0, st, a, b, c, m, n, k);
-  else if (dtype == I8)
+  if (dtype == F32 || dtype == F16)
+    return launch_gemm_ex(st, dtype, a, b, c, m, n, k, false, nullptr, 1);
+  if (dtype == I8)
     hipLaunchKernelGGL(gemm_i8_kernel, g, dim3(256), 0, st, (const int8_t*)a, (const int8_t*)b, (int32_t*)c, m, n,
                        k);
   else

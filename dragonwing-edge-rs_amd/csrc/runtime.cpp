@@ -276,6 +276,10 @@ void Runtime::build(Backend* b, const GraphIR& graph, bool stats_mode) {
     if (ti.dims.size() == 4) {
       r.rank4 = true;
       r.n = ti.dims[0]; r.h = ti.dims[1]; r.w = ti.dims[2]; r.c = ti.dims[3];
+    } else if (ti.dims.size() == 2 && !ti.is_init) {
+      // [rows, cols] activations (Gemm, Flatten) as rows pixels of cols channels
+      r.rank4 = true;
+      r.n = ti.dims[0]; r.h = 1; r.w = 1; r.c = ti.dims[1];
     } else {
       r.c = ti.numel();
     }
@@ -670,7 +674,13 @@ void Runtime::lower(std::vector<Group>& groups) {
       groups.push_back(gr);
       continue;
     }
-    if (op.type == "Resize") {
+    if (op.type == "GlobalAveragePool") {
+      gr.kind = "gap";
+    } else if (op.type == "Gemm" || op.type == "MatMul") {
+      gr.kind = "gemm";
+    } else if (op.type == "Flatten") {
+      gr.kind = "flatten";
+    } else if (op.type == "Resize") {
       if (!op.p.mode_nearest) fail(DW_ERR_UNSUPPORTED, "runtime: only nearest Resize is implemented");
       gr.kind = "resize";
     } else if (op.type == "Concat") {
@@ -921,6 +931,60 @@ void Runtime::emit(const Group& gr) {
     L.op = op.name;
     L.bytes = (double)x.bytes() + y.bytes();
     L.fn = [=](hipStream_t st) { launch_resize_nearest(st, a, dt); };
+    launches.push_back(L);
+    return;
+  }
+  if (gr.kind == "gap" || gr.kind == "gemm" || gr.kind == "flatten") {
+    // classifier-head ops: dense tensors only
+    const OpNode& op = g.ops[gr.ops[0]];
+    RtTensor& x = T(op.in[0]);
+    RtTensor& y = T(op.out[0]);
+    auto dense = [](const RtTensor& t) { return t.rank4 && t.pix_stride == t.c && t.abs_off == 0; };
+    if (!dense(x) || !dense(y)) fail(DW_ERR_UNSUPPORTED, "runtime: " + op.type + " on a channel slice");
+    Launch L;
+    L.op = op.name;
+    L.bytes = (double)x.bytes() + y.bytes();
+    const int dt = x.dtype;
+    if (dt != F32 && dt != F16) fail(DW_ERR_UNSUPPORTED, "runtime: " + op.type + " needs f32 or f16");
+    const void* xb = x.base;
+    void* yb = y.base;
+    if (gr.kind == "gap") {
+      if (y.pixels() != x.n || y.c != x.c) fail(DW_ERR_RUNTIME, "GlobalAveragePool: output shape");
+      const int n = (int)x.n, hw = (int)(x.h * x.w), c = (int)x.c;
+      L.kernel = "global_avg_pool";
+      L.fn = [=](hipStream_t st) { launch_global_avg_pool(st, dt, xb, yb, n, hw, c); };
+    } else if (gr.kind == "flatten") {
+      if (x.bytes() != y.bytes()) fail(DW_ERR_RUNTIME, "Flatten: element count");
+      const size_t nb = x.bytes();
+      L.kernel = "copy";
+      L.fn = [=](hipStream_t st) { DW_HIP(hipMemcpyAsync(yb, xb, nb, hipMemcpyDeviceToDevice, st)); };
+    } else {
+      // Gemm / MatMul (dispatch_gemm, onnx runtime.rs:1178-1275): A [m][k]
+      // activation, B an initializer ([k][n], or [n][k] with trans_b),
+      // optional bias over the columns
+      const bool tb = op.type == "Gemm" && op.p.trans_b;
+      if (op.type == "Gemm" && op.p.trans_a) fail(DW_ERR_UNSUPPORTED, "Gemm: transA");
+      const TensorInfo& B = g.t.at(op.in[1]);
+      if (!B.is_init || B.dims.size() != 2) fail(DW_ERR_UNSUPPORTED, "Gemm: B must be a 2-D initializer");
+      const int m = (int)x.n, k = (int)x.c;
+      const int n = (int)(tb ? B.dims[0] : B.dims[1]);
+      if ((tb ? B.dims[1] : B.dims[0]) != k) fail(DW_ERR_RUNTIME, "Gemm: inner dimensions differ");
+      if (y.pixels() != m || y.c != n) fail(DW_ERR_RUNTIME, "Gemm: output shape");
+      if (B.dtype != dt) fail(DW_ERR_UNSUPPORTED, "Gemm: A and B element types differ");
+      const void* wb = upload(B.data.data(), B.data.size());
+      const void* bb = nullptr;
+      int blen = 0;
+      if (op.in.size() > 2 && !op.in[2].empty()) {
+        const TensorInfo& Bi = g.t.at(op.in[2]);
+        if (!Bi.is_init || Bi.dtype != dt) fail(DW_ERR_UNSUPPORTED, "Gemm: bias must be an initializer of A's type");
+        bb = upload(Bi.data.data(), Bi.data.size());
+        blen = (int)Bi.numel();
+        if (blen <= 0) fail(DW_ERR_RUNTIME, "Gemm: empty bias");
+      }
+      L.kernel = "gemm";
+      L.bytes += (double)B.data.size();
+      L.fn = [=](hipStream_t st) { launch_gemm_ex(st, dt, xb, wb, yb, m, n, k, tb, bb, blen); };
+    }
     launches.push_back(L);
     return;
   }

@@ -24,12 +24,13 @@ OP_KIND = {
     "None": 0, "Conv2d": 1, "Add": 2, "Mul": 3, "Sigmoid": 4, "MaxPool": 5, "Concat": 6, "Split": 7,
     "Resize": 8, "BatchNorm": 9, "Requantize": 10, "AddQuantized": 11, "Quantize": 12, "Dequantize": 13,
     "Conv2dRequantReluI8Nhwc": 14, "QLinearConv": 32, "QuantizeLinear": 33, "DequantizeLinear": 34,
-    "QLinearAdd": 35, "QLinearLUT": 36,
+    "QLinearAdd": 35, "QLinearLUT": 36, "Gemm": 15, "GlobalAvgPool": 16,
 }
 # default OpParams kind per op_type
 KIND_OF_TYPE = {"Conv": "Conv2d", "Add": "Add", "Mul": "Mul", "Sigmoid": "Sigmoid", "MaxPool": "MaxPool",
                 "Concat": "Concat", "Split": "Split", "Resize": "Resize", "BatchNormalization": "BatchNorm",
-                "Relu": "None", "SiLU": "None"}
+                "Relu": "None", "SiLU": "None", "Gemm": "Gemm", "MatMul": "None", "Flatten": "None",
+                "GlobalAveragePool": "GlobalAvgPool"}
 
 
 def _params(kind: str, **kw) -> DwOpParams:
@@ -54,6 +55,10 @@ def _params(kind: str, **kw) -> DwOpParams:
     p.has_relu = int(kw.get("has_relu", 0))
     p.epsilon = kw.get("epsilon", 1e-5)
     p.act = kw.get("act", 0)
+    p.alpha = kw.get("alpha", 1.0)
+    p.beta = kw.get("beta", 1.0)
+    p.trans_a = int(kw.get("trans_a", 0))
+    p.trans_b = int(kw.get("trans_b", 0))
     return p
 
 

@@ -297,6 +297,8 @@ typedef enum dw_op_kind {
   DW_OP_QUANTIZE = 12,   /* OpParams::Quantize                                */
   DW_OP_DEQUANTIZE = 13, /* OpParams::Dequantize                              */
   DW_OP_CONV2D_REQUANT_RELU_I8 = 14, /* OpParams::Conv2dRequantReluI8Nhwc     */
+  DW_OP_GEMM = 15,       /* OpParams::Gemm (alpha, beta, trans_a, trans_b)    */
+  DW_OP_GLOBAL_AVG_POOL = 16, /* OpParams::GlobalAvgPool                      */
   /* extensions */
   DW_OP_QLINEAR_CONV = 32,  /* QLinearConv (+ fused LUT activation, + QLinearAdd residual) */
   DW_OP_QUANTIZE_LINEAR = 33,
@@ -323,6 +325,8 @@ typedef struct dw_op_params {
   int has_relu;             /* Conv2dRequantReluI8Nhwc                        */
   float epsilon;            /* BatchNormalization                             */
   int act;                  /* QLinearLUT: DW_ACT_* the table encodes         */
+  float alpha, beta;        /* Gemm (carried; the reference's runtime ignores them) */
+  int trans_a, trans_b;     /* Gemm                                           */
 } dw_op_params;
 
 /* Graph dtypes (dragonwing_core::Dtype subset, crates/dragonwing-core/src/dtype.rs). */

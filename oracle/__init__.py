@@ -94,6 +94,8 @@ def _declare(L: C.CDLL) -> None:
         "dwo_gemm_f32": (None, [_P, _P, _P, _Z, _Z, _Z]),
         "dwo_gemm_fp16": (None, [_P, _P, _P, _Z, _Z, _Z]),
         "dwo_gemm_i8": (None, [_P, _P, _P, _Z, _Z, _Z]),
+        "dwo_gemm_f32_tb": (None, [_P, _P, _P, _Z, _Z, _Z]),
+        "dwo_gemm_fp16_tb": (None, [_P, _P, _P, _Z, _Z, _Z]),
         "dwo_global_avg_pool_f32": (None, [_P, _P, _Z, _Z, _Z, _Z]),
         "dwo_global_avg_pool_fp16": (None, [_P, _P, _Z, _Z, _Z, _Z]),
         "dwo_softmax_f32": (None, [_P, _P, _Z, _Z]),
@@ -493,3 +495,17 @@ def softmax_f32(x):
     y = np.empty_like(x)
     lib().dwo_softmax_f32(_p(y), _p(x), x.size // n, n)
     return y
+
+
+def gemm_tb(a, b):
+    """The graph runtime's transposed Gemm: B is [n][k]; f32 or f16 bits
+    (uint16) by a's dtype; unfused multiply and add."""
+    f16 = a.dtype == np.uint16
+    dt = np.uint16 if f16 else np.float32
+    a = np.ascontiguousarray(a, dt)
+    b = np.ascontiguousarray(b, dt)
+    (m, k), (n, k2) = a.shape, b.shape
+    assert k == k2
+    c = np.empty((m, n), dt)
+    (lib().dwo_gemm_fp16_tb if f16 else lib().dwo_gemm_f32_tb)(_p(c), _p(a), _p(b), m, n, k)
+    return c

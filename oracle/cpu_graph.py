@@ -122,5 +122,28 @@ class CpuGraph:
             parts = oracle.split_channels(ins[0], op["split_sizes"])
             for n, v in zip(out, parts):
                 self.vals[n] = v
+        elif ty == "GlobalAveragePool":
+            x = ins[0]
+            y = oracle.global_avg_pool_f32(x) if x.dtype == np.float32 else oracle.global_avg_pool_fp16(x)
+            self.vals[out[0]] = y.reshape(t[out[0]]["dims"])
+        elif ty == "Flatten":
+            self.vals[out[0]] = ins[0].reshape(t[out[0]]["dims"])
+        elif ty in ("Gemm", "MatMul"):
+            # dispatch_gemm (onnx runtime.rs:1178-1275): the fma path without
+            # transposes, the unfused one with; then the bias pass
+            a, b = ins[0].reshape(-1, ins[0].shape[-1]), ins[1]
+            tb = ty == "Gemm" and op.get("trans_b", 0)
+            if ty == "Gemm" and op.get("trans_a", 0):
+                raise NotImplementedError("Gemm transA")
+            f16 = a.dtype == np.uint16
+            if tb:
+                c = oracle.gemm_tb(a, b)
+            else:
+                c = oracle.gemm_fp16(a, b) if f16 else oracle.gemm_f32(a, b)
+            if len(ins) > 2 and ins[2] is not None:
+                bias = np.ascontiguousarray(ins[2]).ravel()
+                cols = np.ascontiguousarray(bias[np.arange(c.shape[1]) % bias.size])
+                c = oracle.bias_add_f16(c, cols) if f16 else oracle.bias_add_f32(c, cols)
+            self.vals[out[0]] = c.reshape(t[out[0]]["dims"])
         else:
             raise NotImplementedError(f"oracle graph: op type {ty}")

@@ -582,6 +582,34 @@ void dwo_gemm_i8(int32_t* c, const int8_t* a, const int8_t* b, size_t m, size_t 
     }
 }
 
+// CpuGraphRuntime::dispatch_gemm's transposed path (onnx runtime.rs:
+// 1220-1233, f16 :1256-1266) with trans_b: B is [n][k]; sum += a * b with
+// the product rounded before the add (no fma); f16 widens with F16::to_f32
+// and stores F16::from_f32 of the sum.
+void dwo_gemm_f32_tb(float* c, const float* a, const float* b, size_t m, size_t n, size_t k) {
+  for (size_t i = 0; i < m; ++i)
+    for (size_t j = 0; j < n; ++j) {
+      float sum = 0.0f;
+      for (size_t p = 0; p < k; ++p) {
+        volatile float prod = a[i * k + p] * b[j * k + p];
+        sum += prod;
+      }
+      c[i * n + j] = sum;
+    }
+}
+
+void dwo_gemm_fp16_tb(uint16_t* c, const uint16_t* a, const uint16_t* b, size_t m, size_t n, size_t k) {
+  for (size_t i = 0; i < m; ++i)
+    for (size_t j = 0; j < n; ++j) {
+      float sum = 0.0f;
+      for (size_t p = 0; p < k; ++p) {
+        volatile float prod = dwo_f16_to_f32(a[i * k + p]) * dwo_f16_to_f32(b[j * k + p]);
+        sum += prod;
+      }
+      c[i * n + j] = dwo_f16_from_f32(sum);
+    }
+}
+
 // CpuGraphRuntime::dispatch_global_avg_pool (onnx runtime.rs:1109-1175),
 // NHWC: per (batch, channel) an f32 sum over rows then columns, divided by
 // h * w as f32; f16 widens with F16::to_f32 and stores F16::from_f32.

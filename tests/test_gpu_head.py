@@ -81,3 +81,45 @@ def test_softmax_f32(backend, rows_n):
     ref = oracle.softmax_f32(x)
     np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-30)
     np.testing.assert_allclose(got.astype(np.float64).sum(axis=1), 1.0, rtol=1e-5)
+
+
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("trans_b", [0, 1])
+def test_classifier_head_graph_bit_exact(backend, f16, trans_b):
+    # GlobalAveragePool -> Flatten -> Gemm (+ bias), and MatMul, on the graph
+    # runtime against the oracle's CpuGraph (dispatch_global_avg_pool,
+    # dispatch_reshape, dispatch_gemm: fma chain without transposes, separate
+    # multiply and add with trans_b; then the bias pass).
+    from dragonwing_edge_rs_amd.graph import Graph, GRAPH_F16, GRAPH_F32, HipGraphRuntime
+    from oracle.cpu_graph import CpuGraph
+    r = np.random.default_rng(40 + 2 * trans_b + f16)
+    n, h, w, c, k = 5, 7, 7, 64, 100
+    dt = "f16" if f16 else "f32"
+    cast = (lambda a: a.astype(np.float16).view(np.uint16)) if f16 else (lambda a: a.astype(np.float32))
+    x = cast(r.normal(0, 1, (n, h, w, c)))
+    wt = cast(r.normal(0, 0.1, (k, c) if trans_b else (c, k)))
+    b = cast(r.normal(0, 0.1, (k,)))
+    w2 = cast(r.normal(0, 0.1, (k, 10)))
+    g = Graph(GRAPH_F16 if f16 else GRAPH_F32)
+    g.add_tensor("x", x.shape, dt)
+    g.add_tensor("pool", (n, 1, 1, c), dt)
+    g.add_tensor("flat", (n, c), dt)
+    g.add_initializer("w", wt, dt)
+    g.add_initializer("b", b, dt)
+    g.add_initializer("w2", w2, dt)
+    g.add_tensor("logits", (n, k), dt)
+    g.add_tensor("out", (n, 10), dt)
+    g.add_op("gap", "GlobalAveragePool", ["x"], ["pool"])
+    g.add_op("flatten", "Flatten", ["pool"], ["flat"])
+    g.add_op("fc", "Gemm", ["flat", "w", "b"], ["logits"], trans_b=trans_b)
+    g.add_op("mm", "MatMul", ["logits", "w2"], ["out"])
+    g.set_io(["x"], ["logits", "out"])
+    rt = HipGraphRuntime(g, backend)
+    rt.set_input_bytes("x", x)
+    rt.run()
+    cg = CpuGraph(g.to_dict(), g.initializer)
+    cg.set_input("x", x)
+    ref = cg.run()
+    for o, shp in (("logits", (n, k)), ("out", (n, 10))):
+        got = rt.get_output_bytes(o).view(np.uint16 if f16 else np.float32).reshape(shp)
+        np.testing.assert_array_equal(got, ref[o], err_msg=o)

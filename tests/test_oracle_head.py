@@ -93,3 +93,42 @@ def test_softmax_known_answer_and_f64():
     x = np.random.default_rng(4).normal(0, 3, (6, 17)).astype(np.float32)
     e = np.exp(x.astype(np.float64) - x.max(axis=1, keepdims=True))
     np.testing.assert_allclose(oracle.softmax_f32(x), e / e.sum(axis=1, keepdims=True), rtol=1e-6, atol=0)
+
+
+def test_gemm_tb_is_unfused_and_transposed():
+    # B given as [n][k]; each step rounds the product before the add: after
+    # -(1 + 2^-11), the product (1 + 2^-12)^2 = 1 + 2^-11 + 2^-24 rounds to
+    # 1 + 2^-11 and the sum is 0; an fma keeps the 2^-24
+    a = np.array([[-1.0, 1 + 2.0 ** -12]], np.float32)
+    b = np.array([[1 + 2.0 ** -11, 1 + 2.0 ** -12]], np.float32)
+    assert float(oracle.gemm_tb(a, b)[0, 0]) == 0.0
+    assert float(oracle.gemm_f32(a, b.T.copy())[0, 0]) == 2.0 ** -24
+
+
+def test_classifier_head_graph_matches_f64():
+    # GlobalAveragePool -> Flatten -> Gemm(trans_b, bias) on the oracle's
+    # CpuGraph against a float64 evaluation (catches a transposed weight)
+    import __graft_entry__
+    __graft_entry__.import_pkg()
+    from dragonwing_edge_rs_amd.graph import Graph, GRAPH_F32
+    from oracle.cpu_graph import CpuGraph
+    r = np.random.default_rng(1)
+    n, h, w, c, k = 3, 5, 5, 16, 12
+    x = r.normal(0, 1, (n, h, w, c)).astype(np.float32)
+    wt = r.normal(0, 0.1, (k, c)).astype(np.float32)
+    b = r.normal(0, 0.1, (k,)).astype(np.float32)
+    g = Graph(GRAPH_F32)
+    g.add_tensor("x", x.shape, "f32")
+    g.add_tensor("pool", (n, 1, 1, c), "f32")
+    g.add_tensor("flat", (n, c), "f32")
+    g.add_initializer("w", wt, "f32")
+    g.add_initializer("b", b, "f32")
+    g.add_tensor("y", (n, k), "f32")
+    g.add_op("gap", "GlobalAveragePool", ["x"], ["pool"])
+    g.add_op("flatten", "Flatten", ["pool"], ["flat"])
+    g.add_op("fc", "Gemm", ["flat", "w", "b"], ["y"], trans_b=1)
+    g.set_io(["x"], ["y"])
+    cg = CpuGraph(g.to_dict(), g.initializer)
+    cg.set_input("x", x)
+    ref = x.astype(np.float64).mean(axis=(1, 2)) @ wt.T.astype(np.float64) + b
+    np.testing.assert_allclose(cg.run()["y"], ref, rtol=0, atol=1e-5)
