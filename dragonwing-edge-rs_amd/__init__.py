@@ -18,9 +18,10 @@ import ctypes as C
 
 import numpy as np
 
-from ._lib import HipError, check, load
+from ._lib import (RELEASE_BACKEND, RELEASE_BUFFER, HipError, check, load, native_calls_allowed,
+                   release_all, track)
 
-__all__ = ["Backend", "Buffer", "HipError", "load", "BUFFER_STORAGE"]
+__all__ = ["Backend", "Buffer", "HipError", "load", "release_all", "BUFFER_STORAGE"]
 
 BUFFER_STORAGE = 0
 
@@ -32,6 +33,7 @@ class Buffer:
         self._backend = backend
         self._h = handle
         self._len = len_bytes
+        track(self, RELEASE_BUFFER)
 
     @property
     def handle(self) -> int:
@@ -46,13 +48,18 @@ class Buffer:
         return load().dw_hip_buffer_device_ptr(self.handle)
 
     def free(self) -> None:
-        if self._h is not None and self._backend._h is not None:
+        # The C buffer holds its backend (reference-counted there), so it is
+        # freed even after the Python Backend was closed.
+        if self._h is not None:
             load().dw_hip_buffer_free(self._h)
         self._h = None
 
+    _release = free
+
     def __del__(self):
         try:
-            self.free()
+            if native_calls_allowed():
+                self.free()
         except Exception:
             pass
 
@@ -65,7 +72,7 @@ class Backend:
         h = C.c_void_p()
         check(lib.dw_hip_backend_create(device, C.byref(h)))
         self._h = h.value
-        self._buffers: list = []
+        track(self, RELEASE_BACKEND)
 
     @property
     def handle(self) -> int:
@@ -108,8 +115,11 @@ class Backend:
             load().dw_hip_backend_destroy(self._h)
             self._h = None
 
+    _release = close
+
     def __del__(self):
         try:
-            self.close()
+            if native_calls_allowed():
+                self.close()
         except Exception:
             pass

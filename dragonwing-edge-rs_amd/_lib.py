@@ -5,8 +5,11 @@ every entry point raises; there is no CPU fallback.
 """
 from __future__ import annotations
 
+import atexit
 import ctypes as C
 import re
+import sys
+import weakref
 from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
@@ -47,6 +50,8 @@ class DwOpParams(C.Structure):
         ("beta", F),
         ("trans_a", I),
         ("trans_b", I),
+        ("clip_min", F),
+        ("clip_max", F),
     ]
 
 
@@ -111,6 +116,7 @@ SIGNATURES = {
     "dw_graph_fold_batchnorm": (I, [P]),
     "dw_graph_convert_nchw_to_nhwc": (I, [P]),
     "dw_graph_apply_fusion_passes": (I, [P, C.POINTER(I)]),
+    "dw_op_params_size": (Z, []),
     "dw_graph_convert_to_f16": (I, [P]),
     "dw_graph_set_activation_range": (I, [P, S, F, F]),
     "dw_graph_quantize_qdq": (I, [P, P, I]),
@@ -138,6 +144,42 @@ SIGNATURES = {
 }
 
 _lib = None
+
+# Live native handles, released in this order at interpreter exit: graph
+# runtimes (streams, events, captured graphs, device memory), then buffers,
+# then backends, then host-only graph IRs.  Objects left to the garbage
+# collector during interpreter finalization would otherwise be destroyed in
+# whatever order it reaches them, possibly after modules they need are torn
+# down; at exit they are released here instead, while the HIP runtime is
+# fully up, and their finalizers do nothing afterwards.
+RELEASE_RUNTIME, RELEASE_BUFFER, RELEASE_BACKEND, RELEASE_GRAPH = 0, 1, 2, 3
+_live = {k: weakref.WeakSet() for k in (RELEASE_RUNTIME, RELEASE_BUFFER, RELEASE_BACKEND, RELEASE_GRAPH)}
+_released = False
+
+
+def track(obj, order: int) -> None:
+    """Registers an object with a ``_release()`` method for ordered teardown."""
+    _live[order].add(obj)
+
+
+def native_calls_allowed() -> bool:
+    """False once the exit hook has run or the interpreter is finalizing."""
+    return not _released and not sys.is_finalizing()
+
+
+@atexit.register
+def release_all() -> None:
+    """Releases every live handle (runtimes, buffers, backends, graphs)."""
+    global _released
+    if _released:
+        return
+    for order in sorted(_live):
+        for obj in list(_live[order]):
+            try:
+                obj._release()
+            except Exception:
+                pass
+    _released = True
 
 
 class HipError(RuntimeError):

@@ -220,6 +220,7 @@ const char* dw_hip_backend_name(const dw_hip_backend* be) {
 int dw_hip_alloc(dw_hip_backend* be, size_t len_bytes, int kind, dw_hip_buffer** out) {
   API_BEGIN
   Backend* b = B(be);
+  std::lock_guard<std::mutex> lock(b->mu);
   if (kind != DW_BUFFER_STORAGE) dw::fail(DW_ERR_UNSUPPORTED, "unknown buffer kind");
   if (!out) dw::fail(DW_ERR_INVALID, "null out");
   void* p = nullptr;
@@ -248,6 +249,7 @@ void* dw_hip_buffer_device_ptr(const dw_hip_buffer* buf) { return buf ? buf->ptr
 int dw_hip_upload(dw_hip_backend* be, dw_hip_buffer* dst, const void* src, size_t len) {
   API_BEGIN
   Backend* b = B(be);
+  std::lock_guard<std::mutex> lock(b->mu);
   if (!dst) dw::fail(DW_ERR_INVALID, "null buffer");
   if (len != dst->len)
     dw::fail(DW_ERR_INVALID, "upload size mismatch: buffer " + std::to_string(dst->len) +
@@ -262,6 +264,7 @@ int dw_hip_upload(dw_hip_backend* be, dw_hip_buffer* dst, const void* src, size_
 int dw_hip_download(dw_hip_backend* be, const dw_hip_buffer* src, void* dst, size_t len) {
   API_BEGIN
   Backend* b = B(be);
+  std::lock_guard<std::mutex> lock(b->mu);
   if (!src) dw::fail(DW_ERR_INVALID, "null buffer");
   if (len != src->len)
     dw::fail(DW_ERR_INVALID, "download size mismatch: buffer " + std::to_string(src->len) +
@@ -277,6 +280,7 @@ int dw_hip_download(dw_hip_backend* be, const dw_hip_buffer* src, void* dst, siz
 int dw_hip_synchronize(dw_hip_backend* be) {
   API_BEGIN
   Backend* b = B(be);
+  std::lock_guard<std::mutex> lock(b->mu);
   DW_HIP(hipStreamSynchronize(b->stream));
   API_END
 }
@@ -291,6 +295,7 @@ static int conv_f32_common(dw_hip_backend* be, const dw_hip_buffer* input, const
                            size_t stride_h, size_t stride_w, size_t pad_h, size_t pad_w, int act) {
   API_BEGIN
   Backend* b = B(be);
+  std::lock_guard<std::mutex> lock(b->mu);
   Geo g = geo(n, h_in, w_in, c_in, c_out, k_h, k_w, stride_h, stride_w, pad_h, pad_w);
   need(input, n * h_in * w_in * c_in * 4, "conv2d_f32: input");
   need(kernel, k_h * k_w * c_in * c_out * 4, "conv2d_f32: kernel");
@@ -331,6 +336,7 @@ int dw_hip_conv2d_bias_act_f16_nhwc(dw_hip_backend* be, const dw_hip_buffer* inp
                                     int act, int exact) {
   API_BEGIN
   Backend* b = B(be);
+  std::lock_guard<std::mutex> lock(b->mu);
   Geo g = geo(n, h_in, w_in, c_in, c_out, k_h, k_w, stride_h, stride_w, pad_h, pad_w);
   need(input, n * h_in * w_in * c_in * 2, "conv2d_fp16: input");
   need(kernel, k_h * k_w * c_in * c_out * 2, "conv2d_fp16: kernel");
@@ -366,6 +372,7 @@ static int dwconv_common(dw_hip_backend* be, int dtype, const dw_hip_buffer* inp
                          size_t stride_h, size_t stride_w, size_t pad_h, size_t pad_w, int act) {
   API_BEGIN
   Backend* b = B(be);
+  std::lock_guard<std::mutex> lock(b->mu);
   const size_t es = dtype == DW_DTYPE_F16 ? 2 : 4;
   Geo g = geo(n, h_in, w_in, c, c, k_h, k_w, stride_h, stride_w, pad_h, pad_w);
   // f16 3x3 with stride 1 or 2 runs on the sliding-window kernel (channel
@@ -412,6 +419,7 @@ int dw_hip_qlinearconv_u8s8(dw_hip_backend* be, const dw_hip_buffer* input, cons
                             float x_scale, int x_zp, const float* w_scales, float y_scale, int y_zp) {
   API_BEGIN
   Backend* b = B(be);
+  std::lock_guard<std::mutex> lock(b->mu);
   Geo g = geo(n, h_in, w_in, c_in, c_out, k_h, k_w, stride_h, stride_w, pad_h, pad_w);
   require_igemm(g, 1);
   need(input, n * h_in * w_in * c_in, "qlinearconv: input");
@@ -451,6 +459,7 @@ int dw_hip_conv2d_i8_nhwc(dw_hip_backend* be, const dw_hip_buffer* input, const 
                           size_t pad_h, size_t pad_w) {
   API_BEGIN
   Backend* b = B(be);
+  std::lock_guard<std::mutex> lock(b->mu);
   Geo g = geo(n, h_in, w_in, c_in, c_out, k_h, k_w, stride_h, stride_w, pad_h, pad_w);
   require_igemm(g, 1);
   need(input, n * h_in * w_in * c_in, "conv2d_i8: input");
@@ -470,6 +479,7 @@ int dw_hip_conv2d_requant_relu_i8(dw_hip_backend* be, const dw_hip_buffer* input
                                   size_t pad_w, float requant_scale, int do_relu) {
   API_BEGIN
   Backend* b = B(be);
+  std::lock_guard<std::mutex> lock(b->mu);
   Geo g = geo(n, h_in, w_in, c_in, c_out, k_h, k_w, stride_h, stride_w, pad_h, pad_w);
   require_igemm(g, 1);
   need(input, n * h_in * w_in * c_in, "conv_fused: input");
@@ -489,14 +499,14 @@ int dw_hip_conv2d_requant_relu_i8(dw_hip_backend* be, const dw_hip_buffer* input
 // ---------------------------------------------------------------------------
 #define EW1(NAME, OP, DT, IES, OES)                                                              \
   int NAME(dw_hip_backend* be, const dw_hip_buffer* x, dw_hip_buffer* y, size_t count) {         \
-    API_BEGIN Backend* b = B(be);                                                               \
+    API_BEGIN Backend* b = B(be); std::lock_guard<std::mutex> lock(b->mu);                       \
     ew(b, OP, DT, x, nullptr, y, count, IES, OES);                                              \
     API_END                                                                                      \
   }
 #define EW2(NAME, OP, DT, ES)                                                                    \
   int NAME(dw_hip_backend* be, const dw_hip_buffer* a, const dw_hip_buffer* bb, dw_hip_buffer* y, \
            size_t count) {                                                                       \
-    API_BEGIN Backend* b = B(be);                                                               \
+    API_BEGIN Backend* b = B(be); std::lock_guard<std::mutex> lock(b->mu);                       \
     ew(b, OP, DT, a, bb, y, count, ES, ES);                                                     \
     API_END                                                                                      \
   }
@@ -517,6 +527,7 @@ int dw_hip_bias_add_f32_nhwc(dw_hip_backend* be, dw_hip_buffer* y, const dw_hip_
                              size_t count, size_t c) {
   API_BEGIN
   Backend* b = B(be);
+  std::lock_guard<std::mutex> lock(b->mu);
   need(y, count * 4, "bias_add: y");
   need(bias, c * 4, "bias_add: bias");
   if (c == 0 || count % c != 0) dw::fail(DW_ERR_INVALID, "bias_add: count must be a multiple of c");
@@ -531,6 +542,7 @@ int dw_hip_requantize_i32_to_i8(dw_hip_backend* be, const dw_hip_buffer* x_i32, 
                                 size_t count, float requant_scale) {
   API_BEGIN
   Backend* b = B(be);
+  std::lock_guard<std::mutex> lock(b->mu);
   ew(b, dw::EW_REQUANT_I32_I8, dw::I32, x_i32, nullptr, y_i8, count, 4, 1, requant_scale);
   API_END
 }
@@ -539,6 +551,7 @@ int dw_hip_quantize_f32_to_i8(dw_hip_backend* be, const dw_hip_buffer* x, dw_hip
                               size_t count, float scale) {
   API_BEGIN
   Backend* b = B(be);
+  std::lock_guard<std::mutex> lock(b->mu);
   const float inv = 1.0f / scale;  // quantize_f32_to_i8 (ops.rs:3503-3516) multiplies by 1/scale
   ew(b, dw::EW_QUANT_F32_I8, dw::F32, x, nullptr, y_i8, count, 4, 1, inv);
   API_END
@@ -548,6 +561,7 @@ int dw_hip_dequantize_i8_to_f32(dw_hip_backend* be, const dw_hip_buffer* x_i8, d
                                 size_t count, float scale) {
   API_BEGIN
   Backend* b = B(be);
+  std::lock_guard<std::mutex> lock(b->mu);
   ew(b, dw::EW_DEQUANT_I8_F32, dw::I8, x_i8, nullptr, y, count, 1, 4, scale);
   API_END
 }
@@ -556,6 +570,7 @@ int dw_hip_add_i8(dw_hip_backend* be, const dw_hip_buffer* a, const dw_hip_buffe
                   size_t count, float scale_a_over_y, float scale_b_over_y) {
   API_BEGIN
   Backend* b = B(be);
+  std::lock_guard<std::mutex> lock(b->mu);
   ew(b, dw::EW_ADD_I8, dw::I8, a, bb, y, count, 1, 1, scale_a_over_y, scale_b_over_y);
   API_END
 }
@@ -564,6 +579,7 @@ int dw_hip_quantize_linear_f16_u8(dw_hip_backend* be, const dw_hip_buffer* x, dw
                                   size_t count, float scale, int zp) {
   API_BEGIN
   Backend* b = B(be);
+  std::lock_guard<std::mutex> lock(b->mu);
   ew(b, dw::EW_QUANT_LINEAR_F16_U8, dw::F16, x, nullptr, y, count, 2, 1, scale, 0, zp);
   API_END
 }
@@ -572,6 +588,7 @@ int dw_hip_dequantize_linear_u8_f16(dw_hip_backend* be, const dw_hip_buffer* x, 
                                     size_t count, float scale, int zp) {
   API_BEGIN
   Backend* b = B(be);
+  std::lock_guard<std::mutex> lock(b->mu);
   ew(b, dw::EW_DEQUANT_LINEAR_U8_F16, dw::U8, x, nullptr, y, count, 1, 2, scale, 0, zp);
   API_END
 }
@@ -581,6 +598,7 @@ int dw_hip_qlinear_add_u8(dw_hip_backend* be, const dw_hip_buffer* a, const dw_h
                           int b_zp, float y_scale, int y_zp) {
   API_BEGIN
   Backend* b = B(be);
+  std::lock_guard<std::mutex> lock(b->mu);
   const float ra = a_scale / y_scale, rb = b_scale / y_scale;
   ew(b, dw::EW_QADD_U8, dw::U8, a, bb, y, count, 1, 1, ra, rb, a_zp, b_zp, y_zp);
   API_END
@@ -590,6 +608,7 @@ int dw_hip_lut_u8(dw_hip_backend* be, const dw_hip_buffer* x, dw_hip_buffer* y, 
                   const uint8_t* lut256) {
   API_BEGIN
   Backend* b = B(be);
+  std::lock_guard<std::mutex> lock(b->mu);
   if (!lut256) dw::fail(DW_ERR_INVALID, "lut: null table");
   uint8_t* lut = (uint8_t*)b->workspace(Backend::WS_LUT, 256);
   b->upload_async(lut, lut256, 256);
@@ -607,6 +626,7 @@ int dw_hip_maxpool2d_nhwc(dw_hip_backend* be, int dtype, const dw_hip_buffer* x,
                           size_t pad_r) {
   API_BEGIN
   Backend* b = B(be);
+  std::lock_guard<std::mutex> lock(b->mu);
   if (dtype != DW_DTYPE_F32 && dtype != DW_DTYPE_F16 && dtype != DW_DTYPE_U8 && dtype != DW_DTYPE_I8)
     dw::fail(DW_ERR_UNSUPPORTED, "maxpool: dtype");
   if (!pool_h || !pool_w || !stride_h || !stride_w) dw::fail(DW_ERR_INVALID, "maxpool: zero size");
@@ -633,6 +653,7 @@ int dw_hip_resize_nearest_nhwc(dw_hip_backend* be, int dtype, const dw_hip_buffe
                                size_t n, size_t h_in, size_t w_in, size_t h_out, size_t w_out, size_t c) {
   API_BEGIN
   Backend* b = B(be);
+  std::lock_guard<std::mutex> lock(b->mu);
   const size_t es = dw::dtype_size(dtype);
   if (!h_in || !w_in || !h_out || !w_out) dw::fail(DW_ERR_INVALID, "resize: zero size");
   need(x, n * h_in * w_in * c * es, "resize: input");
@@ -650,6 +671,7 @@ int dw_hip_concat_channels_nhwc(dw_hip_backend* be, int dtype, const dw_hip_buff
                                 size_t pixels) {
   API_BEGIN
   Backend* b = B(be);
+  std::lock_guard<std::mutex> lock(b->mu);
   const size_t es = dw::dtype_size(dtype);
   size_t total = 0;
   for (size_t i = 0; i < num_inputs; ++i) total += channels[i];
@@ -669,6 +691,7 @@ int dw_hip_split_channels_nhwc(dw_hip_backend* be, int dtype, const dw_hip_buffe
                                size_t num_outputs, size_t pixels) {
   API_BEGIN
   Backend* b = B(be);
+  std::lock_guard<std::mutex> lock(b->mu);
   const size_t es = dw::dtype_size(dtype);
   size_t total = 0;
   for (size_t i = 0; i < num_outputs; ++i) total += channels[i];
@@ -689,6 +712,7 @@ int dw_hip_gemm_f32(dw_hip_backend* be, const dw_hip_buffer* a, const dw_hip_buf
                     size_t m, size_t n, size_t k) {
   API_BEGIN
   Backend* bk = B(be);
+  std::lock_guard<std::mutex> lock(bk->mu);
   if (!m || !n || !k) dw::fail(DW_ERR_INVALID, "gemm_f32: zero size");
   if (m > 65535 || n > INT32_MAX || k > INT32_MAX) dw::fail(DW_ERR_UNSUPPORTED, "gemm_f32: m > 65535 or n, k > 2^31 - 1");
   need(a, m * k * 4, "gemm_f32: A size");
@@ -702,6 +726,7 @@ int dw_hip_gemm_fp16(dw_hip_backend* be, const dw_hip_buffer* a, const dw_hip_bu
                      size_t m, size_t n, size_t k) {
   API_BEGIN
   Backend* bk = B(be);
+  std::lock_guard<std::mutex> lock(bk->mu);
   if (!m || !n || !k) dw::fail(DW_ERR_INVALID, "gemm_fp16: zero size");
   if (m > 65535 || n > INT32_MAX || k > INT32_MAX) dw::fail(DW_ERR_UNSUPPORTED, "gemm_fp16: m > 65535 or n, k > 2^31 - 1");
   need(a, m * k * 2, "gemm_fp16: A size");
@@ -715,6 +740,7 @@ int dw_hip_gemm_i8(dw_hip_backend* be, const dw_hip_buffer* a, const dw_hip_buff
                    size_t m, size_t n, size_t k) {
   API_BEGIN
   Backend* bk = B(be);
+  std::lock_guard<std::mutex> lock(bk->mu);
   if (!m || !n || !k) dw::fail(DW_ERR_INVALID, "gemm_i8: zero size");
   if (m > 65535 || n > INT32_MAX || k > INT32_MAX) dw::fail(DW_ERR_UNSUPPORTED, "gemm_i8: m > 65535 or n, k > 2^31 - 1");
   need(a, m * k, "gemm_i8: A size");
@@ -728,6 +754,7 @@ int dw_hip_global_avg_pool_nhwc(dw_hip_backend* be, int dtype, const dw_hip_buff
                                 size_t n, size_t h, size_t w, size_t c) {
   API_BEGIN
   Backend* bk = B(be);
+  std::lock_guard<std::mutex> lock(bk->mu);
   if (dtype != DW_DTYPE_F32 && dtype != DW_DTYPE_F16)
     dw::fail(DW_ERR_UNSUPPORTED, "global_avg_pool: unsupported dtype");
   if (!n || !h || !w || !c) dw::fail(DW_ERR_INVALID, "global_avg_pool: zero size");
@@ -742,6 +769,7 @@ int dw_hip_global_avg_pool_nhwc(dw_hip_backend* be, int dtype, const dw_hip_buff
 int dw_hip_softmax_f32(dw_hip_backend* be, const dw_hip_buffer* x, dw_hip_buffer* y, size_t rows, size_t n) {
   API_BEGIN
   Backend* bk = B(be);
+  std::lock_guard<std::mutex> lock(bk->mu);
   if (!rows || !n) dw::fail(DW_ERR_INVALID, "softmax_f32: zero size");
   if (rows > INT32_MAX || n > INT32_MAX) dw::fail(DW_ERR_UNSUPPORTED, "softmax_f32: size");
   need(x, rows * n * 4, "softmax_f32: input size");

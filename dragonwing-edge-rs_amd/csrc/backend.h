@@ -4,6 +4,7 @@
 #include "dw_common.h"
 
 #include <atomic>
+#include <mutex>
 
 namespace dw {
 
@@ -12,6 +13,12 @@ void set_last_error(const std::string& m);
 // One device, one in-order stream (default priority).  Op functions that need
 // temporary device memory (packed weights, per-channel scales) use grow-only
 // workspaces owned by the backend, so repeated calls do not allocate.
+//
+// Thread safety: every entry point that touches the stream or the
+// workspaces holds `mu` for its whole sequence (workspace sizing, parameter
+// uploads, launches), so one backend can be shared by several host threads
+// (the reference's backends are Send + Sync, backend.rs:42-48).  Work from
+// different threads is queued in the order the lock is taken.
 struct Backend {
   enum { WS_WPACK = 0, WS_SCALE = 1, WS_BIAS = 2, WS_LUT = 3, kWsSlots = 4 };
   struct Ws {
@@ -22,6 +29,7 @@ struct Backend {
   int num_cus = 0;
   hipStream_t stream = nullptr;
   Ws ws[kWsSlots];
+  std::mutex mu;
 
   // Holders: the handle itself, every buffer and every graph runtime made
   // on it (as the reference's Arc<Backend>): destroying the handle while

@@ -167,13 +167,14 @@ void launch_gemm_ex(hipStream_t st, int dtype, const void* a, const void* b, voi
                     bool trans_b, const void* bias, int blen);
 void launch_global_avg_pool(hipStream_t st, int dtype, const void* x, void* y, int n, int hw, int c);
 void launch_softmax_rows(hipStream_t st, const float* x, float* y, int rows, int n);
+void launch_softmax_rows_t(hipStream_t st, int dtype, const void* x, void* y, int rows, int n);
 
 // Elementwise glue (count elements, contiguous).
 enum EwOp : int {
   EW_RELU = 0, EW_ADD, EW_MUL, EW_SIGMOID, EW_SILU, EW_BIAS_ADD,
   EW_REQUANT_I32_I8, EW_QUANT_F32_I8, EW_DEQUANT_I8_F32, EW_ADD_I8, EW_RELU_I8,
   EW_QUANT_LINEAR_F16_U8, EW_DEQUANT_LINEAR_U8_F16, EW_QADD_U8, EW_LUT_U8,
-  EW_F32_TO_F16, EW_F16_TO_F32
+  EW_F32_TO_F16, EW_F16_TO_F32, EW_CLIP
 };
 struct EwArgs {
   int op;

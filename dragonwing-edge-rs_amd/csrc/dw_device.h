@@ -15,9 +15,17 @@ __device__ __forceinline__ float h2f_ieee(uint16_t b) { return (float)__builtin_
 // v_fma_mixlo_f16, which rounds the exact sum to f16 once, not to f32 and
 // then to f16 as the reference does (the two differ by an f16 ulp when the
 // f32 rounding lands on an f16 rounding midpoint).
+// A NaN is encoded as F16::from_f32_soft does (dtype.rs:173-178): its sign,
+// the quiet bit and the top payload bits clamped below it, sign | 0x7E00 |
+// min(mant >> 13, 0x1FF) (so a quiet f32 NaN gives 0x7FFF, where the
+// hardware conversion gives 0x7E00).  The packed conversions (pk_f2h) and
+// packed f16 arithmetic keep the hardware's NaN encoding.
 __device__ __forceinline__ uint16_t f2h(float f) {
   asm("" : "+v"(f));
-  return __builtin_bit_cast(uint16_t, (_Float16)f);
+  const uint16_t h = __builtin_bit_cast(uint16_t, (_Float16)f);
+  const uint32_t b = __builtin_bit_cast(uint32_t, f);
+  const uint32_t nan_bits = ((b >> 16) & 0x8000u) | 0x7E00u | min((b & 0x7FFFFFu) >> 13, 0x1FFu);
+  return __builtin_isnan(f) ? (uint16_t)nan_bits : h;
 }
 
 // F16::to_f32_soft (crates/dragonwing-core/src/dtype.rs:226-263).  It is the

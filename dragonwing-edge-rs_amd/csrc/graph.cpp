@@ -126,6 +126,9 @@ std::string jesc(const std::string& s) {
 }
 
 std::string fstr(float f) {
+  // infinities as out-of-range literals that JSON readers take as +-inf
+  if (isinf(f)) return f > 0 ? "1e999" : "-1e999";
+  if (isnan(f)) return "NaN";
   char b[64];
   snprintf(b, sizeof b, "%.9g", (double)f);
   return b;
@@ -227,35 +230,146 @@ void convert_nchw_to_nhwc(GraphIR& g) {
 }
 
 // --------------------------------------------------------------------------
-// apply_fusion_passes, SiLU pattern (fusion.rs:126-190): Sigmoid(x) = s and
-// Mul(x, s) = y (either operand order), s used only by that Mul, become
-// CompiledOp{op_type "SiLU", params None, inputs [x], outputs [y]}.
+// apply_fusion_passes (fusion.rs:42-348).  As in the reference, all three
+// passes look at one snapshot of the op list (producer = last op writing a
+// tensor, consumers = ops reading it), record replacements and removals, and
+// apply them at the end:
+//  1. Relu whose input is written by a Conv read by nothing else: the Conv
+//     becomes "<conv>_fused_relu" writing the Relu's output (fusion.rs:65-123).
+//     The reference keeps plain Conv2d params there and so loses the ReLU;
+//     here has_relu = 1 carries it (the runtimes apply it after the bias).
+//  2. Mul(x, Sigmoid(x)) with the Sigmoid read only by that Mul becomes
+//     SiLU "<mul>_silu" (fusion.rs:125-190).  The reference inspects the
+//     first operand's producer and gives up when it is not the Sigmoid, so
+//     Mul(x, s) with x written by an op is never fused there; both operand
+//     orders are matched here.
+//  3. Requantize writing tensor t, with the closest earlier group-1,
+//     bias-free Conv also writing t, becomes Conv2dRequantReluI8
+//     "<conv>_fused_qrelu" (+ the Relu when it is t's only other reader)
+//     (fusion.rs:192-334).
+// Tensors no op reads or writes afterwards (and that are not graph inputs or
+// outputs) are dropped from the IR.
 // --------------------------------------------------------------------------
-int fuse_silu(GraphIR& g) {
-  int fused = 0;
-  for (size_t i = 0; i < g.ops.size(); ++i) {
-    if (g.ops[i].type != "Sigmoid") continue;
-    const std::string x = g.ops[i].in[0], s = g.ops[i].out[0];
-    auto cs = g.consumers(s);
-    if (cs.size() != 1 || g.is_output(s)) continue;
-    OpNode& mul = g.ops[cs[0]];
-    if (mul.type != "Mul" || mul.in.size() != 2) continue;
-    if (!((mul.in[0] == x && mul.in[1] == s) || (mul.in[0] == s && mul.in[1] == x))) continue;
-    OpNode silu;
-    silu.name = mul.name.empty() ? g.ops[i].name + "_silu" : mul.name;
-    silu.type = "SiLU";
-    silu.in = {x};
-    silu.out = mul.out;
-    silu.p.kind = DW_OP_NONE;
-    const int mi = cs[0];
-    g.ops[mi] = silu;
-    g.t.erase(s);
-    g.ops.erase(g.ops.begin() + i);
-    --i;
-    ++fused;
+namespace {
+void drop_unreferenced(GraphIR& g) {
+  std::set<std::string> used(g.inputs.begin(), g.inputs.end());
+  used.insert(g.outputs.begin(), g.outputs.end());
+  for (auto& op : g.ops) {
+    used.insert(op.in.begin(), op.in.end());
+    used.insert(op.out.begin(), op.out.end());
   }
-  return fused;
+  for (auto it = g.t.begin(); it != g.t.end();) {
+    if (!it->second.is_init && !used.count(it->first))
+      it = g.t.erase(it);
+    else
+      ++it;
+  }
 }
+}  // namespace
+
+int apply_fusion_passes(GraphIR& g, bool conv_relu, bool silu, bool conv_requant) {
+  const size_t n = g.ops.size();
+  std::map<std::string, size_t> producer;
+  std::map<std::string, std::vector<size_t>> consumers;
+  for (size_t i = 0; i < n; ++i)
+    for (auto& o : g.ops[i].out) producer[o] = i;
+  for (size_t i = 0; i < n; ++i)
+    for (auto& in : g.ops[i].in) consumers[in].push_back(i);
+  auto n_consumers = [&](const std::string& t) {
+    auto it = consumers.find(t);
+    return it == consumers.end() ? (size_t)0 : it->second.size();
+  };
+  std::set<size_t> remove;
+  std::vector<std::pair<size_t, OpNode>> fused;
+
+  // pass 1: Conv + Relu
+  for (size_t i = 0; conv_relu && i < n; ++i) {
+    const OpNode& op = g.ops[i];
+    if (remove.count(i) || op.type != "Relu" || op.in.empty()) continue;
+    auto pr = producer.find(op.in[0]);
+    if (pr == producer.end()) continue;
+    const OpNode& conv = g.ops[pr->second];
+    if (conv.type != "Conv" || n_consumers(op.in[0]) != 1) continue;
+    remove.insert(i);
+    OpNode f = conv;
+    f.name = conv.name + "_fused_relu";
+    f.out = op.out;
+    f.p.has_relu = 1;
+    fused.push_back({pr->second, f});
+  }
+  // pass 2: Mul(x, Sigmoid(x)) -> SiLU
+  for (size_t i = 0; silu && i < n; ++i) {
+    const OpNode& op = g.ops[i];
+    if (remove.count(i) || op.type != "Mul" || op.in.size() != 2) continue;
+    int sig = -1;
+    std::string x;
+    for (int k = 0; k < 2 && sig < 0; ++k) {
+      auto pr = producer.find(op.in[k]);
+      if (pr == producer.end()) continue;
+      const OpNode& s = g.ops[pr->second];
+      if (s.type == "Sigmoid" && !s.in.empty() && s.in[0] == op.in[1 - k]) {
+        sig = (int)pr->second;
+        x = op.in[1 - k];
+      }
+    }
+    if (sig < 0 || remove.count((size_t)sig)) continue;
+    const std::string& sout = g.ops[sig].out[0];
+    if (n_consumers(sout) != 1 || g.is_output(sout)) continue;
+    remove.insert((size_t)sig);
+    OpNode f;
+    f.name = op.name + "_silu";
+    f.type = "SiLU";
+    f.in = {x};
+    f.out = op.out;
+    f.p.kind = DW_OP_NONE;
+    fused.push_back({i, f});
+  }
+  // pass 3: INT8 Conv + Requantize (+ Relu)
+  for (size_t i = 0; conv_requant && i < n; ++i) {
+    const OpNode& op = g.ops[i];
+    if (remove.count(i) || op.type != "Requantize" || op.out.empty()) continue;
+    const std::string fin = op.out[0];
+    int ci = -1;
+    for (int k = (int)i - 1; k >= 0; --k) {
+      const OpNode& prev = g.ops[k];
+      if (prev.type == "Conv" && !prev.out.empty() && prev.out[0] == fin && prev.p.kind == DW_OP_CONV2D) {
+        ci = k;
+        break;
+      }
+    }
+    if (ci < 0 || remove.count((size_t)ci)) continue;
+    const OpNode& conv = g.ops[ci];
+    if (conv.in.size() < 2 || conv.p.group != 1 || op.p.kind != DW_OP_REQUANTIZE) continue;
+    int relu = -1;
+    auto cs = consumers.find(fin);
+    if (cs != consumers.end()) {
+      std::vector<size_t> live;
+      for (size_t c : cs->second)
+        if (c != i && !remove.count(c)) live.push_back(c);
+      if (live.size() == 1 && g.ops[live[0]].type == "Relu") relu = (int)live[0];
+    }
+    if (conv.in.size() > 2 && !conv.in[2].empty()) continue;  // biased INT8 convs are not fused
+    OpNode f;
+    f.name = conv.name + "_fused_qrelu";
+    f.type = "Conv2dRequantReluI8";
+    f.in = conv.in;
+    f.out = {relu >= 0 ? (g.ops[relu].out.empty() ? fin : g.ops[relu].out[0]) : fin};
+    f.p = conv.p;
+    f.p.kind = DW_OP_CONV2D_REQUANT_RELU_I8;
+    f.p.scale = op.p.scale;
+    f.p.has_relu = relu >= 0 ? 1 : 0;
+    remove.insert(i);
+    if (relu >= 0) remove.insert((size_t)relu);
+    fused.push_back({(size_t)ci, f});
+  }
+  for (auto& kv : fused) g.ops[kv.first] = kv.second;
+  std::vector<size_t> rm(remove.begin(), remove.end());
+  for (auto it = rm.rbegin(); it != rm.rend(); ++it) g.ops.erase(g.ops.begin() + *it);
+  drop_unreferenced(g);
+  return (int)fused.size();
+}
+
+int fuse_silu(GraphIR& g) { return apply_fusion_passes(g, false, true, false); }
 
 void convert_to_f16(GraphIR& g) {
   if (g.dtype != DW_GRAPH_F32) fail(DW_ERR_RUNTIME, "convert_to_f16 needs an F32 graph");
@@ -557,7 +671,8 @@ std::string to_json(const GraphIR& g) {
       << ",\"scale\":" << fstr(p.scale) << ",\"scale_a_over_out\":" << fstr(p.scale_a_over_out)
       << ",\"scale_b_over_out\":" << fstr(p.scale_b_over_out) << ",\"has_relu\":" << p.has_relu
       << ",\"epsilon\":" << fstr(p.epsilon) << ",\"act\":" << p.act << ",\"trans_a\":" << p.trans_a
-      << ",\"trans_b\":" << p.trans_b << "}";
+      << ",\"trans_b\":" << p.trans_b << ",\"clip_min\":" << fstr(p.clip_min)
+      << ",\"clip_max\":" << fstr(p.clip_max) << "}";
   }
   o << "]}";
   return o.str();
@@ -590,7 +705,7 @@ extern "C" {
 int dw_graph_create(int dtype, dw_graph** out) {
   API_BEGIN
   if (!out) dw::fail(DW_ERR_INVALID, "null out");
-  if (dtype != DW_GRAPH_F32 && dtype != DW_GRAPH_F16 && dtype != DW_GRAPH_QU8)
+  if (dtype != DW_GRAPH_F32 && dtype != DW_GRAPH_F16 && dtype != DW_GRAPH_I8 && dtype != DW_GRAPH_QU8)
     dw::fail(DW_ERR_UNSUPPORTED, "graph dtype");
   dw_graph* g = new dw_graph();
   g->g.dtype = dtype;
@@ -706,10 +821,12 @@ int dw_graph_convert_nchw_to_nhwc(dw_graph* gh) {
 
 int dw_graph_apply_fusion_passes(dw_graph* gh, int* num_fused) {
   API_BEGIN
-  int n = dw::fuse_silu(G(gh));
+  int n = dw::apply_fusion_passes(G(gh), true, true, true);
   if (num_fused) *num_fused = n;
   API_END
 }
+
+size_t dw_op_params_size(void) { return sizeof(dw_op_params); }
 
 int dw_graph_convert_to_f16(dw_graph* gh) {
   API_BEGIN

@@ -118,6 +118,27 @@ __device__ __forceinline__ void ew_one(const EwArgs& a, size_t i) {
     case EW_F16_TO_F32:
       ((float*)a.y)[i] = h2f(((const uint16_t*)a.a)[i]);
       break;
+    case EW_CLIP:  // dispatch_clip (onnx runtime.rs:1004-1042): f32::clamp(min = s0, max = s1)
+      if (a.dtype == F32) {
+        const float v = ((const float*)a.a)[i];
+        ((float*)a.y)[i] = v < a.s0 ? a.s0 : (v > a.s1 ? a.s1 : v);
+      } else {  // F16::from_f32(to_f32().clamp(min, max))
+        const float v = h2f(((const uint16_t*)a.a)[i]);
+        ((uint16_t*)a.y)[i] = f2h(v < a.s0 ? a.s0 : (v > a.s1 ? a.s1 : v));
+      }
+      break;
+  }
+}
+
+// Element sizes of an op's first operand and its result.
+__device__ __forceinline__ void ew_sizes(int op, int dtype, int& in, int& out) {
+  switch (op) {
+    case EW_QADD_U8: case EW_LUT_U8: case EW_ADD_I8: case EW_RELU_I8: in = 1; out = 1; return;
+    case EW_DEQUANT_LINEAR_U8_F16: in = 1; out = 2; return;
+    case EW_QUANT_LINEAR_F16_U8: in = 2; out = 1; return;
+    case EW_REQUANT_I32_I8: case EW_QUANT_F32_I8: in = 4; out = 1; return;
+    case EW_DEQUANT_I8_F32: in = 1; out = 4; return;
+    default: in = out = dtype_size(dtype); return;
   }
 }
 
@@ -132,12 +153,8 @@ __global__ __launch_bounds__(256) void elementwise_kernel(const EwArgs a) {
 // runtime for ops whose operands are slices of concat buffers.
 __global__ __launch_bounds__(256) void elementwise2d_kernel(const Ew2Args e) {
   const size_t total = (size_t)e.pixels * e.channels;
-  const int esz_in = (e.op == EW_QADD_U8 || e.op == EW_LUT_U8 || e.op == EW_DEQUANT_LINEAR_U8_F16)
-                         ? 1
-                         : dtype_size(e.dtype);
-  const int esz_out = (e.op == EW_QUANT_LINEAR_F16_U8 || e.op == EW_QADD_U8 || e.op == EW_LUT_U8)
-                          ? 1
-                          : (e.op == EW_DEQUANT_LINEAR_U8_F16 ? 2 : dtype_size(e.dtype));
+  int esz_in, esz_out;
+  ew_sizes(e.op, e.dtype, esz_in, esz_out);
   for (size_t t = blockIdx.x * (size_t)blockDim.x + threadIdx.x; t < total;
        t += (size_t)gridDim.x * blockDim.x) {
     const size_t p = t / e.channels;
@@ -436,8 +453,10 @@ __global__ __launch_bounds__(256) void minmax_kernel(View x, int pixels, int cha
     const size_t p = t / channels;
     const int c = (int)(t - p * channels);
     const float v = ((const float*)x.base)[p * x.pix_stride + x.c_off + c];
-    lo = fminf(lo, v);
-    hi = fmaxf(hi, v);
+    if (__builtin_isfinite(v)) {  // TensorStats::update skips non-finite values (calibration.rs:56-63)
+      lo = fminf(lo, v);
+      hi = fmaxf(hi, v);
+    }
   }
   for (int off = 32; off > 0; off >>= 1) {
     lo = fminf(lo, __shfl_xor(lo, off));
@@ -453,6 +472,10 @@ __global__ __launch_bounds__(256) void minmax_kernel(View x, int pixels, int cha
       hi = fmaxf(hi, shi[w]);
     }
     if (lo <= hi) {
+      // -0 and +0 are equal as range ends; +0's bit pattern keeps the
+      // integer orderings of atomic_min_f / atomic_max_f valid
+      if (lo == 0.0f) lo = 0.0f;
+      if (hi == 0.0f) hi = 0.0f;
       atomic_min_f(out, lo);
       atomic_max_f(out + 1, hi);
     }

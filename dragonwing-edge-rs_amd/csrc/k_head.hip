@@ -98,22 +98,30 @@ __global__ __launch_bounds__(256) void global_avg_pool_kernel(const void* X, voi
 // Softmax over rows of n (softmax_f32, ops.rs:1609-1638), one thread per
 // row: the max from -inf (fmaxf: a NaN operand loses, as f32::max), e =
 // exp(x - max), the sum in order, out = e * (1 / sum).  exp is the device
-// expf, so outputs agree with the host's to within a few ulps.
-__global__ __launch_bounds__(256) void softmax_rows_kernel(const float* X, float* Y, int rows, int n) {
+// expf, so outputs agree with the host's to within a few ulps.  The f16 form
+// (CpuGraphRuntime::dispatch_softmax, runtime.rs:1311-1322) widens every
+// input with the reference decode, runs the f32 softmax and rounds each
+// output once to f16.
+template <bool H>
+__global__ __launch_bounds__(256) void softmax_rows_kernel(const void* X, void* Y, int rows, int n) {
   const int r = blockIdx.x * 256 + threadIdx.x;
   if (r >= rows) return;
-  const float* x = X + (size_t)r * n;
-  float* y = Y + (size_t)r * n;
+  auto ld = [&](int i) -> float {
+    if (H) return h2f(((const uint16_t*)X)[(size_t)r * n + i]);
+    return ((const float*)X)[(size_t)r * n + i];
+  };
   float mx = -INFINITY;
-  for (int i = 0; i < n; ++i) mx = fmaxf(mx, x[i]);
+  for (int i = 0; i < n; ++i) mx = fmaxf(mx, ld(i));
   float sum = 0.0f;
-  for (int i = 0; i < n; ++i) {
-    const float e = expf(x[i] - mx);
-    y[i] = e;
-    sum += e;
-  }
+  for (int i = 0; i < n; ++i) sum += expf(ld(i) - mx);
   const float inv = __fdiv_rn(1.0f, sum);
-  for (int i = 0; i < n; ++i) y[i] *= inv;
+  for (int i = 0; i < n; ++i) {
+    const float v = expf(ld(i) - mx) * inv;
+    if (H)
+      ((uint16_t*)Y)[(size_t)r * n + i] = f2h(v);
+    else
+      ((float*)Y)[(size_t)r * n + i] = v;
+  }
 }
 
 }  // namespace
@@ -159,7 +167,17 @@ void launch_global_avg_pool(hipStream_t st, int dtype, const void* x, void* y, i
 }
 
 void launch_softmax_rows(hipStream_t st, const float* x, float* y, int rows, int n) {
-  hipLaunchKernelGGL(softmax_rows_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st, x, y, rows, n);
+  launch_softmax_rows_t(st, F32, x, y, rows, n);
+}
+
+void launch_softmax_rows_t(hipStream_t st, int dtype, const void* x, void* y, int rows, int n) {
+  const dim3 g((unsigned)((rows + 255) / 256));
+  if (dtype == F32)
+    hipLaunchKernelGGL(softmax_rows_kernel<false>, g, dim3(256), 0, st, x, y, rows, n);
+  else if (dtype == F16)
+    hipLaunchKernelGGL(softmax_rows_kernel<true>, g, dim3(256), 0, st, x, y, rows, n);
+  else
+    fail(-2, "softmax: dtype");
   DW_HIP(hipGetLastError());
 }
 

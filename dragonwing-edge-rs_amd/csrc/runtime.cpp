@@ -94,6 +94,10 @@ struct Group {
   bool lut = false;
   std::string lut_out;       // tensor after the table (QLinearLUT output)
   int conv = -1;             // index of the conv op
+  // reference-form INT8 conv (s8 x s8): requantized to s8 with one scale
+  // (Requantize / Conv2dRequantReluI8Nhwc) or the raw int32 accumulator
+  bool requant = false;
+  float requant_scale = 1.0f;
 };
 
 struct Runtime {
@@ -156,6 +160,8 @@ struct Runtime {
   void emit_conv(const Group& gr);
   void emit_qconv(const Group& gr);
   void emit_ew(const OpNode& op);
+  void emit_iconv(const Group& gr);
+  void normalize();
   void push_igemm(Launch& L, const IgemmArgs& a, int esize);
   void autotune();
   void tag_group(const Group& gr, size_t first, int gid);
@@ -276,10 +282,12 @@ void Runtime::build(Backend* b, const GraphIR& graph, bool stats_mode) {
     if (ti.dims.size() == 4) {
       r.rank4 = true;
       r.n = ti.dims[0]; r.h = ti.dims[1]; r.w = ti.dims[2]; r.c = ti.dims[3];
-    } else if (ti.dims.size() == 2 && !ti.is_init) {
-      // [rows, cols] activations (Gemm, Flatten) as rows pixels of cols channels
+    } else if (!ti.is_init && !ti.dims.empty()) {
+      // other ranks (Gemm, Flatten, Reshape, Softmax operands): rows of the
+      // last dimension, as rows pixels of cols channels
       r.rank4 = true;
-      r.n = ti.dims[0]; r.h = 1; r.w = 1; r.c = ti.dims[1];
+      r.c = ti.dims.back();
+      r.n = ti.numel() / std::max<int64_t>(1, r.c); r.h = 1; r.w = 1;
     } else {
       r.c = ti.numel();
     }
@@ -293,6 +301,7 @@ void Runtime::build(Backend* b, const GraphIR& graph, bool stats_mode) {
     for (auto& o : op.out)
       if (!T(o).rank4) fail(DW_ERR_UNSUPPORTED, "runtime: activations must be 4-D NHWC (" + o + ")");
   }
+  normalize();
   std::vector<Group> groups;
   lower(groups);
   place(groups);
@@ -328,6 +337,58 @@ void Runtime::build(Backend* b, const GraphIR& graph, bool stats_mode) {
   int ns = 4;
   if (const char* env = getenv("DW_GRAPH_STREAMS")) ns = atoi(env);
   plan_streams(stats ? 1 : std::max(1, std::min(ns, 8)));
+}
+
+namespace {
+// Concat / Split along channels: whether the operand shapes are those of a
+// channel concatenation (every input agrees with the output on N, H, W and
+// the channel counts add up).  convert_nchw_to_nhwc leaves these ops'
+// axis attribute in NCHW numbering (graph.rs:248-290: axis 1 for channels),
+// so a graph that went through the reference's passes carries axis 1 on
+// NHWC data; the shapes decide.
+bool channel_join(const std::vector<const RtTensor*>& parts, const RtTensor& whole) {
+  int64_t c = 0;
+  for (const RtTensor* t : parts) {
+    if (t->n != whole.n || t->h != whole.h || t->w != whole.w) return false;
+    c += t->c;
+  }
+  return c == whole.c;
+}
+}  // namespace
+
+// Graph forms normalised before lowering:
+//  * the reference's INT8 form names a conv's int32 accumulator "<t>_i32"
+//    without any op writing it: Conv writes t, then Requantize reads
+//    "<t>_i32" and writes t again (QuantizedGraphCompiler::create_requant_op,
+//    quantize.rs:205-223).  The Conv is given the accumulator as its output,
+//    so every tensor has one writer;
+//  * Concat / Split with an NCHW-numbered channel axis (1) on NHWC tensors
+//    are renumbered to axis 3 when the shapes are a channel join.
+void Runtime::normalize() {
+  for (size_t i = 0; i < g.ops.size(); ++i) {
+    OpNode& rq = g.ops[i];
+    if (rq.type != "Requantize" || rq.in.empty() || rq.out.empty()) continue;
+    bool written = false;
+    for (size_t k = 0; k < i; ++k)
+      for (auto& o : g.ops[k].out) written |= o == rq.in[0];
+    if (written) continue;
+    for (int k = (int)i - 1; k >= 0; --k) {
+      OpNode& cv = g.ops[k];
+      if (cv.type == "Conv" && !cv.out.empty() && cv.out[0] == rq.out[0]) {
+        if (T(rq.in[0]).dtype != I32) fail(DW_ERR_RUNTIME, "Requantize input " + rq.in[0] + " must be int32");
+        cv.out[0] = rq.in[0];
+        break;
+      }
+    }
+  }
+  for (auto& op : g.ops) {
+    if (op.type != "Concat" && op.type != "Split") continue;
+    if (op.p.axis == 3 || op.in.empty() || op.out.empty()) continue;
+    std::vector<const RtTensor*> parts;
+    const bool cat = op.type == "Concat";
+    for (auto& n : cat ? op.in : op.out) parts.push_back(&T(n));
+    if (op.p.axis == 1 && channel_join(parts, T(cat ? op.out[0] : op.in[0]))) op.p.axis = 3;
+  }
 }
 
 // The storage a group's launches touch: every materialized activation its
@@ -494,8 +555,10 @@ void Runtime::lower(std::vector<Group>& groups) {
       gr.conv = i;
       gr.in = op.in[0];
       std::string cur = op.out[0];
-      int c = single(cur);
-      if (c >= 0 && (g.ops[c].type == "Relu" || g.ops[c].type == "SiLU")) {
+      int c = op.p.has_relu ? -1 : single(cur);
+      if (op.p.has_relu) {
+        gr.act = ACT_RELU;  // Conv + Relu fused by apply_fusion_passes
+      } else if (c >= 0 && (g.ops[c].type == "Relu" || g.ops[c].type == "SiLU")) {
         gr.act = g.ops[c].type == "Relu" ? ACT_RELU : ACT_SILU;
       } else if (!stats && !g.is_output(cur)) {
         auto cs = g.consumers(cur);
@@ -514,11 +577,45 @@ void Runtime::lower(std::vector<Group>& groups) {
           }
         }
       }
-      if (gr.act != ACT_NONE) {
+      if (gr.act != ACT_NONE && c >= 0) {
         used[c] = true;
         gr.ops.push_back(c);
         T(cur).materialized = false;
         cur = g.ops[c].out[0];
+      }
+      gr.out = cur;
+      groups.push_back(gr);
+      continue;
+    }
+    if (op.type == "Conv2dRequantReluI8" || (op.type == "Conv" && T(op.in[0]).dtype == I8)) {
+      // the reference's INT8 conv: s8 x s8 -> int32, then (fused, or as the
+      // following Requantize [+ Relu]) requantize_i32_to_i8 with one scale
+      gr.kind = "iconv";
+      gr.conv = i;
+      gr.in = op.in[0];
+      std::string cur = op.out[0];
+      if (op.type == "Conv2dRequantReluI8") {
+        gr.requant = true;
+        gr.requant_scale = op.p.scale;
+        gr.act = op.p.has_relu ? ACT_RELU : ACT_NONE;
+      } else {
+        const int rq = single(cur);
+        if (rq >= 0 && g.ops[rq].type == "Requantize" && T(g.ops[rq].out[0]).dtype == I8) {
+          used[rq] = true;
+          gr.ops.push_back(rq);
+          T(cur).materialized = false;
+          cur = g.ops[rq].out[0];
+          gr.requant = true;
+          gr.requant_scale = g.ops[rq].p.scale;
+          const int rl = single(cur);
+          if (rl >= 0 && g.ops[rl].type == "Relu" && T(g.ops[rl].out[0]).dtype == I8) {
+            used[rl] = true;
+            gr.ops.push_back(rl);
+            T(cur).materialized = false;
+            cur = g.ops[rl].out[0];
+            gr.act = ACT_RELU;
+          }
+        }
       }
       gr.out = cur;
       groups.push_back(gr);
@@ -545,8 +642,10 @@ void Runtime::lower(std::vector<Group>& groups) {
       }
       gr.out_kind = T(op.out[0]).dtype == F32 ? 0 : 1;
       std::string cur = op.out[0];
-      int c = single(cur);
-      if (c >= 0 && g.ops[c].type == "Relu") {
+      int c = op.p.has_relu ? -1 : single(cur);
+      if (op.p.has_relu) {
+        gr.act = ACT_RELU;  // Conv + Relu fused by apply_fusion_passes
+      } else if (c >= 0 && g.ops[c].type == "Relu") {
         gr.act = ACT_RELU;
       } else if (c >= 0 && g.ops[c].type == "SiLU") {
         gr.act = ACT_SILU;
@@ -571,7 +670,7 @@ void Runtime::lower(std::vector<Group>& groups) {
           }
         }
       }
-      if (gr.act != ACT_NONE) {
+      if (gr.act != ACT_NONE && c >= 0) {
         used[c] = true;
         gr.ops.push_back(c);
         T(cur).materialized = false;
@@ -678,8 +777,10 @@ void Runtime::lower(std::vector<Group>& groups) {
       gr.kind = "gap";
     } else if (op.type == "Gemm" || op.type == "MatMul") {
       gr.kind = "gemm";
-    } else if (op.type == "Flatten") {
+    } else if (op.type == "Flatten" || op.type == "Reshape") {
       gr.kind = "flatten";
+    } else if (op.type == "Softmax") {
+      gr.kind = "softmax";
     } else if (op.type == "Resize") {
       if (!op.p.mode_nearest) fail(DW_ERR_UNSUPPORTED, "runtime: only nearest Resize is implemented");
       gr.kind = "resize";
@@ -689,7 +790,9 @@ void Runtime::lower(std::vector<Group>& groups) {
       gr.kind = "split";
     } else if (op.type == "Relu" || op.type == "Sigmoid" || op.type == "Mul" || op.type == "Add" ||
                op.type == "SiLU" || op.type == "QLinearLUT" || op.type == "QLinearAdd" ||
-               op.type == "QuantizeLinear" || op.type == "DequantizeLinear") {
+               op.type == "QuantizeLinear" || op.type == "DequantizeLinear" || op.type == "Requantize" ||
+               op.type == "AddQuantized" || op.type == "Quantize" || op.type == "Dequantize" ||
+               op.type == "Clip") {
       gr.kind = "ew";
     } else {
       fail(DW_ERR_UNSUPPORTED, "runtime: no kernel for op type '" + op.type + "' (" + op.name + ")");
@@ -860,6 +963,7 @@ void Runtime::emit(const Group& gr) {
     return;
   }
   if (gr.kind == "qconv") return emit_qconv(gr);
+  if (gr.kind == "iconv") return emit_iconv(gr);
   if (gr.kind == "split") return;
   if (gr.kind == "concat") {
     const OpNode& op = g.ops[gr.ops[0]];
@@ -934,7 +1038,7 @@ void Runtime::emit(const Group& gr) {
     launches.push_back(L);
     return;
   }
-  if (gr.kind == "gap" || gr.kind == "gemm" || gr.kind == "flatten") {
+  if (gr.kind == "gap" || gr.kind == "gemm" || gr.kind == "flatten" || gr.kind == "softmax") {
     // classifier-head ops: dense tensors only
     const OpNode& op = g.ops[gr.ops[0]];
     RtTensor& x = T(op.in[0]);
@@ -945,10 +1049,18 @@ void Runtime::emit(const Group& gr) {
     L.op = op.name;
     L.bytes = (double)x.bytes() + y.bytes();
     const int dt = x.dtype;
-    if (dt != F32 && dt != F16) fail(DW_ERR_UNSUPPORTED, "runtime: " + op.type + " needs f32 or f16");
+    if (dt != F32 && dt != F16 && gr.kind != "flatten")
+      fail(DW_ERR_UNSUPPORTED, "runtime: " + op.type + " needs f32 or f16");
     const void* xb = x.base;
     void* yb = y.base;
-    if (gr.kind == "gap") {
+    if (gr.kind == "softmax") {
+      // CpuGraphRuntime::dispatch_softmax (runtime.rs:1288-1326): along the
+      // last dimension whatever the axis attribute says
+      if (y.dtype != dt || x.bytes() != y.bytes()) fail(DW_ERR_RUNTIME, "Softmax: output shape or dtype");
+      const int rows = (int)x.pixels(), n = (int)x.c;
+      L.kernel = "softmax";
+      L.fn = [=](hipStream_t st) { launch_softmax_rows_t(st, dt, xb, yb, rows, n); };
+    } else if (gr.kind == "gap") {
       if (y.pixels() != x.n || y.c != x.c) fail(DW_ERR_RUNTIME, "GlobalAveragePool: output shape");
       const int n = (int)x.n, hw = (int)(x.h * x.w), c = (int)x.c;
       L.kernel = "global_avg_pool";
@@ -1009,7 +1121,45 @@ void Runtime::emit_ew(const OpNode& op) {
     e.b = b.view();
     bytes += b.bytes();
   }
-  if (op.type == "Relu") e.op = EW_RELU;
+  const bool fl = a.dtype == F32 || a.dtype == F16;
+  auto need_dt = [&](const RtTensor& t, int dt) {
+    if (t.dtype != dt) fail(DW_ERR_RUNTIME, "runtime: " + op.type + " " + op.name + ": operand element type");
+  };
+  if (op.type == "Relu" && a.dtype == I8) {
+    need_dt(y, I8);
+    e.op = EW_RELU_I8;  // relu_i8 (ops.rs:3301-3320)
+  } else if (op.type == "Requantize") {  // requantize_i32_to_i8 (ops.rs:3380-3386)
+    need_dt(a, I32);
+    need_dt(y, I8);
+    e.op = EW_REQUANT_I32_I8;
+    e.s0 = op.p.scale;
+  } else if (op.type == "AddQuantized") {  // add_i8 (ops.rs:3176-3209)
+    need_dt(a, I8);
+    need_dt(T(op.in[1]), I8);
+    need_dt(y, I8);
+    e.op = EW_ADD_I8;
+    e.s0 = op.p.scale_a_over_out;
+    e.s1 = op.p.scale_b_over_out;
+  } else if (op.type == "Quantize") {  // quantize_f32_to_i8 (ops.rs:3503-3516): x * (1 / scale)
+    need_dt(a, F32);
+    need_dt(y, I8);
+    e.op = EW_QUANT_F32_I8;
+    e.s0 = 1.0f / op.p.scale;
+  } else if (op.type == "Dequantize") {  // dequantize_i8_to_f32 (ops.rs:3439-3457)
+    need_dt(a, I8);
+    need_dt(y, F32);
+    e.op = EW_DEQUANT_I8_F32;
+    e.s0 = op.p.scale;
+  } else if (op.type == "Clip") {
+    if (!fl) fail(DW_ERR_UNSUPPORTED, "runtime: Clip needs f32 or f16");
+    need_dt(y, a.dtype);
+    e.op = EW_CLIP;
+    e.s0 = op.p.clip_min;
+    e.s1 = op.p.clip_max;
+  } else if (!fl && (op.type == "Relu" || op.type == "Sigmoid" || op.type == "Mul" || op.type == "Add" ||
+                     op.type == "SiLU")) {
+    fail(DW_ERR_UNSUPPORTED, "runtime: " + op.type + " " + op.name + " needs f32 or f16 operands");
+  } else if (op.type == "Relu") e.op = EW_RELU;
   else if (op.type == "Sigmoid") e.op = EW_SIGMOID;
   else if (op.type == "Mul") e.op = EW_MUL;
   else if (op.type == "Add") e.op = EW_ADD;
@@ -1246,6 +1396,62 @@ void Runtime::emit_qconv(const Group& gr) {
   push_igemm(L, a, 1);
 }
 
+// The reference's INT8 conv (s8 activations, s8 HWIO weights, zero padding):
+// conv2d_i8_nhwc (ops.rs:3086-3142) to the int32 accumulator, or with
+// requantize_i32_to_i8 (ops.rs:3380-3386) and relu_i8 fused, which is
+// conv2d_requant_relu_i8_packed (dragonwing-vulkan ops.rs:2294-2430).
+void Runtime::emit_iconv(const Group& gr) {
+  const OpNode& op = g.ops[gr.conv];
+  const TensorInfo& W = g.t[op.in[1]];
+  RtTensor& x = T(gr.in);
+  RtTensor& y = T(gr.out);
+  if (!W.is_init || W.dims.size() != 4 || W.dtype != DW_DTYPE_I8)
+    fail(DW_ERR_UNSUPPORTED, "runtime: INT8 conv " + op.name + " needs HWIO int8 weights");
+  const int kh = (int)W.dims[0], kw = (int)W.dims[1], ci = (int)W.dims[2], co = (int)W.dims[3];
+  if (ci != x.c || co != y.c) fail(DW_ERR_RUNTIME, "runtime: conv " + op.name + " channel mismatch");
+  if (x.dtype != I8) fail(DW_ERR_RUNTIME, "runtime: INT8 conv " + op.name + " needs an int8 input");
+  if (gr.requant ? y.dtype != I8 : y.dtype != I32)
+    fail(DW_ERR_RUNTIME, "runtime: INT8 conv " + op.name +
+                             (gr.requant ? " must requantize to int8" : " without Requantize must write int32"));
+  if (op.in.size() > 2 && !op.in[2].empty())
+    fail(DW_ERR_UNSUPPORTED, "runtime: INT8 conv " + op.name +
+                                 " has a bias (the reference's INT8 convs take none: fusion.rs:303-309)");
+  if (op.p.group > 1) fail(DW_ERR_UNSUPPORTED, "runtime: grouped INT8 conv " + op.name);
+  if (op.p.dilations[0] > 1 || op.p.dilations[1] > 1) fail(DW_ERR_UNSUPPORTED, "runtime: dilation != 1");
+  if (ci % 16 != 0 || co % 4 != 0 || kh * kw > 31)
+    fail(DW_ERR_UNSUPPORTED, "runtime: INT8 conv needs c_in % 16 == 0, c_out % 4 == 0 and at most 31 taps (" +
+                                 op.name + ")");
+  if (x.pix_stride % 16 != 0 || x.abs_off % 16 != 0 || y.pix_stride % 4 != 0 || y.abs_off % 4 != 0)
+    fail(DW_ERR_RUNTIME, "runtime: misaligned view for " + op.name);
+  IgemmArgs a{};
+  a.x = (const uint8_t*)x.base;
+  a.y = y.base;
+  a.n = (int)x.n; a.h = (int)x.h; a.w = (int)x.w; a.cin = ci; a.cout = co; a.kh = kh; a.kw = kw;
+  a.sh = std::max(1, op.p.strides[0]); a.sw = std::max(1, op.p.strides[1]);
+  a.pt = op.p.pads[0]; a.pl = op.p.pads[1]; a.ho = (int)y.h; a.wo = (int)y.w;
+  a.m = (int)y.pixels();
+  a.ksteps = (kh * kw * ci + 63) / 64;
+  const int bc = igemm_channel_tile(co);
+  a.cout_pad = (co + bc - 1) / bc * bc;
+  a.x_pix_stride = x.pix_stride; a.x_c_off = x.abs_off;
+  a.y_pix_stride = y.pix_stride; a.y_c_off = y.abs_off;
+  void* whwio = upload(W.data.data(), W.data.size());
+  void* wpk = dalloc((size_t)a.ksteps * a.cout_pad * 64);
+  launch_pack_weights(be->stream, whwio, wpk, kh * kw * ci, co, a.cout_pad, a.ksteps, 1);
+  a.wpk = (const uint8_t*)wpk;
+  a.epi = gr.requant ? EPI_QS8_REF : EPI_I32;
+  a.tscale = gr.requant_scale;
+  a.act = gr.act;
+  a.xxor = 0;  // s8 operands as they are; padding taps read 0
+  a.xpad = 0;
+  Launch L;
+  L.op = join_names(g, gr.ops);
+  L.work = 2.0 * (double)y.pixels() * co * kh * kw * ci;
+  L.bytes = (double)x.bytes() + W.data.size() + (double)y.bytes();
+  DW_HIP(hipStreamSynchronize(be->stream));
+  push_igemm(L, a, 1);
+}
+
 void Runtime::push_igemm(Launch& L, const IgemmArgs& a, int esize) {
   auto ig = std::make_shared<IgemmArgs>(a);
   L.ig = ig;
@@ -1381,6 +1587,7 @@ int dw_hip_graph_runtime_create(dw_hip_backend* be, const dw_graph* g, dw_hip_gr
   API_BEGIN
   if (!g || !out) dw::fail(DW_ERR_INVALID, "null argument");
   dw::Backend* b = Bk(be);
+  std::lock_guard<std::mutex> lock(b->mu);
   auto* rt = new dw_hip_graph_runtime();
   dw::hold(b);  // released with the runtime
   try {
@@ -1404,6 +1611,7 @@ void dw_hip_graph_runtime_destroy(dw_hip_graph_runtime* rt) {
 int dw_hip_graph_set_input_bytes(dw_hip_graph_runtime* rth, const char* name, const void* data, size_t len) {
   API_BEGIN
   dw::Runtime& rt = R(rth);
+  std::lock_guard<std::mutex> lock(rt.be->mu);
   if (!name || std::find(rt.g.inputs.begin(), rt.g.inputs.end(), std::string(name)) == rt.g.inputs.end())
     dw::fail(DW_ERR_RUNTIME, std::string("input not found: ") + (name ? name : "(null)"));
   dw::RtTensor& t = rt.T(name);
@@ -1418,6 +1626,7 @@ int dw_hip_graph_set_input_bytes(dw_hip_graph_runtime* rth, const char* name, co
 int dw_hip_graph_set_input_f32(dw_hip_graph_runtime* rth, const char* name, const float* data, size_t count) {
   API_BEGIN
   dw::Runtime& rt = R(rth);
+  std::lock_guard<std::mutex> lock(rt.be->mu);
   if (!name || std::find(rt.g.inputs.begin(), rt.g.inputs.end(), std::string(name)) == rt.g.inputs.end())
     dw::fail(DW_ERR_RUNTIME, std::string("input not found: ") + (name ? name : "(null)"));
   dw::RtTensor& t = rt.T(name);
@@ -1440,13 +1649,16 @@ int dw_hip_graph_set_input_f32(dw_hip_graph_runtime* rth, const char* name, cons
 
 int dw_hip_graph_run(dw_hip_graph_runtime* rth) {
   API_BEGIN
-  R(rth).run();
+  dw::Runtime& rt = R(rth);
+  std::lock_guard<std::mutex> lock(rt.be->mu);
+  rt.run();
   API_END
 }
 
 int dw_hip_graph_run_unbatched(dw_hip_graph_runtime* rth) {
   API_BEGIN
   dw::Runtime& rt = R(rth);
+  std::lock_guard<std::mutex> lock(rt.be->mu);
   const bool trace = getenv("DW_TRACE") != nullptr;
   hipStream_t st = rt.be->stream;
   for (size_t i = 0; i < rt.launches.size(); ++i) {
@@ -1477,6 +1689,7 @@ const char* dw_hip_graph_io_name(dw_hip_graph_runtime* rth, int which, int index
 int dw_hip_graph_tensor_shape(dw_hip_graph_runtime* rth, const char* name, int64_t* dims4, int* rank) {
   API_BEGIN
   dw::Runtime& rt = R(rth);
+  std::lock_guard<std::mutex> lock(rt.be->mu);
   if (!name || !dims4 || !rank) dw::fail(DW_ERR_INVALID, "null argument");
   auto it = rt.g.t.find(name);
   if (it == rt.g.t.end()) dw::fail(DW_ERR_RUNTIME, std::string("runtime: unknown tensor '") + name + "'");
@@ -1500,6 +1713,7 @@ static void download_tensor(dw::Runtime& rt, const std::string& name, std::vecto
 int dw_hip_graph_get_output_bytes(dw_hip_graph_runtime* rth, const char* name, void* data, size_t len) {
   API_BEGIN
   dw::Runtime& rt = R(rth);
+  std::lock_guard<std::mutex> lock(rt.be->mu);
   if (!name) dw::fail(DW_ERR_INVALID, "null name");
   std::vector<uint8_t> buf;
   download_tensor(rt, name, buf);
@@ -1513,6 +1727,7 @@ int dw_hip_graph_get_output_bytes(dw_hip_graph_runtime* rth, const char* name, v
 int dw_hip_graph_get_output_f32(dw_hip_graph_runtime* rth, const char* name, float* data, size_t count) {
   API_BEGIN
   dw::Runtime& rt = R(rth);
+  std::lock_guard<std::mutex> lock(rt.be->mu);
   if (!name) dw::fail(DW_ERR_INVALID, "null name");
   dw::RtTensor& t = rt.T(name);
   std::vector<uint8_t> buf;
@@ -1535,6 +1750,7 @@ int dw_hip_graph_get_output_f32(dw_hip_graph_runtime* rth, const char* name, flo
 int dw_hip_graph_tensor_bytes(dw_hip_graph_runtime* rth, const char* name, size_t* len) {
   API_BEGIN
   dw::Runtime& rt = R(rth);
+  std::lock_guard<std::mutex> lock(rt.be->mu);
   if (!name || !len) dw::fail(DW_ERR_INVALID, "null argument");
   *len = rt.T(name).bytes();
   API_END
@@ -1543,6 +1759,7 @@ int dw_hip_graph_tensor_bytes(dw_hip_graph_runtime* rth, const char* name, size_
 int dw_hip_graph_enable_capture(dw_hip_graph_runtime* rth, int enable) {
   API_BEGIN
   dw::Runtime& rt = R(rth);
+  std::lock_guard<std::mutex> lock(rt.be->mu);
   rt.capture = enable != 0;
   API_END
 }
@@ -1569,6 +1786,7 @@ const char* dw_hip_graph_launch_info(dw_hip_graph_runtime* rth, int index) {
 int dw_hip_graph_run_profiled(dw_hip_graph_runtime* rth, float* launch_ms) {
   API_BEGIN
   dw::Runtime& rt = R(rth);
+  std::lock_guard<std::mutex> lock(rt.be->mu);
   if (!launch_ms) dw::fail(DW_ERR_INVALID, "null output");
   const size_t n = rt.launches.size();
   std::vector<hipEvent_t> ev(n + 1);
@@ -1588,6 +1806,7 @@ int dw_hip_graph_run_profiled(dw_hip_graph_runtime* rth, float* launch_ms) {
 int dw_hip_graph_time_launches(dw_hip_graph_runtime* rth, int repeat, float* launch_ms) {
   API_BEGIN
   dw::Runtime& rt = R(rth);
+  std::lock_guard<std::mutex> lock(rt.be->mu);
   if (!launch_ms || repeat < 1) dw::fail(DW_ERR_INVALID, "time_launches: null output or repeat < 1");
   const size_t n = rt.launches.size();
   hipEvent_t e0, e1;
@@ -1613,6 +1832,7 @@ int dw_hip_graph_time_launches_rotated(dw_hip_graph_runtime* const* rths, int n_
   if (!rths || n_rt < 1 || !launch_ms || repeat < 1)
     dw::fail(DW_ERR_INVALID, "time_launches_rotated: null argument, no runtime or repeat < 1");
   const dw::Runtime& r0 = R(rths[0]);
+  std::lock_guard<std::mutex> lock(r0.be->mu);
   for (int k = 1; k < n_rt; ++k) {
     const dw::Runtime& rk = R(rths[k]);
     if (rk.launches.size() != r0.launches.size() || rk.be != r0.be)
@@ -1645,6 +1865,7 @@ int dw_hip_calibrate(dw_hip_backend* be, dw_graph* gh, const char* input_name, c
                      size_t floats_per_image, int num_images) {
   API_BEGIN
   dw::Backend* b = Bk(be);
+  std::lock_guard<std::mutex> lock(b->mu);
   if (!gh || !images || !input_name) dw::fail(DW_ERR_INVALID, "null argument");
   if (gh->g.dtype != DW_GRAPH_F32) dw::fail(DW_ERR_RUNTIME, "calibration needs the F32 graph");
   gh->g.json.clear();

@@ -14,9 +14,9 @@ import json
 
 import numpy as np
 
-from ._lib import DwOpParams, check, load
+from ._lib import RELEASE_GRAPH, RELEASE_RUNTIME, DwOpParams, check, load, native_calls_allowed, track
 
-GRAPH_F32, GRAPH_F16, GRAPH_QU8 = 0, 1, 3
+GRAPH_F32, GRAPH_F16, GRAPH_I8, GRAPH_QU8 = 0, 1, 2, 3
 DT = {"f32": 0, "f16": 1, "i8": 2, "u8": 3, "i32": 4}
 NP_OF_DT = {0: np.float32, 1: np.uint16, 2: np.int8, 3: np.uint8, 4: np.int32}
 
@@ -24,13 +24,17 @@ OP_KIND = {
     "None": 0, "Conv2d": 1, "Add": 2, "Mul": 3, "Sigmoid": 4, "MaxPool": 5, "Concat": 6, "Split": 7,
     "Resize": 8, "BatchNorm": 9, "Requantize": 10, "AddQuantized": 11, "Quantize": 12, "Dequantize": 13,
     "Conv2dRequantReluI8Nhwc": 14, "QLinearConv": 32, "QuantizeLinear": 33, "DequantizeLinear": 34,
-    "QLinearAdd": 35, "QLinearLUT": 36, "Gemm": 15, "GlobalAvgPool": 16,
+    "QLinearAdd": 35, "QLinearLUT": 36, "Gemm": 15, "GlobalAvgPool": 16, "Softmax": 17, "Clip": 18,
+    "Reshape": 19,
 }
 # default OpParams kind per op_type
 KIND_OF_TYPE = {"Conv": "Conv2d", "Add": "Add", "Mul": "Mul", "Sigmoid": "Sigmoid", "MaxPool": "MaxPool",
                 "Concat": "Concat", "Split": "Split", "Resize": "Resize", "BatchNormalization": "BatchNorm",
                 "Relu": "None", "SiLU": "None", "Gemm": "Gemm", "MatMul": "None", "Flatten": "None",
-                "GlobalAveragePool": "GlobalAvgPool"}
+                "GlobalAveragePool": "GlobalAvgPool", "Softmax": "Softmax", "Clip": "Clip",
+                "Reshape": "Reshape", "Requantize": "Requantize", "AddQuantized": "AddQuantized",
+                "Quantize": "Quantize", "Dequantize": "Dequantize",
+                "Conv2dRequantReluI8": "Conv2dRequantReluI8Nhwc"}
 
 
 def _params(kind: str, **kw) -> DwOpParams:
@@ -59,6 +63,8 @@ def _params(kind: str, **kw) -> DwOpParams:
     p.beta = kw.get("beta", 1.0)
     p.trans_a = int(kw.get("trans_a", 0))
     p.trans_b = int(kw.get("trans_b", 0))
+    p.clip_min = kw.get("clip_min", float("-inf"))
+    p.clip_max = kw.get("clip_max", float("inf"))
     return p
 
 
@@ -74,16 +80,21 @@ class Graph:
         h = C.c_void_p()
         check(load().dw_graph_create(dtype, C.byref(h)))
         self._h = h.value
+        track(self, RELEASE_GRAPH)
 
     @property
     def handle(self):
         return self._h
 
+    def _release(self):
+        if self._h:
+            load().dw_graph_destroy(self._h)
+            self._h = None
+
     def __del__(self):
         try:
-            if self._h:
-                load().dw_graph_destroy(self._h)
-                self._h = None
+            if native_calls_allowed():
+                self._release()
         except Exception:
             pass
 
@@ -165,17 +176,22 @@ class HipGraphRuntime:
         check(load().dw_hip_graph_runtime_create(backend.handle, graph.handle, C.byref(h)))
         self._h = h.value
         self._backend = backend  # keeps the backend alive
+        track(self, RELEASE_RUNTIME)
+
+    def _release(self):
+        if self._h:
+            load().dw_hip_graph_runtime_destroy(self._h)
+            self._h = None
 
     def __del__(self):
         try:
-            if self._h:
-                load().dw_hip_graph_runtime_destroy(self._h)
-                self._h = None
+            if native_calls_allowed():
+                self._release()
         except Exception:
             pass
 
     def close(self):
-        self.__del__()
+        self._release()
 
     def set_input_f32(self, name: str, data):
         a = np.ascontiguousarray(data, np.float32)

@@ -218,6 +218,14 @@ def int8_graph_from_ranges(ranges: dict, batch: int = 32, size: int = 640, seed:
     return g, info
 
 
+def calibration_graph(batch: int, size: int = 640, seed: int | None = None):
+    """The F32 NHWC graph calibration runs on: fold_batchnorm -> NHWC."""
+    g, info = build_yolov8n(batch, size, seed)
+    g.fold_batchnorm()
+    g.convert_nchw_to_nhwc()
+    return g, info
+
+
 def int8_graph(backend, batch: int = 32, size: int = 640, calib: np.ndarray | None = None,
                seed: int | None = None, calib_batch: int | None = None):
     """The u8 QDQ graph: calibrate the F32 graph on the GPU over `calib`

@@ -299,6 +299,9 @@ typedef enum dw_op_kind {
   DW_OP_CONV2D_REQUANT_RELU_I8 = 14, /* OpParams::Conv2dRequantReluI8Nhwc     */
   DW_OP_GEMM = 15,       /* OpParams::Gemm (alpha, beta, trans_a, trans_b)    */
   DW_OP_GLOBAL_AVG_POOL = 16, /* OpParams::GlobalAvgPool                      */
+  DW_OP_SOFTMAX = 17,    /* OpParams::Softmax { axis } (axis = last dim only)  */
+  DW_OP_CLIP = 18,       /* OpParams::Clip { min, max }                        */
+  DW_OP_RESHAPE = 19,    /* OpParams::Reshape (the output tensor's dims)       */
   /* extensions */
   DW_OP_QLINEAR_CONV = 32,  /* QLinearConv (+ fused LUT activation, + QLinearAdd residual) */
   DW_OP_QUANTIZE_LINEAR = 33,
@@ -327,11 +330,20 @@ typedef struct dw_op_params {
   int act;                  /* QLinearLUT: DW_ACT_* the table encodes         */
   float alpha, beta;        /* Gemm (carried; the reference's runtime ignores them) */
   int trans_a, trans_b;     /* Gemm                                           */
+  float clip_min, clip_max; /* Clip                                           */
 } dw_op_params;
+
+/* sizeof(dw_op_params) as compiled into the library.  A binding that declares
+ * its own copy of the struct (ctypes, Rust #[repr(C)]) checks its size
+ * against this before passing one to dw_graph_add_op, which copies the whole
+ * struct.  No counterpart in the reference (layout check for FFI callers). */
+size_t dw_op_params_size(void);
 
 /* Graph dtypes (dragonwing_core::Dtype subset, crates/dragonwing-core/src/dtype.rs). */
 #define DW_GRAPH_F32 0
 #define DW_GRAPH_F16 1
+#define DW_GRAPH_I8 2  /* Dtype::I8: the reference's symmetric INT8 form      */
+                       /* (QuantizedGraphCompiler, quantize.rs:73-368)        */
 #define DW_GRAPH_QU8 3 /* quantized: u8 activations with zero points (QDQ-folded) */
 
 int dw_graph_create(int dtype, dw_graph** out);
@@ -355,7 +367,13 @@ int dw_graph_set_io(dw_graph* g, const char* const* inputs, int num_inputs,
 /* Passes (crates/dragonwing-onnx/src/graph.rs, fusion.rs, quantize.rs). */
 int dw_graph_fold_batchnorm(dw_graph* g);         /* graph.rs:521-690 (f64 math)   */
 int dw_graph_convert_nchw_to_nhwc(dw_graph* g);   /* graph.rs:248-290              */
-int dw_graph_apply_fusion_passes(dw_graph* g, int* num_fused); /* fusion.rs:42-348 */
+/* apply_fusion_passes (fusion.rs:42-348), all three passes on one snapshot
+ * of the op list: 1. Conv + Relu -> Conv "<conv>_fused_relu" writing the
+ * Relu's output, with has_relu = 1 (the reference drops the ReLU there; here
+ * the flag keeps it); 2. Sigmoid + Mul -> SiLU "<mul>_silu" (either Mul
+ * operand order); 3. INT8 Conv + Requantize (+ Relu) -> Conv2dRequantReluI8.
+ * *num_fused receives the number of fused ops written. */
+int dw_graph_apply_fusion_passes(dw_graph* g, int* num_fused);
 int dw_graph_convert_to_f16(dw_graph* g);          /* runtime.rs:800-811: f32 initializers -> F16 RNE */
 
 /* Calibration statistics (calibration.rs:56-69) and the QDQ quantizer that

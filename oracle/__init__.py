@@ -116,7 +116,10 @@ def num_cpus() -> int:
 
 
 def default_threads() -> int:
-    return num_cpus()
+    """Threads for the oracle's row-parallel loops: the online CPUs, at most
+    OMP_NUM_THREADS (default 16), the CPU share a one-GPU host gives a job."""
+    cap = int(os.environ.get("OMP_NUM_THREADS", "16") or 16)
+    return max(1, min(num_cpus(), cap))
 
 
 # --- F16 -------------------------------------------------------------------
@@ -346,7 +349,11 @@ def maxpool2d_f32(x, k, s):
 
 
 def maxpool2d_padded(x, k, s, pads):
-    """pads = (top, left, bottom, right); dtype float32 / uint16 (f16 bits) / uint8."""
+    """pads = (top, left, bottom, right); dtype float32 / uint16 (f16 bits) /
+    uint8 / int8 (int8 through the order-preserving map q ^ 0x80 to uint8)."""
+    if np.asarray(x).dtype == np.int8:
+        u = np.ascontiguousarray(x).view(np.uint8) ^ np.uint8(0x80)
+        return (maxpool2d_padded(u, k, s, pads) ^ np.uint8(0x80)).view(np.int8)
     x = np.ascontiguousarray(x)
     n, h, w, c = x.shape
     pt, pl, pb, pr = pads
@@ -486,6 +493,22 @@ def global_avg_pool_fp16(x):
     y = np.empty((n, c), np.uint16)
     lib().dwo_global_avg_pool_fp16(_p(y), _p(x), n, h, w, c)
     return y
+
+
+def clip(x, lo, hi):
+    """dispatch_clip (onnx runtime.rs:1004-1042): f32::clamp(min, max) (NaN
+    passes through); f16 bits through F16::to_f32, clamp, F16::from_f32."""
+    if x.dtype == np.uint16:
+        return f16_from_f32(clip(f16_to_f32(x), lo, hi))
+    x = np.asarray(x, np.float32)
+    lo, hi = np.float32(lo), np.float32(hi)
+    return np.where(x < lo, lo, np.where(x > hi, hi, x)).astype(np.float32)
+
+
+def softmax_f16(xh):
+    """CpuGraphRuntime::dispatch_softmax for F16 (runtime.rs:1311-1322): every
+    input through F16::to_f32, softmax_f32, each output F16::from_f32."""
+    return f16_from_f32(softmax_f32(f16_to_f32(xh)))
 
 
 def softmax_f32(x):

@@ -9,6 +9,20 @@ intermediate stored in its own dtype, conv bias as a separate pass
 ops (QLinearConv, QLinearLUT, QLinearAdd, QuantizeLinear,
 DequantizeLinear) and padded MaxPool are the extensions defined in
 ``oracle/dw_oracle.cpp`` Part B.
+
+The reference's INT8 form (``QuantizedGraphCompiler``, ``quantize.rs:73-368``,
+and fusion pass 3, ``fusion.rs:192-334``) runs with the semantics of the ops
+it names, which ``CpuGraphRuntime`` itself refuses (``runtime.rs:934-941``,
+``:1497``): an INT8 Conv is ``conv2d_i8_nhwc`` (``ops.rs:3086-3142``) to its
+int32 accumulator, Requantize is ``requantize_i32_to_i8`` (``ops.rs:3380-3386``),
+Conv2dRequantReluI8 is the three in sequence as
+``conv2d_requant_relu_i8_packed`` defines them (``dragonwing-vulkan
+ops.rs:2294-2430``), AddQuantized is ``add_i8``, Quantize / Dequantize are
+``quantize_f32_to_i8`` / ``dequantize_i8_to_f32``.  The accumulator that
+the reference names "<t>_i32" without any op writing it becomes the Conv's
+output, and a Concat/Split axis left in NCHW numbering (1) on NHWC tensors
+is taken as the channel axis when the shapes are a channel join -- the
+same two normalisations the HIP runtime applies.
 """
 from __future__ import annotations
 
@@ -36,9 +50,32 @@ class CpuGraph:
         self.vals[name] = np.ascontiguousarray(arr, NP[ti["dtype"]]).reshape(ti["dims"])
 
     def run(self, keep: set[str] | None = None):
-        for op in self.d["ops"]:
+        for op in self._normalized_ops():
             self._dispatch(op)
         return self.vals
+
+    def _normalized_ops(self):
+        ops = [dict(op, inputs=list(op["inputs"]), outputs=list(op["outputs"])) for op in self.d["ops"]]
+        for i, rq in enumerate(ops):
+            if rq["type"] != "Requantize":
+                continue
+            src = rq["inputs"][0]
+            if any(src in o["outputs"] for o in ops[:i]):
+                continue
+            for cv in reversed(ops[:i]):
+                if cv["type"] == "Conv" and cv["outputs"][0] == rq["outputs"][0]:
+                    cv["outputs"][0] = src
+                    break
+        dims = lambda n: self.t[n]["dims"]
+        for op in ops:
+            if op["type"] not in ("Concat", "Split") or op["axis"] != 1:
+                continue
+            parts, whole = (op["inputs"], op["outputs"][0]) if op["type"] == "Concat" else (op["outputs"], op["inputs"][0])
+            w = dims(whole)
+            if len(w) == 4 and all(len(dims(q)) == 4 and dims(q)[:3] == w[:3] for q in parts) and \
+                    sum(dims(q)[3] for q in parts) == w[3]:
+                op["axis"] = 3
+        return ops
 
     def _dispatch(self, op):
         ty = op["type"]
@@ -57,20 +94,53 @@ class CpuGraph:
                 if x.dtype == np.float32:
                     y = oracle.depthwise_f32(x, k, s, (p[0], p[1]), self.threads)
                     y = oracle.bias_add_f32(y, b) if b is not None else y
+                    y = oracle.relu_f32(y) if op.get("has_relu") else y
                 else:
                     y = oracle.depthwise_fp16(x, k, s, (p[0], p[1]), self.threads)
                     y = oracle.bias_add_f16(y, b) if b is not None else y
+                    y = oracle.relu_fp16(y) if op.get("has_relu") else y
                 self.vals[out[0]] = y
+                return
+            if x.dtype == np.int8:
+                if b is not None:
+                    raise NotImplementedError("biased INT8 conv")
+                self.vals[out[0]] = oracle.conv2d_i8_nhwc(x, w, s, (p[0], p[1]), self.threads)
                 return
             if x.dtype == np.float32:
                 y = oracle.conv2d_f32_nhwc(x, w, s, (p[0], p[1]), self.threads)
                 if b is not None:
                     y = oracle.bias_add_f32(y, b)
+                if op.get("has_relu"):  # Conv + Relu from fusion pass 1
+                    y = oracle.relu_f32(y)
             else:
                 y = oracle.conv2d_fp16_nhwc(x, w, s, (p[0], p[1]), self.threads)
                 if b is not None:
                     y = oracle.bias_add_f16(y, b)
+                if op.get("has_relu"):
+                    y = oracle.relu_fp16(y)
             self.vals[out[0]] = y
+        elif ty == "Conv2dRequantReluI8":
+            x, w = ins[0], ins[1]
+            if len(ins) > 2 and ins[2] is not None:
+                raise NotImplementedError("biased INT8 conv")
+            s, p = op["strides"], op["pads"]
+            y = oracle.requantize_i32_to_i8(oracle.conv2d_i8_nhwc(x, w, s, (p[0], p[1]), self.threads), op["scale"])
+            self.vals[out[0]] = oracle.relu_i8(y) if op["has_relu"] else y
+        elif ty == "Requantize":
+            self.vals[out[0]] = oracle.requantize_i32_to_i8(ins[0], op["scale"])
+        elif ty == "AddQuantized":
+            self.vals[out[0]] = oracle.add_i8(ins[0], ins[1], op["scale_a_over_out"], op["scale_b_over_out"])
+        elif ty == "Quantize":
+            self.vals[out[0]] = oracle.quantize_f32_to_i8(ins[0], op["scale"])
+        elif ty == "Dequantize":
+            self.vals[out[0]] = oracle.dequantize_i8_to_f32(ins[0], op["scale"])
+        elif ty == "Clip":
+            self.vals[out[0]] = oracle.clip(ins[0], op["clip_min"], op["clip_max"])
+        elif ty == "Softmax":
+            x = ins[0]
+            self.vals[out[0]] = (oracle.softmax_f16 if x.dtype == np.uint16 else oracle.softmax_f32)(x)
+        elif ty == "Reshape":
+            self.vals[out[0]] = np.ascontiguousarray(ins[0]).reshape(t[out[0]]["dims"])
         elif ty == "QLinearConv":
             x, w = ins[0], ins[1]
             b = ins[2] if len(ins) > 2 else None
@@ -102,7 +172,10 @@ class CpuGraph:
         elif ty == "Add":
             self.vals[out[0]] = (oracle.add_f32 if ins[0].dtype == np.float32 else oracle.add_fp16)(ins[0], ins[1])
         elif ty == "Relu":
-            self.vals[out[0]] = (oracle.relu_f32 if ins[0].dtype == np.float32 else oracle.relu_fp16)(ins[0])
+            x = ins[0]
+            fn = {np.dtype(np.float32): oracle.relu_f32, np.dtype(np.uint16): oracle.relu_fp16,
+                  np.dtype(np.int8): oracle.relu_i8}[x.dtype]
+            self.vals[out[0]] = fn(x)
         elif ty == "SiLU":
             self.vals[out[0]] = (oracle.silu_f32 if ins[0].dtype == np.float32 else oracle.silu_fp16)(ins[0])
         elif ty == "MaxPool":
@@ -147,3 +220,50 @@ class CpuGraph:
             self.vals[out[0]] = c.reshape(t[out[0]]["dims"])
         else:
             raise NotImplementedError(f"oracle graph: op type {ty}")
+
+
+def calibrate(desc: dict, initializer, input_name: str, images: np.ndarray, threads: int | None = None):
+    """Calibrator::new / feed / compute_params (crates/dragonwing-onnx/src/
+    calibration.rs:90-260) over an F32 NHWC graph: the images run through the
+    graph in batches of its N, and after every op each f32 tensor it wrote
+    updates that tensor's (min, max) with its finite values only
+    (TensorStats::update, calibration.rs:56-63; feed, :170-205).  As in feed,
+    only op outputs are recorded, not the graph input.  Returns
+    {name: (min, max)}; QuantScale::from_range turns a range into absmax/127.
+
+    Where this departs from calibration.rs:632-830: the ops run with
+    CpuGraphRuntime's semantics on the NHWC graph (the conv's kh -> kw -> ic
+    chain of fused multiply-adds, the bias pass after it, padded MaxPool),
+    i.e. the graph the quantized runtime executes; the reference's
+    Calibrator instead indexes its convs as NCHW (ic -> kh -> kw, separate
+    multiply and add) and ignores MaxPool padding, which the documented
+    pipeline's NHWC graph (docs/yolo-vulkan-pipeline.md:228-240) cannot run.
+    """
+    if desc["dtype"] != F32:
+        raise ValueError("calibration requires an F32 graph")
+    t = desc["tensors"]
+    batch = t[input_name]["dims"][0]
+    images = np.ascontiguousarray(images, np.float32)
+    if images.shape[0] % batch:
+        raise ValueError("image count must be a multiple of the graph batch")
+    cg = CpuGraph(desc, initializer, threads)
+    stats: dict[str, tuple[float, float]] = {}
+    ops = cg._normalized_ops()
+    for i0 in range(0, images.shape[0], batch):
+        cg.set_input(input_name, images[i0:i0 + batch])
+        for op in ops:
+            cg._dispatch(op)
+            for o in op["outputs"]:
+                if t[o]["init"]:
+                    continue
+                v = cg.vals[o]
+                if v.dtype != np.float32:
+                    continue
+                f = v[np.isfinite(v)]
+                if f.size == 0:
+                    continue
+                lo, hi = float(f.min()), float(f.max())
+                if o in stats:
+                    lo, hi = min(stats[o][0], lo), max(stats[o][1], hi)
+                stats[o] = (lo, hi)
+    return stats

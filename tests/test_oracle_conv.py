@@ -153,3 +153,80 @@ def test_fold_batchnorm_closed_form():
     sf = g.astype(np.float64) / np.sqrt(var.astype(np.float64) + np.float64(np.float32(1e-3)))
     np.testing.assert_array_equal(w2, (w.astype(np.float64) * sf[:, None, None, None]).astype(np.float32))
     np.testing.assert_array_equal(b2, ((0 - mean.astype(np.float64)) * sf + beta).astype(np.float32))
+
+
+# --- accumulation order, in exact rationals ----------------------------------
+from fractions import Fraction  # noqa: E402
+
+
+def _round_f32(q: Fraction) -> Fraction:
+    """q rounded to the nearest binary32 value, ties to even (subnormals
+    included; the magnitudes here never overflow)."""
+    if q == 0:
+        return Fraction(0)
+    a = abs(q)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** e > a:
+        e -= 1
+    e = max(e, -126)
+    ulp = Fraction(2) ** (e - 23)
+    m = a / ulp
+    n = m.numerator // m.denominator
+    r = m - n
+    if r > Fraction(1, 2) or (r == Fraction(1, 2) and n % 2 == 1):
+        n += 1
+    return (n * ulp) if q > 0 else -(n * ulp)
+
+
+def _conv_exact(x, w, pad, order="kh_kw_ic", fused=True):
+    """Direct convolution whose every step is one rounding to f32 of the
+    exact value: fma(x, w, acc) when fused, else round(round(x*w) + acc).
+    order names the loop nesting of the taps, outermost first."""
+    n, h, wd, ci = x.shape
+    kh, kw, _, co = w.shape
+    ho, wo = h + 2 * pad - kh + 1, wd + 2 * pad - kw + 1
+    X = [[[[Fraction(float(v)) for v in px] for px in row] for row in img] for img in x]
+    W = [[[[Fraction(float(w[a, b, c, d])) for d in range(co)] for c in range(ci)] for b in range(kw)] for a in range(kh)]
+    taps = [(a, b, c) for a in range(kh) for b in range(kw) for c in range(ci)]
+    if order == "ic_kh_kw":
+        taps.sort(key=lambda t: (t[2], t[0], t[1]))
+    y = np.zeros((n, ho, wo, co), np.float32)
+    for b_ in range(n):
+        for oh in range(ho):
+            for ow in range(wo):
+                for oc in range(co):
+                    acc = Fraction(0)
+                    for a, b, c in taps:
+                        ih, iw = oh + a - pad, ow + b - pad
+                        if not (0 <= ih < h and 0 <= iw < wd):
+                            continue  # out-of-image taps are skipped, as ops.rs:1402-1410 does
+                        p = X[b_][ih][iw][c] * W[a][b][c][oc]
+                        acc = _round_f32(acc + p) if fused else _round_f32(acc + _round_f32(p))
+                    y[b_, oh, ow, oc] = np.float32(float(acc))
+    return y
+
+
+def test_conv_accumulation_order_pinned_in_exact_rationals():
+    # conv2d_f32_nhwc (ops.rs:1356-1436) is acc = fma(x, w, acc) over kh,
+    # then kw, then ic, each step rounded once.  The oracle must equal that
+    # chain evaluated exactly, and the inputs are chosen so that an ic-first
+    # chain or a separately rounded multiply and add give other bits.
+    r = np.random.default_rng(2024)
+    x = r.uniform(-1, 1, (1, 4, 4, 6)).astype(np.float32)
+    w = r.uniform(-1, 1, (3, 3, 6, 3)).astype(np.float32)
+    ref = _conv_exact(x, w, 1)
+    got = oracle.conv2d_f32_nhwc(x, w, (1, 1), (1, 1))
+    np.testing.assert_array_equal(got, ref)
+    np.testing.assert_array_equal(oracle.conv2d_f32_nhwc_st(x, w, (1, 1), (1, 1)), ref)
+    # the planted mistakes are visible on these inputs
+    assert np.any(_conv_exact(x, w, 1, order="ic_kh_kw") != ref)
+    assert np.any(_conv_exact(x, w, 1, fused=False) != ref)
+
+
+def test_round_f32_helper_against_numpy():
+    # the rounding helper itself: equal to numpy's double -> float cast on
+    # values exactly representable in double, ties and subnormals included
+    vals = [1 + 2.0 ** -24, 1 + 3 * 2.0 ** -24, -(1 + 2.0 ** -24), 2.0 ** -149 * 1.5, 2.0 ** -149 * 2.5,
+            3.0 * 2.0 ** -130, 0.1, -123456.789]
+    for v in vals:
+        assert float(_round_f32(Fraction(v))) == float(np.float32(v)), v
