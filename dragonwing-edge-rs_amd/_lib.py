@@ -74,6 +74,7 @@ SIGNATURES = {
     "dw_hip_depthwise_conv2d_f16_nhwc": (I, [P, P, P, P, P] + [Z] * 10 + [I]),
     "dw_hip_depthwise_conv2d_f32_nhwc": (I, [P, P, P, P, P] + [Z] * 10 + [I]),
     "dw_hip_qlinearconv_u8s8": (I, [P, P, P, P, P] + [Z] * 11 + [F, I, P, F, I]),
+    "dw_hip_qlinearconv_u8s8_noalloc": (I, [P, P, P, P, P] + [Z] * 11 + [F, I, P, F, I]),
     "dw_hip_conv2d_i8_nhwc": (I, _CONV),
     "dw_hip_conv2d_requant_relu_i8": (I, _CONV + [F, I]),
     "dw_hip_relu_f32": (I, [P, P, P, Z]),

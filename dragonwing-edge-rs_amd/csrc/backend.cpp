@@ -200,9 +200,11 @@ int dw_hip_backend_create(int device, dw_hip_backend** out) {
   DW_HIP(hipGetDeviceProperties(&prop, device));
   if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
     dw::fail(DW_ERR_UNSUPPORTED, std::string("device is ") + prop.gcnArchName + ", need gfx950");
+  void* scratch = dw::noalloc_scratch_setup(device);
   Backend* b = new Backend();
   b->device = device;
   b->num_cus = prop.multiProcessorCount;
+  b->scratch = scratch;
   DW_HIP(hipStreamCreateWithFlags(&b->stream, hipStreamNonBlocking));
   *out = reinterpret_cast<dw_hip_backend*>(b);
   API_END
@@ -412,14 +414,22 @@ int dw_hip_depthwise_conv2d_f32_nhwc(dw_hip_backend* be, const dw_hip_buffer* in
                        stride_h, stride_w, pad_h, pad_w, act);
 }
 
-int dw_hip_qlinearconv_u8s8(dw_hip_backend* be, const dw_hip_buffer* input, const dw_hip_buffer* kernel,
-                            const dw_hip_buffer* bias, dw_hip_buffer* output, size_t n, size_t h_in,
-                            size_t w_in, size_t c_in, size_t c_out, size_t k_h, size_t k_w,
-                            size_t stride_h, size_t stride_w, size_t pad_h, size_t pad_w,
-                            float x_scale, int x_zp, const float* w_scales, float y_scale, int y_zp) {
-  API_BEGIN
-  Backend* b = B(be);
-  std::lock_guard<std::mutex> lock(b->mu);
+namespace {
+
+// Where a QLinearConv's per-call device data goes: the backend's grow-only
+// workspaces (wpk == nullptr), or caller-provided space of fixed capacity.
+struct QconvSpace {
+  void* wpk = nullptr;
+  size_t wpk_cap = 0;
+  float* ms = nullptr;
+  int* bi = nullptr;
+};
+
+void qlinearconv_impl(Backend* b, const dw_hip_buffer* input, const dw_hip_buffer* kernel,
+                      const dw_hip_buffer* bias, dw_hip_buffer* output, size_t n, size_t h_in, size_t w_in,
+                      size_t c_in, size_t c_out, size_t k_h, size_t k_w, size_t stride_h, size_t stride_w,
+                      size_t pad_h, size_t pad_w, float x_scale, int x_zp, const float* w_scales,
+                      float y_scale, int y_zp, QconvSpace sp, float* m_host) {
   Geo g = geo(n, h_in, w_in, c_in, c_out, k_h, k_w, stride_h, stride_w, pad_h, pad_w);
   require_igemm(g, 1);
   need(input, n * h_in * w_in * c_in, "qlinearconv: input");
@@ -430,26 +440,73 @@ int dw_hip_qlinearconv_u8s8(dw_hip_backend* be, const dw_hip_buffer* input, cons
   if (x_zp < 0 || x_zp > 255 || y_zp < 0 || y_zp > 255)
     dw::fail(DW_ERR_INVALID, "qlinearconv: zero points must be in [0, 255]");
   if (!(x_scale > 0) || !(y_scale > 0)) dw::fail(DW_ERR_INVALID, "qlinearconv: scales must be > 0");
-  std::vector<float> m(c_out);
   for (size_t c = 0; c < c_out; ++c) {
     if (!(w_scales[c] > 0)) dw::fail(DW_ERR_INVALID, "qlinearconv: weight scales must be > 0");
-    m[c] = (x_scale * w_scales[c]) / y_scale;
+    m_host[c] = (x_scale * w_scales[c]) / y_scale;
   }
   dw::IgemmArgs a = igemm_args(g, input->ptr, nullptr, output->ptr, 1);
-  a.wpk = (const uint8_t*)pack_into_ws(b, kernel, a, g, 1);
-  float* ms = (float*)b->workspace(Backend::WS_SCALE, c_out * 4);
-  int* bi = (int*)b->workspace(Backend::WS_BIAS, c_out * 4);
-  b->upload_async(ms, m.data(), c_out * 4);
+  const size_t wpk_bytes = (size_t)a.ksteps * a.cout_pad * 64;
+  if (sp.wpk) {
+    if (wpk_bytes > sp.wpk_cap)
+      dw::fail(DW_ERR_UNSUPPORTED, "qlinearconv: packed weights of " + std::to_string(wpk_bytes) +
+                                       " bytes exceed the no-alloc scratch's " + std::to_string(sp.wpk_cap));
+    dw::launch_pack_weights(b->stream, kernel->ptr, sp.wpk, (int)(g.kh * g.kw * g.ci), (int)g.co, a.cout_pad,
+                            a.ksteps, 1);
+    a.wpk = (const uint8_t*)sp.wpk;
+  } else {
+    a.wpk = (const uint8_t*)pack_into_ws(b, kernel, a, g, 1);
+    sp.ms = (float*)b->workspace(Backend::WS_SCALE, c_out * 4);
+    sp.bi = (int*)b->workspace(Backend::WS_BIAS, c_out * 4);
+  }
+  b->upload_async(sp.ms, m_host, c_out * 4);
   dw::launch_qconv_bias(b->stream, (const int8_t*)kernel->ptr, bias ? (const int*)bias->ptr : nullptr,
-                        bi, (int)(k_h * k_w * c_in), (int)c_out, 128 - x_zp);
+                        sp.bi, (int)(k_h * k_w * c_in), (int)c_out, 128 - x_zp);
   a.epi = dw::EPI_QU8;
   a.xxor = 0x80808080u;
   const uint32_t pb = (uint32_t)((x_zp ^ 0x80) & 0xff);
   a.xpad = pb * 0x01010101u;
-  a.bias_i = bi;
-  a.mscale = ms;
+  a.bias_i = sp.bi;
+  a.mscale = sp.ms;
   a.y_zp = y_zp;
   dw::launch_igemm(b->stream, a, 1);
+}
+
+}  // namespace
+
+int dw_hip_qlinearconv_u8s8(dw_hip_backend* be, const dw_hip_buffer* input, const dw_hip_buffer* kernel,
+                            const dw_hip_buffer* bias, dw_hip_buffer* output, size_t n, size_t h_in,
+                            size_t w_in, size_t c_in, size_t c_out, size_t k_h, size_t k_w,
+                            size_t stride_h, size_t stride_w, size_t pad_h, size_t pad_w,
+                            float x_scale, int x_zp, const float* w_scales, float y_scale, int y_zp) {
+  API_BEGIN
+  Backend* b = B(be);
+  std::lock_guard<std::mutex> lock(b->mu);
+  std::vector<float> m(c_out);
+  qlinearconv_impl(b, input, kernel, bias, output, n, h_in, w_in, c_in, c_out, k_h, k_w, stride_h, stride_w,
+                   pad_h, pad_w, x_scale, x_zp, w_scales, y_scale, y_zp, QconvSpace{}, m.data());
+  API_END
+}
+
+int dw_hip_qlinearconv_u8s8_noalloc(dw_hip_backend* be, const dw_hip_buffer* input, const dw_hip_buffer* kernel,
+                                    const dw_hip_buffer* bias, dw_hip_buffer* output, size_t n, size_t h_in,
+                                    size_t w_in, size_t c_in, size_t c_out, size_t k_h, size_t k_w,
+                                    size_t stride_h, size_t stride_w, size_t pad_h, size_t pad_w,
+                                    float x_scale, int x_zp, const float* w_scales, float y_scale, int y_zp) {
+  API_BEGIN
+  Backend* b = B(be);
+  std::lock_guard<std::mutex> lock(b->mu);
+  if (!b->scratch) dw::fail(DW_ERR_BACKEND, "qlinearconv_noalloc: no scratch on this device");
+  if (c_out > dw::kNoAllocMaxChannels)
+    dw::fail(DW_ERR_UNSUPPORTED, "qlinearconv_noalloc: c_out above " + std::to_string(dw::kNoAllocMaxChannels));
+  float m[dw::kNoAllocMaxChannels];
+  QconvSpace sp;
+  uint8_t* base = (uint8_t*)b->scratch;
+  sp.ms = (float*)base;
+  sp.bi = (int*)(base + dw::kNoAllocMaxChannels * 4);
+  sp.wpk = base + dw::kNoAllocTableBytes;
+  sp.wpk_cap = dw::kNoAllocScratchBytes - dw::kNoAllocTableBytes;
+  qlinearconv_impl(b, input, kernel, bias, output, n, h_in, w_in, c_in, c_out, k_h, k_w, stride_h, stride_w,
+                   pad_h, pad_w, x_scale, x_zp, w_scales, y_scale, y_zp, sp, m);
   API_END
 }
 

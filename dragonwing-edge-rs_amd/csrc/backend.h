@@ -10,6 +10,16 @@ namespace dw {
 
 void set_last_error(const std::string& m);
 
+// Scratch of the no-alloc entry points: one array of this size per device
+// (k_noalloc.hip), laid out as the per-channel multipliers and bias' tables
+// (kNoAllocMaxChannels entries each) followed by the packed weights.
+constexpr size_t kNoAllocScratchBytes = (size_t)8 << 20;
+constexpr size_t kNoAllocMaxChannels = 4096;
+constexpr size_t kNoAllocTableBytes = 2 * kNoAllocMaxChannels * 4;
+// Device address of this device's scratch array (looked up on the first
+// call per device, which must run with that device current).
+void* noalloc_scratch_setup(int device);
+
 // One device, one in-order stream (default priority).  Op functions that need
 // temporary device memory (packed weights, per-channel scales) use grow-only
 // workspaces owned by the backend, so repeated calls do not allocate.
@@ -30,6 +40,7 @@ struct Backend {
   hipStream_t stream = nullptr;
   Ws ws[kWsSlots];
   std::mutex mu;
+  void* scratch = nullptr;  // this device's no-alloc scratch (its device address)
 
   // Holders: the handle itself, every buffer and every graph runtime made
   // on it (as the reference's Arc<Backend>): destroying the handle while

@@ -65,6 +65,17 @@ def qlinearconv_u8s8(be, inp, kernel, bias, out, n, h_in, w_in, c_in, c_out, k_h
                                          float(y_scale), int(y_zp)))
 
 
+def qlinearconv_u8s8_noalloc(be, inp, kernel, bias, out, n, h_in, w_in, c_in, c_out, k_h, k_w, stride_h,
+                             stride_w, pad_h, pad_w, x_scale, x_zp, w_scales, y_scale, y_zp):
+    """qlinearconv_u8s8 with no device allocation (the per-device scratch)."""
+    ws = np.ascontiguousarray(w_scales, np.float32)
+    assert ws.size == c_out
+    check(load().dw_hip_qlinearconv_u8s8_noalloc(be.handle, inp.handle, kernel.handle, _h(bias), out.handle, n,
+                                                 h_in, w_in, c_in, c_out, k_h, k_w, stride_h, stride_w, pad_h,
+                                                 pad_w, float(x_scale), int(x_zp), ws.ctypes.data,
+                                                 float(y_scale), int(y_zp)))
+
+
 def conv2d_i8_nhwc(be, inp, kernel, out_i32, n, h_in, w_in, c_in, c_out, k_h, k_w, stride_h,
                    stride_w, pad_h, pad_w):
     check(load().dw_hip_conv2d_i8_nhwc(be.handle, inp.handle, kernel.handle, out_i32.handle, n, h_in,

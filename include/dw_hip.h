@@ -169,6 +169,26 @@ int dw_hip_qlinearconv_u8s8(dw_hip_backend* be, const dw_hip_buffer* input,
                             size_t stride_w, size_t pad_h, size_t pad_w, float x_scale,
                             int x_zp, const float* w_scales, float y_scale, int y_zp);
 
+/* dw_hip_qlinearconv_u8s8 without any device allocation.  No counterpart in
+ * the reference: for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, hosts that forbid hipMalloc).  The
+ * per-call data the other entry point keeps in grow-only workspaces (packed
+ * weights, per-channel multipliers, bias') goes to a fixed 8 MiB scratch
+ * array per device instead, set up when the backend is created: c_out at
+ * most 4096 and packed weights (ceil(k_h*k_w*c_in / 64) * c_out rounded up
+ * to the channel tile * 64 bytes) at most 8 MiB - 32 KiB, else
+ * DW_ERR_UNSUPPORTED.  Same arguments, results and errors as
+ * dw_hip_qlinearconv_u8s8.  Every call on a device shares that device's
+ * scratch: calls through one backend are ordered on its stream, but calls
+ * that overlap on one device through different backends (streams) race. */
+int dw_hip_qlinearconv_u8s8_noalloc(dw_hip_backend* be, const dw_hip_buffer* input,
+                                    const dw_hip_buffer* kernel, const dw_hip_buffer* bias,
+                                    dw_hip_buffer* output, size_t n, size_t h_in, size_t w_in,
+                                    size_t c_in, size_t c_out, size_t k_h, size_t k_w,
+                                    size_t stride_h, size_t stride_w, size_t pad_h, size_t pad_w,
+                                    float x_scale, int x_zp, const float* w_scales, float y_scale,
+                                    int y_zp);
+
 /* conv2d_i8_nhwc (crates/dragonwing-cpu/src/ops.rs:3086-3142): s8 x s8 ->
  * int32 accumulator, zero padding.  Requires c_in % 16 == 0, c_out % 4 == 0,
  * k_h*k_w <= 31. */

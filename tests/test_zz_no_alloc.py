@@ -1,0 +1,58 @@
+"""dw_hip_qlinearconv_u8s8_noalloc through the C ABI: on two calls in a row,
+the second with a smaller input, its output equals dw_hip_qlinearconv_u8s8's
+(and the oracle's) byte for byte; sizes past its fixed scratch are refused
+before anything is launched."""
+import numpy as np
+import pytest
+
+import oracle
+from dragonwing_edge_rs_amd import HipError, ops, synth
+
+pytestmark = pytest.mark.gpu
+
+
+def run_pair(backend, case, stride):
+    x, w, b = case["x"], case["w"], case["bias"]
+    n, h, wd, ci = x.shape
+    co = w.shape[3]
+    ho, wo = oracle.out_hw(h, wd, 3, 3, stride, stride, 1, 1)
+    bx, bw, bb = backend.from_numpy(x), backend.from_numpy(w), backend.from_numpy(b)
+    y0, y1 = backend.alloc(n * ho * wo * co), backend.alloc(n * ho * wo * co)
+    args = (n, h, wd, ci, co, 3, 3, stride, stride, 1, 1, case["x_scale"], case["x_zp"], case["w_scales"],
+            case["y_scale"], case["y_zp"])
+    ops.qlinearconv_u8s8(backend, bx, bw, bb, y0, *args)
+    ops.qlinearconv_u8s8_noalloc(backend, bx, bw, bb, y1, *args)
+    a = backend.to_numpy(y0, np.uint8, (n, ho, wo, co))
+    c = backend.to_numpy(y1, np.uint8, (n, ho, wo, co))
+    ref = oracle.qlinearconv_u8s8(x, w, b, (stride, stride), (1, 1), case["x_scale"], case["x_zp"],
+                                  case["w_scales"], case["y_scale"], case["y_zp"])
+    return a, c, ref
+
+
+def test_noalloc_matches_allocating_entry_on_two_calls(backend):
+    big = synth.qlinearconv_case(51, n=2, h=40, w=40, c_in=128, c_out=256)
+    small = synth.qlinearconv_case(52, n=1, h=12, w=20, c_in=32, c_out=48)
+    for case, stride in ((big, 2), (small, 1)):
+        a, c, ref = run_pair(backend, case, stride)
+        np.testing.assert_array_equal(c, a)
+        np.testing.assert_array_equal(c, ref)
+        assert len(np.unique(c)) > 50
+
+
+def test_noalloc_refuses_sizes_past_its_scratch(backend):
+    # c_out above 4096, and packed weights above the scratch: refused before
+    # any launch, with the sizes in the message
+    x = np.zeros((1, 4, 4, 16), np.uint8)
+    w = np.zeros((3, 3, 16, 4100), np.int8)
+    bx, bw = backend.from_numpy(x), backend.from_numpy(w)
+    by = backend.alloc(4 * 4 * 4100)
+    with pytest.raises(HipError, match="c_out above 4096"):
+        ops.qlinearconv_u8s8_noalloc(backend, bx, bw, None, by, 1, 4, 4, 16, 4100, 3, 3, 1, 1, 1, 1, 0.02, 128,
+                                     np.full(4100, 0.01, np.float32), 0.05, 128)
+    x = np.zeros((1, 4, 4, 4096), np.uint8)
+    w = np.zeros((3, 3, 4096, 256), np.int8)
+    bx, bw = backend.from_numpy(x), backend.from_numpy(w)
+    by = backend.alloc(4 * 4 * 256)
+    with pytest.raises(HipError, match="exceed the no-alloc scratch"):
+        ops.qlinearconv_u8s8_noalloc(backend, bx, bw, None, by, 1, 4, 4, 4096, 256, 3, 3, 1, 1, 1, 1, 0.02, 128,
+                                     np.full(256, 0.01, np.float32), 0.05, 128)
