@@ -52,6 +52,8 @@ class DwOpParams(C.Structure):
         ("trans_b", I),
         ("clip_min", F),
         ("clip_max", F),
+        ("reg_max", I),
+        ("level_strides", F * 4),
     ]
 
 
@@ -106,6 +108,8 @@ SIGNATURES = {
     "dw_hip_gemm_i8": (I, [P, P, P, P, Z, Z, Z]),
     "dw_hip_global_avg_pool_nhwc": (I, [P, I, P, P, Z, Z, Z, Z]),
     "dw_hip_softmax_f32": (I, [P, P, P, Z, Z]),
+    "dw_hip_yolo_detect_tail": (I, [P, I, P, P, P, P, I, Z, I, I, P]),
+    "dw_hip_yolo_postprocess": (I, [P, P, Z, I, Z, C.c_uint32, C.c_uint32, C.c_float, C.c_float, I, P, Z, P]),
     "dw_graph_create": (I, [I, PP]),
     "dw_graph_destroy": (None, [P]),
     "dw_graph_add_tensor": (I, [P, S, P, I, I]),

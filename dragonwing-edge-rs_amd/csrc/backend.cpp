@@ -835,4 +835,132 @@ int dw_hip_softmax_f32(dw_hip_backend* be, const dw_hip_buffer* x, dw_hip_buffer
   API_END
 }
 
+int dw_hip_yolo_detect_tail(dw_hip_backend* be, int dtype, const dw_hip_buffer* const* levels, const int* h,
+                            const int* w, const float* strides, int num_levels, size_t n, int nc, int reg_max,
+                            dw_hip_buffer* out) {
+  API_BEGIN
+  Backend* bk = B(be);
+  std::lock_guard<std::mutex> lock(bk->mu);
+  if (!levels || !h || !w || !strides) dw::fail(DW_ERR_INVALID, "detect tail: null argument");
+  if (num_levels < 1 || num_levels > 4) dw::fail(DW_ERR_UNSUPPORTED, "detect tail: 1 to 4 levels");
+  if (dtype != DW_DTYPE_F16 && dtype != DW_DTYPE_F32) dw::fail(DW_ERR_UNSUPPORTED, "detect tail: f16 or f32");
+  if (!n || nc < 1 || reg_max < 1) dw::fail(DW_ERR_INVALID, "detect tail: zero size");
+  check_i32(n, "detect tail: batch");
+  const size_t es = dtype == DW_DTYPE_F16 ? 2 : 4;
+  const size_t pix = (size_t)4 * reg_max + (size_t)nc;
+  dw::DetectTailArgs t{};
+  size_t A = 0;
+  for (int s = 0; s < num_levels; ++s) {
+    if (h[s] < 1 || w[s] < 1) dw::fail(DW_ERR_INVALID, "detect tail: empty level");
+    need(levels[s], n * (size_t)h[s] * w[s] * pix * es, "detect tail: level size");
+    t.x[s] = levels[s]->ptr;
+    t.h[s] = h[s];
+    t.w[s] = w[s];
+    t.pix[s] = (int)pix;
+    t.stride[s] = strides[s];
+    A += (size_t)h[s] * w[s];
+  }
+  check_i32(A * (4 + nc), "detect tail: output row");
+  need(out, n * (4 + (size_t)nc) * A * 4, "detect tail: output size");
+  t.levels = num_levels;
+  t.nc = nc;
+  t.reg_max = reg_max;
+  dw::launch_detect_tail(bk->stream, dtype == DW_DTYPE_F16 ? dw::F16 : dw::F32, t, (float*)out->ptr, (int)n);
+  API_END
+}
+
+int dw_hip_yolo_postprocess(dw_hip_backend* be, const dw_hip_buffer* raw, size_t n, int nc, size_t num_det,
+                            uint32_t img_w, uint32_t img_h, float conf_threshold, float iou_threshold,
+                            int agnostic, dw_detection* out, size_t cap, size_t* counts) {
+  API_BEGIN
+  Backend* bk = B(be);
+  std::lock_guard<std::mutex> lock(bk->mu);
+  static_assert(sizeof(dw_detection) == sizeof(dw::DwDetection), "detection layout");
+  if (!counts || (cap && !out)) dw::fail(DW_ERR_INVALID, "postprocess: null output");
+  if (!n || nc < 1 || !num_det) dw::fail(DW_ERR_INVALID, "postprocess: zero size");
+  if (nc > 1024) dw::fail(DW_ERR_UNSUPPORTED, "postprocess: more than 1024 classes");
+  if (num_det > 16384) dw::fail(DW_ERR_UNSUPPORTED, "postprocess: more than 16384 anchors per image");
+  check_i32(n, "postprocess: batch");
+  need(raw, n * (4 + (size_t)nc) * num_det * 4, "postprocess: raw output size");
+  int dev_lds = 0;
+  DW_HIP(hipDeviceGetAttribute(&dev_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, bk->device));
+  const int nmax = dw::kPPMaxCandidates;
+  if ((size_t)dev_lds < dw::pp_nms_lds_bytes(nmax)) dw::fail(DW_ERR_UNSUPPORTED, "postprocess: LDS per workgroup");
+  // workspace: keys, per-anchor detections, then per image nmax-sized arrays
+  const size_t A = num_det;
+  auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
+  const size_t o_keys = 0, o_det = o_keys + al(n * A * 8), o_sa = o_det + al(n * A * 24);
+  const size_t o_pp = o_sa + al(n * nmax * 4), o_od = o_pp + al(n * nmax * 4);
+  const size_t o_op = o_od + al(n * nmax * 24), o_cnt = o_op + al(n * nmax * 4), total = o_cnt + al(n * 16);
+  uint8_t* ws = (uint8_t*)bk->workspace(Backend::WS_POST, total);
+  dw::PostprocessArgs a{};
+  a.raw = (const float*)raw->ptr;
+  a.n = (int)n;
+  a.nc = nc;
+  a.A = (int)A;
+  const float model = 640.0f;  // the reference's fixed model size (postprocess.rs:98)
+  a.sx = (float)img_w / model;
+  a.sy = (float)img_h / model;
+  a.img_w = (float)img_w;
+  a.img_h = (float)img_h;
+  a.conf = conf_threshold;
+  a.iou = iou_threshold;
+  a.agnostic = agnostic ? 1 : 0;
+  a.nmax = nmax;
+  a.keys = (unsigned long long*)(ws + o_keys);
+  a.det = (dw::DwDetection*)(ws + o_det);
+  a.sorted_anchor = (int*)(ws + o_sa);
+  a.part_pos = (int*)(ws + o_pp);
+  a.out_det = (dw::DwDetection*)(ws + o_od);
+  a.out_pos = (int*)(ws + o_op);
+  a.counts = (int*)(ws + o_cnt);
+  dw::launch_yolo_postprocess(bk->stream, a);
+  std::vector<int> cnt(n * 4);
+  DW_HIP(hipMemcpyAsync(cnt.data(), a.counts, n * 16, hipMemcpyDeviceToHost, bk->stream));
+  DW_HIP(hipStreamSynchronize(bk->stream));
+  size_t maxk = 0;
+  for (size_t b = 0; b < n; ++b) {
+    if (cnt[4 * b + 2])
+      dw::fail(DW_ERR_UNSUPPORTED, "postprocess: image " + std::to_string(b) + " has " +
+                                       std::to_string(cnt[4 * b]) + " candidates over the threshold (at most " +
+                                       std::to_string(nmax) + ")");
+    maxk = std::max(maxk, (size_t)cnt[4 * b + 1]);
+  }
+  std::vector<dw::DwDetection> kd(n * (size_t)nmax);
+  std::vector<int> kp(n * (size_t)nmax);
+  if (maxk) {
+    DW_HIP(hipMemcpy2DAsync(kd.data(), (size_t)nmax * 24, a.out_det, (size_t)nmax * 24, maxk * 24, n,
+                            hipMemcpyDeviceToHost, bk->stream));
+    DW_HIP(hipMemcpy2DAsync(kp.data(), (size_t)nmax * 4, a.out_pos, (size_t)nmax * 4, maxk * 4, n,
+                            hipMemcpyDeviceToHost, bk->stream));
+    DW_HIP(hipStreamSynchronize(bk->stream));
+  }
+  // The reference removes suppressed entries from the back with swap_remove
+  // (postprocess.rs:235-242): walking the sorted positions downwards, a
+  // suppressed slot takes the current last element and the list shrinks.
+  // Replayed on slots that name kept detections (-1: suppressed).
+  bool over = false;
+  std::vector<int> slot;
+  for (size_t b = 0; b < n; ++b) {
+    const int nc_b = cnt[4 * b], k = cnt[4 * b + 1];
+    counts[b] = (size_t)k;
+    if ((size_t)k > cap) {
+      over = true;
+      continue;
+    }
+    slot.assign((size_t)nc_b, -1);
+    for (int i = 0; i < k; ++i) slot[(size_t)kp[b * nmax + i]] = i;
+    int len = nc_b;
+    for (int i = nc_b - 1; i >= 0; --i)
+      if (slot[(size_t)i] < 0) {
+        slot[(size_t)i] = slot[(size_t)len - 1];
+        --len;
+      }
+    dw_detection* o = out + b * cap;
+    for (int i = 0; i < len; ++i) memcpy(&o[i], &kd[b * nmax + (size_t)slot[(size_t)i]], sizeof(dw_detection));
+  }
+  if (over) dw::fail(DW_ERR_INVALID, "postprocess: more detections than cap in an image (see counts)");
+  API_END
+}
+
 }  // extern "C"

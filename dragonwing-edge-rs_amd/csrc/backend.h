@@ -30,7 +30,7 @@ void* noalloc_scratch_setup(int device);
 // (the reference's backends are Send + Sync, backend.rs:42-48).  Work from
 // different threads is queued in the order the lock is taken.
 struct Backend {
-  enum { WS_WPACK = 0, WS_SCALE = 1, WS_BIAS = 2, WS_LUT = 3, kWsSlots = 4 };
+  enum { WS_WPACK = 0, WS_SCALE = 1, WS_BIAS = 2, WS_LUT = 3, WS_POST = 4, kWsSlots = 5 };
   struct Ws {
     void* ptr = nullptr;
     size_t bytes = 0;

@@ -169,6 +169,41 @@ void launch_global_avg_pool(hipStream_t st, int dtype, const void* x, void* y, i
 void launch_softmax_rows(hipStream_t st, const float* x, float* y, int rows, int n);
 void launch_softmax_rows_t(hipStream_t st, int dtype, const void* x, void* y, int rows, int n);
 
+// YOLOv8 detect tail and post-processing (k_detect.hip).
+// Detection as postprocess.rs:11-19 lays it out (24 bytes).
+struct DwDetection {
+  float bbox[4];
+  uint32_t class_id;
+  float confidence;
+};
+// Per-level NHWC head outputs [n][h][w][pix], 4 * reg_max box channels
+// then nc class channels at the start of each pixel.
+struct DetectTailArgs {
+  const void* x[4];
+  int h[4], w[4], pix[4];
+  float stride[4];
+  int levels, nc, reg_max;
+};
+void launch_detect_tail(hipStream_t st, int dtype, const DetectTailArgs& t, float* out, int n);
+// Most candidates above the threshold one image may hold (LDS capacity of
+// the per-image NMS workgroup); at most 16384 anchors per image.
+constexpr int kPPMaxCandidates = 8704;
+struct PostprocessArgs {
+  const float* raw;
+  int n, nc, A;
+  float sx, sy, img_w, img_h, conf, iou;
+  int agnostic, nmax;
+  unsigned long long* keys;
+  DwDetection* det;
+  int* sorted_anchor;
+  int* part_pos;
+  DwDetection* out_det;
+  int* out_pos;
+  int* counts;
+};
+size_t pp_nms_lds_bytes(int nmax);
+void launch_yolo_postprocess(hipStream_t st, const PostprocessArgs& a);
+
 // Elementwise glue (count elements, contiguous).
 enum EwOp : int {
   EW_RELU = 0, EW_ADD, EW_MUL, EW_SIGMOID, EW_SILU, EW_BIAS_ADD,

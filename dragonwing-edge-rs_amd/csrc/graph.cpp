@@ -672,7 +672,9 @@ std::string to_json(const GraphIR& g) {
       << ",\"scale_b_over_out\":" << fstr(p.scale_b_over_out) << ",\"has_relu\":" << p.has_relu
       << ",\"epsilon\":" << fstr(p.epsilon) << ",\"act\":" << p.act << ",\"trans_a\":" << p.trans_a
       << ",\"trans_b\":" << p.trans_b << ",\"clip_min\":" << fstr(p.clip_min)
-      << ",\"clip_max\":" << fstr(p.clip_max) << "}";
+      << ",\"clip_max\":" << fstr(p.clip_max) << ",\"reg_max\":" << p.reg_max << ",\"level_strides\":["
+      << fstr(p.level_strides[0]) << "," << fstr(p.level_strides[1]) << "," << fstr(p.level_strides[2]) << ","
+      << fstr(p.level_strides[3]) << "]}";
   }
   o << "]}";
   return o.str();

@@ -781,6 +781,8 @@ void Runtime::lower(std::vector<Group>& groups) {
       gr.kind = "flatten";
     } else if (op.type == "Softmax") {
       gr.kind = "softmax";
+    } else if (op.type == "YoloDetect") {
+      gr.kind = "detect";
     } else if (op.type == "Resize") {
       if (!op.p.mode_nearest) fail(DW_ERR_UNSUPPORTED, "runtime: only nearest Resize is implemented");
       gr.kind = "resize";
@@ -1097,6 +1099,48 @@ void Runtime::emit(const Group& gr) {
       L.bytes += (double)B.data.size();
       L.fn = [=](hipStream_t st) { launch_gemm_ex(st, dt, xb, wb, yb, m, n, k, tb, bb, blen); };
     }
+    launches.push_back(L);
+    return;
+  }
+  if (gr.kind == "detect") {
+    // YOLOv8 detect tail (k_detect.hip): the per-level head outputs, each a
+    // dense or channel-strided NHWC tensor, into [n][4 + nc][A] f32
+    const OpNode& op = g.ops[gr.ops[0]];
+    const int levels = (int)op.in.size();
+    if (levels < 1 || levels > 4) fail(DW_ERR_UNSUPPORTED, "YoloDetect: 1 to 4 inputs");
+    const int reg_max = op.p.reg_max;
+    if (reg_max < 1) fail(DW_ERR_RUNTIME, "YoloDetect: reg_max");
+    DetectTailArgs t{};
+    const RtTensor& x0 = T(op.in[0]);
+    const int dt = x0.dtype;
+    if (dt != F16 && dt != F32) fail(DW_ERR_UNSUPPORTED, "YoloDetect: f16 or f32 inputs");
+    const int nc = (int)x0.c - 4 * reg_max;
+    if (nc < 1) fail(DW_ERR_RUNTIME, "YoloDetect: fewer channels than 4 * reg_max + 1");
+    int64_t A = 0;
+    Launch L;
+    L.op = op.name;
+    L.kernel = "detect_tail";
+    for (int s = 0; s < levels; ++s) {
+      const RtTensor& x = T(op.in[s]);
+      if (x.dtype != dt || x.c != x0.c || x.n != x0.n) fail(DW_ERR_RUNTIME, "YoloDetect: inputs differ");
+      t.x[s] = (const uint8_t*)x.base + (size_t)x.abs_off * dtype_size(dt);
+      t.h[s] = (int)x.h;
+      t.w[s] = (int)x.w;
+      t.pix[s] = x.pix_stride;
+      t.stride[s] = op.p.level_strides[s];
+      A += x.h * x.w;
+      L.bytes += (double)x.bytes();
+    }
+    const RtTensor& y = T(op.out[0]);
+    if (y.dtype != F32 || y.pixels() * y.c != x0.n * (4 + nc) * A)
+      fail(DW_ERR_RUNTIME, "YoloDetect: output must be f32 [n][4 + nc][A]");
+    t.levels = levels;
+    t.nc = nc;
+    t.reg_max = reg_max;
+    float* yb = (float*)y.base;
+    const int n = (int)x0.n;
+    L.bytes += (double)y.bytes();
+    L.fn = [=](hipStream_t st) { launch_detect_tail(st, dt, t, yb, n); };
     launches.push_back(L);
     return;
   }

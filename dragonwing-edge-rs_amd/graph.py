@@ -25,7 +25,7 @@ OP_KIND = {
     "Resize": 8, "BatchNorm": 9, "Requantize": 10, "AddQuantized": 11, "Quantize": 12, "Dequantize": 13,
     "Conv2dRequantReluI8Nhwc": 14, "QLinearConv": 32, "QuantizeLinear": 33, "DequantizeLinear": 34,
     "QLinearAdd": 35, "QLinearLUT": 36, "Gemm": 15, "GlobalAvgPool": 16, "Softmax": 17, "Clip": 18,
-    "Reshape": 19,
+    "Reshape": 19, "YoloDetect": 37,
 }
 # default OpParams kind per op_type
 KIND_OF_TYPE = {"Conv": "Conv2d", "Add": "Add", "Mul": "Mul", "Sigmoid": "Sigmoid", "MaxPool": "MaxPool",
@@ -34,7 +34,7 @@ KIND_OF_TYPE = {"Conv": "Conv2d", "Add": "Add", "Mul": "Mul", "Sigmoid": "Sigmoi
                 "GlobalAveragePool": "GlobalAvgPool", "Softmax": "Softmax", "Clip": "Clip",
                 "Reshape": "Reshape", "Requantize": "Requantize", "AddQuantized": "AddQuantized",
                 "Quantize": "Quantize", "Dequantize": "Dequantize",
-                "Conv2dRequantReluI8": "Conv2dRequantReluI8Nhwc"}
+                "Conv2dRequantReluI8": "Conv2dRequantReluI8Nhwc", "YoloDetect": "YoloDetect"}
 
 
 def _params(kind: str, **kw) -> DwOpParams:
@@ -65,6 +65,10 @@ def _params(kind: str, **kw) -> DwOpParams:
     p.trans_b = int(kw.get("trans_b", 0))
     p.clip_min = kw.get("clip_min", float("-inf"))
     p.clip_max = kw.get("clip_max", float("inf"))
+    p.reg_max = int(kw.get("reg_max", 0))
+    ls = list(kw.get("level_strides", ()))
+    for i, v in enumerate(ls[:4]):
+        p.level_strides[i] = float(v)
     return p
 
 

@@ -199,3 +199,35 @@ def global_avg_pool_nhwc(be, dtype, x, y, n, h, w, c):
 
 def softmax_f32(be, x, y, rows, n):
     check(load().dw_hip_softmax_f32(be.handle, x.handle, y.handle, rows, n))
+
+
+# --- YOLOv8 detect tail and post-processing ---------------------------------
+
+DETECTION = np.dtype([("bbox", np.float32, 4), ("class_id", np.uint32), ("confidence", np.float32)])
+
+
+def yolo_detect_tail(be, levels, hw, strides, n, out, nc=80, reg_max=16, dtype=DTYPE_F16):
+    """The exported detect tail (DFL, dist2bbox, sigmoid, concat) over the
+    per-level NHWC head outputs (buffers of [n, h, w, 4*reg_max + nc]) into
+    out [n, 4 + nc, A] f32.  hw: [(h, w)] per level."""
+    k = len(levels)
+    bufs = (C.c_void_p * k)(*[b.handle for b in levels])
+    hs = (C.c_int * k)(*[int(h) for h, _ in hw])
+    ws = (C.c_int * k)(*[int(w) for _, w in hw])
+    st = (C.c_float * k)(*[float(s) for s in strides])
+    check(load().dw_hip_yolo_detect_tail(be.handle, dtype, C.cast(bufs, C.c_void_p), C.cast(hs, C.c_void_p),
+                                         C.cast(ws, C.c_void_p), C.cast(st, C.c_void_p), k, n, nc, reg_max,
+                                         out.handle))
+
+
+def yolo_postprocess(be, raw, n, nc, num_det, img_w=640, img_h=640, conf=0.25, iou=0.45, agnostic=False,
+                     cap=None):
+    """postprocess_yolo (postprocess.rs:279-305) per image of the device
+    buffer raw [n, 4 + nc, num_det] f32: a list of DETECTION arrays, one per
+    image, in the reference's order."""
+    cap = num_det if cap is None else cap
+    out = np.zeros((n, cap), DETECTION)
+    counts = np.zeros(n, np.uint64)
+    check(load().dw_hip_yolo_postprocess(be.handle, raw.handle, n, nc, num_det, img_w, img_h, conf, iou,
+                                         int(agnostic), out.ctypes.data, cap, counts.ctypes.data))
+    return [out[b, :int(counts[b])].copy() for b in range(n)]

@@ -249,3 +249,21 @@ def int8_graph(backend, batch: int = 32, size: int = 640, calib: np.ndarray | No
     g.quantize_qdq(info["keep_f16"])
     info["ranges"] = ranges
     return g, info
+
+
+def add_detect_tail(g: Graph, info: dict, name: str = "output0", keep_heads: bool = False) -> str:
+    """Appends the exported detect tail (DFL, dist2bbox, sigmoid, concat) to a
+    finished f16 or u8 graph whose outputs are the three per-level head
+    tensors: one YoloDetect op writing [batch, 4 + NC, A] f32, which becomes
+    the graph's output (after the head tensors with keep_heads).  Strides
+    8, 16, 32 (input size over level size)."""
+    outs = info["outputs"]
+    d = g.to_dict()["tensors"]
+    size = info["size"]
+    levels = [d[o]["dims"] for o in outs]  # NHWC after the passes
+    A = sum(h * w for _, h, w, _ in levels)
+    strides = [size // h for _, h, _, _ in levels]
+    g.add_tensor(name, (info["batch"], 4 + NC, A), "f32")
+    g.add_op("detect_tail", "YoloDetect", list(outs), [name], reg_max=REG_MAX, level_strides=strides)
+    g.set_io([info["input"]], (list(outs) if keep_heads else []) + [name])
+    return name

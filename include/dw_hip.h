@@ -291,6 +291,38 @@ int dw_hip_global_avg_pool_nhwc(dw_hip_backend* be, int dtype, const dw_hip_buff
  * agree with the CPU to a few ulps. */
 int dw_hip_softmax_f32(dw_hip_backend* be, const dw_hip_buffer* x, dw_hip_buffer* y, size_t rows, size_t n);
 
+/* YOLOv8 detect tail: the exported graph's ops after the head convs
+ * (ultralytics Detect: DFL softmax over each side's reg_max bins and the 1x1
+ * expectation, dist2bbox, times the level stride, sigmoid of the classes),
+ * as the reference's f32 ops compute them (softmax_f32 ops.rs:1609-1638,
+ * conv2d_f32 ops.rs:1356-1436, sigmoid_f32 ops.rs:1866-1870).  levels[i]:
+ * NHWC [n][h[i]][w[i]][4*reg_max + nc] head outputs of element type dtype
+ * (DW_DTYPE_F16 or DW_DTYPE_F32); out: [n][4 + nc][A] f32, A = sum h*w,
+ * anchors level by level in row-major order.  exp is the device's. */
+int dw_hip_yolo_detect_tail(dw_hip_backend* be, int dtype, const dw_hip_buffer* const* levels, const int* h,
+                            const int* w, const float* strides, int num_levels, size_t n, int nc, int reg_max,
+                            dw_hip_buffer* out);
+
+/* Detection (crates/dragonwing-onnx/src/postprocess.rs:11-19). */
+typedef struct dw_detection {
+  float bbox[4]; /* x1, y1, x2, y2 in image pixels */
+  uint32_t class_id;
+  float confidence;
+} dw_detection;
+
+/* postprocess_yolo (postprocess.rs:279-305) for each of n images of raw
+ * [n][4 + nc][A] f32 on the device: decode_detections_v8 (:78-146), then
+ * nms (:214-243), or nms_agnostic (:245-277) when agnostic is nonzero.
+ * Results are the reference's, in its order (stable sort by confidence,
+ * greedy suppression, swap_remove of the suppressed entries).  out holds
+ * cap detections per image (image b at out + b * cap); counts[b] receives
+ * image b's number of detections.  DW_ERR_INVALID if one exceeds cap;
+ * DW_ERR_UNSUPPORTED above 16384 anchors per image or 8704 candidates
+ * over the threshold in one image.  Synchronous (results on the host). */
+int dw_hip_yolo_postprocess(dw_hip_backend* be, const dw_hip_buffer* raw, size_t n, int nc, size_t num_det,
+                            uint32_t img_w, uint32_t img_h, float conf_threshold, float iou_threshold,
+                            int agnostic, dw_detection* out, size_t cap, size_t* counts);
+
 /* ------------------------------------------------------------------------ */
 /* Graph IR — the C form of dragonwing_onnx::Graph / CompiledOp / OpParams   */
 /* (crates/dragonwing-onnx/src/graph.rs:18-31, builder.rs:204-361), plus the */
@@ -327,7 +359,9 @@ typedef enum dw_op_kind {
   DW_OP_QUANTIZE_LINEAR = 33,
   DW_OP_DEQUANTIZE_LINEAR = 34,
   DW_OP_QLINEAR_ADD = 35,
-  DW_OP_QLINEAR_LUT = 36    /* quantized elementwise activation by 256-entry table */
+  DW_OP_QLINEAR_LUT = 36,   /* quantized elementwise activation by 256-entry table */
+  DW_OP_YOLO_DETECT = 37    /* YOLOv8 detect tail (dw_hip_yolo_detect_tail): inputs the
+                             * per-level head outputs, output [n][4 + nc][A] f32 */
 } dw_op_kind;
 
 typedef struct dw_op_params {
@@ -351,6 +385,8 @@ typedef struct dw_op_params {
   float alpha, beta;        /* Gemm (carried; the reference's runtime ignores them) */
   int trans_a, trans_b;     /* Gemm                                           */
   float clip_min, clip_max; /* Clip                                           */
+  int reg_max;              /* YoloDetect: DFL bins per box side               */
+  float level_strides[4];   /* YoloDetect: stride of each input level          */
 } dw_op_params;
 
 /* sizeof(dw_op_params) as compiled into the library.  A binding that declares

@@ -99,6 +99,9 @@ def _declare(L: C.CDLL) -> None:
         "dwo_global_avg_pool_f32": (None, [_P, _P, _Z, _Z, _Z, _Z]),
         "dwo_global_avg_pool_fp16": (None, [_P, _P, _Z, _Z, _Z, _Z]),
         "dwo_softmax_f32": (None, [_P, _P, _Z, _Z]),
+        "dwo_yolo_detect_tail_f16": (None, [_P, _P, _P, _P, _P, _I, _I, _I, _I]),
+        "dwo_iou": (_F, [_P, _P]),
+        "dwo_yolo_postprocess": (None, [_P, _P, _P, _Z, _Z, _Z, C.c_uint32, C.c_uint32, _F, _F, _I, _Z]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -532,3 +535,49 @@ def gemm_tb(a, b):
     c = np.empty((m, n), dt)
     (lib().dwo_gemm_fp16_tb if f16 else lib().dwo_gemm_f32_tb)(_p(c), _p(a), _p(b), m, n, k)
     return c
+
+
+# --- YOLOv8 detect tail and post-processing (Part C) -----------------------
+
+DETECTION = np.dtype([("bbox", np.float32, 4), ("class_id", np.uint32), ("confidence", np.float32)])
+
+
+def yolo_detect_tail_f16(levels, strides, nc=80, reg_max=16):
+    """The exported detect tail (DFL softmax + 1x1 expectation, dist2bbox,
+    sigmoid, concat) over per-level NHWC f16 head outputs [n, h, w, 4*reg_max + nc]
+    (uint16 bits).  Returns [n, 4 + nc, A] f32."""
+    xs = [np.ascontiguousarray(x, np.uint16) for x in levels]
+    n = xs[0].shape[0]
+    hs = np.array([x.shape[1] for x in xs], np.int32)
+    ws = np.array([x.shape[2] for x in xs], np.int32)
+    for x in xs:
+        assert x.shape[0] == n and x.shape[3] == 4 * reg_max + nc
+    st = np.asarray(strides, np.float32)
+    ptrs = (C.c_void_p * len(xs))(*[x.ctypes.data for x in xs])
+    A = int((hs * ws).sum())
+    out = np.empty((n, 4 + nc, A), np.float32)
+    lib().dwo_yolo_detect_tail_f16(_p(out), C.cast(ptrs, C.c_void_p), _p(hs), _p(ws), _p(st), len(xs), n, nc,
+                                   reg_max)
+    return out
+
+
+def iou(a, b):
+    """iou (postprocess.rs:36-55) of two [x1, y1, x2, y2] boxes."""
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    return float(lib().dwo_iou(_p(a), _p(b)))
+
+
+def yolo_postprocess(raw, img_w=640, img_h=640, conf=0.25, iou_thr=0.45, agnostic=False):
+    """postprocess_yolo (postprocess.rs:279-305) per image of raw [n, 4 + nc, A]
+    f32: a list (one per image) of DETECTION arrays in the reference's order."""
+    raw = np.ascontiguousarray(raw, np.float32)
+    if raw.ndim == 2:
+        raw = raw[None]
+    n, ch, A = raw.shape
+    cap = A
+    out = np.zeros((n, cap), DETECTION)
+    counts = np.zeros(n, np.uint64)
+    lib().dwo_yolo_postprocess(out.ctypes.data, counts.ctypes.data, _p(raw), n, ch - 4, A, img_w, img_h, conf,
+                               iou_thr, int(agnostic), cap)
+    return [out[b, :int(counts[b])].copy() for b in range(n)]

@@ -136,6 +136,13 @@ class CpuGraph:
             self.vals[out[0]] = oracle.dequantize_i8_to_f32(ins[0], op["scale"])
         elif ty == "Clip":
             self.vals[out[0]] = oracle.clip(ins[0], op["clip_min"], op["clip_max"])
+        elif ty == "YoloDetect":
+            # the exported detect tail (oracle Part C), f16 levels
+            if any(x.dtype != np.uint16 for x in ins):
+                raise NotImplementedError("YoloDetect on non-f16 inputs")
+            nc = ins[0].shape[3] - 4 * op["reg_max"]
+            y = oracle.yolo_detect_tail_f16(ins, op["level_strides"][:len(ins)], nc, op["reg_max"])
+            self.vals[out[0]] = y.reshape(t[out[0]]["dims"])
         elif ty == "Softmax":
             x = ins[0]
             self.vals[out[0]] = (oracle.softmax_f16 if x.dtype == np.uint16 else oracle.softmax_f32)(x)

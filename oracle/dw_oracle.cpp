@@ -772,4 +772,157 @@ void dwo_maxpool2d_padded_nhwc(void* out, const void* in, size_t n, size_t h_in,
         }
 }
 
+// ===========================================================================
+// Part C — YOLOv8 detect tail and post-processing
+// ===========================================================================
+
+// The detect tail of an exported YOLOv8 graph (ultralytics Detect in
+// inference: DFL, dist2bbox, sigmoid, concat), written with the reference's
+// f32 ops in the order the exported graph applies them:
+//   per anchor (level s, grid cell gy, gx; stride st), x = the level's 4*R + nc
+//   channels widened by F16::to_f32 (dtype.rs:226-263);
+//   side j in 0..4: p = softmax_f32 over x[j*R .. j*R+R) (ops.rs:1609-1638),
+//     d_j = the 1x1 DFL conv with weights 0..R-1: acc = fma(p_k, k, acc) from
+//     +0 in k order (conv2d_f32_nhwc, ops.rs:1356-1436);
+//   anchor (gx + 0.5, gy + 0.5); x1 = ax - d0, y1 = ay - d1, x2 = ax + d2,
+//     y2 = ay + d3 (sub_f32 / add_f32); cx = (x1 + x2) / 2, cy = (y1 + y2) / 2,
+//     w = x2 - x1, h = y2 - y1 (div_f32 by 2), each times st (mul_f32);
+//   class c: sigmoid_f32 (ops.rs:1866-1870, 1 / (1 + exp(-x))).
+// Output [n][4 + nc][A], A = sum of the levels' h * w, level-major then
+// row-major anchors (the ONNX export's [1, 84, 8400] layout).
+// x[s]: [n][h_s][w_s][4*R + nc] f16 bits.
+void dwo_yolo_detect_tail_f16(float* out, const uint16_t* const* x, const int* hs, const int* ws,
+                              const float* strides, int levels, int n, int nc, int reg_max) {
+  int A = 0;
+  for (int s = 0; s < levels; ++s) A += hs[s] * ws[s];
+  const int ch = 4 * reg_max + nc;
+  std::vector<float> v(reg_max), e(reg_max);
+  for (int b = 0; b < n; ++b) {
+    int a = 0;
+    for (int s = 0; s < levels; ++s)
+      for (int gy = 0; gy < hs[s]; ++gy)
+        for (int gx = 0; gx < ws[s]; ++gx, ++a) {
+          const uint16_t* px = x[s] + (((size_t)b * hs[s] + gy) * ws[s] + gx) * ch;
+          float* o = out + (size_t)b * (4 + nc) * A + a;
+          float d[4];
+          for (int j = 0; j < 4; ++j) {
+            for (int k = 0; k < reg_max; ++k) v[k] = dwo_f16_to_f32(px[j * reg_max + k]);
+            dwo_softmax_f32(e.data(), v.data(), 1, reg_max);
+            float acc = 0.0f;
+            for (int k = 0; k < reg_max; ++k) acc = fmaf(e[k], (float)k, acc);
+            d[j] = acc;
+          }
+          const float ax = (float)gx + 0.5f, ay = (float)gy + 0.5f;
+          const float x1 = ax - d[0], y1 = ay - d[1], x2 = ax + d[2], y2 = ay + d[3];
+          const float cx = (x1 + x2) / 2.0f, cy = (y1 + y2) / 2.0f;
+          const float w = x2 - x1, h = y2 - y1;
+          o[0] = cx * strides[s];
+          o[(size_t)A] = cy * strides[s];
+          o[(size_t)2 * A] = w * strides[s];
+          o[(size_t)3 * A] = h * strides[s];
+          for (int c = 0; c < nc; ++c) {
+            const float xv = dwo_f16_to_f32(px[4 * reg_max + c]);
+            o[(size_t)(4 + c) * A] = 1.0f / (1.0f + expf(-xv));
+          }
+        }
+  }
+}
+
+// Detection (postprocess.rs:11-19): bbox [x1, y1, x2, y2], class id, confidence.
+struct DwoDetection {
+  float bbox[4];
+  uint32_t class_id;
+  float confidence;
+};
+
+static float det_area(const DwoDetection& d) {  // Detection::area, postprocess.rs:28-32
+  const float w = fmaxf(d.bbox[2] - d.bbox[0], 0.0f);
+  const float h = fmaxf(d.bbox[3] - d.bbox[1], 0.0f);
+  return w * h;
+}
+
+// iou (postprocess.rs:36-55).
+float dwo_iou(const float* a, const float* b) {
+  DwoDetection da{}, db{};
+  memcpy(da.bbox, a, 16);
+  memcpy(db.bbox, b, 16);
+  const float x1 = fmaxf(a[0], b[0]), y1 = fmaxf(a[1], b[1]);
+  const float x2 = fminf(a[2], b[2]), y2 = fminf(a[3], b[3]);
+  const float iw = fmaxf(x2 - x1, 0.0f), ih = fmaxf(y2 - y1, 0.0f);
+  const float inter = iw * ih;
+  const float uni = det_area(da) + det_area(db) - inter;
+  return uni > 0.0f ? inter / uni : 0.0f;
+}
+
+// decode_detections_v8 (postprocess.rs:78-146) on one image's [4 + nc][A]
+// output: best class by strict '>' from (0, 0.0); skipped below the
+// threshold; corners from the centre and size through the fixed 640 model
+// size, clamped to the image.
+static void decode_v8(std::vector<DwoDetection>& dets, const float* raw, size_t nc, size_t A,
+                      uint32_t img_w, uint32_t img_h, float conf) {
+  const float model = 640.0f;
+  const float sx = (float)img_w / model, sy = (float)img_h / model;
+  for (size_t a = 0; a < A; ++a) {
+    const float cx = raw[a], cy = raw[A + a], w = raw[2 * A + a], h = raw[3 * A + a];
+    size_t best = 0;
+    float best_conf = 0.0f;
+    for (size_t c = 0; c < nc; ++c) {
+      const float v = raw[(4 + c) * A + a];
+      if (v > best_conf) {
+        best_conf = v;
+        best = c;
+      }
+    }
+    if (best_conf < conf) continue;
+    float x1 = (cx - w / 2.0f) * sx, y1 = (cy - h / 2.0f) * sy;
+    float x2 = (cx + w / 2.0f) * sx, y2 = (cy + h / 2.0f) * sy;
+    x1 = fminf(fmaxf(x1, 0.0f), (float)img_w);
+    y1 = fminf(fmaxf(y1, 0.0f), (float)img_h);
+    x2 = fminf(fmaxf(x2, 0.0f), (float)img_w);
+    y2 = fminf(fmaxf(y2, 0.0f), (float)img_h);
+    dets.push_back({{x1, y1, x2, y2}, (uint32_t)best, best_conf});
+  }
+}
+
+// nms / nms_agnostic (postprocess.rs:214-277): stable sort by confidence,
+// descending; greedy suppression (same class unless agnostic) where
+// IoU > threshold; suppressed entries removed by swap_remove from the back.
+static void nms_v8(std::vector<DwoDetection>& d, float iou_thr, bool agnostic) {
+  std::stable_sort(d.begin(), d.end(), [](const DwoDetection& a, const DwoDetection& b) {
+    return b.confidence < a.confidence;  // partial_cmp(b, a) == Less
+  });
+  std::vector<char> keep(d.size(), 1);
+  for (size_t i = 0; i < d.size(); ++i) {
+    if (!keep[i]) continue;
+    for (size_t j = i + 1; j < d.size(); ++j) {
+      if (!keep[j]) continue;
+      if (!agnostic && d[i].class_id != d[j].class_id) continue;
+      if (dwo_iou(d[i].bbox, d[j].bbox) > iou_thr) keep[j] = 0;
+    }
+  }
+  size_t i = d.size();
+  while (i > 0) {
+    --i;
+    if (!keep[i]) {
+      d[i] = d.back();
+      d.pop_back();
+    }
+  }
+}
+
+// postprocess_yolo (postprocess.rs:279-305) for each of n images of
+// raw [n][4 + nc][A]; agnostic selects nms_agnostic.  Writes at most `cap`
+// detections per image to out[b * cap ...] and the full count to counts[b].
+void dwo_yolo_postprocess(DwoDetection* out, size_t* counts, const float* raw, size_t n, size_t nc,
+                          size_t A, uint32_t img_w, uint32_t img_h, float conf, float iou_thr,
+                          int agnostic, size_t cap) {
+  for (size_t b = 0; b < n; ++b) {
+    std::vector<DwoDetection> d;
+    decode_v8(d, raw + b * (4 + nc) * A, nc, A, img_w, img_h, conf);
+    nms_v8(d, iou_thr, agnostic != 0);
+    counts[b] = d.size();
+    for (size_t i = 0; i < d.size() && i < cap; ++i) out[b * cap + i] = d[i];
+  }
+}
+
 }  // extern "C"
