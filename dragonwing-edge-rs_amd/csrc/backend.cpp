@@ -510,6 +510,49 @@ int dw_hip_qlinearconv_u8s8_noalloc(dw_hip_backend* be, const dw_hip_buffer* inp
   API_END
 }
 
+int dw_hip_qgemm_u8s8(dw_hip_backend* be, const dw_hip_buffer* a, const dw_hip_buffer* b, const dw_hip_buffer* bias,
+                      dw_hip_buffer* y, size_t m, size_t n, size_t k, int trans_b, float a_scale, int a_zp,
+                      const float* b_scales, float y_scale, int y_zp) {
+  API_BEGIN
+  Backend* bk = B(be);
+  std::lock_guard<std::mutex> lock(bk->mu);
+  if (!m || !n || !k) dw::fail(DW_ERR_INVALID, "qgemm: zero size");
+  check_i32(m * k, "qgemm: A");
+  check_i32(k * n, "qgemm: B");
+  need(b, k * n, "qgemm: B");
+  // B as [k][n] (the 1x1 HWIO layout); a transposed B goes through a
+  // workspace copy first
+  dw_hip_buffer bt{bk, b->ptr, b->len};
+  if (trans_b) {
+    bt.ptr = bk->workspace(Backend::WS_POST, k * n);
+    dw::launch_transpose_u8(bk->stream, b->ptr, bt.ptr, (int)n, (int)k);
+  }
+  std::vector<float> ms(n);
+  // rows of A are the pixels of a 1x1 convolution over n = m images of 1 x 1
+  qlinearconv_impl(bk, a, &bt, bias, y, m, 1, 1, k, n, 1, 1, 1, 1, 0, 0, a_scale, a_zp, b_scales, y_scale, y_zp,
+                   QconvSpace{}, ms.data());
+  API_END
+}
+
+int dw_hip_qlinear_global_avg_pool_u8(dw_hip_backend* be, const dw_hip_buffer* x, dw_hip_buffer* y, size_t n,
+                                      size_t h, size_t w, size_t c, float x_scale, int x_zp, float y_scale,
+                                      int y_zp) {
+  API_BEGIN
+  Backend* bk = B(be);
+  std::lock_guard<std::mutex> lock(bk->mu);
+  if (!n || !h || !w || !c) dw::fail(DW_ERR_INVALID, "qlinear_gap: zero size");
+  check_i32(n * h * w * c, "qlinear_gap: input");
+  if (h * w > (size_t)(1 << 23)) dw::fail(DW_ERR_UNSUPPORTED, "qlinear_gap: more than 2^23 pixels per image");
+  if (!(x_scale > 0) || !(y_scale > 0)) dw::fail(DW_ERR_INVALID, "qlinear_gap: scales must be > 0");
+  if (x_zp < 0 || x_zp > 255 || y_zp < 0 || y_zp > 255) dw::fail(DW_ERR_INVALID, "qlinear_gap: zero points");
+  need(x, n * h * w * c, "qlinear_gap: input");
+  need(y, n * c, "qlinear_gap: output");
+  const float m = (x_scale / y_scale) / (float)(h * w);
+  dw::launch_qlinear_gap(bk->stream, (const uint8_t*)x->ptr, (uint8_t*)y->ptr, (int)n, (int)(h * w), (int)c, x_zp, m,
+                         y_zp);
+  API_END
+}
+
 int dw_hip_conv2d_i8_nhwc(dw_hip_backend* be, const dw_hip_buffer* input, const dw_hip_buffer* kernel,
                           dw_hip_buffer* output_i32, size_t n, size_t h_in, size_t w_in, size_t c_in,
                           size_t c_out, size_t k_h, size_t k_w, size_t stride_h, size_t stride_w,

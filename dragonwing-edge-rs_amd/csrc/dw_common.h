@@ -169,6 +169,12 @@ void launch_global_avg_pool(hipStream_t st, int dtype, const void* x, void* y, i
 void launch_softmax_rows(hipStream_t st, const float* x, float* y, int rows, int n);
 void launch_softmax_rows_t(hipStream_t st, int dtype, const void* x, void* y, int rows, int n);
 
+// QLinearGlobalAveragePool (u8 NHWC [n][hw][c] -> [n][c]) with
+// m = (x_scale / y_scale) / hw; byte-matrix transpose (dst = src^T).
+void launch_qlinear_gap(hipStream_t st, const uint8_t* x, uint8_t* y, int n, int hw, int c, int x_zp, float m,
+                        int y_zp);
+void launch_transpose_u8(hipStream_t st, const void* src, void* dst, int rows, int cols);
+
 // YOLOv8 detect tail and post-processing (k_detect.hip).
 // Detection as postprocess.rs:11-19 lays it out (24 bytes).
 struct DwDetection {

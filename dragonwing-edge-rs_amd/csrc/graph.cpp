@@ -435,7 +435,8 @@ void quantize_qdq(GraphIR& g, const std::set<std::string>& keep_f16) {
   // --- shared-scale groups
   UF uf;
   for (auto& op : g.ops) {
-    if (op.type == "Concat" || op.type == "Split" || op.type == "MaxPool" || op.type == "Resize") {
+    if (op.type == "Concat" || op.type == "Split" || op.type == "MaxPool" || op.type == "Resize" ||
+        op.type == "Flatten" || op.type == "Reshape") {
       for (auto& i : op.in)
         if (!g.tensor(i).is_init)
           for (auto& o : op.out) uf.join(i, o);
@@ -615,10 +616,76 @@ void quantize_qdq(GraphIR& g, const std::set<std::string>& keep_f16) {
       out.push_back(op);  // f16 concat of fp16 results
       continue;
     }
-    if (op.type == "Concat" || op.type == "Split" || op.type == "MaxPool" || op.type == "Resize") {
+    if (op.type == "Concat" || op.type == "Split" || op.type == "MaxPool" || op.type == "Resize" ||
+        op.type == "Flatten" || op.type == "Reshape") {
       for (auto& i : op.in)
         if (!g.tensor(i).is_init) i = need_u8(i);
       for (auto& o : op.out) make_u8(o);
+      out.push_back(op);
+      continue;
+    }
+    if (op.type == "GlobalAveragePool") {
+      op.in[0] = need_u8(op.in[0]);
+      make_u8(op.out[0]);
+      op.type = "QLinearGlobalAveragePool";
+      out.push_back(op);
+      continue;
+    }
+    if (op.type == "Gemm") {
+      // QGemm: B quantized per output column (symmetric s8, as the convs'
+      // output channels), stored [1][1][k][n] so it runs as a 1x1
+      // QLinearConv over the rows of A; bias rint(b / (xs * ws[j]))
+      if (op.p.trans_a) fail(DW_ERR_UNSUPPORTED, "quantize_qdq: Gemm transA");
+      TensorInfo& W = g.tensor(op.in[1]);
+      if (!W.is_init || W.dims.size() != 2 || W.dtype != DW_DTYPE_F32)
+        fail(DW_ERR_UNSUPPORTED, "quantize_qdq: Gemm B must be a 2-D f32 initializer");
+      const bool tb = op.p.trans_b != 0;
+      const int64_t k = tb ? W.dims[1] : W.dims[0], n = tb ? W.dims[0] : W.dims[1];
+      auto w = as_f32(W);
+      std::vector<float> wk((size_t)(k * n));
+      for (int64_t p = 0; p < k; ++p)
+        for (int64_t j = 0; j < n; ++j) wk[p * n + j] = tb ? w[j * k + p] : w[p * n + j];
+      const std::string x = need_u8(op.in[0]);
+      const TensorInfo& X = g.tensor(x);
+      std::vector<float> ws(n);
+      std::vector<int8_t> wq(wk.size());
+      for (int64_t j = 0; j < n; ++j) {
+        float am = 0.0f;
+        for (int64_t p = 0; p < k; ++p) am = fmaxf(am, fabsf(wk[p * n + j]));
+        ws[j] = am > 0.0f ? am / 127.0f : 1.0f;
+        const float inv = 1.0f / ws[j];
+        for (int64_t p = 0; p < k; ++p) {
+          float r = roundf(wk[p * n + j] * inv);
+          r = r < -128.0f ? -128.0f : (r > 127.0f ? 127.0f : r);
+          wq[p * n + j] = (int8_t)r;
+        }
+      }
+      W.data.assign((const uint8_t*)wq.data(), (const uint8_t*)wq.data() + wq.size());
+      W.dtype = DW_DTYPE_I8;
+      W.dims = {1, 1, k, n};
+      W.ch_scales = ws;
+      if (op.in.size() > 2 && !op.in[2].empty()) {
+        TensorInfo& Bt = g.tensor(op.in[2]);
+        auto b = as_f32(Bt);
+        if ((int64_t)b.size() != n) fail(DW_ERR_UNSUPPORTED, "quantize_qdq: Gemm bias must have n values");
+        std::vector<int32_t> bq(n);
+        for (int64_t j = 0; j < n; ++j) {
+          const double sc = (double)(X.scale * ws[j]);
+          double r = nearbyint((double)b[j] / sc);
+          r = std::min(std::max(r, -2147483648.0), 2147483647.0);
+          bq[j] = (int32_t)r;
+        }
+        Bt.data.assign((const uint8_t*)bq.data(), (const uint8_t*)bq.data() + bq.size() * 4);
+        Bt.dtype = DW_DTYPE_I32;
+      }
+      op.type = "QGemm";
+      op.p.kind = DW_OP_QLINEAR_CONV;
+      op.p.kernel_shape[0] = op.p.kernel_shape[1] = 1;
+      op.p.strides[0] = op.p.strides[1] = 1;
+      for (int& pd : op.p.pads) pd = 0;
+      op.p.trans_b = 0;
+      op.in[0] = x;
+      make_u8(op.out[0]);
       out.push_back(op);
       continue;
     }

@@ -124,6 +124,39 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(const void* X, void* 
   }
 }
 
+// QLinearGlobalAveragePool over NHWC u8: thread (batch, channel) sums its
+// h x w values minus the input zero point as an int32, then
+// y = clamp(rint((float)sum * M) + y_zp, 0, 255) with M = (x_scale / y_scale)
+// / (h * w) in f32 (rint: round half to even).
+__global__ __launch_bounds__(256) void qlinear_gap_kernel(const uint8_t* X, uint8_t* Y, int n, int hw, int c,
+                                                          int x_zp, float m, int y_zp) {
+  const int ch = blockIdx.x * 256 + threadIdx.x;
+  const int b = blockIdx.y;
+  if (ch >= c || b >= n) return;
+  const uint8_t* x = X + (size_t)b * hw * c + ch;
+  int acc = 0;
+  for (int s = 0; s < hw; ++s) acc += (int)x[(size_t)s * c] - x_zp;
+  float q = rintf((float)acc * m) + (float)y_zp;
+  q = fminf(fmaxf(q, 0.0f), 255.0f);
+  Y[(size_t)b * c + ch] = (uint8_t)q;
+}
+
+// dst[c][r] = src[r][c] for a rows x cols byte matrix (32 x 32 tiles through LDS).
+__global__ __launch_bounds__(256) void transpose_u8_kernel(const uint8_t* src, uint8_t* dst, int rows, int cols) {
+  __shared__ uint8_t t[32][33];
+  const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  for (int k = ty; k < 32; k += 8) {
+    const int r = r0 + k, c = c0 + tx;
+    if (r < rows && c < cols) t[k][tx] = src[(size_t)r * cols + c];
+  }
+  __syncthreads();
+  for (int k = ty; k < 32; k += 8) {
+    const int c = c0 + k, r = r0 + tx;
+    if (r < rows && c < cols) dst[(size_t)c * rows + r] = t[tx][k];
+  }
+}
+
 }  // namespace
 
 void launch_gemm_ex(hipStream_t st, int dtype, const void* a, const void* b, void* c, int m, int n, int k,
@@ -178,6 +211,23 @@ void launch_softmax_rows_t(hipStream_t st, int dtype, const void* x, void* y, in
     hipLaunchKernelGGL(softmax_rows_kernel<true>, g, dim3(256), 0, st, x, y, rows, n);
   else
     fail(-2, "softmax: dtype");
+  DW_HIP(hipGetLastError());
+}
+
+}  // namespace dw
+
+namespace dw {
+
+void launch_qlinear_gap(hipStream_t st, const uint8_t* x, uint8_t* y, int n, int hw, int c, int x_zp, float m,
+                        int y_zp) {
+  const dim3 g((unsigned)((c + 255) / 256), (unsigned)n);
+  hipLaunchKernelGGL(qlinear_gap_kernel, g, dim3(256), 0, st, x, y, n, hw, c, x_zp, m, y_zp);
+  DW_HIP(hipGetLastError());
+}
+
+void launch_transpose_u8(hipStream_t st, const void* src, void* dst, int rows, int cols) {
+  const dim3 g((unsigned)((cols + 31) / 32), (unsigned)((rows + 31) / 32));
+  hipLaunchKernelGGL(transpose_u8_kernel, g, dim3(256), 0, st, (const uint8_t*)src, (uint8_t*)dst, rows, cols);
   DW_HIP(hipGetLastError());
 }
 

@@ -714,7 +714,9 @@ void Runtime::lower(std::vector<Group>& groups) {
       groups.push_back(gr);
       continue;
     }
-    if (op.type == "QLinearConv") {
+    if (op.type == "QLinearConv" || op.type == "QGemm") {
+      // QGemm is the QLinearConv definition on a 1x1 kernel over the rows
+      // of A (its weights are stored as [1][1][k][n])
       gr.kind = "qconv";
       gr.conv = i;
       gr.in = op.in[0];
@@ -773,7 +775,7 @@ void Runtime::lower(std::vector<Group>& groups) {
       groups.push_back(gr);
       continue;
     }
-    if (op.type == "GlobalAveragePool") {
+    if (op.type == "GlobalAveragePool" || op.type == "QLinearGlobalAveragePool") {
       gr.kind = "gap";
     } else if (op.type == "Gemm" || op.type == "MatMul") {
       gr.kind = "gemm";
@@ -1051,7 +1053,7 @@ void Runtime::emit(const Group& gr) {
     L.op = op.name;
     L.bytes = (double)x.bytes() + y.bytes();
     const int dt = x.dtype;
-    if (dt != F32 && dt != F16 && gr.kind != "flatten")
+    if (dt != F32 && dt != F16 && gr.kind != "flatten" && !(gr.kind == "gap" && dt == U8))
       fail(DW_ERR_UNSUPPORTED, "runtime: " + op.type + " needs f32 or f16");
     const void* xb = x.base;
     void* yb = y.base;
@@ -1066,7 +1068,17 @@ void Runtime::emit(const Group& gr) {
       if (y.pixels() != x.n || y.c != x.c) fail(DW_ERR_RUNTIME, "GlobalAveragePool: output shape");
       const int n = (int)x.n, hw = (int)(x.h * x.w), c = (int)x.c;
       L.kernel = "global_avg_pool";
-      L.fn = [=](hipStream_t st) { launch_global_avg_pool(st, dt, xb, yb, n, hw, c); };
+      if (dt == U8) {
+        // QLinearGlobalAveragePool
+        if (y.dtype != U8) fail(DW_ERR_RUNTIME, "QLinearGlobalAveragePool: u8 output");
+        const float m = (x.scale / y.scale) / (float)hw;
+        const int xz = x.zp, yz = y.zp;
+        L.fn = [=](hipStream_t st) {
+          launch_qlinear_gap(st, (const uint8_t*)xb, (uint8_t*)yb, n, hw, c, xz, m, yz);
+        };
+      } else {
+        L.fn = [=](hipStream_t st) { launch_global_avg_pool(st, dt, xb, yb, n, hw, c); };
+      }
     } else if (gr.kind == "flatten") {
       if (x.bytes() != y.bytes()) fail(DW_ERR_RUNTIME, "Flatten: element count");
       const size_t nb = x.bytes();

@@ -231,3 +231,17 @@ def yolo_postprocess(be, raw, n, nc, num_det, img_w=640, img_h=640, conf=0.25, i
     check(load().dw_hip_yolo_postprocess(be.handle, raw.handle, n, nc, num_det, img_w, img_h, conf, iou,
                                          int(agnostic), out.ctypes.data, cap, counts.ctypes.data))
     return [out[b, :int(counts[b])].copy() for b in range(n)]
+
+
+# --- quantized classifier head ------------------------------------------------
+
+def qgemm_u8s8(be, a, b, bias, y, m, n, k, a_scale, a_zp, b_scales, y_scale, y_zp, trans_b=False):
+    """QGemm u8 x s8 -> u8 (per-column weight scales, int32 bias, RNE)."""
+    sc = np.ascontiguousarray(b_scales, np.float32)
+    check(load().dw_hip_qgemm_u8s8(be.handle, a.handle, b.handle, _h(bias), y.handle, m, n, k, int(trans_b),
+                                   float(a_scale), int(a_zp), sc.ctypes.data, float(y_scale), int(y_zp)))
+
+
+def qlinear_global_avg_pool_u8(be, x, y, n, h, w, c, x_scale, x_zp, y_scale, y_zp):
+    check(load().dw_hip_qlinear_global_avg_pool_u8(be.handle, x.handle, y.handle, n, h, w, c, float(x_scale),
+                                                   int(x_zp), float(y_scale), int(y_zp)))

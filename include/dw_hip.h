@@ -291,6 +291,28 @@ int dw_hip_global_avg_pool_nhwc(dw_hip_backend* be, int dtype, const dw_hip_buff
  * agree with the CPU to a few ulps. */
 int dw_hip_softmax_f32(dw_hip_backend* be, const dw_hip_buffer* x, dw_hip_buffer* y, size_t rows, size_t n);
 
+/* QGemm u8 x s8 -> u8 (the quantized classifier head; no counterpart in the
+ * reference, whose INT8 Gemm is symmetric s8 with a Requantize after it,
+ * quantize.rs:225-260): A [m][k] u8 (zero point a_zp, scale a_scale), B s8
+ * [k][n] or, with trans_b, [n][k] (per-column scales b_scales[n], zero
+ * point 0), optional int32 bias [n] (scale a_scale * b_scales[j]);
+ * acc = sum_p (A[i][p] - a_zp) * B[p][j] + bias[j],
+ * Y[i][j] = clamp(rint((float)acc * M[j]) + y_zp, 0, 255),
+ * M[j] = a_scale * b_scales[j] / y_scale in f32, rint half to even: the
+ * QLinearConv definition on a 1x1 kernel (same MFMA kernels).  Needs
+ * k % 16 == 0 and n % 4 == 0. */
+int dw_hip_qgemm_u8s8(dw_hip_backend* be, const dw_hip_buffer* a, const dw_hip_buffer* b, const dw_hip_buffer* bias,
+                      dw_hip_buffer* y, size_t m, size_t n, size_t k, int trans_b, float a_scale, int a_zp,
+                      const float* b_scales, float y_scale, int y_zp);
+
+/* QLinearGlobalAveragePool over NHWC u8 (the quantized form of
+ * dispatch_global_avg_pool, onnx runtime.rs:1109-1175): per image and
+ * channel, acc = sum (x - x_zp) in int32, y = clamp(rint((float)acc * M) +
+ * y_zp, 0, 255) with M = (x_scale / y_scale) / (h * w) in f32. */
+int dw_hip_qlinear_global_avg_pool_u8(dw_hip_backend* be, const dw_hip_buffer* x, dw_hip_buffer* y, size_t n,
+                                      size_t h, size_t w, size_t c, float x_scale, int x_zp, float y_scale,
+                                      int y_zp);
+
 /* YOLOv8 detect tail: the exported graph's ops after the head convs
  * (ultralytics Detect: DFL softmax over each side's reg_max bins and the 1x1
  * expectation, dist2bbox, times the level stride, sigmoid of the classes),

@@ -101,6 +101,7 @@ def _declare(L: C.CDLL) -> None:
         "dwo_softmax_f32": (None, [_P, _P, _Z, _Z]),
         "dwo_yolo_detect_tail_f16": (None, [_P, _P, _P, _P, _P, _I, _I, _I, _I]),
         "dwo_iou": (_F, [_P, _P]),
+        "dwo_qlinear_gap_u8": (None, [_P, _P, _Z, _Z, _Z, _Z, _F, _I, _F, _I]),
         "dwo_yolo_postprocess": (None, [_P, _P, _P, _Z, _Z, _Z, C.c_uint32, C.c_uint32, _F, _F, _I, _Z]),
     }
     for name, (res, args) in sig.items():
@@ -581,3 +582,28 @@ def yolo_postprocess(raw, img_w=640, img_h=640, conf=0.25, iou_thr=0.45, agnosti
     lib().dwo_yolo_postprocess(out.ctypes.data, counts.ctypes.data, _p(raw), n, ch - 4, A, img_w, img_h, conf,
                                iou_thr, int(agnostic), cap)
     return [out[b, :int(counts[b])].copy() for b in range(n)]
+
+
+# --- quantized classifier head ----------------------------------------------
+
+def qgemm_u8s8(a, b, bias, a_scale, a_zp, b_scales, y_scale, y_zp, trans_b=False):
+    """QGemm u8 x s8 -> u8: the QLinearConv restatement on a 1x1 kernel over
+    the rows of A ([m][k]); B [k][n] (or [n][k] with trans_b)."""
+    a = np.ascontiguousarray(a, np.uint8)
+    b = np.ascontiguousarray(b, np.int8)
+    if trans_b:
+        b = np.ascontiguousarray(b.T)
+    m, k = a.shape
+    n = b.shape[1]
+    y = qlinearconv_u8s8(a.reshape(m, 1, 1, k), b.reshape(1, 1, k, n), bias, (1, 1), (0, 0), a_scale, a_zp,
+                         b_scales, y_scale, y_zp)
+    return y.reshape(m, n)
+
+
+def qlinear_gap_u8(x, x_scale, x_zp, y_scale, y_zp):
+    """QLinearGlobalAveragePool over NHWC u8 [n, h, w, c] -> [n, c]."""
+    x = np.ascontiguousarray(x, np.uint8)
+    n, h, w, c = x.shape
+    y = np.empty((n, c), np.uint8)
+    lib().dwo_qlinear_gap_u8(_p(y), _p(x), n, h, w, c, x_scale, x_zp, y_scale, y_zp)
+    return y

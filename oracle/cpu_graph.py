@@ -156,6 +156,19 @@ class CpuGraph:
             self.vals[out[0]] = oracle.qlinearconv_u8s8(
                 x, w, b, s, (p[0], p[1]), tx["scale"], tx["zp"], np.array(tw["ch_scales"], np.float32),
                 ty_["scale"], ty_["zp"], self.threads)
+        elif ty == "QGemm":
+            # QLinearConv on a 1x1 kernel over the rows of A; B stored [1][1][k][n]
+            a, w = ins[0], ins[1]
+            b = ins[2] if len(ins) > 2 else None
+            ta, tw, ty_ = t[op["inputs"][0]], t[op["inputs"][1]], t[out[0]]
+            k, n = w.shape[2], w.shape[3]
+            y = oracle.qgemm_u8s8(a.reshape(-1, k), w.reshape(k, n), b, ta["scale"], ta["zp"],
+                                  np.array(tw["ch_scales"], np.float32), ty_["scale"], ty_["zp"])
+            self.vals[out[0]] = y.reshape(ty_["dims"])
+        elif ty == "QLinearGlobalAveragePool":
+            tx, ty_ = t[op["inputs"][0]], t[out[0]]
+            y = oracle.qlinear_gap_u8(ins[0], tx["scale"], tx["zp"], ty_["scale"], ty_["zp"])
+            self.vals[out[0]] = y.reshape(ty_["dims"])
         elif ty == "QLinearLUT":
             tx, ty_ = t[op["inputs"][0]], t[out[0]]
             if op["act"] != 2:
@@ -207,7 +220,7 @@ class CpuGraph:
             y = oracle.global_avg_pool_f32(x) if x.dtype == np.float32 else oracle.global_avg_pool_fp16(x)
             self.vals[out[0]] = y.reshape(t[out[0]]["dims"])
         elif ty == "Flatten":
-            self.vals[out[0]] = ins[0].reshape(t[out[0]]["dims"])
+            self.vals[out[0]] = np.ascontiguousarray(ins[0]).reshape(t[out[0]]["dims"])
         elif ty in ("Gemm", "MatMul"):
             # dispatch_gemm (onnx runtime.rs:1178-1275): the fma path without
             # transposes, the unfused one with; then the bias pass

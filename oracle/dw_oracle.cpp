@@ -743,6 +743,21 @@ void dwo_silu_lut_u8(uint8_t* lut, float sx, int zx, float sy, int zy) {
 void dwo_lut_u8(uint8_t* y, const uint8_t* x, size_t n, const uint8_t* lut) {
   for (size_t i = 0; i < n; ++i) y[i] = lut[x[i]];
 }
+// QLinearGlobalAveragePool (the quantized dispatch_global_avg_pool, onnx
+// runtime.rs:1109-1175): acc = sum over h*w of (x - x_zp) in int32,
+// y = clamp(rint((float)acc * ((x_scale / y_scale) / (h*w))) + y_zp, 0, 255).
+void dwo_qlinear_gap_u8(uint8_t* y, const uint8_t* x, size_t n, size_t h, size_t w, size_t c, float x_scale,
+                        int x_zp, float y_scale, int y_zp) {
+  const float m = (x_scale / y_scale) / (float)(h * w);
+  for (size_t b = 0; b < n; ++b)
+    for (size_t ch = 0; ch < c; ++ch) {
+      int32_t acc = 0;
+      for (size_t p = 0; p < h * w; ++p) acc += (int32_t)x[(b * h * w + p) * c + ch] - x_zp;
+      float q = nearbyintf((float)acc * m) + (float)y_zp;
+      q = q < 0.0f ? 0.0f : (q > 255.0f ? 255.0f : q);
+      y[b * c + ch] = (uint8_t)q;
+    }
+}
 // MaxPool with padding (ONNX): padded taps never win.  Element type by
 // esize: 4 = f32, 2 = f16 (compared as f32), 1 = u8.
 void dwo_maxpool2d_padded_nhwc(void* out, const void* in, size_t n, size_t h_in, size_t w_in, size_t c,
