@@ -109,6 +109,11 @@ SIGNATURES = {
     "dw_hip_global_avg_pool_nhwc": (I, [P, I, P, P, Z, Z, Z, Z]),
     "dw_hip_softmax_f32": (I, [P, P, P, Z, Z]),
     "dw_hip_yolo_detect_tail": (I, [P, I, P, P, P, P, I, Z, I, I, P]),
+    "dw_hip_graph_set_input_nchw_f32": (I, [P, C.c_char_p, P, Z]),
+    "dw_hip_graph_bind_input_nchw_f32": (I, [P, C.c_char_p, P]),
+    "dw_hip_transpose_nchw_to_nhwc": (I, [P, P, P, Z, Z, Z, Z, I]),
+    "dw_hip_transpose_nhwc_to_nchw": (I, [P, P, P, Z, Z, Z, Z, I]),
+    "dw_hip_fold_batchnorm": (I, [P, P, P, P, P, P, P, C.c_float, Z, Z, P, P]),
     "dw_hip_qgemm_u8s8": (I, [P, P, P, P, P, Z, Z, Z, I, C.c_float, I, P, C.c_float, I]),
     "dw_hip_qlinear_global_avg_pool_u8": (I, [P, P, P, Z, Z, Z, Z, C.c_float, I, C.c_float, I]),
     "dw_hip_yolo_postprocess": (I, [P, P, Z, I, Z, C.c_uint32, C.c_uint32, C.c_float, C.c_float, I, P, Z, P]),

@@ -878,6 +878,68 @@ int dw_hip_softmax_f32(dw_hip_backend* be, const dw_hip_buffer* x, dw_hip_buffer
   API_END
 }
 
+static size_t dtype_bytes(int dtype) {
+  if (dtype == DW_DTYPE_F32 || dtype == DW_DTYPE_I32) return 4;
+  if (dtype == DW_DTYPE_F16) return 2;
+  if (dtype == DW_DTYPE_I8 || dtype == DW_DTYPE_U8) return 1;
+  dw::fail(DW_ERR_INVALID, "unknown dtype");
+}
+
+int dw_hip_transpose_nchw_to_nhwc(dw_hip_backend* be, const dw_hip_buffer* x, dw_hip_buffer* y, size_t n, size_t c,
+                                  size_t h, size_t w, int dtype) {
+  API_BEGIN
+  Backend* bk = B(be);
+  std::lock_guard<std::mutex> lock(bk->mu);
+  const size_t es = dtype_bytes(dtype);
+  if (!n || !c || !h || !w) dw::fail(DW_ERR_INVALID, "transpose: zero size");
+  check_i32(c * h * w, "transpose: image");
+  if (n > 65535) dw::fail(DW_ERR_UNSUPPORTED, "transpose: batch above 65535");
+  need(x, n * c * h * w * es, "transpose: input");
+  need(y, n * c * h * w * es, "transpose: output");
+  dw::launch_transpose(bk->stream, x->ptr, y->ptr, (int)n, (int)c, (int)(h * w), (int)es);
+  API_END
+}
+
+int dw_hip_transpose_nhwc_to_nchw(dw_hip_backend* be, const dw_hip_buffer* x, dw_hip_buffer* y, size_t n, size_t h,
+                                  size_t w, size_t c, int dtype) {
+  API_BEGIN
+  Backend* bk = B(be);
+  std::lock_guard<std::mutex> lock(bk->mu);
+  const size_t es = dtype_bytes(dtype);
+  if (!n || !c || !h || !w) dw::fail(DW_ERR_INVALID, "transpose: zero size");
+  check_i32(c * h * w, "transpose: image");
+  if (n > 65535) dw::fail(DW_ERR_UNSUPPORTED, "transpose: batch above 65535");
+  need(x, n * c * h * w * es, "transpose: input");
+  need(y, n * c * h * w * es, "transpose: output");
+  dw::launch_transpose(bk->stream, x->ptr, y->ptr, (int)n, (int)(h * w), (int)c, (int)es);
+  API_END
+}
+
+int dw_hip_fold_batchnorm(dw_hip_backend* be, const dw_hip_buffer* w, const dw_hip_buffer* bias_in,
+                          const dw_hip_buffer* gamma, const dw_hip_buffer* beta, const dw_hip_buffer* mean,
+                          const dw_hip_buffer* var, float epsilon, size_t c_out, size_t per_channel,
+                          dw_hip_buffer* w_out, dw_hip_buffer* bias_out) {
+  API_BEGIN
+  Backend* bk = B(be);
+  std::lock_guard<std::mutex> lock(bk->mu);
+  if (!c_out || !per_channel) dw::fail(DW_ERR_INVALID, "fold_batchnorm: zero size");
+  if (c_out > 65535) dw::fail(DW_ERR_UNSUPPORTED, "fold_batchnorm: more than 65535 channels");
+  check_i32(c_out * per_channel, "fold_batchnorm: weights");
+  need(w, c_out * per_channel * 4, "fold_batchnorm: weights");
+  need(w_out, c_out * per_channel * 4, "fold_batchnorm: output weights");
+  if (bias_in) need(bias_in, c_out * 4, "fold_batchnorm: bias");
+  need(gamma, c_out * 4, "fold_batchnorm: gamma");
+  need(beta, c_out * 4, "fold_batchnorm: beta");
+  need(mean, c_out * 4, "fold_batchnorm: mean");
+  need(var, c_out * 4, "fold_batchnorm: var");
+  need(bias_out, c_out * 4, "fold_batchnorm: output bias");
+  dw::launch_fold_batchnorm(bk->stream, (const float*)w->ptr, bias_in ? (const float*)bias_in->ptr : nullptr,
+                            (const float*)gamma->ptr, (const float*)beta->ptr, (const float*)mean->ptr,
+                            (const float*)var->ptr, epsilon, (int)c_out, (int)per_channel, (float*)w_out->ptr,
+                            (float*)bias_out->ptr);
+  API_END
+}
+
 int dw_hip_yolo_detect_tail(dw_hip_backend* be, int dtype, const dw_hip_buffer* const* levels, const int* h,
                             const int* w, const float* strides, int num_levels, size_t n, int nc, int reg_max,
                             dw_hip_buffer* out) {

@@ -94,7 +94,8 @@ struct DirectArgs {
   int n, h, w, cin, cout, kh, kw, sh, sw, pt, pl, ho, wo;
   int m;
   int x_pix_stride, x_c_off, y_pix_stride, y_c_off;
-  int in_kind;   // 0 f32, 1 f16, 2 u8 dequantized to f16 ((q-zp)*scale)
+  int in_kind;   // 0 f32, 1 f16, 2 u8 dequantized to f16 ((q-zp)*scale),
+                 // 3 NCHW f32 planes rounded to f16 (3x3 three-channel stem only)
   int out_kind;  // 0 f32, 1 f16, 2 u8 (QuantizeLinear of the f16 result)
   int act;
   const float* bias_f;     // f32 bias (out f32)
@@ -174,6 +175,16 @@ void launch_softmax_rows_t(hipStream_t st, int dtype, const void* x, void* y, in
 void launch_qlinear_gap(hipStream_t st, const uint8_t* x, uint8_t* y, int n, int hw, int c, int x_zp, float m,
                         int y_zp);
 void launch_transpose_u8(hipStream_t st, const void* src, void* dst, int rows, int cols);
+
+// Layout kernels (k_layout.hip): per batch entry dst[col][row] = src[row][col]
+// (esize 1, 2 or 4); NCHW f32 -> NHWC f32 or f16 (rounded as F16::from_f32)
+// into a view with pix_stride / c_off; fold_batchnorm on device weights.
+void launch_transpose(hipStream_t st, const void* src, void* dst, int batch, int rows, int cols, int esize);
+void launch_nchw_f32_to_nhwc(hipStream_t st, const float* src, void* dst, int n, int c, int hw, int out_dtype,
+                             int pix_stride, int c_off);
+void launch_fold_batchnorm(hipStream_t st, const float* w, const float* bias_in, const float* gamma,
+                           const float* beta, const float* mean, const float* var, float eps, int c_out, int per,
+                           float* w_out, float* b_out);
 
 // YOLOv8 detect tail and post-processing (k_detect.hip).
 // Detection as postprocess.rs:11-19 lays it out (24 bytes).

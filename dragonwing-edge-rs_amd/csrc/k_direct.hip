@@ -108,7 +108,7 @@ __global__ __launch_bounds__(256) void direct_conv_kernel(const DirectArgs a) {
 template <int IN_KIND, int OC, int KH, int KW, int CIN, bool FE, int PAR>
 __global__ __launch_bounds__(256) void conv_small_kernel(const DirectArgs a) {
   static_assert(PAR < 0 || (IN_KIND == 1 && KW == 3 && CIN == 3), "row loads: f16, 3x3 taps of 3 channels");
-  constexpr int ES = IN_KIND == 0 ? 4 : (IN_KIND == 1 ? 2 : 1);
+  constexpr int ES = IN_KIND == 0 || IN_KIND == 3 ? 4 : (IN_KIND == 1 ? 2 : 1);
   constexpr int KT = KH * KW;
   // the activation table in LDS (one byte per thread)
   __shared__ uint8_t s_lut[256];
@@ -154,6 +154,25 @@ __global__ __launch_bounds__(256) void conv_small_kernel(const DirectArgs a) {
         }
       }
     }
+  } else if constexpr (IN_KIND == 3) {
+    // NCHW f32 planes (the graph's input before the layout pass): each value
+    // is rounded to f16 as F16::from_f32 stores it and widened with the
+    // reference decode, i.e. exactly the f16 NHWC input the host conversion
+    // would have produced.
+    const float* Xf = (const float*)a.x;
+    const size_t plane = (size_t)a.h * a.w;
+#pragma unroll
+    for (int kh = 0; kh < KH; ++kh)
+#pragma unroll
+      for (int kw = 0; kw < KW; ++kw) {
+        const int ih = ih0 + kh, iw = iw0 + kw;
+        const bool v = (unsigned)ih < (unsigned)a.h && (unsigned)iw < (unsigned)a.w;
+        ok[kh * KW + kw] = v;
+        const int ihc = min(max(ih, 0), a.h - 1), iwc = min(max(iw, 0), a.w - 1);
+        const float* xp = Xf + (size_t)nn * CIN * plane + (size_t)ihc * a.w + iwc;
+#pragma unroll
+        for (int ic = 0; ic < CIN; ++ic) xv[kh * KW + kw][ic] = h2f(f2h(xp[(size_t)ic * plane]));
+      }
   } else {
 #pragma unroll
     for (int kh = 0; kh < KH; ++kh)
@@ -484,7 +503,9 @@ void launch_direct_conv(hipStream_t st, const DirectArgs& a_in) {
   if (launch_conv1x1_exact(st, a_in)) return;
   DirectArgs a = a_in;
   // the 3x3, 3-channel stem
-  if (a.kh == 3 && a.kw == 3 && a.cin == 3 && a.cout % 16 == 0 && a.in_kind <= 1) {
+  if (a.in_kind == 3 && !(a.kh == 3 && a.kw == 3 && a.cin == 3 && a.cout % 16 == 0))
+    fail(-2, "direct conv: NCHW f32 input only for the 3x3 three-channel stem");
+  if (a.kh == 3 && a.kw == 3 && a.cin == 3 && a.cout % 16 == 0 && (a.in_kind <= 1 || a.in_kind == 3)) {
     const int oes = a.out_kind == 0 ? 4 : (a.out_kind == 1 ? 2 : 1);
     auto aligned = [&](int v) {
       return (16 * oes) % v == 0 && (a.y_pix_stride * oes) % v == 0 && (a.y_c_off * oes) % v == 0 &&
@@ -504,6 +525,10 @@ void launch_direct_conv(hipStream_t st, const DirectArgs& a_in) {
   hipLaunchKernelGGL((conv_small_kernel<1, 16, 3, 3, 3, FE_, PAR_>), grid, dim3(256), 0, st, a)
     if (a.in_kind == 0)
       hipLaunchKernelGGL((conv_small_kernel<0, 16, 3, 3, 3, false, -1>), grid, dim3(256), 0, st, a);
+    else if (a.in_kind == 3 && a.fast_epi)
+      hipLaunchKernelGGL((conv_small_kernel<3, 16, 3, 3, 3, true, -1>), grid, dim3(256), 0, st, a);
+    else if (a.in_kind == 3)
+      hipLaunchKernelGGL((conv_small_kernel<3, 16, 3, 3, 3, false, -1>), grid, dim3(256), 0, st, a);
     else if (rows && par == 1 && a.fast_epi)
       DW_SMALL(true, 1);
     else if (rows && par == 1)

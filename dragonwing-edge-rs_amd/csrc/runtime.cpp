@@ -70,6 +70,9 @@ struct Launch {
   // implicit-GEMM launches: their arguments, shared with `fn`, so the tuner
   // can change the tile shape after the launch list is built
   std::shared_ptr<IgemmArgs> ig;
+  // direct-conv launches: their arguments, shared with `fn`, so an input
+  // can be switched to the NCHW f32 loader after the list is built
+  std::shared_ptr<DirectArgs> da;
   int esize = 0;
   // schedule over several streams: the storage this launch touches, its
   // stream, the launches on other streams it waits for, and whether a
@@ -117,6 +120,22 @@ struct Runtime {
   std::vector<hipStream_t> side;  // streams 1 .. nstreams - 1
   std::vector<hipEvent_t> evs;    // per launch (recorded ones only), then fork
   bool stats = false;
+  // graph inputs given in NCHW f32 (the layout before convert_nchw_to_nhwc):
+  // the one stem conv that reads such an input loads the NCHW planes itself
+  // (rounding to f16 in its loader); any other input is converted by a
+  // transpose launch at the head of every run
+  struct NchwIn {
+    int launch = -2;        // the stem launch reading the input, -1 none, -2 not looked up
+    DirectArgs orig{};      // its arguments for the NHWC input
+    void* stage = nullptr;  // owned device copy of host NCHW data
+    size_t stage_bytes = 0;
+    const void* src = nullptr;  // NCHW data the runs read (stage or a bound buffer)
+    bool active = false;
+  };
+  std::map<std::string, NchwIn> nchw;
+  void set_input_nchw(const std::string& name, const void* src);
+  void reset_input_layout(const std::string& name);
+  void drop_capture();
   float* stats_dev = nullptr;
   std::vector<std::string> stats_names;
 
@@ -132,6 +151,8 @@ struct Runtime {
     for (hipEvent_t e : evs)
       if (e) (void)hipEventDestroy(e);
     for (void* p : allocs) (void)hipFree(p);
+    for (auto& kv : nchw)
+      if (kv.second.stage) (void)hipFree(kv.second.stage);
   }
 
   void* dalloc(size_t bytes) {
@@ -486,6 +507,13 @@ void Runtime::plan_streams(int n) {
 }
 
 void Runtime::enqueue(hipStream_t st) {
+  for (auto& kv : nchw) {
+    const NchwIn& e = kv.second;
+    if (!e.active || e.launch >= 0) continue;
+    const RtTensor& t = T(kv.first);
+    launch_nchw_f32_to_nhwc(st, (const float*)e.src, t.base, (int)t.n, (int)t.c, (int)(t.h * t.w), t.dtype,
+                            t.pix_stride, t.abs_off);
+  }
   if (nstreams <= 1 || stats) {
     for (auto& L : launches) L.fn(st);
     return;
@@ -1365,7 +1393,8 @@ void Runtime::emit_conv(const Group& gr) {
   }
   L.kernel = "direct_conv";
   L.bytes += (double)x.bytes() + W.numel() * 4.0 + (double)y.bytes();
-  L.fn = [=](hipStream_t st) { launch_direct_conv(st, a); };
+  L.da = std::make_shared<DirectArgs>(a);
+  L.fn = [da = L.da](hipStream_t st) { launch_direct_conv(st, *da); };
   launches.push_back(L);
 }
 
@@ -1573,6 +1602,64 @@ void Runtime::autotune() {
   info.clear();
 }
 
+void Runtime::drop_capture() {
+  if (hexec) {
+    DW_HIP(hipStreamSynchronize(be->stream));
+    (void)hipGraphExecDestroy(hexec);
+    hexec = nullptr;
+  }
+  if (hgraph) {
+    (void)hipGraphDestroy(hgraph);
+    hgraph = nullptr;
+  }
+}
+
+void Runtime::set_input_nchw(const std::string& name, const void* src) {
+  RtTensor& t = T(name);
+  if (t.dtype != F32 && t.dtype != F16) fail(DW_ERR_UNSUPPORTED, "NCHW input: the input must be f32 or f16");
+  NchwIn& e = nchw[name];
+  if (e.launch == -2) {
+    // the stem that can read NCHW itself: the only launch reading the
+    // input, a 3x3 three-channel direct conv on the dense f16 tensor
+    int found = -1, count = 0;
+    for (size_t k = 0; k < launches.size(); ++k)
+      for (const Region& r : launches[k].reads)
+        if (r.base == t.base) {
+          ++count;
+          found = (int)k;
+          break;
+        }
+    e.launch = -1;
+    if (count == 1 && launches[found].da) {
+      const DirectArgs& a = *launches[found].da;
+      if (a.in_kind == 1 && a.x == t.base && a.kh == 3 && a.kw == 3 && a.cin == 3 && a.cout % 16 == 0 &&
+          a.x_pix_stride == 3 && a.x_c_off == 0 && t.pix_stride == 3 && t.abs_off == 0) {
+        e.launch = found;
+        e.orig = a;
+      }
+    }
+  }
+  e.src = src;
+  e.active = true;
+  if (e.launch >= 0) {
+    DirectArgs& a = *launches[e.launch].da;
+    a = e.orig;
+    a.x = src;
+    a.in_kind = 3;
+  }
+  drop_capture();
+}
+
+void Runtime::reset_input_layout(const std::string& name) {
+  auto it = nchw.find(name);
+  if (it == nchw.end() || !it->second.active) return;
+  NchwIn& e = it->second;
+  if (e.launch >= 0) *launches[e.launch].da = e.orig;
+  e.active = false;
+  e.src = nullptr;
+  drop_capture();
+}
+
 void Runtime::run() {
   hipStream_t st = be->stream;
   if (stats) {
@@ -1671,6 +1758,7 @@ int dw_hip_graph_set_input_bytes(dw_hip_graph_runtime* rth, const char* name, co
   if (!name || std::find(rt.g.inputs.begin(), rt.g.inputs.end(), std::string(name)) == rt.g.inputs.end())
     dw::fail(DW_ERR_RUNTIME, std::string("input not found: ") + (name ? name : "(null)"));
   dw::RtTensor& t = rt.T(name);
+  rt.reset_input_layout(name);
   if (len != t.bytes())
     dw::fail(DW_ERR_RUNTIME, "input size mismatch: expected " + std::to_string(t.bytes()) + ", got " +
                                  std::to_string(len));
@@ -1686,6 +1774,7 @@ int dw_hip_graph_set_input_f32(dw_hip_graph_runtime* rth, const char* name, cons
   if (!name || std::find(rt.g.inputs.begin(), rt.g.inputs.end(), std::string(name)) == rt.g.inputs.end())
     dw::fail(DW_ERR_RUNTIME, std::string("input not found: ") + (name ? name : "(null)"));
   dw::RtTensor& t = rt.T(name);
+  rt.reset_input_layout(name);
   const size_t n = (size_t)(t.pixels() * t.c);
   if (count != n)
     dw::fail(DW_ERR_RUNTIME, "input size mismatch: expected " + std::to_string(n) + ", got " + std::to_string(count));
@@ -1700,6 +1789,46 @@ int dw_hip_graph_set_input_f32(dw_hip_graph_runtime* rth, const char* name, cons
     dw::fail(DW_ERR_RUNTIME, "unsupported dtype for set_input_f32");
   }
   DW_HIP(hipStreamSynchronize(rt.be->stream));
+  API_END
+}
+
+int dw_hip_graph_set_input_nchw_f32(dw_hip_graph_runtime* rth, const char* name, const float* data, size_t count) {
+  API_BEGIN
+  dw::Runtime& rt = R(rth);
+  std::lock_guard<std::mutex> lock(rt.be->mu);
+  if (!name || std::find(rt.g.inputs.begin(), rt.g.inputs.end(), std::string(name)) == rt.g.inputs.end())
+    dw::fail(DW_ERR_RUNTIME, std::string("input not found: ") + (name ? name : "(null)"));
+  if (!data) dw::fail(DW_ERR_INVALID, "null data");
+  dw::RtTensor& t = rt.T(name);
+  const size_t n = (size_t)(t.pixels() * t.c);
+  if (count != n)
+    dw::fail(DW_ERR_RUNTIME, "input size mismatch: expected " + std::to_string(n) + ", got " + std::to_string(count));
+  auto& e = rt.nchw[name];
+  if (e.stage_bytes != n * 4) {
+    if (e.stage) DW_HIP(hipFree(e.stage));
+    e.stage = nullptr;
+    e.stage_bytes = 0;
+    DW_HIP(hipMalloc(&e.stage, n * 4));
+    e.stage_bytes = n * 4;
+  }
+  DW_HIP(hipMemcpyAsync(e.stage, data, n * 4, hipMemcpyHostToDevice, rt.be->stream));
+  DW_HIP(hipStreamSynchronize(rt.be->stream));
+  rt.set_input_nchw(name, e.stage);
+  API_END
+}
+
+int dw_hip_graph_bind_input_nchw_f32(dw_hip_graph_runtime* rth, const char* name, const dw_hip_buffer* buf) {
+  API_BEGIN
+  dw::Runtime& rt = R(rth);
+  std::lock_guard<std::mutex> lock(rt.be->mu);
+  if (!name || std::find(rt.g.inputs.begin(), rt.g.inputs.end(), std::string(name)) == rt.g.inputs.end())
+    dw::fail(DW_ERR_RUNTIME, std::string("input not found: ") + (name ? name : "(null)"));
+  if (!buf) dw::fail(DW_ERR_INVALID, "null buffer");
+  dw::RtTensor& t = rt.T(name);
+  const size_t n = (size_t)(t.pixels() * t.c);
+  if (dw_hip_buffer_len_bytes(buf) != n * 4)
+    dw::fail(DW_ERR_RUNTIME, "input size mismatch: expected " + std::to_string(n * 4) + " bytes");
+  rt.set_input_nchw(name, dw_hip_buffer_device_ptr(buf));
   API_END
 }
 

@@ -205,6 +205,16 @@ class HipGraphRuntime:
         a = np.ascontiguousarray(data)
         check(load().dw_hip_graph_set_input_bytes(self._h, name.encode(), a.ctypes.data, a.nbytes))
 
+    def set_input_nchw_f32(self, name: str, data):
+        """The input as NCHW f32 (before the layout pass); the GPU transposes
+        it, or the stem conv reads it directly."""
+        a = np.ascontiguousarray(data, np.float32)
+        check(load().dw_hip_graph_set_input_nchw_f32(self._h, name.encode(), a.ctypes.data, a.size))
+
+    def bind_input_nchw_f32(self, name: str, buf):
+        """Every run reads the input from the device buffer (NCHW f32)."""
+        check(load().dw_hip_graph_bind_input_nchw_f32(self._h, name.encode(), buf.handle))
+
     def run_unbatched(self):
         """run_unbatched (vulkan_runtime.rs:423-470): launches one by one,
         errors name the failing launch; DW_TRACE=1 prints and syncs each."""

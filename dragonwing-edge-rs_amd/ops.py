@@ -245,3 +245,21 @@ def qgemm_u8s8(be, a, b, bias, y, m, n, k, a_scale, a_zp, b_scales, y_scale, y_z
 def qlinear_global_avg_pool_u8(be, x, y, n, h, w, c, x_scale, x_zp, y_scale, y_zp):
     check(load().dw_hip_qlinear_global_avg_pool_u8(be.handle, x.handle, y.handle, n, h, w, c, float(x_scale),
                                                    int(x_zp), float(y_scale), int(y_zp)))
+
+
+# --- layout and BN fold on the device -----------------------------------------
+
+def transpose_nchw_to_nhwc(be, x, y, n, c, h, w, dtype=DTYPE_F32):
+    """graph.rs:339-356 on the device."""
+    check(load().dw_hip_transpose_nchw_to_nhwc(be.handle, x.handle, y.handle, n, c, h, w, dtype))
+
+
+def transpose_nhwc_to_nchw(be, x, y, n, h, w, c, dtype=DTYPE_F32):
+    """graph.rs:358-379 on the device."""
+    check(load().dw_hip_transpose_nhwc_to_nchw(be.handle, x.handle, y.handle, n, h, w, c, dtype))
+
+
+def fold_batchnorm(be, w, bias, gamma, beta, mean, var, eps, c_out, per_channel, w_out, bias_out):
+    """fold_batchnorm (graph.rs:521-690) on device buffers (f32, f64 math)."""
+    check(load().dw_hip_fold_batchnorm(be.handle, w.handle, _h(bias), gamma.handle, beta.handle, mean.handle,
+                                       var.handle, float(eps), c_out, per_channel, w_out.handle, bias_out.handle))

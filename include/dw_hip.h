@@ -291,6 +291,23 @@ int dw_hip_global_avg_pool_nhwc(dw_hip_backend* be, int dtype, const dw_hip_buff
  * agree with the CPU to a few ulps. */
 int dw_hip_softmax_f32(dw_hip_backend* be, const dw_hip_buffer* x, dw_hip_buffer* y, size_t rows, size_t n);
 
+/* Layout transposes on the device (transpose_nchw_to_nhwc /
+ * transpose_nhwc_to_nchw, crates/dragonwing-onnx/src/graph.rs:339-379):
+ * elements of dtype (any DW_DTYPE_*) moved, never converted. */
+int dw_hip_transpose_nchw_to_nhwc(dw_hip_backend* be, const dw_hip_buffer* x, dw_hip_buffer* y, size_t n, size_t c,
+                                  size_t h, size_t w, int dtype);
+int dw_hip_transpose_nhwc_to_nchw(dw_hip_backend* be, const dw_hip_buffer* x, dw_hip_buffer* y, size_t n, size_t h,
+                                  size_t w, size_t c, int dtype);
+
+/* fold_batchnorm (graph.rs:521-690) on device-resident f32 weights: w is
+ * [c_out][per_channel] (OIHW), bias_in optional; in f64 per channel
+ * s = gamma / sqrt(var + eps), w_out = (f32)(w * s),
+ * bias_out = (f32)((bias_in - mean) * s + beta). */
+int dw_hip_fold_batchnorm(dw_hip_backend* be, const dw_hip_buffer* w, const dw_hip_buffer* bias_in,
+                          const dw_hip_buffer* gamma, const dw_hip_buffer* beta, const dw_hip_buffer* mean,
+                          const dw_hip_buffer* var, float epsilon, size_t c_out, size_t per_channel,
+                          dw_hip_buffer* w_out, dw_hip_buffer* bias_out);
+
 /* QGemm u8 x s8 -> u8 (the quantized classifier head; no counterpart in the
  * reference, whose INT8 Gemm is symmetric s8 with a Requantize after it,
  * quantize.rs:225-260): A [m][k] u8 (zero point a_zp, scale a_scale), B s8
@@ -487,6 +504,18 @@ void dw_hip_graph_runtime_destroy(dw_hip_graph_runtime* rt);
 int dw_hip_graph_set_input_f32(dw_hip_graph_runtime* rt, const char* name, const float* data, size_t count);
 /* set_input_bytes (vulkan_runtime.rs:2113): raw bytes in the tensor's dtype. */
 int dw_hip_graph_set_input_bytes(dw_hip_graph_runtime* rt, const char* name, const void* data, size_t len);
+/* An input given in NCHW f32, the layout a graph has before
+ * convert_nchw_to_nhwc (what transpose_nchw_to_nhwc, graph.rs:339-356,
+ * prepares on the host in the reference's recipe): the values are the same
+ * as set_input_f32 of the transposed data.  When the input feeds only a 3x3
+ * three-channel stem conv (f16 graphs), that conv reads the NCHW planes and
+ * rounds them to f16 in its loader; otherwise each run starts with a
+ * transpose launch into the NHWC input.  set_input_nchw_f32 copies host
+ * data (count = n*c*h*w); bind_input_nchw_f32 reads the device buffer at
+ * every run until the next set_input or bind call for that input (the
+ * buffer must outlive those runs).  No counterpart in the reference. */
+int dw_hip_graph_set_input_nchw_f32(dw_hip_graph_runtime* rt, const char* name, const float* data, size_t count);
+int dw_hip_graph_bind_input_nchw_f32(dw_hip_graph_runtime* rt, const char* name, const dw_hip_buffer* buf);
 /* run (vulkan_runtime.rs:359-419): enqueue every op; returns without waiting. */
 int dw_hip_graph_run(dw_hip_graph_runtime* rt);
 /* run_unbatched (vulkan_runtime.rs:423-470): enqueue the launches one by one
