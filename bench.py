@@ -115,6 +115,16 @@ def roofline_of(fam):
 # ---------------------------------------------------------------------------
 # CPU baselines (oracle, bounded samples)
 # ---------------------------------------------------------------------------
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline_yolo_int8(info, x_f16, seconds: float):
     from oracle.cpu_graph import CpuGraph
     from dragonwing_edge_rs_amd import yolo
@@ -122,20 +132,31 @@ def cpu_baseline_yolo_int8(info, x_f16, seconds: float):
     threads = cpu_threads()
     g1, info1 = yolo.int8_graph_from_ranges(info["ranges"], batch=1, size=info["size"])
     desc = g1.to_dict()
-    done, t0 = 0, time.perf_counter()
-    while True:
-        cg = CpuGraph(desc, g1.initializer, threads=threads)
-        cg.set_input(info1["input"], x_f16[done % x_f16.shape[0]][None])
-        cg.run()
-        done += 1
-        el = time.perf_counter() - t0
-        if el >= seconds or done >= 4 * x_f16.shape[0]:
-            break
+
+    def sample(int8_threads, secs, most):
+        done, t0 = 0, time.perf_counter()
+        while True:
+            cg = CpuGraph(desc, g1.initializer, threads=threads, int8_threads=int8_threads)
+            cg.set_input(info1["input"], x_f16[done % x_f16.shape[0]][None])
+            cg.run()
+            done += 1
+            el = time.perf_counter() - t0
+            if el >= secs or done >= most:
+                return done, el
+
+    done, el = sample(threads, seconds, 4 * x_f16.shape[0])
+    # the reference's own form: conv2d_i8_nhwc has no _mt variant
+    # (ops.rs:3086-3142), so its int8 convs run on one thread
+    d1, e1 = sample(1, min(seconds, 10.0), x_f16.shape[0])
     return {"value": round(done / el, 3), "unit": "images/s", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(),
             "sample": f"{done} images (cycling through the batch's 32, 640x640) through the oracle's CpuGraph "
                       f"on the same u8 graph "
                       f"at batch 1; int8 convs row-parallel on {threads} threads (bit-identical to the "
-                      f"single-threaded conv2d_i8_nhwc form); {el:.1f} s"}
+                      f"single-threaded conv2d_i8_nhwc form); {el:.1f} s",
+            "int8_convs_one_thread": {"value": round(d1 / e1, 3), "unit": "images/s",
+                                      "sample": f"{d1} images with the int8 convs on one thread as the "
+                                                f"reference runs them (other ops on {threads}); {e1:.1f} s"}}
 
 
 def cpu_baseline_yolo_f16(info, x_f16, seconds: float):
@@ -155,6 +176,7 @@ def cpu_baseline_yolo_f16(info, x_f16, seconds: float):
         if el >= seconds or done >= x_f16.shape[0]:
             break
     return {"value": round(done / el, 3), "unit": "images/s", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(),
             "sample": f"{done} of the 32 images through the oracle's CpuGraph (conv2d_fp16_nhwc_mt on "
                       f"{threads} threads); {el:.1f} s"}
 
@@ -173,6 +195,7 @@ def cpu_baseline_qconv(case, seconds: float):
         if el >= seconds or done >= 32:
             break
     return {"value": round(done / el, 3), "unit": "images/s", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(),
             "sample": f"{done} of the 32 images (80x80x128 -> 40x40x256) through the oracle QLinearConv on "
                       f"{threads} threads; {el:.1f} s"}
 
@@ -192,6 +215,7 @@ def cpu_baseline_dwconv(xwb, seconds: float):
         if el >= seconds or done >= 32:
             break
     return {"value": round(done / el, 3), "unit": "images/s", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(),
             "sample": f"{done} of the 32 images through depthwise_conv2d_fp16_nhwc_mt + bias + sigmoid/mul "
                       f"on {threads} threads; {el:.1f} s"}
 
@@ -209,7 +233,85 @@ def cpu_baseline_conv_f32(xwb, seconds: float):
         if el >= seconds:
             break
     return {"value": round(done / el, 3), "unit": "images/s", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(),
             "sample": f"{done} runs of conv2d_f32_nhwc_mt + bias + relu on {threads} threads; {el:.1f} s"}
+
+
+# ---------------------------------------------------------------------------
+# HBM traffic from rocprofv3 counters
+# ---------------------------------------------------------------------------
+PROBE_BYTES = 256 << 20
+
+
+def copy_probe(be):
+    """One plain copy kernel of PROBE_BYTES read + PROBE_BYTES written: the
+    known-size reference for scaling FETCH_SIZE / WRITE_SIZE readings."""
+    from dragonwing_edge_rs_amd import ops
+
+    src, dst = be.alloc(PROBE_BYTES), be.alloc(PROBE_BYTES)
+    ops.concat_channels_nhwc(be, ops.DTYPE_U8, [src], [PROBE_BYTES >> 10], dst, 1 << 10)
+    be.synchronize()
+    src.free()
+    dst.free()
+
+
+def read_counter_csv(d: Path):
+    import csv
+
+    files = sorted(d.rglob("*counter_collection.csv"))
+    if not files:
+        raise RuntimeError(f"no counter_collection.csv under {d}")
+    rows = {}
+    with open(files[0]) as f:
+        for r in csv.DictReader(f):
+            k = int(r["Dispatch_Id"])
+            name, v = r["Kernel_Name"], float(r["Counter_Value"])
+            rows[k] = (name, rows[k][1] + v if k in rows else v)
+    return [rows[k] for k in sorted(rows)]
+
+
+def measure_traffic(workload: str, launches, timeout: float = 240.0):
+    """Per-launch HBM bytes: two rocprofv3 counter passes (FETCH_SIZE, then
+    WRITE_SIZE) over a child run of this workload that brackets one graph
+    run between two copy probes; each counter is scaled by what it reads for
+    the second probe.  Returns (fetch_bytes[], write_bytes[], scales) in
+    launch order, or raises."""
+    import shutil
+    import signal
+    import subprocess
+    import tempfile
+
+    exe = shutil.which("rocprofv3")
+    if not exe:
+        raise RuntimeError("rocprofv3 not found")
+    base = Path(tempfile.mkdtemp(prefix="dw_traffic_", dir="/tmp"))
+    per, scales = {}, {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        d = base / counter
+        cmd = [exe, "--pmc", counter, "--output-format", "csv", "-d", str(d), "-o", "run", "--",
+               sys.executable, str(ROOT / "bench.py"), "--workload", workload, "--traffic-child"]
+        p = subprocess.Popen(cmd, cwd="/tmp", env=dict(os.environ, TMPDIR="/tmp"), stdout=subprocess.DEVNULL,
+                             stderr=subprocess.DEVNULL, start_new_session=True)
+        try:
+            p.wait(timeout=timeout)
+        except subprocess.TimeoutExpired:
+            os.killpg(p.pid, signal.SIGKILL)
+            p.wait()
+            raise RuntimeError(f"{counter} pass timed out")
+        rows = read_counter_csv(d)
+        copies = [i for i, (n, _) in enumerate(rows) if "copy_channels" in n]
+        if len(copies) < 2:
+            raise RuntimeError(f"{counter}: copy probes not found")
+        b = copies[-1]
+        a = b - len(launches) - 1
+        if a < 0 or "copy_channels" not in rows[a][0]:
+            raise RuntimeError(f"{counter}: {b - copies[-2] - 1} dispatches between the probes, "
+                               f"{len(launches)} launches expected")
+        scale = (PROBE_BYTES / 1024.0) / rows[b][1]
+        per[counter] = [rows[i][1] * scale * 1024.0 for i in range(a + 1, b)]
+        scales[counter] = round(scale, 4)
+    shutil.rmtree(base, ignore_errors=True)
+    return per["FETCH_SIZE"], per["WRITE_SIZE"], scales
 
 
 # ---------------------------------------------------------------------------
@@ -228,6 +330,9 @@ def main():
                     help="back-to-back repeats of each launch per timing pass")
     ap.add_argument("--capture", action="store_true", help="replay one captured HIP graph per step")
     ap.add_argument("--dump-launches", default="", help="write per-launch timings (JSON lines) to this file")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the two rocprofv3 counter passes that measure roofline.traffic")
+    ap.add_argument("--traffic-child", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--traffic-probe", action="store_true",
                     help="end with one plain 256 MiB device copy (copy_channels kernel), the known-size "
                          "reference for scaling FETCH_SIZE / WRITE_SIZE counters of the same run")
@@ -282,6 +387,15 @@ def main():
             rt.enable_capture(True)
     t_setup = time.perf_counter() - t_setup
     images = work["images"]
+    if args.traffic_child:
+        # counted run: probe, one graph run, probe (nothing else on the GPU)
+        rts[0].run()
+        be.synchronize()
+        copy_probe(be)
+        rts[0].run()
+        be.synchronize()
+        copy_probe(be)
+        return
 
     for i in range(args.warmup):
         rts[i % rotate].run()
@@ -344,14 +458,24 @@ def main():
         "gpu_ms_sum_of_launches": round(float(ms.sum()), 4),
         "setup_s": round(t_setup, 1),
     }
+    if not args.no_traffic:
+        try:
+            fetch, write, scales = measure_traffic(wl, launches)
+            idx = [i for i, L in enumerate(launches) if family(L["kernel"]) == dom["kernel"]]
+            fb = sum(fetch[i] for i in idx) / len(idx)
+            wb = sum(write[i] for i in idx) / len(idx)
+            roof["traffic"] = round(fb + wb)
+            roof["traffic_fetch"] = round(fb)
+            roof["traffic_write"] = round(wb)
+            roof["traffic_over_algorithmic"] = round((fb + wb) / roof["bytes_per_launch"], 3)
+            roof["traffic_source"] = ("rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes over one graph run, "
+                                      "per-dispatch KiB scaled by the readings of a 256 MiB copy (scales %s)"
+                                      % scales)
+        except Exception as e:  # the counters are optional: the line stands without them
+            roof["traffic_source"] = f"not measured: {e}"
     if args.traffic_probe:
-        from dragonwing_edge_rs_amd import ops
-
-        n = 256 << 20
-        src, dst = be.alloc(n), be.alloc(n)
-        ops.concat_channels_nhwc(be, ops.DTYPE_U8, [src], [n >> 10], dst, 1 << 10)
-        be.synchronize()
-        line["traffic_probe_bytes"] = {"read": n, "write": n}
+        copy_probe(be)
+        line["traffic_probe_bytes"] = {"read": PROBE_BYTES, "write": PROBE_BYTES}
     print(json.dumps(line), flush=True)
 
 

@@ -35,11 +35,15 @@ NP = {F32: np.float32, F16: np.uint16, I8: np.int8, U8: np.uint8, I32: np.int32}
 
 
 class CpuGraph:
-    def __init__(self, desc: dict, initializer, threads: int | None = None):
-        """desc: Graph.to_dict(); initializer(name, dtype, shape) -> ndarray."""
+    def __init__(self, desc: dict, initializer, threads: int | None = None, int8_threads: int | None = None):
+        """desc: Graph.to_dict(); initializer(name, dtype, shape) -> ndarray.
+        threads: the _mt ops' thread count; int8_threads: the integer convs'
+        (the reference's conv2d_i8_nhwc is single-threaded, ops.rs:3086-3142;
+        row-parallel runs give the same integers)."""
         self.d = desc
         self.t = desc["tensors"]
         self.threads = threads or oracle.default_threads()
+        self.int8_threads = int8_threads or self.threads
         self.vals: dict[str, np.ndarray] = {}
         for name, ti in self.t.items():
             if ti["init"]:
@@ -104,7 +108,7 @@ class CpuGraph:
             if x.dtype == np.int8:
                 if b is not None:
                     raise NotImplementedError("biased INT8 conv")
-                self.vals[out[0]] = oracle.conv2d_i8_nhwc(x, w, s, (p[0], p[1]), self.threads)
+                self.vals[out[0]] = oracle.conv2d_i8_nhwc(x, w, s, (p[0], p[1]), self.int8_threads)
                 return
             if x.dtype == np.float32:
                 y = oracle.conv2d_f32_nhwc(x, w, s, (p[0], p[1]), self.threads)
@@ -124,7 +128,7 @@ class CpuGraph:
             if len(ins) > 2 and ins[2] is not None:
                 raise NotImplementedError("biased INT8 conv")
             s, p = op["strides"], op["pads"]
-            y = oracle.requantize_i32_to_i8(oracle.conv2d_i8_nhwc(x, w, s, (p[0], p[1]), self.threads), op["scale"])
+            y = oracle.requantize_i32_to_i8(oracle.conv2d_i8_nhwc(x, w, s, (p[0], p[1]), self.int8_threads), op["scale"])
             self.vals[out[0]] = oracle.relu_i8(y) if op["has_relu"] else y
         elif ty == "Requantize":
             self.vals[out[0]] = oracle.requantize_i32_to_i8(ins[0], op["scale"])
@@ -155,7 +159,7 @@ class CpuGraph:
             s, p = op["strides"], op["pads"]
             self.vals[out[0]] = oracle.qlinearconv_u8s8(
                 x, w, b, s, (p[0], p[1]), tx["scale"], tx["zp"], np.array(tw["ch_scales"], np.float32),
-                ty_["scale"], ty_["zp"], self.threads)
+                ty_["scale"], ty_["zp"], self.int8_threads)
         elif ty == "QGemm":
             # QLinearConv on a 1x1 kernel over the rows of A; B stored [1][1][k][n]
             a, w = ins[0], ins[1]
