@@ -109,6 +109,8 @@ SIGNATURES = {
     "dw_hip_global_avg_pool_nhwc": (I, [P, I, P, P, Z, Z, Z, Z]),
     "dw_hip_softmax_f32": (I, [P, P, P, Z, Z]),
     "dw_hip_yolo_detect_tail": (I, [P, I, P, P, P, P, I, Z, I, I, P]),
+    "dw_graph_from_onnx": (I, [P, Z, P]),
+    "dw_onnx_inspect": (I, [P, Z, P, Z, P]),
     "dw_hip_graph_set_input_nchw_f32": (I, [P, C.c_char_p, P, Z]),
     "dw_hip_graph_bind_input_nchw_f32": (I, [P, C.c_char_p, P]),
     "dw_hip_transpose_nchw_to_nhwc": (I, [P, P, P, Z, Z, Z, Z, I]),

@@ -442,12 +442,16 @@ void quantize_qdq(GraphIR& g, const std::set<std::string>& keep_f16) {
           for (auto& o : op.out) uf.join(i, o);
     }
   }
+  bool qdq_model = false;  // quantization fixed by an imported QDQ model
+  for (auto& kv : g.t) qdq_model = qdq_model || kv.second.q_fixed || kv.second.prequant;
   // Tensors that stay f16: graph inputs, outputs of kept convs (and of f16
   // concats of those).
   std::set<std::string> f16t(g.inputs.begin(), g.inputs.end());
   for (auto& in : g.inputs) g.tensor(in).dtype = DW_DTYPE_F16;
   for (auto& op : g.ops) {
-    if (op.type == "Conv" && keep_f16.count(op.name)) f16t.insert(op.out[0]);
+    if (op.type == "Conv" && (keep_f16.count(op.name) ||
+                              (qdq_model && op.in.size() > 1 && !g.tensor(op.in[1]).prequant)))
+      f16t.insert(op.out[0]);
     if (op.type == "Concat") {
       bool all = true;
       for (auto& i : op.in) all = all && f16t.count(i);
@@ -466,17 +470,38 @@ void quantize_qdq(GraphIR& g, const std::set<std::string>& keep_f16) {
     else
       it->second = {std::min(it->second.first, ti.rmin), std::max(it->second.second, ti.rmax)};
   }
+  // quantization fixed by the model (QDQ import), per shared-scale group
+  std::map<std::string, std::pair<float, int>> gfixed;
+  for (auto& kv : g.t) {
+    const TensorInfo& ti = kv.second;
+    if (ti.is_init || !ti.q_fixed) continue;
+    const std::string r = uf.find(kv.first);
+    auto it = gfixed.find(r);
+    if (it == gfixed.end())
+      gfixed[r] = {ti.scale, ti.zp};
+    else if (it->second.first != ti.scale || it->second.second != ti.zp)
+      fail(DW_ERR_UNSUPPORTED, "quantize_qdq: '" + kv.first + "' must share its quantization with the tensors "
+                               "it is concatenated, split, pooled or resized with");
+  }
   auto qscale = [&](const std::string& name) -> float {
+    auto f = gfixed.find(uf.find(name));
+    if (f != gfixed.end()) return f->second.first;
     auto it = grange.find(uf.find(name));
     if (it == grange.end()) fail(DW_ERR_RUNTIME, "no calibration range for '" + name + "'");
     return sym_scale(it->second.first, it->second.second);
   };
+  auto qzp = [&](const std::string& name) -> int {
+    auto f = gfixed.find(uf.find(name));
+    return f != gfixed.end() ? f->second.second : 128;
+  };
   auto make_u8 = [&](const std::string& name) {
     TensorInfo& ti = g.tensor(name);
+    const float sc = qscale(name);
+    const int zp = qzp(name);
     ti.dtype = DW_DTYPE_U8;
     ti.has_q = true;
-    ti.scale = qscale(name);
-    ti.zp = 128;
+    ti.scale = sc;
+    ti.zp = zp;
   };
 
   std::vector<OpNode> out;
@@ -497,7 +522,7 @@ void quantize_qdq(GraphIR& g, const std::set<std::string>& keep_f16) {
     TensorInfo& tq = g.tensor(q);
     tq.has_q = true;
     tq.scale = qscale(x);
-    tq.zp = 128;
+    tq.zp = qzp(x);
     OpNode op;
     op.name = x + "_quantize";
     op.type = "QuantizeLinear";
@@ -530,7 +555,8 @@ void quantize_qdq(GraphIR& g, const std::set<std::string>& keep_f16) {
     if (op.type == "Conv") {
       TensorInfo& W = g.tensor(op.in[1]);
       if (W.dims.size() != 4) fail(DW_ERR_UNSUPPORTED, "quantize: conv weight must be 4-D (HWIO)");
-      const bool keep = keep_f16.count(op.name) != 0;
+      // a QDQ model leaves the convs it keeps in float with float weights
+      const bool keep = keep_f16.count(op.name) != 0 || (qdq_model && !W.prequant);
       if (keep) {
         op.in[0] = need_f16(op.in[0]);
         // weights / bias -> f16
@@ -559,15 +585,23 @@ void quantize_qdq(GraphIR& g, const std::set<std::string>& keep_f16) {
       auto w = as_f32(W);
       std::vector<float> ws(co);
       std::vector<int8_t> wq(w.size());
-      for (int64_t c = 0; c < co; ++c) {
-        float am = 0.0f;
-        for (int64_t k = 0; k < kh * kw * ci; ++k) am = fmaxf(am, fabsf(w[k * co + c]));
-        ws[c] = am > 0.0f ? am / 127.0f : 1.0f;
-        const float inv = 1.0f / ws[c];
-        for (int64_t k = 0; k < kh * kw * ci; ++k) {
-          float r = roundf(w[k * co + c] * inv);
-          r = r < -128.0f ? -128.0f : (r > 127.0f ? 127.0f : r);
-          wq[k * co + c] = (int8_t)r;
+      if (W.prequant) {
+        // the model's own int8 weights and per-output-channel scales
+        if (!(W.q_axis == 0 || (W.q_axis < 0 && W.ch_scales.size() == 1)))
+          fail(DW_ERR_UNSUPPORTED, "quantize_qdq: weight scales of " + op.name + " are not per output channel");
+        for (int64_t c = 0; c < co; ++c) ws[c] = W.ch_scales.size() == 1 ? W.ch_scales[0] : W.ch_scales[c];
+        for (size_t e = 0; e < w.size(); ++e) wq[e] = (int8_t)w[e];
+      } else {
+        for (int64_t c = 0; c < co; ++c) {
+          float am = 0.0f;
+          for (int64_t k = 0; k < kh * kw * ci; ++k) am = fmaxf(am, fabsf(w[k * co + c]));
+          ws[c] = am > 0.0f ? am / 127.0f : 1.0f;
+          const float inv = 1.0f / ws[c];
+          for (int64_t k = 0; k < kh * kw * ci; ++k) {
+            float r = roundf(w[k * co + c] * inv);
+            r = r < -128.0f ? -128.0f : (r > 127.0f ? 127.0f : r);
+            wq[k * co + c] = (int8_t)r;
+          }
         }
       }
       W.data.assign((const uint8_t*)wq.data(), (const uint8_t*)wq.data() + wq.size());
@@ -579,7 +613,12 @@ void quantize_qdq(GraphIR& g, const std::set<std::string>& keep_f16) {
         std::vector<int32_t> bq(co);
         for (int64_t c = 0; c < co; ++c) {
           const double s = (double)(X.scale * ws[c]);
-          double r = nearbyint((double)b[c] / s);
+          // a QDQ model's int32 bias is q * its scale (input scale x weight
+          // scale, so q itself comes back)
+          const double bv = Bt.prequant ? (double)b[c] * (double)(Bt.ch_scales.size() == 1 ? Bt.ch_scales[0]
+                                                                                          : Bt.ch_scales[c])
+                                        : (double)b[c];
+          double r = nearbyint(bv / s);
           r = std::min(std::max(r, -2147483648.0), 2147483647.0);
           bq[c] = (int32_t)r;
         }
@@ -649,15 +688,24 @@ void quantize_qdq(GraphIR& g, const std::set<std::string>& keep_f16) {
       const TensorInfo& X = g.tensor(x);
       std::vector<float> ws(n);
       std::vector<int8_t> wq(wk.size());
-      for (int64_t j = 0; j < n; ++j) {
-        float am = 0.0f;
-        for (int64_t p = 0; p < k; ++p) am = fmaxf(am, fabsf(wk[p * n + j]));
-        ws[j] = am > 0.0f ? am / 127.0f : 1.0f;
-        const float inv = 1.0f / ws[j];
-        for (int64_t p = 0; p < k; ++p) {
-          float r = roundf(wk[p * n + j] * inv);
-          r = r < -128.0f ? -128.0f : (r > 127.0f ? 127.0f : r);
-          wq[p * n + j] = (int8_t)r;
+      if (W.prequant) {
+        // scales per output column: along B's n dimension (axis 1, or 0 with transB)
+        const int n_axis = tb ? 0 : 1;
+        if (!(W.q_axis == n_axis || (W.q_axis < 0 && W.ch_scales.size() == 1)))
+          fail(DW_ERR_UNSUPPORTED, "quantize_qdq: weight scales of " + op.name + " are not per output column");
+        for (int64_t j = 0; j < n; ++j) ws[j] = W.ch_scales.size() == 1 ? W.ch_scales[0] : W.ch_scales[j];
+        for (size_t e = 0; e < wk.size(); ++e) wq[e] = (int8_t)wk[e];
+      } else {
+        for (int64_t j = 0; j < n; ++j) {
+          float am = 0.0f;
+          for (int64_t p = 0; p < k; ++p) am = fmaxf(am, fabsf(wk[p * n + j]));
+          ws[j] = am > 0.0f ? am / 127.0f : 1.0f;
+          const float inv = 1.0f / ws[j];
+          for (int64_t p = 0; p < k; ++p) {
+            float r = roundf(wk[p * n + j] * inv);
+            r = r < -128.0f ? -128.0f : (r > 127.0f ? 127.0f : r);
+            wq[p * n + j] = (int8_t)r;
+          }
         }
       }
       W.data.assign((const uint8_t*)wq.data(), (const uint8_t*)wq.data() + wq.size());
@@ -671,7 +719,10 @@ void quantize_qdq(GraphIR& g, const std::set<std::string>& keep_f16) {
         std::vector<int32_t> bq(n);
         for (int64_t j = 0; j < n; ++j) {
           const double sc = (double)(X.scale * ws[j]);
-          double r = nearbyint((double)b[j] / sc);
+          const double bv = Bt.prequant ? (double)b[j] * (double)(Bt.ch_scales.size() == 1 ? Bt.ch_scales[0]
+                                                                                           : Bt.ch_scales[j])
+                                        : (double)b[j];
+          double r = nearbyint(bv / sc);
           r = std::min(std::max(r, -2147483648.0), 2147483647.0);
           bq[j] = (int32_t)r;
         }

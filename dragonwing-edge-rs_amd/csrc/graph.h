@@ -27,6 +27,15 @@ struct TensorInfo {
   // calibration range (calibration.rs:56-69)
   bool has_range = false;
   float rmin = 0.0f, rmax = 0.0f;
+  // quantization fixed by the model (QDQ import): an f32 activation whose
+  // scale / zp (has_q) quantize_qdq takes as given
+  bool q_fixed = false;
+  // an initializer holding integers as exact f32 values (a dequantized int8
+  // weight or int32 bias of a QDQ model) with their scales in ch_scales
+  // (one, or one per index of dimension q_axis of the original layout)
+  bool prequant = false;
+  bool prequant_i32 = false;
+  int q_axis = -1;
 
   int64_t numel() const {
     int64_t n = 1;

@@ -80,11 +80,22 @@ def _cstrs(names):
 class Graph:
     """A compiled-graph IR owned by libdwhip (one ``dw_graph``)."""
 
-    def __init__(self, dtype: int = GRAPH_F32):
-        h = C.c_void_p()
-        check(load().dw_graph_create(dtype, C.byref(h)))
-        self._h = h.value
+    def __init__(self, dtype: int = GRAPH_F32, _handle=None):
+        if _handle is None:
+            h = C.c_void_p()
+            check(load().dw_graph_create(dtype, C.byref(h)))
+            _handle = h.value
+        self._h = _handle
         track(self, RELEASE_GRAPH)
+
+    @classmethod
+    def from_onnx(cls, data: bytes) -> "Graph":
+        """The F32 NCHW graph of a serialized ONNX model (QDQ models carry
+        their quantization for quantize_qdq)."""
+        buf = C.create_string_buffer(bytes(data), len(data))
+        h = C.c_void_p()
+        check(load().dw_graph_from_onnx(buf, len(data), C.byref(h)))
+        return cls(_handle=h.value)
 
     @property
     def handle(self):
@@ -305,3 +316,14 @@ def calibrate(backend, graph: Graph, input_name: str, images: np.ndarray):
     per = int(np.prod(imgs.shape[1:]))
     check(load().dw_hip_calibrate(backend.handle, graph.handle, input_name.encode(), imgs.ctypes.data, per,
                                   imgs.shape[0]))
+
+
+def onnx_inspect(data: bytes) -> dict:
+    """The parsed model as the loader sees it (nodes, attributes,
+    initializers, inputs, outputs, opset)."""
+    buf = C.create_string_buffer(bytes(data), len(data))
+    need = C.c_size_t()
+    check(load().dw_onnx_inspect(buf, len(data), None, 0, C.byref(need)))
+    out = C.create_string_buffer(need.value)
+    check(load().dw_onnx_inspect(buf, len(data), out, need.value, C.byref(need)))
+    return json.loads(out.value.decode())

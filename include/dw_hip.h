@@ -434,6 +434,23 @@ typedef struct dw_op_params {
  * struct.  No counterpart in the reference (layout check for FFI callers). */
 size_t dw_op_params_size(void);
 
+/* ONNX model loading (crates/dragonwing-onnx/src/proto.rs:129-271,
+ * model.rs:324-707; op builders builder.rs:386-420).  dw_graph_from_onnx
+ * parses a serialized ModelProto (opset 12 to 20) and builds an F32 graph in
+ * ONNX's NCHW layout, ready for dw_graph_fold_batchnorm,
+ * dw_graph_convert_nchw_to_nhwc and the rest.  Ops: Conv, Relu, Sigmoid,
+ * Clip, Add, Mul (same shapes), MaxPool, Concat, Split, Resize / Upsample
+ * (nearest, constant scales or sizes), BatchNormalization,
+ * GlobalAveragePool, Flatten, Reshape, Softmax, Gemm, MatMul, Constant,
+ * Identity.  A QDQ model (QuantizeLinear / DequantizeLinear, u8 activations,
+ * symmetric s8 weights, int32 biases) loads as the float graph with its
+ * quantization fixed, which dw_graph_quantize_qdq then uses as given (no
+ * calibration).  dw_onnx_inspect writes a JSON summary of the parsed model
+ * (nodes, attributes, initializers, inputs, outputs) into buf (cap bytes);
+ * *need receives the size it takes. */
+int dw_graph_from_onnx(const void* bytes, size_t len, dw_graph** out);
+int dw_onnx_inspect(const void* bytes, size_t len, char* buf, size_t cap, size_t* need);
+
 /* Graph dtypes (dragonwing_core::Dtype subset, crates/dragonwing-core/src/dtype.rs). */
 #define DW_GRAPH_F32 0
 #define DW_GRAPH_F16 1
