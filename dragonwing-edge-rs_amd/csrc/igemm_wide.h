@@ -1,0 +1,264 @@
+// Wide-tile int8 implicit GEMM for convolutions whose input rows are
+// multiples of 128 bytes (c_in % 128 == 0): the variant for layers where
+// igemm_kernel is bound by its im2col loads.
+//
+// igemm_kernel loads each im2col k-step straight into the MFMA registers:
+// one wave instruction fetches 64 bytes of 16 pixels, which for c_in >= 128
+// (or any strided layer) are half-used 128-byte lines, and the per-CU
+// vector-memory path serves those at half the rate of whole lines.  It also
+// streams its BC-channel weight slice once per 256-pixel workgroup, so the
+// bytes per operation grow as the channel tile shrinks.  Here:
+//
+//  * a workgroup of 8 waves owns 256 output pixels x BC output channels
+//    (BC up to 256, i.e. the whole layer for c_out <= 256): wave w computes
+//    64 pixels (w / 2) x BC / 2 channels (w % 2);
+//  * K is walked in pairs of k-steps: 128 consecutive input channels of one
+//    filter tap.  For each pair the workgroup copies the 256 pixels' 128
+//    bytes into LDS with buffer loads that write LDS directly: 8 lanes per
+//    pixel, so every wave instruction reads 8 whole lines.  Out-of-image
+//    taps use an out-of-range offset, which writes zeros;
+//  * the 16-byte chunks of a pixel's row are stored xor-swizzled (chunk c of
+//    pixel p in slot c ^ (p & 7)), so the MFMA reads, 16 consecutive pixels
+//    x one chunk, hit 8 distinct bank groups per LDS cycle;
+//  * the pair's weight fragments (2 k-steps x BC channels, fragment order)
+//    arrive the same way; both go to double buffers, so the next pair's
+//    loads are in flight while this pair's MFMAs run, with one barrier per
+//    pair;
+//  * the u8 -> s8 xor (or the padding pattern) is applied to the operands
+//    read from LDS, per pixel and tap, as in igemm_kernel; the epilogues are
+//    igemm_kernel's.
+// Integer sums do not depend on the order of K, so the results are those of
+// every other tile shape.
+#pragma once
+
+#include "igemm_kernel.h"
+
+namespace dw {
+
+bool igemm_launch_wide_i8_a(hipStream_t st, const IgemmArgs& a, const TileCfg& t, int epv);  // generic, QU8
+bool igemm_launch_wide_i8_b(hipStream_t st, const IgemmArgs& a, const TileCfg& t, int epv);  // LUT variants
+
+namespace ig {
+
+constexpr int kWidePix = 256;      // output pixels per workgroup
+constexpr int kWideThreads = 512;  // 8 waves
+
+// Static LDS of one instantiation (two im2col stages, two weight stages,
+// epilogue data) and the dynamic k-pair table.
+__host__ __device__ constexpr int wide_static_lds(int bc) { return 2 * kWidePix * 128 + 2 * (2 * bc * 64) + 256 + 8 * bc; }
+inline size_t wide_lds_bytes(int bc, int ksteps) { return (size_t)wide_static_lds(bc) + (size_t)(ksteps / 2 + 1) * 8; }
+
+// Element offset of pixel p's top-left tap and the in-image bit of every
+// tap (no bits for pixels past the end).
+__device__ __forceinline__ void wide_pixel(const IgemmArgs& a, int p, int& base, uint32_t& mask) {
+  const bool pv = p < a.m;
+  const int pp = pv ? p : 0;
+  const int hw_o = a.ho * a.wo;
+  const int nn = div_small(pp, hw_o, a.r_hwo);
+  const int r = pp - nn * hw_o;
+  const int oh = div_small(r, a.wo, a.r_wo);
+  const int ow = r - oh * a.wo;
+  const int ih0 = oh * a.sh - a.pt, iw0 = ow * a.sw - a.pl;
+  base = ((nn * a.h + ih0) * a.w + iw0) * a.x_pix_stride + a.x_c_off;
+  const int rlo = max(0, -ih0), rhi = min(a.kh, a.h - ih0);
+  const int clo = max(0, -iw0), chi = min(a.kw, a.w - iw0);
+  const uint32_t cols = chi > clo ? (1u << chi) - (1u << clo) : 0u;
+  uint32_t m = 0;
+  for (int kh = 0; kh < a.kh; ++kh) m |= (kh >= rlo && kh < rhi) ? cols << (kh * a.kw) : 0u;
+  mask = pv ? m : 0u;
+}
+
+template <int BC, int EPV>
+__global__ __launch_bounds__(kWideThreads) void igemm_wide_kernel(const IgemmArgs a) {
+  constexpr int CBT = BC / 16;  // 16-channel blocks of the tile
+  constexpr int CB = CBT / 2;   // per wave
+  constexpr int PB = 4;         // 16-pixel blocks per wave
+  constexpr int HC = BC / 2;    // channels per wave
+  constexpr bool FAST = EPV != EPV_GENERIC;
+  constexpr int WPAIR = 2 * CBT * 1024;
+  static_assert(BC == 256 || BC == 128 || BC == 64, "wide tile");
+  __shared__ __attribute__((aligned(16))) uint8_t s_x0[kWidePix * 128];
+  __shared__ __attribute__((aligned(16))) uint8_t s_x1[kWidePix * 128];
+  __shared__ __attribute__((aligned(16))) uint8_t s_w0[WPAIR];
+  __shared__ __attribute__((aligned(16))) uint8_t s_w1[WPAIR];
+  __shared__ __attribute__((aligned(16))) uint8_t s_epi[256 + 8 * BC];
+  extern __shared__ __attribute__((aligned(16))) int2 ktab[];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int NP = a.ksteps / 2;
+
+  // XCD-aware tile order, as igemm_kernel
+  const int nwg = gridDim.x;
+  const int bid = blockIdx.x;
+  const int xcd = bid & 7, idx = bid >> 3;
+  const int base = nwg >> 3, rem = nwg & 7;
+  const int tile = xcd * base + min(xcd, rem) + idx;
+  const int ctiles = a.cout_pad / BC;
+  const int ptile = tile / ctiles;
+  const int c0 = (tile - ptile * ctiles) * BC;
+  const int tp0 = ptile * kWidePix;
+  const int chh = wave & 1, pq = wave >> 1;
+
+  uint8_t* const s_lut = s_epi;
+  uint8_t* const s_bias = s_epi + 256;
+  uint8_t* const s_ms = s_epi + 256 + 4 * BC;
+
+  // ---- k-pair table: pair q is 128 input channels of one tap
+  for (int q = tid; q < NP; q += kWideThreads) {
+    const int e = q * 128;
+    const int tap = div_small(e, a.cin, a.r_cin);
+    const int ci = e - tap * a.cin;
+    const int kh = div_small(tap, a.kw, a.r_kw);
+    const int kw = tap - kh * a.kw;
+    ktab[q] = make_int2((kh * a.w + kw) * a.x_pix_stride + ci, tap);
+  }
+  // ---- epilogue data of the channel tile
+  const int nvalid = min(BC, a.cout - c0);
+  if (a.epi == EPI_QU8) {
+    if (tid < nvalid) {
+      reinterpret_cast<int*>(s_bias)[tid] = a.bias_i ? a.bias_i[c0 + tid] : 0;
+      reinterpret_cast<float*>(s_ms)[tid] = a.mscale[c0 + tid];
+    }
+    if (a.lut && tid < 256) s_lut[tid] = a.lut[tid];
+  }
+
+  // ---- the pixels this thread loads (i * 64 + tid / 8, chunk slot tid % 8)
+  int lbase[4];
+  uint32_t lmask[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) wide_pixel(a, tp0 + i * 64 + (tid >> 3), lbase[i], lmask[i]);
+  const int lchunk = (tid & 7) ^ ((tid >> 3) & 7);  // chunk this lane loads into slot tid % 8
+  // ---- this lane's MFMA pixels: in-image bits (tp0 + pq * 64 + pb * 16 + lane % 16)
+  int mbase[PB];
+  uint32_t mmask[PB];
+  pixel_setup<PB>(a, tp0 + pq * 64, lane, true, mbase, mmask);
+
+  const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, a.x_bytes, 0x00020000);
+  const int frag_lane = ((lane & 15) * 64 + (lane >> 4) * 16);
+  __syncthreads();  // the k-pair table
+
+  // pair q's im2col rows and weight fragments, straight into LDS
+  auto issue = [&](int q, uint8_t* sx, uint8_t* sw) {
+    const int2 t = ktab[q];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool ok = (lmask[i] >> t.y) & 1u;
+      const int off = ok ? lbase[i] + t.x + lchunk * 16 : (int)0x80000000;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          xrsrc, (__attribute__((address_space(3))) void*)(sx + (i * 64 + wave * 8) * 128), 16, off, 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < (2 * CBT + 7) / 8; ++j) {
+      const int f = wave + 8 * j;
+      if (f < 2 * CBT) {
+        const int ks = f / CBT, cb = f - (f / CBT) * CBT;
+        const uint8_t* src = a.wpk + (((uint32_t)(2 * q + ks) * a.cout_pad + c0 + cb * 16) * 64u + frag_lane);
+        __builtin_amdgcn_global_load_lds((const void*)src, (__attribute__((address_space(3))) void*)(sw + f * 1024),
+                                         16, 0, 0);
+      }
+    }
+  };
+
+  issue(0, s_x0, s_w0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  const int cq = 4 * (lane >> 4);
+  v4i acc[CB][PB];
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb) {
+    v4i init = v4i{0, 0, 0, 0};
+    if constexpr (FAST) {
+      if (a.bias_i) init = *reinterpret_cast<const v4i*>(s_bias + 4 * (chh * HC + cb * 16 + cq));
+    }
+#pragma unroll
+    for (int pb = 0; pb < PB; ++pb) acc[cb][pb] = init;
+  }
+
+  // pair q from stage (sx, sw): two k-steps of CB x PB MFMAs.  Both
+  // k-steps' pixel fragments are read first; each weight fragment is read
+  // one MFMA group ahead of its use, so LDS reads overlap the MFMAs.
+  auto compute = [&](int q, const uint8_t* sx, const uint8_t* sw) {
+    const int tap = ktab[q].y;
+    uint32_t key[PB];
+#pragma unroll
+    for (int pb = 0; pb < PB; ++pb) key[pb] = ((mmask[pb] >> tap) & 1u) ? a.xxor : a.xpad;
+    u32x4 bf[2][PB];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int slot = ((4 * h) + (lane >> 4)) ^ (lane & 7);
+#pragma unroll
+      for (int pb = 0; pb < PB; ++pb) {
+        const int pl = pq * 64 + pb * 16 + (lane & 15);
+        bf[h][pb] = *reinterpret_cast<const u32x4*>(sx + pl * 128 + slot * 16);
+      }
+    }
+    const uint8_t* const wl = sw + chh * CB * 1024 + lane * 16;
+    v4i ar[2];
+    ar[0] = *reinterpret_cast<const v4i*>(wl);
+#pragma unroll
+    for (int pb = 0; pb < PB; ++pb) {
+      bf[0][pb] ^= key[pb];
+      bf[1][pb] ^= key[pb];
+    }
+#pragma unroll
+    for (int i = 0; i < 2 * CB; ++i) {
+      const int h = i / CB, cb = i - (i / CB) * CB;
+      if (i + 1 < 2 * CB) {
+        const int h1 = (i + 1) / CB, cb1 = (i + 1) - ((i + 1) / CB) * CB;
+        ar[(i + 1) & 1] = *reinterpret_cast<const v4i*>(wl + (h1 * CBT + cb1) * 1024);
+      }
+      const v4i af = ar[i & 1];
+#pragma unroll
+      for (int pb = 0; pb < PB; ++pb)
+        acc[cb][pb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, __builtin_bit_cast(v4i, bf[h][pb]), acc[cb][pb], 0, 0, 0);
+    }
+  };
+
+  for (int q = 0; q < NP; q += 2) {
+    if (q + 1 < NP) issue(q + 1, s_x1, s_w1);
+    compute(q, s_x0, s_w0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (q + 1 < NP) {
+      if (q + 2 < NP) issue(q + 2, s_x0, s_w0);
+      compute(q + 1, s_x1, s_w1);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
+  }
+
+  // epilogue: this wave's 64 pixels x HC channels; the first im2col stage
+  // regroups the u8 results (every wave is past its last read of it)
+  EpiLds ep{nullptr, nullptr, nullptr, nullptr};
+  if (a.epi == EPI_QU8) {
+    ep.bias = a.bias_i ? reinterpret_cast<const int*>(s_bias) + chh * HC : nullptr;
+    ep.ms = reinterpret_cast<const float*>(s_ms) + chh * HC;
+    ep.lut = a.lut ? s_lut : nullptr;
+  }
+  uint8_t* xp = nullptr;
+  if constexpr (FAST && HC >= 32) xp = s_x0 + wave * 16 * xpose_row(HC);
+  igemm_store<1, HC, PB, EPV>(a, ep, acc, c0 + chh * HC, tp0 + pq * 64, lane, s_ms + 4 * chh * HC, s_lut, xp);
+}
+
+template <int EPV>
+bool launch_wide_tiles(hipStream_t st, const IgemmArgs& a, const TileCfg& t) {
+  const dim3 grid((unsigned)(((a.m + kWidePix - 1) / kWidePix) * (a.cout_pad / t.bc)));
+  const size_t dyn = (size_t)(a.ksteps / 2 + 1) * 8;
+#define DW_B(BC_)                                                                                   \
+  case BC_:                                                                                         \
+    hipLaunchKernelGGL((igemm_wide_kernel<BC_, EPV>), grid, dim3(kWideThreads), dyn, st, a);      \
+    return true;
+  switch (t.bc) {
+    DW_B(256)
+    DW_B(128)
+    DW_B(64)
+  }
+#undef DW_B
+  return false;
+}
+
+}  // namespace ig
+}  // namespace dw

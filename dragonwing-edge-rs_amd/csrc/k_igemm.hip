@@ -6,6 +6,7 @@
 #include "igemm_rows.h"
 #include "igemm_sk.h"
 #include "igemm_stream.h"
+#include "igemm_wide.h"
 
 #include <stdio.h>
 #include <stdlib.h>
@@ -118,6 +119,24 @@ TileCfg make_rows_tile(const IgemmArgs& a, int bc) {
   return t;
 }
 
+// The wide-tile kernel (tpw = -3): int8, input rows of whole 128-byte
+// units (c_in % 128 == 0, 16-byte aligned views), 256-pixel workgroups of
+// 64, 128 or 256 channels.
+bool wide_ok(const IgemmArgs& a, int bc) {
+  if (a.epi == EPI_F16 || a.cin % 128 != 0 || a.x_pix_stride % 16 != 0 || a.x_c_off % 16 != 0) return false;
+  if (!(bc == 256 || bc == 128 || bc == 64) || a.cout_pad % bc != 0 || a.ksteps % 2 != 0) return false;
+  if (bc > 64 && a.cout <= bc / 2) return false;  // half the tile would be padding
+  return ig::wide_lds_bytes(bc, a.ksteps) <= 160 * 1024;
+}
+
+TileCfg make_wide_tile(const IgemmArgs& a, int bc) {
+  TileCfg t = make_tile(a, std::min(bc, 128), 4);
+  t.bc = bc;
+  t.kchunk = a.ksteps;
+  t.tpw = -3;
+  return t;
+}
+
 // Tile shape for a problem: an override from DW_IGEMM_TILE (tests and
 // tuning runs), an explicit choice (a.tile_bc / a.tile_pb, set by the graph
 // runtime's tuner), else the widest channel tile and the widest pixel tile
@@ -131,12 +150,14 @@ TileCfg pick(const IgemmArgs& a) {
     if (nv == 3 && sk_ok(a, v0, v1, v2)) return make_sk_tile(a, v0, v1, v2);
     if (nv == 3 && v2 == -1 && st_ok(a, v0, v1)) return make_st_tile(a, v0, v1);
     if (nv == 3 && v2 == -2 && rows_ok(a, v0)) return make_rows_tile(a, v0);
+    if (nv == 3 && v2 == -3 && wide_ok(a, v0)) return make_wide_tile(a, v0);
     if (nv >= 2 && tile_ok(a, v0, v1)) return make_tile(a, v0, v1);
     if (nv == 1 && tile_ok(a, channel_tile(a.cout), v0)) return make_tile(a, channel_tile(a.cout), v0);
   }
   if (a.tile_bc && sk_ok(a, a.tile_bc, a.tile_pb, a.tile_tpw)) return make_sk_tile(a, a.tile_bc, a.tile_pb, a.tile_tpw);
   if (a.tile_bc && a.tile_tpw == -1 && st_ok(a, a.tile_bc, a.tile_pb)) return make_st_tile(a, a.tile_bc, a.tile_pb);
   if (a.tile_bc && a.tile_tpw == -2 && rows_ok(a, a.tile_bc)) return make_rows_tile(a, a.tile_bc);
+  if (a.tile_bc && a.tile_tpw == -3 && wide_ok(a, a.tile_bc)) return make_wide_tile(a, a.tile_bc);
   if (a.tile_bc && tile_ok(a, a.tile_bc, a.tile_pb)) return make_tile(a, a.tile_bc, a.tile_pb);
   const int bc = channel_tile(a.cout);
   const int ctiles = a.cout_pad / bc;
@@ -160,6 +181,13 @@ int igemm_channel_tile(int cout) { return channel_tile(cout); }
 
 int igemm_candidates(const IgemmArgs& a, int* bc, int* pb, int* tpw, int max) {
   int n = 0;
+  for (int b : {256, 128, 64})
+    if (n < max && wide_ok(a, b)) {
+      bc[n] = b;
+      pb[n] = 4;
+      tpw[n] = -3;
+      ++n;
+    }
   for (int b : {128, 96, 80, 64, 48, 32, 16})
     for (int p : {4, 2, 1}) {
       if (n < max && tile_ok(a, b, p)) {
@@ -202,6 +230,8 @@ const char* igemm_tile_name(const IgemmArgs& a, int esize) {
     snprintf(buf, sizeof buf, "igemm_%s_c%d_p%d_st", esize == 1 ? "i8" : "f16", t.bc, 64 * t.pb);
   else if (t.tpw == -2)
     snprintf(buf, sizeof buf, "igemm_%s_c%d_rows", esize == 1 ? "i8" : "f16", t.bc);
+  else if (t.tpw == -3)
+    snprintf(buf, sizeof buf, "igemm_%s_c%d_wide", esize == 1 ? "i8" : "f16", t.bc);
   else
     snprintf(buf, sizeof buf, "igemm_%s_c%d_p%d", esize == 1 ? "i8" : "f16", t.bc, 64 * t.pb);
   return buf;
@@ -220,6 +250,7 @@ void launch_igemm(hipStream_t st, const IgemmArgs& a_in, int esize) {
   const size_t lds = t.tpw > 0     ? ig::sk_lds_bytes(t.bc, a.ksteps)
                      : t.tpw == -1 ? ig::st_lds_bytes(t.bc, a.ksteps, t.pd)
                      : t.tpw == -2 ? ig::rows_lds_bytes(t.bc, a.ksteps, a.w, a.cin)
+                     : t.tpw == -3 ? ig::wide_lds_bytes(t.bc, a.ksteps)
                                    : ig::lds_bytes(t, a.ksteps);
   if (lds > 160 * 1024) fail(-2, "igemm: k-slice table does not fit LDS");
   if ((long long)a.ho * a.wo >= (1ll << 23)) fail(-2, "igemm: more than 2^23 output pixels per image");
@@ -246,6 +277,8 @@ void launch_igemm(hipStream_t st, const IgemmArgs& a_in, int esize) {
       ok = ab ? igemm_launch_st_i8_a(st, a, t, epv) : igemm_launch_st_i8_b(st, a, t, epv);
     else if (t.tpw == -2)
       ok = ab ? igemm_launch_rows_i8_a(st, a, t, epv) : igemm_launch_rows_i8_b(st, a, t, epv);
+    else if (t.tpw == -3)
+      ok = ab ? igemm_launch_wide_i8_a(st, a, t, epv) : igemm_launch_wide_i8_b(st, a, t, epv);
     else
       ok = ab ? igemm_launch_i8_a(st, a, t, epv) : igemm_launch_i8_b(st, a, t, epv);
   } else {

@@ -118,6 +118,23 @@ def test_int8_graph_persistent_tiles_bit_exact(backend, int8_small, monkeypatch,
         np.testing.assert_array_equal(gv, ref[o], err_msg=f"{o} tile {tile}")
 
 
+@pytest.mark.parametrize("tile", ["256,4,-3", "128,4,-3", "64,4,-3"])
+def test_int8_graph_wide_tiles_bit_exact(backend, monkeypatch, tile):
+    # Every layer with c_in a multiple of 128 on the wide-tile kernel
+    # (requantize, table and table + residual epilogues).
+    g, info = yolo.int8_graph(backend, batch=2, size=160, calib=yolo.calibration_images(4, 160))
+    monkeypatch.setenv("DW_IGEMM_TILE", tile)
+    x = yolo.input_images(2, 160)
+    rt = HipGraphRuntime(g, backend)
+    assert sum(L["kernel"].endswith("_wide") for L in rt.launches()) >= 4
+    rt.set_input_f32(info["input"], x)
+    rt.run()
+    got = gpu_outputs(rt, info)
+    ref = oracle_run(g, {info["input"]: synth.f16_bits(x)})
+    for o, gv in zip(info["outputs"], got):
+        np.testing.assert_array_equal(gv, ref[o], err_msg=f"{o} tile {tile}")
+
+
 @pytest.mark.parametrize("tile", ["128,1,-1", "64,2,-1", "32,4,-1"])
 def test_int8_graph_streamed_tiles_bit_exact(backend, int8_small, monkeypatch, tile):
     # Every layer with two or more k-steps on the streamed-weight kernel

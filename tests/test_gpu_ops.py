@@ -287,6 +287,45 @@ def test_qlinearconv_row_tiles_bit_exact(backend, geom, monkeypatch):
         np.testing.assert_array_equal(run_qconv(backend, c, s, p), ref, err_msg=f"tile {bc},4,-2")
 
 
+def wide_tiles(co):
+    """The wide-tile kernel's channel tiles for c_out = co (input rows of
+    whole 128-byte units)."""
+    top = channel_tile(co)
+    pad = -(-co // top) * top
+    return [bc for bc in (256, 128, 64) if pad % bc == 0 and not (bc > 64 and co <= bc // 2)]
+
+
+@pytest.mark.parametrize("geom,x_zp", [((2, 9, 11, 128, 256, 3, 2, 1), 128), ((1, 13, 7, 256, 128, 3, 1, 1), 119),
+                                       ((2, 10, 10, 128, 64, 1, 1, 0), 140), ((1, 6, 6, 384, 256, 1, 1, 0), 128),
+                                       ((2, 20, 20, 128, 128, 3, 2, 1), 100), ((3, 5, 3, 128, 192, 3, 1, 1), 7)])
+def test_qlinearconv_wide_tiles_bit_exact(backend, geom, x_zp, monkeypatch):
+    # The wide-tile kernel (k-step pairs staged through LDS with swizzled
+    # whole-line loads, 256-pixel workgroups) over every channel tile it has;
+    # ragged pixel counts, padding with zero points other than 128, 1x1 and
+    # strided 3x3 layers.
+    n, h, w, ci, co, k, s, p = geom
+    r = synth.Rng(synth.seed_for(1100 + sum(geom)))
+    c = dict(x=r.integers((n, h, w, ci), 0, 255).astype(np.uint8),
+             w=r.integers((k, k, ci, co), -127, 127).astype(np.int8),
+             bias=r.integers((co,), -4096, 4096).astype(np.int32),
+             w_scales=r.log_uniform((co,), 1e-3, 1e-2), x_scale=0.02, x_zp=x_zp, y_scale=0.05, y_zp=131)
+    ref = oracle_qconv(c, s, p)
+    tiles = wide_tiles(co)
+    assert tiles
+    for bc in tiles:
+        monkeypatch.setenv("DW_IGEMM_TILE", f"{bc},4,-3")
+        np.testing.assert_array_equal(run_qconv(backend, c, s, p), ref, err_msg=f"tile {bc},4,-3")
+
+
+def test_qlinearconv_full_workload_wide_bit_exact(backend, monkeypatch):
+    # batch 32, 80x80x128 -> 40x40x256 on the wide-tile kernel, every tile
+    c = synth.qlinearconv_case(1)
+    ref = oracle_qconv(c, 2, 1)
+    for bc in (256, 128, 64):
+        monkeypatch.setenv("DW_IGEMM_TILE", f"{bc},4,-3")
+        np.testing.assert_array_equal(run_qconv(backend, c, 2, 1), ref, err_msg=f"tile {bc},4,-3")
+
+
 def test_qlinearconv_golden_fixtures(backend):
     cases = json.loads((GOLDEN / "qlinear_cases.json").read_text())["qlinearconv"]
     for g in cases:
