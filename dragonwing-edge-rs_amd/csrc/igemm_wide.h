@@ -23,7 +23,11 @@
 //  * the pair's weight fragments (2 k-steps x BC channels, fragment order)
 //    arrive the same way; both go to double buffers, so the next pair's
 //    loads are in flight while this pair's MFMAs run, with one barrier per
-//    pair;
+//    pair.  The last two MFMA groups of a pair run after that barrier, from
+//    registers, to cover the latency of the next pair's first LDS reads;
+//  * LDS carries 128 bytes per cycle per CU; a pair costs 8 waves x 24 KB
+//    of fragment reads plus 64 KB of copies against 2 x 64 MFMAs per SIMD
+//    (2048 cycles), so the loop is bound by LDS as much as by the MFMAs;
 //  * the u8 -> s8 xor (or the padding pattern) is applied to the operands
 //    read from LDS, per pixel and tap, as in igemm_kernel; the epilogues are
 //    igemm_kernel's.
@@ -105,25 +109,6 @@ __global__ __launch_bounds__(kWideThreads) void igemm_wide_kernel(const IgemmArg
   uint8_t* const s_bias = s_epi + 256;
   uint8_t* const s_ms = s_epi + 256 + 4 * BC;
 
-  // ---- k-pair table: pair q is 128 input channels of one tap
-  for (int q = tid; q < NP; q += kWideThreads) {
-    const int e = q * 128;
-    const int tap = div_small(e, a.cin, a.r_cin);
-    const int ci = e - tap * a.cin;
-    const int kh = div_small(tap, a.kw, a.r_kw);
-    const int kw = tap - kh * a.kw;
-    ktab[q] = make_int2((kh * a.w + kw) * a.x_pix_stride + ci, tap);
-  }
-  // ---- epilogue data of the channel tile
-  const int nvalid = min(BC, a.cout - c0);
-  if (a.epi == EPI_QU8) {
-    if (tid < nvalid) {
-      reinterpret_cast<int*>(s_bias)[tid] = a.bias_i ? a.bias_i[c0 + tid] : 0;
-      reinterpret_cast<float*>(s_ms)[tid] = a.mscale[c0 + tid];
-    }
-    if (a.lut && tid < 256) s_lut[tid] = a.lut[tid];
-  }
-
   // ---- the pixels this thread loads (i * 64 + tid / 8, chunk slot tid % 8)
   int lbase[4];
   uint32_t lmask[4];
@@ -137,11 +122,9 @@ __global__ __launch_bounds__(kWideThreads) void igemm_wide_kernel(const IgemmArg
 
   const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, a.x_bytes, 0x00020000);
   const int frag_lane = ((lane & 15) * 64 + (lane >> 4) * 16);
-  __syncthreads();  // the k-pair table
-
-  // pair q's im2col rows and weight fragments, straight into LDS
-  auto issue = [&](int q, uint8_t* sx, uint8_t* sw) {
-    const int2 t = ktab[q];
+  // pair q's im2col rows and weight fragments (t: its ktab entry), straight
+  // into LDS
+  auto issue_t = [&](int q, int2 t, uint8_t* sx, uint8_t* sw) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const bool ok = (lmask[i] >> t.y) & 1u;
@@ -161,9 +144,30 @@ __global__ __launch_bounds__(kWideThreads) void igemm_wide_kernel(const IgemmArg
     }
   };
 
-  issue(0, s_x0, s_w0);
+  auto issue = [&](int q, uint8_t* sx, uint8_t* sw) { issue_t(q, ktab[q], sx, sw); };
+
+  // pair 0 (tap 0, channels 0..127) is in flight while the tables are built
+  issue_t(0, make_int2(0, 0), s_x0, s_w0);
+  // ---- k-pair table: pair q is 128 input channels of one tap
+  for (int q = tid; q < NP; q += kWideThreads) {
+    const int e = q * 128;
+    const int tap = div_small(e, a.cin, a.r_cin);
+    const int ci = e - tap * a.cin;
+    const int kh = div_small(tap, a.kw, a.r_kw);
+    const int kw = tap - kh * a.kw;
+    ktab[q] = make_int2((kh * a.w + kw) * a.x_pix_stride + ci, tap);
+  }
+  // ---- epilogue data of the channel tile
+  const int nvalid = min(BC, a.cout - c0);
+  if (a.epi == EPI_QU8) {
+    if (tid < nvalid) {
+      reinterpret_cast<int*>(s_bias)[tid] = a.bias_i ? a.bias_i[c0 + tid] : 0;
+      reinterpret_cast<float*>(s_ms)[tid] = a.mscale[c0 + tid];
+    }
+    if (a.lut && tid < 256) s_lut[tid] = a.lut[tid];
+  }
   __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
+  __syncthreads();  // pair 0, the k-pair table and the epilogue data
 
   const int cq = 4 * (lane >> 4);
   v4i acc[CB][PB];
@@ -177,58 +181,98 @@ __global__ __launch_bounds__(kWideThreads) void igemm_wide_kernel(const IgemmArg
     for (int pb = 0; pb < PB; ++pb) acc[cb][pb] = init;
   }
 
-  // pair q from stage (sx, sw): two k-steps of CB x PB MFMAs.  Both
-  // k-steps' pixel fragments are read first; each weight fragment is read
-  // one MFMA group ahead of its use, so LDS reads overlap the MFMAs.
-  auto compute = [&](int q, const uint8_t* sx, const uint8_t* sw) {
+  // pair q from stage (sx, sw): two k-steps of CB x PB MFMAs, one group
+  // (one weight fragment x PB pixel fragments) at a time.  The pixel
+  // fragments and the first two weight fragments are read up front; each
+  // later weight fragment two groups ahead of its use.  The last kDefer
+  // groups are held back in registers (weight fragments pa, pixel fragments
+  // pbf) and run after the barrier, at the start of the next pair, while
+  // that pair's first reads are in flight.  sched_barrier keeps the reads
+  // where they are placed.
+  constexpr int kDefer = 2;
+  constexpr int NG = 2 * CB - kDefer;  // groups run within their own pair
+  static_assert(kDefer <= CB, "the held-back groups are second k-step groups");
+  v4i pa[kDefer];
+  u32x4 pbf[PB];
+  auto held_back = [&]() {
+#pragma unroll
+    for (int d = 0; d < kDefer; ++d)
+#pragma unroll
+      for (int pb = 0; pb < PB; ++pb)
+        acc[CB - kDefer + d][pb] =
+            __builtin_amdgcn_mfma_i32_16x16x64_i8(pa[d], __builtin_bit_cast(v4i, pbf[pb]), acc[CB - kDefer + d][pb], 0, 0, 0);
+  };
+  auto compute = [&](int q, const uint8_t* sx, const uint8_t* sw, bool pend) {
     const int tap = ktab[q].y;
-    uint32_t key[PB];
-#pragma unroll
-    for (int pb = 0; pb < PB; ++pb) key[pb] = ((mmask[pb] >> tap) & 1u) ? a.xxor : a.xpad;
+    const uint8_t* const wl = sw + chh * CB * 1024 + lane * 16;
     u32x4 bf[2][PB];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    v4i ar[3];
+    auto read_pix = [&](int h) {
       const int slot = ((4 * h) + (lane >> 4)) ^ (lane & 7);
 #pragma unroll
       for (int pb = 0; pb < PB; ++pb) {
         const int pl = pq * 64 + pb * 16 + (lane & 15);
         bf[h][pb] = *reinterpret_cast<const u32x4*>(sx + pl * 128 + slot * 16);
       }
-    }
-    const uint8_t* const wl = sw + chh * CB * 1024 + lane * 16;
-    v4i ar[2];
-    ar[0] = *reinterpret_cast<const v4i*>(wl);
-#pragma unroll
-    for (int pb = 0; pb < PB; ++pb) {
-      bf[0][pb] ^= key[pb];
-      bf[1][pb] ^= key[pb];
-    }
-#pragma unroll
-    for (int i = 0; i < 2 * CB; ++i) {
+    };
+    auto read_w = [&](int i) {  // group i's weight fragment: k-step i / CB, block i % CB
       const int h = i / CB, cb = i - (i / CB) * CB;
-      if (i + 1 < 2 * CB) {
-        const int h1 = (i + 1) / CB, cb1 = (i + 1) - ((i + 1) / CB) * CB;
-        ar[(i + 1) & 1] = *reinterpret_cast<const v4i*>(wl + (h1 * CBT + cb1) * 1024);
+      const v4i v = *reinterpret_cast<const v4i*>(wl + (h * CBT + cb) * 1024);
+      if (i >= NG)
+        pa[i - NG] = v;
+      else
+        ar[i % 3] = v;
+    };
+    read_pix(0);
+    read_w(0);
+    read_w(1);
+    read_pix(1);
+    __builtin_amdgcn_sched_barrier(0);
+    if (pend) held_back();
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t key[PB];
+#pragma unroll
+    for (int pb = 0; pb < PB; ++pb) key[pb] = ((mmask[pb] >> tap) & 1u) ? a.xxor : a.xpad;
+#pragma unroll
+    for (int pb = 0; pb < PB; ++pb) bf[0][pb] ^= key[pb];
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+      const int h = i / CB, cb = i - (i / CB) * CB;
+      if (i + 2 < 2 * CB) read_w(i + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      if (i == CB) {
+#pragma unroll
+        for (int pb = 0; pb < PB; ++pb) bf[1][pb] ^= key[pb];
       }
-      const v4i af = ar[i & 1];
+      const v4i af = ar[i % 3];
 #pragma unroll
       for (int pb = 0; pb < PB; ++pb)
         acc[cb][pb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, __builtin_bit_cast(v4i, bf[h][pb]), acc[cb][pb], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
+    if constexpr (NG <= CB) {
+#pragma unroll
+      for (int pb = 0; pb < PB; ++pb) bf[1][pb] ^= key[pb];
+    }
+#pragma unroll
+    for (int pb = 0; pb < PB; ++pb) pbf[pb] = bf[1][pb];
   };
 
+  // the waitcnt also covers this pair's LDS reads (pa, pbf included), so the
+  // stage may be overwritten after the barrier
   for (int q = 0; q < NP; q += 2) {
     if (q + 1 < NP) issue(q + 1, s_x1, s_w1);
-    compute(q, s_x0, s_w0);
+    compute(q, s_x0, s_w0, q > 0);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (q + 1 < NP) {
       if (q + 2 < NP) issue(q + 2, s_x0, s_w0);
-      compute(q + 1, s_x1, s_w1);
+      compute(q + 1, s_x1, s_w1, true);
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
     }
   }
+  held_back();
 
   // epilogue: this wave's 64 pixels x HC channels; the first im2col stage
   // regroups the u8 results (every wave is past its last read of it)
