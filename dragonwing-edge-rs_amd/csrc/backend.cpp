@@ -308,6 +308,11 @@ static int conv_f32_common(dw_hip_backend* be, const dw_hip_buffer* input, const
   a.out_kind = 0;
   a.act = act;
   a.bias_f = bias ? (const float*)bias->ptr : nullptr;
+  if (c_in % 16 == 0 && c_out % 4 == 0) {
+    float* wq = (float*)b->workspace(Backend::WS_WPACK, k_h * k_w * c_in * c_out * 4);
+    dw::launch_repack_oc4(b->stream, (const float*)kernel->ptr, wq, (int)(k_h * k_w * c_in), (int)c_out);
+    a.wq = wq;
+  }
   dw::launch_direct_conv(b->stream, a);
   API_END
 }

@@ -120,6 +120,8 @@ struct DirectArgs {
                            // and the quantization may widen as IEEE f16 (results that
                            // round to f16 subnormals are checked in the kernel)
   int out_plain;           // 1: rint(x * out_rcp) == rint(x / out_scale) for every finite f16 x
+  const float* wq;         // optional (f32 input, c_in % 16 == 0, c_out % 4 == 0): the weights as
+                           // [c_out / 4][kh * kw * c_in][4], for the tiled kernel
 };
 
 // Depthwise convolution (channel multiplier 1).
@@ -155,6 +157,8 @@ int igemm_channel_tile(int cout);
 int igemm_candidates(const IgemmArgs& a, int* bc, int* pb, int* tpw, int max);
 
 void launch_direct_conv(hipStream_t st, const DirectArgs& a);
+// HWIO f32 weights [rows][cout] -> [cout / 4][rows][4] (DirectArgs::wq)
+void launch_repack_oc4(hipStream_t st, const float* w, float* wq, int rows, int cout);
 void launch_dwconv(hipStream_t st, const DwArgs& a, int dtype);
 
 // Classifier-head ops (k_head.hip).  gemm: row-major C[m][n] = A[m][k] B[k][n]

@@ -18,6 +18,8 @@
 // NHWC).  No matrix cores: the op is HBM-bound.
 #include "direct_util.h"
 
+#include <stdlib.h>
+
 namespace dw {
 namespace {
 
@@ -91,6 +93,207 @@ __global__ __launch_bounds__(256) void direct_conv_kernel(const DirectArgs a) {
   const int OES = a.out_kind == 0 ? 4 : (a.out_kind == 1 ? 2 : 1);
   const size_t yo = (size_t)p * a.y_pix_stride + a.y_c_off + oc0;
   dx::store_outputs<OC>(a, acc, oc0, (uint8_t*)a.y + yo * OES);
+}
+
+// f32 convolutions whose input window fits LDS (3x3 at stride 1 with c_in
+// 32 or 64, as the 1 x 56 x 56 x 64 -> 64 fp32 layer).  direct_conv_kernel
+// reads each input vector straight from
+// global memory, 16 bytes per lane at the pixel stride, so every wave
+// instruction touches 64 distinct lines and the per-CU load path, not the
+// FMAs, sets its pace.  Here a workgroup owns a TH x TW tile of output
+// pixels (one per thread) x 4 output channels:
+//  * it copies the tile's input window, all c_in channels of every pixel,
+//    into LDS with 16-byte buffer loads (consecutive lanes: consecutive
+//    channel quads of one pixel; zeros outside the image), and its 4
+//    channels' weights (kh * kw * c_in x 4 floats, packed by the host as
+//    [c_out / 4][kh * kw * c_in][4]), every load in flight before the
+//    first LDS store;
+//  * the LDS pixel stride is c_in + 4 floats, so the 8 lanes of one
+//    ds_read_b128 cycle (8 neighbouring pixels) hit 8 distinct bank groups;
+//  * the weights reach the FMAs through DPP: one VGPR holds the 16 weights
+//    of 4 input x 4 output channels in lanes 0..15 of every row of 16
+//    lanes, and v_fmac_f32_dpp row_newbcast:n multiplies by lane n's value,
+//    so a weight costs neither an SGPR load (whose latency cannot be
+//    overlapped: scalar loads complete out of order, so every wait on one
+//    is a wait for all) nor a broadcast LDS read per FMA.  All LDS reads
+//    complete in order, so the next block's reads are in flight while this
+//    block's FMAs run;
+//  * every lane runs every tap with all lanes enabled (DPP reads its
+//    source lane whatever that lane's own tap is), and a lane whose tap
+//    lies outside the image restores its accumulators after that tap, so
+//    its chain is exactly the reference's with the tap skipped.
+// The FMA chain of each output is the reference's: kh, kw, ic in order,
+// one fused multiply-add per (tap, ic), fma(w, x, acc) = fma(x, w, acc).
+constexpr int kTileLdsFloats = 22 * 1024;  // 88 KB: the input window of one workgroup
+constexpr int kTileWRows = 1536;           // kh * kw * c_in (24 KB of weights)
+
+// One block of 16 input channels for 4 outputs:
+//   acc[j] = fma(w[ic e][oc j], x[e], acc[j]) for e = 0..15 in order, j = 0..3,
+// where lane 4 (e % 4) + j of each row of VGPR w[e / 4] holds w[ic e][oc j].
+// The s_nop covers the two wait states a DPP source needs after a VALU
+// write.
+#define DW_FMAC_DPP(N, J, W, XI) \
+  "v_fmac_f32_dpp %" #J ", %" #W ", %" #XI " row_newbcast:" #N " row_mask:0xf bank_mask:0xf\n"
+#define DW_FMAC_QUAD(W, X0, X1, X2, X3)                                                        \
+  DW_FMAC_DPP(0, 0, W, X0) DW_FMAC_DPP(1, 1, W, X0) DW_FMAC_DPP(2, 2, W, X0) DW_FMAC_DPP(3, 3, W, X0) \
+  DW_FMAC_DPP(4, 0, W, X1) DW_FMAC_DPP(5, 1, W, X1) DW_FMAC_DPP(6, 2, W, X1) DW_FMAC_DPP(7, 3, W, X1) \
+  DW_FMAC_DPP(8, 0, W, X2) DW_FMAC_DPP(9, 1, W, X2) DW_FMAC_DPP(10, 2, W, X2) DW_FMAC_DPP(11, 3, W, X2) \
+  DW_FMAC_DPP(12, 0, W, X3) DW_FMAC_DPP(13, 1, W, X3) DW_FMAC_DPP(14, 2, W, X3) DW_FMAC_DPP(15, 3, W, X3)
+__device__ __forceinline__ void fma16x4_dpp(float (&acc)[4], const float4& w, const float4 (&x)[4]) {
+  asm("s_nop 1\n"
+      DW_FMAC_QUAD(4, 8, 9, 10, 11) DW_FMAC_QUAD(5, 12, 13, 14, 15)
+      DW_FMAC_QUAD(6, 16, 17, 18, 19) DW_FMAC_QUAD(7, 20, 21, 22, 23)
+      : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3])
+      : "v"(w.x), "v"(w.y), "v"(w.z), "v"(w.w),
+        "v"(x[0].x), "v"(x[0].y), "v"(x[0].z), "v"(x[0].w), "v"(x[1].x), "v"(x[1].y), "v"(x[1].z), "v"(x[1].w),
+        "v"(x[2].x), "v"(x[2].y), "v"(x[2].z), "v"(x[2].w), "v"(x[3].x), "v"(x[3].y), "v"(x[3].z), "v"(x[3].w));
+}
+#undef DW_FMAC_QUAD
+#undef DW_FMAC_DPP
+
+template <int TH, int TW, int NBT>
+__global__ __launch_bounds__(TH * TW) void conv_tile_f32_kernel(const DirectArgs a, int tiles_w, int tiles_hw,
+                                                                int iwin_w, int pstr) {
+  constexpr int C = 4;
+  __shared__ __attribute__((aligned(16))) float s_x[kTileLdsFloats];
+  __shared__ __attribute__((aligned(16))) float s_w[kTileWRows * 4];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int tile = blockIdx.x;
+  const int nn = tile / tiles_hw;
+  const int tr = tile - nn * tiles_hw;
+  const int tyi = tr / tiles_w;
+  const int ty0 = tyi * TH, tx0 = (tr - tyi * tiles_w) * TW;
+  const int oc0 = blockIdx.y * C;
+  const int cin = a.cin;
+  const int ih0 = ty0 * a.sh - a.pt, iw0 = tx0 * a.sw - a.pl;
+  const int iwin_h = (TH - 1) * a.sh + a.kh;
+  const int quads = cin >> 2;
+  const int rows = a.kh * a.kw * cin;
+  // All global loads of the workgroup are issued before any LDS store: the
+  // weights (up to 6 float4 per thread) and the input window (up to 24
+  // float4 per thread: c_in 64 at 16 x 16 pixels and a 3 x 3 window), so
+  // their latencies overlap.
+  //
+  // weights: block b of 16 input channels (64 floats of [row][4]) stored so
+  // that float v of lane n's 16-byte read is element 16 v + n of the block
+  constexpr int kWLoads = kTileWRows / (TH * TW);
+  const float4* __restrict__ wq4 = reinterpret_cast<const float4*>(a.wq + (size_t)blockIdx.y * rows * 4);
+  float4 wv4[kWLoads];
+#pragma unroll
+  for (int k = 0; k < kWLoads; ++k) {
+    const int f4 = tid + k * TH * TW;
+    if (f4 < rows) wv4[k] = wq4[f4];
+  }
+  // input window: thread tid loads channel quad q = tid % quads of window
+  // columns c and c + cpp (c = tid / quads, cpp = 256 / quads) in every
+  // window row: at most 2 x 24 loads, all in flight together.  Buffer
+  // loads: a pixel outside the image (or past the window) reads with an
+  // offset past the buffer, which returns zeros with no memory access.
+  constexpr int kXRows = 24;
+  const int cpp = (TH * TW) / quads;
+  const int q = tid % quads, c = tid / quads;
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, a.x_bytes, 0x00020000);
+  const int ps4 = a.x_pix_stride * 4, rstep = a.w * ps4;
+  // rows rlo..rhi-1 of the window lie in the image; an offset with bit 31
+  // set is past the buffer (x_bytes < 2^31)
+  const int rlo = max(0, -ih0), rhi = min(iwin_h, a.h - ih0);
+  float4 xv4[2][kXRows];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int cc = c + h * cpp, iw = iw0 + cc;
+    const bool col_ok = cc < iwin_w && iw >= 0 && iw < a.w;
+    int goff = col_ok ? (((nn * a.h + ih0) * a.w + iw) * a.x_pix_stride + a.x_c_off + 4 * q) * 4 : (int)0x80000000;
+#pragma unroll
+    for (int r = 0; r < kXRows; ++r) {
+      const int roff = (r >= rlo && r < rhi) ? 0 : (int)0x80000000;
+      xv4[h][r] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, goff | roff, 0, 0));
+      goff += rstep;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kWLoads; ++k) {
+    const int f4 = tid + k * TH * TW;
+    if (f4 < rows) {
+      // float4 f4 holds elements 4 f4 .. 4 f4 + 3 of the [row][4] layout
+      const float e[4] = {wv4[k].x, wv4[k].y, wv4[k].z, wv4[k].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int f = 4 * f4 + i, rr = f & 63;
+        s_w[(f & ~63) + (rr & 15) * 4 + (rr >> 4)] = e[i];
+      }
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int cc = c + h * cpp;
+    if (cc < iwin_w) {
+#pragma unroll
+      for (int r = 0; r < kXRows; ++r)
+        if (r < iwin_h) *reinterpret_cast<float4*>(s_x + (r * iwin_w + cc) * pstr + 4 * q) = xv4[h][r];
+    }
+  }
+  __syncthreads();
+
+  const int ty = tid / TW, tx = tid - (tid / TW) * TW;
+  const int oh = ty0 + ty, ow = tx0 + tx;
+  const bool valid = oh < a.ho && ow < a.wo;
+  float acc[C] = {0.0f, 0.0f, 0.0f, 0.0f};
+  static_assert(NBT % 2 == 0, "blocks alternate between two register sets within a tap");
+  const float* const xpix = s_x + (ty * a.sh * iwin_w + tx * a.sw) * pstr;
+  const float* const wl = s_w + 4 * (lane & 15);
+  const int taps = a.kh * a.kw;
+  // block b of the tap whose input offset is xoff, weights of block t
+  auto load = [&](int xoff, int t, float4 (&xv)[4], float4& wv) {
+    const float* xs = xpix + xoff;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xv[i] = *reinterpret_cast<const float4*>(xs + 4 * i);
+    wv = *reinterpret_cast<const float4*>(wl + 64 * t);
+  };
+  // Taps in order (kh, kw); within a tap NBT blocks of 16 input channels,
+  // each block's reads issued before the previous block's FMAs (two
+  // register sets).  The read after the last block repeats it, so every
+  // iteration issues the same reads and the compiler's LDS wait counts stay
+  // exact.  A lane whose tap lies outside the image restores the
+  // accumulators it had before the tap.
+  float4 xa[4], wa, xb[4], wb;
+  load(0, 0, xa, wa);
+  int kh = 0, kw = 0, xoff = 0;
+  for (int tap = 0; tap < taps; ++tap) {
+    const bool last_tap = tap + 1 == taps;
+    const int nxoff = kw + 1 == a.kw ? xoff + (iwin_w - a.kw + 1) * pstr : xoff + pstr;
+    float keep[C];
+#pragma unroll
+    for (int j = 0; j < C; ++j) keep[j] = acc[j];
+#pragma unroll
+    for (int b = 0; b < NBT; b += 2) {
+      const int t = tap * NBT + b;
+      load(xoff + 16 * (b + 1), t + 1, xb, wb);
+      __builtin_amdgcn_sched_barrier(0);
+      fma16x4_dpp(acc, wa, xa);
+      __builtin_amdgcn_sched_barrier(0);
+      if (b + 2 < NBT)
+        load(xoff + 16 * (b + 2), t + 2, xa, wa);
+      else
+        load(last_tap ? xoff + 16 * (b + 1) : nxoff, last_tap ? t + 1 : t + 2, xa, wa);
+      __builtin_amdgcn_sched_barrier(0);
+      fma16x4_dpp(acc, wb, xb);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    const int ih = oh * a.sh - a.pt + kh, iw = ow * a.sw - a.pl + kw;
+    const bool skip = !(ih >= 0 && ih < a.h && iw >= 0 && iw < a.w);
+#pragma unroll
+    for (int j = 0; j < C; ++j) acc[j] = skip ? keep[j] : acc[j];
+    xoff = nxoff;
+    if (++kw == a.kw) {
+      kw = 0;
+      ++kh;
+    }
+  }
+  if (!valid) return;
+  const size_t p = ((size_t)nn * a.ho + oh) * a.wo + ow;
+  const int OES = a.out_kind == 0 ? 4 : (a.out_kind == 1 ? 2 : 1);
+  dx::store_outputs<C>(a, acc, oc0, (uint8_t*)a.y + (p * a.y_pix_stride + a.y_c_off + oc0) * OES);
 }
 
 // Small-kernel, few-channel case (the 3-channel stem): KH x KW x CIN known
@@ -549,6 +752,38 @@ void launch_direct_conv(hipStream_t st, const DirectArgs& a_in) {
   const int vn = 16 / es;
   const bool vin = a.cin % vn == 0 && (a.x_pix_stride * es) % 16 == 0 && (a.x_c_off * es) % 16 == 0 &&
                    ((uintptr_t)a.x & 15) == 0;
+  // f32 input whose tile window fits LDS, weights packed by channel quads:
+  // the tiled kernel (4 channels per thread, 16 x 16 output pixels per
+  // workgroup)
+  if (a.wq && a.in_kind == 0 && vin && (a.cin == 32 || a.cin == 64) && a.cout % 4 == 0 &&
+      a.kh * a.kw * a.cin <= kTileWRows) {
+    constexpr int TH = 16, TW = 16, C = 4;
+    const int iwin_w = (TW - 1) * a.sw + a.kw, iwin_h = (TH - 1) * a.sh + a.kh;
+    const int pstr = a.cin + 4;
+    const size_t lds = (size_t)iwin_h * iwin_w * pstr;
+    // (the window's channel quads in at most 24 loads per thread)
+    const long long xbytes = (((long long)a.n * a.h * a.w - 1) * a.x_pix_stride + a.x_c_off + a.cin) * 4;
+    const int cpp = TH * TW / (a.cin / 4);  // window columns one pass of the workgroup loads
+    if (lds <= (size_t)kTileLdsFloats && iwin_h <= 24 && iwin_w <= 2 * cpp && xbytes < (1ll << 31)) {
+      const int oes = a.out_kind == 0 ? 4 : (a.out_kind == 1 ? 2 : 1);
+      auto aligned = [&](int v) {
+        return (C * oes) % v == 0 && (a.y_pix_stride * oes) % v == 0 && (a.y_c_off * oes) % v == 0 &&
+               ((uintptr_t)a.y % v) == 0;
+      };
+      a.vec_out = aligned(16) ? 16 : (aligned(4) ? 4 : 1);
+      a.x_bytes = (int)xbytes;
+      const int tiles_w = (a.wo + TW - 1) / TW, tiles_h = (a.ho + TH - 1) / TH;
+      const dim3 grid((unsigned)(a.n * tiles_w * tiles_h), a.cout / C);
+      if (a.cin == 64)
+        hipLaunchKernelGGL((conv_tile_f32_kernel<TH, TW, 4>), grid, dim3(TH * TW), 0, st, a, tiles_w,
+                           tiles_w * tiles_h, iwin_w, pstr);
+      else
+        hipLaunchKernelGGL((conv_tile_f32_kernel<TH, TW, 2>), grid, dim3(TH * TW), 0, st, a, tiles_w,
+                           tiles_w * tiles_h, iwin_w, pstr);
+      DW_HIP(hipGetLastError());
+      return;
+    }
+  }
   // Output channels per thread: the widest chunk of c_out that still gives
   // about four wavefronts per CU (wide chunks pay the input decode once for
   // more FMAs; narrow ones spread small layers over the GPU).
@@ -593,6 +828,26 @@ void launch_direct_conv(hipStream_t st, const DirectArgs& a_in) {
 #undef DW_DC_ALL
 #undef DW_DC
   fail(-2, "direct conv: no kernel for this channel count");
+}
+
+namespace {
+__global__ __launch_bounds__(256) void repack_oc4_kernel(const float* __restrict__ w, float4* __restrict__ wq,
+                                                         int rows, int cout) {
+  const int i = blockIdx.x * 256 + threadIdx.x;  // output float4: (quad, row)
+  const int quads = cout / 4;
+  if (i >= rows * quads) return;
+  const int g = i / rows, r = i - (i / rows) * rows;
+  wq[i] = *reinterpret_cast<const float4*>(w + (size_t)r * cout + 4 * g);
+}
+}  // namespace
+
+void launch_repack_oc4(hipStream_t st, const float* w, float* wq, int rows, int cout) {
+  if (cout % 4 != 0 || ((uintptr_t)w & 15) != 0 || ((uintptr_t)wq & 15) != 0) fail(-2, "repack_oc4: alignment");
+  const long long n = (long long)rows * (cout / 4);
+  if (n == 0) return;
+  hipLaunchKernelGGL(repack_oc4_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, w, (float4*)wq, rows,
+                     cout);
+  DW_HIP(hipGetLastError());
 }
 
 void launch_dwconv(hipStream_t st, const DwArgs& a, int dtype) {

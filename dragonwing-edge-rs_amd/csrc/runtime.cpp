@@ -1357,6 +1357,15 @@ void Runtime::emit_conv(const Group& gr) {
     fail(DW_ERR_UNSUPPORTED, "runtime: conv weight dtype");
   }
   if (!a.wf) a.wf = (const float*)upload(wf.data(), wf.size() * 4);
+  if (a.in_kind == 0 && W.dtype == DW_DTYPE_F32 && ci % 16 == 0 && co % 4 == 0) {
+    // the tiled kernel's layout: [co / 4][kh * kw * ci][4]
+    const size_t rows = (size_t)kh * kw * ci;
+    std::vector<float> wq(wf.size());
+    for (int g4 = 0; g4 < co / 4; ++g4)
+      for (size_t r = 0; r < rows; ++r)
+        for (int j = 0; j < 4; ++j) wq[((size_t)g4 * rows + r) * 4 + j] = wf[r * co + 4 * g4 + j];
+    a.wq = (const float*)upload(wq.data(), wq.size() * 4);
+  }
   if (has_bias) {
     const TensorInfo& B = g.t[op.in[2]];
     if (gr.out_kind == 0) {

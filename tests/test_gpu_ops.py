@@ -100,6 +100,25 @@ def test_conv_f32_wide_channels_bit_exact(backend, shape):
     np.testing.assert_array_equal(got, ref)
 
 
+@pytest.mark.parametrize("shape", [(2, 37, 41, 64, 20, 3, 1, 1), (1, 20, 23, 32, 8, 3, 1, 1),
+                                   (2, 5, 7, 64, 4, 3, 1, 1), (1, 30, 18, 16, 8, 5, 2, 2),
+                                   (1, 56, 56, 64, 64, 3, 2, 1), (2, 17, 16, 48, 12, 3, 1, 0)])
+def test_conv_f32_tiled_bit_exact(backend, shape):
+    # the LDS-tiled kernel (c_in 32 or 64, c_out a multiple of 4, 3x3 at
+    # stride 1): several 16 x 16 tiles per image with ragged last tiles, an
+    # image smaller than one tile, and shapes it does not take (5x5 at
+    # stride 2, c_in 48, stride 2 windows); the tap order and the skipped
+    # out-of-image taps of the reference
+    n, h, w, ci, co, k, s, p = shape
+    rng = np.random.default_rng(sum(shape) + 7)
+    x = rng.uniform(-1, 1, (n, h, w, ci)).astype(np.float32)
+    kk = rng.uniform(-1, 1, (k, k, ci, co)).astype(np.float32)
+    b = rng.uniform(-0.1, 0.1, (co,)).astype(np.float32)
+    got = run_conv_f32(backend, x, kk, b, s, p, ops.ACT_RELU)
+    ref = oracle.relu_f32(oracle.bias_add_f32(oracle.conv2d_f32_nhwc(x, kk, (s, s), (p, p)), b))
+    np.testing.assert_array_equal(got, ref)
+
+
 def test_conv_f32_plain_entry(backend):
     x, k, _ = synth.conv_f32_case(0, c_in=16, c_out=8, h=12, w=12)
     n, h, w, ci = x.shape
