@@ -6,6 +6,7 @@
 #include "dw_common.h"
 #include "dw_device.h"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace dw {
@@ -321,10 +322,14 @@ __global__ __launch_bounds__(256) void maxpool_cascade3_kernel(const PoolArgs a,
 }
 
 // SPPF cascade for planes that fit in LDS: one workgroup owns one image and
-// one 16-byte channel slice (16 u8 / 8 f16 / 4 f32 channels), keeps the
-// whole H x W plane in LDS and runs the three k x k pools as separable row
-// and column maxima, writing each result to its output view.  Max is exact,
-// so the order of comparisons does not change any value.
+// one 16-byte channel slice (16 u8 / 8 f16 / 4 f32 channels) and keeps the
+// whole H x W plane in LDS.  The cascade of three k x k pools (stride 1,
+// pad k/2) equals single pools of sizes k, 2k - 1 and 3k - 2, each the
+// separable row-then-column maximum, so one pass computes the three row
+// maxima of every pixel from one read of its 3k - 2 row neighbours, and a
+// second pass the three column maxima, which are the three outputs: two
+// barriers for the whole cascade.  Max is exact, so the order of the
+// comparisons does not change any value.
 typedef unsigned char u8x16 __attribute__((ext_vector_type(16)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
@@ -343,43 +348,58 @@ __device__ __forceinline__ uint4 vmax16(uint4 a, uint4 b) {
   }
 }
 
+// plane: hw pixels of the input, then three planes of row maxima (radius
+// r, 2r, 3r); 4 * hw * 16 bytes of LDS
 template <int ES>
-__global__ __launch_bounds__(256) void sppf_lds_kernel(const PoolArgs a, View y2, View y3) {
+__global__ __launch_bounds__(512) void sppf_lds_kernel(const PoolArgs a, View y2, View y3) {
   extern __shared__ uint4 plane[];
   const int hw = a.h * a.w;
-  uint4* A = plane;       // current plane
-  uint4* B = plane + hw;  // row maxima
+  uint4* const X = plane;
+  uint4* const R1 = plane + hw;
+  uint4* const R2 = plane + 2 * hw;
+  uint4* const R3 = plane + 3 * hw;
   const int nn = blockIdx.x;
   const int c0 = blockIdx.y * (16 / ES);
   const int r = a.kh / 2;
   auto gaddr = [&](const View& v, int pix) {
     return (uint8_t*)v.base + ((size_t)(nn * hw + pix) * v.pix_stride + v.c_off + c0) * ES;
   };
-  for (int i = threadIdx.x; i < hw; i += blockDim.x) A[i] = *reinterpret_cast<const uint4*>(gaddr(a.x, i));
+  for (int i = threadIdx.x; i < hw; i += blockDim.x) X[i] = *reinterpret_cast<const uint4*>(gaddr(a.x, i));
   __syncthreads();
-  const View outs[3] = {a.y, y2, y3};
-  for (int stage = 0; stage < 3; ++stage) {
-    for (int i = threadIdx.x; i < hw; i += blockDim.x) {
-      const int y = i / a.w, x = i - (i / a.w) * a.w;
-      uint4 m = A[i];
-      for (int d = 1; d <= r; ++d) {
-        if (x - d >= 0) m = vmax16<ES>(m, A[y * a.w + x - d]);
-        if (x + d < a.w) m = vmax16<ES>(m, A[y * a.w + x + d]);
-      }
-      B[i] = m;
+  // row maxima over |dx| <= r, 2r, 3r (columns outside the image never win)
+  for (int i = threadIdx.x; i < hw; i += blockDim.x) {
+    const int y = i / a.w, x = i - (i / a.w) * a.w;
+    const uint4* row = X + y * a.w;
+    uint4 m = row[x];
+    for (int d = 1; d <= 3 * r; ++d) {
+      if (x - d >= 0) m = vmax16<ES>(m, row[x - d]);
+      if (x + d < a.w) m = vmax16<ES>(m, row[x + d]);
+      if (d == r) R1[i] = m;
+      if (d == 2 * r) R2[i] = m;
     }
-    __syncthreads();
-    for (int i = threadIdx.x; i < hw; i += blockDim.x) {
-      const int y = i / a.w, x = i - (i / a.w) * a.w;
-      uint4 m = B[i];
-      for (int d = 1; d <= r; ++d) {
-        if (y - d >= 0) m = vmax16<ES>(m, B[(y - d) * a.w + x]);
-        if (y + d < a.h) m = vmax16<ES>(m, B[(y + d) * a.w + x]);
+    R3[i] = m;
+  }
+  __syncthreads();
+  // column maxima of the three row-maximum planes: the three outputs
+  for (int i = threadIdx.x; i < hw; i += blockDim.x) {
+    const int y = i / a.w, x = i - (i / a.w) * a.w;
+    uint4 m1 = R1[i], m2 = R2[i], m3 = R3[i];
+    for (int d = 1; d <= 3 * r; ++d) {
+      const bool up = y - d >= 0, dn = y + d < a.h;
+      if (d <= r) {
+        if (up) m1 = vmax16<ES>(m1, R1[i - d * a.w]);
+        if (dn) m1 = vmax16<ES>(m1, R1[i + d * a.w]);
       }
-      A[i] = m;
-      *reinterpret_cast<uint4*>(gaddr(outs[stage], i)) = m;
+      if (d <= 2 * r) {
+        if (up) m2 = vmax16<ES>(m2, R2[i - d * a.w]);
+        if (dn) m2 = vmax16<ES>(m2, R2[i + d * a.w]);
+      }
+      if (up) m3 = vmax16<ES>(m3, R3[i - d * a.w]);
+      if (dn) m3 = vmax16<ES>(m3, R3[i + d * a.w]);
     }
-    __syncthreads();
+    *reinterpret_cast<uint4*>(gaddr(a.y, i)) = m1;
+    *reinterpret_cast<uint4*>(gaddr(y2, i)) = m2;
+    *reinterpret_cast<uint4*>(gaddr(y3, i)) = m3;
   }
 }
 
@@ -522,11 +542,13 @@ void launch_maxpool_cascade3(hipStream_t st, const PoolArgs& a, View y2, View y3
   const size_t total = (size_t)a.n * a.h * a.w * a.c;
   if (total == 0) return;
   const int es = dtype_size(dtype);
-  const size_t lds = (size_t)2 * a.h * a.w * 16;
+  const size_t lds = (size_t)4 * a.h * a.w * 16;
   auto al16 = [&](const View& v) { return (v.pix_stride * es) % 16 == 0 && (v.c_off * es) % 16 == 0; };
   if ((a.c * es) % 16 == 0 && lds <= 65536 && al16(a.x) && al16(a.y) && al16(y2) && al16(y3) &&
       (dtype == U8 || dtype == F16 || dtype == F32)) {
-    const dim3 g(a.n, a.c * es / 16), b(256);
+    // one thread per pixel up to 512 pixels
+    const int threads = std::min(512, ((a.h * a.w + 63) / 64) * 64);
+    const dim3 g(a.n, a.c * es / 16), b(threads);
     if (es == 1)
       hipLaunchKernelGGL(sppf_lds_kernel<1>, g, b, lds, st, a, y2, y3);
     else if (es == 2)
