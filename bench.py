@@ -458,6 +458,8 @@ def main():
         "gpu_ms_sum_of_launches": round(float(ms.sum()), 4),
         "setup_s": round(t_setup, 1),
     }
+    arena, unshared = rts[0].activation_bytes()
+    line["activation_bytes"] = {"arena": arena, "without_reuse": unshared}
     if not args.no_traffic:
         try:
             fetch, write, scales = measure_traffic(wl, launches)

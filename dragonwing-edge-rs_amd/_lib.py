@@ -145,6 +145,7 @@ SIGNATURES = {
     "dw_hip_graph_get_output_f32": (I, [P, S, P, Z]),
     "dw_hip_graph_get_output_bytes": (I, [P, S, P, Z]),
     "dw_hip_graph_tensor_bytes": (I, [P, S, C.POINTER(Z)]),
+    "dw_hip_graph_activation_bytes": (I, [P, C.POINTER(Z), C.POINTER(Z)]),
     "dw_hip_graph_enable_capture": (I, [P, I]),
     "dw_hip_graph_num_launches": (I, [P]),
     "dw_hip_graph_launch_info": (S, [P, I]),

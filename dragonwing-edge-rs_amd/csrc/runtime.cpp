@@ -46,6 +46,8 @@ struct RtTensor {
   void* base = nullptr;
   int pix_stride = 0;
   int abs_off = 0;
+  int rid = -1;                   // storage root (index), set by allocate()
+  uintptr_t ra0 = 0, ra1 = 0;     // the root's bytes in the activation arena
   float scale = 1.0f;
   int zp = 0;
   int64_t pixels() const { return n * h * w; }
@@ -53,12 +55,17 @@ struct RtTensor {
   size_t bytes() const { return (size_t)(n * h * w * c) * dtype_size(dtype); }
 };
 
-// Channels [lo, hi) of every pixel of the storage root at `base`: what a
-// launch reads or writes (every activation is a channel slice of a root).
+// Channels [lo, hi) of every pixel of storage root `rid`, which occupies
+// bytes [a0, a1): what a launch reads or writes (every activation is a
+// channel slice of a root).  Roots whose lifetimes do not overlap may share
+// bytes, so two regions of different roots overlap when their bytes do.
 struct Region {
-  const void* base;
+  int rid;
   int lo, hi;
-  bool overlaps(const Region& o) const { return base == o.base && lo < o.hi && o.lo < hi; }
+  uintptr_t a0, a1;
+  bool overlaps(const Region& o) const {
+    return rid == o.rid ? (lo < o.hi && o.lo < hi) : (a0 < o.a1 && o.a0 < a1);
+  }
 };
 
 struct Launch {
@@ -108,6 +115,8 @@ struct Runtime {
   GraphIR g;
   std::map<std::string, RtTensor> ts;
   std::vector<void*> allocs;
+  size_t act_bytes = 0;           // the activation arena
+  size_t act_bytes_unshared = 0;  // what the roots would take without reuse
   std::vector<Launch> launches;
   std::vector<std::string> info;
   bool capture = false;
@@ -176,7 +185,7 @@ struct Runtime {
   void build(Backend* b, const GraphIR& graph, bool stats_mode);
   void lower(std::vector<Group>& groups);
   void place(const std::vector<Group>& groups);
-  void allocate();
+  void allocate(const std::vector<Group>& groups);
   void emit(const Group& gr);
   void emit_conv(const Group& gr);
   void emit_qconv(const Group& gr);
@@ -326,7 +335,7 @@ void Runtime::build(Backend* b, const GraphIR& graph, bool stats_mode) {
   std::vector<Group> groups;
   lower(groups);
   place(groups);
-  allocate();
+  allocate(groups);
   if (stats) {
     for (auto& kv : ts)
       if (kv.second.rank4 && !g.t[kv.first].is_init && kv.second.dtype == F32) stats_names.push_back(kv.first);
@@ -422,7 +431,7 @@ void Runtime::tag_group(const Group& gr, size_t first, int gid) {
     if (it == ts.end() || g.t[name].is_init) return;
     const RtTensor& r = it->second;
     if (!r.rank4 || !r.base) return;
-    v.push_back({r.base, r.abs_off, r.abs_off + (int)r.c});
+    v.push_back({r.rid, r.abs_off, r.abs_off + (int)r.c, r.ra0, r.ra1});
   };
   for (int oi : gr.ops) {
     for (auto& n : g.ops[oi].in) add(rd, n);
@@ -904,40 +913,163 @@ void Runtime::place(const std::vector<Group>& groups) {
   }
 }
 
-void Runtime::allocate() {
+// Activation storage.  Every storage root (a materialized tensor without a
+// parent, or a concat buffer its inputs are placed in) is touched by a set
+// of groups; graph inputs and outputs are kept apart.  Roots are placed in
+// one arena, largest first, each at the lowest 256-byte-aligned offset that
+// no placed root it may not share with occupies (the liveness reuse of the
+// reference's slab allocator, slab.rs:228-367).  Two roots share only when
+// the data dependencies already order every use of one before every use of
+// the other, so independent branches (the detect heads) keep running
+// concurrently.  The stream schedule orders launches by the bytes they
+// touch (Region) in any case.  DW_ACT_REUSE=0 gives every root its own
+// bytes.
+void Runtime::allocate(const std::vector<Group>& groups) {
+  auto root_of = [&](std::string t) {
+    while (!T(t).parent.empty()) t = T(t).parent;
+    return t;
+  };
+  auto is_io = [&](const std::string& n) {
+    return g.is_output(n) || std::find(g.inputs.begin(), g.inputs.end(), n) != g.inputs.end();
+  };
   // roots that need storage: graph inputs, outputs and every materialized
-  // tensor without a parent.  A placed tensor is materialized inside its
-  // root.
+  // tensor without a parent, and the roots of placed tensors
+  std::vector<std::string> roots;
+  std::map<std::string, int> rid;
+  auto add_root = [&](const std::string& r) {
+    if (rid.count(r)) return;
+    rid[r] = (int)roots.size();
+    roots.push_back(r);
+  };
   for (auto& kv : ts) {
-    RtTensor& r = kv.second;
+    const RtTensor& r = kv.second;
     if (!r.rank4 || g.t[kv.first].is_init) continue;
-    if (!r.parent.empty()) continue;
-    const bool needed = r.materialized || g.is_output(kv.first) ||
-                        std::find(g.inputs.begin(), g.inputs.end(), kv.first) != g.inputs.end();
-    if (!needed) continue;
-    // a root whose only users are fused-away intermediates still gets
-    // storage if any placed child is materialized
-    r.base = dalloc(r.bytes());
+    if (!r.parent.empty()) {
+      add_root(root_of(kv.first));
+      continue;
+    }
+    if (r.materialized || is_io(kv.first)) add_root(kv.first);
+  }
+  // the groups touching each root, and each group's storage as (root,
+  // channels) regions, read and written
+  auto root_off = [&](std::string t, int& o) {
+    o = 0;
+    while (!T(t).parent.empty()) {
+      o += T(t).c_off;
+      t = T(t).parent;
+    }
+    return t;
+  };
+  const int ng = (int)groups.size();
+  std::vector<std::vector<int>> touch(roots.size());
+  std::vector<std::vector<Region>> grd(ng), gwr(ng);
+  for (int gi = 0; gi < ng; ++gi)
+    for (int oi : groups[gi].ops) {
+      const OpNode& op = g.ops[oi];
+      for (int w = 0; w < 2; ++w)
+        for (const auto& n : w ? op.out : op.in) {
+          auto it = ts.find(n);
+          if (it == ts.end() || !it->second.rank4 || g.t[n].is_init) continue;
+          int o = 0;
+          auto r = rid.find(root_off(n, o));
+          if (r == rid.end()) continue;
+          auto& tv = touch[r->second];
+          if (tv.empty() || tv.back() != gi) tv.push_back(gi);
+          (w ? gwr : grd)[gi].push_back({r->second, o, o + (int)it->second.c, 0, 0});
+        }
+    }
+  // ancestors of each group along data dependencies (one group writes
+  // storage the other reads or writes): the order every stream schedule
+  // keeps whatever the placement
+  std::vector<std::vector<char>> anc(ng, std::vector<char>(ng, 0));
+  auto dep = [&](int i, int j) {
+    for (const Region& w : gwr[i]) {
+      for (const Region& r : grd[j]) if (w.overlaps(r)) return true;
+      for (const Region& r : gwr[j]) if (w.overlaps(r)) return true;
+    }
+    for (const Region& r : grd[i])
+      for (const Region& w : gwr[j]) if (r.overlaps(w)) return true;
+    return false;
+  };
+  for (int j = 0; j < ng; ++j)
+    for (int i = 0; i < j; ++i)
+      if (!anc[j][i] && dep(i, j)) {
+        anc[j][i] = 1;
+        for (int k = 0; k < i; ++k) anc[j][k] |= anc[i][k];
+      }
+  bool reuse = true;
+  if (const char* e = getenv("DW_ACT_REUSE")) reuse = atoi(e) != 0;
+  std::vector<char> pinned(roots.size(), 0);
+  for (size_t i = 0; i < roots.size(); ++i) {
+    pinned[i] = !reuse || touch[i].empty() || is_io(roots[i]);
+    for (auto& kv : ts)  // a root holding a graph input or output
+      if (!pinned[i] && kv.second.rank4 && is_io(kv.first) && !kv.second.parent.empty() &&
+          root_of(kv.first) == roots[i])
+        pinned[i] = 1;
+  }
+  // Two roots may share bytes when every group touching one is an ancestor
+  // of every group touching the other: the data dependencies then already
+  // order all uses of the first before any use of the second, so sharing
+  // adds no wait to the stream schedule.
+  auto before = [&](int a, int b) {
+    for (int gb : touch[b])
+      for (int ga : touch[a])
+        if (ga >= gb || !anc[gb][ga]) return false;
+    return true;
+  };
+  auto conflict = [&](int a, int b) { return pinned[a] || pinned[b] || !(before(a, b) || before(b, a)); };
+  auto align = [](size_t v) { return (v + 255) & ~(size_t)255; };
+  std::vector<size_t> size(roots.size()), off(roots.size(), 0);
+  for (size_t i = 0; i < roots.size(); ++i) size[i] = align(std::max<size_t>(T(roots[i]).bytes(), 256));
+  std::vector<int> order(roots.size());
+  for (size_t i = 0; i < order.size(); ++i) order[i] = (int)i;
+  std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return size[a] > size[b]; });
+  std::vector<int> placed;
+  size_t total = 0;
+  for (int i : order) {
+    // occupied byte ranges of the placed roots it may not share with
+    std::vector<std::pair<size_t, size_t>> busy;
+    for (int j : placed)
+      if (conflict(i, j)) busy.push_back({off[j], off[j] + size[j]});
+    std::sort(busy.begin(), busy.end());
+    size_t o = 0;
+    for (auto& b : busy) {
+      if (o + size[i] <= b.first) break;
+      o = std::max(o, b.second);
+    }
+    off[i] = o;
+    placed.push_back(i);
+    total = std::max(total, o + size[i]);
+  }
+  uint8_t* arena = (uint8_t*)dalloc(total);
+  act_bytes = total;
+  act_bytes_unshared = 0;
+  for (size_t i = 0; i < roots.size(); ++i) {
+    act_bytes_unshared += size[i];
+    RtTensor& r = T(roots[i]);
+    r.base = arena + off[i];
     r.pix_stride = (int)r.c;
     r.abs_off = 0;
+    r.rid = (int)i;
+    r.ra0 = (uintptr_t)r.base;
+    r.ra1 = r.ra0 + size[i];
   }
   for (auto& kv : ts) {
     RtTensor& r = kv.second;
     if (r.parent.empty()) continue;
-    int off = 0;
+    int o = 0;
     std::string t = kv.first;
     while (!T(t).parent.empty()) {
-      off += T(t).c_off;
+      o += T(t).c_off;
       t = T(t).parent;
     }
-    RtTensor& root = T(t);
-    if (!root.base) {
-      root.base = dalloc(root.bytes());
-      root.pix_stride = (int)root.c;
-    }
+    const RtTensor& root = T(t);
     r.base = root.base;
     r.pix_stride = root.pix_stride;
-    r.abs_off = off;
+    r.abs_off = o;
+    r.rid = root.rid;
+    r.ra0 = root.ra0;
+    r.ra1 = root.ra1;
   }
 }
 
@@ -1633,7 +1765,7 @@ void Runtime::set_input_nchw(const std::string& name, const void* src) {
     int found = -1, count = 0;
     for (size_t k = 0; k < launches.size(); ++k)
       for (const Region& r : launches[k].reads)
-        if (r.base == t.base) {
+        if (r.rid == t.rid) {
           ++count;
           found = (int)k;
           break;
@@ -1865,6 +1997,14 @@ int dw_hip_graph_run_unbatched(dw_hip_graph_runtime* rth) {
       dw::fail(e.code, "launch[" + std::to_string(i) + "] " + L.kernel + " (" + L.op + ") failed: " + e.msg);
     }
   }
+  API_END
+}
+
+int dw_hip_graph_activation_bytes(dw_hip_graph_runtime* rth, size_t* arena, size_t* unshared) {
+  API_BEGIN
+  if (!rth) dw::fail(DW_ERR_INVALID, "null graph runtime");
+  if (arena) *arena = rth->rt.act_bytes;
+  if (unshared) *unshared = rth->rt.act_bytes_unshared;
   API_END
 }
 

@@ -258,6 +258,14 @@ class HipGraphRuntime:
         check(load().dw_hip_graph_tensor_bytes(self._h, name.encode(), C.byref(n)))
         return n.value
 
+    def activation_bytes(self) -> tuple[int, int]:
+        """(arena bytes, bytes without reuse): the activation arena, in which
+        storage whose lifetimes do not overlap shares bytes, and what the
+        same storage takes with no sharing (the reference's SlabStats)."""
+        a, u = C.c_size_t(), C.c_size_t()
+        check(load().dw_hip_graph_activation_bytes(self._h, C.byref(a), C.byref(u)))
+        return a.value, u.value
+
     def get_output_bytes(self, name: str) -> np.ndarray:
         out = np.empty(self.tensor_bytes(name), np.uint8)
         check(load().dw_hip_graph_get_output_bytes(self._h, name.encode(), out.ctypes.data, out.nbytes))

@@ -551,6 +551,11 @@ int dw_hip_graph_tensor_shape(dw_hip_graph_runtime* rt, const char* name, int64_
 int dw_hip_graph_get_output_f32(dw_hip_graph_runtime* rt, const char* name, float* data, size_t count);
 /* get_output_bytes (vulkan_runtime.rs:2131): synchronizes, raw bytes. */
 int dw_hip_graph_get_output_bytes(dw_hip_graph_runtime* rt, const char* name, void* data, size_t len);
+/* Activation memory (SlabStats, crates/dragonwing-vulkan/src/slab.rs:349-367):
+ * the bytes of the runtime's activation arena, where storage roots whose
+ * lifetimes do not overlap share bytes, and what the same roots would take
+ * each in its own allocation.  Either pointer may be null. */
+int dw_hip_graph_activation_bytes(dw_hip_graph_runtime* rt, size_t* arena, size_t* unshared);
 /* Byte size of a graph tensor as the runtime stores it. */
 int dw_hip_graph_tensor_bytes(dw_hip_graph_runtime* rt, const char* name, size_t* len);
 /* Capture the launch list into a HIP graph and replay it on later runs

@@ -244,6 +244,37 @@ def test_int8_graph_streams_match_one_stream(backend, int8_small, monkeypatch):
             backend.synchronize()
 
 
+def test_activation_reuse_matches_unshared_storage(backend, int8_small, monkeypatch):
+    # Storage whose lifetimes do not overlap shares the activation arena;
+    # on four streams (independent detect-head branches run concurrently,
+    # so reused bytes must wait for their last readers) and captured, the
+    # outputs equal those of a runtime where every tensor has its own bytes.
+    g, info = int8_small
+    x = yolo.input_images(2, 96)
+    monkeypatch.setenv("DW_ACT_REUSE", "0")
+    ref_rt = HipGraphRuntime(g, backend)
+    monkeypatch.setenv("DW_ACT_REUSE", "1")
+    monkeypatch.setenv("DW_GRAPH_STREAMS", "4")
+    rt = HipGraphRuntime(g, backend)
+    arena, unshared = rt.activation_bytes()
+    ref_arena, ref_unshared = ref_rt.activation_bytes()
+    assert ref_arena == ref_unshared == unshared
+    assert arena < 0.6 * unshared, (arena, unshared)
+    ref_rt.set_input_f32(info["input"], x)
+    ref_rt.run()
+    ref = gpu_outputs(ref_rt, info)
+    for capture in (False, True):
+        rt.enable_capture(capture)
+        for i in range(3):
+            rt.set_input_f32(info["input"], x if i % 2 == 0 else np.zeros_like(x))
+            rt.run()
+            outs = gpu_outputs(rt, info)
+            if i % 2 == 0:
+                for a, b in zip(outs, ref):
+                    np.testing.assert_array_equal(a, b)
+            backend.synchronize()
+
+
 def test_run_unbatched_and_io(backend, int8_small, monkeypatch):
     g, info = int8_small
     rt = HipGraphRuntime(g, backend)
