@@ -122,6 +122,8 @@ struct DirectArgs {
   int out_plain;           // 1: rint(x * out_rcp) == rint(x / out_scale) for every finite f16 x
   const float* wq;         // optional (f32 input, c_in % 16 == 0, c_out % 4 == 0): the weights as
                            // [c_out / 4][kh * kw * c_in][4], for the tiled kernel
+  const float* wq16;       // optional (1x1, c_out % 16 == 0): the weights as [c_out / 16][c_in][16],
+                           // for the 1x1 kernel's 16-channel groups
 };
 
 // Depthwise convolution (channel multiplier 1).

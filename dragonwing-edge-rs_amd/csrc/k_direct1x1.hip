@@ -46,14 +46,19 @@ __device__ __forceinline__ float decode_x(const DirectArgs& a, const uint4& u, i
   }
 }
 
-template <int IN_KIND, int C, int P, bool NOSUB>
+// PK: the weights come from a.wq16 ([c_out / 16][c_in][16], C = 16), so the
+// rows of one group are consecutive 64-byte lines and a block's 16 scalar
+// loads take immediate offsets from one base: no address arithmetic per row.
+template <int IN_KIND, int C, int P, bool NOSUB, bool PK>
 __global__ __launch_bounds__(64) void conv1x1_exact_kernel(const DirectArgs a) {
+  static_assert(!PK || C == 16, "packed rows hold 16 channels");
   constexpr int ES = IN_KIND == 0 ? 4 : (IN_KIND == 1 ? 2 : 1);
   constexpr int VN = dx::vec_elems<IN_KIND>();
-  const int K = a.cin, cout = a.cout;
+  const int K = a.cin;
   const int oc0 = blockIdx.y * C;
   const int lane = threadIdx.x;
-  const wrow_t wbase = (wrow_t)(a.wf + oc0);
+  const int wstride = PK ? C : a.cout;  // floats between consecutive weight rows
+  const wrow_t wbase = PK ? (wrow_t)(a.wq16 + (size_t)blockIdx.y * K * C) : (wrow_t)(a.wf + oc0);
   // u8 -> f32 of the f16 dequantized value, (q - zp) * scale rounded to f16
   __shared__ float s_deq[IN_KIND == 2 && NOSUB ? 256 : 1];
   if constexpr (IN_KIND == 2 && NOSUB) {
@@ -93,7 +98,8 @@ __global__ __launch_bounds__(64) void conv1x1_exact_kernel(const DirectArgs a) {
   uint4 cur[P], nxt[P];
 #pragma unroll
   for (int j = 0; j < P; ++j) cur[j] = *reinterpret_cast<const uint4*>(xp[j]);
-  for (int k0 = 0; k0 < K; k0 += VN) {
+  wrow_t wk = wbase;  // weight row k0
+  for (int k0 = 0; k0 < K; k0 += VN, wk += (size_t)VN * wstride) {
     // prefetch the next vector (the last iteration reloads the first one)
     const int kn = k0 + VN < K ? k0 + VN : 0;
 #pragma unroll
@@ -103,7 +109,7 @@ __global__ __launch_bounds__(64) void conv1x1_exact_kernel(const DirectArgs a) {
       float xv[P];
 #pragma unroll
       for (int j = 0; j < P; ++j) xv[j] = decode_x<IN_KIND, NOSUB>(a, cur[j], e, s_deq);
-      const wrow_t wr = wbase + (size_t)(k0 + e) * cout;
+      const wrow_t wr = PK ? wk + e * C : wk + (size_t)e * wstride;
 #pragma unroll
       for (int c = 0; c < C; ++c) {
         const float wv = wr[c];
@@ -179,9 +185,13 @@ bool launch_conv1x1_exact(hipStream_t st, const DirectArgs& a_in) {
   };
   a.vec_out = aligned(16) ? 16 : (aligned(4) ? 4 : 1);
   const dim3 grid((a.m + 64 * best.p - 1) / (64 * best.p), a.cout / best.c);
+  const bool pk = best.c == 16 && a.wq16 != nullptr;
 #define DW_K(KIND, CC, PP, NS)                                                                    \
   if (a.in_kind == KIND && best.c == CC && best.p == PP && nosub == NS) {                           \
-    hipLaunchKernelGGL((conv1x1_exact_kernel<KIND, CC, PP, NS>), grid, dim3(64), 0, st, a);         \
+    if (CC == 16 && pk)                                                                             \
+      hipLaunchKernelGGL((conv1x1_exact_kernel<KIND, CC, PP, NS, CC == 16>), grid, dim3(64), 0, st, a); \
+    else                                                                                            \
+      hipLaunchKernelGGL((conv1x1_exact_kernel<KIND, CC, PP, NS, false>), grid, dim3(64), 0, st, a); \
     DW_HIP(hipGetLastError());                                                                      \
     return true;                                                                                    \
   }

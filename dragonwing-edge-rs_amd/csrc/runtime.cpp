@@ -1489,6 +1489,20 @@ void Runtime::emit_conv(const Group& gr) {
     fail(DW_ERR_UNSUPPORTED, "runtime: conv weight dtype");
   }
   if (!a.wf) a.wf = (const float*)upload(wf.data(), wf.size() * 4);
+  if (kh == 1 && kw == 1 && co % 16 == 0 && (W.dtype == DW_DTYPE_F32 || W.dtype == DW_DTYPE_F16)) {
+    // the 1x1 kernel's layout: [co / 16][ci][16] (each 16-channel group's
+    // weight rows contiguous)
+    std::vector<float> w(W.numel());
+    if (W.dtype == DW_DTYPE_F32)
+      memcpy(w.data(), W.data.data(), w.size() * 4);
+    else
+      for (size_t i = 0; i < w.size(); ++i) w[i] = f16_to_f32_ref(((const uint16_t*)W.data.data())[i]);
+    std::vector<float> wq(w.size());
+    for (int g16 = 0; g16 < co / 16; ++g16)
+      for (int r = 0; r < ci; ++r)
+        for (int j = 0; j < 16; ++j) wq[((size_t)g16 * ci + r) * 16 + j] = w[(size_t)r * co + 16 * g16 + j];
+    a.wq16 = (const float*)upload(wq.data(), wq.size() * 4);
+  }
   if (a.in_kind == 0 && W.dtype == DW_DTYPE_F32 && ci % 16 == 0 && co % 4 == 0) {
     // the tiled kernel's layout: [co / 4][kh * kw * ci][4]
     const size_t rows = (size_t)kh * kw * ci;
