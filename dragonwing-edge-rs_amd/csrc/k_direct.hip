@@ -432,7 +432,7 @@ __global__ __launch_bounds__(256) void conv_small_kernel(const DirectArgs a) {
 // is the correctly rounded f16 sum (f32 holds 2 * 11 + 2 bits), so two
 // channels are added by one packed f16 add, unless the rounded sum or the
 // bias is an f16 subnormal (decoded at half value by the reference): then
-// the output takes the scalar decoding path.  SiLU: silu_f16_pk (fp16
+// the output takes the scalar decoding path.  SiLU: silu_f16_pk_lite (fp16
 // tolerance).  The buffer offsets are 32-bit: x spans at most 2^30 bytes,
 // so an offset plus BAD (2^30) is always past the buffer's x_bytes records.
 template <int SW, int SEG, int ROWS, bool WPLAIN, bool BIAS, int ACT>
@@ -595,8 +595,8 @@ __global__ __launch_bounds__(256) void dwconv3_f16_kernel(const DwArgs a, int se
         }
       }
       if constexpr (ACT == ACT_SILU) {
-        p01 = silu_f16_pk(p01);
-        p23 = silu_f16_pk(p23);
+        p01 = silu_f16_pk_lite(p01);
+        p23 = silu_f16_pk_lite(p23);
       } else if constexpr (ACT == ACT_RELU) {
         uint16_t hb[CPT] = {pk_lo(p01), pk_hi(p01), pk_lo(p23), pk_hi(p23)};
 #pragma unroll
