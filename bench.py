@@ -56,6 +56,33 @@ def kernel_bound(kernel: str):
     return PEAKS["hbm"]
 
 
+def conv_rooflines(launches, ms):
+    """Each conv launch against its roofline: the larger of its algorithmic
+    work at the dense peak of its arithmetic and its algorithmic bytes at
+    8 TB/s is the floor; the fraction is floor / measured time.  Returns the
+    per-launch rows and a summary (median, and floor sum / time sum)."""
+    rows = []
+    for L, t in zip(launches, ms):
+        k = L["kernel"]
+        if not (k.startswith("igemm") or k.startswith("direct_conv") or k.startswith("dwconv")):
+            continue
+        bound, peak, unit = kernel_bound(k)
+        t_mfma = L["work"] / (peak * 1e12) if bound == "mfma" else 0.0
+        t_hbm = L["bytes"] / (PEAKS["hbm"][1] * 1e9)
+        floor = max(t_mfma, t_hbm)
+        secs = float(t) * 1e-3
+        rows.append({"op": L["ops"].split("+")[0], "kernel": k, "us": round(secs * 1e6, 2),
+                     "floor_us": round(floor * 1e6, 2), "bound": "mfma" if t_mfma >= t_hbm else "hbm",
+                     "frac": round(floor / secs, 4) if secs > 0 else None})
+    if not rows:
+        return rows, None
+    fr = sorted(r["frac"] for r in rows)
+    summary = {"launches": len(rows), "median_frac": fr[len(fr) // 2],
+               "floor_over_time": round(sum(r["floor_us"] for r in rows) / sum(r["us"] for r in rows), 4),
+               "note": "per conv launch: max(work at the dense peak of its arithmetic, bytes at 8 TB/s) / time"}
+    return rows, summary
+
+
 def cpu_threads() -> int:
     try:
         return len(os.sched_getaffinity(0))
@@ -458,6 +485,12 @@ def main():
         "gpu_ms_sum_of_launches": round(float(ms.sum()), 4),
         "setup_s": round(t_setup, 1),
     }
+    conv_rows, conv_summary = conv_rooflines(launches, ms)
+    if conv_summary:
+        line["convs"] = conv_summary
+    if args.dump_launches:
+        with open(args.dump_launches + ".convs.json", "w") as f:
+            json.dump(conv_rows, f, indent=0)
     arena, unshared = rts[0].activation_bytes()
     line["activation_bytes"] = {"arena": arena, "without_reuse": unshared}
     if not args.no_traffic:
