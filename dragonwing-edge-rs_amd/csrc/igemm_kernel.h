@@ -116,7 +116,7 @@ struct EpiLds {
 // f16, then the bias pass, the activation and the residual add, each on
 // stored f16.  The MFMA sums already differ from the reference's order, so
 // these results are held to the fp16 tolerance, and the store runs the
-// chain two channels at a time in packed f16 (IEEE operands, silu_f16_pk).
+// chain two channels at a time in packed f16 (IEEE operands, silu_f16_pk_lite).
 
 // QLinearConv requantization of one accumulator (bias' already added):
 // rint(acc * M) + y_zp, saturated to [0, 255] (ONNX QLinearConv, RNE).
@@ -198,8 +198,8 @@ __device__ __forceinline__ void epilogue4(const IgemmArgs& a, const EpiLds& e, c
       p23 = p23 + pk_make(e.bias_h[cl + 2], e.bias_h[cl + 3]);
     }
     if (a.act == ACT_SILU) {
-      p01 = silu_f16_pk(p01);
-      p23 = silu_f16_pk(p23);
+      p01 = silu_f16_pk_lite(p01);
+      p23 = silu_f16_pk_lite(p23);
     } else if (a.act != ACT_NONE) {
       p01 = pk_make(f16_act_bits(pk_lo(p01), a.act), f16_act_bits(pk_hi(p01), a.act));
       p23 = pk_make(f16_act_bits(pk_lo(p23), a.act), f16_act_bits(pk_hi(p23), a.act));
