@@ -1,6 +1,6 @@
-// Implicit-GEMM 3x3 convolution (stride 1, padding 1, int8) over whole
-// output rows, with the input rows staged in LDS: the variant for the large
-// feature maps.
+// Implicit-GEMM 3x3 convolution (stride 1, padding 1, int8 or fp16) over
+// whole output rows, with the input rows staged in LDS: the variant for the
+// large feature maps.
 //
 // igemm_kernel loads every im2col row from the input view, so each input
 // pixel passes the vector-memory path 9 times (once per tap), 16 pixels x
@@ -8,16 +8,19 @@
 // large 3x3 layers.  Here a workgroup owns NPIX = 320 output pixels, which
 // are R = 320 / W whole rows of one image, and BC output channels.  It loads
 // the R + 2 input rows its taps touch (with the one-pixel halo, padding
-// included) into LDS once, as whole 16-byte units of consecutive channels,
-// converted to the MFMA operand there (u8 xor 0x80, or the padding pattern),
+// included) into LDS once, as whole 16-byte units of consecutive channels
+// (16 u8 or 8 f16), converted to the MFMA operand there (int8: u8 xor 0x80,
+// or the padding pattern; fp16: as they are, padding +0),
 // together with all of K's weights; the k-loop then reads both operands
 // from LDS and issues no global load.
 //
 // LDS layout of the input tile: tile pixel (tr, tc) (tr in [0, R + 2), tc
 // in [0, W + 2), tile pixel (0, 0) = image pixel (r0 - 1, -1)) holds its
-// c_in / 16 units at ((tr * (W + 2) + tc) * SU + u) * 16, with SU = c_in / 16
-// made odd: the 8 lanes that one LDS cycle serves (8 consecutive pixels, one
-// unit each) then fall in 8 distinct 16-byte bank groups.
+// CU = c_in * esize / 16 units at ((tr * (W + 2) + tc) * SU + u) * 16, with
+// SU = CU made odd: the 8 lanes that one LDS cycle serves (8 consecutive
+// pixels, one unit each) then fall in 8 distinct 16-byte bank groups.
+// A k-step is 64 bytes of K either way (v_mfma_i32_16x16x64_i8 or
+// v_mfma_f32_16x16x32_f16), so the same tables serve both element sizes.
 //
 // Work split: wave w owns the output pixels w * 80 .. w * 80 + 79 of the
 // workgroup (PB = 5 blocks of 16) and all BC channels, as igemm_kernel's
@@ -30,37 +33,40 @@ namespace dw {
 
 bool igemm_launch_rows_i8_a(hipStream_t st, const IgemmArgs& a, const TileCfg& t, int epv);  // generic, QU8
 bool igemm_launch_rows_i8_b(hipStream_t st, const IgemmArgs& a, const TileCfg& t, int epv);  // LUT variants
+bool igemm_launch_rows_f16(hipStream_t st, const IgemmArgs& a, const TileCfg& t);
 
 namespace ig {
 
 constexpr int kRowsPix = 320;  // output pixels per workgroup
 constexpr int kRowsPB = 5;     // 16-pixel blocks per wave
 
-__host__ __device__ constexpr int rows_su(int cin) { return (cin / 16) | 1; }
+// LDS pixel stride in 16-byte units for c_in channels of esize bytes
+__host__ __device__ constexpr int rows_su(int cin, int esize) { return (cin * esize / 16) | 1; }
 // LDS: epilogue data, k-slice offsets, all of K's weights, the input tile.
 __host__ __device__ constexpr int rows_tab_off(int bc) { return 256 + 8 * bc; }
 __host__ __device__ constexpr int rows_w_off(int bc, int ksteps) { return (rows_tab_off(bc) + ksteps * 16 + 15) / 16 * 16; }
 __host__ __device__ constexpr int rows_x_off(int bc, int ksteps) { return rows_w_off(bc, ksteps) + ksteps * bc * 64; }
-inline size_t rows_lds_bytes(int bc, int ksteps, int w, int cin) {
+inline size_t rows_lds_bytes(int bc, int ksteps, int w, int cin, int esize) {
   const int r = kRowsPix / w;
-  return (size_t)rows_x_off(bc, ksteps) + (size_t)(r + 2) * (w + 2) * rows_su(cin) * 16;
+  return (size_t)rows_x_off(bc, ksteps) + (size_t)(r + 2) * (w + 2) * rows_su(cin, esize) * 16;
 }
 // Input units each thread loads at start-up (at most).
 constexpr int kRowsFill = 16;
 
-template <int BC, int EPV>
+template <int ESZ, int BC, int EPV>
 __global__ __launch_bounds__(256) void igemm_rows_kernel(const IgemmArgs a) {
   constexpr int CB = BC / 16;
   constexpr int PB = kRowsPB;
   constexpr bool FAST = EPV != EPV_GENERIC;
-  using acc_t = v4i;
+  static_assert(!FAST || ESZ == 1, "specialised epilogues are int8");
+  using acc_t = typename std::conditional<ESZ == 1, v4i, v4f>::type;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
   const int KSTEPS = a.ksteps, COUTP = a.cout_pad, CIN = a.cin;
   const int W = a.w, H = a.h;
   const int R = kRowsPix / W;
   const int TW = W + 2;
-  const int CU = CIN / 16;        // 16-byte units per pixel
+  const int CU = CIN * ESZ / 16;  // 16-byte units per pixel
   const int SU = CU | 1;          // LDS pixel stride in units
 
   const int tid = threadIdx.x;
@@ -115,6 +121,11 @@ __global__ __launch_bounds__(256) void igemm_rows_kernel(const IgemmArgs a) {
     if (wave == 2 && a.lut && lane < 16)
       __builtin_amdgcn_global_load_lds((const void*)(a.lut + lane * 16),
                                        (__attribute__((address_space(3))) void*)s_lut, 16, 0, 0);
+  } else if (a.epi == EPI_F16 && a.bias_h) {
+    ep.bias_h = reinterpret_cast<const uint16_t*>(s_bias);
+    if (wave == 0 && lane < nvalid / 2)
+      __builtin_amdgcn_global_load_lds((const void*)(a.bias_h + c0 + lane * 2),
+                                       (__attribute__((address_space(3))) void*)s_bias, 4, 0, 0);
   }
 
   // ---- input tile: raw 16-byte units (out-of-image units: out-of-range
@@ -136,7 +147,8 @@ __global__ __launch_bounds__(256) void igemm_rows_kernel(const IgemmArgs a) {
       const int tr = div_small(ip, TW, r_tw), tc = ip - tr * TW;
       const int ih = r0 - 1 + tr, iw = tc - 1;
       const bool ok = (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W;
-      const int off = ok ? (((n * H + ih) * W + iw) * a.x_pix_stride + a.x_c_off + cu * 16) : (int)0x80000000;
+      // byte offset: the view's element offset times the element size
+      const int off = ok ? ((((n * H + ih) * W + iw) * a.x_pix_stride + a.x_c_off) * ESZ + cu * 16) : (int)0x80000000;
       xv[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrsrc, off, 0, 0));
       xdst[i] = (ip * SU + cu) * 16;
       xin[i] = ok;
@@ -147,12 +159,12 @@ __global__ __launch_bounds__(256) void igemm_rows_kernel(const IgemmArgs a) {
   // tap; its unit's offset from the pixel's top-left tap in the tile (slices
   // past K: any unit, their weights are zero)
   for (int e = tid; e < KSTEPS * 4; e += 256) {
-    const int k = e * 16;
+    const int k = e * (16 / ESZ);  // the slice's first element of K
     int off = 0;
     if (k < 9 * CIN) {
       const int tap = k / CIN, ci = k - (k / CIN) * CIN;
       const int kh = tap / 3, kw = tap - (tap / 3) * 3;
-      off = ((kh * TW + kw) * SU + ci / 16) * 16;
+      off = ((kh * TW + kw) * SU + ci * ESZ / 16) * 16;
     }
     s_tab[e] = off;
   }
@@ -162,8 +174,12 @@ __global__ __launch_bounds__(256) void igemm_rows_kernel(const IgemmArgs a) {
 #pragma unroll
   for (int i = 0; i < kRowsFill; ++i) {
     if (xdst[i] >= 0) {
-      const uint32_t key = xin[i] ? a.xxor : a.xpad;
-      *reinterpret_cast<u32x4*>(s_x + xdst[i]) = xv[i] ^ key;
+      if constexpr (ESZ == 1) {
+        const uint32_t key = xin[i] ? a.xxor : a.xpad;
+        *reinterpret_cast<u32x4*>(s_x + xdst[i]) = xv[i] ^ key;
+      } else {
+        *reinterpret_cast<u32x4*>(s_x + xdst[i]) = xv[i];  // padding: the zeros of the out-of-range load
+      }
     }
   }
   __syncthreads();
@@ -212,8 +228,13 @@ __global__ __launch_bounds__(256) void igemm_rows_kernel(const IgemmArgs a) {
 #pragma unroll
         for (int cb = 0; cb < CB; ++cb)
 #pragma unroll
-          for (int pb = 0; pb < PB; ++pb)
-            acc[cb][pb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[r][cb], bfr[r][pb], acc[cb][pb], 0, 0, 0);
+          for (int pb = 0; pb < PB; ++pb) {
+            if constexpr (ESZ == 1)
+              acc[cb][pb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[r][cb], bfr[r][pb], acc[cb][pb], 0, 0, 0);
+            else
+              acc[cb][pb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, afr[r][cb]),
+                                                                   __builtin_bit_cast(v8h, bfr[r][pb]), acc[cb][pb], 0, 0, 0);
+          }
       }
     }
   }
@@ -226,17 +247,17 @@ __global__ __launch_bounds__(256) void igemm_rows_kernel(const IgemmArgs a) {
     __syncthreads();
     xp = s_x + wave * 16 * xpose_row(BC);
   }
-  igemm_store<1, BC, PB, EPV>(a, ep, acc, c0, p0, lane, s_ms, s_lut, xp);
+  igemm_store<ESZ, BC, PB, EPV>(a, ep, acc, c0, p0, lane, s_ms, s_lut, xp);
 }
 
-template <int EPV>
+template <int ESZ, int EPV>
 bool launch_rows_tiles(hipStream_t st, const IgemmArgs& a, const TileCfg& t) {
   const int r = kRowsPix / a.w;
   const dim3 grid((unsigned)(a.n * (a.h / r) * (a.cout_pad / t.bc)));
-  const size_t lds = rows_lds_bytes(t.bc, a.ksteps, a.w, a.cin);
+  const size_t lds = rows_lds_bytes(t.bc, a.ksteps, a.w, a.cin, ESZ);
 #define DW_B(BC_)                                                                          \
   case BC_:                                                                                \
-    hipLaunchKernelGGL((igemm_rows_kernel<BC_, EPV>), grid, dim3(256), lds, st, a);      \
+    hipLaunchKernelGGL((igemm_rows_kernel<ESZ, BC_, EPV>), grid, dim3(256), lds, st, a); \
     return true;
   switch (t.bc) {
     DW_B(96)

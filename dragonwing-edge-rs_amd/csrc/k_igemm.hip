@@ -104,12 +104,13 @@ TileCfg make_st_tile(const IgemmArgs& a, int bc, int pb) {
 // the row count per tile divides H), channel tiles up to 96 (register
 // budget), the input tile within the start-up loads and LDS.
 bool rows_ok(const IgemmArgs& a, int bc) {
-  if (a.epi == EPI_F16 || a.kh != 3 || a.kw != 3 || a.sh != 1 || a.sw != 1 || a.pt != 1 || a.pl != 1) return false;
-  if (a.ho != a.h || a.wo != a.w || a.cin % 16 != 0 || a.w <= 0 || ig::kRowsPix % a.w != 0) return false;
+  const int es = a.epi == EPI_F16 ? 2 : 1;
+  if (a.kh != 3 || a.kw != 3 || a.sh != 1 || a.sw != 1 || a.pt != 1 || a.pl != 1) return false;
+  if (a.ho != a.h || a.wo != a.w || (a.cin * es) % 16 != 0 || a.w <= 0 || ig::kRowsPix % a.w != 0) return false;
   const int r = ig::kRowsPix / a.w;
   if (a.h % r != 0 || bc > 96 || !tile_ok(a, bc, 4)) return false;
-  if ((r + 2) * (a.w + 2) * (a.cin / 16) > ig::kRowsFill * 256) return false;
-  return ig::rows_lds_bytes(bc, a.ksteps, a.w, a.cin) <= 160 * 1024;
+  if ((r + 2) * (a.w + 2) * (a.cin * es / 16) > ig::kRowsFill * 256) return false;
+  return ig::rows_lds_bytes(bc, a.ksteps, a.w, a.cin, es) <= 160 * 1024;
 }
 
 TileCfg make_rows_tile(const IgemmArgs& a, int bc) {
@@ -249,7 +250,7 @@ void launch_igemm(hipStream_t st, const IgemmArgs& a_in, int esize) {
   a.x_bytes = (int)xb;
   const size_t lds = t.tpw > 0     ? ig::sk_lds_bytes(t.bc, a.ksteps)
                      : t.tpw == -1 ? ig::st_lds_bytes(t.bc, a.ksteps, t.pd)
-                     : t.tpw == -2 ? ig::rows_lds_bytes(t.bc, a.ksteps, a.w, a.cin)
+                     : t.tpw == -2 ? ig::rows_lds_bytes(t.bc, a.ksteps, a.w, a.cin, esize)
                      : t.tpw == -3 ? ig::wide_lds_bytes(t.bc, a.ksteps)
                                    : ig::lds_bytes(t, a.ksteps);
   if (lds > 160 * 1024) fail(-2, "igemm: k-slice table does not fit LDS");
@@ -282,7 +283,10 @@ void launch_igemm(hipStream_t st, const IgemmArgs& a_in, int esize) {
     else
       ok = ab ? igemm_launch_i8_a(st, a, t, epv) : igemm_launch_i8_b(st, a, t, epv);
   } else {
-    ok = t.tpw > 0 ? igemm_launch_sk_f16(st, a, t) : (t.tpw == -1 ? igemm_launch_st_f16(st, a, t) : igemm_launch_f16(st, a, t));
+    ok = t.tpw > 0     ? igemm_launch_sk_f16(st, a, t)
+         : t.tpw == -1 ? igemm_launch_st_f16(st, a, t)
+         : t.tpw == -2 ? igemm_launch_rows_f16(st, a, t)
+                       : igemm_launch_f16(st, a, t);
   }
   if (!ok) fail(-2, "igemm: no kernel for tile");
   DW_HIP(hipGetLastError());

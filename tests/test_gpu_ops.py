@@ -531,6 +531,28 @@ def test_conv_f16_streamed_tiles_identical(backend, monkeypatch):
         np.testing.assert_array_equal(got, first, err_msg=f"tile {bc},{pb},-1")
 
 
+@pytest.mark.parametrize("geom", [(2, 16, 40, 64, 64), (1, 8, 80, 32, 48), (1, 4, 160, 16, 32)])
+def test_conv_f16_row_tiles_identical(backend, monkeypatch, geom):
+    # 3x3 stride 1 over whole rows of 40, 80 and 160 pixels: the row-tile
+    # kernel stages the input rows in LDS and sums the same k-steps in the
+    # same order as the staged kernel, so the results are identical.
+    n, h, w, ci, co = geom
+    r = synth.Rng(synth.seed_for(603 + w))
+    xh = synth.f16_bits(r.normal((n, h, w, ci), 0.0, 1.0))
+    kh_ = synth.f16_bits(r.normal((3, 3, ci, co), 0.0, (1.0 / (9 * ci)) ** 0.5))
+    bh = synth.f16_bits(r.normal((co,), 0.0, 0.1))
+    ref = oracle_conv_f16(xh, kh_, bh, 1, 1, ops.ACT_SILU)
+    monkeypatch.setenv("DW_IGEMM_TILE", "16,4")
+    first = run_conv_f16(backend, xh, kh_, bh, 1, 1, ops.ACT_SILU, exact=False)
+    assert rel_err(f16v(first), f16v(ref)) <= 1e-2
+    for bc in (16, 32, 48, 64):
+        if co % bc:
+            continue
+        monkeypatch.setenv("DW_IGEMM_TILE", f"{bc},4,-2")
+        got = run_conv_f16(backend, xh, kh_, bh, 1, 1, ops.ACT_SILU, exact=False)
+        np.testing.assert_array_equal(got, first, err_msg=f"tile {bc},4,-2")
+
+
 @pytest.mark.parametrize("geom", [(2, 32, 32, 3, 16, 3, 2, 1), (1, 12, 12, 64, 64, 1, 1, 0),
                                   (1, 10, 10, 80, 80, 1, 1, 0), (1, 17, 15, 3, 16, 3, 2, 1),
                                   (2, 20, 22, 3, 16, 3, 2, 0), (1, 9, 12, 3, 32, 3, 2, 1),
