@@ -171,14 +171,15 @@ def test_int8_graph_row_tiles_bit_exact(backend, monkeypatch):
 
 @pytest.mark.parametrize("plant_subnormal_weight", [False, True])
 @pytest.mark.parametrize("stride", [1, 2])
-def test_depthwise_graph_bit_exact(backend, plant_subnormal_weight, stride):
+@pytest.mark.parametrize("shape", [(2, 23, 29, 48), (1, 9, 83, 64)])
+def test_depthwise_graph_bit_exact(backend, plant_subnormal_weight, stride, shape):
     # Depthwise conv + bias without activation: bit-exact, on the path that
     # feeds the f16 weights straight into the fma and (one weight planted
     # subnormal) on the path that widens them as the reference does; the
     # inputs carry subnormals too.
     from dragonwing_edge_rs_amd.graph import Graph, GRAPH_F16
-    r = synth.Rng(synth.seed_for(900 + stride))
-    n, h, w, c = 2, 23, 29, 48
+    r = synth.Rng(synth.seed_for(900 + stride + shape[2]))
+    n, h, w, c = shape
     x = synth.f16_bits(r.normal((n, h, w, c), 0.0, 1.0))
     x.ravel()[::997] = np.uint16(0x0003)  # subnormal inputs scattered over the tensor
     wt = synth.f16_bits(r.normal((3, 3, 1, c), 0.0, 0.3))

@@ -639,6 +639,32 @@ def test_depthwise_f16_sliding_window_shapes(backend, geom):
     assert rel_err(f16v(got), f16v(ref)) <= 1e-2
 
 
+@pytest.mark.parametrize("geom", [(2, 7, 83, 64, 0), (1, 9, 40, 128, 1), (3, 5, 6, 8, 1), (1, 11, 45, 24, 0),
+                                  (1, 1, 1, 64, 0), (2, 4, 41, 72, 1)])
+def test_depthwise_f16_stride1_shapes(backend, geom):
+    # Stride-1 shapes: wide rows, odd heights, 64- and 8-channel multiples, a
+    # 1x1 map; subnormal inputs planted in some (the reference decodes them
+    # at half value).
+    n, h, w, c, plant = geom
+    r = synth.Rng(synth.seed_for(460 + sum(geom)))
+    xh = synth.f16_bits(r.normal((n, h, w, c), 0.0, 1.0))
+    if plant:
+        xh.ravel()[::331] = np.uint16(0x8007)
+    kh_ = synth.f16_bits(r.normal((3, 3, c), 0.0, 0.3))
+    bh = synth.f16_bits(r.normal((c,), 0.0, 0.1))
+    bx, bk, bb = backend.from_numpy(xh), backend.from_numpy(kh_), backend.from_numpy(bh)
+    by = backend.alloc(xh.nbytes)
+    conv = oracle.depthwise_fp16(xh, kh_, (1, 1), (1, 1))
+    ops.depthwise_conv2d_f16_nhwc(backend, bx, bk, bb, by, n, h, w, c, 3, 3, 1, 1, 1, 1, ops.ACT_NONE)
+    np.testing.assert_array_equal(backend.to_numpy(by, np.uint16, xh.shape), oracle.bias_add_f16(conv, bh))
+    ops.depthwise_conv2d_f16_nhwc(backend, bx, bk, None, by, n, h, w, c, 3, 3, 1, 1, 1, 1, ops.ACT_RELU)
+    np.testing.assert_array_equal(backend.to_numpy(by, np.uint16, xh.shape), oracle.relu_fp16(conv))
+    ops.depthwise_conv2d_f16_nhwc(backend, bx, bk, bb, by, n, h, w, c, 3, 3, 1, 1, 1, 1, ops.ACT_SILU)
+    got = backend.to_numpy(by, np.uint16, xh.shape)
+    ref = oracle.silu_fp16(oracle.bias_add_f16(conv, bh))
+    assert rel_err(f16v(got), f16v(ref)) <= 1e-2
+
+
 @pytest.mark.parametrize("geom", [(1, 7, 5, 8, 2), (2, 9, 9, 16, 1), (1, 6, 6, 24, 2)])
 def test_depthwise_f32_and_f16_ragged(backend, geom):
     n, h, w, c, s = geom
