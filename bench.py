@@ -346,7 +346,8 @@ def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=0,
-                    help="timed steps (default: 50 for the graphs, 1000 for the single-op workloads)")
+                    help="timed steps (default: 3000 for the graphs, 10000 for the single-op workloads: a "
+                         "few seconds of GPU work, long enough for an outside utilisation sampler to see it)")
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="yolov8n_int8",
                     choices=["yolov8n_int8", "yolov8n_f16", "qlinearconv", "dwconv", "conv_f32"])
@@ -370,7 +371,7 @@ def main():
         sys.exit(2)
 
     if args.steps <= 0:
-        args.steps = 50 if args.workload.startswith("yolov8n") else 1000
+        args.steps = 3000 if args.workload.startswith("yolov8n") else 10000
     import __graft_entry__
 
     dw = __graft_entry__.import_pkg()
