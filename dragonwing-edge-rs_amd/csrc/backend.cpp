@@ -504,6 +504,7 @@ int dw_hip_qlinearconv_u8s8_noalloc(dw_hip_backend* be, const dw_hip_buffer* inp
   if (c_out > dw::kNoAllocMaxChannels)
     dw::fail(DW_ERR_UNSUPPORTED, "qlinearconv_noalloc: c_out above " + std::to_string(dw::kNoAllocMaxChannels));
   float m[dw::kNoAllocMaxChannels];
+  dw::ScratchUse use(b->device, b->stream);
   QconvSpace sp;
   uint8_t* base = (uint8_t*)b->scratch;
   sp.ms = (float*)base;

@@ -19,6 +19,18 @@ constexpr size_t kNoAllocTableBytes = 2 * kNoAllocMaxChannels * 4;
 // Device address of this device's scratch array (looked up on the first
 // call per device, which must run with that device current).
 void* noalloc_scratch_setup(int device);
+// One call's use of its device's scratch, from construction (before the
+// first write) to destruction (after the last launch that reads it): holds
+// the device's scratch mutex, makes `stream` wait for the previous call's
+// work on the scratch, and marks this call's work as the one the next call
+// waits for.
+struct ScratchUse {
+  int device;
+  hipStream_t stream;
+  std::lock_guard<std::mutex> lock;
+  ScratchUse(int device, hipStream_t stream);
+  ~ScratchUse();
+};
 
 // One device, one in-order stream (default priority).  Op functions that need
 // temporary device memory (packed weights, per-channel scales) use grow-only

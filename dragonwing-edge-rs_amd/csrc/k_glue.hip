@@ -371,6 +371,8 @@ __global__ __launch_bounds__(512) void sppf_lds_kernel(const PoolArgs a, View y2
     const int y = i / a.w, x = i - (i / a.w) * a.w;
     const uint4* row = X + y * a.w;
     uint4 m = row[x];
+    R1[i] = m;  // r = 0 (a 1x1 pool): the loops below add nothing
+    R2[i] = m;
     for (int d = 1; d <= 3 * r; ++d) {
       if (x - d >= 0) m = vmax16<ES>(m, row[x - d]);
       if (x + d < a.w) m = vmax16<ES>(m, row[x + d]);

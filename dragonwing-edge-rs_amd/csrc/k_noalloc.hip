@@ -16,6 +16,12 @@ static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
+// Per device: held from the first write of a call's tables to the launch of
+// its last kernel, and the event recorded after that launch, which the next
+// call's stream waits on before writing the scratch again.  Together they
+// order calls through different backends (streams) on one device.
+std::mutex g_use_mu[kMaxDevices];
+hipEvent_t g_last_use[kMaxDevices] = {};
 
 }  // namespace
 
@@ -24,12 +30,24 @@ void* noalloc_scratch_setup(int device) {
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch_ptr[device]) {
     void* p = nullptr;
-    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !p)
       fail(-1, std::string("no-alloc scratch: hipGetSymbolAddress failed: ") + hipGetErrorString(e));
+    e = hipEventCreateWithFlags(&g_last_use[device], hipEventDisableTiming);
+    if (e != hipSuccess) fail(-1, std::string("no-alloc scratch: hipEventCreate failed: ") + hipGetErrorString(e));
     g_scratch_ptr[device] = p;
   }
   return g_scratch_ptr[device];
+}
+
+ScratchUse::ScratchUse(int dev, hipStream_t s) : device(dev), stream(s), lock(g_use_mu[dev]) {
+  // An event never recorded is complete, so the first call does not wait.
+  DW_HIP(hipStreamWaitEvent(stream, g_last_use[device], 0));
+}
+
+ScratchUse::~ScratchUse() {
+  // After whatever this call enqueued (also when it failed part way).
+  (void)hipEventRecord(g_last_use[device], stream);
 }
 
 }  // namespace dw

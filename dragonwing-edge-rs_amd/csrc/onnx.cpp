@@ -139,6 +139,21 @@ void floats(const Field& f, std::vector<float>& out) {
 // ---------------------------------------------------------------------------
 enum DataType { DT_FLOAT = 1, DT_UINT8 = 2, DT_INT8 = 3, DT_INT32 = 6, DT_INT64 = 7, DT_FLOAT16 = 10, DT_DOUBLE = 11 };
 
+// bytes per element of a TensorProto data type (0: not one this reader holds)
+inline int64_t dtype_bytes(int dt) {
+  switch (dt) {
+    case DT_UINT8: case DT_INT8: return 1;
+    case DT_FLOAT16: return 2;
+    case DT_FLOAT: case DT_INT32: return 4;
+    case DT_INT64: case DT_DOUBLE: return 8;
+    default: return 0;
+  }
+}
+
+// Largest element count a tensor may declare: its dims are checked against
+// this when parsed, so numel() never overflows.
+constexpr int64_t kMaxElements = int64_t(1) << 40;
+
 struct Tensor {
   std::string name;
   std::vector<int64_t> dims;
@@ -148,6 +163,14 @@ struct Tensor {
     int64_t n = 1;
     for (auto d : dims) n *= d;
     return n;
+  }
+  // The payload must hold exactly the elements the dims declare, at the
+  // element size of `dt` (the type the caller is about to read it as).
+  void require_payload(int dt) const {
+    const int64_t es = dtype_bytes(dt);
+    if (es == 0 || (int64_t)data.size() != numel() * es)
+      fail(DW_ERR_INVALID, "onnx: tensor '" + name + "' holds " + std::to_string(data.size()) +
+                               " bytes, its dims and type declare " + std::to_string(numel() * es));
   }
 };
 
@@ -224,6 +247,12 @@ Tensor parse_tensor(Reader r) {
         break;
       default: break;
     }
+  }
+  int64_t n = 1;
+  for (auto d : t.dims) {
+    if (d < 0 || d > kMaxElements || (d > 0 && n > kMaxElements / d))
+      fail(DW_ERR_INVALID, "onnx: tensor '" + t.name + "' has a negative or oversized dimension");
+    n *= d;
   }
   if (raw) return t;
   if (!fd.empty()) {
@@ -492,29 +521,42 @@ struct Builder {
   std::vector<int64_t> const_ints(const std::string& n) const {
     const Tensor* t = const_of(n);
     if (!t) fail(DW_ERR_UNSUPPORTED, "onnx: '" + n + "' must be a constant");
+    if (t->dtype != DT_INT64 && t->dtype != DT_INT32)
+      fail(DW_ERR_UNSUPPORTED, "onnx: '" + n + "' must be an integer constant");
+    t->require_payload(t->dtype);
     std::vector<int64_t> v(t->numel());
-    if (t->dtype == DT_INT64) memcpy(v.data(), t->data.data(), v.size() * 8);
-    else if (t->dtype == DT_INT32)
-      for (size_t i = 0; i < v.size(); ++i) v[i] = ((const int32_t*)t->data.data())[i];
-    else fail(DW_ERR_UNSUPPORTED, "onnx: '" + n + "' must be an integer constant");
+    if (t->dtype == DT_INT64) {
+      if (!v.empty()) memcpy(v.data(), t->data.data(), v.size() * 8);
+    } else {
+      for (size_t i = 0; i < v.size(); ++i) {
+        int32_t e;
+        memcpy(&e, &t->data[i * 4], 4);
+        v[i] = e;
+      }
+    }
     return v;
   }
   std::vector<float> const_floats(const std::string& n) const {
     const Tensor* t = const_of(n);
     if (!t) fail(DW_ERR_UNSUPPORTED, "onnx: '" + n + "' must be a constant");
+    if (t->dtype != DT_FLOAT) fail(DW_ERR_UNSUPPORTED, "onnx: '" + n + "' must be a float constant");
+    t->require_payload(DT_FLOAT);
     std::vector<float> v(t->numel());
-    if (t->dtype == DT_FLOAT) memcpy(v.data(), t->data.data(), v.size() * 4);
-    else fail(DW_ERR_UNSUPPORTED, "onnx: '" + n + "' must be a float constant");
+    if (!v.empty()) memcpy(v.data(), t->data.data(), v.size() * 4);
     return v;
   }
   int const_zp(const std::string& n) const {
     if (n.empty()) return 0;
     const Tensor* t = const_of(n);
     if (!t || t->numel() != 1) fail(DW_ERR_UNSUPPORTED, "onnx: zero point '" + n + "' must be a scalar constant");
+    if (t->dtype != DT_UINT8 && t->dtype != DT_INT8 && t->dtype != DT_INT32)
+      fail(DW_ERR_UNSUPPORTED, "onnx: zero point type");
+    t->require_payload(t->dtype);
     if (t->dtype == DT_UINT8) return t->data[0];
     if (t->dtype == DT_INT8) return (int8_t)t->data[0];
-    if (t->dtype == DT_INT32) return ((const int32_t*)t->data.data())[0];
-    fail(DW_ERR_UNSUPPORTED, "onnx: zero point type");
+    int32_t v;
+    memcpy(&v, t->data.data(), 4);
+    return v;
   }
 
   TensorInfo& T(const std::string& n) { return g.tensor(A(n)); }
@@ -541,8 +583,8 @@ struct Builder {
     ti.dims = t->dims.empty() ? std::vector<int64_t>{1} : t->dims;
     ti.dtype = DW_DTYPE_F32;
     ti.is_init = true;
+    t->require_payload(DT_FLOAT);
     ti.data = t->data;
-    if ((int64_t)ti.data.size() != ti.numel() * 4) fail(DW_ERR_INVALID, "onnx: initializer '" + n + "' size");
     g.t[n] = ti;
   }
   std::string in_name(const std::string& n) {
@@ -608,10 +650,12 @@ struct Builder {
     if (!zpn.empty()) {
       const Tensor* z = const_of(zpn);
       if (!z) fail(DW_ERR_UNSUPPORTED, "onnx: weight zero point must be constant");
+      z->require_payload(z->dtype);
       for (uint8_t b : z->data)
         if (b != 0) fail(DW_ERR_UNSUPPORTED, "onnx: weights need zero point 0 (symmetric)");
     }
     if (q->dtype == DT_UINT8) fail(DW_ERR_UNSUPPORTED, "onnx: u8 weights (s8 symmetric only)");
+    q->require_payload(q->dtype);
     const int64_t cnt = q->numel();
     TensorInfo ti;
     ti.dims = q->dims.empty() ? std::vector<int64_t>{1} : q->dims;
@@ -619,9 +663,15 @@ struct Builder {
     ti.is_init = true;
     ti.prequant = true;
     std::vector<float> v(cnt);
-    for (int64_t i = 0; i < cnt; ++i)
-      v[i] = q->dtype == DT_INT8 ? (float)((const int8_t*)q->data.data())[i]
-                                 : (float)((const int32_t*)q->data.data())[i];
+    for (int64_t i = 0; i < cnt; ++i) {
+      if (q->dtype == DT_INT8) {
+        v[i] = (float)(int8_t)q->data[i];
+      } else {
+        int32_t e;
+        memcpy(&e, &q->data[i * 4], 4);
+        v[i] = (float)e;
+      }
+    }
     ti.data.resize(cnt * 4);
     memcpy(ti.data.data(), v.data(), ti.data.size());
     // per-channel scales along `axis` (opset 13 default 1), or one scale

@@ -170,8 +170,8 @@ int dw_hip_qlinearconv_u8s8(dw_hip_backend* be, const dw_hip_buffer* input,
                             int x_zp, const float* w_scales, float y_scale, int y_zp);
 
 /* dw_hip_qlinearconv_u8s8 without any device allocation.  No counterpart in
- * the reference: for callers that cannot allocate device memory (code under
- * HIP graph capture, tight serving loops, hosts that forbid hipMalloc).  The
+ * the reference: for callers that cannot allocate device memory (tight
+ * serving loops, hosts that forbid hipMalloc).  The
  * per-call data the other entry point keeps in grow-only workspaces (packed
  * weights, per-channel multipliers, bias') goes to a fixed 8 MiB scratch
  * array per device instead, set up when the backend is created: c_out at
@@ -179,8 +179,10 @@ int dw_hip_qlinearconv_u8s8(dw_hip_backend* be, const dw_hip_buffer* input,
  * to the channel tile * 64 bytes) at most 8 MiB - 32 KiB, else
  * DW_ERR_UNSUPPORTED.  Same arguments, results and errors as
  * dw_hip_qlinearconv_u8s8.  Every call on a device shares that device's
- * scratch: calls through one backend are ordered on its stream, but calls
- * that overlap on one device through different backends (streams) race. */
+ * scratch; calls through different backends (streams) on one device are
+ * ordered on it (each call's stream waits for the previous call's last
+ * launch).  Not capturable: the per-channel scales are copied from the
+ * caller's host array and the call waits for that copy. */
 int dw_hip_qlinearconv_u8s8_noalloc(dw_hip_backend* be, const dw_hip_buffer* input,
                                     const dw_hip_buffer* kernel, const dw_hip_buffer* bias,
                                     dw_hip_buffer* output, size_t n, size_t h_in, size_t w_in,

@@ -287,3 +287,28 @@ def test_reference_int8_graph_oracle_forms_agree():
     f = np.clip(acc.astype(np.float32) * np.float32(scale), -128, 127)
     q = (np.sign(f) * np.floor(np.abs(f).astype(np.float64) + 0.5)).astype(np.int8)  # half away from zero
     np.testing.assert_array_equal(a["c1.relu"], np.maximum(q, 0))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("k", [1, 3, 5])
+def test_maxpool_cascade_radius(backend, k):
+    # Three chained k x k stride-1 MaxPools with pads k // 2 run as one
+    # cascade launch; k = 1 (radius 0, each pool the identity) included.
+    r = synth.Rng(synth.seed_for(50 + k))
+    g = Graph(GRAPH_F16)
+    shape = (2, 9, 11, 16)
+    for t in ("x", "p1", "p2", "p3"):
+        g.add_tensor(t, shape, "f16")
+    for i, (a, b) in enumerate((("x", "p1"), ("p1", "p2"), ("p2", "p3"))):
+        g.add_op(f"pool{i}", "MaxPool", [a], [b], kernel_shape=(k, k), strides=(1, 1), pads=(k // 2,) * 4)
+    g.set_io(["x"], ["p1", "p2", "p3"])
+    x = synth.f16_bits(r.normal(shape, 0.0, 1.0))
+    rt = HipGraphRuntime(g, backend)
+    assert [L["kernel"] for L in rt.launches()] == ["maxpool_cascade3"]
+    rt.set_input_bytes("x", x)
+    rt.run()
+    ref = oracle_run(g, {"x": x})
+    for t in ("p1", "p2", "p3"):
+        np.testing.assert_array_equal(rt.get_output_bytes(t).view(np.uint16).reshape(shape), ref[t], err_msg=t)
+    if k == 1:
+        np.testing.assert_array_equal(ref["p3"], x)

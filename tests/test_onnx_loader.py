@@ -164,3 +164,46 @@ def test_qdq_model_computes_the_same_bytes():
     x = synth.f16_bits(yolo.input_images(1, 64))
     for a, b in zip(oracle_outputs(g, x), oracle_outputs(g2, x)):
         np.testing.assert_array_equal(a, b)
+
+
+def bad_tensor(name, dims, dtype, payload: bytes) -> bytes:
+    """A TensorProto whose declared dims do not match its raw payload."""
+    return ox.f_ints(1, dims) + ox.f_varint(2, dtype) + ox.f_bytes(9, payload) + ox.f_str(8, name)
+
+
+def clip_model(inits, zp_node=None):
+    nodes = [ox.node("Clip", ["x", "lo", "hi"], ["y"], "clip")]
+    return ox.model(nodes, inits, [ox.value_info("x", [1, 3, 8, 8])], [ox.value_info("y", [1, 3, 8, 8])])
+
+
+@pytest.mark.parametrize("case", ["float_dims_too_large", "float_short_payload", "negative_dim",
+                                  "overflowing_dims", "int64_shape", "dq_int8_weight", "empty_zero_point"])
+def test_constant_payload_must_match_dims(case):
+    # Every constant the builder reads is checked against the element count
+    # its dims declare before it is read; a mismatch is DW_ERR_INVALID (a
+    # malformed model), never a read past the payload.
+    hi = ox.tensor("hi", np.array([6.0], np.float32))
+    four = np.float32(0.0).tobytes()
+    if case in ("float_dims_too_large", "float_short_payload", "negative_dim", "overflowing_dims"):
+        dims = {"float_dims_too_large": [1 << 26], "float_short_payload": [2], "negative_dim": [-1],
+                "overflowing_dims": [1 << 31, 1 << 31, 1 << 31]}[case]
+        m = clip_model([bad_tensor("lo", dims, ox.FLOAT, four), hi])
+    elif case == "int64_shape":
+        nodes = [ox.node("Reshape", ["x", "shape"], ["y"], "r")]
+        m = ox.model(nodes, [bad_tensor("shape", [1 << 20], 7, np.int64(2).tobytes() * 2)],
+                     [ox.value_info("x", [1, 3, 8, 8])], [ox.value_info("y", [1, 192])])
+    elif case == "dq_int8_weight":
+        nodes = [ox.node("DequantizeLinear", ["wq", "ws"], ["w"], "dq"),
+                 ox.node("Conv", ["x", "w"], ["y"], "conv", kernel_shape=[3, 3], pads=[1, 1, 1, 1])]
+        m = ox.model(nodes, [bad_tensor("wq", [2, 3, 3, 3], 3, bytes(10)),
+                             ox.tensor("ws", np.array([0.1], np.float32))],
+                     [ox.value_info("x", [1, 3, 8, 8])], [ox.value_info("y", [1, 2, 8, 8])])
+    else:  # a scalar u8 zero point with no bytes
+        nodes = [ox.node("QuantizeLinear", ["x", "s", "zp"], ["xq"], "q"),
+                 ox.node("DequantizeLinear", ["xq", "s", "zp"], ["xd"], "dq"),
+                 ox.node("Relu", ["xd"], ["y"], "relu")]
+        m = ox.model(nodes, [ox.tensor("s", np.array(0.1, np.float32)), bad_tensor("zp", [], 2, b"")],
+                     [ox.value_info("x", [1, 3, 8, 8])], [ox.value_info("y", [1, 3, 8, 8])])
+    with pytest.raises(HipError) as e:
+        Graph.from_onnx(m)
+    assert e.value.code == -4, (case, e.value.code, str(e.value))  # DW_ERR_INVALID

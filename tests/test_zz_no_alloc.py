@@ -56,3 +56,38 @@ def test_noalloc_refuses_sizes_past_its_scratch(backend):
     with pytest.raises(HipError, match="exceed the no-alloc scratch"):
         ops.qlinearconv_u8s8_noalloc(backend, bx, bw, None, by, 1, 4, 4, 4096, 256, 3, 3, 1, 1, 1, 1, 0.02, 128,
                                      np.full(256, 0.01, np.float32), 0.05, 128)
+
+
+def test_noalloc_two_backends_back_to_back(backend):
+    # Two backends on one device share its scratch: a large call on one and a
+    # smaller call on the other, issued back to back with no wait between
+    # them, must both equal the oracle (the second call's weight packing
+    # waits for the first call's GEMM).
+    import dragonwing_edge_rs_amd as dw
+
+    other = dw.Backend(0)
+    try:
+        cases = [(backend, synth.qlinearconv_case(53, n=4, h=40, w=40, c_in=128, c_out=256), 2),
+                 (other, synth.qlinearconv_case(54, n=1, h=16, w=16, c_in=64, c_out=128), 1)]
+        staged = []
+        for be, case, stride in cases:
+            x, w, b = case["x"], case["w"], case["bias"]
+            n, h, wd, ci = x.shape
+            co = w.shape[3]
+            ho, wo = oracle.out_hw(h, wd, 3, 3, stride, stride, 1, 1)
+            bufs = (be.from_numpy(x), be.from_numpy(w), be.from_numpy(b), be.alloc(n * ho * wo * co))
+            staged.append((be, case, stride, bufs, (n, ho, wo, co)))
+        for be, case, stride, (bx, bw, bb, by), _ in staged:
+            x = case["x"]
+            n, h, wd, ci = x.shape
+            ops.qlinearconv_u8s8_noalloc(be, bx, bw, bb, by, n, h, wd, ci, case["w"].shape[3], 3, 3, stride,
+                                         stride, 1, 1, case["x_scale"], case["x_zp"], case["w_scales"],
+                                         case["y_scale"], case["y_zp"])
+        for be, case, stride, (bx, bw, bb, by), shape in staged:
+            got = be.to_numpy(by, np.uint8, shape)
+            ref = oracle.qlinearconv_u8s8(case["x"], case["w"], case["bias"], (stride, stride), (1, 1),
+                                          case["x_scale"], case["x_zp"], case["w_scales"], case["y_scale"],
+                                          case["y_zp"])
+            np.testing.assert_array_equal(got, ref)
+    finally:
+        other.close()
