@@ -47,13 +47,23 @@ PEAKS = {  # MI355X dense peaks
 
 
 def kernel_bound(kernel: str):
+    """The roofline a kernel family is reported against."""
     if kernel.startswith("igemm_i8"):
         return PEAKS["int8"]
     if kernel.startswith("igemm_f16"):
         return PEAKS["f16"]
     if kernel.startswith("direct_conv"):
         return PEAKS["f32"]
-    return PEAKS["hbm"]
+    return PEAKS["hbm"]  # the u8 -> f16 1x1 convs (conv1x1_u8_f16) are HBM-bound
+
+
+def arith_peak(kernel: str):
+    """Dense peak (TFLOP/s or TOP/s) of a conv kernel's arithmetic."""
+    if kernel.startswith("igemm_i8"):
+        return PEAKS["int8"][1]
+    if kernel.startswith("igemm_f16") or kernel.startswith("conv1x1"):
+        return PEAKS["f16"][1]
+    return PEAKS["f32"][1]
 
 
 def conv_rooflines(launches, ms):
@@ -64,10 +74,10 @@ def conv_rooflines(launches, ms):
     rows = []
     for L, t in zip(launches, ms):
         k = L["kernel"]
-        if not (k.startswith("igemm") or k.startswith("direct_conv") or k.startswith("dwconv")):
+        if not (k.startswith("igemm") or k.startswith("direct_conv") or k.startswith("dwconv") or
+                k.startswith("conv1x1")):
             continue
-        bound, peak, unit = kernel_bound(k)
-        t_mfma = L["work"] / (peak * 1e12) if bound == "mfma" else 0.0
+        t_mfma = L["work"] / (arith_peak(k) * 1e12) if not k.startswith("dwconv") else 0.0
         t_hbm = L["bytes"] / (PEAKS["hbm"][1] * 1e9)
         floor = max(t_mfma, t_hbm)
         secs = float(t) * 1e-3

@@ -138,6 +138,7 @@ SIGNATURES = {
     "dw_graph_to_json": (S, [P]),
     "dw_graph_get_initializer": (I, [P, S, PP, C.POINTER(Z)]),
     "dw_hip_graph_runtime_create": (I, [P, P, PP]),
+    "dw_hip_graph_runtime_create_ex": (I, [P, P, C.c_uint, PP]),
     "dw_hip_graph_runtime_destroy": (None, [P]),
     "dw_hip_graph_set_input_f32": (I, [P, S, P, Z]),
     "dw_hip_graph_set_input_bytes": (I, [P, S, P, Z]),

@@ -126,6 +126,21 @@ struct DirectArgs {
                            // for the 1x1 kernel's 16-channel groups
 };
 
+// 1x1 convolution (stride 1, no padding) with u8 input dequantized to f16,
+// on the fp16 matrix cores (k_conv1x1_f16.hip).
+struct Conv1x1F16Args {
+  const uint8_t* x;        // u8 input view
+  const uint16_t* wfrag;   // f16 weights in fragment order [cout/16][ceil(cin/32)][64][8]
+  const uint16_t* bias;    // f16 bias [cout] or null
+  uint16_t* y;             // f16 output view
+  int m, cin, cout;        // pixels, channels
+  int x_pix_stride, x_c_off, y_pix_stride, y_c_off;
+  float in_scale;
+  int in_zp;
+  uint32_t zp_bytes;       // in_zp in every byte (the value of K past c_in: dequantizes to 0)
+  int act;
+};
+
 // Depthwise convolution (channel multiplier 1).
 struct DwArgs {
   const void* x;
@@ -159,6 +174,8 @@ int igemm_channel_tile(int cout);
 int igemm_candidates(const IgemmArgs& a, int* bc, int* pb, int* tpw, int max);
 
 void launch_direct_conv(hipStream_t st, const DirectArgs& a);
+bool conv1x1_u8_f16_supported(int cin, int cout);
+void launch_conv1x1_u8_f16(hipStream_t st, const Conv1x1F16Args& a);
 // HWIO f32 weights [rows][cout] -> [cout / 4][rows][4] (DirectArgs::wq)
 void launch_repack_oc4(hipStream_t st, const float* w, float* wq, int rows, int cout);
 void launch_dwconv(hipStream_t st, const DwArgs& a, int dtype);

@@ -129,6 +129,10 @@ struct Runtime {
   std::vector<hipStream_t> side;  // streams 1 .. nstreams - 1
   std::vector<hipEvent_t> evs;    // per launch (recorded ones only), then fork
   bool stats = false;
+  // DW_RT_EXACT_U8_F16_CONV: convs that read u8 (dequantized to f16) and
+  // write f16 run in the reference's accumulation order (bit-identical to
+  // the CPU) instead of on the fp16 matrix cores
+  bool exact_u8_f16 = false;
   // graph inputs given in NCHW f32 (the layout before convert_nchw_to_nhwc):
   // the one stem conv that reads such an input loads the NCHW planes itself
   // (rounding to f16 in its loader); any other input is converted by a
@@ -1459,6 +1463,51 @@ void Runtime::emit_conv(const Group& gr) {
     push_igemm(L, a, 2);
     return;
   }
+  // u8 -> f16 1x1 on the fp16 matrix cores (the dequantized fp16 layers of a
+  // quantized graph), held to the fp16 tolerance like the other MFMA convs
+  const bool head_mfma = !exact_u8_f16 && gr.in_kind == 2 && gr.out_kind == 1 && gr.res.empty() && kh == 1 &&
+                         kw == 1 && sh == 1 && sw == 1 && pt == 0 && pl == 0 && op.p.pads[2] == 0 &&
+                         op.p.pads[3] == 0 && conv1x1_u8_f16_supported(ci, co) && x.pix_stride % 8 == 0 &&
+                         x.abs_off % 8 == 0 && y.pix_stride % 4 == 0 && y.abs_off % 4 == 0 &&
+                         (W.dtype == DW_DTYPE_F16 || W.dtype == DW_DTYPE_F32) &&
+                         (!has_bias || g.t[op.in[2]].dtype == DW_DTYPE_F16);
+  if (head_mfma) {
+    // weights widened as the reference does (subnormals at half value) and
+    // re-encoded to f16, in fragment order: [cb][ks][lane][j] =
+    // W[k = 32 ks + 8 (lane / 16) + j][c = 16 cb + lane % 16], zero past K or c_out
+    const int cbn = (co + 15) / 16, ksn = (ci + 31) / 32;
+    std::vector<uint16_t> frag((size_t)cbn * ksn * 64 * 8, 0);
+    for (int cb = 0; cb < cbn; ++cb)
+      for (int ks = 0; ks < ksn; ++ks)
+        for (int l = 0; l < 64; ++l)
+          for (int j = 0; j < 8; ++j) {
+            const int k = 32 * ks + 8 * (l / 16) + j, c = 16 * cb + l % 16;
+            if (k >= ci || c >= co) continue;
+            const size_t src = (size_t)k * co + c;
+            const float v = W.dtype == DW_DTYPE_F16 ? f16_to_f32_ref(((const uint16_t*)W.data.data())[src])
+                                                    : ((const float*)W.data.data())[src];
+            frag[(((size_t)cb * ksn + ks) * 64 + l) * 8 + j] = f16_bits_from_f32(v);
+          }
+    Conv1x1F16Args a{};
+    a.x = (const uint8_t*)x.base;
+    a.wfrag = (const uint16_t*)upload(frag.data(), frag.size() * 2);
+    a.bias = has_bias ? (const uint16_t*)upload(g.t[op.in[2]].data.data(), g.t[op.in[2]].data.size()) : nullptr;
+    a.y = (uint16_t*)y.base;
+    a.m = (int)y.pixels();
+    a.cin = ci;
+    a.cout = co;
+    a.x_pix_stride = x.pix_stride; a.x_c_off = x.abs_off;
+    a.y_pix_stride = y.pix_stride; a.y_c_off = y.abs_off;
+    a.in_scale = gr.in_scale;
+    a.in_zp = gr.in_zp;
+    a.zp_bytes = (uint32_t)(gr.in_zp & 0xff) * 0x01010101u;
+    a.act = gr.act;
+    L.kernel = "conv1x1_u8_f16";
+    L.bytes += (double)x.bytes() + frag.size() * 2.0 + (double)y.bytes();
+    L.fn = [a](hipStream_t st) { launch_conv1x1_u8_f16(st, a); };
+    launches.push_back(L);
+    return;
+  }
   // direct (reference accumulation order)
   DirectArgs a{};
   a.x = x.base;
@@ -1882,11 +1931,18 @@ using dw::f16_to_f32_ref;
 extern "C" {
 
 int dw_hip_graph_runtime_create(dw_hip_backend* be, const dw_graph* g, dw_hip_graph_runtime** out) {
+  return dw_hip_graph_runtime_create_ex(be, g, 0u, out);
+}
+
+int dw_hip_graph_runtime_create_ex(dw_hip_backend* be, const dw_graph* g, unsigned flags,
+                                   dw_hip_graph_runtime** out) {
   API_BEGIN
   if (!g || !out) dw::fail(DW_ERR_INVALID, "null argument");
+  if (flags & ~(unsigned)DW_RT_EXACT_U8_F16_CONV) dw::fail(DW_ERR_INVALID, "unknown runtime flags");
   dw::Backend* b = Bk(be);
   std::lock_guard<std::mutex> lock(b->mu);
   auto* rt = new dw_hip_graph_runtime();
+  rt->rt.exact_u8_f16 = (flags & DW_RT_EXACT_U8_F16_CONV) != 0;
   dw::hold(b);  // released with the runtime
   try {
     rt->rt.build(b, g->g, false);

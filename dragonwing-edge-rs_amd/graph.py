@@ -183,12 +183,19 @@ class Graph:
         return raw
 
 
+RT_EXACT_U8_F16_CONV = 1  # DW_RT_EXACT_U8_F16_CONV
+
+
 class HipGraphRuntime:
     """``VulkanGraphRuntime`` on the HIP backend."""
 
-    def __init__(self, graph: Graph, backend):
+    def __init__(self, graph: Graph, backend, exact_u8_f16: bool = False):
+        """exact_u8_f16: the convs that read u8 activations and write f16 (a
+        QDQ graph's fp16 tail layers) run in the reference's accumulation
+        order, bit-identical to the CPU, instead of on the fp16 matrix cores."""
         h = C.c_void_p()
-        check(load().dw_hip_graph_runtime_create(backend.handle, graph.handle, C.byref(h)))
+        flags = RT_EXACT_U8_F16_CONV if exact_u8_f16 else 0
+        check(load().dw_hip_graph_runtime_create_ex(backend.handle, graph.handle, flags, C.byref(h)))
         self._h = h.value
         self._backend = backend  # keeps the backend alive
         track(self, RELEASE_RUNTIME)

@@ -518,6 +518,16 @@ typedef struct dw_hip_graph_runtime dw_hip_graph_runtime;
 /* VulkanGraphRuntime::new: plans device memory, packs weights, builds the
  * launch list.  The graph is copied; it can be destroyed afterwards. */
 int dw_hip_graph_runtime_create(dw_hip_backend* be, const dw_graph* g, dw_hip_graph_runtime** out);
+/* dw_hip_graph_runtime_create with plan options (flags 0: the same plan).
+ * DW_RT_EXACT_U8_F16_CONV: convs that read u8 activations (dequantized to
+ * f16) and write f16 -- the fp16 layers of a QDQ graph after its int8 part,
+ * e.g. a detect head's last 1x1 convs -- run in dragonwing-cpu's
+ * accumulation order, bit-identical to CpuGraphRuntime, instead of on the
+ * fp16 matrix cores (results within the fp16 tolerance).  The INT8 layers
+ * are bit-exact either way.  Unknown flags: DW_ERR_INVALID. */
+#define DW_RT_EXACT_U8_F16_CONV 1u
+int dw_hip_graph_runtime_create_ex(dw_hip_backend* be, const dw_graph* g, unsigned flags,
+                                   dw_hip_graph_runtime** out);
 void dw_hip_graph_runtime_destroy(dw_hip_graph_runtime* rt);
 /* set_input_f32 (vulkan_runtime.rs:238): converts to the graph dtype (F16 RNE). */
 int dw_hip_graph_set_input_f32(dw_hip_graph_runtime* rt, const char* name, const float* data, size_t count);
