@@ -54,6 +54,12 @@ class DwOpParams(C.Structure):
         ("clip_max", F),
         ("reg_max", I),
         ("level_strides", F * 4),
+        ("perm", I * 4),
+        ("num_slice_axes", I),
+        ("slice_axes", I * 4),
+        ("slice_starts", I * 4),
+        ("slice_ends", I * 4),
+        ("slice_steps", I * 4),
     ]
 
 

@@ -141,6 +141,40 @@ struct Conv1x1F16Args {
   int act;
 };
 
+// Rank-4 strided copy (k_shape.hip): y[y_off + sum i_k ys_k] =
+// x[x_off + sum i_k xs_k] over 0 <= i_k < dims_k (elements).
+struct StridedCopyArgs {
+  const void* x;
+  void* y;
+  int esize;
+  int f16_round_trip;  // f16: F16::from_f32(to_f32(v)) (the reference's f16 Transpose / Slice)
+  long long dims[4];
+  long long xs[4], ys[4];
+  long long x_off, y_off;
+};
+
+// Broadcasting elementwise op (k_shape.hip): y over dims, every operand
+// addressed by its own strides (0 along a broadcast axis).
+enum BinOp : int { BIN_ADD = 0, BIN_SUB = 1, BIN_MUL = 2, BIN_DIV = 3 };
+struct BinaryArgs {
+  const void* a;
+  const void* b;
+  void* y;
+  int op;
+  int f16;
+  long long dims[4];
+  long long as[4], bs[4], ys[4];
+  long long a_off, b_off, y_off;
+};
+
+// Unpadded NHWC average pool (k_shape.hip).
+struct AvgPoolArgs {
+  const void* x;
+  void* y;
+  int n, h, w, c, kh, kw, sh, sw, ho, wo;
+  int f16;
+};
+
 // Depthwise convolution (channel multiplier 1).
 struct DwArgs {
   const void* x;
@@ -175,6 +209,9 @@ int igemm_candidates(const IgemmArgs& a, int* bc, int* pb, int* tpw, int max);
 
 void launch_direct_conv(hipStream_t st, const DirectArgs& a);
 bool conv1x1_u8_f16_supported(int cin, int cout);
+void launch_strided_copy(hipStream_t st, const StridedCopyArgs& a);
+void launch_broadcast_binary(hipStream_t st, const BinaryArgs& a);
+void launch_avgpool(hipStream_t st, const AvgPoolArgs& a);
 void launch_conv1x1_u8_f16(hipStream_t st, const Conv1x1F16Args& a);
 // HWIO f32 weights [rows][cout] -> [cout / 4][rows][4] (DirectArgs::wq)
 void launch_repack_oc4(hipStream_t st, const float* w, float* wq, int rows, int cout);

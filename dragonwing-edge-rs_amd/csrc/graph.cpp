@@ -192,10 +192,64 @@ int fold_batchnorm(GraphIR& g) {
 // --------------------------------------------------------------------------
 // convert_nchw_to_nhwc (graph.rs:248-290): conv weights [Co,Ci,kh,kw] ->
 // [kh,kw,Ci,Co] (perm [2,3,1,0]); every other 4-D shape [N,C,H,W] ->
-// [N,H,W,C].  The reference leaves Concat/Split axes in NCHW numbering; here
-// they are renumbered (1 -> 3, 2 -> 1, 3 -> 2) so channel concats stay
-// channel concats on NHWC data.
+// [N,H,W,C] (4-D initializers that are not conv weights have their data
+// permuted with them).  Ops whose meaning depends on the memory order are
+// rewritten so the graph still computes what the NCHW model means; the
+// reference changes the shapes only, so its NHWC graphs of such models
+// compute something else:
+//  * Concat / Split / Softmax / Slice axes and Transpose perms of 4-D
+//    tensors are renumbered to the NHWC axes (logical axis 1 -> 3, 2 -> 1,
+//    3 -> 2);
+//  * a Reshape / Flatten that reads a 4-D tensor reads it through a
+//    Transpose to NCHW order, and one that writes a 4-D tensor writes NCHW
+//    order followed by a Transpose to NHWC (skipped when the permutation
+//    only moves dimensions of size 1, where the bytes are the same);
+//  * a constant operand of lower rank broadcast against a 4-D tensor in an
+//    Add / Mul / Sub / Div becomes a 4-D NHWC initializer.
 // --------------------------------------------------------------------------
+namespace {
+constexpr int kPhysOfLogical[4] = {0, 3, 1, 2};  // NCHW axis -> NHWC position
+constexpr int kLogicalOfPhys[4] = {0, 2, 3, 1};  // NHWC position -> NCHW axis
+
+// permute the bytes of a row-major tensor of dims d (esize es) by perm:
+// output axis k is input axis perm[k]
+std::vector<uint8_t> permute_bytes(const std::vector<uint8_t>& src, const std::vector<int64_t>& d,
+                                   const std::vector<int>& perm, int es) {
+  const size_t r = d.size();
+  std::vector<int64_t> od(r), is(r, 1), os(r, 1);
+  for (size_t k = 0; k < r; ++k) od[k] = d[perm[k]];
+  for (int64_t k = (int64_t)r - 2; k >= 0; --k) {
+    is[k] = is[k + 1] * d[k + 1];
+    os[k] = os[k + 1] * od[k + 1];
+  }
+  int64_t total = 1;
+  for (auto v : d) total *= v;
+  std::vector<uint8_t> out(src.size());
+  for (int64_t o = 0; o < total; ++o) {
+    int64_t rem = o, si = 0;
+    for (size_t k = 0; k < r; ++k) {
+      const int64_t c = rem / os[k];
+      rem -= c * os[k];
+      si += c * is[perm[k]];
+    }
+    memcpy(&out[o * es], &src[si * es], es);
+  }
+  return out;
+}
+
+// true when permuting dims d by perm keeps every dimension above 1 in its
+// order, i.e. the row-major bytes do not move
+bool permutation_is_trivial(const std::vector<int64_t>& d, const std::vector<int>& perm) {
+  int last = -1;
+  for (int a : perm) {
+    if (d[a] == 1) continue;
+    if (a < last) return false;
+    last = a;
+  }
+  return true;
+}
+}  // namespace
+
 void convert_nchw_to_nhwc(GraphIR& g) {
   std::set<std::string> weights;
   for (auto& op : g.ops)
@@ -218,15 +272,90 @@ void convert_nchw_to_nhwc(GraphIR& g) {
     W.data.swap(out);
     W.dims = {kh, kw, ci, co};
   }
+  // the NCHW dims of every tensor before conversion
+  std::map<std::string, std::vector<int64_t>> nchw;
+  for (auto& kv : g.t) nchw[kv.first] = kv.second.dims;
   for (auto& kv : g.t) {
     if (weights.count(kv.first) || kv.second.dims.size() != 4) continue;
     auto& d = kv.second.dims;
+    if (kv.second.is_init && !kv.second.data.empty())
+      kv.second.data = permute_bytes(kv.second.data, d, {0, 2, 3, 1}, dtype_size(kv.second.dtype));
     d = {d[0], d[2], d[3], d[1]};
   }
-  static const int remap[4] = {0, 3, 1, 2};
-  for (auto& op : g.ops)
-    if ((op.p.kind == DW_OP_CONCAT || op.p.kind == DW_OP_SPLIT) && op.p.axis >= 0 && op.p.axis < 4)
-      op.p.axis = remap[op.p.axis];
+  auto rank_of = [&](const std::string& n) { return nchw.count(n) ? nchw[n].size() : g.tensor(n).dims.size(); };
+  std::vector<OpNode> out;
+  out.reserve(g.ops.size());
+  auto transpose_op = [&](const std::string& name, const std::string& x, const std::string& y,
+                          const std::vector<int>& perm) {
+    OpNode t;
+    t.name = name;
+    t.type = "LayoutTranspose";  // a pure byte permutation (no f16 value round trip)
+    t.in = {x};
+    t.out = {y};
+    t.p.kind = DW_OP_TRANSPOSE;
+    for (int k = 0; k < 4; ++k) t.p.perm[k] = perm[k];
+    out.push_back(t);
+  };
+  for (OpNode op : g.ops) {
+    const bool in4 = !op.in.empty() && rank_of(op.in[0]) == 4;
+    if ((op.type == "Concat" || op.type == "Split" || op.type == "Softmax") && in4 && op.p.axis >= 0 &&
+        op.p.axis < 4) {
+      op.p.axis = kPhysOfLogical[op.p.axis];
+    } else if (op.type == "Slice" && in4) {
+      for (int k = 0; k < op.p.num_slice_axes; ++k) op.p.slice_axes[k] = kPhysOfLogical[op.p.slice_axes[k]];
+    } else if (op.type == "Transpose" && in4) {
+      // physical output axis j is logical output axis L[j], which is logical
+      // input axis perm[L[j]], found at NHWC position P[perm[L[j]]]
+      int q[4];
+      for (int j = 0; j < 4; ++j) q[j] = kPhysOfLogical[op.p.perm[kLogicalOfPhys[j]]];
+      for (int j = 0; j < 4; ++j) op.p.perm[j] = q[j];
+    } else if ((op.type == "Reshape" || op.type == "Flatten") && !op.in.empty() && !op.out.empty()) {
+      const std::string x = op.in[0], y = op.out[0];
+      if (rank_of(x) == 4 && !permutation_is_trivial(g.tensor(x).dims, {0, 3, 1, 2})) {
+        const std::string xr = x + "__nchw";
+        if (!g.has(xr)) {
+          TensorInfo ti = g.tensor(x);
+          ti.is_init = false;
+          ti.data.clear();
+          ti.dims = nchw[x];
+          g.t[xr] = ti;
+          transpose_op(op.name + "__to_nchw", x, xr, {0, 3, 1, 2});
+        }
+        op.in[0] = xr;
+      }
+      if (rank_of(y) == 4 && !permutation_is_trivial(nchw[y], {0, 2, 3, 1})) {
+        const std::string yr = y + "__nchw";
+        TensorInfo ti = g.tensor(y);
+        ti.dims = nchw[y];
+        g.t[yr] = ti;
+        op.out[0] = yr;
+        out.push_back(op);
+        transpose_op(op.name + "__to_nhwc", yr, y, {0, 2, 3, 1});
+        continue;
+      }
+    } else if ((op.type == "Add" || op.type == "Mul" || op.type == "Sub" || op.type == "Div") &&
+               op.out.size() == 1 && rank_of(op.out[0]) == 4) {
+      for (auto& in : op.in) {
+        if (rank_of(in) == 4) continue;
+        TensorInfo& ti = g.tensor(in);
+        if (ti.numel() == 1) continue;  // a scalar broadcasts the same either way
+        if (!ti.is_init) fail(DW_ERR_UNSUPPORTED, "nhwc: " + op.name + " broadcasts a lower-rank activation");
+        // ONNX aligns trailing dims: pad to 4-D NCHW, then permute to NHWC
+        std::vector<int64_t> d4 = ti.dims;
+        while (d4.size() < 4) d4.insert(d4.begin(), 1);
+        const std::string n4 = in + "__nhwc";
+        if (!g.has(n4)) {
+          TensorInfo t4 = ti;
+          t4.data = permute_bytes(ti.data, d4, {0, 2, 3, 1}, dtype_size(ti.dtype));
+          t4.dims = {d4[0], d4[2], d4[3], d4[1]};
+          g.t[n4] = t4;
+        }
+        in = n4;
+      }
+    }
+    out.push_back(op);
+  }
+  g.ops.swap(out);
 }
 
 // --------------------------------------------------------------------------
@@ -434,9 +563,12 @@ void quantize_qdq(GraphIR& g, const std::set<std::string>& keep_f16) {
   fuse_silu(g);
   // --- shared-scale groups
   UF uf;
+  auto moves_bytes = [](const std::string& ty) {
+    return ty == "Concat" || ty == "Split" || ty == "MaxPool" || ty == "Resize" || ty == "Flatten" ||
+           ty == "Reshape" || ty == "Transpose" || ty == "LayoutTranspose" || ty == "Slice";
+  };
   for (auto& op : g.ops) {
-    if (op.type == "Concat" || op.type == "Split" || op.type == "MaxPool" || op.type == "Resize" ||
-        op.type == "Flatten" || op.type == "Reshape") {
+    if (moves_bytes(op.type)) {
       for (auto& i : op.in)
         if (!g.tensor(i).is_init)
           for (auto& o : op.out) uf.join(i, o);
@@ -448,15 +580,28 @@ void quantize_qdq(GraphIR& g, const std::set<std::string>& keep_f16) {
   // concats of those).
   std::set<std::string> f16t(g.inputs.begin(), g.inputs.end());
   for (auto& in : g.inputs) g.tensor(in).dtype = DW_DTYPE_F16;
+  // The float tail after the kept fp16 layers (a detect head's layout ops,
+  // DFL softmax, box arithmetic, sigmoid): ops of these types that read
+  // only f16 tensors and constants stay f16.
+  static const std::set<std::string> tail_types = {"Concat", "Split", "Reshape", "Flatten", "Transpose",
+                                                   "LayoutTranspose", "Slice", "Softmax", "Sigmoid", "Mul",
+                                                   "Add", "Sub", "Div", "Clip", "Relu", "AveragePool",
+                                                   "YoloDetect"};
+  auto reads_f16_only = [&](const OpNode& op) {
+    bool any = false;
+    for (auto& i : op.in) {
+      if (i.empty() || g.tensor(i).is_init) continue;
+      if (!f16t.count(i)) return false;
+      any = true;
+    }
+    return any;
+  };
   for (auto& op : g.ops) {
     if (op.type == "Conv" && (keep_f16.count(op.name) ||
                               (qdq_model && op.in.size() > 1 && !g.tensor(op.in[1]).prequant)))
       f16t.insert(op.out[0]);
-    if (op.type == "Concat") {
-      bool all = true;
-      for (auto& i : op.in) all = all && f16t.count(i);
-      if (all) f16t.insert(op.out[0]);
-    }
+    else if (tail_types.count(op.type) && reads_f16_only(op))
+      for (auto& o : op.out) f16t.insert(o);
   }
   // group ranges
   std::map<std::string, std::pair<float, float>> grange;
@@ -552,6 +697,26 @@ void quantize_qdq(GraphIR& g, const std::set<std::string>& keep_f16) {
 
   for (size_t oi = 0; oi < g.ops.size(); ++oi) {
     OpNode op = g.ops[oi];
+    if (tail_types.count(op.type) && !op.out.empty() && f16t.count(op.out[0])) {
+      // f16 op of the float tail: its float constants become f16
+      for (auto& i : op.in) {
+        if (i.empty()) continue;
+        TensorInfo& ti = g.tensor(i);
+        if (!ti.is_init || ti.dtype != DW_DTYPE_F32) continue;
+        std::vector<uint8_t> h(ti.data.size() / 2);
+        for (size_t e = 0; e < ti.data.size() / 4; ++e) {
+          float f;
+          memcpy(&f, &ti.data[e * 4], 4);
+          const uint16_t b = f16_from_f32(f);
+          memcpy(&h[e * 2], &b, 2);
+        }
+        ti.data.swap(h);
+        ti.dtype = DW_DTYPE_F16;
+      }
+      for (auto& o : op.out) g.tensor(o).dtype = DW_DTYPE_F16;
+      out.push_back(op);
+      continue;
+    }
     if (op.type == "Conv") {
       TensorInfo& W = g.tensor(op.in[1]);
       if (W.dims.size() != 4) fail(DW_ERR_UNSUPPORTED, "quantize: conv weight must be 4-D (HWIO)");
@@ -650,13 +815,8 @@ void quantize_qdq(GraphIR& g, const std::set<std::string>& keep_f16) {
       out.push_back(op);
       continue;
     }
-    if (op.type == "Concat" && f16t.count(op.out[0])) {
-      g.tensor(op.out[0]).dtype = DW_DTYPE_F16;
-      out.push_back(op);  // f16 concat of fp16 results
-      continue;
-    }
-    if (op.type == "Concat" || op.type == "Split" || op.type == "MaxPool" || op.type == "Resize" ||
-        op.type == "Flatten" || op.type == "Reshape") {
+
+    if (moves_bytes(op.type)) {
       for (auto& i : op.in)
         if (!g.tensor(i).is_init) i = need_u8(i);
       for (auto& o : op.out) make_u8(o);
@@ -792,7 +952,12 @@ std::string to_json(const GraphIR& g) {
       << ",\"trans_b\":" << p.trans_b << ",\"clip_min\":" << fstr(p.clip_min)
       << ",\"clip_max\":" << fstr(p.clip_max) << ",\"reg_max\":" << p.reg_max << ",\"level_strides\":["
       << fstr(p.level_strides[0]) << "," << fstr(p.level_strides[1]) << "," << fstr(p.level_strides[2]) << ","
-      << fstr(p.level_strides[3]) << "]}";
+      << fstr(p.level_strides[3]) << "],\"perm\":[" << p.perm[0] << "," << p.perm[1] << "," << p.perm[2] << ","
+      << p.perm[3] << "],\"slices\":[";
+    for (int k = 0; k < p.num_slice_axes && k < 4; ++k)
+      o << (k ? "," : "") << "[" << p.slice_axes[k] << "," << p.slice_starts[k] << "," << p.slice_ends[k] << ","
+        << p.slice_steps[k] << "]";
+    o << "]}";
   }
   o << "]}";
   return o.str();

@@ -21,6 +21,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <deque>
 #include <functional>
 #include <map>
 #include <set>
@@ -502,7 +503,10 @@ struct Builder {
   const Model& m;
   GraphIR& g;
   std::map<std::string, const Tensor*> init;   // ONNX initializers and Constant values
-  std::vector<Tensor> consts;                  // storage of Constant node values
+  std::deque<Tensor> consts;                   // storage of Constant node values and folded constants
+  // Pad nodes folded into the Conv that reads them: padded tensor ->
+  // (unpadded source, [top, left, bottom, right])
+  std::map<std::string, std::pair<std::string, std::vector<int64_t>>> pads_of;
   std::map<std::string, std::string> alias;    // tensor name -> the name it stands for
   std::map<std::string, std::pair<float, int>> qparams;  // activation -> (scale, zero point)
   std::set<std::string> used_init;
@@ -589,8 +593,89 @@ struct Builder {
   }
   std::string in_name(const std::string& n) {
     const std::string a = A(n);
+    if (pads_of.count(a)) fail(DW_ERR_UNSUPPORTED, "onnx: Pad output '" + a + "' must feed a Conv");
     if (!g.has(a)) use_init(a);
     return a;
+  }
+
+  // ---- constants --------------------------------------------------------
+  const Tensor& add_const(const std::string& name, std::vector<int64_t> dims, int dtype,
+                          std::vector<uint8_t> data) {
+    Tensor t;
+    t.name = name;
+    t.dims = std::move(dims);
+    t.dtype = dtype;
+    t.data = std::move(data);
+    t.require_payload(dtype);
+    consts.push_back(std::move(t));
+    init[name] = &consts.back();
+    return consts.back();
+  }
+  static std::vector<uint8_t> bytes_of(const std::vector<int64_t>& v) {
+    std::vector<uint8_t> b(v.size() * 8);
+    if (!v.empty()) memcpy(b.data(), v.data(), b.size());
+    return b;
+  }
+  static std::vector<uint8_t> bytes_of(const std::vector<float>& v) {
+    std::vector<uint8_t> b(v.size() * 4);
+    if (!v.empty()) memcpy(b.data(), v.data(), b.size());
+    return b;
+  }
+  // a constant's values as f64 (integer or float types)
+  std::vector<double> const_values(const Tensor& t) const {
+    t.require_payload(t.dtype);
+    std::vector<double> v((size_t)t.numel());
+    for (size_t i = 0; i < v.size(); ++i) {
+      switch (t.dtype) {
+        case DT_INT64: { int64_t e; memcpy(&e, &t.data[i * 8], 8); v[i] = (double)e; break; }
+        case DT_INT32: { int32_t e; memcpy(&e, &t.data[i * 4], 4); v[i] = e; break; }
+        case DT_FLOAT: { float e; memcpy(&e, &t.data[i * 4], 4); v[i] = e; break; }
+        case DT_DOUBLE: { double e; memcpy(&e, &t.data[i * 8], 8); v[i] = e; break; }
+        case DT_UINT8: v[i] = t.data[i]; break;
+        case DT_INT8: v[i] = (int8_t)t.data[i]; break;
+        default: fail(DW_ERR_UNSUPPORTED, "onnx: constant '" + t.name + "' of type " + std::to_string(t.dtype));
+      }
+    }
+    return v;
+  }
+  // a constant of type dt holding values v (integers exactly)
+  const Tensor& const_from_values(const std::string& name, std::vector<int64_t> dims, int dt,
+                                  const std::vector<double>& v) {
+    if (dt == DT_INT64 || dt == DT_INT32) {
+      std::vector<int64_t> iv(v.size());
+      for (size_t i = 0; i < v.size(); ++i) iv[i] = (int64_t)v[i];
+      return add_const(name, std::move(dims), DT_INT64, bytes_of(iv));
+    }
+    std::vector<float> fv(v.begin(), v.end());
+    return add_const(name, std::move(dims), DT_FLOAT, bytes_of(fv));
+  }
+  // dims of an activation or a constant
+  std::vector<int64_t> dims_any(const std::string& n) {
+    const std::string a = A(n);
+    if (g.has(a)) return g.tensor(a).dims;
+    const Tensor* t = const_of(a);
+    if (!t) fail(DW_ERR_RUNTIME, "onnx: unknown tensor '" + n + "'");
+    return t->dims;
+  }
+  bool is_const(const std::string& n) const { return !n.empty() && const_of(n) && !g.has(A(n)); }
+  // the axes list of Squeeze / Unsqueeze / ReduceX: an input (opset 13+) or an attribute
+  std::vector<int64_t> axes_of(const Node& n) {
+    if (n.in.size() > 1 && !n.in[1].empty()) return const_ints(n.in[1]);
+    return n.get_ints("axes");
+  }
+
+  // ONNX multidirectional broadcast of two shapes
+  static std::vector<int64_t> broadcast(const std::vector<int64_t>& a, const std::vector<int64_t>& b,
+                                        const std::string& who) {
+    const size_t r = std::max(a.size(), b.size());
+    std::vector<int64_t> o(r);
+    for (size_t k = 0; k < r; ++k) {
+      const int64_t da = k + a.size() >= r ? a[k + a.size() - r] : 1;
+      const int64_t db = k + b.size() >= r ? b[k + b.size() - r] : 1;
+      if (da != db && da != 1 && db != 1) fail(DW_ERR_RUNTIME, "onnx: " + who + ": shapes do not broadcast");
+      o[k] = std::max(da, db);
+    }
+    return o;
   }
 
   void add(const std::string& name, const std::string& type, std::vector<std::string> in,
@@ -764,7 +849,14 @@ struct Builder {
       return;
     }
     if (op == "Conv") {
-      const std::string x = in_name(n.in[0]), w = in_name(n.in[1]);
+      std::vector<int64_t> pre_pad(4, 0);
+      std::string xin = A(n.in[0]);
+      auto pf = pads_of.find(xin);
+      if (pf != pads_of.end()) {
+        pre_pad = pf->second.second;
+        xin = pf->second.first;
+      }
+      const std::string x = in_name(xin), w = in_name(n.in[1]);
       const auto& xd = dims(x);
       const auto& wd = dims(w);
       if (xd.size() != 4 || wd.size() != 4) fail(DW_ERR_UNSUPPORTED, "onnx: Conv " + n.name + " is not 2-D");
@@ -788,6 +880,7 @@ struct Builder {
         pd.assign(4, 0);
       }
       if (pd.empty()) pd.assign(4, 0);
+      for (int k = 0; k < 4; ++k) pd[k] += pre_pad[k];
       const int64_t group = n.get_int("group", 1);
       p.kernel_shape[0] = (int)ks[0]; p.kernel_shape[1] = (int)ks[1];
       p.strides[0] = (int)st[0]; p.strides[1] = (int)st[1];
@@ -824,11 +917,212 @@ struct Builder {
       add(n.name, "Clip", {x}, {n.out[0]}, p);
       return;
     }
-    if (op == "Add" || op == "Mul") {
+    if (op == "Add" || op == "Mul" || op == "Sub" || op == "Div") {
+      const auto da = dims_any(n.in[0]), db = dims_any(n.in[1]);
+      const auto dy = broadcast(da, db, op + " " + n.name);
+      if (is_const(n.in[0]) && is_const(n.in[1])) {
+        // shape arithmetic on constants: folded (scalar or equal-size operands)
+        const Tensor& ta = *const_of(n.in[0]);
+        const Tensor& tb = *const_of(n.in[1]);
+        const auto va = const_values(ta), vb = const_values(tb);
+        if (!(va.size() == vb.size() || va.size() == 1 || vb.size() == 1))
+          fail(DW_ERR_UNSUPPORTED, "onnx: constant " + op + " " + n.name + " with general broadcasting");
+        const bool ints = (ta.dtype == DT_INT64 || ta.dtype == DT_INT32) && (tb.dtype == DT_INT64 || tb.dtype == DT_INT32);
+        std::vector<double> r(std::max(va.size(), vb.size()));
+        for (size_t i = 0; i < r.size(); ++i) {
+          const double x = va[va.size() == 1 ? 0 : i], y = vb[vb.size() == 1 ? 0 : i];
+          if (op == "Add") r[i] = x + y;
+          else if (op == "Sub") r[i] = x - y;
+          else if (op == "Mul") r[i] = x * y;
+          else if (ints) {
+            if (y == 0) fail(DW_ERR_INVALID, "onnx: integer division by zero in " + n.name);
+            r[i] = (double)((int64_t)x / (int64_t)y);  // ONNX integer Div truncates
+          } else {
+            r[i] = (float)x / (float)y;
+          }
+          if (!ints) r[i] = (float)r[i];
+        }
+        const_from_values(n.out[0], dy, ints ? DT_INT64 : DT_FLOAT, r);
+        return;
+      }
       const std::string a = in_name(n.in[0]), b = in_name(n.in[1]);
-      if (dims(a) != dims(b)) fail(DW_ERR_UNSUPPORTED, "onnx: " + op + " " + n.name + " broadcasts");
-      out_like(n, a);
-      add(n.name, op, {a, b}, {n.out[0]}, params(op == "Add" ? DW_OP_ADD : DW_OP_MUL));
+      if (dy.size() > 4) fail(DW_ERR_UNSUPPORTED, "onnx: " + op + " " + n.name + " above rank 4");
+      declare(n.out[0], dy);
+      const int kind = op == "Add" ? DW_OP_ADD : op == "Mul" ? DW_OP_MUL : op == "Sub" ? DW_OP_SUB : DW_OP_DIV;
+      add(n.name, op, {a, b}, {n.out[0]}, params(kind));
+      return;
+    }
+    if (op == "Shape") {
+      const auto d = dims_any(n.in[0]);
+      const int64_t r = (int64_t)d.size();
+      int64_t st = n.get_int("start", 0), en = n.get_int("end", r);
+      if (st < 0) st += r;
+      if (en < 0) en += r;
+      st = std::min(std::max<int64_t>(st, 0), r);
+      en = std::min(std::max<int64_t>(en, st), r);
+      std::vector<int64_t> v(d.begin() + st, d.begin() + en);
+      add_const(n.out[0], {(int64_t)v.size()}, DT_INT64, bytes_of(v));
+      return;
+    }
+    if (op == "Gather") {
+      if (!is_const(n.in[0]) || !is_const(n.in[1]))
+        fail(DW_ERR_UNSUPPORTED, "onnx: Gather " + n.name + " of an activation");
+      const Tensor& td = *const_of(n.in[0]);
+      const Tensor& ti = *const_of(n.in[1]);
+      if (td.dims.size() != 1 || n.get_int("axis", 0) != 0)
+        fail(DW_ERR_UNSUPPORTED, "onnx: Gather " + n.name + ": only 1-D constants along axis 0");
+      const auto vd = const_values(td);
+      const auto vi = const_ints(n.in[1]);
+      std::vector<double> r;
+      for (int64_t k : vi) {
+        const int64_t i = k < 0 ? k + (int64_t)vd.size() : k;
+        if (i < 0 || i >= (int64_t)vd.size()) fail(DW_ERR_INVALID, "onnx: Gather " + n.name + " index out of range");
+        r.push_back(vd[(size_t)i]);
+      }
+      const_from_values(n.out[0], ti.dims, td.dtype, r);
+      return;
+    }
+    if (op == "Unsqueeze" || op == "Squeeze") {
+      auto d = dims_any(n.in[0]);
+      auto ax = axes_of(n);
+      std::vector<int64_t> out;
+      if (op == "Unsqueeze") {
+        const int64_t r = (int64_t)(d.size() + ax.size());
+        for (auto& a : ax) a = a < 0 ? a + r : a;
+        std::sort(ax.begin(), ax.end());
+        out = d;
+        for (int64_t a : ax) {
+          if (a < 0 || a > (int64_t)out.size()) fail(DW_ERR_INVALID, "onnx: Unsqueeze " + n.name + " axis");
+          out.insert(out.begin() + a, 1);
+        }
+      } else {
+        const int64_t r = (int64_t)d.size();
+        for (auto& a : ax) a = a < 0 ? a + r : a;
+        for (int64_t k = 0; k < r; ++k) {
+          const bool drop = ax.empty() ? d[k] == 1 : std::find(ax.begin(), ax.end(), k) != ax.end();
+          if (drop && d[k] != 1) fail(DW_ERR_INVALID, "onnx: Squeeze " + n.name + " of a dimension above 1");
+          if (!drop) out.push_back(d[k]);
+        }
+      }
+      if (is_const(n.in[0])) {
+        const Tensor& t = *const_of(n.in[0]);
+        add_const(n.out[0], out, t.dtype, t.data);
+        return;
+      }
+      const std::string x = in_name(n.in[0]);
+      declare(n.out[0], out);
+      add(n.name, "Reshape", {x}, {n.out[0]}, params(DW_OP_RESHAPE));
+      return;
+    }
+    if (op == "Cast") {
+      if (!is_const(n.in[0])) {
+        // a float activation cast to float: the identity
+        if (n.get_int("to", DT_FLOAT) != DT_FLOAT) fail(DW_ERR_UNSUPPORTED, "onnx: Cast " + n.name + " of an activation");
+        alias[n.out[0]] = A(n.in[0]);
+        return;
+      }
+      const Tensor& t = *const_of(n.in[0]);
+      const int to = (int)n.get_int("to", DT_FLOAT);
+      if (to != DT_FLOAT && to != DT_INT64 && to != DT_INT32)
+        fail(DW_ERR_UNSUPPORTED, "onnx: Cast " + n.name + " to type " + std::to_string(to));
+      auto v = const_values(t);
+      if (to != DT_FLOAT)
+        for (auto& e : v) e = std::trunc(e);
+      const_from_values(n.out[0], t.dims, to, v);
+      return;
+    }
+    if (op == "Transpose") {
+      const std::string x = in_name(n.in[0]);
+      const auto xd = dims(x);
+      std::vector<int64_t> perm = n.get_ints("perm");
+      if (perm.empty())
+        for (int64_t k = (int64_t)xd.size() - 1; k >= 0; --k) perm.push_back(k);
+      if (perm.size() != xd.size() || xd.size() > 4) fail(DW_ERR_UNSUPPORTED, "onnx: Transpose " + n.name + " rank");
+      std::vector<int64_t> od;
+      std::vector<int> seen(xd.size(), 0);
+      for (int64_t a : perm) {
+        if (a < 0 || a >= (int64_t)xd.size() || seen[a]++) fail(DW_ERR_INVALID, "onnx: Transpose " + n.name + " perm");
+        od.push_back(xd[a]);
+      }
+      dw_op_params p = params(DW_OP_TRANSPOSE);
+      for (size_t k = 0; k < 4; ++k) p.perm[k] = k < perm.size() ? (int)perm[k] : (int)k;
+      declare(n.out[0], od);
+      add(n.name, "Transpose", {x}, {n.out[0]}, p);
+      return;
+    }
+    if (op == "Slice") {
+      const std::string x = in_name(n.in[0]);
+      const auto xd = dims(x);
+      const auto st = const_ints(n.in[1]), en = const_ints(n.in[2]);
+      std::vector<int64_t> ax, sp;
+      if (n.in.size() > 3 && !n.in[3].empty()) ax = const_ints(n.in[3]);
+      else for (size_t k = 0; k < st.size(); ++k) ax.push_back((int64_t)k);
+      if (n.in.size() > 4 && !n.in[4].empty()) sp = const_ints(n.in[4]);
+      else sp.assign(st.size(), 1);
+      if (en.size() != st.size() || ax.size() != st.size() || sp.size() != st.size() || st.size() > 4)
+        fail(DW_ERR_INVALID, "onnx: Slice " + n.name + " arguments");
+      dw_op_params p = params(DW_OP_SLICE);
+      auto od = xd;
+      const int64_t r = (int64_t)xd.size();
+      for (size_t k = 0; k < st.size(); ++k) {
+        int64_t a = ax[k] < 0 ? ax[k] + r : ax[k];
+        if (a < 0 || a >= r) fail(DW_ERR_INVALID, "onnx: Slice " + n.name + " axis");
+        if (sp[k] < 1) fail(DW_ERR_UNSUPPORTED, "onnx: Slice " + n.name + " with a step below 1");
+        const int64_t dim = xd[a];
+        // ONNX: negative indices count from the end; both clamped to [0, dim]
+        int64_t s0 = st[k] < 0 ? st[k] + dim : st[k];
+        int64_t e0 = en[k] < 0 ? en[k] + dim : en[k];
+        s0 = std::min(std::max<int64_t>(s0, 0), dim);
+        e0 = std::min(std::max<int64_t>(e0, s0), dim);
+        p.slice_axes[k] = (int)a;
+        p.slice_starts[k] = (int)s0;
+        p.slice_ends[k] = (int)e0;
+        p.slice_steps[k] = (int)sp[k];
+        od[a] = (e0 - s0 + sp[k] - 1) / sp[k];
+      }
+      p.num_slice_axes = (int)st.size();
+      declare(n.out[0], od);
+      add(n.name, "Slice", {x}, {n.out[0]}, p);
+      return;
+    }
+    if (op == "AveragePool") {
+      const std::string x = in_name(n.in[0]);
+      const auto& xd = dims(x);
+      if (xd.size() != 4) fail(DW_ERR_UNSUPPORTED, "onnx: AveragePool " + n.name + " is not 2-D");
+      if (n.get_int("ceil_mode", 0)) fail(DW_ERR_UNSUPPORTED, "onnx: AveragePool ceil_mode");
+      const auto ks = n.get_ints("kernel_shape");
+      auto st = n.get_ints("strides");
+      auto pd = n.get_ints("pads");
+      if (ks.size() != 2) fail(DW_ERR_UNSUPPORTED, "onnx: AveragePool kernel_shape");
+      if (st.empty()) st = {1, 1};
+      for (auto v : pd)
+        if (v != 0) fail(DW_ERR_UNSUPPORTED, "onnx: padded AveragePool " + n.name);
+      const std::string ap = n.get_string("auto_pad", "NOTSET");
+      if (ap != "NOTSET" && ap != "VALID") fail(DW_ERR_UNSUPPORTED, "onnx: AveragePool auto_pad " + ap);
+      dw_op_params p = params(DW_OP_AVGPOOL);
+      p.kernel_shape[0] = (int)ks[0]; p.kernel_shape[1] = (int)ks[1];
+      p.strides[0] = (int)st[0]; p.strides[1] = (int)st[1];
+      declare(n.out[0], {xd[0], xd[1], (xd[2] - ks[0]) / st[0] + 1, (xd[3] - ks[1]) / st[1] + 1});
+      add(n.name, "AveragePool", {x}, {n.out[0]}, p);
+      return;
+    }
+    if (op == "Pad") {
+      // a constant zero spatial pad is folded into the Conv that reads it
+      if (n.get_string("mode", "constant") != "constant") fail(DW_ERR_UNSUPPORTED, "onnx: Pad mode");
+      const std::string x = A(n.in[0]);
+      const auto xd = dims_any(x);
+      std::vector<int64_t> pd = n.in.size() > 1 && !n.in[1].empty() ? const_ints(n.in[1]) : n.get_ints("pads");
+      if (n.in.size() > 2 && !n.in[2].empty()) {
+        const auto v = const_values(*const_of(n.in[2]));
+        if (!v.empty() && v[0] != 0.0) fail(DW_ERR_UNSUPPORTED, "onnx: Pad " + n.name + " with a nonzero value");
+      }
+      if (n.in.size() > 3 && !n.in[3].empty()) fail(DW_ERR_UNSUPPORTED, "onnx: Pad axes");
+      if (xd.size() != 4 || pd.size() != 8 || pd[0] || pd[1] || pd[4] || pd[5])
+        fail(DW_ERR_UNSUPPORTED, "onnx: Pad " + n.name + " other than spatial on a 4-D tensor");
+      for (auto v : pd)
+        if (v < 0) fail(DW_ERR_UNSUPPORTED, "onnx: negative Pad");
+      if (pads_of.count(x)) fail(DW_ERR_UNSUPPORTED, "onnx: Pad of a Pad");
+      pads_of[n.out[0]] = {x, {pd[2], pd[3], pd[6], pd[7]}};
       return;
     }
     if (op == "MaxPool") {
@@ -852,6 +1146,21 @@ struct Builder {
       return;
     }
     if (op == "Concat") {
+      bool all_const = true;
+      for (auto& i : n.in) all_const = all_const && is_const(i);
+      if (all_const) {
+        std::vector<double> v;
+        int dt = DT_INT64;
+        for (auto& i : n.in) {
+          const Tensor& t = *const_of(i);
+          if (t.dims.size() > 1) fail(DW_ERR_UNSUPPORTED, "onnx: Concat " + n.name + " of constants above rank 1");
+          if (t.dtype != DT_INT64 && t.dtype != DT_INT32) dt = DT_FLOAT;
+          const auto tv = const_values(t);
+          v.insert(v.end(), tv.begin(), tv.end());
+        }
+        const_from_values(n.out[0], {(int64_t)v.size()}, dt, v);
+        return;
+      }
       std::vector<std::string> ins;
       for (auto& i : n.in) ins.push_back(in_name(i));
       auto d = dims(ins[0]);
@@ -959,8 +1268,19 @@ struct Builder {
     }
     if (op == "Softmax") {
       const std::string x = in_name(n.in[0]);
+      const auto xd = dims(x);
+      const int64_t r = (int64_t)xd.size();
+      int64_t axis = n.get_int("axis", m.opset >= 13 ? -1 : 1);
+      if (axis < 0) axis += r;
+      if (axis < 0 || axis >= r) fail(DW_ERR_INVALID, "onnx: Softmax " + n.name + " axis");
+      if (m.opset < 13) {
+        // opset < 13: softmax over the flattened dimensions from axis on,
+        // which is the per-axis softmax when every later dimension is 1
+        for (int64_t k = axis + 1; k < r; ++k)
+          if (xd[k] != 1) fail(DW_ERR_UNSUPPORTED, "onnx: opset < 13 Softmax " + n.name + " over several axes");
+      }
       dw_op_params p = params(DW_OP_SOFTMAX);
-      p.axis = (int)n.get_int("axis", -1);
+      p.axis = (int)axis;
       out_like(n, x);
       add(n.name, "Softmax", {x}, {n.out[0]}, p);
       return;

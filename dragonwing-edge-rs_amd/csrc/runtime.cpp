@@ -195,6 +195,18 @@ struct Runtime {
   void emit_qconv(const Group& gr);
   void emit_ew(const OpNode& op);
   void emit_iconv(const Group& gr);
+  void emit_shape(const Group& gr);
+  // a tensor as a rank-4 index space (its dims padded with leading 1s) with
+  // the element strides and offset of its storage
+  struct Addr4 {
+    void* base = nullptr;
+    long long d[4] = {1, 1, 1, 1};
+    long long st[4] = {0, 0, 0, 1};
+    long long off = 0;
+    int es = 1;
+    int rank = 0;
+  };
+  Addr4 addr4(const std::string& name);
   void normalize();
   void push_igemm(Launch& L, const IgemmArgs& a, int esize);
   void autotune();
@@ -417,11 +429,19 @@ void Runtime::normalize() {
   }
   for (auto& op : g.ops) {
     if (op.type != "Concat" && op.type != "Split") continue;
-    if (op.p.axis == 3 || op.in.empty() || op.out.empty()) continue;
-    std::vector<const RtTensor*> parts;
+    if (op.in.empty() || op.out.empty()) continue;
     const bool cat = op.type == "Concat";
+    const std::string& whole = cat ? op.out[0] : op.in[0];
+    const int rank = (int)g.t[whole].dims.size();
+    if (op.p.axis < 0) op.p.axis += rank;
+    if (rank == 4 && op.p.axis == 3) continue;
+    std::vector<const RtTensor*> parts;
     for (auto& n : cat ? op.in : op.out) parts.push_back(&T(n));
-    if (op.p.axis == 1 && channel_join(parts, T(cat ? op.out[0] : op.in[0]))) op.p.axis = 3;
+    // axis 3 below means the channel (last) axis of the rows x channels
+    // view; other axes are joined by copies
+    const bool last = rank != 4 && op.p.axis == rank - 1;
+    if ((last || (rank == 4 && op.p.axis == 1)) && channel_join(parts, T(whole))) op.p.axis = 3;
+    else if (rank != 4) op.p.axis += 4 - rank;  // as an axis of the rank-4 index space
   }
 }
 
@@ -830,9 +850,19 @@ void Runtime::lower(std::vector<Group>& groups) {
       if (!op.p.mode_nearest) fail(DW_ERR_UNSUPPORTED, "runtime: only nearest Resize is implemented");
       gr.kind = "resize";
     } else if (op.type == "Concat") {
-      gr.kind = "concat";
+      gr.kind = op.p.axis == 3 ? "concat" : "concat_copy";
     } else if (op.type == "Split") {
-      gr.kind = "split";
+      gr.kind = op.p.axis == 3 ? "split" : "split_copy";
+    } else if (op.type == "Transpose" || op.type == "LayoutTranspose") {
+      gr.kind = "transpose";
+    } else if (op.type == "Slice") {
+      gr.kind = "slice";
+    } else if (op.type == "AveragePool") {
+      gr.kind = "avgpool";
+    } else if (op.type == "Sub" || op.type == "Div" ||
+               ((op.type == "Add" || op.type == "Mul") && op.in.size() == 2 &&
+                (g.t[op.in[0]].is_init || g.t[op.in[1]].is_init || g.t[op.in[0]].dims != g.t[op.in[1]].dims))) {
+      gr.kind = "bin";
     } else if (op.type == "Relu" || op.type == "Sigmoid" || op.type == "Mul" || op.type == "Add" ||
                op.type == "SiLU" || op.type == "QLinearLUT" || op.type == "QLinearAdd" ||
                op.type == "QuantizeLinear" || op.type == "DequantizeLinear" || op.type == "Requantize" ||
@@ -878,6 +908,14 @@ void Runtime::place(const std::vector<Group>& groups) {
     }
     return t;
   };
+  // Producers that write dense tensors only (no channel-strided output
+  // view): their outputs are copied into a concat buffer, not placed in it.
+  std::set<std::string> dense_only;
+  for (auto& gr : groups)
+    if (gr.kind == "flatten" || gr.kind == "softmax" || gr.kind == "gemm" || gr.kind == "gap" ||
+        gr.kind == "avgpool" || gr.kind == "detect")
+      for (int oi : gr.ops)
+        for (auto& o : g.ops[oi].out) dense_only.insert(o);
   // Concats, last first, so nested placements resolve through parents.
   for (auto it = groups.rbegin(); it != groups.rend(); ++it) {
     if (it->kind != "concat") continue;
@@ -898,7 +936,7 @@ void Runtime::place(const std::vector<Group>& groups) {
       const std::string r = root_of(pr.first, roff);
       if (r.empty()) continue;
       const int d = pr.second - roff;
-      if (protect.count(r) || g.t[r].is_init || !T(r).parent.empty() || r == out ||
+      if (protect.count(r) || g.t[r].is_init || !T(r).parent.empty() || r == out || dense_only.count(r) ||
           T(r).dtype != T(out).dtype || d < 0 || d + T(r).c > total || (d % 16) != 0 || (total % 16) != 0 ||
           T(r).pixels() != T(out).pixels()) {
         bad.insert(r);
@@ -1206,7 +1244,44 @@ void Runtime::emit(const Group& gr) {
     launches.push_back(L);
     return;
   }
-  if (gr.kind == "gap" || gr.kind == "gemm" || gr.kind == "flatten" || gr.kind == "softmax") {
+  if (gr.kind == "transpose" || gr.kind == "slice" || gr.kind == "bin" || gr.kind == "avgpool" ||
+      gr.kind == "concat_copy" || gr.kind == "split_copy")
+    return emit_shape(gr);
+  if (gr.kind == "flatten") {
+    // Reshape / Flatten: the row-major order of the elements is kept; a
+    // dense input is one copy, a channel view a strided one
+    const OpNode& op = g.ops[gr.ops[0]];
+    RtTensor& x = T(op.in[0]);
+    RtTensor& y = T(op.out[0]);
+    if (x.bytes() != y.bytes() || x.dtype != y.dtype) fail(DW_ERR_RUNTIME, op.type + " " + op.name + ": element count");
+    Launch L;
+    L.op = op.name;
+    L.bytes = (double)x.bytes() + y.bytes();
+    if (y.pix_stride != y.c || y.abs_off != 0) fail(DW_ERR_RUNTIME, op.type + " " + op.name + ": output view");
+    if (x.pix_stride == x.c && x.abs_off == 0) {
+      const void* xb = x.base;
+      void* yb = y.base;
+      const size_t nb = x.bytes();
+      L.kernel = "copy";
+      L.fn = [=](hipStream_t st) { DW_HIP(hipMemcpyAsync(yb, xb, nb, hipMemcpyDeviceToDevice, st)); };
+    } else {
+      StridedCopyArgs c{};
+      c.x = x.base;
+      c.y = y.base;
+      c.esize = dtype_size(x.dtype);
+      c.dims[0] = c.dims[1] = 1;
+      c.dims[2] = x.pixels();
+      c.dims[3] = x.c;
+      c.xs[2] = x.pix_stride; c.xs[3] = 1;
+      c.ys[2] = x.c; c.ys[3] = 1;
+      c.x_off = x.abs_off;
+      L.kernel = "strided_copy";
+      L.fn = [=](hipStream_t st) { launch_strided_copy(st, c); };
+    }
+    launches.push_back(L);
+    return;
+  }
+  if (gr.kind == "gap" || gr.kind == "gemm" || gr.kind == "softmax") {
     // classifier-head ops: dense tensors only
     const OpNode& op = g.ops[gr.ops[0]];
     RtTensor& x = T(op.in[0]);
@@ -1223,7 +1298,11 @@ void Runtime::emit(const Group& gr) {
     void* yb = y.base;
     if (gr.kind == "softmax") {
       // CpuGraphRuntime::dispatch_softmax (runtime.rs:1288-1326): along the
-      // last dimension whatever the axis attribute says
+      // last dimension; an axis other than the last is refused (after
+      // convert_nchw_to_nhwc, a 4-D tensor's axes are NHWC positions)
+      const int rank = (int)g.t[op.in[0]].dims.size();
+      const int ax = op.p.axis < 0 ? op.p.axis + rank : op.p.axis;
+      if (ax != rank - 1) fail(DW_ERR_UNSUPPORTED, "Softmax " + op.name + ": only along the last axis");
       if (y.dtype != dt || x.bytes() != y.bytes()) fail(DW_ERR_RUNTIME, "Softmax: output shape or dtype");
       const int rows = (int)x.pixels(), n = (int)x.c;
       L.kernel = "softmax";
@@ -1243,11 +1322,6 @@ void Runtime::emit(const Group& gr) {
       } else {
         L.fn = [=](hipStream_t st) { launch_global_avg_pool(st, dt, xb, yb, n, hw, c); };
       }
-    } else if (gr.kind == "flatten") {
-      if (x.bytes() != y.bytes()) fail(DW_ERR_RUNTIME, "Flatten: element count");
-      const size_t nb = x.bytes();
-      L.kernel = "copy";
-      L.fn = [=](hipStream_t st) { DW_HIP(hipMemcpyAsync(yb, xb, nb, hipMemcpyDeviceToDevice, st)); };
     } else {
       // Gemm / MatMul (dispatch_gemm, onnx runtime.rs:1178-1275): A [m][k]
       // activation, B an initializer ([k][n], or [n][k] with trans_b),
@@ -1322,6 +1396,156 @@ void Runtime::emit(const Group& gr) {
   }
   if (gr.kind == "ew") return emit_ew(g.ops[gr.ops[0]]);
   fail(DW_ERR_RUNTIME, "runtime: unhandled group " + gr.kind);
+}
+
+Runtime::Addr4 Runtime::addr4(const std::string& name) {
+  const TensorInfo& ti = g.t.at(name);
+  Addr4 a;
+  a.rank = (int)ti.dims.size();
+  if (a.rank > 4) fail(DW_ERR_UNSUPPORTED, "runtime: '" + name + "' above rank 4");
+  for (int k = 0; k < a.rank; ++k) a.d[4 - a.rank + k] = ti.dims[k];
+  a.es = dtype_size(ti.dtype);
+  if (ti.is_init) {
+    a.base = upload(ti.data.data(), ti.data.size());
+    a.st[3] = 1;
+    for (int k = 2; k >= 0; --k) a.st[k] = a.st[k + 1] * a.d[k + 1];
+    return a;
+  }
+  const RtTensor& r = T(name);
+  if (a.d[3] != r.c) fail(DW_ERR_RUNTIME, "runtime: '" + name + "' layout");
+  // rows of the last dimension, pix_stride elements apart
+  a.base = r.base;
+  a.off = r.abs_off;
+  a.st[3] = 1;
+  a.st[2] = r.pix_stride;
+  a.st[1] = a.d[2] * a.st[2];
+  a.st[0] = a.d[1] * a.st[1];
+  return a;
+}
+
+// Transpose, Slice, broadcasting Add / Sub / Mul / Div, AveragePool, and
+// Concat / Split along a non-channel axis (k_shape.hip).
+void Runtime::emit_shape(const Group& gr) {
+  const OpNode& op = g.ops[gr.ops[0]];
+  Launch L;
+  L.op = op.name;
+  auto copy_launch = [&](const StridedCopyArgs& c, const std::string& what) {
+    Launch C = L;
+    C.op = what;
+    C.kernel = "strided_copy";
+    C.bytes = 2.0 * c.dims[0] * c.dims[1] * c.dims[2] * c.dims[3] * c.esize;
+    C.fn = [c](hipStream_t st) { launch_strided_copy(st, c); };
+    launches.push_back(C);
+  };
+  if (gr.kind == "transpose" || gr.kind == "slice") {
+    const Addr4 x = addr4(op.in[0]), y = addr4(op.out[0]);
+    if (x.es != y.es || x.rank != y.rank) fail(DW_ERR_RUNTIME, op.type + " " + op.name + ": operand types");
+    StridedCopyArgs c{};
+    c.x = x.base;
+    c.y = y.base;
+    c.esize = x.es;
+    // the reference's f16 Transpose / Slice go through f32 (runtime.rs:2073-2084, :2130-2140)
+    c.f16_round_trip = op.type != "LayoutTranspose" && T(op.in[0]).dtype == F16;
+    c.x_off = x.off;
+    c.y_off = y.off;
+    for (int k = 0; k < 4; ++k) {
+      c.dims[k] = y.d[k];
+      c.ys[k] = y.st[k];
+    }
+    const int lead = 4 - x.rank;
+    if (gr.kind == "transpose") {
+      for (int k = 0; k < 4; ++k) {
+        const int src = k < lead ? k : lead + op.p.perm[k - lead];
+        if (src < 0 || src > 3 || x.d[src] != y.d[k]) fail(DW_ERR_RUNTIME, "Transpose " + op.name + ": perm");
+        c.xs[k] = x.st[src];
+      }
+    } else {
+      for (int k = 0; k < 4; ++k) c.xs[k] = x.st[k];
+      for (int i = 0; i < op.p.num_slice_axes; ++i) {
+        const int ax = lead + op.p.slice_axes[i];
+        if (ax < 0 || ax > 3) fail(DW_ERR_RUNTIME, "Slice " + op.name + ": axis");
+        c.x_off += (long long)op.p.slice_starts[i] * x.st[ax];
+        c.xs[ax] *= op.p.slice_steps[i];
+      }
+    }
+    copy_launch(c, op.name);
+    return;
+  }
+  if (gr.kind == "concat_copy" || gr.kind == "split_copy") {
+    const bool cat = gr.kind == "concat_copy";
+    const std::string& whole = cat ? op.out[0] : op.in[0];
+    const Addr4 w = addr4(whole);
+    const int ax = op.p.axis;
+    if (ax < 0 || ax > 3) fail(DW_ERR_RUNTIME, op.type + " " + op.name + ": axis");
+    long long off = 0;
+    for (auto& part : cat ? op.in : op.out) {
+      const Addr4 pa = addr4(part);
+      StridedCopyArgs c{};
+      c.esize = pa.es;
+      for (int k = 0; k < 4; ++k) c.dims[k] = pa.d[k];
+      if (cat) {
+        c.x = pa.base; c.y = w.base;
+        c.x_off = pa.off;
+        c.y_off = w.off + off * w.st[ax];
+        for (int k = 0; k < 4; ++k) { c.xs[k] = pa.st[k]; c.ys[k] = w.st[k]; }
+      } else {
+        c.x = w.base; c.y = pa.base;
+        c.x_off = w.off + off * w.st[ax];
+        c.y_off = pa.off;
+        for (int k = 0; k < 4; ++k) { c.xs[k] = w.st[k]; c.ys[k] = pa.st[k]; }
+      }
+      off += pa.d[ax];
+      copy_launch(c, op.name + ":" + part);
+    }
+    if (off != w.d[ax]) fail(DW_ERR_RUNTIME, op.type + " " + op.name + ": sizes along the axis");
+    return;
+  }
+  if (gr.kind == "bin") {
+    const Addr4 a = addr4(op.in[0]), b = addr4(op.in[1]), y = addr4(op.out[0]);
+    const int dt = T(op.out[0]).dtype;
+    if (dt != F32 && dt != F16) fail(DW_ERR_UNSUPPORTED, op.type + " " + op.name + " needs f32 or f16");
+    if (g.t[op.in[0]].dtype != dt || g.t[op.in[1]].dtype != dt)
+      fail(DW_ERR_RUNTIME, op.type + " " + op.name + ": operand element types");
+    BinaryArgs e{};
+    e.a = a.base; e.b = b.base; e.y = y.base;
+    e.a_off = a.off; e.b_off = b.off; e.y_off = y.off;
+    e.f16 = dt == F16;
+    e.op = op.type == "Add" ? BIN_ADD : op.type == "Sub" ? BIN_SUB : op.type == "Mul" ? BIN_MUL : BIN_DIV;
+    for (int k = 0; k < 4; ++k) {
+      e.dims[k] = y.d[k];
+      e.ys[k] = y.st[k];
+      // a size-1 axis broadcasts (stride 0)
+      if ((a.d[k] != y.d[k] && a.d[k] != 1) || (b.d[k] != y.d[k] && b.d[k] != 1))
+        fail(DW_ERR_RUNTIME, op.type + " " + op.name + ": operands do not broadcast to the output");
+      e.as[k] = a.d[k] == 1 ? 0 : a.st[k];
+      e.bs[k] = b.d[k] == 1 ? 0 : b.st[k];
+    }
+    L.kernel = "broadcast_binary";
+    L.bytes = (double)(y.d[0] * y.d[1] * y.d[2] * y.d[3]) * y.es * 3.0;
+    L.fn = [e](hipStream_t st) { launch_broadcast_binary(st, e); };
+    launches.push_back(L);
+    return;
+  }
+  // avgpool
+  RtTensor& x = T(op.in[0]);
+  RtTensor& y = T(op.out[0]);
+  if (x.dtype != y.dtype || (x.dtype != F32 && x.dtype != F16))
+    fail(DW_ERR_UNSUPPORTED, "AveragePool " + op.name + " needs f32 or f16");
+  if (x.pix_stride != x.c || x.abs_off != 0 || y.pix_stride != y.c || y.abs_off != 0)
+    fail(DW_ERR_RUNTIME, "AveragePool " + op.name + ": channel views");
+  AvgPoolArgs a{};
+  a.x = x.base; a.y = y.base;
+  a.n = (int)x.n; a.h = (int)x.h; a.w = (int)x.w; a.c = (int)x.c;
+  a.kh = op.p.kernel_shape[0]; a.kw = op.p.kernel_shape[1];
+  a.sh = std::max(1, op.p.strides[0]); a.sw = std::max(1, op.p.strides[1]);
+  a.ho = (int)y.h; a.wo = (int)y.w;
+  a.f16 = x.dtype == F16;
+  if (a.ho != (a.h - a.kh) / a.sh + 1 || a.wo != (a.w - a.kw) / a.sw + 1 || y.c != x.c || y.n != x.n)
+    fail(DW_ERR_RUNTIME, "AveragePool " + op.name + ": output shape");
+  L.kernel = "avgpool";
+  L.bytes = (double)x.bytes() + y.bytes();
+  L.fn = [a](hipStream_t st) { launch_avgpool(st, a); };
+  launches.push_back(L);
 }
 
 void Runtime::emit_ew(const OpNode& op) {

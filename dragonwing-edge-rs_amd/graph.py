@@ -25,7 +25,7 @@ OP_KIND = {
     "Resize": 8, "BatchNorm": 9, "Requantize": 10, "AddQuantized": 11, "Quantize": 12, "Dequantize": 13,
     "Conv2dRequantReluI8Nhwc": 14, "QLinearConv": 32, "QuantizeLinear": 33, "DequantizeLinear": 34,
     "QLinearAdd": 35, "QLinearLUT": 36, "Gemm": 15, "GlobalAvgPool": 16, "Softmax": 17, "Clip": 18,
-    "Reshape": 19, "YoloDetect": 37,
+    "Reshape": 19, "YoloDetect": 37, "AvgPool": 20, "Sub": 21, "Div": 22, "Transpose": 23, "Slice": 24,
 }
 # default OpParams kind per op_type
 KIND_OF_TYPE = {"Conv": "Conv2d", "Add": "Add", "Mul": "Mul", "Sigmoid": "Sigmoid", "MaxPool": "MaxPool",
@@ -34,7 +34,8 @@ KIND_OF_TYPE = {"Conv": "Conv2d", "Add": "Add", "Mul": "Mul", "Sigmoid": "Sigmoi
                 "GlobalAveragePool": "GlobalAvgPool", "Softmax": "Softmax", "Clip": "Clip",
                 "Reshape": "Reshape", "Requantize": "Requantize", "AddQuantized": "AddQuantized",
                 "Quantize": "Quantize", "Dequantize": "Dequantize",
-                "Conv2dRequantReluI8": "Conv2dRequantReluI8Nhwc", "YoloDetect": "YoloDetect"}
+                "Conv2dRequantReluI8": "Conv2dRequantReluI8Nhwc", "YoloDetect": "YoloDetect",
+                "AveragePool": "AvgPool", "Sub": "Sub", "Div": "Div", "Transpose": "Transpose", "Slice": "Slice"}
 
 
 def _params(kind: str, **kw) -> DwOpParams:
@@ -69,6 +70,12 @@ def _params(kind: str, **kw) -> DwOpParams:
     ls = list(kw.get("level_strides", ()))
     for i, v in enumerate(ls[:4]):
         p.level_strides[i] = float(v)
+    for i, v in enumerate(kw.get("perm", ())):
+        p.perm[i] = int(v)
+    sl = kw.get("slices", ())  # (axis, start, end, step) per sliced axis, resolved
+    p.num_slice_axes = len(sl)
+    for i, (ax, st, en, sp) in enumerate(sl):
+        p.slice_axes[i], p.slice_starts[i], p.slice_ends[i], p.slice_steps[i] = ax, st, en, sp
     return p
 
 

@@ -395,6 +395,11 @@ typedef enum dw_op_kind {
   DW_OP_SOFTMAX = 17,    /* OpParams::Softmax { axis } (axis = last dim only)  */
   DW_OP_CLIP = 18,       /* OpParams::Clip { min, max }                        */
   DW_OP_RESHAPE = 19,    /* OpParams::Reshape (the output tensor's dims)       */
+  DW_OP_AVGPOOL = 20,    /* OpParams::AvgPool { kernel_shape, strides, pads }  */
+  DW_OP_SUB = 21,        /* OpParams::Sub                                      */
+  DW_OP_DIV = 22,        /* OpParams::Div                                      */
+  DW_OP_TRANSPOSE = 23,  /* OpParams::Transpose { perm }                       */
+  DW_OP_SLICE = 24,      /* OpParams::Slice { starts, ends, axes, steps }      */
   /* extensions */
   DW_OP_QLINEAR_CONV = 32,  /* QLinearConv (+ fused LUT activation, + QLinearAdd residual) */
   DW_OP_QUANTIZE_LINEAR = 33,
@@ -428,6 +433,12 @@ typedef struct dw_op_params {
   float clip_min, clip_max; /* Clip                                           */
   int reg_max;              /* YoloDetect: DFL bins per box side               */
   float level_strides[4];   /* YoloDetect: stride of each input level          */
+  int perm[4];              /* Transpose: output axis k is input axis perm[k]  */
+  int num_slice_axes;       /* Slice: entries used in the four arrays below    */
+  int slice_axes[4];        /* Slice: axis of each entry                       */
+  int slice_starts[4];      /* Slice: first index (resolved: 0 <= start <= dim) */
+  int slice_ends[4];        /* Slice: end index (resolved: start <= end <= dim) */
+  int slice_steps[4];       /* Slice: step (>= 1)                              */
 } dw_op_params;
 
 /* sizeof(dw_op_params) as compiled into the library.  A binding that declares
@@ -441,10 +452,15 @@ size_t dw_op_params_size(void);
  * parses a serialized ModelProto (opset 12 to 20) and builds an F32 graph in
  * ONNX's NCHW layout, ready for dw_graph_fold_batchnorm,
  * dw_graph_convert_nchw_to_nhwc and the rest.  Ops: Conv, Relu, Sigmoid,
- * Clip, Add, Mul (same shapes), MaxPool, Concat, Split, Resize / Upsample
- * (nearest, constant scales or sizes), BatchNormalization,
- * GlobalAveragePool, Flatten, Reshape, Softmax, Gemm, MatMul, Constant,
- * Identity.  A QDQ model (QuantizeLinear / DequantizeLinear, u8 activations,
+ * Clip, Add, Sub, Mul, Div (ONNX broadcasting), MaxPool, AveragePool
+ * (unpadded), Concat, Split, Slice, Transpose, Resize / Upsample (nearest,
+ * constant scales or sizes), BatchNormalization, GlobalAveragePool,
+ * Flatten, Reshape, Squeeze / Unsqueeze (as Reshape), Softmax, Gemm,
+ * MatMul, Constant, Identity, Cast of a float activation to float; Shape,
+ * Gather, Unsqueeze, Squeeze, Concat, Cast and Add / Sub / Mul / Div of
+ * constants are folded into constants (the shape arithmetic of
+ * unsimplified exports); a constant zero spatial Pad read by a Conv is
+ * folded into the Conv's pads.  A QDQ model (QuantizeLinear / DequantizeLinear, u8 activations,
  * symmetric s8 weights, int32 biases) loads as the float graph with its
  * quantization fixed, which dw_graph_quantize_qdq then uses as given (no
  * calibration).  dw_onnx_inspect writes a JSON summary of the parsed model

@@ -607,3 +607,71 @@ def qlinear_gap_u8(x, x_scale, x_zp, y_scale, y_zp):
     y = np.empty((n, c), np.uint8)
     lib().dwo_qlinear_gap_u8(_p(y), _p(x), n, h, w, c, x_scale, x_zp, y_scale, y_zp)
     return y
+
+
+# --- Part D: layout ops, broadcasting, average pool (numpy restatements) -----
+
+def _f16_round_trip(y):
+    """F16::from_f32(to_f32(v)): the identity except subnormals (halved by
+    the decode) and NaN payloads (dtype.rs:164-263)."""
+    return f16_from_f32(f16_to_f32(y))
+
+
+def transpose(x, perm, f16_round_trip=True):
+    """transpose_f32 (crates/dragonwing-cpu/src/ops.rs:2468-2520) on a tensor
+    of rank <= 4 stored row-major: output axis k is input axis perm[k].  An
+    f16 tensor goes through to_f32 / from_f32 (dispatch_transpose,
+    crates/dragonwing-onnx/src/runtime.rs:2073-2084) unless the transpose is
+    a pure layout change (f16_round_trip False)."""
+    y = np.ascontiguousarray(np.transpose(np.asarray(x), perm))
+    return _f16_round_trip(y) if f16_round_trip and y.dtype == np.uint16 else y
+
+
+def slice_axes(x, slices, f16_round_trip=True):
+    """slice_f32 (ops.rs:2532-2570) with resolved (axis, start, end, step)
+    entries (0 <= start <= end <= dim, step >= 1); f16 through f32 as
+    dispatch_slice does (runtime.rs:2130-2140)."""
+    idx = [slice(None)] * np.asarray(x).ndim
+    for ax, st, en, sp in slices:
+        idx[ax] = slice(st, en, sp)
+    y = np.ascontiguousarray(np.asarray(x)[tuple(idx)])
+    return _f16_round_trip(y) if f16_round_trip and y.dtype == np.uint16 else y
+
+
+_BIN = {"Add": np.add, "Sub": np.subtract, "Mul": np.multiply, "Div": np.divide}
+
+
+def binary(op, a, b):
+    """Add / Sub / Mul / Div: one f32 operation per element (add_f32 ops.rs:363-384,
+    sub_f32 :1978-2003, mul_f32 :1899-1919, div_f32 :2057-2082); f16
+    operands widened with to_f32 and the result stored with from_f32
+    (add_fp16 :434-442, sub_fp16 :2038-2046, mul_fp16 :1959-1967,
+    div_fp16 :2117-2125).  Broadcasting: the runtime's b[i % len(b)] loops
+    (runtime.rs:1045-1860) for a second operand that tiles the first are
+    numpy's trailing broadcast; a smaller first operand broadcasts the same
+    way (ONNX multidirectional broadcasting)."""
+    a, b = np.asarray(a), np.asarray(b)
+    f16 = a.dtype == np.uint16
+    af = f16_to_f32(a) if f16 else a.astype(np.float32)
+    bf = f16_to_f32(b) if f16 else b.astype(np.float32)
+    with np.errstate(all="ignore"):
+        r = _BIN[op](af, bf, dtype=np.float32)
+    return f16_from_f32(r) if f16 else np.ascontiguousarray(r, np.float32)
+
+
+def avgpool2d_nhwc(x, k, s):
+    """avgpool2d_f32_nhwc (ops.rs:1556-1595): unpadded windows, the sum over
+    ph then pw in f32, then one division by kh * kw; f16 tensors widened
+    with to_f32 and the average stored with from_f32 (runtime.rs:1571-1630)."""
+    x = np.asarray(x)
+    f16 = x.dtype == np.uint16
+    xf = f16_to_f32(x) if f16 else x.astype(np.float32)
+    n, h, w, c = xf.shape
+    (kh, kw), (sh, sw) = k, s
+    ho, wo = (h - kh) // sh + 1, (w - kw) // sw + 1
+    acc = np.zeros((n, ho, wo, c), np.float32)
+    for ph in range(kh):
+        for pw in range(kw):
+            acc = (acc + xf[:, ph:ph + (ho - 1) * sh + 1:sh, pw:pw + (wo - 1) * sw + 1:sw, :]).astype(np.float32)
+    r = (acc / np.float32(kh * kw)).astype(np.float32)
+    return f16_from_f32(r) if f16 else r

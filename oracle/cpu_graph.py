@@ -8,7 +8,10 @@ intermediate stored in its own dtype, conv bias as a separate pass
 (``runtime.rs:1445-1498``), SiLU as Sigmoid then Mul.  The ONNX quantized
 ops (QLinearConv, QLinearLUT, QLinearAdd, QuantizeLinear,
 DequantizeLinear) and padded MaxPool are the extensions defined in
-``oracle/dw_oracle.cpp`` Part B.
+``oracle/dw_oracle.cpp`` Part B.  Transpose, Slice, Sub, Div, broadcasting
+Add / Mul and AveragePool are the numpy restatements of Part D
+(``oracle/__init__.py``); LayoutTranspose is the pure byte permutation that
+convert_nchw_to_nhwc inserts around a Reshape of a 4-D tensor.
 
 The reference's INT8 form (``QuantizedGraphCompiler``, ``quantize.rs:73-368``,
 and fusion pass 3, ``fusion.rs:192-334``) runs with the semantics of the ops
@@ -191,10 +194,19 @@ class CpuGraph:
             self.vals[out[0]] = oracle.dequantize_linear_u8_f16(ins[0], tx["scale"], tx["zp"])
         elif ty == "Sigmoid":
             self.vals[out[0]] = (oracle.sigmoid_f32 if ins[0].dtype == np.float32 else oracle.sigmoid_fp16)(ins[0])
-        elif ty == "Mul":
-            self.vals[out[0]] = (oracle.mul_f32 if ins[0].dtype == np.float32 else oracle.mul_fp16)(ins[0], ins[1])
-        elif ty == "Add":
-            self.vals[out[0]] = (oracle.add_f32 if ins[0].dtype == np.float32 else oracle.add_fp16)(ins[0], ins[1])
+        elif ty in ("Add", "Mul") and ins[0].shape == ins[1].shape:
+            fn = {("Add", True): oracle.add_f32, ("Add", False): oracle.add_fp16,
+                  ("Mul", True): oracle.mul_f32, ("Mul", False): oracle.mul_fp16}[(ty, ins[0].dtype == np.float32)]
+            self.vals[out[0]] = fn(ins[0], ins[1])
+        elif ty in ("Add", "Mul", "Sub", "Div"):
+            self.vals[out[0]] = oracle.binary(ty, ins[0], ins[1]).reshape(t[out[0]]["dims"])
+        elif ty in ("Transpose", "LayoutTranspose"):
+            r = ins[0].ndim
+            self.vals[out[0]] = oracle.transpose(ins[0], op["perm"][:r], f16_round_trip=ty == "Transpose")
+        elif ty == "Slice":
+            self.vals[out[0]] = oracle.slice_axes(ins[0], op["slices"])
+        elif ty == "AveragePool":
+            self.vals[out[0]] = oracle.avgpool2d_nhwc(ins[0], op["kernel_shape"], op["strides"])
         elif ty == "Relu":
             x = ins[0]
             fn = {np.dtype(np.float32): oracle.relu_f32, np.dtype(np.uint16): oracle.relu_fp16,
@@ -210,13 +222,16 @@ class CpuGraph:
                 raise NotImplementedError("linear resize")
             self.vals[out[0]] = oracle.resize_nearest(ins[0], op["out_h"], op["out_w"])
         elif ty == "Concat":
-            if op["axis"] != 3:
-                raise NotImplementedError("concat axis")
-            self.vals[out[0]] = oracle.concat_channels(ins)
+            if op["axis"] == 3 and ins[0].ndim == 4:
+                self.vals[out[0]] = oracle.concat_channels(ins)
+            else:  # any other axis of the row-major tensors: the elements in order
+                self.vals[out[0]] = np.ascontiguousarray(np.concatenate(ins, axis=op["axis"]))
         elif ty == "Split":
-            if op["axis"] != 3:
-                raise NotImplementedError("split axis")
-            parts = oracle.split_channels(ins[0], op["split_sizes"])
+            if op["axis"] == 3 and ins[0].ndim == 4:
+                parts = oracle.split_channels(ins[0], op["split_sizes"])
+            else:
+                cuts = np.cumsum(op["split_sizes"])[:-1]
+                parts = [np.ascontiguousarray(v) for v in np.split(ins[0], cuts, axis=op["axis"])]
             for n, v in zip(out, parts):
                 self.vals[n] = v
         elif ty == "GlobalAveragePool":

@@ -58,7 +58,8 @@ def f_ints(num: int, vals, packed=True) -> bytes:
 
 
 def tensor(name: str, arr, raw=True, packed_dims=True) -> bytes:
-    a = np.ascontiguousarray(arr)
+    a = np.asarray(arr)
+    a = np.ascontiguousarray(a) if a.ndim else a  # keep 0-d scalars 0-d
     out = f_ints(1, a.shape, packed_dims) if a.shape else b""
     out += f_varint(2, NP_TYPE[a.dtype])
     if raw:
@@ -128,36 +129,7 @@ def export_float_nchw(g) -> bytes:
     as an int64 input, Resize with roi / scales inputs."""
     d = g.to_dict()
     t = d["tensors"]
-    nodes, inits = [], []
-    for name, ti in t.items():
-        if ti["init"]:
-            inits.append(tensor(name, g.initializer(name, np.float32, tuple(ti["dims"]))))
-    for op in d["ops"]:
-        ty, ins, outs = op["type"], op["inputs"], op["outputs"]
-        if ty == "Conv":
-            nodes.append(node("Conv", ins, outs, op["name"], **_conv_attrs(op)))
-        elif ty == "BatchNormalization":
-            nodes.append(node(ty, ins, outs, op["name"], epsilon=float(op["epsilon"])))
-        elif ty in ("Sigmoid", "Mul", "Add", "Relu"):
-            nodes.append(node(ty, ins, outs, op["name"]))
-        elif ty == "Concat":
-            nodes.append(node(ty, ins, outs, op["name"], axis=op["axis"]))
-        elif ty == "Split":
-            sp = op["name"] + ".split"
-            inits.append(tensor(sp, np.array(op["split_sizes"], np.int64)))
-            nodes.append(node(ty, [ins[0], sp], outs, op["name"], axis=op["axis"]))
-        elif ty == "MaxPool":
-            nodes.append(node(ty, ins, outs, op["name"], kernel_shape=op["kernel_shape"], strides=op["strides"],
-                              pads=op["pads"]))
-        elif ty == "Resize":
-            x = t[ins[0]]["dims"]
-            sc = op["name"] + ".scales"
-            inits.append(tensor(sc, np.array([1, 1, op["out_h"] / x[2], op["out_w"] / x[3]], np.float32)))
-            nodes.append(node(ty, [ins[0], "", sc], outs, op["name"], mode="nearest",
-                              coordinate_transformation_mode="asymmetric", nearest_mode="floor"))
-        else:
-            raise NotImplementedError(ty)
-    vin = [value_info(n, t[n]["dims"]) for n in d["inputs"]]
+    nodes, inits, vin, _ = _float_parts(g)
     vout = [value_info(n, t[n]["dims"]) for n in d["outputs"]]
     return model(nodes, inits, vin, vout)
 
@@ -275,3 +247,157 @@ def export_qdq(g) -> bytes:
     vin = [value_info(n, nchw(t[n]["dims"])) for n in d["inputs"]]
     vout = [value_info(src(n), nchw(t[n]["dims"])) for n in d["outputs"]]
     return model(nodes, inits, vin, vout)
+
+
+# ---------------------------------------------------------------------------
+# the exported YOLOv8 detect tail (ultralytics Detect in export mode)
+# ---------------------------------------------------------------------------
+def make_anchors(level_hw, strides):
+    """Anchor points (cell centres, row-major per level) as [1, 2, A] and the
+    per-anchor stride as [1, A] (ultralytics make_anchors, offset 0.5)."""
+    pts, st = [], []
+    for (h, w), s in zip(level_hw, strides):
+        sy, sx = np.meshgrid(np.arange(h, dtype=np.float32) + 0.5, np.arange(w, dtype=np.float32) + 0.5,
+                             indexing="ij")
+        pts.append(np.stack([sx.ravel(), sy.ravel()], 0))
+        st.append(np.full(h * w, s, np.float32))
+    return np.concatenate(pts, 1)[None].astype(np.float32), np.concatenate(st)[None].astype(np.float32)
+
+
+def exported_tail(levels, level_dims, strides, nc=80, reg_max=16, shape_ops=False, out="output0"):
+    """Nodes and initializers of the exported tail over the per-level head
+    outputs `levels` (NCHW [b, 4 reg_max + nc, h, w]):
+      Reshape [b, no, h*w] per level -> Concat axis 2 -> Split [4R, nc] axis 1;
+      DFL: Reshape [b, 4, R, A] -> Transpose (0, 2, 1, 3) -> Softmax axis 1 ->
+        Conv 1x1 (R -> 1, weights 0..R-1) -> Reshape [b, 4, A];
+      dist2bbox: Slice lt / rb -> anchors - lt, anchors + rb -> (x1y1 + x2y2) / 2,
+        x2y2 - x1y1 -> Concat axis 1 -> Mul strides;
+      Sigmoid of the classes; Concat axis 1 -> [b, 4 + nc, A].
+    With shape_ops the Reshape shapes are computed as unsimplified exports do
+    (Shape -> Gather -> Unsqueeze -> Concat of constants)."""
+    b = level_dims[0][0]
+    no = 4 * reg_max + nc
+    hw = [(d[2], d[3]) for d in level_dims]
+    A = sum(h * w for h, w in hw)
+    nodes, inits = [], []
+
+    def const(name, arr):
+        inits.append(tensor(name, np.asarray(arr)))
+        return name
+
+    def shape_of(tag, src, rest):
+        """the shape [b] + rest, from Shape(src)[0] when shape_ops"""
+        if not shape_ops:
+            return const(f"{tag}.shape", np.array([b] + list(rest), np.int64))
+        nodes.append(node("Shape", [src], [f"{tag}.s"], f"{tag}.shape_op"))
+        nodes.append(node("Gather", [f"{tag}.s", const(f"{tag}.i0", np.array(0, np.int64))], [f"{tag}.b"],
+                          f"{tag}.gather", axis=0))
+        nodes.append(node("Unsqueeze", [f"{tag}.b", const(f"{tag}.ax", np.array([0], np.int64))], [f"{tag}.b1"],
+                          f"{tag}.unsqueeze"))
+        nodes.append(node("Concat", [f"{tag}.b1", const(f"{tag}.rest", np.array(rest, np.int64))], [f"{tag}.shape"],
+                          f"{tag}.concat", axis=0))
+        return f"{tag}.shape"
+
+    flat = []
+    for i, (x, (h, w)) in enumerate(zip(levels, hw)):
+        sh = shape_of(f"tail.r{i}", x, [no, -1])
+        nodes.append(node("Reshape", [x, sh], [f"tail.r{i}"], f"tail.reshape{i}"))
+        flat.append(f"tail.r{i}")
+    nodes.append(node("Concat", flat, ["tail.cat"], "tail.concat", axis=2))
+    nodes.append(node("Split", ["tail.cat", const("tail.split", np.array([4 * reg_max, nc], np.int64))],
+                      ["tail.box", "tail.cls"], "tail.split_op", axis=1))
+    sh = shape_of("tail.dfl", "tail.box", [4, reg_max, A])
+    nodes.append(node("Reshape", ["tail.box", sh], ["tail.dfl.r"], "tail.dfl.reshape"))
+    nodes.append(node("Transpose", ["tail.dfl.r"], ["tail.dfl.t"], "tail.dfl.transpose", perm=[0, 2, 1, 3]))
+    nodes.append(node("Softmax", ["tail.dfl.t"], ["tail.dfl.p"], "tail.dfl.softmax", axis=1))
+    dflw = const("tail.dfl.w", np.arange(reg_max, dtype=np.float32).reshape(1, reg_max, 1, 1))
+    nodes.append(node("Conv", ["tail.dfl.p", dflw], ["tail.dfl.c"], "tail.dfl.conv", kernel_shape=[1, 1]))
+    sh = shape_of("tail.dist", "tail.dfl.c", [4, A])
+    nodes.append(node("Reshape", ["tail.dfl.c", sh], ["tail.dist"], "tail.dist.reshape"))
+    ax1 = const("tail.ax1", np.array([1], np.int64))
+    nodes.append(node("Slice", ["tail.dist", const("tail.s0", np.array([0], np.int64)),
+                                const("tail.e2", np.array([2], np.int64)), ax1], ["tail.lt"], "tail.slice_lt"))
+    nodes.append(node("Slice", ["tail.dist", const("tail.s2", np.array([2], np.int64)),
+                                const("tail.e4", np.array([4], np.int64)), ax1], ["tail.rb"], "tail.slice_rb"))
+    anchors, stv = make_anchors(hw, strides)
+    const("tail.anchors", anchors)
+    const("tail.strides", stv)
+    nodes.append(node("Sub", ["tail.anchors", "tail.lt"], ["tail.x1y1"], "tail.sub1"))
+    nodes.append(node("Add", ["tail.anchors", "tail.rb"], ["tail.x2y2"], "tail.add1"))
+    nodes.append(node("Add", ["tail.x1y1", "tail.x2y2"], ["tail.csum"], "tail.add2"))
+    nodes.append(node("Div", ["tail.csum", const("tail.two", np.array(2.0, np.float32))], ["tail.cxy"], "tail.div"))
+    nodes.append(node("Sub", ["tail.x2y2", "tail.x1y1"], ["tail.wh"], "tail.sub2"))
+    nodes.append(node("Concat", ["tail.cxy", "tail.wh"], ["tail.dbox0"], "tail.concat_box", axis=1))
+    nodes.append(node("Mul", ["tail.dbox0", "tail.strides"], ["tail.dbox"], "tail.mul_stride"))
+    nodes.append(node("Sigmoid", ["tail.cls"], ["tail.scores"], "tail.sigmoid"))
+    nodes.append(node("Concat", ["tail.dbox", "tail.scores"], [out], "tail.concat_out", axis=1))
+    return nodes, inits, (b, 4 + nc, A)
+
+
+def export_float_nchw_with_tail(g, strides=(8, 16, 32), shape_ops=False, opset=17, keep_heads=False) -> bytes:
+    """export_float_nchw of the YOLOv8n-shaped graph with the exported detect
+    tail after its three per-level outputs: the model's output is
+    output0 [b, 84, A] (and the three head tensors after it with keep_heads)."""
+    d = g.to_dict()
+    t = d["tensors"]
+    nodes, inits, vin, _ = _float_parts(g)
+    heads = d["outputs"]
+    tn, ti, odims = exported_tail(heads, [t[h]["dims"] for h in heads], strides, shape_ops=shape_ops)
+    vout = [value_info("output0", list(odims))]
+    if keep_heads:
+        vout += [value_info(h, t[h]["dims"]) for h in heads]
+    return model(nodes + tn, inits + ti, vin, vout, opset=opset)
+
+
+def _float_parts(g):
+    """The node, initializer and input lists export_float_nchw writes."""
+    d = g.to_dict()
+    t = d["tensors"]
+    nodes, inits = [], []
+    for name, ti in t.items():
+        if ti["init"]:
+            inits.append(tensor(name, g.initializer(name, np.float32, tuple(ti["dims"]))))
+    for op in d["ops"]:
+        ty, ins, outs = op["type"], op["inputs"], op["outputs"]
+        if ty == "Conv":
+            nodes.append(node("Conv", ins, outs, op["name"], **_conv_attrs(op)))
+        elif ty == "BatchNormalization":
+            nodes.append(node(ty, ins, outs, op["name"], epsilon=float(op["epsilon"])))
+        elif ty in ("Sigmoid", "Mul", "Add", "Relu"):
+            nodes.append(node(ty, ins, outs, op["name"]))
+        elif ty == "Concat":
+            nodes.append(node(ty, ins, outs, op["name"], axis=op["axis"]))
+        elif ty == "Split":
+            sp = op["name"] + ".split"
+            inits.append(tensor(sp, np.array(op["split_sizes"], np.int64)))
+            nodes.append(node(ty, [ins[0], sp], outs, op["name"], axis=op["axis"]))
+        elif ty == "MaxPool":
+            nodes.append(node(ty, ins, outs, op["name"], kernel_shape=op["kernel_shape"], strides=op["strides"],
+                              pads=op["pads"]))
+        elif ty == "Resize":
+            x = t[ins[0]]["dims"]
+            sc = op["name"] + ".scales"
+            inits.append(tensor(sc, np.array([1, 1, op["out_h"] / x[2], op["out_w"] / x[3]], np.float32)))
+            nodes.append(node(ty, [ins[0], "", sc], outs, op["name"], mode="nearest",
+                              coordinate_transformation_mode="asymmetric", nearest_mode="floor"))
+        else:
+            raise NotImplementedError(ty)
+    vin = [value_info(n, t[n]["dims"]) for n in d["inputs"]]
+    return nodes, inits, vin, None
+
+
+def tail_reference_nchw(heads, strides=(8, 16, 32), nc=80, reg_max=16):
+    """The exported tail's meaning, in f64 numpy on NCHW head outputs (an
+    independent statement of the ONNX graph above)."""
+    b = heads[0].shape[0]
+    x = np.concatenate([h.astype(np.float64).reshape(b, h.shape[1], -1) for h in heads], 2)
+    box, cls = x[:, :4 * reg_max], x[:, 4 * reg_max:]
+    d = box.reshape(b, 4, reg_max, -1)
+    e = np.exp(d - d.max(axis=2, keepdims=True))
+    p = e / e.sum(axis=2, keepdims=True)
+    dist = (p * np.arange(reg_max).reshape(1, 1, reg_max, 1)).sum(axis=2)
+    anchors, stv = make_anchors([h.shape[2:] for h in heads], strides)
+    a = anchors.astype(np.float64)
+    x1y1, x2y2 = a - dist[:, :2], a + dist[:, 2:]
+    dbox = np.concatenate([(x1y1 + x2y2) / 2, x2y2 - x1y1], 1) * stv.astype(np.float64)
+    return np.concatenate([dbox, 1 / (1 + np.exp(-cls))], 1)

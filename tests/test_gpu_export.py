@@ -1,0 +1,201 @@
+"""The ops of exported models on the GPU (Transpose, Slice, Sub, Div,
+broadcasting Add / Mul, AveragePool, Concat / Split along a non-channel
+axis, the layout transposes around a Reshape of a 4-D tensor) against the
+oracle's CpuGraph, and the YOLOv8n-shaped model with the exported detect
+tail loaded from ONNX (dw_graph_from_onnx):
+
+* op graphs: bit-exact (f32 and f16, with the reference's f16 round trip on
+  Transpose / Slice: subnormals halved);
+* the exported model in f32 (batch 2, 96x96): the heads bit-exact, the tail
+  within 1e-3 (its softmax and sigmoid use the device's exp);
+* in f16 at batch 32, 640x640: every image within 1e-2 of the oracle
+  (boxes relative to the largest box coordinate, class scores absolute),
+  and the exported tail within 1e-2 of the fused YoloDetect statement of
+  the same heads;
+* u8 QDQ with the exported tail (exact fp16 convs) at batch 32, 640x640:
+  the head tensors bit-exact, the tail within 1e-2.
+"""
+import numpy as np
+import pytest
+
+import onnx_writer as ox
+import oracle
+from oracle.cpu_graph import CpuGraph
+from dragonwing_edge_rs_amd import synth, yolo
+from dragonwing_edge_rs_amd.graph import GRAPH_F16, GRAPH_F32, Graph, HipGraphRuntime
+
+pytestmark = pytest.mark.gpu
+
+NP = {0: np.float32, 1: np.uint16, 3: np.uint8}
+
+
+def oracle_run(g, inputs):
+    cg = CpuGraph(g.to_dict(), g.initializer)
+    for k, v in inputs.items():
+        cg.set_input(k, v)
+    return cg.run()
+
+
+def run_graph(backend, g, inputs, outs, **kw):
+    rt = HipGraphRuntime(g, backend, **kw)
+    for k, v in inputs.items():
+        rt.set_input_bytes(k, v)
+    rt.run()
+    t = g.to_dict()["tensors"]
+    return {o: rt.get_output_bytes(o).view(NP[t[o]["dtype"]]).reshape(t[o]["dims"]) for o in outs}, rt
+
+
+def f16(x):
+    return synth.f16_bits(np.asarray(x, np.float32))
+
+
+@pytest.mark.parametrize("dt", ["f32", "f16"])
+def test_layout_ops_bit_exact(backend, dt):
+    r = synth.Rng(synth.seed_for(61))
+    g = Graph(GRAPH_F32 if dt == "f32" else GRAPH_F16)
+    x = r.normal((2, 6, 5, 16), 0.0, 1.0).astype(np.float32)
+    xb = x if dt == "f32" else f16(x)
+    if dt == "f16":
+        xb.ravel()[::13] = np.uint16(0x0003)  # subnormals: the reference's f16 Transpose halves them
+    g.add_tensor("x", x.shape, dt)
+    g.add_tensor("t", (2, 16, 6, 5), dt)
+    g.add_op("tr", "Transpose", ["x"], ["t"], perm=(0, 3, 1, 2))
+    g.add_tensor("s", (2, 8, 3, 5), dt)
+    g.add_op("sl", "Slice", ["t"], ["s"], slices=[(1, 0, 16, 2), (2, 1, 6, 2)])
+    g.add_tensor("r", (2, 8, 15), dt)
+    g.add_op("rs", "Reshape", ["s"], ["r"])
+    g.add_tensor("a3", (2, 3, 15), dt)
+    g.add_tensor("b5", (2, 5, 15), dt)
+    g.add_op("split", "Split", ["r"], ["a3", "b5"], axis=1, split_sizes=(3, 5))
+    g.add_tensor("cat", (2, 8, 15), dt)
+    g.add_op("cat", "Concat", ["b5", "a3"], ["cat"], axis=1)
+    g.add_tensor("lt", (2, 2, 15), dt)
+    g.add_op("slt", "Slice", ["cat"], ["lt"], slices=[(1, 0, 2, 1)])
+    g.set_io(["x"], ["t", "s", "cat", "lt"])
+    got, _ = run_graph(backend, g, {"x": xb}, ["t", "s", "cat", "lt"])
+    ref = oracle_run(g, {"x": xb})
+    for o in ("t", "s", "cat", "lt"):
+        np.testing.assert_array_equal(got[o], ref[o], err_msg=o)
+    if dt == "f16":
+        assert np.any(ref["t"] != xb.transpose(0, 3, 1, 2))  # the round trip changed the subnormals
+
+
+@pytest.mark.parametrize("dt", ["f32", "f16"])
+def test_broadcast_binary_and_avgpool_bit_exact(backend, dt):
+    r = synth.Rng(synth.seed_for(62))
+    g = Graph(GRAPH_F32 if dt == "f32" else GRAPH_F16)
+    conv = (lambda a: a) if dt == "f32" else f16
+    x = conv(r.normal((3, 2, 40), 0.0, 4.0))
+    anchors = conv(r.uniform((1, 2, 40), 0.0, 20.0))
+    st = conv(np.full((1, 40), 8.0, np.float32))
+    g.add_tensor("x", x.shape, dt)
+    g.add_initializer("anc", anchors, dt)
+    g.add_initializer("st", st, dt)
+    g.add_initializer("two", conv(np.array([2.0], np.float32)), dt)
+    for n in ("d", "s", "q", "m"):
+        g.add_tensor(n, x.shape, dt)
+    g.add_op("sub", "Sub", ["anc", "x"], ["d"])      # smaller first operand
+    g.add_op("add", "Add", ["x", "anc"], ["s"])      # smaller second operand
+    g.add_op("div", "Div", ["s", "two"], ["q"])      # scalar
+    g.add_op("mul", "Mul", ["q", "st"], ["m"])       # trailing broadcast
+    p = conv(r.normal((2, 9, 7, 24), 0.0, 1.0))
+    g.add_tensor("p", p.shape, dt)
+    g.add_tensor("ap", (2, 4, 6, 24), dt)
+    g.add_op("pool", "AveragePool", ["p"], ["ap"], kernel_shape=(3, 2), strides=(2, 1))
+    outs = ["d", "s", "q", "m", "ap"]
+    g.set_io(["x", "p"], outs)
+    got, _ = run_graph(backend, g, {"x": x, "p": p}, outs)
+    ref = oracle_run(g, {"x": x, "p": p})
+    for o in outs:
+        np.testing.assert_array_equal(got[o], ref[o], err_msg=o)
+
+
+def exported_model(batch, size, shape_ops=False):
+    g0, info = yolo.build_yolov8n(batch=batch, size=size)
+    return Graph.from_onnx(ox.export_float_nchw_with_tail(g0, shape_ops=shape_ops, keep_heads=True)), info
+
+
+def tail_err(got, ref):
+    """(boxes: max error over the largest box coordinate, scores: max absolute error)"""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    box = np.max(np.abs(got[:, :4] - ref[:, :4])) / np.max(np.abs(ref[:, :4]))
+    return box, np.max(np.abs(got[:, 4:] - ref[:, 4:]))
+
+
+def test_exported_model_f32(backend):
+    g, info = exported_model(2, 96, shape_ops=True)
+    g.fold_batchnorm()
+    g.convert_nchw_to_nhwc()
+    d = g.to_dict()
+    x = yolo.input_images(2, 96)
+    outs = d["outputs"]
+    got, rt = run_graph(backend, g, {d["inputs"][0]: x}, outs)
+    assert "strided_copy" in [L["kernel"] for L in rt.launches()]
+    ref = oracle_run(g, {d["inputs"][0]: x})
+    for h in outs[1:]:
+        e = np.max(np.abs(got[h] - ref[h])) / np.max(np.abs(ref[h]))
+        assert e <= 1e-4, (h, e)  # SiLU's expf is the device's
+    box, cls = tail_err(got["output0"], ref["output0"])
+    print(f"f32 exported tail: boxes {box:.2e}, scores {cls:.2e}")
+    assert box <= 1e-3 and cls <= 1e-3
+
+
+def test_exported_model_f16_full_workload(backend):
+    g, info = exported_model(32, 640)
+    g.fold_batchnorm()
+    g.convert_nchw_to_nhwc()
+    g.convert_to_f16()
+    d = g.to_dict()
+    x = yolo.input_images(32, 640)
+    got, rt = run_graph(backend, g, {d["inputs"][0]: synth.f16_bits(x)}, d["outputs"])
+    out = oracle.f16_to_f32(got["output0"])
+    # the exported tail against the fused statement of the same heads
+    heads = [got[h] for h in d["outputs"][1:]]
+    fused = oracle.yolo_detect_tail_f16(heads, (8, 16, 32))
+    box, cls = tail_err(out, fused)
+    print(f"exported tail vs fused tail on the GPU heads: boxes {box:.2e}, scores {cls:.2e}", flush=True)
+    assert box <= 1e-2 and cls <= 1e-2
+    g1, _ = exported_model(1, 640)
+    g1.fold_batchnorm()
+    g1.convert_nchw_to_nhwc()
+    g1.convert_to_f16()
+    d1 = g1.to_dict()
+    worst = (0.0, 0.0)
+    for img in range(32):
+        ref = oracle_run(g1, {d1["inputs"][0]: synth.f16_bits(x[img:img + 1])})
+        box, cls = tail_err(out[img:img + 1], oracle.f16_to_f32(ref["output0"]))
+        worst = (max(worst[0], box), max(worst[1], cls))
+        assert box <= 1e-2 and cls <= 1e-2, (img, box, cls)
+    print(f"all 32 images: boxes {worst[0]:.2e}, scores {worst[1]:.2e}", flush=True)
+
+
+def test_exported_model_int8_full_workload(backend):
+    # the u8 QDQ graph of the exported model: scales from the GPU
+    # calibration of the plain graph's 16 seeded images (the tail stays f16
+    # and needs none); the DFL's 1x1 conv kept fp16 with the head
+    gq, info_q = yolo.int8_graph(backend, batch=32, size=640)
+    ranges = info_q["ranges"]
+
+    def build(batch):
+        g, info = exported_model(batch, 640)
+        g.fold_batchnorm()
+        g.convert_nchw_to_nhwc()
+        for n, (lo, hi) in ranges.items():
+            g.set_activation_range(n, lo, hi)
+        g.quantize_qdq(list(info["keep_f16"]) + ["tail.dfl.conv"])
+        return g
+
+    g = build(32)
+    d = g.to_dict()
+    assert d["tensors"]["output0"]["dtype"] == 1  # the tail in f16
+    x = yolo.input_images(32, 640)
+    got, _ = run_graph(backend, g, {d["inputs"][0]: synth.f16_bits(x)}, d["outputs"], exact_u8_f16=True)
+    g1 = build(1)
+    d1 = g1.to_dict()
+    for img in (0, 13, 31):
+        ref = oracle_run(g1, {d1["inputs"][0]: synth.f16_bits(x[img:img + 1])})
+        for h in d["outputs"][1:]:
+            np.testing.assert_array_equal(got[h][img:img + 1], ref[h], err_msg=f"{h} image {img}")
+        box, cls = tail_err(oracle.f16_to_f32(got["output0"][img:img + 1]), oracle.f16_to_f32(ref["output0"]))
+        assert box <= 1e-2 and cls <= 1e-2, (img, box, cls)

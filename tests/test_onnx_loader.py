@@ -19,6 +19,7 @@ import numpy as np
 import pytest
 
 import onnx_writer as ox
+import oracle
 from dragonwing_edge_rs_amd import HipError, synth, yolo
 from dragonwing_edge_rs_amd.graph import Graph, onnx_inspect
 
@@ -207,3 +208,98 @@ def test_constant_payload_must_match_dims(case):
     with pytest.raises(HipError) as e:
         Graph.from_onnx(m)
     assert e.value.code == -4, (case, e.value.code, str(e.value))  # DW_ERR_INVALID
+
+
+def tail_run_on_oracle(size=64, shape_ops=False):
+    """The YOLOv8n-shaped float model with the exported detect tail, loaded
+    (dw_graph_from_onnx), through fold_batchnorm and convert_nchw_to_nhwc,
+    run on the oracle's CpuGraph: (graph, output0 [1, 84, A], the three
+    head tensors in NCHW)."""
+    from oracle.cpu_graph import CpuGraph
+    g0, info = yolo.build_yolov8n(batch=1, size=size)
+    g = Graph.from_onnx(ox.export_float_nchw_with_tail(g0, shape_ops=shape_ops, keep_heads=True))
+    g.fold_batchnorm()
+    g.convert_nchw_to_nhwc()
+    d = g.to_dict()
+    cg = CpuGraph(d, g.initializer)
+    cg.set_input(d["inputs"][0], yolo.input_images(1, size))
+    vals = cg.run()
+    heads = [np.ascontiguousarray(vals[h].transpose(0, 3, 1, 2)) for h in d["outputs"][1:]]
+    return g, vals["output0"], heads
+
+
+def test_exported_tail_loads_and_computes_the_onnx_meaning():
+    # the exported tail (Reshape, Concat, Split, Transpose, Softmax, Conv,
+    # Slice, Sub, Add, Div, Mul, Sigmoid, Concat) after convert_nchw_to_nhwc
+    # computes what the NCHW ONNX graph means: the f64 statement of the same
+    # graph on the same head outputs
+    g, out, heads = tail_run_on_oracle()
+    ref = ox.tail_reference_nchw(heads)
+    assert out.shape == ref.shape == (1, 84, 8 * 8 + 4 * 4 + 2 * 2)
+    box, cls = np.abs(out[:, :4] - ref[:, :4]), np.abs(out[:, 4:] - ref[:, 4:])
+    assert box.max() <= 1e-5 * np.abs(ref[:, :4]).max() and cls.max() <= 1e-6, (box.max(), cls.max())
+    types = [op["type"] for op in g.to_dict()["ops"]]
+    for ty in ("Transpose", "Slice", "Sub", "Div", "LayoutTranspose"):
+        assert ty in types, ty
+    # the layout transposes sit where a Reshape reads an NHWC tensor
+    assert types.count("LayoutTranspose") == 4  # three heads and the DFL's 4-D reshape
+
+
+def test_exported_tail_shape_ops_fold_to_constants():
+    # Shape -> Gather -> Unsqueeze -> Concat chains for the Reshape shapes
+    # (unsimplified exports) fold into constants: the same ops, same result
+    g1, out1, _ = tail_run_on_oracle(shape_ops=False)
+    g2, out2, _ = tail_run_on_oracle(shape_ops=True)
+    t1 = [op["type"] for op in g1.to_dict()["ops"]]
+    t2 = [op["type"] for op in g2.to_dict()["ops"]]
+    assert t1 == t2 and "Shape" not in t2 and "Gather" not in t2
+    np.testing.assert_array_equal(out1, out2)
+
+
+def test_pad_folds_into_conv_and_avgpool_loads():
+    w = np.arange(2 * 3 * 3 * 3, dtype=np.float32).reshape(2, 3, 3, 3) / 10
+    nodes = [ox.node("Pad", ["x", "pads"], ["xp"], "pad"),
+             ox.node("Conv", ["xp", "w"], ["y"], "conv", kernel_shape=[3, 3]),
+             ox.node("AveragePool", ["y"], ["z"], "pool", kernel_shape=[2, 2], strides=[2, 2])]
+    m = ox.model(nodes, [ox.tensor("w", w), ox.tensor("pads", np.array([0, 0, 1, 2, 0, 0, 1, 0], np.int64))],
+                 [ox.value_info("x", [1, 3, 8, 8])], [ox.value_info("z", [1, 2, 4, 4])], opset=17)
+    d = Graph.from_onnx(m).to_dict()
+    assert [op["type"] for op in d["ops"]] == ["Conv", "AveragePool"]
+    assert d["ops"][0]["pads"] == [1, 2, 1, 0] and d["tensors"]["y"]["dims"] == [1, 2, 8, 9 - 1]
+    bad = ox.model([ox.node("Pad", ["x", "pads"], ["xp"], "pad"), ox.node("Relu", ["xp"], ["y"], "relu")],
+                   [ox.tensor("pads", np.array([0, 0, 1, 1, 0, 0, 1, 1], np.int64))],
+                   [ox.value_info("x", [1, 3, 8, 8])], [ox.value_info("y", [1, 3, 10, 10])], opset=17)
+    with pytest.raises(HipError):  # a Pad that no Conv reads
+        Graph.from_onnx(bad)
+
+
+def test_exported_tail_int8_graph_on_oracle():
+    # quantize_qdq of the exported model: the INT8 body as before, the tail
+    # after the fp16 head convs stays f16 (with the DFL conv kept fp16), and
+    # the u8 graph's output is the f16 statement of the same tail
+    from oracle.cpu_graph import CpuGraph, calibrate
+    g0, info = yolo.build_yolov8n(batch=1, size=64)
+    model = ox.export_float_nchw_with_tail(g0, keep_heads=True)
+    gc = Graph.from_onnx(model)
+    gc.fold_batchnorm()
+    gc.convert_nchw_to_nhwc()
+    dc = gc.to_dict()
+    ranges = calibrate(dc, gc.initializer, dc["inputs"][0], yolo.calibration_images(2, 64))
+    gq = Graph.from_onnx(model)
+    gq.fold_batchnorm()
+    gq.convert_nchw_to_nhwc()
+    for n, (lo, hi) in ranges.items():
+        gq.set_activation_range(n, lo, hi)
+    gq.quantize_qdq(list(info["keep_f16"]) + ["tail.dfl.conv"])
+    d = gq.to_dict()
+    t = d["tensors"]
+    assert t["output0"]["dtype"] == 1 and t["tail.dfl.p"]["dtype"] == 1
+    assert sum(op["type"] == "QLinearConv" for op in d["ops"]) == 56
+    cg = CpuGraph(d, gq.initializer)
+    cg.set_input(d["inputs"][0], synth.f16_bits(yolo.input_images(1, 64)))
+    vals = cg.run()
+    out = oracle.f16_to_f32(vals["output0"])
+    heads = [vals[h] for h in d["outputs"][1:]]
+    fused = oracle.yolo_detect_tail_f16(heads, (8, 16, 32))
+    box = np.max(np.abs(out[:, :4] - fused[:, :4])) / np.max(np.abs(fused[:, :4]))
+    assert box <= 1e-2 and np.max(np.abs(out[:, 4:] - fused[:, 4:])) <= 1e-2
