@@ -216,6 +216,10 @@ void launch_conv1x1_u8_f16(hipStream_t st, const Conv1x1F16Args& a);
 // HWIO f32 weights [rows][cout] -> [cout / 4][rows][4] (DirectArgs::wq)
 void launch_repack_oc4(hipStream_t st, const float* w, float* wq, int rows, int cout);
 void launch_dwconv(hipStream_t st, const DwArgs& a, int dtype);
+// fp16 3x3 stride-1 depthwise on LDS row bands, packed f16 arithmetic (k_dwtile.hip)
+bool dwconv3_tile_ok(const DwArgs& a);
+bool dwconv3_tile_cfg_ok(const DwArgs& a, int units, int band_rows);
+void launch_dwconv3_tile(hipStream_t st, const DwArgs& a, int units, int band_rows);
 
 // Classifier-head ops (k_head.hip).  gemm: row-major C[m][n] = A[m][k] B[k][n]
 // (dtype F32, F16 or I8 with an int32 C); global average pool over NHWC

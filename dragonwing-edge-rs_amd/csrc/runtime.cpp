@@ -80,6 +80,9 @@ struct Launch {
   // direct-conv launches: their arguments, shared with `fn`, so an input
   // can be switched to the NCHW f32 loader after the list is built
   std::shared_ptr<DirectArgs> da;
+  // band-tile depthwise launches: their output rows per band, chosen by the tuner
+  std::shared_ptr<int> dw_band;  // units * 100 + band rows
+  std::shared_ptr<DwArgs> dwa;
   int esize = 0;
   // schedule over several streams: the storage this launch touches, its
   // stream, the launches on other streams it waits for, and whether a
@@ -133,6 +136,9 @@ struct Runtime {
   // write f16 run in the reference's accumulation order (bit-identical to
   // the CPU) instead of on the fp16 matrix cores
   bool exact_u8_f16 = false;
+  // DW_RT_EXACT_F16_DEPTHWISE: fp16 depthwise convs in the reference's
+  // accumulation order instead of the packed-f16 band kernel
+  bool exact_f16_dw = false;
   // graph inputs given in NCHW f32 (the layout before convert_nchw_to_nhwc):
   // the one stem conv that reads such an input loads the NCHW planes itself
   // (rounding to f16 in its loader); any other input is converted by a
@@ -1164,6 +1170,15 @@ void Runtime::emit(const Group& gr) {
     L.op = join_names(g, gr.ops);
     L.work = 2.0 * (double)y.pixels() * y.c * a.kh * a.kw;
     L.bytes = (double)x.bytes() + (double)y.bytes() + W.data.size() + (a.bias ? y.c * dtype_size(dt) : 0);
+    if (dt == F16 && !exact_f16_dw && (dwconv3_tile_cfg_ok(a, 8, 4) || dwconv3_tile_cfg_ok(a, 4, 4))) {
+      // packed-f16 band kernel (fp16 tolerance); the tuner picks the band height
+      L.kernel = "dwconv3_tile";
+      L.dwa = std::make_shared<DwArgs>(a);
+      L.dw_band = std::make_shared<int>(dwconv3_tile_cfg_ok(a, 8, 4) ? 804 : 404);
+      L.fn = [a, cfg = L.dw_band](hipStream_t st) { launch_dwconv3_tile(st, a, *cfg / 100, *cfg % 100); };
+      launches.push_back(L);
+      return;
+    }
     L.fn = [=](hipStream_t st) { launch_dwconv(st, a, dt); };
     launches.push_back(L);
     return;
@@ -1990,6 +2005,34 @@ void Runtime::autotune() {
   DW_HIP(hipEventCreate(&e0));
   DW_HIP(hipEventCreate(&e1));
   for (auto& L : launches) {
+    if (!L.dw_band) continue;
+    // band heights whose tile fits LDS (two workgroups a CU where possible)
+    float best = 1e30f;
+    int bb = *L.dw_band;
+    for (int cand : {404, 408, 410, 420, 804, 808, 810}) {
+      if (!dwconv3_tile_cfg_ok(*L.dwa, cand / 100, cand % 100)) continue;
+      const int band = cand;
+      *L.dw_band = band;
+      L.fn(st);
+      float t_min = 1e30f;
+      for (int r = 0; r < 3; ++r) {
+        DW_HIP(hipEventRecord(e0, st));
+        for (int k = 0; k < 4; ++k) L.fn(st);
+        DW_HIP(hipEventRecord(e1, st));
+        DW_HIP(hipEventSynchronize(e1));
+        float ms = 0;
+        DW_HIP(hipEventElapsedTime(&ms, e0, e1));
+        t_min = std::min(t_min, ms);
+      }
+      if (t_min < best) {
+        best = t_min;
+        bb = band;
+      }
+    }
+    *L.dw_band = bb;
+    L.kernel = "dwconv3_tile_u" + std::to_string(bb / 100) + "r" + std::to_string(bb % 100);
+  }
+  for (auto& L : launches) {
     if (!L.ig) continue;
     IgemmArgs& a = *L.ig;
     int bc[64], pb[64], tpw[64];
@@ -2162,11 +2205,13 @@ int dw_hip_graph_runtime_create_ex(dw_hip_backend* be, const dw_graph* g, unsign
                                    dw_hip_graph_runtime** out) {
   API_BEGIN
   if (!g || !out) dw::fail(DW_ERR_INVALID, "null argument");
-  if (flags & ~(unsigned)DW_RT_EXACT_U8_F16_CONV) dw::fail(DW_ERR_INVALID, "unknown runtime flags");
+  if (flags & ~(unsigned)(DW_RT_EXACT_U8_F16_CONV | DW_RT_EXACT_F16_DEPTHWISE))
+    dw::fail(DW_ERR_INVALID, "unknown runtime flags");
   dw::Backend* b = Bk(be);
   std::lock_guard<std::mutex> lock(b->mu);
   auto* rt = new dw_hip_graph_runtime();
   rt->rt.exact_u8_f16 = (flags & DW_RT_EXACT_U8_F16_CONV) != 0;
+  rt->rt.exact_f16_dw = (flags & DW_RT_EXACT_F16_DEPTHWISE) != 0;
   dw::hold(b);  // released with the runtime
   try {
     rt->rt.build(b, g->g, false);

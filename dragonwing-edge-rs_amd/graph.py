@@ -191,17 +191,20 @@ class Graph:
 
 
 RT_EXACT_U8_F16_CONV = 1  # DW_RT_EXACT_U8_F16_CONV
+RT_EXACT_F16_DEPTHWISE = 2  # DW_RT_EXACT_F16_DEPTHWISE
 
 
 class HipGraphRuntime:
     """``VulkanGraphRuntime`` on the HIP backend."""
 
-    def __init__(self, graph: Graph, backend, exact_u8_f16: bool = False):
+    def __init__(self, graph: Graph, backend, exact_u8_f16: bool = False, exact_f16_dw: bool = False):
         """exact_u8_f16: the convs that read u8 activations and write f16 (a
         QDQ graph's fp16 tail layers) run in the reference's accumulation
-        order, bit-identical to the CPU, instead of on the fp16 matrix cores."""
+        order, bit-identical to the CPU, instead of on the fp16 matrix cores.
+        exact_f16_dw: fp16 depthwise convs in the reference's order instead
+        of the packed-f16 band kernel."""
         h = C.c_void_p()
-        flags = RT_EXACT_U8_F16_CONV if exact_u8_f16 else 0
+        flags = (RT_EXACT_U8_F16_CONV if exact_u8_f16 else 0) | (RT_EXACT_F16_DEPTHWISE if exact_f16_dw else 0)
         check(load().dw_hip_graph_runtime_create_ex(backend.handle, graph.handle, flags, C.byref(h)))
         self._h = h.value
         self._backend = backend  # keeps the backend alive

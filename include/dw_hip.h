@@ -542,6 +542,10 @@ int dw_hip_graph_runtime_create(dw_hip_backend* be, const dw_graph* g, dw_hip_gr
  * fp16 matrix cores (results within the fp16 tolerance).  The INT8 layers
  * are bit-exact either way.  Unknown flags: DW_ERR_INVALID. */
 #define DW_RT_EXACT_U8_F16_CONV 1u
+/* DW_RT_EXACT_F16_DEPTHWISE: fp16 depthwise convs in dragonwing-cpu's
+ * accumulation order (an f32 fma chain, bit-identical before the
+ * activation) instead of the packed-f16 band kernel (fp16 tolerance). */
+#define DW_RT_EXACT_F16_DEPTHWISE 2u
 int dw_hip_graph_runtime_create_ex(dw_hip_backend* be, const dw_graph* g, unsigned flags,
                                    dw_hip_graph_runtime** out);
 void dw_hip_graph_runtime_destroy(dw_hip_graph_runtime* rt);
