@@ -517,6 +517,13 @@ def main():
             roof["traffic_source"] = ("rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes over one graph run, "
                                       "per-dispatch KiB scaled by the readings of a 256 MiB copy (scales %s)"
                                       % scales)
+            # every listed family: measured HBM bytes per launch against its algorithmic bytes
+            for k in kernels:
+                fi = [i for i, L in enumerate(launches) if family(L["kernel"]) == k["kernel"]]
+                alg = sum(launches[i]["bytes"] for i in fi) / len(fi)
+                t = sum(fetch[i] + write[i] for i in fi) / len(fi)
+                k["traffic_per_launch"] = round(t)
+                k["traffic_over_algorithmic"] = round(t / alg, 3) if alg > 0 else None
         except Exception as e:  # the counters are optional: the line stands without them
             roof["traffic_source"] = f"not measured: {e}"
     if args.traffic_probe:
