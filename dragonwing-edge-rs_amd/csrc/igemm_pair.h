@@ -1,0 +1,357 @@
+// Two chained int8 3x3 convolutions (stride 1, padding 1, c -> c -> c
+// channels, c = 16, 32 or 64) in one launch, the intermediate tensor kept in
+// LDS: the bottleneck of a C2f block (QLinearConv + SiLU table, QLinearConv
+// + SiLU table, optionally + the block input through QLinearAdd).
+//
+// Each launch of a small layer carries a fixed cost of several
+// microseconds (dispatch, the first loads' latency, the epilogue, the
+// kernel's end), which on the 20x20 .. 160x160 maps of a batch-32 graph is
+// most of the layer's time.  Here a workgroup owns R output rows (whole
+// rows, 320 output pixels) of one image and every channel:
+//
+//  * start-up: both convs' weights (all of K, fragment order), their
+//    epilogue data and the R + 4 input rows the two 3x3 windows reach (with
+//    the one-pixel halo and padding) go to LDS, the rows as whole 16-byte
+//    units converted to the MFMA operand (u8 xor 0x80, or the padding
+//    pattern), as igemm_rows_kernel stages them;
+//  * phase 1: the first conv over the R + 2 rows the second conv's window
+//    needs (its halo rows computed twice, once by each neighbouring band),
+//    all operands from LDS; its epilogue (requantize, table) writes the
+//    u8 results, converted to the second conv's operand form, into a second
+//    LDS tile whose padding (the columns beside the image and rows outside
+//    it) holds the second conv's padding pattern;
+//  * phase 2: the second conv over the R rows from that tile; its epilogue
+//    (requantize, table, QLinearAdd of the block input read back from the
+//    first tile) stores the u8 output.
+//
+// The per-output arithmetic is igemm_kernel's (bias' as the accumulator's
+// start, requant_bits, the table, qadd_u8), and integer sums do not depend
+// on the k-order, so the results are those of the two separate launches.
+#pragma once
+
+#include "igemm_kernel.h"
+
+namespace dw {
+namespace ig {
+
+constexpr int kPairPix = 320;  // output pixels per workgroup (phase 2)
+constexpr int kPairPB2 = 5;    // 16-pixel blocks per wave in phase 2
+
+struct PairArgs {
+  IgemmArgs a1, a2;
+  int rows;  // output rows per workgroup (kPairPix / w)
+};
+
+// LDS layout (bytes): two epilogue blocks (table 256, bias' 4c, multipliers
+// 4c), the k-slice table, both weight sets, the input tile, the
+// intermediate tile.
+__host__ __device__ constexpr int pair_su(int c) { return (c / 16) | 1; }
+__host__ __device__ constexpr int pair_epi_bytes(int c) { return 256 + 8 * c; }
+__host__ __device__ constexpr int pair_tab_off(int c) { return 2 * pair_epi_bytes(c); }
+__host__ __device__ constexpr int pair_w_off(int c, int ks) { return (pair_tab_off(c) + ks * 16 + 15) / 16 * 16; }
+__host__ __device__ constexpr int pair_x_off(int c, int ks) { return pair_w_off(c, ks) + 2 * ks * c * 64; }
+__host__ __device__ constexpr int pair_m_off(int c, int ks, int w, int rows) {
+  return pair_x_off(c, ks) + (rows + 4) * (w + 2) * pair_su(c) * 16;
+}
+__host__ __device__ constexpr int pair_lds_bytes(int c, int ks, int w, int rows) {
+  return pair_m_off(c, ks, w, rows) + (rows + 2) * (w + 2) * pair_su(c) * 16;
+}
+constexpr int kPairFill = 8;  // input units each thread loads at start-up (at most)
+
+// CB: 16-channel blocks (c / 16); PB1: 16-pixel blocks per wave in phase 1
+// ((rows + 2) * w pixels over 4 waves); RES: the second epilogue adds the
+// block input.
+template <int CB, int PB1, bool RES>
+__global__ __launch_bounds__(256, CB <= 2 ? 2 : 1) void igemm_pair_kernel(const PairArgs p) {
+  constexpr int C = CB * 16;
+  constexpr int PB2 = kPairPB2;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const IgemmArgs& a1 = p.a1;
+  const IgemmArgs& a2 = p.a2;
+  const int W = a1.w, H = a1.h, R = p.rows;
+  const int TW = W + 2;
+  constexpr int CU = C / 16;  // 16-byte units per pixel
+  constexpr int SU = CU | 1;  // LDS pixel stride in units
+  const int KS = a1.ksteps;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+
+  // XCD-aware tile order, as igemm_kernel: tile = (image, band)
+  const int nwg = gridDim.x;
+  const int bid = blockIdx.x;
+  const int xcd = bid & 7, idx = bid >> 3;
+  const int base = nwg >> 3, rem = nwg & 7;
+  const int tile = xcd * base + min(xcd, rem) + idx;
+  const int bands = H / R;
+  const int n = tile / bands;
+  const int r0 = (tile - n * bands) * R;
+
+  uint8_t* const s_lut1 = smem;
+  uint8_t* const s_bias1 = smem + 256;
+  uint8_t* const s_ms1 = smem + 256 + 4 * C;
+  uint8_t* const s_lut2 = smem + pair_epi_bytes(C);
+  uint8_t* const s_bias2 = s_lut2 + 256;
+  uint8_t* const s_ms2 = s_lut2 + 256 + 4 * C;
+  int* const s_tab = reinterpret_cast<int*>(smem + pair_tab_off(C));
+  uint8_t* const s_w1 = smem + pair_w_off(C, KS);
+  uint8_t* const s_w2 = s_w1 + KS * C * 64;
+  uint8_t* const s_x = smem + pair_x_off(C, KS);
+  uint8_t* const s_m = smem + pair_m_off(C, KS, W, R);
+
+  // ---- both weight sets (fragment order) and both epilogue blocks, direct to LDS
+  const int frag_lane = ((lane & 15) * 64 + (lane >> 4) * 16);
+  {
+    const int nfr = KS * CB;
+    for (int f = wave; f < 2 * nfr; f += 4) {
+      const int second = f >= nfr;
+      const int ff = f - second * nfr;
+      const int sl = ff / CB, cb = ff - sl * CB;
+      const IgemmArgs& aa = second ? a2 : a1;
+      const uint8_t* src = aa.wpk + (((uint32_t)sl * aa.cout_pad + cb * 16) * 64u + frag_lane);
+      __builtin_amdgcn_global_load_lds((const void*)src,
+                                       (__attribute__((address_space(3))) void*)((second ? s_w2 : s_w1) + ff * 1024),
+                                       16, 0, 0);
+    }
+  }
+  if (wave == 0 && lane < C / 4) {
+    __builtin_amdgcn_global_load_lds((const void*)(a1.bias_i + lane * 4), (__attribute__((address_space(3))) void*)s_bias1,
+                                     16, 0, 0);
+    __builtin_amdgcn_global_load_lds((const void*)(a2.bias_i + lane * 4), (__attribute__((address_space(3))) void*)s_bias2,
+                                     16, 0, 0);
+  }
+  if (wave == 1 && lane < C / 4) {
+    __builtin_amdgcn_global_load_lds((const void*)(a1.mscale + lane * 4), (__attribute__((address_space(3))) void*)s_ms1,
+                                     16, 0, 0);
+    __builtin_amdgcn_global_load_lds((const void*)(a2.mscale + lane * 4), (__attribute__((address_space(3))) void*)s_ms2,
+                                     16, 0, 0);
+  }
+  if (wave == 2 && lane < 16) {
+    __builtin_amdgcn_global_load_lds((const void*)(a1.lut + lane * 16), (__attribute__((address_space(3))) void*)s_lut1,
+                                     16, 0, 0);
+    __builtin_amdgcn_global_load_lds((const void*)(a2.lut + lane * 16), (__attribute__((address_space(3))) void*)s_lut2,
+                                     16, 0, 0);
+  }
+
+  // ---- input tile: rows r0 - 2 .. r0 + R + 1, columns -1 .. W, raw
+  // 16-byte units (out-of-image units: out-of-range loads, which return
+  // zero), all in flight together
+  const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc((void*)a1.x, (short)0, a1.x_bytes, 0x00020000);
+  const int units = (R + 4) * TW * CU;
+  const float r_tw = 1.0f / (float)TW;
+  u32x4 xv[kPairFill];
+  int xdst[kPairFill];  // LDS offset of the unit, or -1 for none
+  bool xin[kPairFill];
+#pragma unroll
+  for (int i = 0; i < kPairFill; ++i) {
+    const int u = tid + i * 256;
+    xdst[i] = -1;
+    xin[i] = false;
+    if (u < units) {
+      const int ip = u / CU;  // CU is a power of two
+      const int cu = u - ip * CU;
+      const int tr = div_small(ip, TW, r_tw), tc = ip - tr * TW;
+      const int ih = r0 - 2 + tr, iw = tc - 1;
+      const bool ok = (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W;
+      const int off = ok ? (((n * H + ih) * W + iw) * a1.x_pix_stride + a1.x_c_off + cu * 16) : (int)0x80000000;
+      xv[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrsrc, off, 0, 0));
+      xdst[i] = (ip * SU + cu) * 16;
+      xin[i] = ok;
+    }
+  }
+
+  // ---- k-slice offsets (shared by both convs: same tile geometry and
+  // channel count): slice s of k-step q is 16 input channels of one tap
+  for (int e = tid; e < KS * 4; e += 256) {
+    const int k = e * 16;
+    int off = 0;
+    if (k < 9 * C) {
+      const int tap = k / C, ci = k - (k / C) * C;
+      const int kh = tap / 3, kw = tap - (tap / 3) * 3;
+      off = ((kh * TW + kw) * SU + ci / 16) * 16;
+    }
+    s_tab[e] = off;
+  }
+
+  // ---- the intermediate tile's padding: columns -1 and W of every row,
+  // and whole rows outside the image, hold the second conv's padding
+  // pattern (phase 1 writes the rest)
+  {
+    const u32x4 pad2 = u32x4{a2.xpad, a2.xpad, a2.xpad, a2.xpad};
+    const int mrows = R + 2;
+    const int mun = mrows * TW * CU;
+    for (int u = tid; u < mun; u += 256) {
+      const int ip = u / CU;
+      const int cu = u - ip * CU;
+      const int tr = div_small(ip, TW, r_tw), tc = ip - tr * TW;
+      const int ih = r0 - 1 + tr;
+      if (tc == 0 || tc == TW - 1 || (unsigned)ih >= (unsigned)H)
+        *reinterpret_cast<u32x4*>(s_m + (ip * SU + cu) * 16) = pad2;
+    }
+  }
+
+  // everything above has landed (direct loads included); write the tile
+  __builtin_amdgcn_s_waitcnt(0);
+#pragma unroll
+  for (int i = 0; i < kPairFill; ++i) {
+    if (xdst[i] >= 0) {
+      const uint32_t key = xin[i] ? a1.xxor : a1.xpad;
+      *reinterpret_cast<u32x4*>(s_x + xdst[i]) = xv[i] ^ key;
+    }
+  }
+  __syncthreads();
+
+  const int cq = 4 * (lane >> 4);
+  const uint8_t* const a1_lane = s_w1 + lane * 16;
+  const uint8_t* const a2_lane = s_w2 + lane * 16;
+  const int* const my_tab = s_tab + (lane >> 4);
+
+  // ================= phase 1: (R + 2) x W pixels of the intermediate
+  {
+    const int np1 = (R + 2) * W;
+    int pbase[PB1];
+    int prow[PB1], pcol[PB1];
+#pragma unroll
+    for (int pb = 0; pb < PB1; ++pb) {
+      int pl = (wave * PB1 + pb) * 16 + (lane & 15);
+      if (pl >= np1) pl = -1;
+      const int q = pl < 0 ? 0 : pl;
+      const int r = div_small(q, W, a1.r_wo), c = q - r * W;
+      pbase[pb] = (r * TW + c) * SU * 16;  // tile rows r .. r + 2 feed intermediate row r
+      prow[pb] = pl < 0 ? -1 : r;
+      pcol[pb] = c;
+    }
+    v4i acc[CB][PB1];
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+      const v4i init = *reinterpret_cast<const v4i*>(s_bias1 + 4 * (cb * 16 + cq));
+#pragma unroll
+      for (int pb = 0; pb < PB1; ++pb) acc[cb][pb] = init;
+    }
+    v4i afr[2][CB], bfr[2][PB1];
+#define DW_READ_K1(q_, slot_)                                                              \
+  {                                                                                        \
+    const int toff_ = my_tab[(q_) * 4];                                                    \
+    _Pragma("unroll") for (int cb = 0; cb < CB; ++cb)                                      \
+      afr[slot_][cb] = *reinterpret_cast<const v4i*>(a1_lane + ((q_) * CB + cb) * 1024);   \
+    _Pragma("unroll") for (int pb = 0; pb < PB1; ++pb)                                     \
+      bfr[slot_][pb] = *reinterpret_cast<const v4i*>(s_x + pbase[pb] + toff_);             \
+  }
+    DW_READ_K1(0, 0);
+    for (int q0 = 0; q0 < KS; q0 += 2) {
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int q = q0 + r;
+        if (q < KS) {
+          if (q + 1 < KS) DW_READ_K1(q + 1, (r + 1) & 1);
+#pragma unroll
+          for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+            for (int pb = 0; pb < PB1; ++pb)
+              acc[cb][pb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[r][cb], bfr[r][pb], acc[cb][pb], 0, 0, 0);
+        }
+      }
+    }
+#undef DW_READ_K1
+    // epilogue 1: requantize, table, then the second conv's operand form
+    // (u8 xor 0x80) into the intermediate tile; rows outside the image keep
+    // their padding
+    const int qbase = 0x4B400000 - a1.y_zp;
+    const float qlo = 12582912.0f - (float)a1.y_zp, qhi = qlo + 255.0f;
+    const __attribute__((address_space(3))) uint8_t* lut3 = (const __attribute__((address_space(3))) uint8_t*)s_lut1;
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+      const float4 m4 = *reinterpret_cast<const float4*>(s_ms1 + 4 * (cb * 16 + cq));
+      const float ms4[4] = {m4.x, m4.y, m4.z, m4.w};
+#pragma unroll
+      for (int pb = 0; pb < PB1; ++pb) {
+        const int ih = r0 - 1 + prow[pb];
+        if (prow[pb] < 0 || (unsigned)ih >= (unsigned)H) continue;
+        uint32_t out = 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int qb = requant_bits(acc[cb][pb][r], ms4[r], qlo, qhi);
+          const int qi = lut3[(uint32_t)qb - (uint32_t)qbase];
+          out |= (uint32_t)qi << (8 * r);
+        }
+        *reinterpret_cast<uint32_t*>(s_m + ((prow[pb] * TW + pcol[pb] + 1) * SU + cb) * 16 + cq) = out ^ a2.xxor;
+      }
+    }
+  }
+  __syncthreads();
+
+  // ================= phase 2: R x W output pixels
+  {
+    int pbase[PB2];
+    int pixel[PB2];
+    int xres[PB2];  // the pixel's unit offset in the input tile (residual)
+#pragma unroll
+    for (int pb = 0; pb < PB2; ++pb) {
+      const int pl = (wave * PB2 + pb) * 16 + (lane & 15);  // 0 .. 319
+      const int r = div_small(pl, W, a1.r_wo), c = pl - r * W;
+      pbase[pb] = (r * TW + c) * SU * 16;
+      pixel[pb] = (n * H + r0 + r) * W + c;
+      xres[pb] = ((r + 2) * TW + c + 1) * SU * 16;
+    }
+    v4i acc[CB][PB2];
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+      const v4i init = *reinterpret_cast<const v4i*>(s_bias2 + 4 * (cb * 16 + cq));
+#pragma unroll
+      for (int pb = 0; pb < PB2; ++pb) acc[cb][pb] = init;
+    }
+    v4i afr[2][CB], bfr[2][PB2];
+#define DW_READ_K2(q_, slot_)                                                              \
+  {                                                                                        \
+    const int toff_ = my_tab[(q_) * 4];                                                    \
+    _Pragma("unroll") for (int cb = 0; cb < CB; ++cb)                                      \
+      afr[slot_][cb] = *reinterpret_cast<const v4i*>(a2_lane + ((q_) * CB + cb) * 1024);   \
+    _Pragma("unroll") for (int pb = 0; pb < PB2; ++pb)                                     \
+      bfr[slot_][pb] = *reinterpret_cast<const v4i*>(s_m + pbase[pb] + toff_);             \
+  }
+    DW_READ_K2(0, 0);
+    for (int q0 = 0; q0 < KS; q0 += 2) {
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int q = q0 + r;
+        if (q < KS) {
+          if (q + 1 < KS) DW_READ_K2(q + 1, (r + 1) & 1);
+#pragma unroll
+          for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+            for (int pb = 0; pb < PB2; ++pb)
+              acc[cb][pb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[r][cb], bfr[r][pb], acc[cb][pb], 0, 0, 0);
+        }
+      }
+    }
+#undef DW_READ_K2
+    // epilogue 2: requantize, table, QLinearAdd of the block input, u8 out
+    const int qbase = 0x4B400000 - a2.y_zp;
+    const float qlo = 12582912.0f - (float)a2.y_zp, qhi = qlo + 255.0f;
+    const __attribute__((address_space(3))) uint8_t* lut3 = (const __attribute__((address_space(3))) uint8_t*)s_lut2;
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+      const float4 m4 = *reinterpret_cast<const float4*>(s_ms2 + 4 * (cb * 16 + cq));
+      const float ms4[4] = {m4.x, m4.y, m4.z, m4.w};
+#pragma unroll
+      for (int pb = 0; pb < PB2; ++pb) {
+        uint32_t rres = 0;
+        if constexpr (RES) rres = *reinterpret_cast<const uint32_t*>(s_x + xres[pb] + cb * 16 + cq) ^ a1.xxor;
+        uint32_t out = 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int qb = requant_bits(acc[cb][pb][r], ms4[r], qlo, qhi);
+          int qi = lut3[(uint32_t)qb - (uint32_t)qbase];
+          if constexpr (RES) qi = qadd_u8(qi, (rres >> (8 * r)) & 0xff, a2);
+          out |= (uint32_t)qi << (8 * r);
+        }
+        uint8_t* yrow = (uint8_t*)a2.y + (size_t)pixel[pb] * a2.y_pix_stride + a2.y_c_off + cb * 16 + cq;
+        *reinterpret_cast<uint32_t*>(yrow) = out;
+      }
+    }
+  }
+}
+
+}  // namespace ig
+}  // namespace dw

@@ -84,6 +84,11 @@ struct Launch {
   std::shared_ptr<int> dw_band;  // units * 100 + band rows
   std::shared_ptr<DwArgs> dwa;
   int esize = 0;
+  // QLinearConv launches: the group's input and final output tensors (the
+  // pass that chains two convs into one launch matches them), and the
+  // tuner's time for 4 launches of the chosen tile (ms; 0 when untimed)
+  std::string t_in, t_out;
+  float tuned_ms = 0;
   // schedule over several streams: the storage this launch touches, its
   // stream, the launches on other streams it waits for, and whether a
   // later launch on another stream waits for it
@@ -216,6 +221,7 @@ struct Runtime {
   void normalize();
   void push_igemm(Launch& L, const IgemmArgs& a, int esize);
   void autotune();
+  void fuse_pairs();
   void tag_group(const Group& gr, size_t first, int gid);
   void plan_streams(int n);
   void enqueue(hipStream_t st);
@@ -385,7 +391,10 @@ void Runtime::build(Backend* b, const GraphIR& graph, bool stats_mode) {
         launches.push_back(S);
       }
   }
-  if (!stats) autotune();
+  if (!stats) {
+    autotune();
+    fuse_pairs();
+  }
   int ns = 4;
   if (const char* env = getenv("DW_GRAPH_STREAMS")) ns = atoi(env);
   plan_streams(stats ? 1 : std::max(1, std::min(ns, 8)));
@@ -1921,7 +1930,76 @@ void Runtime::emit_qconv(const Group& gr) {
     L.bytes += r.bytes();
   }
   DW_HIP(hipStreamSynchronize(be->stream));
+  L.t_in = gr.in;
+  L.t_out = gr.out;
   push_igemm(L, a, 1);
+}
+
+// Chained QLinearConv pairs in one launch (igemm_pair.h): a 3x3 conv whose
+// output only the next launch's 3x3 conv reads (the bottleneck of a C2f
+// block, c = 16, 32 or 64 channels) may run with it, the intermediate kept
+// in LDS.  The outputs are those of the two launches.  After the tile
+// tuner, each candidate pair is timed as the tuner times a tile and kept
+// only if it beats the two tuned launches.  DW_PAIR=1 keeps every
+// candidate pair, DW_PAIR=0 none; untuned plans (DW_AUTOTUNE=0,
+// DW_IGEMM_TILE) keep none unless DW_PAIR=1.
+void Runtime::fuse_pairs() {
+  const char* env = getenv("DW_PAIR");
+  if (env && env[0] == '0') return;
+  const bool force = env && env[0] == '1';
+  hipStream_t st = be->stream;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  DW_HIP(hipEventCreate(&e0));
+  DW_HIP(hipEventCreate(&e1));
+  auto readers = [&](const std::string& t) {
+    int k = 0;
+    for (auto& op : g.ops)
+      for (auto& i : op.in) k += i == t;
+    return k;
+  };
+  for (size_t i = 0; i + 1 < launches.size(); ++i) {
+    Launch& L1 = launches[i];
+    Launch& L2 = launches[i + 1];
+    if (!L1.ig || !L2.ig || L1.esize != 1 || L2.esize != 1 || L1.t_out.empty() || L2.t_in != L1.t_out) continue;
+    if (readers(L1.t_out) != 1 || std::find(g.outputs.begin(), g.outputs.end(), L1.t_out) != g.outputs.end())
+      continue;
+    if (!igemm_pair_ok(*L1.ig, *L2.ig)) continue;
+    if (!force) {
+      if (L1.tuned_ms <= 0 || L2.tuned_ms <= 0) continue;
+      launch_igemm_pair(st, *L1.ig, *L2.ig);
+      float t_min = 1e30f;
+      for (int r = 0; r < 3; ++r) {
+        DW_HIP(hipEventRecord(e0, st));
+        for (int k = 0; k < 4; ++k) launch_igemm_pair(st, *L1.ig, *L2.ig);
+        DW_HIP(hipEventRecord(e1, st));
+        DW_HIP(hipEventSynchronize(e1));
+        float ms = 0;
+        DW_HIP(hipEventElapsedTime(&ms, e0, e1));
+        t_min = std::min(t_min, ms);
+      }
+      if (t_min >= L1.tuned_ms + L2.tuned_ms) continue;
+    }
+    Launch P;
+    P.kernel = "igemm_i8_pair_c" + std::to_string(L1.ig->cin);
+    P.op = L1.op + "+" + L2.op;
+    P.work = L1.work + L2.work;
+    // the intermediate neither written nor read back
+    P.bytes = L1.bytes + L2.bytes - 2.0 * (double)T(L1.t_out).pixels() * T(L1.t_out).c;
+    auto a1 = L1.ig, a2 = L2.ig;
+    P.fn = [a1, a2](hipStream_t st) { launch_igemm_pair(st, *a1, *a2); };
+    P.esize = 1;
+    P.group = L1.group;
+    P.reads = L1.reads;
+    P.reads.insert(P.reads.end(), L2.reads.begin(), L2.reads.end());
+    P.writes = L1.writes;
+    P.writes.insert(P.writes.end(), L2.writes.begin(), L2.writes.end());
+    P.t_in = L1.t_in;
+    P.t_out = L2.t_out;
+    launches[i] = P;
+    launches.erase(launches.begin() + (long)i + 1);
+  }
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
 }
 
 // The reference's INT8 conv (s8 activations, s8 HWIO weights, zero padding):
@@ -1996,10 +2074,13 @@ void Runtime::push_igemm(Launch& L, const IgemmArgs& a, int esize) {
 // result is accumulated over, so outputs are identical for every choice.
 // The launches write only buffers the next run() rewrites.  Set
 // DW_AUTOTUNE=0 to keep the built-in heuristic (DW_IGEMM_TILE, which forces
-// a shape, also disables it).
+// a shape, also disables it).  DW_AUTOTUNE_LOG=<file> appends every
+// candidate's time per launch (op, kernel, microseconds) to that file.
 void Runtime::autotune() {
   const char* env = getenv("DW_AUTOTUNE");
   if ((env && env[0] == '0') || getenv("DW_IGEMM_TILE")) return;
+  FILE* log = nullptr;
+  if (const char* lp = getenv("DW_AUTOTUNE_LOG")) log = fopen(lp, "a");
   hipStream_t st = be->stream;
   hipEvent_t e0, e1;
   DW_HIP(hipEventCreate(&e0));
@@ -2043,6 +2124,7 @@ void Runtime::autotune() {
       a.tile_bc = bc[i];
       a.tile_pb = pb[i];
       a.tile_tpw = tpw[i];
+      if (log) fprintf(log, "%s\t%s\t", L.op.c_str(), igemm_tile_name(a, L.esize));
       launch_igemm(st, a, L.esize);
       // back-to-back launches between the events: the event overhead is
       // spread over several kernels, so close candidates are told apart
@@ -2056,6 +2138,7 @@ void Runtime::autotune() {
         DW_HIP(hipEventElapsedTime(&ms, e0, e1));
         t_min = std::min(t_min, ms);
       }
+      if (log) fprintf(log, "%.2f\n", t_min * 1e3f / 4);
       if (t_min < best) {
         best = t_min;
         bi = i;
@@ -2065,11 +2148,13 @@ void Runtime::autotune() {
       a.tile_bc = bc[bi];
       a.tile_pb = pb[bi];
       a.tile_tpw = tpw[bi];
+      L.tuned_ms = best;
     }
     L.kernel = igemm_tile_name(a, L.esize);
   }
   (void)hipEventDestroy(e0);
   (void)hipEventDestroy(e1);
+  if (log) fclose(log);
   info.clear();
 }
 

@@ -66,16 +66,22 @@ def expose_head_inputs(g, info):
     return [(h, tuple(dims[h]["dims"])) for h in heads]
 
 
-def check_mfma_head(rt, info, heads, ref, img=None):
+def mfma_head_outputs(rt, info, heads):
+    """The head inputs and the detect outputs of a run, downloaded once."""
+    return {h: rt.get_output_bytes(h).reshape(shp) for h, shp in heads}, gpu_outputs(rt, info)
+
+
+def check_mfma_head(got, info, heads, ref, img=None):
     """Default plan: the head inputs (INT8 parts) bit-exact, the fp16 head
-    outputs within 1e-2 of each output's largest magnitude.  ref: the
-    oracle's tensors (for image img of the batch when img is given)."""
+    outputs within 1e-2 of each output's largest magnitude.  got: the run's
+    tensors (mfma_head_outputs); ref: the oracle's tensors (for image img of
+    the batch when img is given)."""
     sl = slice(None) if img is None else slice(img, img + 1)
+    got_heads, got_outs = got
     for h, shp in heads:
-        got = rt.get_output_bytes(h).reshape(shp)[sl]
-        np.testing.assert_array_equal(got, ref[h], err_msg=h)
+        np.testing.assert_array_equal(got_heads[h][sl], ref[h], err_msg=h)
     worst = 0.0
-    for o, gv in zip(info["outputs"], gpu_outputs(rt, info)):
+    for o, gv in zip(info["outputs"], got_outs):
         e = rel_err(oracle.f16_to_f32(gv[sl]), oracle.f16_to_f32(ref[o]))
         worst = max(worst, e)
         assert e <= 1e-2, (o, e)
@@ -142,7 +148,7 @@ def test_int8_graph_small_mfma_head(backend):
     rt.set_input_f32(info["input"], x)
     rt.run()
     ref = oracle_run(g, {info["input"]: synth.f16_bits(x)})
-    worst = check_mfma_head(rt, info, heads, ref)
+    worst = check_mfma_head(mfma_head_outputs(rt, info, heads), info, heads, ref)
     print(f"head outputs: worst rel err {worst:.2e}")
     # the exact plan of the same graph gives the oracle's bytes
     rt_x = HipGraphRuntime(g, backend, exact_u8_f16=True)
@@ -378,15 +384,45 @@ def test_int8_graph_launch_plan(backend, int8_small):
     kinds = {}
     for L in ls:
         kinds[L["kernel"].split("_")[0]] = kinds.get(L["kernel"].split("_")[0], 0) + 1
-    # 56 int8 MFMA convs (each with its table / residual fused), the fp16
-    # stem as a direct conv, the six fp16 head 1x1 convs on the fp16 matrix
-    # cores, one SPPF cascade, two resizes, no copies or elementwise.
-    assert kinds.get("igemm") == 56, kinds
+    # 56 int8 MFMA convs (each with its table / residual fused; at 96x96 no
+    # map has whole rows dividing 320 pixels, so no bottleneck pair is
+    # chained), the fp16 stem as a direct conv, the six fp16 head 1x1 convs
+    # on the fp16 matrix cores, one SPPF cascade, two resizes, no copies or
+    # elementwise.
+    pairs = sum(L["kernel"].startswith("igemm_i8_pair") for L in ls)
+    assert pairs == 0 and kinds.get("igemm") == 56, (pairs, kinds)
     assert kinds.get("direct") == 1 and kinds.get("conv1x1") == 6, kinds
     assert kinds.get("maxpool") == 1 and kinds.get("resize") == 2, kinds
     assert "copy" not in kinds and "elementwise" not in kinds, kinds
     ms = rt.run_profiled()
     assert len(ms) == len(ls) and np.all(ms > 0)
+
+
+def test_int8_graph_pairs_bit_exact(backend, monkeypatch):
+    # At 320x320 the C2f bottlenecks of the 80x80 (16 channels) and 40x40
+    # (32 channels, with and without the shortcut) maps, and the first two
+    # 3x3 convs of the stride-8 detect head's box branch (64 channels, 40x40),
+    # run as chained pairs, the intermediate in LDS: bit-exact against the
+    # oracle, and the same bytes as the unchained launches.
+    g, info = yolo.int8_graph(backend, batch=2, size=320, calib=yolo.calibration_images(4, 320))
+    x = yolo.input_images(2, 320)
+    monkeypatch.setenv("DW_PAIR", "1")  # every candidate pair, whatever the timing
+    rt = HipGraphRuntime(g, backend, exact_u8_f16=True)
+    pairs = sorted(L["kernel"] for L in rt.launches() if L["kernel"].startswith("igemm_i8_pair"))
+    assert pairs == ["igemm_i8_pair_c16"] + ["igemm_i8_pair_c32"] * 3 + ["igemm_i8_pair_c64"], pairs
+    rt.set_input_f32(info["input"], x)
+    rt.run()
+    got = gpu_outputs(rt, info)
+    ref = oracle_run(g, {info["input"]: synth.f16_bits(x)})
+    for o, gv in zip(info["outputs"], got):
+        np.testing.assert_array_equal(gv, ref[o], err_msg=o)
+    monkeypatch.setenv("DW_PAIR", "0")
+    rt0 = HipGraphRuntime(g, backend, exact_u8_f16=True)
+    assert not any(L["kernel"].startswith("igemm_i8_pair") for L in rt0.launches())
+    rt0.set_input_f32(info["input"], x)
+    rt0.run()
+    for o, gv, g0 in zip(info["outputs"], got, gpu_outputs(rt0, info)):
+        np.testing.assert_array_equal(gv, g0, err_msg=o)
 
 
 def gpu_ranges(backend, batch, size, images):
@@ -431,11 +467,16 @@ def test_calibration_matches_oracle_small(backend):
     assert worst <= 1e-5
 
 
-def check_int8_batch_bit_exact(g, info, x, backend, graph1):
-    """Runs the batch-32 u8 graph g on the GPU (exact plan) and compares
-    every image of the batch with the oracle's CpuGraph run on the same
-    graph at batch 1."""
+def check_int8_batch_bit_exact(g, info, x, backend, graph1, monkeypatch):
+    """Runs the batch-32 u8 graph g on the GPU (exact plan, every candidate
+    pair of chained 3x3 convs in one launch) and compares every image of the
+    batch with the oracle's CpuGraph run on the same graph at batch 1."""
+    monkeypatch.setenv("DW_PAIR", "1")
     rt = HipGraphRuntime(g, backend, exact_u8_f16=True)
+    # the eight C2f bottlenecks of 16, 32 and 64 channels run as chained
+    # pairs (with and without the shortcut)
+    pairs = [L["kernel"] for L in rt.launches() if L["kernel"].startswith("igemm_i8_pair")]
+    assert sorted(pairs) == sorted(["igemm_i8_pair_c16"] + ["igemm_i8_pair_c32"] * 3 + ["igemm_i8_pair_c64"] * 4), pairs
     rt.set_input_f32(info["input"], x)
     rt.run()
     got = gpu_outputs(rt, info)
@@ -444,10 +485,12 @@ def check_int8_batch_bit_exact(g, info, x, backend, graph1):
         ref = oracle_run(g1, {info1["input"]: synth.f16_bits(x[img:img + 1])})
         for o, gv in zip(info["outputs"], got):
             np.testing.assert_array_equal(gv[img:img + 1], ref[o], err_msg=f"{o} image {img}")
+        if img % 8 == 7:
+            print(f"images 0..{img} bit-exact", flush=True)
     print(f"all {x.shape[0]} images bit-exact on all three detect outputs", flush=True)
 
 
-def test_int8_graph_full_workload_bit_exact(backend):
+def test_int8_graph_full_workload_bit_exact(backend, monkeypatch):
     # The headline workload end to end: the oracle Calibrator over the 16
     # seeded calibration images at 640x640 fixes every activation scale; the
     # GPU's calibration of the same images agrees with it (counted and
@@ -463,7 +506,7 @@ def test_int8_graph_full_workload_bit_exact(backend):
     assert worst <= 1e-5
     g, info = yolo.int8_graph_from_ranges(orr, batch=32, size=640)
     x = yolo.input_images(32, 640)
-    check_int8_batch_bit_exact(g, info, x, backend, yolo.int8_graph_from_ranges(orr, batch=1, size=640))
+    check_int8_batch_bit_exact(g, info, x, backend, yolo.int8_graph_from_ranges(orr, batch=1, size=640), monkeypatch)
 
 
 def test_int8_benchmark_graph(backend):
@@ -486,9 +529,12 @@ def test_int8_benchmark_graph(backend):
     g1, info1 = yolo.int8_graph_from_ranges(info["ranges"], batch=1, size=640)
     expose_head_inputs(g1, info1)
     worst = 0.0
+    got = mfma_head_outputs(rt, info, heads)
     for img in range(32):
         ref = oracle_run(g1, {info1["input"]: synth.f16_bits(x[img:img + 1])})
-        worst = max(worst, check_mfma_head(rt, info, heads, ref, img))
+        worst = max(worst, check_mfma_head(got, info, heads, ref, img))
+        if img % 8 == 7:
+            print(f"images 0..{img} checked", flush=True)
     print(f"all 32 images: INT8 parts bit-exact, head outputs worst rel err {worst:.2e}", flush=True)
 
 
@@ -511,6 +557,8 @@ def test_f16_graph_full_workload_vs_oracle(backend):
             e = rel_err(oracle.f16_to_f32(gv[img:img + 1]), oracle.f16_to_f32(ref[o]))
             worst = max(worst, e)
             assert e <= 1e-2, (o, img, e)
+        if img % 8 == 7:
+            print(f"images 0..{img} within tolerance", flush=True)
     print(f"all 32 images within tolerance, worst rel err {worst:.2e}", flush=True)
 
 
