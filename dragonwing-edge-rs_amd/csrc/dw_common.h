@@ -200,9 +200,12 @@ void launch_qconv_bias(hipStream_t st, const int8_t* w_hwio, const int* bias, in
 void launch_igemm(hipStream_t st, const IgemmArgs& a, int esize);
 // Two chained 3x3 QLinearConvs (c -> c -> c, c = 16, 32 or 64, stride 1,
 // padding 1; a1 writes what a2 reads, a2's residual is a1's input or none)
-// in one launch, the intermediate in LDS (k_igemm_pair.hip).
-bool igemm_pair_ok(const IgemmArgs& a1, const IgemmArgs& a2);
-void launch_igemm_pair(hipStream_t st, const IgemmArgs& a1, const IgemmArgs& a2);
+// in one launch, the intermediate in LDS, `rows` output rows per workgroup
+// (k_igemm_pair.hip).  igemm_pair_rows lists the valid band heights.
+bool igemm_pair_ok(const IgemmArgs& a1, const IgemmArgs& a2, int rows);
+int igemm_pair_rows(const IgemmArgs& a1, const IgemmArgs& a2, int* rows, int max);
+bool igemm_pair_lds_two_per_cu(const IgemmArgs& a1, int rows);  // LDS of the band <= 80 KB
+void launch_igemm_pair(hipStream_t st, const IgemmArgs& a1, const IgemmArgs& a2, int rows);
 // Returns the tile name chosen for a problem (for launch descriptions).
 const char* igemm_tile_name(const IgemmArgs& a, int esize);
 // Channel-tile width used for `cout` output channels; packed weights must

@@ -6,8 +6,9 @@
 // Each launch of a small layer carries a fixed cost of several
 // microseconds (dispatch, the first loads' latency, the epilogue, the
 // kernel's end), which on the 20x20 .. 160x160 maps of a batch-32 graph is
-// most of the layer's time.  Here a workgroup owns R output rows (whole
-// rows, 320 output pixels) of one image and every channel:
+// most of the layer's time.  Here a workgroup owns R whole output rows of
+// one image and every channel (R chosen by the runtime's tuner, a divisor of
+// the height):
 //
 //  * start-up: both convs' weights (all of K, fragment order), their
 //    epilogue data and the R + 4 input rows the two 3x3 windows reach (with
@@ -34,18 +35,17 @@
 namespace dw {
 namespace ig {
 
-constexpr int kPairPix = 320;  // output pixels per workgroup (phase 2)
-constexpr int kPairPB2 = 5;    // 16-pixel blocks per wave in phase 2
-
 struct PairArgs {
   IgemmArgs a1, a2;
-  int rows;  // output rows per workgroup (kPairPix / w)
+  int rows;  // output rows per workgroup
 };
 
+// LDS pixel stride in 16-byte units: 8 lanes reading one unit of 8
+// consecutive pixels each hit 8 distinct 16-byte bank groups
+__host__ __device__ constexpr int pair_su(int c) { return c == 32 ? 2 : (c / 16) | 1; }
 // LDS layout (bytes): two epilogue blocks (table 256, bias' 4c, multipliers
 // 4c), the k-slice table, both weight sets, the input tile, the
 // intermediate tile.
-__host__ __device__ constexpr int pair_su(int c) { return (c / 16) | 1; }
 __host__ __device__ constexpr int pair_epi_bytes(int c) { return 256 + 8 * c; }
 __host__ __device__ constexpr int pair_tab_off(int c) { return 2 * pair_epi_bytes(c); }
 __host__ __device__ constexpr int pair_w_off(int c, int ks) { return (pair_tab_off(c) + ks * 16 + 15) / 16 * 16; }
@@ -57,21 +57,24 @@ __host__ __device__ constexpr int pair_lds_bytes(int c, int ks, int w, int rows)
   return pair_m_off(c, ks, w, rows) + (rows + 2) * (w + 2) * pair_su(c) * 16;
 }
 constexpr int kPairFill = 8;  // input units each thread loads at start-up (at most)
+// 16-pixel blocks a wave computes at a time (accumulators CB x PBC)
+__host__ __device__ constexpr int pair_pbc(int cb) { return cb == 1 ? 8 : (cb == 2 ? 6 : 5); }
 
-// CB: 16-channel blocks (c / 16); PB1: 16-pixel blocks per wave in phase 1
-// ((rows + 2) * w pixels over 4 waves); RES: the second epilogue adds the
-// block input.
-template <int CB, int PB1, bool RES>
+// CB: 16-channel blocks (c / 16); RES: the second epilogue adds the block
+// input.  Both phases walk their 16-pixel blocks PBC at a time per wave
+// (blocks wave * PBC + 4 * PBC * j ..), so any band height fits the
+// registers.
+template <int CB, bool RES>
 __global__ __launch_bounds__(256, CB <= 2 ? 2 : 1) void igemm_pair_kernel(const PairArgs p) {
   constexpr int C = CB * 16;
-  constexpr int PB2 = kPairPB2;
+  constexpr int PBC = pair_pbc(CB);
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const IgemmArgs& a1 = p.a1;
   const IgemmArgs& a2 = p.a2;
   const int W = a1.w, H = a1.h, R = p.rows;
   const int TW = W + 2;
-  constexpr int CU = C / 16;  // 16-byte units per pixel
-  constexpr int SU = CU | 1;  // LDS pixel stride in units
+  constexpr int CU = C / 16;       // 16-byte units per pixel
+  constexpr int SU = pair_su(C);   // LDS pixel stride in units
   const int KS = a1.ksteps;
 
   const int tid = threadIdx.x;
@@ -108,8 +111,8 @@ __global__ __launch_bounds__(256, CB <= 2 ? 2 : 1) void igemm_pair_kernel(const 
       const int second = f >= nfr;
       const int ff = f - second * nfr;
       const int sl = ff / CB, cb = ff - sl * CB;
-      const IgemmArgs& aa = second ? a2 : a1;
-      const uint8_t* src = aa.wpk + (((uint32_t)sl * aa.cout_pad + cb * 16) * 64u + frag_lane);
+      const uint8_t* src = (second ? a2.wpk : a1.wpk) +
+                           (((uint32_t)sl * (second ? a2.cout_pad : a1.cout_pad) + cb * 16) * 64u + frag_lane);
       __builtin_amdgcn_global_load_lds((const void*)src,
                                        (__attribute__((address_space(3))) void*)((second ? s_w2 : s_w1) + ff * 1024),
                                        16, 0, 0);
@@ -179,8 +182,7 @@ __global__ __launch_bounds__(256, CB <= 2 ? 2 : 1) void igemm_pair_kernel(const 
   // pattern (phase 1 writes the rest)
   {
     const u32x4 pad2 = u32x4{a2.xpad, a2.xpad, a2.xpad, a2.xpad};
-    const int mrows = R + 2;
-    const int mun = mrows * TW * CU;
+    const int mun = (R + 2) * TW * CU;
     for (int u = tid; u < mun; u += 256) {
       const int ip = u / CU;
       const int cu = u - ip * CU;
@@ -203,79 +205,85 @@ __global__ __launch_bounds__(256, CB <= 2 ? 2 : 1) void igemm_pair_kernel(const 
   __syncthreads();
 
   const int cq = 4 * (lane >> 4);
-  const uint8_t* const a1_lane = s_w1 + lane * 16;
-  const uint8_t* const a2_lane = s_w2 + lane * 16;
   const int* const my_tab = s_tab + (lane >> 4);
 
-  // ================= phase 1: (R + 2) x W pixels of the intermediate
-  {
-    const int np1 = (R + 2) * W;
-    int pbase[PB1];
-    int prow[PB1], pcol[PB1];
-#pragma unroll
-    for (int pb = 0; pb < PB1; ++pb) {
-      int pl = (wave * PB1 + pb) * 16 + (lane & 15);
-      if (pl >= np1) pl = -1;
-      const int q = pl < 0 ? 0 : pl;
-      const int r = div_small(q, W, a1.r_wo), c = q - r * W;
-      pbase[pb] = (r * TW + c) * SU * 16;  // tile rows r .. r + 2 feed intermediate row r
-      prow[pb] = pl < 0 ? -1 : r;
-      pcol[pb] = c;
-    }
-    v4i acc[CB][PB1];
-#pragma unroll
-    for (int cb = 0; cb < CB; ++cb) {
-      const v4i init = *reinterpret_cast<const v4i*>(s_bias1 + 4 * (cb * 16 + cq));
-#pragma unroll
-      for (int pb = 0; pb < PB1; ++pb) acc[cb][pb] = init;
-    }
-    v4i afr[2][CB], bfr[2][PB1];
-#define DW_READ_K1(q_, slot_)                                                              \
-  {                                                                                        \
-    const int toff_ = my_tab[(q_) * 4];                                                    \
-    _Pragma("unroll") for (int cb = 0; cb < CB; ++cb)                                      \
-      afr[slot_][cb] = *reinterpret_cast<const v4i*>(a1_lane + ((q_) * CB + cb) * 1024);   \
-    _Pragma("unroll") for (int pb = 0; pb < PB1; ++pb)                                     \
-      bfr[slot_][pb] = *reinterpret_cast<const v4i*>(s_x + pbase[pb] + toff_);             \
+  // One chunk of PBC blocks: the k-loop over both operands in LDS (the next
+  // k-step's fragments read while this one's MFMAs run).  src: the tile the
+  // windows read; wl: this lane's weight fragments; pbase: each block's
+  // top-left tap in the tile.
+  auto chunk_gemm = [&](v4i (&acc)[CB][PBC], const uint8_t* src, const uint8_t* wl, const int (&pbase)[PBC]) {
+    v4i afr[2][CB], bfr[2][PBC];
+#define DW_READ_K(q_, slot_)                                                            \
+  {                                                                                     \
+    const int toff_ = my_tab[(q_) * 4];                                                 \
+    _Pragma("unroll") for (int cb = 0; cb < CB; ++cb)                                   \
+      afr[slot_][cb] = *reinterpret_cast<const v4i*>(wl + ((q_) * CB + cb) * 1024);     \
+    _Pragma("unroll") for (int pb = 0; pb < PBC; ++pb)                                  \
+      bfr[slot_][pb] = *reinterpret_cast<const v4i*>(src + pbase[pb] + toff_);          \
   }
-    DW_READ_K1(0, 0);
+    DW_READ_K(0, 0);
     for (int q0 = 0; q0 < KS; q0 += 2) {
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
         const int q = q0 + r;
         if (q < KS) {
-          if (q + 1 < KS) DW_READ_K1(q + 1, (r + 1) & 1);
+          if (q + 1 < KS) DW_READ_K(q + 1, (r + 1) & 1);
 #pragma unroll
           for (int cb = 0; cb < CB; ++cb)
 #pragma unroll
-            for (int pb = 0; pb < PB1; ++pb)
+            for (int pb = 0; pb < PBC; ++pb)
               acc[cb][pb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[r][cb], bfr[r][pb], acc[cb][pb], 0, 0, 0);
         }
       }
     }
-#undef DW_READ_K1
-    // epilogue 1: requantize, table, then the second conv's operand form
-    // (u8 xor 0x80) into the intermediate tile; rows outside the image keep
-    // their padding
+#undef DW_READ_K
+  };
+
+  // ================= phase 1: (R + 2) x W pixels of the intermediate
+  {
+    const int np = (R + 2) * W;
+    const int nb = (np + 15) / 16;
     const int qbase = 0x4B400000 - a1.y_zp;
     const float qlo = 12582912.0f - (float)a1.y_zp, qhi = qlo + 255.0f;
     const __attribute__((address_space(3))) uint8_t* lut3 = (const __attribute__((address_space(3))) uint8_t*)s_lut1;
+    for (int b0 = wave * PBC; b0 < nb; b0 += 4 * PBC) {
+      int pbase[PBC], poff[PBC];  // window in the input tile; result in the intermediate tile (-1: none)
 #pragma unroll
-    for (int cb = 0; cb < CB; ++cb) {
-      const float4 m4 = *reinterpret_cast<const float4*>(s_ms1 + 4 * (cb * 16 + cq));
-      const float ms4[4] = {m4.x, m4.y, m4.z, m4.w};
+      for (int pb = 0; pb < PBC; ++pb) {
+        const int pl = (b0 + pb) * 16 + (lane & 15);
+        const int q = pl < np ? pl : 0;
+        const int r = div_small(q, W, a1.r_wo), c = q - r * W;
+        pbase[pb] = (r * TW + c) * SU * 16;  // tile rows r .. r + 2 feed intermediate row r
+        const int ih = r0 - 1 + r;
+        poff[pb] = (pl < np && (unsigned)ih < (unsigned)H) ? ((r * TW + c + 1) * SU * 16 + cq) : -1;
+      }
+      v4i acc[CB][PBC];
 #pragma unroll
-      for (int pb = 0; pb < PB1; ++pb) {
-        const int ih = r0 - 1 + prow[pb];
-        if (prow[pb] < 0 || (unsigned)ih >= (unsigned)H) continue;
-        uint32_t out = 0;
+      for (int cb = 0; cb < CB; ++cb) {
+        const v4i init = *reinterpret_cast<const v4i*>(s_bias1 + 4 * (cb * 16 + cq));
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int qb = requant_bits(acc[cb][pb][r], ms4[r], qlo, qhi);
-          const int qi = lut3[(uint32_t)qb - (uint32_t)qbase];
-          out |= (uint32_t)qi << (8 * r);
+        for (int pb = 0; pb < PBC; ++pb) acc[cb][pb] = init;
+      }
+      chunk_gemm(acc, s_x, s_w1 + lane * 16, pbase);
+      // epilogue 1: requantize, table, then the second conv's operand form
+      // (u8 xor 0x80) into the intermediate tile; rows outside the image
+      // keep their padding
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) {
+        const float4 m4 = *reinterpret_cast<const float4*>(s_ms1 + 4 * (cb * 16 + cq));
+        const float ms4[4] = {m4.x, m4.y, m4.z, m4.w};
+#pragma unroll
+        for (int pb = 0; pb < PBC; ++pb) {
+          if (poff[pb] < 0) continue;
+          uint32_t out = 0;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int qb = requant_bits(acc[cb][pb][r], ms4[r], qlo, qhi);
+            const int qi = lut3[(uint32_t)qb - (uint32_t)qbase];
+            out |= (uint32_t)qi << (8 * r);
+          }
+          *reinterpret_cast<uint32_t*>(s_m + poff[pb] + cb * 16) = out ^ a2.xxor;
         }
-        *reinterpret_cast<uint32_t*>(s_m + ((prow[pb] * TW + pcol[pb] + 1) * SU + cb) * 16 + cq) = out ^ a2.xxor;
       }
     }
   }
@@ -283,71 +291,51 @@ __global__ __launch_bounds__(256, CB <= 2 ? 2 : 1) void igemm_pair_kernel(const 
 
   // ================= phase 2: R x W output pixels
   {
-    int pbase[PB2];
-    int pixel[PB2];
-    int xres[PB2];  // the pixel's unit offset in the input tile (residual)
-#pragma unroll
-    for (int pb = 0; pb < PB2; ++pb) {
-      const int pl = (wave * PB2 + pb) * 16 + (lane & 15);  // 0 .. 319
-      const int r = div_small(pl, W, a1.r_wo), c = pl - r * W;
-      pbase[pb] = (r * TW + c) * SU * 16;
-      pixel[pb] = (n * H + r0 + r) * W + c;
-      xres[pb] = ((r + 2) * TW + c + 1) * SU * 16;
-    }
-    v4i acc[CB][PB2];
-#pragma unroll
-    for (int cb = 0; cb < CB; ++cb) {
-      const v4i init = *reinterpret_cast<const v4i*>(s_bias2 + 4 * (cb * 16 + cq));
-#pragma unroll
-      for (int pb = 0; pb < PB2; ++pb) acc[cb][pb] = init;
-    }
-    v4i afr[2][CB], bfr[2][PB2];
-#define DW_READ_K2(q_, slot_)                                                              \
-  {                                                                                        \
-    const int toff_ = my_tab[(q_) * 4];                                                    \
-    _Pragma("unroll") for (int cb = 0; cb < CB; ++cb)                                      \
-      afr[slot_][cb] = *reinterpret_cast<const v4i*>(a2_lane + ((q_) * CB + cb) * 1024);   \
-    _Pragma("unroll") for (int pb = 0; pb < PB2; ++pb)                                     \
-      bfr[slot_][pb] = *reinterpret_cast<const v4i*>(s_m + pbase[pb] + toff_);             \
-  }
-    DW_READ_K2(0, 0);
-    for (int q0 = 0; q0 < KS; q0 += 2) {
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const int q = q0 + r;
-        if (q < KS) {
-          if (q + 1 < KS) DW_READ_K2(q + 1, (r + 1) & 1);
-#pragma unroll
-          for (int cb = 0; cb < CB; ++cb)
-#pragma unroll
-            for (int pb = 0; pb < PB2; ++pb)
-              acc[cb][pb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[r][cb], bfr[r][pb], acc[cb][pb], 0, 0, 0);
-        }
-      }
-    }
-#undef DW_READ_K2
-    // epilogue 2: requantize, table, QLinearAdd of the block input, u8 out
+    const int np = R * W;
+    const int nb = (np + 15) / 16;
     const int qbase = 0x4B400000 - a2.y_zp;
     const float qlo = 12582912.0f - (float)a2.y_zp, qhi = qlo + 255.0f;
     const __attribute__((address_space(3))) uint8_t* lut3 = (const __attribute__((address_space(3))) uint8_t*)s_lut2;
+    for (int b0 = wave * PBC; b0 < nb; b0 += 4 * PBC) {
+      int pbase[PBC], pixel[PBC], xres[PBC];  // window; output pixel (-1: none); the residual's unit
 #pragma unroll
-    for (int cb = 0; cb < CB; ++cb) {
-      const float4 m4 = *reinterpret_cast<const float4*>(s_ms2 + 4 * (cb * 16 + cq));
-      const float ms4[4] = {m4.x, m4.y, m4.z, m4.w};
+      for (int pb = 0; pb < PBC; ++pb) {
+        const int pl = (b0 + pb) * 16 + (lane & 15);
+        const int q = pl < np ? pl : 0;
+        const int r = div_small(q, W, a1.r_wo), c = q - r * W;
+        pbase[pb] = (r * TW + c) * SU * 16;
+        pixel[pb] = pl < np ? (n * H + r0 + r) * W + c : -1;
+        xres[pb] = ((r + 2) * TW + c + 1) * SU * 16 + cq;
+      }
+      v4i acc[CB][PBC];
 #pragma unroll
-      for (int pb = 0; pb < PB2; ++pb) {
-        uint32_t rres = 0;
-        if constexpr (RES) rres = *reinterpret_cast<const uint32_t*>(s_x + xres[pb] + cb * 16 + cq) ^ a1.xxor;
-        uint32_t out = 0;
+      for (int cb = 0; cb < CB; ++cb) {
+        const v4i init = *reinterpret_cast<const v4i*>(s_bias2 + 4 * (cb * 16 + cq));
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int qb = requant_bits(acc[cb][pb][r], ms4[r], qlo, qhi);
-          int qi = lut3[(uint32_t)qb - (uint32_t)qbase];
-          if constexpr (RES) qi = qadd_u8(qi, (rres >> (8 * r)) & 0xff, a2);
-          out |= (uint32_t)qi << (8 * r);
+        for (int pb = 0; pb < PBC; ++pb) acc[cb][pb] = init;
+      }
+      chunk_gemm(acc, s_m, s_w2 + lane * 16, pbase);
+      // epilogue 2: requantize, table, QLinearAdd of the block input, u8 out
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) {
+        const float4 m4 = *reinterpret_cast<const float4*>(s_ms2 + 4 * (cb * 16 + cq));
+        const float ms4[4] = {m4.x, m4.y, m4.z, m4.w};
+#pragma unroll
+        for (int pb = 0; pb < PBC; ++pb) {
+          if (pixel[pb] < 0) continue;
+          uint32_t rres = 0;
+          if constexpr (RES) rres = *reinterpret_cast<const uint32_t*>(s_x + xres[pb] + cb * 16) ^ a1.xxor;
+          uint32_t out = 0;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int qb = requant_bits(acc[cb][pb][r], ms4[r], qlo, qhi);
+            int qi = lut3[(uint32_t)qb - (uint32_t)qbase];
+            if constexpr (RES) qi = qadd_u8(qi, (rres >> (8 * r)) & 0xff, a2);
+            out |= (uint32_t)qi << (8 * r);
+          }
+          uint8_t* yrow = (uint8_t*)a2.y + (size_t)pixel[pb] * a2.y_pix_stride + a2.y_c_off + cb * 16 + cq;
+          *reinterpret_cast<uint32_t*>(yrow) = out;
         }
-        uint8_t* yrow = (uint8_t*)a2.y + (size_t)pixel[pb] * a2.y_pix_stride + a2.y_c_off + cb * 16 + cq;
-        *reinterpret_cast<uint32_t*>(yrow) = out;
       }
     }
   }

@@ -1939,23 +1939,43 @@ void Runtime::emit_qconv(const Group& gr) {
 // output only the next launch's 3x3 conv reads (the bottleneck of a C2f
 // block, c = 16, 32 or 64 channels) may run with it, the intermediate kept
 // in LDS.  The outputs are those of the two launches.  After the tile
-// tuner, each candidate pair is timed as the tuner times a tile and kept
-// only if it beats the two tuned launches.  DW_PAIR=1 keeps every
-// candidate pair, DW_PAIR=0 none; untuned plans (DW_AUTOTUNE=0,
-// DW_IGEMM_TILE) keep none unless DW_PAIR=1.
+// tuner, each candidate pair is timed at every valid band height, as the
+// tuner times a tile, and kept (at its fastest height) only if it beats the
+// two tuned launches.  DW_PAIR=1 keeps every candidate pair, DW_PAIR=0
+// none; untuned plans (DW_AUTOTUNE=0, DW_IGEMM_TILE) keep none unless
+// DW_PAIR=1, which then takes the tallest band that leaves two workgroups
+// a CU their LDS (or the tallest).  DW_PAIR_ROWS=<r> forces band height r
+// wherever it is valid (tests).
 void Runtime::fuse_pairs() {
   const char* env = getenv("DW_PAIR");
   if (env && env[0] == '0') return;
   const bool force = env && env[0] == '1';
-  hipStream_t st = be->stream;
-  hipEvent_t e0 = nullptr, e1 = nullptr;
-  DW_HIP(hipEventCreate(&e0));
-  DW_HIP(hipEventCreate(&e1));
+  const char* tune_env = getenv("DW_AUTOTUNE");
+  const bool tuned = !((tune_env && tune_env[0] == '0') || getenv("DW_IGEMM_TILE"));
+  if (!force && !tuned) return;
   auto readers = [&](const std::string& t) {
     int k = 0;
     for (auto& op : g.ops)
       for (auto& i : op.in) k += i == t;
     return k;
+  };
+  hipStream_t st = be->stream;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  DW_HIP(hipEventCreate(&e0));
+  DW_HIP(hipEventCreate(&e1));
+  auto time4 = [&](const IgemmArgs& a1, const IgemmArgs& a2, int rows) {
+    launch_igemm_pair(st, a1, a2, rows);
+    float t_min = 1e30f;
+    for (int r = 0; r < 3; ++r) {
+      DW_HIP(hipEventRecord(e0, st));
+      for (int k = 0; k < 4; ++k) launch_igemm_pair(st, a1, a2, rows);
+      DW_HIP(hipEventRecord(e1, st));
+      DW_HIP(hipEventSynchronize(e1));
+      float ms = 0;
+      DW_HIP(hipEventElapsedTime(&ms, e0, e1));
+      t_min = std::min(t_min, ms);
+    }
+    return t_min;
   };
   for (size_t i = 0; i + 1 < launches.size(); ++i) {
     Launch& L1 = launches[i];
@@ -1963,21 +1983,31 @@ void Runtime::fuse_pairs() {
     if (!L1.ig || !L2.ig || L1.esize != 1 || L2.esize != 1 || L1.t_out.empty() || L2.t_in != L1.t_out) continue;
     if (readers(L1.t_out) != 1 || std::find(g.outputs.begin(), g.outputs.end(), L1.t_out) != g.outputs.end())
       continue;
-    if (!igemm_pair_ok(*L1.ig, *L2.ig)) continue;
-    if (!force) {
+    int cand[16];
+    const int nc = igemm_pair_rows(*L1.ig, *L2.ig, cand, 16);
+    if (nc == 0) continue;
+    int rows = cand[0];
+    if (tuned) {
       if (L1.tuned_ms <= 0 || L2.tuned_ms <= 0) continue;
-      launch_igemm_pair(st, *L1.ig, *L2.ig);
-      float t_min = 1e30f;
-      for (int r = 0; r < 3; ++r) {
-        DW_HIP(hipEventRecord(e0, st));
-        for (int k = 0; k < 4; ++k) launch_igemm_pair(st, *L1.ig, *L2.ig);
-        DW_HIP(hipEventRecord(e1, st));
-        DW_HIP(hipEventSynchronize(e1));
-        float ms = 0;
-        DW_HIP(hipEventElapsedTime(&ms, e0, e1));
-        t_min = std::min(t_min, ms);
+      float best = 1e30f;
+      for (int k = 0; k < nc; ++k) {
+        const float t = time4(*L1.ig, *L2.ig, cand[k]);
+        if (t < best) {
+          best = t;
+          rows = cand[k];
+        }
       }
-      if (t_min >= L1.tuned_ms + L2.tuned_ms) continue;
+      if (!force && best >= L1.tuned_ms + L2.tuned_ms) continue;
+    } else {
+      for (int k = 0; k < nc; ++k)
+        if (igemm_pair_lds_two_per_cu(*L1.ig, cand[k])) {
+          rows = cand[k];
+          break;
+        }
+    }
+    if (const char* fr = getenv("DW_PAIR_ROWS")) {
+      const int r = atoi(fr);
+      if (igemm_pair_ok(*L1.ig, *L2.ig, r)) rows = r;
     }
     Launch P;
     P.kernel = "igemm_i8_pair_c" + std::to_string(L1.ig->cin);
@@ -1986,7 +2016,7 @@ void Runtime::fuse_pairs() {
     // the intermediate neither written nor read back
     P.bytes = L1.bytes + L2.bytes - 2.0 * (double)T(L1.t_out).pixels() * T(L1.t_out).c;
     auto a1 = L1.ig, a2 = L2.ig;
-    P.fn = [a1, a2](hipStream_t st) { launch_igemm_pair(st, *a1, *a2); };
+    P.fn = [a1, a2, rows](hipStream_t s) { launch_igemm_pair(s, *a1, *a2, rows); };
     P.esize = 1;
     P.group = L1.group;
     P.reads = L1.reads;

@@ -399,23 +399,34 @@ def test_int8_graph_launch_plan(backend, int8_small):
 
 
 def test_int8_graph_pairs_bit_exact(backend, monkeypatch):
-    # At 320x320 the C2f bottlenecks of the 80x80 (16 channels) and 40x40
-    # (32 channels, with and without the shortcut) maps, and the first two
-    # 3x3 convs of the stride-8 detect head's box branch (64 channels, 40x40),
-    # run as chained pairs, the intermediate in LDS: bit-exact against the
-    # oracle, and the same bytes as the unchained launches.
+    # At 320x320 the C2f bottlenecks of the 80x80 (16 channels), 40x40 (32
+    # channels, with and without the shortcut) and 20x20 (64 channels) maps,
+    # and the first two 3x3 convs of the stride-8 detect head's box branch
+    # (64 channels, 40x40), run as chained pairs, the intermediate in LDS:
+    # bit-exact against the oracle, and the same bytes as the unchained
+    # launches.
     g, info = yolo.int8_graph(backend, batch=2, size=320, calib=yolo.calibration_images(4, 320))
     x = yolo.input_images(2, 320)
     monkeypatch.setenv("DW_PAIR", "1")  # every candidate pair, whatever the timing
     rt = HipGraphRuntime(g, backend, exact_u8_f16=True)
     pairs = sorted(L["kernel"] for L in rt.launches() if L["kernel"].startswith("igemm_i8_pair"))
-    assert pairs == ["igemm_i8_pair_c16"] + ["igemm_i8_pair_c32"] * 3 + ["igemm_i8_pair_c64"], pairs
+    assert pairs == ["igemm_i8_pair_c16"] + ["igemm_i8_pair_c32"] * 3 + ["igemm_i8_pair_c64"] * 5, pairs
     rt.set_input_f32(info["input"], x)
     rt.run()
     got = gpu_outputs(rt, info)
     ref = oracle_run(g, {info["input"]: synth.f16_bits(x)})
     for o, gv in zip(info["outputs"], got):
         np.testing.assert_array_equal(gv, ref[o], err_msg=o)
+    # every band height (rows per workgroup; heights invalid for a pair
+    # leave its choice as it is), and the unchained launches
+    for rows in ("1", "2", "4", "5", "8"):
+        monkeypatch.setenv("DW_PAIR_ROWS", rows)
+        rtr = HipGraphRuntime(g, backend, exact_u8_f16=True)
+        rtr.set_input_f32(info["input"], x)
+        rtr.run()
+        for o, gv, gr in zip(info["outputs"], got, gpu_outputs(rtr, info)):
+            np.testing.assert_array_equal(gv, gr, err_msg=f"{o} rows {rows}")
+    monkeypatch.delenv("DW_PAIR_ROWS")
     monkeypatch.setenv("DW_PAIR", "0")
     rt0 = HipGraphRuntime(g, backend, exact_u8_f16=True)
     assert not any(L["kernel"].startswith("igemm_i8_pair") for L in rt0.launches())
@@ -473,10 +484,11 @@ def check_int8_batch_bit_exact(g, info, x, backend, graph1, monkeypatch):
     batch with the oracle's CpuGraph run on the same graph at batch 1."""
     monkeypatch.setenv("DW_PAIR", "1")
     rt = HipGraphRuntime(g, backend, exact_u8_f16=True)
-    # the eight C2f bottlenecks of 16, 32 and 64 channels run as chained
-    # pairs (with and without the shortcut)
+    # the eight C2f bottlenecks of 16, 32 and 64 channels (with and without
+    # the shortcut) and the stride-8 head's first two box convs run as
+    # chained pairs
     pairs = [L["kernel"] for L in rt.launches() if L["kernel"].startswith("igemm_i8_pair")]
-    assert sorted(pairs) == sorted(["igemm_i8_pair_c16"] + ["igemm_i8_pair_c32"] * 3 + ["igemm_i8_pair_c64"] * 4), pairs
+    assert sorted(pairs) == sorted(["igemm_i8_pair_c16"] + ["igemm_i8_pair_c32"] * 3 + ["igemm_i8_pair_c64"] * 5), pairs
     rt.set_input_f32(info["input"], x)
     rt.run()
     got = gpu_outputs(rt, info)
