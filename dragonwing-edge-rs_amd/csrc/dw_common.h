@@ -85,6 +85,15 @@ struct IgemmArgs {
   int x_bytes;             // set by the launcher: bytes of the input view's buffer (< 2^31)
   float r_cin, r_kw, r_hwo, r_wo;  // set by the launcher: 1/cin, 1/kw, 1/(ho*wo), 1/wo
   int y_bytes, r_bytes;            // set by the launcher: bytes of the output and residual views
+  // EPI_QU8 with a detect head's u8 -> f16 1x1 conv fused (h_wfrag set):
+  // the u8 results (requantized, table) are not stored but feed that conv,
+  // conv1x1_u8_f16's arithmetic, whose f16 outputs are (c_out <= BC)
+  const uint16_t* h_wfrag;  // its weights in fragment order [cb][ks][64][8], or null
+  const uint16_t* h_bias;   // f16 bias or null
+  uint16_t* h_y;            // f16 output view
+  int h_cout, h_y_pix_stride, h_y_c_off, h_act;
+  float h_scale;            // the u8 results' quantization (the 1x1's input)
+  int h_zp;
 };
 
 // Arguments of the direct convolution with the reference accumulation order.

@@ -137,6 +137,42 @@ __device__ __forceinline__ h16x2 silu_f16_pk_lite(h16x2 x) {
   return x * pk_f2h(r[0], r[1]);
 }
 
+// The u8 -> f16 1x1 convolution's per-lane pieces (conv1x1_u8_f16_mfma_kernel
+// and the igemm epilogue that runs the same conv on a tile's u8 results):
+// DequantizeLinear of 8 bytes, f16((q - zp) * scale) with the product
+// rounded to f32 first (byte j -> element j), and the f16 epilogue of one
+// lane's 4 accumulators (rounded to f16 two at a time, the f16 bias added,
+// the activation), as the two 32-bit words the lane stores.
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ f16x8 dequant_u8x8_f16(uint2 u, float zp, float scale) {
+  f16x8 r;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t w = j < 4 ? u.x : u.y;
+    const float q = (float)((w >> (8 * (j & 3))) & 0xffu);
+    float f = (q - zp) * scale;
+    asm("" : "+v"(f));  // round the product to f32 before the f16 conversion
+    r[j] = (_Float16)f;
+  }
+  return r;
+}
+__device__ __forceinline__ uint2 conv1x1_f16_finish(f32x4 acc, const uint16_t* bias4, int act) {
+  h16x2 lo = pk_f2h(acc[0], acc[1]), hi = pk_f2h(acc[2], acc[3]);
+  if (bias4) {
+    lo = lo + __builtin_bit_cast(h16x2, *reinterpret_cast<const uint32_t*>(bias4));
+    hi = hi + __builtin_bit_cast(h16x2, *reinterpret_cast<const uint32_t*>(bias4 + 2));
+  }
+  if (act == ACT_SILU) {
+    lo = silu_f16_pk_lite(lo);
+    hi = silu_f16_pk_lite(hi);
+  } else if (act == ACT_RELU) {
+    lo = pk_make(f16_act_bits(pk_lo(lo), ACT_RELU), f16_act_bits(pk_hi(lo), ACT_RELU));
+    hi = pk_make(f16_act_bits(pk_lo(hi), ACT_RELU), f16_act_bits(pk_hi(hi), ACT_RELU));
+  }
+  return make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+}
+
 // acc + (f16 half SEL of x) * (f16 half SEL of w), fused, in f32: the f16
 // values widen exactly (subnormals at their IEEE value).  One v_fma_mix per
 // product; written out because the compiler otherwise widens reused

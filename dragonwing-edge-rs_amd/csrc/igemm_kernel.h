@@ -60,7 +60,8 @@ enum EpiVariant : int {
   EPV_GENERIC = 0,     // any epilogue, decided at run time
   EPV_QU8 = 1,         // requantize to u8
   EPV_QU8_LUT = 2,     // requantize, then the activation table
-  EPV_QU8_LUT_RES = 3  // requantize, table, then the residual QLinearAdd
+  EPV_QU8_LUT_RES = 3, // requantize, table, then the residual QLinearAdd
+  EPV_QU8_LUT_HEAD = 4 // requantize, table, then the fused u8 -> f16 1x1 head conv
 };
 
 // Launch one instantiation (defined in the k_igemm_*.hip files); false if
@@ -68,6 +69,7 @@ enum EpiVariant : int {
 bool igemm_launch_i8_a(hipStream_t st, const IgemmArgs& a, const TileCfg& t, int epv);  // generic, QU8
 bool igemm_launch_i8_b(hipStream_t st, const IgemmArgs& a, const TileCfg& t, int epv);  // LUT variants
 bool igemm_launch_f16(hipStream_t st, const IgemmArgs& a, const TileCfg& t);
+bool igemm_launch_head_i8(hipStream_t st, const IgemmArgs& a, const TileCfg& t);  // EPV_QU8_LUT_HEAD
 
 namespace ig {
 
@@ -272,6 +274,75 @@ __device__ __forceinline__ void pixel_setup(const IgemmArgs& a, int p0, int lane
 __host__ __device__ constexpr int xpose_row(int bc) { return bc + 16; }
 __host__ __device__ constexpr int xpose_bytes(int bc) { return 4 * 16 * xpose_row(bc); }
 
+// EPV_QU8_LUT_HEAD: the tile holds every channel of its pixels (BC >= the
+// conv's c_out, c0 = 0).  Per 16-pixel block the u8 results (requantized,
+// table) go to this wave's LDS rows xp (16 pixels x xpose_row(BC) bytes),
+// and each lane reads back the 8 consecutive channels of its pixel that the
+// fp16 MFMA's B operand takes, dequantized as DequantizeLinear does; the
+// head's 1x1 conv then runs on the fp16 matrix cores and its f16 outputs
+// are stored: conv1x1_u8_f16_mfma_kernel's arithmetic (same operands, same
+// k-order, same epilogue), so the outputs are that kernel's.  The 1x1's
+// weight fragments come from global memory (L2) into registers.
+template <int BC, int PB>
+__device__ __forceinline__ void igemm_store_head(const IgemmArgs& a, const v4i (&acc)[BC / 16][PB], int p0, int lane,
+                                                 const uint8_t* s_ms, const uint8_t* s_lut, uint8_t* xp) {
+  constexpr int CB = BC / 16;
+  constexpr int KS2 = (BC + 31) / 32;  // the 1x1's k-steps over the BC u8 channels
+  const int cq = 4 * (lane >> 4);
+  const int qbase = 0x4B400000 - a.y_zp;
+  const float qlo = 12582912.0f - (float)a.y_zp, qhi = qlo + 255.0f;
+  const __attribute__((address_space(3))) uint8_t* lut3 = (const __attribute__((address_space(3))) uint8_t*)s_lut;
+  uint8_t* const xrow = xp + (lane & 15) * xpose_row(BC);
+  const int ncb2 = (a.h_cout + 15) / 16;
+  v8h wf[CB][KS2];
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+    for (int ks = 0; ks < KS2; ++ks)
+      wf[cb][ks] = cb < ncb2 ? *reinterpret_cast<const v8h*>(a.h_wfrag + (((size_t)cb * KS2 + ks) * 64 + lane) * 8)
+                             : v8h{};
+  float4 msr[CB];
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb) msr[cb] = *reinterpret_cast<const float4*>(s_ms + 4 * (cb * 16 + cq));
+  const float zp = (float)a.h_zp, scale = a.h_scale;
+  const uint32_t zpb = (uint32_t)(a.h_zp & 0xff) * 0x01010101u;
+#pragma unroll
+  for (int pb = 0; pb < PB; ++pb) {
+    const int p = p0 + pb * 16 + (lane & 15);
+    asm volatile("" ::: "memory");  // the previous block's reads are issued
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+      const float ms4[4] = {msr[cb].x, msr[cb].y, msr[cb].z, msr[cb].w};
+      uint32_t out = 0;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int qb = requant_bits(acc[cb][pb][r], ms4[r], qlo, qhi);
+        out |= (uint32_t)lut3[(uint32_t)qb - (uint32_t)qbase] << (8 * r);
+      }
+      *reinterpret_cast<uint32_t*>(xrow + cb * 16 + cq) = out;
+    }
+    asm volatile("" ::: "memory");  // one wave's LDS operations run in order
+    v8h xf[KS2];
+#pragma unroll
+    for (int ks = 0; ks < KS2; ++ks) {
+      const int k = ks * 32 + (lane >> 4) * 8;
+      const uint2 raw = k < BC ? *reinterpret_cast<const uint2*>(xrow + k) : make_uint2(zpb, zpb);
+      xf[ks] = dequant_u8x8_f16(raw, zp, scale);
+    }
+    uint16_t* yrow = a.h_y + (size_t)p * a.h_y_pix_stride + a.h_y_c_off;
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+      const int ch = cb * 16 + cq;
+      if (cb >= ncb2) break;  // wave-uniform
+      v4f acc2 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int ks = 0; ks < KS2; ++ks) acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[cb][ks], xf[ks], acc2, 0, 0, 0);
+      if (p < a.m && ch < a.h_cout)
+        *reinterpret_cast<uint2*>(yrow + ch) = conv1x1_f16_finish(acc2, a.h_bias ? a.h_bias + ch : nullptr, a.h_act);
+    }
+  }
+}
+
 // Epilogue of a workgroup's tile: this lane holds channels c0 + cb*16 + cq
 // .. +3 of pixel p0 + pb*16 + (lane & 15) for every block (cb, pb).  The
 // specialised int8 epilogues (EPV) take bias' from the accumulators' start
@@ -288,7 +359,9 @@ __device__ __forceinline__ void igemm_store(const IgemmArgs& a, const EpiLds& ep
   constexpr int CB = BC / 16;
   constexpr bool FAST = EPV != EPV_GENERIC;
   const int cq = 4 * (lane >> 4);
-  if constexpr (FAST) {
+  if constexpr (EPV == EPV_QU8_LUT_HEAD) {
+    igemm_store_head<BC, PB>(a, acc, p0, lane, s_ms, s_lut, xp);
+  } else if constexpr (FAST) {
     const bool full = c0 + BC <= a.cout;
     const bool wide = CB >= 2 && xp != nullptr && full && (a.y_pix_stride & 15) == 0 &&
                       ((a.y_c_off + c0) & 15) == 0 && (((uintptr_t)a.y) & 15) == 0;

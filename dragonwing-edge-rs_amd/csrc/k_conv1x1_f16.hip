@@ -29,22 +29,8 @@
 namespace dw {
 namespace {
 
-typedef _Float16 v8h __attribute__((ext_vector_type(8)));
-typedef float v4f __attribute__((ext_vector_type(4)));
-
-// f16((q - zp) * scale) of the 8 bytes of u (byte j -> element j)
-__device__ __forceinline__ v8h dequant8(uint2 u, float zp, float scale) {
-  v8h r;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const uint32_t w = j < 4 ? u.x : u.y;
-    const float q = (float)((w >> (8 * (j & 3))) & 0xffu);
-    float f = (q - zp) * scale;
-    asm("" : "+v"(f));  // round the product to f32 before the f16 conversion
-    r[j] = (_Float16)f;
-  }
-  return r;
-}
+typedef f16x8 v8h;
+typedef f32x4 v4f;
 
 template <int CB, int KS>
 __global__ __launch_bounds__(256) void conv1x1_u8_f16_mfma_kernel(const Conv1x1F16Args a) {
@@ -82,7 +68,7 @@ __global__ __launch_bounds__(256) void conv1x1_u8_f16_mfma_kernel(const Conv1x1F
 #pragma unroll
   for (int pb = 0; pb < 4; ++pb)
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) xf[pb][ks] = dequant8(raw[pb][ks], zp, scale);
+    for (int ks = 0; ks < KS; ++ks) xf[pb][ks] = dequant_u8x8_f16(raw[pb][ks], zp, scale);
   // each weight fragment is read from LDS once and used for the four blocks
 #pragma unroll
   for (int cb = 0; cb < CB; ++cb) {
@@ -90,11 +76,6 @@ __global__ __launch_bounds__(256) void conv1x1_u8_f16_mfma_kernel(const Conv1x1F
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) wf[ks] = __builtin_bit_cast(v8h, s_w[(cb * KS + ks) * 64 + lane]);
     const int ch = cb * 16 + 4 * (lane >> 4);
-    h16x2 blo = {0, 0}, bhi = {0, 0};
-    if (a.bias) {
-      blo = __builtin_bit_cast(h16x2, *reinterpret_cast<const uint32_t*>(s_bias + ch));
-      bhi = __builtin_bit_cast(h16x2, *reinterpret_cast<const uint32_t*>(s_bias + ch + 2));
-    }
 #pragma unroll
     for (int pb = 0; pb < 4; ++pb) {
       v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -102,21 +83,8 @@ __global__ __launch_bounds__(256) void conv1x1_u8_f16_mfma_kernel(const Conv1x1F
       for (int ks = 0; ks < KS; ++ks) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[ks], xf[pb][ks], acc, 0, 0, 0);
       const int p = p0 + pb * 16 + (lane & 15);
       if (p >= a.m || ch >= a.cout) continue;
-      h16x2 lo = pk_f2h(acc[0], acc[1]), hi = pk_f2h(acc[2], acc[3]);
-      if (a.bias) {
-        lo = lo + blo;
-        hi = hi + bhi;
-      }
-      if (a.act == ACT_SILU) {
-        lo = silu_f16_pk_lite(lo);
-        hi = silu_f16_pk_lite(hi);
-      } else if (a.act == ACT_RELU) {
-        lo = pk_make(f16_act_bits(pk_lo(lo), ACT_RELU), f16_act_bits(pk_hi(lo), ACT_RELU));
-        hi = pk_make(f16_act_bits(pk_lo(hi), ACT_RELU), f16_act_bits(pk_hi(hi), ACT_RELU));
-      }
       uint16_t* yrow = a.y + (size_t)p * a.y_pix_stride + a.y_c_off;
-      *reinterpret_cast<uint2*>(yrow + ch) =
-          make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+      *reinterpret_cast<uint2*>(yrow + ch) = conv1x1_f16_finish(acc, a.bias ? s_bias + ch : nullptr, a.act);
     }
   }
 }

@@ -10,6 +10,7 @@
 
 #include <stdio.h>
 #include <stdlib.h>
+#include <string.h>
 
 #include <algorithm>
 
@@ -138,6 +139,15 @@ TileCfg make_wide_tile(const IgemmArgs& a, int bc) {
   return t;
 }
 
+// A detect head's 1x1 fused into the epilogue (a.h_wfrag): one tile holds
+// every channel (64 or 80) on the staged kernel (with room for the regroup
+// rows in its weight chunk) or the row-tile kernel.
+bool head_tile_ok(const IgemmArgs& a, const TileCfg& t) {
+  if (!(t.bc == 64 || t.bc == 80) || a.cout_pad != t.bc) return false;
+  if (t.tpw == -2) return rows_ok(a, t.bc);
+  return t.tpw == 0 && tile_ok(a, t.bc, t.pb) && t.kchunk * t.bc * 64 >= ig::xpose_bytes(t.bc);
+}
+
 // Tile shape for a problem: an override from DW_IGEMM_TILE (tests and
 // tuning runs), an explicit choice (a.tile_bc / a.tile_pb, set by the graph
 // runtime's tuner), else the widest channel tile and the widest pixel tile
@@ -145,6 +155,19 @@ TileCfg make_wide_tile(const IgemmArgs& a, int bc) {
 // The weight slice of the channel tile is staged in chunks of at most
 // kWeightLds bytes.
 TileCfg pick(const IgemmArgs& a) {
+  if (a.h_wfrag) {
+    // the tuner's choice when it is a head tile, else the staged kernel with
+    // the widest pixel tile that fits
+    if (a.tile_bc) {
+      const TileCfg t = a.tile_tpw == -2 ? make_rows_tile(a, a.tile_bc) : make_tile(a, a.tile_bc, a.tile_pb);
+      if (head_tile_ok(a, t)) return t;
+    }
+    for (int pb : {4, 2, 1}) {
+      const TileCfg t = make_tile(a, a.cout_pad, pb);
+      if (head_tile_ok(a, t)) return t;
+    }
+    return make_tile(a, a.cout_pad, 1);  // launch_igemm refuses it
+  }
   if (const char* env = getenv("DW_IGEMM_TILE")) {
     int v0 = 0, v1 = 0, v2 = 0;
     const int nv = sscanf(env, "%d,%d,%d", &v0, &v1, &v2);
@@ -172,6 +195,7 @@ TileCfg pick(const IgemmArgs& a) {
 // Epilogue specialisation for the arguments.
 int epilogue_variant(const IgemmArgs& a, int esize) {
   if (esize != 1 || a.epi != EPI_QU8) return EPV_GENERIC;
+  if (a.h_wfrag) return EPV_QU8_LUT_HEAD;
   if (!a.lut) return a.res ? EPV_GENERIC : EPV_QU8;
   return a.res ? EPV_QU8_LUT_RES : EPV_QU8_LUT;
 }
@@ -182,6 +206,22 @@ int igemm_channel_tile(int cout) { return channel_tile(cout); }
 
 int igemm_candidates(const IgemmArgs& a, int* bc, int* pb, int* tpw, int max) {
   int n = 0;
+  if (a.h_wfrag) {
+    for (int p : {4, 2, 1})
+      if (n < max && head_tile_ok(a, make_tile(a, a.cout_pad, p))) {
+        bc[n] = a.cout_pad;
+        pb[n] = p;
+        tpw[n] = 0;
+        ++n;
+      }
+    if (n < max && head_tile_ok(a, make_rows_tile(a, a.cout_pad))) {
+      bc[n] = a.cout_pad;
+      pb[n] = 4;
+      tpw[n] = -2;
+      ++n;
+    }
+    return n;
+  }
   for (int b : {256, 128, 64})
     if (n < max && wide_ok(a, b)) {
       bc[n] = b;
@@ -235,6 +275,7 @@ const char* igemm_tile_name(const IgemmArgs& a, int esize) {
     snprintf(buf, sizeof buf, "igemm_%s_c%d_wide", esize == 1 ? "i8" : "f16", t.bc);
   else
     snprintf(buf, sizeof buf, "igemm_%s_c%d_p%d", esize == 1 ? "i8" : "f16", t.bc, 64 * t.pb);
+  if (a.h_wfrag) strncat(buf, "_head", sizeof buf - strlen(buf) - 1);
   return buf;
 }
 
@@ -269,7 +310,11 @@ void launch_igemm(hipStream_t st, const IgemmArgs& a_in, int esize) {
   a.r_bytes = (int)rb;
   a.tile_tpw = t.tpw;
   bool ok;
-  if (esize == 1) {
+  if (esize == 1 && a.h_wfrag) {
+    if (a.epi != EPI_QU8 || !a.lut || a.res || !head_tile_ok(a, t))
+      fail(-2, "igemm: the fused head 1x1 needs a table epilogue and a tile of every channel");
+    ok = igemm_launch_head_i8(st, a, t);
+  } else if (esize == 1) {
     const int epv = epilogue_variant(a, esize);
     const bool ab = epv == EPV_GENERIC || epv == EPV_QU8;
     if (t.tpw > 0)

@@ -89,6 +89,9 @@ struct Launch {
   // tuner's time for 4 launches of the chosen tile (ms; 0 when untimed)
   std::string t_in, t_out;
   float tuned_ms = 0;
+  // u8 -> f16 1x1 launches (conv1x1_u8_f16): their arguments, so the pass
+  // that fuses them into the conv before can take them over
+  std::shared_ptr<Conv1x1F16Args> c1a;
   // schedule over several streams: the storage this launch touches, its
   // stream, the launches on other streams it waits for, and whether a
   // later launch on another stream waits for it
@@ -222,6 +225,7 @@ struct Runtime {
   void push_igemm(Launch& L, const IgemmArgs& a, int esize);
   void autotune();
   void fuse_pairs();
+  void fuse_heads();
   void tag_group(const Group& gr, size_t first, int gid);
   void plan_streams(int n);
   void enqueue(hipStream_t st);
@@ -394,6 +398,7 @@ void Runtime::build(Backend* b, const GraphIR& graph, bool stats_mode) {
   if (!stats) {
     autotune();
     fuse_pairs();
+    fuse_heads();
   }
   int ns = 4;
   if (const char* env = getenv("DW_GRAPH_STREAMS")) ns = atoi(env);
@@ -1753,6 +1758,9 @@ void Runtime::emit_conv(const Group& gr) {
     L.kernel = "conv1x1_u8_f16";
     L.bytes += (double)x.bytes() + frag.size() * 2.0 + (double)y.bytes();
     L.fn = [a](hipStream_t st) { launch_conv1x1_u8_f16(st, a); };
+    L.c1a = std::make_shared<Conv1x1F16Args>(a);
+    L.t_in = gr.in;
+    L.t_out = gr.out;
     launches.push_back(L);
     return;
   }
@@ -2026,6 +2034,112 @@ void Runtime::fuse_pairs() {
     P.t_in = L1.t_in;
     P.t_out = L2.t_out;
     launches[i] = P;
+    launches.erase(launches.begin() + (long)i + 1);
+  }
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+}
+
+// A detect head's u8 -> f16 1x1 conv (conv1x1_u8_f16) fused into the
+// epilogue of the QLinearConv before it, when that conv's u8 output (all of
+// its 64 or 80 channels in one tile) feeds only the 1x1: the u8 results are
+// regrouped in LDS and go straight to the fp16 matrix cores
+// (EPV_QU8_LUT_HEAD), so the intermediate is neither stored nor read back
+// and the 1x1's launch goes.  The 1x1's arithmetic is conv1x1_u8_f16's, so
+// its outputs are the same.  Each candidate is timed over the head tiles
+// (the staged and row-tile kernels with one tile of every channel) and kept
+// only if it beats the two launches; DW_HEAD_FUSE=1 keeps every candidate,
+// =0 none; untuned plans keep none unless DW_HEAD_FUSE=1.
+void Runtime::fuse_heads() {
+  const char* env = getenv("DW_HEAD_FUSE");
+  if (env && env[0] == '0') return;
+  const bool force = env && env[0] == '1';
+  const char* tune_env = getenv("DW_AUTOTUNE");
+  const bool tuned = !((tune_env && tune_env[0] == '0') || getenv("DW_IGEMM_TILE"));
+  if (!force && !tuned) return;
+  auto readers = [&](const std::string& t) {
+    int k = 0;
+    for (auto& op : g.ops)
+      for (auto& i : op.in) k += i == t;
+    return k;
+  };
+  hipStream_t st = be->stream;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  DW_HIP(hipEventCreate(&e0));
+  DW_HIP(hipEventCreate(&e1));
+  auto time4 = [&](const std::function<void(hipStream_t)>& fn) {
+    fn(st);
+    float t_min = 1e30f;
+    for (int r = 0; r < 3; ++r) {
+      DW_HIP(hipEventRecord(e0, st));
+      for (int k = 0; k < 4; ++k) fn(st);
+      DW_HIP(hipEventRecord(e1, st));
+      DW_HIP(hipEventSynchronize(e1));
+      float ms = 0;
+      DW_HIP(hipEventElapsedTime(&ms, e0, e1));
+      t_min = std::min(t_min, ms);
+    }
+    return t_min;
+  };
+  for (size_t i = 0; i + 1 < launches.size(); ++i) {
+    Launch& L1 = launches[i];
+    Launch& L2 = launches[i + 1];
+    if (!L1.ig || L1.esize != 1 || !L2.c1a || L1.t_out.empty() || L2.t_in != L1.t_out) continue;
+    const IgemmArgs& a = *L1.ig;
+    const Conv1x1F16Args& c = *L2.c1a;
+    if (a.epi != EPI_QU8 || !a.lut || a.res || a.h_wfrag || !(a.cout == 64 || a.cout == 80) || a.cout_pad != a.cout)
+      continue;
+    if (c.cin != a.cout || c.cout > a.cout || c.x != (const uint8_t*)a.y || c.x_pix_stride != a.y_pix_stride ||
+        c.x_c_off != a.y_c_off || c.m != a.m)
+      continue;
+    if (readers(L1.t_out) != 1 || std::find(g.outputs.begin(), g.outputs.end(), L1.t_out) != g.outputs.end())
+      continue;
+    IgemmArgs h = a;
+    h.h_wfrag = c.wfrag;
+    h.h_bias = c.bias;
+    h.h_y = c.y;
+    h.h_cout = c.cout;
+    h.h_y_pix_stride = c.y_pix_stride;
+    h.h_y_c_off = c.y_c_off;
+    h.h_act = c.act;
+    h.h_scale = c.in_scale;
+    h.h_zp = c.in_zp;
+    int bc[8], pb[8], tpw[8];
+    const int n = igemm_candidates(h, bc, pb, tpw, 8);
+    if (n == 0) continue;
+    h.tile_bc = bc[0];
+    h.tile_pb = pb[0];
+    h.tile_tpw = tpw[0];
+    if (tuned) {
+      float best = 1e30f;
+      int bi = 0;
+      for (int k = 0; k < n; ++k) {
+        IgemmArgs hk = h;
+        hk.tile_bc = bc[k];
+        hk.tile_pb = pb[k];
+        hk.tile_tpw = tpw[k];
+        const float t = time4([&hk](hipStream_t s) { launch_igemm(s, hk, 1); });
+        if (t < best) {
+          best = t;
+          bi = k;
+        }
+      }
+      h.tile_bc = bc[bi];
+      h.tile_pb = pb[bi];
+      h.tile_tpw = tpw[bi];
+      if (!force && (L1.tuned_ms <= 0 || best >= L1.tuned_ms + time4(L2.fn))) continue;
+    }
+    auto hp = std::make_shared<IgemmArgs>(h);
+    L1.ig = hp;
+    L1.kernel = igemm_tile_name(h, 1);
+    L1.fn = [hp](hipStream_t s) { launch_igemm(s, *hp, 1); };
+    L1.op += "+" + L2.op;
+    L1.work += L2.work;
+    L1.bytes = L1.bytes + L2.bytes - 2.0 * (double)T(L1.t_out).pixels() * T(L1.t_out).c;
+    L1.reads.insert(L1.reads.end(), L2.reads.begin(), L2.reads.end());
+    L1.writes.insert(L1.writes.end(), L2.writes.begin(), L2.writes.end());
+    L1.t_out = L2.t_out;
+    L1.tuned_ms = 0;
     launches.erase(launches.begin() + (long)i + 1);
   }
   (void)hipEventDestroy(e0);

@@ -384,14 +384,15 @@ def test_int8_graph_launch_plan(backend, int8_small):
     kinds = {}
     for L in ls:
         kinds[L["kernel"].split("_")[0]] = kinds.get(L["kernel"].split("_")[0], 0) + 1
-    # 56 int8 MFMA convs (each with its table / residual fused; at 96x96 no
-    # map has whole rows dividing 320 pixels, so no bottleneck pair is
-    # chained), the fp16 stem as a direct conv, the six fp16 head 1x1 convs
-    # on the fp16 matrix cores, one SPPF cascade, two resizes, no copies or
-    # elementwise.
+    # 56 int8 MFMA convs (each with its table / residual fused; two chained
+    # 3x3 convs in one launch where the tuner finds that faster), the fp16
+    # stem as a direct conv, the six fp16 head 1x1 convs on the fp16 matrix
+    # cores (each in its own launch or inside its 3x3's, "_head"), one SPPF
+    # cascade, two resizes, no copies or elementwise.
     pairs = sum(L["kernel"].startswith("igemm_i8_pair") for L in ls)
-    assert pairs == 0 and kinds.get("igemm") == 56, (pairs, kinds)
-    assert kinds.get("direct") == 1 and kinds.get("conv1x1") == 6, kinds
+    heads = sum(L["kernel"].endswith("_head") for L in ls)
+    assert kinds.get("igemm") + pairs == 56, (pairs, kinds)
+    assert kinds.get("direct") == 1 and kinds.get("conv1x1", 0) + heads == 6, kinds
     assert kinds.get("maxpool") == 1 and kinds.get("resize") == 2, kinds
     assert "copy" not in kinds and "elementwise" not in kinds, kinds
     ms = rt.run_profiled()
@@ -434,6 +435,34 @@ def test_int8_graph_pairs_bit_exact(backend, monkeypatch):
     rt0.run()
     for o, gv, g0 in zip(info["outputs"], got, gpu_outputs(rt0, info)):
         np.testing.assert_array_equal(gv, g0, err_msg=o)
+
+
+@pytest.mark.parametrize("size,batch", [(320, 2), (640, 32)])
+def test_int8_graph_head_fusion_same_bytes(backend, monkeypatch, size, batch):
+    # The detect heads' u8 -> f16 1x1 convs fused into the epilogue of the
+    # 3x3 QLinearConv before them (the u8 results regrouped in LDS and fed to
+    # the fp16 matrix cores): the same bytes as the separate 1x1 launches
+    # (whose outputs test_int8_benchmark_graph checks against the oracle),
+    # at 320x320 and on the benchmark's batch-32 640x640 graph.
+    if size == 640:
+        from dragonwing_edge_rs_amd import workloads
+        g, _, _, _, info = workloads.yolov8n_int8(backend)
+    else:
+        g, info = yolo.int8_graph(backend, batch=batch, size=size, calib=yolo.calibration_images(4, size))
+    x = yolo.input_images(batch, size)
+    monkeypatch.setenv("DW_PAIR", "0")
+    outs = {}
+    for mode in ("0", "1"):
+        monkeypatch.setenv("DW_HEAD_FUSE", mode)
+        rt = HipGraphRuntime(g, backend)
+        fused = [L["kernel"] for L in rt.launches() if L["kernel"].endswith("_head")]
+        assert len(fused) == (6 if mode == "1" else 0), fused
+        assert sum(L["kernel"] == "conv1x1_u8_f16" for L in rt.launches()) == (0 if mode == "1" else 6)
+        rt.set_input_f32(info["input"], x)
+        rt.run()
+        outs[mode] = gpu_outputs(rt, info)
+    for o, a, b in zip(info["outputs"], outs["0"], outs["1"]):
+        np.testing.assert_array_equal(a, b, err_msg=o)
 
 
 def gpu_ranges(backend, batch, size, images):
