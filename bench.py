@@ -307,12 +307,21 @@ def read_counter_csv(d: Path):
     return [rows[k] for k in sorted(rows)]
 
 
+def plan_env(launches):
+    """The timed plan choices of a runtime (which chained pairs and fused
+    head 1x1s it kept), as the environment that makes another process build
+    the same launch list."""
+    first = lambda L: L["ops"].split("+")[0]
+    return {"DW_PAIR_KEEP": ",".join(first(L) for L in launches if L["kernel"].startswith("igemm_i8_pair")),
+            "DW_HEAD_KEEP": ",".join(first(L) for L in launches if L["kernel"].endswith("_head"))}
+
+
 def measure_traffic(workload: str, launches, timeout: float = 240.0):
     """Per-launch HBM bytes: two rocprofv3 counter passes (FETCH_SIZE, then
     WRITE_SIZE) over a child run of this workload that brackets one graph
     run between two copy probes; each counter is scaled by what it reads for
-    the second probe.  Returns (fetch_bytes[], write_bytes[], scales) in
-    launch order, or raises."""
+    the second probe.  The child builds this run's plan (plan_env).  Returns
+    (fetch_bytes[], write_bytes[], scales) in launch order, or raises."""
     import shutil
     import signal
     import subprocess
@@ -327,7 +336,8 @@ def measure_traffic(workload: str, launches, timeout: float = 240.0):
         d = base / counter
         cmd = [exe, "--pmc", counter, "--output-format", "csv", "-d", str(d), "-o", "run", "--",
                sys.executable, str(ROOT / "bench.py"), "--workload", workload, "--traffic-child"]
-        p = subprocess.Popen(cmd, cwd="/tmp", env=dict(os.environ, TMPDIR="/tmp"), stdout=subprocess.DEVNULL,
+        p = subprocess.Popen(cmd, cwd="/tmp", env=dict(os.environ, TMPDIR="/tmp", **plan_env(launches)),
+                             stdout=subprocess.DEVNULL,
                              stderr=subprocess.DEVNULL, start_new_session=True)
         try:
             p.wait(timeout=timeout)

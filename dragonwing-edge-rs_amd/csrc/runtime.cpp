@@ -1943,6 +1943,16 @@ void Runtime::emit_qconv(const Group& gr) {
   push_igemm(L, a, 1);
 }
 
+namespace {
+// Whether the first op name of a launch (its op string up to the first '+')
+// is in a comma-separated list.
+bool listed(const char* csv, const std::string& ops) {
+  const std::string first = ops.substr(0, ops.find('+'));
+  std::string list = std::string(",") + csv + ",";
+  return list.find("," + first + ",") != std::string::npos;
+}
+}  // namespace
+
 // Chained QLinearConv pairs in one launch (igemm_pair.h): a 3x3 conv whose
 // output only the next launch's 3x3 conv reads (the bottleneck of a C2f
 // block, c = 16, 32 or 64 channels) may run with it, the intermediate kept
@@ -1953,11 +1963,13 @@ void Runtime::emit_qconv(const Group& gr) {
 // none; untuned plans (DW_AUTOTUNE=0, DW_IGEMM_TILE) keep none unless
 // DW_PAIR=1, which then takes the tallest band that leaves two workgroups
 // a CU their LDS (or the tallest).  DW_PAIR_ROWS=<r> forces band height r
-// wherever it is valid (tests).
+// wherever it is valid (tests); DW_PAIR_KEEP=<op,op,..> keeps exactly the
+// pairs whose first conv is listed (another process reproducing a plan).
 void Runtime::fuse_pairs() {
   const char* env = getenv("DW_PAIR");
   if (env && env[0] == '0') return;
-  const bool force = env && env[0] == '1';
+  const char* keep = getenv("DW_PAIR_KEEP");
+  const bool force = (env && env[0] == '1') || keep;
   const char* tune_env = getenv("DW_AUTOTUNE");
   const bool tuned = !((tune_env && tune_env[0] == '0') || getenv("DW_IGEMM_TILE"));
   if (!force && !tuned) return;
@@ -1991,6 +2003,7 @@ void Runtime::fuse_pairs() {
     if (!L1.ig || !L2.ig || L1.esize != 1 || L2.esize != 1 || L1.t_out.empty() || L2.t_in != L1.t_out) continue;
     if (readers(L1.t_out) != 1 || std::find(g.outputs.begin(), g.outputs.end(), L1.t_out) != g.outputs.end())
       continue;
+    if (keep && !listed(keep, L1.op)) continue;
     int cand[16];
     const int nc = igemm_pair_rows(*L1.ig, *L2.ig, cand, 16);
     if (nc == 0) continue;
@@ -2049,11 +2062,13 @@ void Runtime::fuse_pairs() {
 // its outputs are the same.  Each candidate is timed over the head tiles
 // (the staged and row-tile kernels with one tile of every channel) and kept
 // only if it beats the two launches; DW_HEAD_FUSE=1 keeps every candidate,
-// =0 none; untuned plans keep none unless DW_HEAD_FUSE=1.
+// =0 none; untuned plans keep none unless DW_HEAD_FUSE=1.  DW_HEAD_KEEP=
+// <op,op,..> keeps exactly the fusions whose 3x3 conv is listed.
 void Runtime::fuse_heads() {
   const char* env = getenv("DW_HEAD_FUSE");
   if (env && env[0] == '0') return;
-  const bool force = env && env[0] == '1';
+  const char* keep = getenv("DW_HEAD_KEEP");
+  const bool force = (env && env[0] == '1') || keep;
   const char* tune_env = getenv("DW_AUTOTUNE");
   const bool tuned = !((tune_env && tune_env[0] == '0') || getenv("DW_IGEMM_TILE"));
   if (!force && !tuned) return;
@@ -2094,6 +2109,7 @@ void Runtime::fuse_heads() {
       continue;
     if (readers(L1.t_out) != 1 || std::find(g.outputs.begin(), g.outputs.end(), L1.t_out) != g.outputs.end())
       continue;
+    if (keep && !listed(keep, L1.op)) continue;
     IgemmArgs h = a;
     h.h_wfrag = c.wfrag;
     h.h_bias = c.bias;
