@@ -350,7 +350,11 @@ __device__ __forceinline__ uint4 vmax16(uint4 a, uint4 b) {
 
 // plane: hw pixels of the input, then three planes of row maxima (radius
 // r, 2r, 3r); 4 * hw * 16 bytes of LDS
-template <int ES>
+// RAD > 0: the radius fixed at compile time (the SPPF's 5x5 pools: 2), the
+// loops unrolled, and neighbours outside the image clamped to the edge
+// pixel instead of skipped (that pixel is in the window already, and max
+// is idempotent, so the results are the same); RAD = 0: any radius.
+template <int ES, int RAD>
 __global__ __launch_bounds__(512) void sppf_lds_kernel(const PoolArgs a, View y2, View y3) {
   extern __shared__ uint4 plane[];
   const int hw = a.h * a.w;
@@ -371,33 +375,53 @@ __global__ __launch_bounds__(512) void sppf_lds_kernel(const PoolArgs a, View y2
     const int y = i / a.w, x = i - (i / a.w) * a.w;
     const uint4* row = X + y * a.w;
     uint4 m = row[x];
-    R1[i] = m;  // r = 0 (a 1x1 pool): the loops below add nothing
-    R2[i] = m;
-    for (int d = 1; d <= 3 * r; ++d) {
-      if (x - d >= 0) m = vmax16<ES>(m, row[x - d]);
-      if (x + d < a.w) m = vmax16<ES>(m, row[x + d]);
-      if (d == r) R1[i] = m;
-      if (d == 2 * r) R2[i] = m;
+    if constexpr (RAD > 0) {
+#pragma unroll
+      for (int d = 1; d <= 3 * RAD; ++d) {
+        m = vmax16<ES>(m, row[max(x - d, 0)]);
+        m = vmax16<ES>(m, row[min(x + d, a.w - 1)]);
+        if (d == RAD) R1[i] = m;
+        if (d == 2 * RAD) R2[i] = m;
+      }
+    } else {
+      R1[i] = m;  // r = 0 (a 1x1 pool): the loops below add nothing
+      R2[i] = m;
+      for (int d = 1; d <= 3 * r; ++d) {
+        if (x - d >= 0) m = vmax16<ES>(m, row[x - d]);
+        if (x + d < a.w) m = vmax16<ES>(m, row[x + d]);
+        if (d == r) R1[i] = m;
+        if (d == 2 * r) R2[i] = m;
+      }
     }
     R3[i] = m;
   }
   __syncthreads();
   // column maxima of the three row-maximum planes: the three outputs
   for (int i = threadIdx.x; i < hw; i += blockDim.x) {
-    const int y = i / a.w, x = i - (i / a.w) * a.w;
+    const int y = i / a.w;
     uint4 m1 = R1[i], m2 = R2[i], m3 = R3[i];
-    for (int d = 1; d <= 3 * r; ++d) {
-      const bool up = y - d >= 0, dn = y + d < a.h;
-      if (d <= r) {
-        if (up) m1 = vmax16<ES>(m1, R1[i - d * a.w]);
-        if (dn) m1 = vmax16<ES>(m1, R1[i + d * a.w]);
+    if constexpr (RAD > 0) {
+#pragma unroll
+      for (int d = 1; d <= 3 * RAD; ++d) {
+        const int up = i - min(d, y) * a.w, dn = i + min(d, a.h - 1 - y) * a.w;
+        if (d <= RAD) m1 = vmax16<ES>(vmax16<ES>(m1, R1[up]), R1[dn]);
+        if (d <= 2 * RAD) m2 = vmax16<ES>(vmax16<ES>(m2, R2[up]), R2[dn]);
+        m3 = vmax16<ES>(vmax16<ES>(m3, R3[up]), R3[dn]);
       }
-      if (d <= 2 * r) {
-        if (up) m2 = vmax16<ES>(m2, R2[i - d * a.w]);
-        if (dn) m2 = vmax16<ES>(m2, R2[i + d * a.w]);
+    } else {
+      for (int d = 1; d <= 3 * r; ++d) {
+        const bool up = y - d >= 0, dn = y + d < a.h;
+        if (d <= r) {
+          if (up) m1 = vmax16<ES>(m1, R1[i - d * a.w]);
+          if (dn) m1 = vmax16<ES>(m1, R1[i + d * a.w]);
+        }
+        if (d <= 2 * r) {
+          if (up) m2 = vmax16<ES>(m2, R2[i - d * a.w]);
+          if (dn) m2 = vmax16<ES>(m2, R2[i + d * a.w]);
+        }
+        if (up) m3 = vmax16<ES>(m3, R3[i - d * a.w]);
+        if (dn) m3 = vmax16<ES>(m3, R3[i + d * a.w]);
       }
-      if (up) m3 = vmax16<ES>(m3, R3[i - d * a.w]);
-      if (dn) m3 = vmax16<ES>(m3, R3[i + d * a.w]);
     }
     *reinterpret_cast<uint4*>(gaddr(a.y, i)) = m1;
     *reinterpret_cast<uint4*>(gaddr(y2, i)) = m2;
@@ -551,12 +575,20 @@ void launch_maxpool_cascade3(hipStream_t st, const PoolArgs& a, View y2, View y3
     // one thread per pixel up to 512 pixels
     const int threads = std::min(512, ((a.h * a.w + 63) / 64) * 64);
     const dim3 g(a.n, a.c * es / 16), b(threads);
-    if (es == 1)
-      hipLaunchKernelGGL(sppf_lds_kernel<1>, g, b, lds, st, a, y2, y3);
-    else if (es == 2)
-      hipLaunchKernelGGL(sppf_lds_kernel<2>, g, b, lds, st, a, y2, y3);
-    else
-      hipLaunchKernelGGL(sppf_lds_kernel<4>, g, b, lds, st, a, y2, y3);
+    const bool k5 = a.kh == 5;  // the SPPF's pools: the unrolled form
+#define DW_SPPF(ES_)                                                                   \
+  if (k5)                                                                              \
+    hipLaunchKernelGGL((sppf_lds_kernel<ES_, 2>), g, b, lds, st, a, y2, y3);          \
+  else                                                                                 \
+    hipLaunchKernelGGL((sppf_lds_kernel<ES_, 0>), g, b, lds, st, a, y2, y3);
+    if (es == 1) {
+      DW_SPPF(1)
+    } else if (es == 2) {
+      DW_SPPF(2)
+    } else {
+      DW_SPPF(4)
+    }
+#undef DW_SPPF
     DW_HIP(hipGetLastError());
     return;
   }
