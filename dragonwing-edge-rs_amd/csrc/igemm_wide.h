@@ -1,6 +1,10 @@
-// Wide-tile int8 implicit GEMM for convolutions whose input rows are
-// multiples of 128 bytes (c_in % 128 == 0): the variant for layers where
-// igemm_kernel is bound by its im2col loads.
+// Wide-tile implicit GEMM (int8, or fp16 with ESZ = 2) for convolutions
+// whose input rows are multiples of 128 bytes (c_in % 128 == 0 int8, c_in %
+// 64 == 0 fp16): the variant for layers where igemm_kernel is bound by its
+// im2col loads.  A k-step is 64 bytes of K either way (v_mfma_i32_16x16x64_i8
+// or v_mfma_f32_16x16x32_f16, the same fragment bytes), so the staging and
+// the fragment reads below are the element size's only in the MFMA, the
+// operand conversion (none for fp16: padding reads as +0) and the epilogue.
 //
 // igemm_kernel loads each im2col k-step straight into the MFMA registers:
 // one wave instruction fetches 64 bytes of 16 pixels, which for c_in >= 128
@@ -41,6 +45,7 @@ namespace dw {
 
 bool igemm_launch_wide_i8_a(hipStream_t st, const IgemmArgs& a, const TileCfg& t, int epv);  // generic, QU8
 bool igemm_launch_wide_i8_b(hipStream_t st, const IgemmArgs& a, const TileCfg& t, int epv);  // LUT variants
+bool igemm_launch_wide_f16(hipStream_t st, const IgemmArgs& a, const TileCfg& t);
 
 namespace ig {
 
@@ -52,8 +57,9 @@ constexpr int kWideThreads = 512;  // 8 waves
 __host__ __device__ constexpr int wide_static_lds(int bc) { return 2 * kWidePix * 128 + 2 * (2 * bc * 64) + 256 + 8 * bc; }
 inline size_t wide_lds_bytes(int bc, int ksteps) { return (size_t)wide_static_lds(bc) + (size_t)(ksteps / 2 + 1) * 8; }
 
-// Element offset of pixel p's top-left tap and the in-image bit of every
-// tap (no bits for pixels past the end).
+// Element offset of pixel p's top-left tap (times ESZ: bytes) and the
+// in-image bit of every tap (no bits for pixels past the end).
+template <int ESZ>
 __device__ __forceinline__ void wide_pixel(const IgemmArgs& a, int p, int& base, uint32_t& mask) {
   const bool pv = p < a.m;
   const int pp = pv ? p : 0;
@@ -63,7 +69,7 @@ __device__ __forceinline__ void wide_pixel(const IgemmArgs& a, int p, int& base,
   const int oh = div_small(r, a.wo, a.r_wo);
   const int ow = r - oh * a.wo;
   const int ih0 = oh * a.sh - a.pt, iw0 = ow * a.sw - a.pl;
-  base = ((nn * a.h + ih0) * a.w + iw0) * a.x_pix_stride + a.x_c_off;
+  base = (((nn * a.h + ih0) * a.w + iw0) * a.x_pix_stride + a.x_c_off) * ESZ;
   const int rlo = max(0, -ih0), rhi = min(a.kh, a.h - ih0);
   const int clo = max(0, -iw0), chi = min(a.kw, a.w - iw0);
   const uint32_t cols = chi > clo ? (1u << chi) - (1u << clo) : 0u;
@@ -72,8 +78,10 @@ __device__ __forceinline__ void wide_pixel(const IgemmArgs& a, int p, int& base,
   mask = pv ? m : 0u;
 }
 
-template <int BC, int EPV>
+template <int ESZ, int BC, int EPV>
 __global__ __launch_bounds__(kWideThreads) void igemm_wide_kernel(const IgemmArgs a) {
+  using acc_t = typename std::conditional<ESZ == 1, v4i, v4f>::type;
+  static_assert(ESZ == 1 || EPV == EPV_GENERIC, "specialised epilogues are int8");
   constexpr int CBT = BC / 16;  // 16-channel blocks of the tile
   constexpr int CB = CBT / 2;   // per wave
   constexpr int PB = 4;         // 16-pixel blocks per wave
@@ -113,7 +121,7 @@ __global__ __launch_bounds__(kWideThreads) void igemm_wide_kernel(const IgemmArg
   int lbase[4];
   uint32_t lmask[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) wide_pixel(a, tp0 + i * 64 + (tid >> 3), lbase[i], lmask[i]);
+  for (int i = 0; i < 4; ++i) wide_pixel<ESZ>(a, tp0 + i * 64 + (tid >> 3), lbase[i], lmask[i]);
   const int lchunk = (tid & 7) ^ ((tid >> 3) & 7);  // chunk this lane loads into slot tid % 8
   // ---- this lane's MFMA pixels: in-image bits (tp0 + pq * 64 + pb * 16 + lane % 16)
   int mbase[PB];
@@ -148,14 +156,15 @@ __global__ __launch_bounds__(kWideThreads) void igemm_wide_kernel(const IgemmArg
 
   // pair 0 (tap 0, channels 0..127) is in flight while the tables are built
   issue_t(0, make_int2(0, 0), s_x0, s_w0);
-  // ---- k-pair table: pair q is 128 input channels of one tap
+  // ---- k-pair table: pair q is 128 bytes (128 / ESZ input channels) of
+  // one tap: its byte offset from the pixel's top-left tap, and the tap
   for (int q = tid; q < NP; q += kWideThreads) {
-    const int e = q * 128;
+    const int e = q * (128 / ESZ);
     const int tap = div_small(e, a.cin, a.r_cin);
     const int ci = e - tap * a.cin;
     const int kh = div_small(tap, a.kw, a.r_kw);
     const int kw = tap - kh * a.kw;
-    ktab[q] = make_int2((kh * a.w + kw) * a.x_pix_stride + ci, tap);
+    ktab[q] = make_int2(((kh * a.w + kw) * a.x_pix_stride + ci) * ESZ, tap);
   }
   // ---- epilogue data of the channel tile
   const int nvalid = min(BC, a.cout - c0);
@@ -165,15 +174,17 @@ __global__ __launch_bounds__(kWideThreads) void igemm_wide_kernel(const IgemmArg
       reinterpret_cast<float*>(s_ms)[tid] = a.mscale[c0 + tid];
     }
     if (a.lut && tid < 256) s_lut[tid] = a.lut[tid];
+  } else if (a.epi == EPI_F16 && a.bias_h && tid < nvalid) {
+    reinterpret_cast<uint16_t*>(s_bias)[tid] = a.bias_h[c0 + tid];
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();  // pair 0, the k-pair table and the epilogue data
 
   const int cq = 4 * (lane >> 4);
-  v4i acc[CB][PB];
+  acc_t acc[CB][PB];
 #pragma unroll
   for (int cb = 0; cb < CB; ++cb) {
-    v4i init = v4i{0, 0, 0, 0};
+    acc_t init = acc_t{0, 0, 0, 0};
     if constexpr (FAST) {
       if (a.bias_i) init = *reinterpret_cast<const v4i*>(s_bias + 4 * (chh * HC + cb * 16 + cq));
     }
@@ -194,13 +205,20 @@ __global__ __launch_bounds__(kWideThreads) void igemm_wide_kernel(const IgemmArg
   static_assert(kDefer <= CB, "the held-back groups are second k-step groups");
   v4i pa[kDefer];
   u32x4 pbf[PB];
+  // one MFMA: weight fragment x pixel fragment (int8 or fp16 operand bytes)
+  auto mma = [](const v4i& w, const u32x4& x, const acc_t& c) -> acc_t {
+    if constexpr (ESZ == 1)
+      return __builtin_amdgcn_mfma_i32_16x16x64_i8(w, __builtin_bit_cast(v4i, x), c, 0, 0, 0);
+    else
+      return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, w), __builtin_bit_cast(v8h, x), c, 0, 0,
+                                                    0);
+  };
   auto held_back = [&]() {
 #pragma unroll
     for (int d = 0; d < kDefer; ++d)
 #pragma unroll
       for (int pb = 0; pb < PB; ++pb)
-        acc[CB - kDefer + d][pb] =
-            __builtin_amdgcn_mfma_i32_16x16x64_i8(pa[d], __builtin_bit_cast(v4i, pbf[pb]), acc[CB - kDefer + d][pb], 0, 0, 0);
+        acc[CB - kDefer + d][pb] = mma(pa[d], pbf[pb], acc[CB - kDefer + d][pb]);
   };
   auto compute = [&](int q, const uint8_t* sx, const uint8_t* sw, bool pend) {
     const int tap = ktab[q].y;
@@ -230,27 +248,31 @@ __global__ __launch_bounds__(kWideThreads) void igemm_wide_kernel(const IgemmArg
     __builtin_amdgcn_sched_barrier(0);
     if (pend) held_back();
     __builtin_amdgcn_sched_barrier(0);
+    // int8: u8 -> s8 for in-image taps, the padding pattern for the others
+    // (fp16 operands are used as they are: padding reads as +0)
     uint32_t key[PB];
 #pragma unroll
     for (int pb = 0; pb < PB; ++pb) key[pb] = ((mmask[pb] >> tap) & 1u) ? a.xxor : a.xpad;
+    if constexpr (ESZ == 1) {
 #pragma unroll
-    for (int pb = 0; pb < PB; ++pb) bf[0][pb] ^= key[pb];
+      for (int pb = 0; pb < PB; ++pb) bf[0][pb] ^= key[pb];
+    }
 #pragma unroll
     for (int i = 0; i < NG; ++i) {
       const int h = i / CB, cb = i - (i / CB) * CB;
       if (i + 2 < 2 * CB) read_w(i + 2);
       __builtin_amdgcn_sched_barrier(0);
-      if (i == CB) {
+      if (ESZ == 1 && i == CB) {
 #pragma unroll
         for (int pb = 0; pb < PB; ++pb) bf[1][pb] ^= key[pb];
       }
       const v4i af = ar[i % 3];
 #pragma unroll
       for (int pb = 0; pb < PB; ++pb)
-        acc[cb][pb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, __builtin_bit_cast(v4i, bf[h][pb]), acc[cb][pb], 0, 0, 0);
+        acc[cb][pb] = mma(af, bf[h][pb], acc[cb][pb]);
       __builtin_amdgcn_sched_barrier(0);
     }
-    if constexpr (NG <= CB) {
+    if constexpr (ESZ == 1 && NG <= CB) {
 #pragma unroll
       for (int pb = 0; pb < PB; ++pb) bf[1][pb] ^= key[pb];
     }
@@ -281,19 +303,21 @@ __global__ __launch_bounds__(kWideThreads) void igemm_wide_kernel(const IgemmArg
     ep.bias = a.bias_i ? reinterpret_cast<const int*>(s_bias) + chh * HC : nullptr;
     ep.ms = reinterpret_cast<const float*>(s_ms) + chh * HC;
     ep.lut = a.lut ? s_lut : nullptr;
+  } else if (a.epi == EPI_F16 && a.bias_h) {
+    ep.bias_h = reinterpret_cast<const uint16_t*>(s_bias) + chh * HC;
   }
   uint8_t* xp = nullptr;
   if constexpr (FAST && HC >= 32) xp = s_x0 + wave * 16 * xpose_row(HC);
-  igemm_store<1, HC, PB, EPV>(a, ep, acc, c0 + chh * HC, tp0 + pq * 64, lane, s_ms + 4 * chh * HC, s_lut, xp);
+  igemm_store<ESZ, HC, PB, EPV>(a, ep, acc, c0 + chh * HC, tp0 + pq * 64, lane, s_ms + 4 * chh * HC, s_lut, xp);
 }
 
-template <int EPV>
+template <int ESZ, int EPV>
 bool launch_wide_tiles(hipStream_t st, const IgemmArgs& a, const TileCfg& t) {
   const dim3 grid((unsigned)(((a.m + kWidePix - 1) / kWidePix) * (a.cout_pad / t.bc)));
   const size_t dyn = (size_t)(a.ksteps / 2 + 1) * 8;
 #define DW_B(BC_)                                                                                   \
   case BC_:                                                                                         \
-    hipLaunchKernelGGL((igemm_wide_kernel<BC_, EPV>), grid, dim3(kWideThreads), dyn, st, a);      \
+    hipLaunchKernelGGL((igemm_wide_kernel<ESZ, BC_, EPV>), grid, dim3(kWideThreads), dyn, st, a); \
     return true;
   switch (t.bc) {
     DW_B(256)

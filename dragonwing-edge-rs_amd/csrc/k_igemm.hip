@@ -121,11 +121,12 @@ TileCfg make_rows_tile(const IgemmArgs& a, int bc) {
   return t;
 }
 
-// The wide-tile kernel (tpw = -3): int8, input rows of whole 128-byte
-// units (c_in % 128 == 0, 16-byte aligned views), 256-pixel workgroups of
-// 64, 128 or 256 channels.
+// The wide-tile kernel (tpw = -3): input rows of whole 128-byte units
+// (c_in % 128 == 0 int8, % 64 == 0 fp16; 16-byte aligned views), 256-pixel
+// workgroups of 64, 128 or 256 channels.
 bool wide_ok(const IgemmArgs& a, int bc) {
-  if (a.epi == EPI_F16 || a.cin % 128 != 0 || a.x_pix_stride % 16 != 0 || a.x_c_off % 16 != 0) return false;
+  const int es = a.epi == EPI_F16 ? 2 : 1;
+  if ((a.cin * es) % 128 != 0 || (a.x_pix_stride * es) % 16 != 0 || (a.x_c_off * es) % 16 != 0) return false;
   if (!(bc == 256 || bc == 128 || bc == 64) || a.cout_pad % bc != 0 || a.ksteps % 2 != 0) return false;
   if (bc > 64 && a.cout <= bc / 2) return false;  // half the tile would be padding
   return ig::wide_lds_bytes(bc, a.ksteps) <= 160 * 1024;
@@ -331,6 +332,7 @@ void launch_igemm(hipStream_t st, const IgemmArgs& a_in, int esize) {
     ok = t.tpw > 0     ? igemm_launch_sk_f16(st, a, t)
          : t.tpw == -1 ? igemm_launch_st_f16(st, a, t)
          : t.tpw == -2 ? igemm_launch_rows_f16(st, a, t)
+         : t.tpw == -3 ? igemm_launch_wide_f16(st, a, t)
                        : igemm_launch_f16(st, a, t);
   }
   if (!ok) fail(-2, "igemm: no kernel for tile");

@@ -5,8 +5,8 @@
 namespace dw {
 
 bool igemm_launch_wide_i8_a(hipStream_t st, const IgemmArgs& a, const TileCfg& t, int epv) {
-  if (epv == EPV_GENERIC) return ig::launch_wide_tiles<EPV_GENERIC>(st, a, t);
-  if (epv == EPV_QU8) return ig::launch_wide_tiles<EPV_QU8>(st, a, t);
+  if (epv == EPV_GENERIC) return ig::launch_wide_tiles<1, EPV_GENERIC>(st, a, t);
+  if (epv == EPV_QU8) return ig::launch_wide_tiles<1, EPV_QU8>(st, a, t);
   return false;
 }
 

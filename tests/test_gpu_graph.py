@@ -209,6 +209,27 @@ def test_int8_graph_wide_tiles_bit_exact(backend, monkeypatch, tile):
         np.testing.assert_array_equal(gv, ref[o], err_msg=f"{o} tile {tile}")
 
 
+@pytest.mark.parametrize("tile", ["256,4,-3", "128,4,-3", "64,4,-3"])
+def test_f16_graph_wide_tiles_identical(backend, monkeypatch, tile):
+    # Every fp16 layer with c_in a multiple of 64 on the wide-tile kernel
+    # (with and without the residual add): the same bytes as the staged
+    # kernel's, which the other graph tests hold to the oracle.
+    g, info = yolo.f16_graph(batch=2, size=160)
+    x = yolo.input_images(2, 160)
+    monkeypatch.setenv("DW_IGEMM_TILE", "16,4")
+    rt0 = HipGraphRuntime(g, backend)
+    rt0.set_input_f32(info["input"], x)
+    rt0.run()
+    ref = gpu_outputs(rt0, info)
+    monkeypatch.setenv("DW_IGEMM_TILE", tile)
+    rt = HipGraphRuntime(g, backend)
+    assert sum(L["kernel"].endswith("_wide") for L in rt.launches()) >= 4
+    rt.set_input_f32(info["input"], x)
+    rt.run()
+    for o, a, b in zip(info["outputs"], ref, gpu_outputs(rt, info)):
+        np.testing.assert_array_equal(b, a, err_msg=f"{o} tile {tile}")
+
+
 @pytest.mark.parametrize("tile", ["128,1,-1", "64,2,-1", "32,4,-1"])
 def test_int8_graph_streamed_tiles_bit_exact(backend, int8_small, monkeypatch, tile):
     # Every layer with two or more k-steps on the streamed-weight kernel

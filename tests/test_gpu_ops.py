@@ -553,6 +553,29 @@ def test_conv_f16_row_tiles_identical(backend, monkeypatch, geom):
         np.testing.assert_array_equal(got, first, err_msg=f"tile {bc},4,-2")
 
 
+@pytest.mark.parametrize("geom", [(2, 11, 9, 64, 128, 3, 1, 1), (2, 20, 18, 128, 64, 3, 2, 1),
+                                  (1, 12, 10, 64, 256, 1, 1, 0), (3, 7, 5, 192, 192, 3, 1, 1)])
+def test_conv_f16_wide_tiles_identical(backend, monkeypatch, geom):
+    # Input rows of whole 128-byte units (c_in % 64 == 0): the wide-tile
+    # kernel stages k-step pairs through LDS and sums the same k-steps in the
+    # same order as the staged kernel, so the results are identical.
+    n, h, w, ci, co, k, s, p = geom
+    r = synth.Rng(synth.seed_for(640 + sum(geom)))
+    xh = synth.f16_bits(r.normal((n, h, w, ci), 0.0, 1.0))
+    kh_ = synth.f16_bits(r.normal((k, k, ci, co), 0.0, (1.0 / (k * k * ci)) ** 0.5))
+    bh = synth.f16_bits(r.normal((co,), 0.0, 0.1))
+    ref = oracle_conv_f16(xh, kh_, bh, s, p, ops.ACT_SILU)
+    monkeypatch.setenv("DW_IGEMM_TILE", "16,4")
+    first = run_conv_f16(backend, xh, kh_, bh, s, p, ops.ACT_SILU, exact=False)
+    assert rel_err(f16v(first), f16v(ref)) <= 1e-2
+    tiles = wide_tiles(co)
+    assert tiles
+    for bc in tiles:
+        monkeypatch.setenv("DW_IGEMM_TILE", f"{bc},4,-3")
+        got = run_conv_f16(backend, xh, kh_, bh, s, p, ops.ACT_SILU, exact=False)
+        np.testing.assert_array_equal(got, first, err_msg=f"tile {bc},4,-3")
+
+
 @pytest.mark.parametrize("geom", [(2, 32, 32, 3, 16, 3, 2, 1), (1, 12, 12, 64, 64, 1, 1, 0),
                                   (1, 10, 10, 80, 80, 1, 1, 0), (1, 17, 15, 3, 16, 3, 2, 1),
                                   (2, 20, 22, 3, 16, 3, 2, 0), (1, 9, 12, 3, 32, 3, 2, 1),
