@@ -150,6 +150,25 @@ struct Conv1x1F16Args {
   int act;
 };
 
+// A conv whose K (kh * kw * c_in) fits one fp16 MFMA k-step (the fp16
+// graphs' three-channel stem; k_stem_f16.hip): f16 NHWC in (or the graph
+// input's NCHW f32 planes, each value rounded to f16 as F16::from_f32 does)
+// and f16 NHWC out, f16 weights in fragment order [cout / 16][64 lanes][8]
+// (K zero-padded to 32).
+struct StemF16Args {
+  const uint16_t* x;
+  const float* x_nchw;  // in_kind 3: dense NCHW f32 [n][cin][h][w], x unused
+  int in_kind;          // 1: f16 NHWC view x, 3: x_nchw
+  const uint16_t* wfrag;
+  const uint16_t* bias;  // f16 bias [cout] or null
+  uint16_t* y;
+  int n, h, w, cin, ho, wo, kh, kw, sh, sw, pt, pl, cout, m;
+  int x_pix_stride, x_c_off, y_pix_stride, y_c_off;
+  int act;
+};
+bool stem_f16_supported(int cin, int kh, int kw, int cout, int wo, int sh, int sw);  // incl. LDS of a band
+void launch_stem_f16(hipStream_t st, const StemF16Args& a);
+
 // Rank-4 strided copy (k_shape.hip): y[y_off + sum i_k ys_k] =
 // x[x_off + sum i_k xs_k] over 0 <= i_k < dims_k (elements).
 struct StridedCopyArgs {

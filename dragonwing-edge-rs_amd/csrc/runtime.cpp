@@ -80,6 +80,7 @@ struct Launch {
   // direct-conv launches: their arguments, shared with `fn`, so an input
   // can be switched to the NCHW f32 loader after the list is built
   std::shared_ptr<DirectArgs> da;
+  std::shared_ptr<StemF16Args> sa;  // the same for the fp16 MFMA stem
   // band-tile depthwise launches: their output rows per band, chosen by the tuner
   std::shared_ptr<int> dw_band;  // units * 100 + band rows
   std::shared_ptr<DwArgs> dwa;
@@ -154,6 +155,7 @@ struct Runtime {
   struct NchwIn {
     int launch = -2;        // the stem launch reading the input, -1 none, -2 not looked up
     DirectArgs orig{};      // its arguments for the NHWC input
+    StemF16Args orig_s{};   // the same when it is the fp16 MFMA stem
     void* stage = nullptr;  // owned device copy of host NCHW data
     size_t stage_bytes = 0;
     const void* src = nullptr;  // NCHW data the runs read (stage or a bound buffer)
@@ -1716,6 +1718,44 @@ void Runtime::emit_conv(const Group& gr) {
     push_igemm(L, a, 2);
     return;
   }
+  // the fp16 graphs' three-channel stem (all of K in one fp16 k-step) on
+  // the fp16 matrix cores, held to the fp16 tolerance like the other MFMA
+  // convs of those graphs
+  const bool stem_mfma = g.dtype == DW_GRAPH_F16 && gr.in_kind == 1 && gr.out_kind == 1 && gr.res.empty() &&
+                         stem_f16_supported(ci, kh, kw, co, (int)y.w, sh, sw) && op.p.group <= 1 && op.p.dilations[0] <= 1 &&
+                         op.p.dilations[1] <= 1 && W.dtype == DW_DTYPE_F16 &&
+                         (!has_bias || g.t[op.in[2]].dtype == DW_DTYPE_F16) && y.pix_stride % 4 == 0 &&
+                         y.abs_off % 4 == 0;
+  if (stem_mfma) {
+    // fragment order [cb][lane][j] = W[k = 8 (lane / 16) + j][c = 16 cb + lane % 16],
+    // zero past K (the HWIO weights flattened over kh, kw, c_in)
+    const int K = kh * kw * ci;
+    std::vector<uint16_t> frag((size_t)(co / 16) * 64 * 8, 0);
+    for (int cb = 0; cb < co / 16; ++cb)
+      for (int l = 0; l < 64; ++l)
+        for (int j = 0; j < 8; ++j) {
+          const int k = 8 * (l / 16) + j, c = 16 * cb + l % 16;
+          if (k < K) frag[((size_t)cb * 64 + l) * 8 + j] = ((const uint16_t*)W.data.data())[(size_t)k * co + c];
+        }
+    StemF16Args a{};
+    a.x = (const uint16_t*)x.base;
+    a.in_kind = 1;
+    a.wfrag = (const uint16_t*)upload(frag.data(), frag.size() * 2);
+    a.bias = has_bias ? (const uint16_t*)upload(g.t[op.in[2]].data.data(), g.t[op.in[2]].data.size()) : nullptr;
+    a.y = (uint16_t*)y.base;
+    a.n = (int)x.n; a.h = (int)x.h; a.w = (int)x.w; a.cin = ci; a.ho = (int)y.h; a.wo = (int)y.w;
+    a.kh = kh; a.kw = kw; a.sh = sh; a.sw = sw; a.pt = pt; a.pl = pl; a.cout = co;
+    a.m = (int)y.pixels();
+    a.x_pix_stride = x.pix_stride; a.x_c_off = x.abs_off;
+    a.y_pix_stride = y.pix_stride; a.y_c_off = y.abs_off;
+    a.act = gr.act;
+    L.kernel = "stem_f16_mfma";
+    L.bytes += (double)x.bytes() + frag.size() * 2.0 + (double)y.bytes();
+    L.sa = std::make_shared<StemF16Args>(a);
+    L.fn = [sa = L.sa](hipStream_t st) { launch_stem_f16(st, *sa); };
+    launches.push_back(L);
+    return;
+  }
   // u8 -> f16 1x1 on the fp16 matrix cores (the dequantized fp16 layers of a
   // quantized graph), held to the fp16 tolerance like the other MFMA convs
   const bool head_mfma = !exact_u8_f16 && gr.in_kind == 2 && gr.out_kind == 1 && gr.res.empty() && kh == 1 &&
@@ -2353,14 +2393,27 @@ void Runtime::set_input_nchw(const std::string& name, const void* src) {
         e.launch = found;
         e.orig = a;
       }
+    } else if (count == 1 && launches[found].sa) {
+      // the fp16 MFMA stem reads any dense f16 input of up to 4 channels
+      const StemF16Args& a = *launches[found].sa;
+      if (t.dtype == F16 && a.in_kind == 1 && (const void*)a.x == t.base && a.x_pix_stride == a.cin &&
+          a.x_c_off == 0 && t.pix_stride == (int)t.c && t.abs_off == 0) {
+        e.launch = found;
+        e.orig_s = a;
+      }
     }
   }
   e.src = src;
   e.active = true;
-  if (e.launch >= 0) {
+  if (e.launch >= 0 && launches[e.launch].da) {
     DirectArgs& a = *launches[e.launch].da;
     a = e.orig;
     a.x = src;
+    a.in_kind = 3;
+  } else if (e.launch >= 0) {
+    StemF16Args& a = *launches[e.launch].sa;
+    a = e.orig_s;
+    a.x_nchw = (const float*)src;
     a.in_kind = 3;
   }
   drop_capture();
@@ -2370,7 +2423,8 @@ void Runtime::reset_input_layout(const std::string& name) {
   auto it = nchw.find(name);
   if (it == nchw.end() || !it->second.active) return;
   NchwIn& e = it->second;
-  if (e.launch >= 0) *launches[e.launch].da = e.orig;
+  if (e.launch >= 0 && launches[e.launch].da) *launches[e.launch].da = e.orig;
+  else if (e.launch >= 0) *launches[e.launch].sa = e.orig_s;
   e.active = false;
   e.src = nullptr;
   drop_capture();

@@ -666,3 +666,51 @@ def test_single_op_graphs(backend):
     got = rt.get_output_bytes("out").view(np.float32).reshape(1, 56, 56, 64)
     np.testing.assert_array_equal(got, oracle.relu_f32(oracle.bias_add_f32(oracle.conv2d_f32_nhwc(x, w, (1, 1), (1, 1)), b)))
     assert [L["kernel"] for L in rt.launches()] == ["direct_conv"]
+
+
+@pytest.mark.parametrize("ci,k,s,p,co,n,h,w,act", [
+    (3, 3, 2, 1, 16, 2, 64, 64, "silu"),    # the YOLO stem, whole 16-pixel blocks per row
+    (3, 3, 2, 1, 48, 3, 37, 29, "silu"),    # ragged rows, an odd last band
+    (3, 3, 2, 1, 64, 1, 21, 70, "none"),
+    (1, 5, 1, 2, 32, 2, 19, 23, "silu"),    # K = 25
+    (2, 3, 1, 1, 16, 1, 9, 33, "none"),     # K = 18
+    (3, 1, 1, 0, 64, 2, 17, 16, "silu"),    # K = 3
+])
+def test_f16_stem_mfma_vs_oracle(backend, ci, k, s, p, co, n, h, w, act):
+    # the fp16 graphs' convs whose whole K fits one fp16 k-step run on the
+    # fp16 matrix cores (stem_f16_mfma): within 1e-2 of the oracle's output's
+    # largest magnitude, every shape class of the kernel (rows of whole or
+    # ragged 16-pixel blocks, a last band of one row, 1..4 channel blocks)
+    from dragonwing_edge_rs_amd.graph import Graph, GRAPH_F16
+
+    r = np.random.default_rng(1000 + ci * 100 + k * 10 + co)
+    x = synth.f16_bits(r.normal(0.0, 1.0, (n, h, w, ci)))
+    wt = synth.f16_bits(r.normal(0.0, (1.0 / (k * k * ci)) ** 0.5, (k, k, ci, co)))
+    b = synth.f16_bits(r.normal(0.0, 0.1, (co,)))
+    ho, wo = (h + 2 * p - k) // s + 1, (w + 2 * p - k) // s + 1
+    g = Graph(GRAPH_F16)
+    g.add_tensor("x", x.shape, "f16")
+    g.add_initializer("w", wt, "f16")
+    g.add_initializer("b", b, "f16")
+    out = "y" if act == "none" else "out"
+    for t in ("y", "sg", "out") if act != "none" else ("y",):
+        g.add_tensor(t, (n, ho, wo, co), "f16")
+    g.add_op("conv", "Conv", ["x", "w", "b"], ["y"], kernel_shape=(k, k), strides=(s, s), pads=(p, p, p, p))
+    if act != "none":
+        g.add_op("sig", "Sigmoid", ["y"], ["sg"])
+        g.add_op("mul", "Mul", ["y", "sg"], ["out"])
+    g.set_io(["x"], [out])
+    ref = oracle_run(g, {"x": x})[out]
+    rt = HipGraphRuntime(g, backend)
+    rt.set_input_bytes("x", x)
+    rt.run()
+    assert [L["kernel"] for L in rt.launches()] == ["stem_f16_mfma"]
+    got = rt.get_output_bytes(out).view(np.uint16).reshape(n, ho, wo, co)
+    e = rel_err(oracle.f16_to_f32(got), oracle.f16_to_f32(ref))
+    print(f"stem {ci}x{k}x{k}/{s} -> {co} at {n}x{h}x{w}: rel err {e:.2e}", flush=True)
+    assert e <= 1e-2
+    # the same input as NCHW f32 planes, read by the stem itself: the same bytes
+    xn = np.ascontiguousarray(synth.f16_value(x).transpose(0, 3, 1, 2))
+    rt.set_input_nchw_f32("x", xn)
+    rt.run()
+    assert rt.get_output_bytes(out).view(np.uint16).reshape(n, ho, wo, co).tobytes() == got.tobytes()
