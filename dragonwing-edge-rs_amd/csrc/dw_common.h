@@ -81,7 +81,9 @@ struct IgemmArgs {
   int tile_bc, tile_pb;    // tile choice (channels, 16-pixel blocks per wave); 0 = heuristic
   int tile_tpw;            // > 0: persistent kernel, pixel tiles per workgroup (small K only);
                            // -1: the streamed-weight kernel (long K); -2: the row-tile kernel;
-                           // -3: the wide-tile kernel (c_in % 128 == 0)
+                           // -3: the wide-tile kernel (c_in % 128 == 0); -4: the band-tile
+                           // kernel (tile_pb: its band height in rows)
+  int band_rows;           // set by the launcher for the band-tile kernel
   int x_bytes;             // set by the launcher: bytes of the input view's buffer (< 2^31)
   float r_cin, r_kw, r_hwo, r_wo;  // set by the launcher: 1/cin, 1/kw, 1/(ho*wo), 1/wo
   int y_bytes, r_bytes;            // set by the launcher: bytes of the output and residual views

@@ -1,0 +1,281 @@
+// Band-tile implicit GEMM for 3x3 convolutions (stride 1, padding 1, int8
+// or fp16): one workgroup of 8 waves owns R whole output rows of one image
+// (R chosen by the graph runtime's tuner, a divisor of the height) and BC
+// output channels, so a layer runs as one round of workgroups, about one a
+// CU, whatever its width.
+//
+// The row-tile kernel (igemm_rows.h) fixes its tile at 320 output pixels,
+// which on the 80x80 maps of a batch-32 graph makes 640 workgroups for 512
+// slots: a second, quarter-full round, and each round pays the start-up
+// loads, the k-loop and the epilogue one after the other.  Here the start-up
+// is the row-tile kernel's (all of K's weights and the R + 2 input rows, with
+// halo and padding, go to LDS once, the rows converted to the MFMA operand:
+// int8 u8 xor 0x80 or the padding pattern, fp16 as they are), and then each
+// wave walks its own contiguous range of the band's 16-pixel blocks, PBC
+// blocks at a time, both operands read from LDS (the next k-step's
+// fragments while this one's MFMAs run).  The ranges of the 8 waves differ
+// by at most one block; blocks past a range's end in its last chunk are
+// skipped (wave-uniform) and never stored.  Each wave has its own LDS rows
+// for the epilogue's regrouping, so a wave's epilogue overlaps the other
+// waves' k-loops.
+//
+// LDS layout: epilogue data [table 256][bias' 4 BC][multipliers 4 BC], the
+// k-slice offsets, the weights (fragment order, [k-step][block][64 lanes x
+// 16 B]), the input tile ((R + 2) x (W + 2) pixels of SU 16-byte units, SU =
+// c_in * esize / 16 made odd: 8 consecutive pixels' units fall in 8
+// distinct bank groups), the 8 waves' regroup rows.
+//
+// The per-output arithmetic and the epilogues are igemm_kernel's
+// (igemm_store), and integer sums do not depend on the k-order, so int8
+// results are those of every other tile shape; fp16 sums run over the same
+// k-steps in the same order as the row-tile kernel.
+#pragma once
+
+#include "igemm_kernel.h"
+
+namespace dw {
+
+bool igemm_launch_band_i8_a(hipStream_t st, const IgemmArgs& a, const TileCfg& t, int epv);  // generic, QU8
+bool igemm_launch_band_i8_b(hipStream_t st, const IgemmArgs& a, const TileCfg& t, int epv);  // LUT variants
+bool igemm_launch_band_f16(hipStream_t st, const IgemmArgs& a, const TileCfg& t);
+
+namespace ig {
+
+constexpr int kBandWaves = 8;
+constexpr int kBandThreads = 64 * kBandWaves;
+constexpr int kBandFill = 16;  // input units each thread loads at start-up (at most)
+
+// 16-pixel blocks per chunk (accumulators CB x PBC)
+__host__ __device__ constexpr int band_pbc(int cb) { return cb <= 2 ? 8 : (cb <= 5 ? 4 : 2); }
+__host__ __device__ constexpr int band_su(int cu) { return cu | 1; }
+__host__ __device__ constexpr int band_tab_off(int bc) { return 256 + 8 * bc; }
+__host__ __device__ constexpr int band_w_off(int bc, int ks) { return (band_tab_off(bc) + ks * 16 + 15) / 16 * 16; }
+__host__ __device__ constexpr int band_x_off(int bc, int ks) { return band_w_off(bc, ks) + ks * bc * 64; }
+__host__ __device__ constexpr int band_tile_bytes(int rows, int w, int cu) { return (rows + 2) * (w + 2) * band_su(cu) * 16; }
+__host__ __device__ constexpr int band_xp_off(int bc, int ks, int rows, int w, int cu) {
+  return band_x_off(bc, ks) + band_tile_bytes(rows, w, cu);
+}
+inline size_t band_lds_bytes(int bc, int ks, int rows, int w, int cu) {
+  return (size_t)band_xp_off(bc, ks, rows, w, cu) + (size_t)kBandWaves * 16 * xpose_row(bc);
+}
+
+template <int ESZ, int BC, int EPV>
+__global__ __launch_bounds__(kBandThreads) void igemm_band_kernel(const IgemmArgs a) {
+  constexpr int CB = BC / 16;
+  constexpr int PBC = band_pbc(CB);
+  constexpr bool FAST = EPV != EPV_GENERIC;
+  static_assert(!FAST || ESZ == 1, "specialised epilogues are int8");
+  using acc_t = typename std::conditional<ESZ == 1, v4i, v4f>::type;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+
+  const int KSTEPS = a.ksteps, COUTP = a.cout_pad, CIN = a.cin;
+  const int W = a.w, H = a.h, R = a.band_rows;
+  const int TW = W + 2;
+  const int CU = CIN * ESZ / 16;  // 16-byte units per pixel
+  const int SU = band_su(CU);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  // XCD-aware tile order, as igemm_kernel: tile = (image, band, channel tile)
+  const int nwg = gridDim.x;
+  const int bid = blockIdx.x;
+  const int xcd = bid & 7, idx = bid >> 3;
+  const int base = nwg >> 3, rem = nwg & 7;
+  const int tile = xcd * base + min(xcd, rem) + idx;
+  const int ctiles = COUTP / BC;
+  const int ptile = tile / ctiles;
+  const int c0 = (tile - ptile * ctiles) * BC;
+  const int bands = H / R;
+  const int n = ptile / bands;
+  const int r0 = (ptile - n * bands) * R;
+  const int pw0 = (n * H + r0) * W;  // the band's first output pixel
+
+  uint8_t* const s_lut = smem;
+  uint8_t* const s_bias = smem + 256;
+  uint8_t* const s_ms = smem + 256 + 4 * BC;
+  int* const s_tab = reinterpret_cast<int*>(smem + band_tab_off(BC));
+  uint8_t* const s_w = smem + band_w_off(BC, KSTEPS);
+  uint8_t* const s_x = smem + band_x_off(BC, KSTEPS);
+  uint8_t* const s_xp = smem + band_xp_off(BC, KSTEPS, R, W, CU);
+
+  // ---- weights (all of K, fragment order) and epilogue data, direct to LDS
+  const int frag_lane = ((lane & 15) * 64 + (lane >> 4) * 16);
+  {
+    const int nfr = KSTEPS * CB;
+    for (int f = wave; f < nfr; f += kBandWaves) {
+      const int sl = f / CB, cb = f - sl * CB;
+      const uint8_t* src = a.wpk + (((uint32_t)sl * COUTP + c0 + cb * 16) * 64u + frag_lane);
+      __builtin_amdgcn_global_load_lds((const void*)src, (__attribute__((address_space(3))) void*)(s_w + f * 1024),
+                                       16, 0, 0);
+    }
+  }
+  const int nvalid = min(BC, a.cout - c0);
+  EpiLds ep{nullptr, nullptr, nullptr, nullptr};
+  if (a.epi == EPI_QU8) {
+    ep.bias = a.bias_i ? reinterpret_cast<const int*>(s_bias) : nullptr;
+    ep.ms = reinterpret_cast<const float*>(s_ms);
+    ep.lut = a.lut ? s_lut : nullptr;
+    if (wave == 0 && a.bias_i && lane < nvalid / 4)
+      __builtin_amdgcn_global_load_lds((const void*)(a.bias_i + c0 + lane * 4),
+                                       (__attribute__((address_space(3))) void*)s_bias, 16, 0, 0);
+    if (wave == 1 && lane < nvalid / 4)
+      __builtin_amdgcn_global_load_lds((const void*)(a.mscale + c0 + lane * 4),
+                                       (__attribute__((address_space(3))) void*)s_ms, 16, 0, 0);
+    if (wave == 2 && a.lut && lane < 16)
+      __builtin_amdgcn_global_load_lds((const void*)(a.lut + lane * 16),
+                                       (__attribute__((address_space(3))) void*)s_lut, 16, 0, 0);
+  } else if (a.epi == EPI_F16 && a.bias_h) {
+    ep.bias_h = reinterpret_cast<const uint16_t*>(s_bias);
+    if (wave == 0 && lane < nvalid / 2)
+      __builtin_amdgcn_global_load_lds((const void*)(a.bias_h + c0 + lane * 2),
+                                       (__attribute__((address_space(3))) void*)s_bias, 4, 0, 0);
+  }
+
+  // ---- input tile: rows r0 - 1 .. r0 + R, columns -1 .. W, raw 16-byte
+  // units (out-of-image units: out-of-range loads, which return zero), all
+  // in flight together
+  const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, a.x_bytes, 0x00020000);
+  const int units = (R + 2) * TW * CU;
+  const float r_cu = 1.0f / (float)CU, r_tw = 1.0f / (float)TW;
+  u32x4 xv[kBandFill];
+  int xdst[kBandFill];  // LDS offset of the unit, or -1 for none
+  bool xin[kBandFill];
+#pragma unroll
+  for (int i = 0; i < kBandFill; ++i) {
+    const int u = tid + i * kBandThreads;
+    xdst[i] = -1;
+    xin[i] = false;
+    if (u < units) {
+      const int ip = div_small(u, CU, r_cu);
+      const int cu = u - ip * CU;
+      const int tr = div_small(ip, TW, r_tw), tc = ip - tr * TW;
+      const int ih = r0 - 1 + tr, iw = tc - 1;
+      const bool ok = (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W;
+      // byte offset: the view's element offset times the element size
+      const int off = ok ? ((((n * H + ih) * W + iw) * a.x_pix_stride + a.x_c_off) * ESZ + cu * 16) : (int)0x80000000;
+      xv[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrsrc, off, 0, 0));
+      xdst[i] = (ip * SU + cu) * 16;
+      xin[i] = ok;
+    }
+  }
+
+  // ---- k-slice offsets: slice s of k-step q is 16 bytes of input channels
+  // of one tap; its unit's offset from the pixel's top-left tap in the tile
+  // (slices past K: any unit, their weights are zero)
+  for (int e = tid; e < KSTEPS * 4; e += kBandThreads) {
+    const int k = e * (16 / ESZ);  // the slice's first element of K
+    int off = 0;
+    if (k < 9 * CIN) {
+      const int tap = k / CIN, ci = k - (k / CIN) * CIN;
+      const int kh = tap / 3, kw = tap - (tap / 3) * 3;
+      off = ((kh * TW + kw) * SU + ci * ESZ / 16) * 16;
+    }
+    s_tab[e] = off;
+  }
+
+  // everything above has landed (direct loads included); write the tile
+  __builtin_amdgcn_s_waitcnt(0);
+#pragma unroll
+  for (int i = 0; i < kBandFill; ++i) {
+    if (xdst[i] >= 0) {
+      if constexpr (ESZ == 1) {
+        const uint32_t key = xin[i] ? a.xxor : a.xpad;
+        *reinterpret_cast<u32x4*>(s_x + xdst[i]) = xv[i] ^ key;
+      } else {
+        *reinterpret_cast<u32x4*>(s_x + xdst[i]) = xv[i];  // padding: the zeros of the out-of-range load
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- this wave's blocks [bbeg, bend) of the band's R * W pixels
+  const int np = R * W;
+  const int nb = (np + 15) / 16;
+  const int bbeg = (wave * nb) / kBandWaves, bend = ((wave + 1) * nb) / kBandWaves;
+  const int pend = pw0 + min(bend * 16, np);  // pixels from here on are another wave's
+  const int cq = 4 * (lane >> 4);
+  const int* const my_tab = s_tab + (lane >> 4);
+  const uint8_t* const a_lane = s_w + lane * 16;
+  uint8_t* const xp = (FAST && (BC >= 32 || EPV == EPV_QU8_LUT_HEAD)) ? s_xp + wave * 16 * xpose_row(BC) : nullptr;
+
+  for (int b0 = bbeg; b0 < bend; b0 += PBC) {
+    const int nvb = min(PBC, bend - b0);  // blocks of this chunk (wave-uniform)
+    int pbase[PBC];
+#pragma unroll
+    for (int pb = 0; pb < PBC; ++pb) {
+      const int pl = (b0 + pb) * 16 + (lane & 15);
+      const int q = (pb < nvb && pl < np) ? pl : 0;
+      const int r = div_small(q, W, a.r_wo), c = q - r * W;
+      pbase[pb] = (r * TW + c) * SU * 16;
+    }
+    acc_t acc[CB][PBC];
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+      acc_t init = acc_t{0, 0, 0, 0};
+      if constexpr (FAST) {
+        if (a.bias_i) init = *reinterpret_cast<const v4i*>(s_bias + 4 * (cb * 16 + cq));
+      }
+#pragma unroll
+      for (int pb = 0; pb < PBC; ++pb) acc[cb][pb] = init;
+    }
+
+    v4i afr[2][CB], bfr[2][PBC];
+#define DW_READ_K(q_, slot_)                                                                 \
+  {                                                                                          \
+    const int toff_ = my_tab[(q_) * 4];                                                      \
+    _Pragma("unroll") for (int cb = 0; cb < CB; ++cb)                                        \
+      afr[slot_][cb] = *reinterpret_cast<const v4i*>(a_lane + ((q_) * CB + cb) * 1024);      \
+    _Pragma("unroll") for (int pb = 0; pb < PBC; ++pb)                                       \
+      bfr[slot_][pb] = *reinterpret_cast<const v4i*>(s_x + pbase[pb] + toff_);               \
+  }
+    DW_READ_K(0, 0);
+    for (int q0 = 0; q0 < KSTEPS; q0 += 2) {
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int q = q0 + r;
+        if (q < KSTEPS) {
+          if (q + 1 < KSTEPS) DW_READ_K(q + 1, (r + 1) & 1);
+#pragma unroll
+          for (int pb = 0; pb < PBC; ++pb) {
+            if (pb >= nvb) break;  // wave-uniform
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) {
+              if constexpr (ESZ == 1)
+                acc[cb][pb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[r][cb], bfr[r][pb], acc[cb][pb], 0, 0, 0);
+              else
+                acc[cb][pb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    __builtin_bit_cast(v8h, afr[r][cb]), __builtin_bit_cast(v8h, bfr[r][pb]), acc[cb][pb], 0, 0, 0);
+            }
+          }
+        }
+      }
+    }
+#undef DW_READ_K
+    igemm_store<ESZ, BC, PBC, EPV>(a, ep, acc, c0, pw0 + b0 * 16, lane, s_ms, s_lut, xp, pend);
+  }
+}
+
+template <int ESZ, int BC, int EPV>
+void launch_band_bc(hipStream_t st, const IgemmArgs& a, const TileCfg& t) {
+  const int rows = a.band_rows;
+  const dim3 grid((unsigned)(a.n * (a.h / rows) * (a.cout_pad / t.bc)));
+  const size_t lds = band_lds_bytes(t.bc, a.ksteps, rows, a.w, a.cin * ESZ / 16);
+  hipLaunchKernelGGL((igemm_band_kernel<ESZ, BC, EPV>), grid, dim3(kBandThreads), lds, st, a);
+}
+
+template <int ESZ, int EPV>
+bool launch_band_tiles(hipStream_t st, const IgemmArgs& a, const TileCfg& t) {
+  switch (t.bc) {
+    case 128: launch_band_bc<ESZ, 128, EPV>(st, a, t); return true;
+    case 80: launch_band_bc<ESZ, 80, EPV>(st, a, t); return true;
+    case 64: launch_band_bc<ESZ, 64, EPV>(st, a, t); return true;
+    case 32: launch_band_bc<ESZ, 32, EPV>(st, a, t); return true;
+    case 16: launch_band_bc<ESZ, 16, EPV>(st, a, t); return true;
+  }
+  return false;
+}
+
+}  // namespace ig
+}  // namespace dw

@@ -285,7 +285,8 @@ __host__ __device__ constexpr int xpose_bytes(int bc) { return 4 * 16 * xpose_ro
 // weight fragments come from global memory (L2) into registers.
 template <int BC, int PB>
 __device__ __forceinline__ void igemm_store_head(const IgemmArgs& a, const v4i (&acc)[BC / 16][PB], int p0, int lane,
-                                                 const uint8_t* s_ms, const uint8_t* s_lut, uint8_t* xp) {
+                                                 const uint8_t* s_ms, const uint8_t* s_lut, uint8_t* xp,
+                                                 int pend) {
   constexpr int CB = BC / 16;
   constexpr int KS2 = (BC + 31) / 32;  // the 1x1's k-steps over the BC u8 channels
   const int cq = 4 * (lane >> 4);
@@ -337,7 +338,7 @@ __device__ __forceinline__ void igemm_store_head(const IgemmArgs& a, const v4i (
       v4f acc2 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int ks = 0; ks < KS2; ++ks) acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[cb][ks], xf[ks], acc2, 0, 0, 0);
-      if (p < a.m && ch < a.h_cout)
+      if (p < pend && ch < a.h_cout)
         *reinterpret_cast<uint2*>(yrow + ch) = conv1x1_f16_finish(acc2, a.h_bias ? a.h_bias + ch : nullptr, a.h_act);
     }
   }
@@ -351,16 +352,19 @@ __device__ __forceinline__ void igemm_store_head(const IgemmArgs& a, const v4i (
 // there so that each lane stores 16 consecutive channels: one 16-byte store
 // per lane and 4 blocks, whole cache lines when the output rows are dense,
 // instead of a 4-byte store per lane and block (a 16-channel tile gains
-// nothing: it has one block).
+// nothing: it has one block).  Pixels at or past min(a.m, pend) are not
+// stored (pend: the end of the caller's pixel range, when its last blocks
+// belong to another wave).
 template <int ESZ, int BC, int PB, int EPV, typename AccT>
 __device__ __forceinline__ void igemm_store(const IgemmArgs& a, const EpiLds& ep, AccT (&acc)[BC / 16][PB], int c0,
                                             int p0, int lane, const uint8_t* s_ms, const uint8_t* s_lut,
-                                            uint8_t* xp = nullptr) {
+                                            uint8_t* xp = nullptr, int pend = 0x7fffffff) {
   constexpr int CB = BC / 16;
   constexpr bool FAST = EPV != EPV_GENERIC;
   const int cq = 4 * (lane >> 4);
+  const int plim = min(a.m, pend);
   if constexpr (EPV == EPV_QU8_LUT_HEAD) {
-    igemm_store_head<BC, PB>(a, acc, p0, lane, s_ms, s_lut, xp);
+    igemm_store_head<BC, PB>(a, acc, p0, lane, s_ms, s_lut, xp, plim);
   } else if constexpr (FAST) {
     const bool full = c0 + BC <= a.cout;
     const bool wide = CB >= 2 && xp != nullptr && full && (a.y_pix_stride & 15) == 0 &&
@@ -375,7 +379,7 @@ __device__ __forceinline__ void igemm_store(const IgemmArgs& a, const EpiLds& ep
 #pragma unroll
     for (int pb = 0; pb < PB; ++pb) {
       const int p = p0 + pb * 16 + (lane & 15);
-      if (p >= a.m) continue;
+      if (p >= plim) continue;
       uint8_t* yrow = (uint8_t*)a.y + (size_t)p * a.y_pix_stride + a.y_c_off + c0 + cq;
       uint32_t rres[CB];
       if constexpr (EPV == EPV_QU8_LUT_RES) {
@@ -427,7 +431,7 @@ __device__ __forceinline__ void igemm_store(const IgemmArgs& a, const EpiLds& ep
 #pragma unroll
       for (int pb = 0; pb < PB; ++pb) {
         const int p = p0 + pb * 16 + (lane & 15);
-        if (p < a.m) epilogue4<ESZ>(a, ep, acc[cb][pb], ch, ch - c0, p);
+        if (p < plim) epilogue4<ESZ>(a, ep, acc[cb][pb], ch, ch - c0, p);
       }
     }
   }

@@ -1,7 +1,8 @@
 // int8 implicit-GEMM instantiations with a detect head's u8 -> f16 1x1
-// conv fused into the epilogue (EPV_QU8_LUT_HEAD): the staged kernel and the
-// row-tile kernel, tiles holding every channel of the 64- or 80-channel
-// head convs.
+// conv fused into the epilogue (EPV_QU8_LUT_HEAD): the staged kernel, the
+// row-tile kernel and the band-tile kernel, tiles holding every channel of
+// the 64- or 80-channel head convs.
+#include "igemm_band.h"
 #include "igemm_rows.h"
 
 namespace dw {
@@ -24,6 +25,16 @@ bool igemm_launch_head_i8(hipStream_t st, const IgemmArgs& a, const TileCfg& t) 
     }
     if (t.bc == 80) {
       hipLaunchKernelGGL((ig::igemm_rows_kernel<1, 80, EPV_QU8_LUT_HEAD>), grid, dim3(256), lds, st, a);
+      return true;
+    }
+  }
+  if (t.tpw == -4) {
+    if (t.bc == 64) {
+      ig::launch_band_bc<1, 64, EPV_QU8_LUT_HEAD>(st, a, t);
+      return true;
+    }
+    if (t.bc == 80) {
+      ig::launch_band_bc<1, 80, EPV_QU8_LUT_HEAD>(st, a, t);
       return true;
     }
   }

@@ -230,6 +230,7 @@ struct Runtime {
   void fuse_heads();
   void tag_group(const Group& gr, size_t first, int gid);
   void plan_streams(int n);
+  float time_graph();
   void enqueue(hipStream_t st);
   void run();
 };
@@ -402,9 +403,52 @@ void Runtime::build(Backend* b, const GraphIR& graph, bool stats_mode) {
     fuse_pairs();
     fuse_heads();
   }
+  // streams: the schedule over 4 streams, or one stream, whichever runs the
+  // whole graph faster (the cross-stream waits cost more than the overlap
+  // gains when the layers already fill the GPU); DW_GRAPH_STREAMS=<n> fixes
+  // the count
   int ns = 4;
-  if (const char* env = getenv("DW_GRAPH_STREAMS")) ns = atoi(env);
-  plan_streams(stats ? 1 : std::max(1, std::min(ns, 8)));
+  const char* senv = getenv("DW_GRAPH_STREAMS");
+  if (senv) ns = atoi(senv);
+  ns = stats ? 1 : std::max(1, std::min(ns, 8));
+  plan_streams(ns);
+  const char* tune_env = getenv("DW_AUTOTUNE");
+  const bool tuned = !((tune_env && tune_env[0] == '0') || getenv("DW_IGEMM_TILE"));
+  if (!senv && !stats && tuned && nstreams > 1) {
+    const float t_multi = time_graph();
+    plan_streams(1);
+    const float t_one = time_graph();
+    if (t_multi < t_one) plan_streams(ns);
+    if (const char* lp = getenv("DW_AUTOTUNE_LOG"))
+      if (FILE* log = fopen(lp, "a")) {
+        fprintf(log, "graph\t%d streams\t%.2f\ngraph\t1 stream\t%.2f\n", ns, t_multi * 1e3f, t_one * 1e3f);
+        fclose(log);
+      }
+  }
+}
+
+// Milliseconds of one graph run on the current stream schedule (the best of
+// 3 timings of 4 runs back to back; the activations hold whatever the last
+// run left, which the timing does not depend on).
+float Runtime::time_graph() {
+  hipStream_t st = be->stream;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  DW_HIP(hipEventCreate(&e0));
+  DW_HIP(hipEventCreate(&e1));
+  enqueue(st);
+  float best = 1e30f;
+  for (int r = 0; r < 3; ++r) {
+    DW_HIP(hipEventRecord(e0, st));
+    for (int k = 0; k < 4; ++k) enqueue(st);
+    DW_HIP(hipEventRecord(e1, st));
+    DW_HIP(hipEventSynchronize(e1));
+    float ms = 0;
+    DW_HIP(hipEventElapsedTime(&ms, e0, e1));
+    best = std::min(best, ms / 4);
+  }
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  return best;
 }
 
 namespace {
@@ -497,6 +541,15 @@ void Runtime::tag_group(const Group& gr, size_t first, int gid) {
 // stream's tail) it takes the stream whose last launch is oldest.  It then
 // waits for the latest dependency on every other stream.
 void Runtime::plan_streams(int n) {
+  // a previous schedule's events (nothing in flight uses them once the
+  // streams are idle)
+  if (!evs.empty()) {
+    DW_HIP(hipStreamSynchronize(be->stream));
+    for (hipStream_t s : side) DW_HIP(hipStreamSynchronize(s));
+    for (hipEvent_t e : evs)
+      if (e) (void)hipEventDestroy(e);
+    evs.clear();
+  }
   nstreams = n;
   for (auto& L : launches) {
     L.stream = 0;
@@ -2100,7 +2153,8 @@ void Runtime::fuse_pairs() {
 // (EPV_QU8_LUT_HEAD), so the intermediate is neither stored nor read back
 // and the 1x1's launch goes.  The 1x1's arithmetic is conv1x1_u8_f16's, so
 // its outputs are the same.  Each candidate is timed over the head tiles
-// (the staged and row-tile kernels with one tile of every channel) and kept
+// (the staged, row-tile and band-tile kernels with one tile of every
+// channel; a DW_IGEMM_TILE row- or band-tile override wins) and kept
 // only if it beats the two launches; DW_HEAD_FUSE=1 keeps every candidate,
 // =0 none; untuned plans keep none unless DW_HEAD_FUSE=1.  DW_HEAD_KEEP=
 // <op,op,..> keeps exactly the fusions whose 3x3 conv is listed.
@@ -2160,8 +2214,8 @@ void Runtime::fuse_heads() {
     h.h_act = c.act;
     h.h_scale = c.in_scale;
     h.h_zp = c.in_zp;
-    int bc[8], pb[8], tpw[8];
-    const int n = igemm_candidates(h, bc, pb, tpw, 8);
+    int bc[16], pb[16], tpw[16];
+    const int n = igemm_candidates(h, bc, pb, tpw, 16);
     if (n == 0) continue;
     h.tile_bc = bc[0];
     h.tile_pb = pb[0];

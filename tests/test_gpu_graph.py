@@ -264,6 +264,52 @@ def test_int8_graph_row_tiles_bit_exact(backend, monkeypatch):
         np.testing.assert_array_equal(gv, ref[o], err_msg=o)
 
 
+@pytest.mark.parametrize("tile", ["16,10,-4", "32,10,-4", "64,5,-4", "64,10,-4", "80,10,-4"])
+def test_int8_graph_band_tiles_bit_exact(backend, monkeypatch, tile):
+    # 320x320 input: the stride-1 3x3 layers the band-tile kernel accepts for
+    # the forced channel tile and band height (C2f bottlenecks with the table
+    # and table + residual epilogues, detect heads), exact plan: every output
+    # bit-exact against the oracle.
+    g, info = yolo.int8_graph(backend, batch=1, size=320, calib=yolo.calibration_images(4, 320))
+    monkeypatch.setenv("DW_IGEMM_TILE", tile)
+    monkeypatch.setenv("DW_PAIR", "0")
+    x = yolo.input_images(1, 320)
+    rt = HipGraphRuntime(g, backend, exact_u8_f16=True)
+    bands = [L["ops"] for L in rt.launches() if "_band" in L["kernel"]]
+    print(f"tile {tile}: {len(bands)} band launches", flush=True)
+    assert len(bands) >= 2, bands
+    rt.set_input_f32(info["input"], x)
+    rt.run()
+    got = gpu_outputs(rt, info)
+    ref = oracle_run(g, {info["input"]: synth.f16_bits(x)})
+    for o, gv in zip(info["outputs"], got):
+        np.testing.assert_array_equal(gv, ref[o], err_msg=f"{o} tile {tile}")
+
+
+@pytest.mark.parametrize("tile", ["64,10,-4", "80,10,-4"])
+def test_int8_graph_band_head_same_bytes(backend, monkeypatch, tile):
+    # The detect heads' fused u8 -> f16 1x1 on the band-tile kernel: the same
+    # bytes as the separate 1x1 launches.
+    g, info = yolo.int8_graph(backend, batch=2, size=320, calib=yolo.calibration_images(4, 320))
+    x = yolo.input_images(2, 320)
+    monkeypatch.setenv("DW_PAIR", "0")
+    monkeypatch.setenv("DW_HEAD_FUSE", "0")
+    rt0 = HipGraphRuntime(g, backend)
+    rt0.set_input_f32(info["input"], x)
+    rt0.run()
+    ref = gpu_outputs(rt0, info)
+    monkeypatch.setenv("DW_HEAD_FUSE", "1")
+    monkeypatch.setenv("DW_IGEMM_TILE", tile)
+    rt = HipGraphRuntime(g, backend)
+    heads = [L["kernel"] for L in rt.launches() if L["kernel"].endswith("_head")]
+    print(f"tile {tile}: heads {heads}", flush=True)
+    assert any("_band" in k for k in heads), heads
+    rt.set_input_f32(info["input"], x)
+    rt.run()
+    for o, a, b in zip(info["outputs"], ref, gpu_outputs(rt, info)):
+        np.testing.assert_array_equal(b, a, err_msg=f"{o} tile {tile}")
+
+
 @pytest.mark.parametrize("plant_subnormal_weight", [False, True])
 @pytest.mark.parametrize("stride", [1, 2])
 @pytest.mark.parametrize("shape", [(2, 23, 29, 48), (1, 9, 83, 64), (3, 17, 40, 192)])

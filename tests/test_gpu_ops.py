@@ -306,6 +306,53 @@ def test_qlinearconv_row_tiles_bit_exact(backend, geom, monkeypatch):
         np.testing.assert_array_equal(run_qconv(backend, c, s, p), ref, err_msg=f"tile {bc},4,-2")
 
 
+def band_tiles(h, w, ci, co, esize=1):
+    """The band-tile kernel's (channel tile, band height) pairs for a 3x3
+    stride-1 conv on an h x w map: channel tiles of 128, 80, 64, 32 or 16
+    that divide the padded c_out, heights that divide h with at least one
+    16-pixel block per wave (8 waves), the input tile within the start-up
+    loads (16 units a thread) and everything within the 160 KB of LDS."""
+    top = channel_tile(co)
+    pad = -(-co // top) * top
+    cu = ci * esize // 16
+    ks = -(-9 * ci * esize // 64)
+    out = []
+    for bc in (128, 80, 64, 32, 16):
+        if pad % bc:
+            continue
+        for rows in range(1, h + 1):
+            if h % rows or rows * w < 128 or (rows + 2) * (w + 2) * cu > 16 * 512:
+                continue
+            w_off = -(-(256 + 8 * bc + ks * 16) // 16) * 16
+            lds = w_off + ks * bc * 64 + (rows + 2) * (w + 2) * (cu | 1) * 16 + 8 * 16 * (bc + 16)
+            if lds <= 160 * 1024:
+                out.append((bc, rows))
+    return out
+
+
+@pytest.mark.parametrize("geom,x_zp", [((2, 10, 20, 64, 80), 119), ((1, 24, 16, 32, 32), 128),
+                                       ((3, 6, 40, 128, 128), 7), ((1, 14, 22, 16, 16), 140),
+                                       ((2, 9, 30, 64, 256), 100)])
+def test_qlinearconv_band_tiles_bit_exact(backend, geom, x_zp, monkeypatch):
+    # The band-tile kernel (3x3 stride 1: R whole rows staged in LDS, 8
+    # waves walking contiguous ranges of 16-pixel blocks, the last chunk of
+    # a range part-full) over every channel tile and band height it accepts;
+    # bands whose pixel count is not a multiple of 16 and of 8 blocks, and
+    # zero points other than 128 (the padding pattern).
+    n, h, w, ci, co = geom
+    r = synth.Rng(synth.seed_for(1300 + sum(geom)))
+    c = dict(x=r.integers((n, h, w, ci), 0, 255).astype(np.uint8),
+             w=r.integers((3, 3, ci, co), -127, 127).astype(np.int8),
+             bias=r.integers((co,), -4096, 4096).astype(np.int32),
+             w_scales=r.log_uniform((co,), 1e-3, 1e-2), x_scale=0.02, x_zp=x_zp, y_scale=0.05, y_zp=133)
+    ref = oracle_qconv(c, 1, 1)
+    tiles = band_tiles(h, w, ci, co)
+    assert tiles
+    for bc, rows in tiles:
+        monkeypatch.setenv("DW_IGEMM_TILE", f"{bc},{rows},-4")
+        np.testing.assert_array_equal(run_qconv(backend, c, 1, 1), ref, err_msg=f"tile {bc},{rows},-4")
+
+
 def wide_tiles(co):
     """The wide-tile kernel's channel tiles for c_out = co (input rows of
     whole 128-byte units)."""
@@ -551,6 +598,27 @@ def test_conv_f16_row_tiles_identical(backend, monkeypatch, geom):
         monkeypatch.setenv("DW_IGEMM_TILE", f"{bc},4,-2")
         got = run_conv_f16(backend, xh, kh_, bh, 1, 1, ops.ACT_SILU, exact=False)
         np.testing.assert_array_equal(got, first, err_msg=f"tile {bc},4,-2")
+
+
+@pytest.mark.parametrize("geom", [(2, 16, 16, 32, 32), (1, 10, 40, 64, 80), (2, 8, 18, 128, 64)])
+def test_conv_f16_band_tiles_identical(backend, monkeypatch, geom):
+    # The band-tile kernel in fp16: the same k-steps summed in the same order
+    # as the staged kernel, so the results are identical.
+    n, h, w, ci, co = geom
+    r = synth.Rng(synth.seed_for(1400 + sum(geom)))
+    xh = synth.f16_bits(r.normal((n, h, w, ci), 0.0, 1.0))
+    kh_ = synth.f16_bits(r.normal((3, 3, ci, co), 0.0, (1.0 / (9 * ci)) ** 0.5))
+    bh = synth.f16_bits(r.normal((co,), 0.0, 0.1))
+    ref = oracle_conv_f16(xh, kh_, bh, 1, 1, ops.ACT_SILU)
+    monkeypatch.setenv("DW_IGEMM_TILE", "16,4")
+    first = run_conv_f16(backend, xh, kh_, bh, 1, 1, ops.ACT_SILU, exact=False)
+    assert rel_err(f16v(first), f16v(ref)) <= 1e-2
+    tiles = band_tiles(h, w, ci, co, esize=2)
+    assert tiles
+    for bc, rows in tiles:
+        monkeypatch.setenv("DW_IGEMM_TILE", f"{bc},{rows},-4")
+        got = run_conv_f16(backend, xh, kh_, bh, 1, 1, ops.ACT_SILU, exact=False)
+        np.testing.assert_array_equal(got, first, err_msg=f"tile {bc},{rows},-4")
 
 
 @pytest.mark.parametrize("geom", [(2, 11, 9, 64, 128, 3, 1, 1), (2, 20, 18, 128, 64, 3, 2, 1),
