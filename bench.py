@@ -308,12 +308,13 @@ def read_counter_csv(d: Path):
 
 
 def plan_env(launches):
-    """The timed plan choices of a runtime (which chained pairs and fused
-    head 1x1s it kept), as the environment that makes another process build
-    the same launch list."""
+    """The timed plan choices of a runtime (which fused C2f blocks, chained
+    pairs and fused head 1x1s it kept), as the environment that makes
+    another process build the same launch list."""
     first = lambda L: L["ops"].split("+")[0]
     return {"DW_PAIR_KEEP": ",".join(first(L) for L in launches if L["kernel"].startswith("igemm_i8_pair")),
-            "DW_HEAD_KEEP": ",".join(first(L) for L in launches if L["kernel"].endswith("_head"))}
+            "DW_HEAD_KEEP": ",".join(first(L) for L in launches if L["kernel"].endswith("_head")),
+            "DW_C2F_KEEP": ",".join(first(L) for L in launches if L["kernel"].startswith("igemm_i8_c2f"))}
 
 
 def measure_traffic(workload: str, launches, timeout: float = 240.0):

@@ -236,6 +236,16 @@ bool igemm_pair_ok(const IgemmArgs& a1, const IgemmArgs& a2, int rows);
 int igemm_pair_rows(const IgemmArgs& a1, const IgemmArgs& a2, int* rows, int max);
 bool igemm_pair_lds_two_per_cu(const IgemmArgs& a1, int rows);  // LDS of the band <= 80 KB
 void launch_igemm_pair(hipStream_t st, const IgemmArgs& a1, const IgemmArgs& a2, int rows);
+// A whole int8 C2f block with one bottleneck (k_igemm_c2f.hip): cv1 (1x1,
+// c1 -> 2c), the bottleneck's two 3x3 convs (c -> c, the second with the
+// shortcut or not) and cv2 (1x1, 3c -> 2c) in one launch, c = 16 or 32,
+// the block's intermediates kept in LDS; R output rows per workgroup.
+bool igemm_c2f_shapes_ok(const IgemmArgs& a0, const IgemmArgs& a1, const IgemmArgs& a2, const IgemmArgs& a3);
+bool igemm_c2f_ok(const IgemmArgs& a0, const IgemmArgs& a1, const IgemmArgs& a2, const IgemmArgs& a3, int rows);
+int igemm_c2f_rows(const IgemmArgs& a0, const IgemmArgs& a1, const IgemmArgs& a2, const IgemmArgs& a3, int* rows,
+                   int max);
+void launch_igemm_c2f(hipStream_t st, const IgemmArgs& a0, const IgemmArgs& a1, const IgemmArgs& a2,
+                      const IgemmArgs& a3, int rows);
 // Returns the tile name chosen for a problem (for launch descriptions).
 const char* igemm_tile_name(const IgemmArgs& a, int esize);
 // Channel-tile width used for `cout` output channels; packed weights must

@@ -231,6 +231,7 @@ struct Runtime {
   void tag_group(const Group& gr, size_t first, int gid);
   void plan_streams(int n);
   float time_graph();
+  void fuse_c2f();
   void enqueue(hipStream_t st);
   void run();
 };
@@ -400,6 +401,7 @@ void Runtime::build(Backend* b, const GraphIR& graph, bool stats_mode) {
   }
   if (!stats) {
     autotune();
+    fuse_c2f();
     fuse_pairs();
     fuse_heads();
   }
@@ -2144,6 +2146,107 @@ void Runtime::fuse_pairs() {
   }
   (void)hipEventDestroy(e0);
   (void)hipEventDestroy(e1);
+}
+
+// A C2f block with one bottleneck (cv1, m.cv1, m.cv2, cv2: four
+// consecutive QLinearConv launches over the block's concat buffer) in one
+// launch (igemm_c2f.h), when nothing else reads or writes the storage of
+// the block's intermediates (y, t, z and their concat) and none of it is a
+// graph output.  Timed over its band heights against the four tuned
+// launches and kept only if faster; DW_C2F=1 keeps every candidate, =0
+// none; DW_C2F_KEEP=<op,op,..> keeps exactly the blocks whose cv1 is
+// listed, DW_C2F_ROWS=<r> forces a band height.
+void Runtime::fuse_c2f() {
+  const char* env = getenv("DW_C2F");
+  if (env && env[0] == '0') return;
+  const char* keep = getenv("DW_C2F_KEEP");
+  const bool force = (env && env[0] == '1') || keep;
+  const char* tune_env = getenv("DW_AUTOTUNE");
+  const bool tuned = !((tune_env && tune_env[0] == '0') || getenv("DW_IGEMM_TILE"));
+  if (!force && !tuned) return;
+  FILE* log = nullptr;
+  if (const char* lp = getenv("DW_AUTOTUNE_LOG")) log = fopen(lp, "a");
+  hipStream_t st = be->stream;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  DW_HIP(hipEventCreate(&e0));
+  DW_HIP(hipEventCreate(&e1));
+  for (size_t i = 0; i + 3 < launches.size(); ++i) {
+    Launch* Ls[4] = {&launches[i], &launches[i + 1], &launches[i + 2], &launches[i + 3]};
+    bool ok = true;
+    for (Launch* L : Ls) ok = ok && L->ig && L->esize == 1;
+    if (!ok || !igemm_c2f_shapes_ok(*Ls[0]->ig, *Ls[1]->ig, *Ls[2]->ig, *Ls[3]->ig)) continue;
+    // the intermediates' storage roots: written by cv1, m.cv1 and m.cv2
+    std::set<int> roots;
+    for (int k = 0; k < 3; ++k)
+      for (const Region& r : Ls[k]->writes) roots.insert(r.rid);
+    for (size_t j = 0; j < launches.size() && ok; ++j) {
+      if (j >= i && j < i + 4) continue;
+      for (const Region& r : launches[j].reads) ok = ok && !roots.count(r.rid);
+      for (const Region& r : launches[j].writes) ok = ok && !roots.count(r.rid);
+    }
+    for (const std::string& o : g.outputs) ok = ok && !roots.count(T(o).rid);
+    if (!ok) continue;
+    if (keep && !listed(keep, Ls[0]->op)) continue;
+    const IgemmArgs &a0 = *Ls[0]->ig, &a1 = *Ls[1]->ig, &a2 = *Ls[2]->ig, &a3 = *Ls[3]->ig;
+    int cand[16];
+    const int nc = igemm_c2f_rows(a0, a1, a2, a3, cand, 16);
+    if (nc == 0) continue;
+    int rows = cand[0];
+    if (tuned) {
+      float sum = 0;
+      for (Launch* L : Ls) sum += L->tuned_ms;
+      float best = 1e30f;
+      for (int k = 0; k < nc; ++k) {
+        launch_igemm_c2f(st, a0, a1, a2, a3, cand[k]);
+        float t_min = 1e30f;
+        for (int r = 0; r < 3; ++r) {
+          DW_HIP(hipEventRecord(e0, st));
+          for (int q = 0; q < 4; ++q) launch_igemm_c2f(st, a0, a1, a2, a3, cand[k]);
+          DW_HIP(hipEventRecord(e1, st));
+          DW_HIP(hipEventSynchronize(e1));
+          float ms = 0;
+          DW_HIP(hipEventElapsedTime(&ms, e0, e1));
+          t_min = std::min(t_min, ms);
+        }
+        if (log) fprintf(log, "%s\tigemm_i8_c2f_c%d_r%d\t%.2f\n", Ls[0]->op.c_str(), a1.cin, cand[k], t_min * 1e3f / 4);
+        if (t_min < best) {
+          best = t_min;
+          rows = cand[k];
+        }
+      }
+      if (log) fprintf(log, "%s\tfour launches\t%.2f\n", Ls[0]->op.c_str(), sum * 1e3f / 4);
+      bool timed = true;
+      for (Launch* L : Ls) timed = timed && L->tuned_ms > 0;
+      if (!force && (!timed || best >= sum)) continue;
+    }
+    if (const char* fr = getenv("DW_C2F_ROWS")) {
+      const int r = atoi(fr);
+      if (igemm_c2f_ok(a0, a1, a2, a3, r)) rows = r;
+    }
+    Launch F;
+    F.kernel = "igemm_i8_c2f_c" + std::to_string(a1.cin);
+    F.op = Ls[0]->op + "+" + Ls[1]->op + "+" + Ls[2]->op + "+" + Ls[3]->op;
+    F.work = 0;
+    for (Launch* L : Ls) F.work += L->work;
+    // x in, the block output out, the four weight sets
+    F.bytes = (double)a0.m * (a0.cin + a3.cout);
+    for (const IgemmArgs* a : {&a0, &a1, &a2, &a3}) F.bytes += (double)a->ksteps * a->cout_pad * 64;
+    auto p0 = Ls[0]->ig, p1 = Ls[1]->ig, p2 = Ls[2]->ig, p3 = Ls[3]->ig;
+    F.fn = [p0, p1, p2, p3, rows](hipStream_t s) { launch_igemm_c2f(s, *p0, *p1, *p2, *p3, rows); };
+    F.esize = 1;
+    F.group = Ls[0]->group;
+    for (Launch* L : Ls) {
+      F.reads.insert(F.reads.end(), L->reads.begin(), L->reads.end());
+      F.writes.insert(F.writes.end(), L->writes.begin(), L->writes.end());
+    }
+    F.t_in = Ls[0]->t_in;
+    F.t_out = Ls[3]->t_out;
+    launches[i] = F;
+    launches.erase(launches.begin() + (long)i + 1, launches.begin() + (long)i + 4);
+  }
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  if (log) fclose(log);
 }
 
 // A detect head's u8 -> f16 1x1 conv (conv1x1_u8_f16) fused into the

@@ -286,6 +286,52 @@ def test_int8_graph_band_tiles_bit_exact(backend, monkeypatch, tile):
         np.testing.assert_array_equal(gv, ref[o], err_msg=f"{o} tile {tile}")
 
 
+@pytest.mark.parametrize("rows", [None, "1", "2", "5"])
+def test_int8_graph_c2f_bit_exact(backend, monkeypatch, rows):
+    # 320x320 input: the one-bottleneck C2f blocks with 16 or 32 hidden
+    # channels (b2 at 80x80 with the shortcut, the neck's P3 block at 40x40
+    # without) each in one launch, the block's intermediates in LDS; the
+    # tuner's band height and forced small ones (bands of 1 and 2 rows: the
+    # halo rows reach past the band's neighbours), exact plan: every output
+    # bit-exact against the oracle.
+    g, info = yolo.int8_graph(backend, batch=1, size=320, calib=yolo.calibration_images(4, 320))
+    monkeypatch.setenv("DW_C2F", "1")
+    monkeypatch.setenv("DW_PAIR", "0")
+    if rows:
+        monkeypatch.setenv("DW_C2F_ROWS", rows)
+    x = yolo.input_images(1, 320)
+    rt = HipGraphRuntime(g, backend, exact_u8_f16=True)
+    fused = [L["ops"].split("+")[0] for L in rt.launches() if L["kernel"].startswith("igemm_i8_c2f")]
+    print(f"rows {rows}: fused C2f blocks {fused}", flush=True)
+    assert {"b2.cv1", "n15.cv1"} <= set(fused), fused
+    rt.set_input_f32(info["input"], x)
+    rt.run()
+    got = gpu_outputs(rt, info)
+    ref = oracle_run(g, {info["input"]: synth.f16_bits(x)})
+    for o, gv in zip(info["outputs"], got):
+        np.testing.assert_array_equal(gv, ref[o], err_msg=f"{o} rows {rows}")
+
+
+def test_int8_benchmark_graph_c2f_same_bytes(backend, monkeypatch):
+    # The benchmark's batch-32 640x640 graph with its one-bottleneck C2f
+    # blocks fused (DW_C2F=1) and not (DW_C2F=0): the same bytes.
+    from dragonwing_edge_rs_amd import workloads
+    g, _, _, _, info = workloads.yolov8n_int8(backend)
+    x = yolo.input_images(32, 640)
+    outs = {}
+    for mode in ("0", "1"):
+        monkeypatch.setenv("DW_C2F", mode)
+        rt = HipGraphRuntime(g, backend)
+        fused = [L["ops"].split("+")[0] for L in rt.launches() if L["kernel"].startswith("igemm_i8_c2f")]
+        print(f"DW_C2F={mode}: fused {fused}", flush=True)
+        assert (len(fused) >= 2) == (mode == "1"), fused
+        rt.set_input_f32(info["input"], x)
+        rt.run()
+        outs[mode] = gpu_outputs(rt, info)
+    for o, a, b in zip(info["outputs"], outs["0"], outs["1"]):
+        np.testing.assert_array_equal(a, b, err_msg=o)
+
+
 @pytest.mark.parametrize("tile", ["64,10,-4", "80,10,-4"])
 def test_int8_graph_band_head_same_bytes(backend, monkeypatch, tile):
     # The detect heads' fused u8 -> f16 1x1 on the band-tile kernel: the same
@@ -452,13 +498,15 @@ def test_int8_graph_launch_plan(backend, int8_small):
     for L in ls:
         kinds[L["kernel"].split("_")[0]] = kinds.get(L["kernel"].split("_")[0], 0) + 1
     # 56 int8 MFMA convs (each with its table / residual fused; two chained
-    # 3x3 convs in one launch where the tuner finds that faster), the fp16
-    # stem as a direct conv, the six fp16 head 1x1 convs on the fp16 matrix
-    # cores (each in its own launch or inside its 3x3's, "_head"), one SPPF
-    # cascade, two resizes, no copies or elementwise.
+    # 3x3 convs in one launch, or a whole one-bottleneck C2f block's four,
+    # where the tuner finds that faster), the fp16 stem as a direct conv,
+    # the six fp16 head 1x1 convs on the fp16 matrix cores (each in its own
+    # launch or inside its 3x3's, "_head"), one SPPF cascade, two resizes, no
+    # copies or elementwise.
     pairs = sum(L["kernel"].startswith("igemm_i8_pair") for L in ls)
+    blocks = sum(L["kernel"].startswith("igemm_i8_c2f") for L in ls)
     heads = sum(L["kernel"].endswith("_head") for L in ls)
-    assert kinds.get("igemm") + pairs == 56, (pairs, kinds)
+    assert kinds.get("igemm") + pairs + 3 * blocks == 56, (pairs, blocks, kinds)
     assert kinds.get("direct") == 1 and kinds.get("conv1x1", 0) + heads == 6, kinds
     assert kinds.get("maxpool") == 1 and kinds.get("resize") == 2, kinds
     assert "copy" not in kinds and "elementwise" not in kinds, kinds
@@ -476,6 +524,7 @@ def test_int8_graph_pairs_bit_exact(backend, monkeypatch):
     g, info = yolo.int8_graph(backend, batch=2, size=320, calib=yolo.calibration_images(4, 320))
     x = yolo.input_images(2, 320)
     monkeypatch.setenv("DW_PAIR", "1")  # every candidate pair, whatever the timing
+    monkeypatch.setenv("DW_C2F", "0")  # the one-bottleneck blocks as pairs too
     rt = HipGraphRuntime(g, backend, exact_u8_f16=True)
     pairs = sorted(L["kernel"] for L in rt.launches() if L["kernel"].startswith("igemm_i8_pair"))
     assert pairs == ["igemm_i8_pair_c16"] + ["igemm_i8_pair_c32"] * 3 + ["igemm_i8_pair_c64"] * 5, pairs
@@ -579,6 +628,7 @@ def check_int8_batch_bit_exact(g, info, x, backend, graph1, monkeypatch):
     pair of chained 3x3 convs in one launch) and compares every image of the
     batch with the oracle's CpuGraph run on the same graph at batch 1."""
     monkeypatch.setenv("DW_PAIR", "1")
+    monkeypatch.setenv("DW_C2F", "0")  # the one-bottleneck blocks as pairs too
     rt = HipGraphRuntime(g, backend, exact_u8_f16=True)
     # the eight C2f bottlenecks of 16, 32 and 64 channels (with and without
     # the shortcut) and the stride-8 head's first two box convs run as
