@@ -211,8 +211,9 @@ __global__ __launch_bounds__(kC2fThreads) void igemm_c2f_kernel(const C2fArgs p)
     const int np = (rhi - rlo) * W;
     const int nb = (np + 15) / 16;
     const uint8_t* const wl = smem + L.w[0] + lane * 16;
-    // a chunk's pixels: x offset (-1: none), Y1 pixel, Y1 row, column
-    auto setup = [&](int b0, int (&goff)[PBC0], int (&tpix)[PBC0], int (&trow)[PBC0], int (&col)[PBC0]) {
+    // a chunk's pixels: x offset, and the byte offsets of their y1 in Y1
+    // and (rows of the band only) y0 in Y0 (-1: none)
+    auto setup = [&](int b0, int (&goff)[PBC0], int (&o1)[PBC0], int (&o0)[PBC0]) {
 #pragma unroll
       for (int pb = 0; pb < PBC0; ++pb) {
         const int pl = (b0 + pb) * 16 + (lane & 15);
@@ -222,9 +223,8 @@ __global__ __launch_bounds__(kC2fThreads) void igemm_c2f_kernel(const C2fArgs p)
         const int tr = rlo + r;
         const int ih = r0 - 2 + tr;
         goff[pb] = v ? ((n * H + ih) * W + c) * a0.x_pix_stride + a0.x_c_off : -1;
-        tpix[pb] = v ? tr * TW + c + 1 : -1;
-        trow[pb] = tr;
-        col[pb] = c;
+        o1[pb] = v ? (tr * TW + c + 1) * SU * 16 + cq : -1;
+        o0[pb] = (v && (unsigned)(tr - 2) < (unsigned)R) ? ((tr - 2) * W + c) * C + cq : -1;
       }
     };
     // its operand rows: this lane's 16 bytes of every k-step (none past c1
@@ -241,15 +241,15 @@ __global__ __launch_bounds__(kC2fThreads) void igemm_c2f_kernel(const C2fArgs p)
       }
     };
     const int stride = kC2fWaves * PBC0;
-    int goff[PBC0], tpix[PBC0], trow[PBC0], col[PBC0];
+    int goff[PBC0], o1[PBC0], o0[PBC0];
     u32x4 bq[KS0][PBC0];
-    setup(wave * PBC0, goff, tpix, trow, col);
+    setup(wave * PBC0, goff, o1, o0);
     issue(goff, bq);
     for (int b0 = wave * PBC0; b0 < nb; b0 += stride) {
       // the next chunk's loads, in flight during this chunk's work
-      int goff_n[PBC0], tpix_n[PBC0], trow_n[PBC0], col_n[PBC0];
+      int goff_n[PBC0], o1_n[PBC0], o0_n[PBC0];
       u32x4 bq_n[KS0][PBC0];
-      setup(b0 + stride, goff_n, tpix_n, trow_n, col_n);
+      setup(b0 + stride, goff_n, o1_n, o0_n);
       issue(goff_n, bq_n);
       v4i acc[CBA][PBC0];
 #pragma unroll
@@ -279,28 +279,25 @@ __global__ __launch_bounds__(kC2fThreads) void igemm_c2f_kernel(const C2fArgs p)
         const float ms4[4] = {m4.x, m4.y, m4.z, m4.w};
 #pragma unroll
         for (int pb = 0; pb < PBC0; ++pb) {
-          if (tpix[pb] < 0) continue;
+          const int o = cb < CB ? o0[pb] : o1[pb];  // y0 only for the band's own rows
+          if (o < 0) continue;
           uint32_t out = 0;
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int qb = requant_bits(acc[cb][pb][r], ms4[r], qlo, qhi);
             out |= (uint32_t)lut3[(uint32_t)qb - (uint32_t)qbase] << (8 * r);
           }
-          if (cb < CB) {
-            const int rr = trow[pb] - 2;
-            if ((unsigned)rr < (unsigned)R)
-              *reinterpret_cast<uint32_t*>(s_y0 + (rr * W + col[pb]) * C + cb * 16 + cq) = out ^ a3.xxor;
-          } else {
-            *reinterpret_cast<uint32_t*>(s_y1 + tpix[pb] * SU * 16 + (cb - CB) * 16 + cq) = out ^ a1.xxor;
-          }
+          if (cb < CB)
+            *reinterpret_cast<uint32_t*>(s_y0 + o + cb * 16) = out ^ a3.xxor;
+          else
+            *reinterpret_cast<uint32_t*>(s_y1 + o + (cb - CB) * 16) = out ^ a1.xxor;
         }
       }
 #pragma unroll
       for (int pb = 0; pb < PBC0; ++pb) {
         goff[pb] = goff_n[pb];
-        tpix[pb] = tpix_n[pb];
-        trow[pb] = trow_n[pb];
-        col[pb] = col_n[pb];
+        o1[pb] = o1_n[pb];
+        o0[pb] = o0_n[pb];
 #pragma unroll
         for (int q = 0; q < KS0; ++q) bq[q][pb] = bq_n[q][pb];
       }
@@ -401,13 +398,18 @@ __global__ __launch_bounds__(kC2fThreads) void igemm_c2f_kernel(const C2fArgs p)
     uint8_t* const zrow = smem + L.zr + (wave * 16 + (lane & 15)) * ZROW;
     const uint8_t* const wdl = smem + L.w[3] + lane * 16;  // cv2's weight fragments
     for (int b0 = wave * PBC; b0 < nb; b0 += kC2fWaves * PBC) {
-      int pbase[PBC];
+      // per block: the window in T, the pixel in Y1 and in Y0, the output
+      // pixel (-1: none)
+      int pbase[PBC], y1c[PBC], y0c[PBC], pix[PBC];
 #pragma unroll
       for (int pb = 0; pb < PBC; ++pb) {
         const int pl = (b0 + pb) * 16 + (lane & 15);
         const int q = pl < np ? pl : 0;
         const int r = div_small(q, W, a1.r_wo), c = q - r * W;
         pbase[pb] = (r * TW + c) * SU * 16;
+        y1c[pb] = ((r + 2) * TW + c + 1) * SU * 16;
+        y0c[pb] = (r * W + c) * C;
+        pix[pb] = pl < np ? (n * H + r0 + r) * W + c : -1;
       }
       v4i acc[CB][PBC];
 #pragma unroll
@@ -420,11 +422,6 @@ __global__ __launch_bounds__(kC2fThreads) void igemm_c2f_kernel(const C2fArgs p)
 #pragma unroll
       for (int pb = 0; pb < PBC; ++pb) {
         if (b0 + pb >= nb) break;  // wave-uniform
-        const int pl = (b0 + pb) * 16 + (lane & 15);
-        const bool pv = pl < np;
-        const int q = pv ? pl : 0;
-        const int r = div_small(q, W, a1.r_wo), c = q - r * W;
-        const int y1c = ((r + 2) * TW + c + 1) * SU * 16;  // the pixel in Y1
         asm volatile("" ::: "memory");  // the previous block's reads of the z rows are issued
         // z: requantize, table, the shortcut's QLinearAdd of y1; to this
         // wave's rows in cv2's operand form
@@ -433,7 +430,7 @@ __global__ __launch_bounds__(kC2fThreads) void igemm_c2f_kernel(const C2fArgs p)
           const float4 m4 = *reinterpret_cast<const float4*>(e2 + 256 + 4 * C + 4 * (cb * 16 + cq));
           const float ms4[4] = {m4.x, m4.y, m4.z, m4.w};
           uint32_t rres = 0;
-          if constexpr (RES) rres = *reinterpret_cast<const uint32_t*>(s_y1 + y1c + cb * 16 + cq) ^ a1.xxor;
+          if constexpr (RES) rres = *reinterpret_cast<const uint32_t*>(s_y1 + y1c[pb] + cb * 16 + cq) ^ a1.xxor;
           uint32_t out = 0;
 #pragma unroll
           for (int rr = 0; rr < 4; ++rr) {
@@ -445,21 +442,20 @@ __global__ __launch_bounds__(kC2fThreads) void igemm_c2f_kernel(const C2fArgs p)
           *reinterpret_cast<uint32_t*>(zrow + cb * 16 + cq) = out ^ a3.xxor;
         }
         asm volatile("" ::: "memory");  // one wave's LDS operations run in order
-        // cv2's operand: 16 bytes of concat(y0, y1, z) per lane and k-step
+        // cv2's operand: 16 bytes of concat(y0, y1, z) per lane and k-step,
+        // one read from whichever holds them (past 3c: any bytes, their
+        // weights are zero)
         v4i xd[KD];
 #pragma unroll
         for (int q2 = 0; q2 < KD; ++q2) {
           const int kb = q2 * 64 + (lane >> 4) * 16;
-          v4i v = v4i{0, 0, 0, 0};
-          if (kb < C)
-            v = *reinterpret_cast<const v4i*>(s_y0 + (r * W + c) * C + kb);
-          else if (kb < 2 * C)
-            v = *reinterpret_cast<const v4i*>(s_y1 + y1c + (kb - C));
-          else if (kb < 3 * C)
-            v = *reinterpret_cast<const v4i*>(zrow + (kb - 2 * C));
-          xd[q2] = v;
+          const uint8_t* src = kb < C ? s_y0 + y0c[pb] + kb
+                               : kb < 2 * C ? s_y1 + y1c[pb] + (kb - C)
+                                            : zrow + (kb < 3 * C ? kb - 2 * C : 0);
+          xd[q2] = *reinterpret_cast<const v4i*>(src);
         }
-        uint8_t* const yrow = (uint8_t*)a3.y + (size_t)((n * H + r0 + r) * W + c) * a3.y_pix_stride + a3.y_c_off;
+        const bool pv = pix[pb] >= 0;
+        uint8_t* const yrow = (uint8_t*)a3.y + (size_t)(pv ? pix[pb] : 0) * a3.y_pix_stride + a3.y_c_off;
 #pragma unroll
         for (int cb = 0; cb < CBD; ++cb) {
           v4i acc2 = *reinterpret_cast<const v4i*>(e3 + 256 + 4 * (cb * 16 + cq));
