@@ -45,8 +45,12 @@ constexpr int kBandWaves = 8;
 constexpr int kBandThreads = 64 * kBandWaves;
 constexpr int kBandFill = 16;  // input units each thread loads at start-up (at most)
 
-// 16-pixel blocks per chunk (accumulators CB x PBC)
-__host__ __device__ constexpr int band_pbc(int cb) { return cb <= 2 ? 8 : (cb <= 5 ? 4 : 2); }
+// 16-pixel blocks per chunk (accumulators CB x PBC): for 64-channel tiles
+// a wave's whole range (6 or 7 blocks on the large maps) in one pass of the
+// k-loop; 80-channel tiles measured fastest at 4 (6 was slower, 7 spills)
+__host__ __device__ constexpr int band_pbc(int cb) {
+  return cb <= 2 ? 8 : (cb <= 4 ? 7 : (cb == 5 ? 4 : 2));
+}
 __host__ __device__ constexpr int band_su(int cu) { return cu | 1; }
 __host__ __device__ constexpr int band_tab_off(int bc) { return 256 + 8 * bc; }
 __host__ __device__ constexpr int band_w_off(int bc, int ks) { return (band_tab_off(bc) + ks * 16 + 15) / 16 * 16; }
