@@ -368,7 +368,9 @@ __device__ __forceinline__ void igemm_store(const IgemmArgs& a, const EpiLds& ep
   } else if constexpr (FAST) {
     const bool full = c0 + BC <= a.cout;
     const bool wide = CB >= 2 && xp != nullptr && full && (a.y_pix_stride & 15) == 0 &&
-                      ((a.y_c_off + c0) & 15) == 0 && (((uintptr_t)a.y) & 15) == 0;
+                      ((a.y_c_off + c0) & 15) == 0 && (((uintptr_t)a.y) & 15) == 0 &&
+                      (!a.y_up || ((a.up_pix_stride & 15) == 0 && ((a.up_c_off + c0) & 15) == 0 &&
+                                   (((uintptr_t)a.y_up) & 15) == 0));
     uint8_t* const xrow = wide ? xp + (lane & 15) * xpose_row(BC) : nullptr;
     const int qbase = 0x4B400000 - a.y_zp;
     const float qlo = 12582912.0f - (float)a.y_zp, qhi = qlo + 255.0f;
@@ -381,6 +383,17 @@ __device__ __forceinline__ void igemm_store(const IgemmArgs& a, const EpiLds& ep
       const int p = p0 + pb * 16 + (lane & 15);
       if (p >= plim) continue;
       uint8_t* yrow = (uint8_t*)a.y + (size_t)p * a.y_pix_stride + a.y_c_off + c0 + cq;
+      // the pixel's top-left pixel in the upsampled view, if any
+      size_t up = 0;
+      if (a.y_up) {
+        const int hw = a.ho * a.wo;
+        const int nn = div_small(p, hw, a.r_hwo);
+        const int r = p - nn * hw;
+        const int oh = div_small(r, a.wo, a.r_wo);
+        const int ow = r - oh * a.wo;
+        up = ((size_t)(nn * 2 * a.ho + 2 * oh) * (2 * a.wo) + 2 * ow) * a.up_pix_stride + a.up_c_off + c0;
+      }
+      const size_t upr = (size_t)2 * a.wo * a.up_pix_stride;  // one upsampled row
       uint32_t rres[CB];
       if constexpr (EPV == EPV_QU8_LUT_RES) {
         const uint8_t* rrow = (const uint8_t*)a.res + (size_t)p * a.r_pix_stride + a.r_c_off + c0 + cq;
@@ -405,10 +418,18 @@ __device__ __forceinline__ void igemm_store(const IgemmArgs& a, const EpiLds& ep
           if constexpr (EPV == EPV_QU8_LUT_RES) qi = qadd_u8(qi, (rres[cb] >> (8 * r)) & 0xff, a);
           out |= (uint32_t)qi << (8 * r);
         }
-        if (wide)
+        if (wide) {
           *reinterpret_cast<uint32_t*>(xrow + cb * 16 + cq) = out;
-        else
+        } else {
           *reinterpret_cast<uint32_t*>(yrow + cb * 16) = out;
+          if (a.y_up) {
+            uint8_t* u = (uint8_t*)a.y_up + up + cb * 16 + cq;
+            *reinterpret_cast<uint32_t*>(u) = out;
+            *reinterpret_cast<uint32_t*>(u + a.up_pix_stride) = out;
+            *reinterpret_cast<uint32_t*>(u + upr) = out;
+            *reinterpret_cast<uint32_t*>(u + upr + a.up_pix_stride) = out;
+          }
+        }
       }
       if (wide) {
         // the pixel's 4 lanes wrote its BC channels; lane g now stores
@@ -418,8 +439,17 @@ __device__ __forceinline__ void igemm_store(const IgemmArgs& a, const EpiLds& ep
 #pragma unroll
         for (int i = 0; i < (CB + 3) / 4; ++i) {
           const int cb = 4 * i + (lane >> 4);
-          if (cb < CB)
-            *reinterpret_cast<uint4*>(ydst + cb * 16) = *reinterpret_cast<const uint4*>(xrow + cb * 16);
+          if (cb < CB) {
+            const uint4 v = *reinterpret_cast<const uint4*>(xrow + cb * 16);
+            *reinterpret_cast<uint4*>(ydst + cb * 16) = v;
+            if (a.y_up) {
+              uint8_t* u = (uint8_t*)a.y_up + up + cb * 16;
+              *reinterpret_cast<uint4*>(u) = v;
+              *reinterpret_cast<uint4*>(u + a.up_pix_stride) = v;
+              *reinterpret_cast<uint4*>(u + upr) = v;
+              *reinterpret_cast<uint4*>(u + upr + a.up_pix_stride) = v;
+            }
+          }
         }
       }
     }

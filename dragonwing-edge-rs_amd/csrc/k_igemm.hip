@@ -192,7 +192,18 @@ bool head_tile_ok(const IgemmArgs& a, const TileCfg& t) {
 // (16 * pb pixels per wave) that still gives about two workgroups per CU.
 // The weight slice of the channel tile is staged in chunks of at most
 // kWeightLds bytes.
+TileCfg pick_any(const IgemmArgs& a);
+
+// A launch that also writes an upsampled copy (a.y_up) takes any tile whose
+// epilogue is igemm_store's; the persistent small-K kernel's is its own, so
+// its tiles become the staged kernel's of the same shape.
 TileCfg pick(const IgemmArgs& a) {
+  TileCfg t = pick_any(a);
+  if (a.y_up && t.tpw > 0) t = make_tile(a, t.bc, t.pb);
+  return t;
+}
+
+TileCfg pick_any(const IgemmArgs& a) {
   if (a.h_wfrag) {
     // a DW_IGEMM_TILE row- or band-tile override, else the tuner's choice
     // when it is a head tile, else the staged kernel with the widest pixel
@@ -354,6 +365,7 @@ const char* igemm_tile_name(const IgemmArgs& a, int esize) {
   else
     snprintf(buf, sizeof buf, "igemm_%s_c%d_p%d", esize == 1 ? "i8" : "f16", t.bc, 64 * t.pb);
   if (a.h_wfrag) strncat(buf, "_head", sizeof buf - strlen(buf) - 1);
+  if (a.y_up) strncat(buf, "_up", sizeof buf - strlen(buf) - 1);
   return buf;
 }
 
@@ -389,6 +401,9 @@ void launch_igemm(hipStream_t st, const IgemmArgs& a_in, int esize) {
   a.r_bytes = (int)rb;
   a.tile_tpw = t.tpw;
   a.band_rows = t.tpw == -4 ? t.pb : 0;
+  if (a.y_up && (esize != 1 || a.epi != EPI_QU8 || a.h_wfrag || (a.res && !a.lut) || a.up_pix_stride % 4 != 0 ||
+                 a.up_c_off % 4 != 0))
+    fail(-2, "igemm: an upsampled copy needs a u8 table or requantize epilogue and 4-byte aligned views");
   bool ok;
   if (esize == 1 && a.h_wfrag) {
     if (a.epi != EPI_QU8 || !a.lut || a.res || !head_tile_ok(a, t))

@@ -81,6 +81,10 @@ struct Launch {
   // can be switched to the NCHW f32 loader after the list is built
   std::shared_ptr<DirectArgs> da;
   std::shared_ptr<StemF16Args> sa;  // the same for the fp16 MFMA stem
+  // nearest-resize launches: their arguments and element type, so the pass
+  // that folds a 2x upsample into its producer can find them
+  std::shared_ptr<ResizeArgs> ra;
+  int rdtype = 0;
   // band-tile depthwise launches: their output rows per band, chosen by the tuner
   std::shared_ptr<int> dw_band;  // units * 100 + band rows
   std::shared_ptr<DwArgs> dwa;
@@ -232,6 +236,7 @@ struct Runtime {
   void plan_streams(int n);
   float time_graph();
   void fuse_c2f();
+  void fuse_resize();
   void enqueue(hipStream_t st);
   void run();
 };
@@ -404,6 +409,7 @@ void Runtime::build(Backend* b, const GraphIR& graph, bool stats_mode) {
     fuse_c2f();
     fuse_pairs();
     fuse_heads();
+    fuse_resize();
   }
   // streams: the schedule over 4 streams, or one stream, whichever runs the
   // whole graph faster (the cross-stream waits cost more than the overlap
@@ -1326,7 +1332,11 @@ void Runtime::emit(const Group& gr) {
     L.kernel = "resize_nearest";
     L.op = op.name;
     L.bytes = (double)x.bytes() + y.bytes();
-    L.fn = [=](hipStream_t st) { launch_resize_nearest(st, a, dt); };
+    L.ra = std::make_shared<ResizeArgs>(a);
+    L.rdtype = dt;
+    L.t_in = op.in[0];
+    L.t_out = op.out[0];
+    L.fn = [ra = L.ra, dt](hipStream_t st) { launch_resize_nearest(st, *ra, dt); };
     launches.push_back(L);
     return;
   }
@@ -2247,6 +2257,89 @@ void Runtime::fuse_c2f() {
   (void)hipEventDestroy(e0);
   (void)hipEventDestroy(e1);
   if (log) fclose(log);
+}
+
+// A nearest 2x upsample (resize) of a u8 tensor folded into the implicit
+// GEMM that writes that tensor: its epilogue stores every output pixel's
+// bytes at the pixel's four pixels of the resize's output view as well
+// (igemm_store, IgemmArgs::y_up), and the resize's launch goes.  The bytes
+// are the resize's.  Timed against the two launches and kept only if
+// faster; DW_RESIZE_FUSE=1 keeps every candidate, =0 none;
+// DW_RESIZE_KEEP=<op,op,..> keeps exactly the listed resizes.
+void Runtime::fuse_resize() {
+  const char* env = getenv("DW_RESIZE_FUSE");
+  if (env && env[0] == '0') return;
+  const char* keep = getenv("DW_RESIZE_KEEP");
+  const bool force = (env && env[0] == '1') || keep;
+  const char* tune_env = getenv("DW_AUTOTUNE");
+  const bool tuned = !((tune_env && tune_env[0] == '0') || getenv("DW_IGEMM_TILE"));
+  if (!force && !tuned) return;
+  hipStream_t st = be->stream;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  DW_HIP(hipEventCreate(&e0));
+  DW_HIP(hipEventCreate(&e1));
+  auto time4 = [&](const std::function<void(hipStream_t)>& fn) {
+    fn(st);
+    float t_min = 1e30f;
+    for (int r = 0; r < 3; ++r) {
+      DW_HIP(hipEventRecord(e0, st));
+      for (int k = 0; k < 4; ++k) fn(st);
+      DW_HIP(hipEventRecord(e1, st));
+      DW_HIP(hipEventSynchronize(e1));
+      float ms = 0;
+      DW_HIP(hipEventElapsedTime(&ms, e0, e1));
+      t_min = std::min(t_min, ms);
+    }
+    return t_min;
+  };
+  for (size_t j = 0; j < launches.size(); ++j) {
+    Launch& R = launches[j];
+    if (!R.ra || R.rdtype != U8) continue;
+    if (keep && !listed(keep, R.op)) continue;
+    const ResizeArgs& ra = *R.ra;
+    if (ra.ho != 2 * ra.h || ra.wo != 2 * ra.w || ra.y.pix_stride % 4 != 0 || ra.y.c_off % 4 != 0) continue;
+    // the launch that writes the resize's input
+    int pi = -1;
+    for (int i = (int)j - 1; i >= 0 && pi < 0; --i)
+      if (launches[i].t_out == R.t_in) pi = i;
+    if (pi < 0) continue;
+    Launch& L = launches[pi];
+    if (!L.ig || L.esize != 1) continue;
+    const IgemmArgs& a = *L.ig;
+    if (a.epi != EPI_QU8 || a.h_wfrag || (a.res && !a.lut) || a.y_up) continue;
+    if (a.y != ra.x.base || a.y_pix_stride != ra.x.pix_stride || a.y_c_off != ra.x.c_off || a.cout != ra.c ||
+        a.n != ra.n || a.ho != ra.h || a.wo != ra.w)
+      continue;
+    // the upsample is now written at the producer's place in the list: no
+    // launch in between may touch its storage (arena bytes shared with a
+    // tensor still in use there)
+    bool clear = true;
+    for (int k = pi + 1; k < (int)j && clear; ++k)
+      for (const Region& w : R.writes) {
+        for (const Region& r : launches[k].reads) clear = clear && !w.overlaps(r);
+        for (const Region& r : launches[k].writes) clear = clear && !w.overlaps(r);
+      }
+    if (!clear) continue;
+    IgemmArgs f = a;
+    f.y_up = ra.y.base;
+    f.up_pix_stride = ra.y.pix_stride;
+    f.up_c_off = ra.y.c_off;
+    if (tuned) {
+      const float both = time4([&a](hipStream_t s) { launch_igemm(s, a, 1); }) + time4(R.fn);
+      const float one = time4([&f](hipStream_t s) { launch_igemm(s, f, 1); });
+      if (!force && one >= both) continue;
+    }
+    *L.ig = f;
+    L.kernel = igemm_tile_name(f, 1);
+    L.op += "+" + R.op;
+    L.bytes += (double)R.bytes - (double)ra.n * ra.h * ra.w * ra.c;  // the resize's read goes
+    L.writes.insert(L.writes.end(), R.writes.begin(), R.writes.end());
+    L.tuned_ms = 0;
+    launches.erase(launches.begin() + (long)j);
+    --j;
+  }
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
 }
 
 // A detect head's u8 -> f16 1x1 conv (conv1x1_u8_f16) fused into the

@@ -332,6 +332,51 @@ def test_int8_benchmark_graph_c2f_same_bytes(backend, monkeypatch):
         np.testing.assert_array_equal(a, b, err_msg=o)
 
 
+@pytest.mark.parametrize("tile", [None, "64,4", "32,4,-2"])
+def test_int8_graph_resize_fused_bit_exact(backend, monkeypatch, tile):
+    # 320x320 input: the neck's two nearest 2x upsamples written by the
+    # epilogues of the convs that produce their inputs (the upsampled bytes
+    # stored at each output pixel's four pixels of the concat slice), with
+    # the tuner's tiles and forced staged / row tiles; exact plan, every
+    # output bit-exact against the oracle.
+    g, info = yolo.int8_graph(backend, batch=1, size=320, calib=yolo.calibration_images(4, 320))
+    monkeypatch.setenv("DW_RESIZE_FUSE", "1")
+    if tile:
+        monkeypatch.setenv("DW_IGEMM_TILE", tile)
+    x = yolo.input_images(1, 320)
+    rt = HipGraphRuntime(g, backend, exact_u8_f16=True)
+    ks = [L["kernel"] for L in rt.launches()]
+    print(f"tile {tile}: resize launches {ks.count('resize_nearest')}", flush=True)
+    assert "resize_nearest" not in ks, ks
+    rt.set_input_f32(info["input"], x)
+    rt.run()
+    got = gpu_outputs(rt, info)
+    ref = oracle_run(g, {info["input"]: synth.f16_bits(x)})
+    for o, gv in zip(info["outputs"], got):
+        np.testing.assert_array_equal(gv, ref[o], err_msg=f"{o} tile {tile}")
+
+
+def test_int8_benchmark_graph_resize_fused_same_bytes(backend, monkeypatch):
+    # The benchmark's batch-32 640x640 graph with its upsamples folded into
+    # their producers (DW_RESIZE_FUSE=1) and as separate launches (=0): the
+    # same bytes.
+    from dragonwing_edge_rs_amd import workloads
+    g, _, _, _, info = workloads.yolov8n_int8(backend)
+    x = yolo.input_images(32, 640)
+    outs = {}
+    for mode in ("0", "1"):
+        monkeypatch.setenv("DW_RESIZE_FUSE", mode)
+        rt = HipGraphRuntime(g, backend)
+        n = sum(L["kernel"] == "resize_nearest" for L in rt.launches())
+        print(f"DW_RESIZE_FUSE={mode}: {n} resize launches", flush=True)
+        assert n == (2 if mode == "0" else 0), n
+        rt.set_input_f32(info["input"], x)
+        rt.run()
+        outs[mode] = gpu_outputs(rt, info)
+    for o, a, b in zip(info["outputs"], outs["0"], outs["1"]):
+        np.testing.assert_array_equal(a, b, err_msg=o)
+
+
 @pytest.mark.parametrize("tile", ["64,10,-4", "80,10,-4"])
 def test_int8_graph_band_head_same_bytes(backend, monkeypatch, tile):
     # The detect heads' fused u8 -> f16 1x1 on the band-tile kernel: the same
@@ -501,14 +546,16 @@ def test_int8_graph_launch_plan(backend, int8_small):
     # 3x3 convs in one launch, or a whole one-bottleneck C2f block's four,
     # where the tuner finds that faster), the fp16 stem as a direct conv,
     # the six fp16 head 1x1 convs on the fp16 matrix cores (each in its own
-    # launch or inside its 3x3's, "_head"), one SPPF cascade, two resizes, no
+    # launch or inside its 3x3's, "_head"), one SPPF cascade, two resizes
+    # (each in its own launch or written by the conv before it, "_up"), no
     # copies or elementwise.
     pairs = sum(L["kernel"].startswith("igemm_i8_pair") for L in ls)
     blocks = sum(L["kernel"].startswith("igemm_i8_c2f") for L in ls)
     heads = sum(L["kernel"].endswith("_head") for L in ls)
     assert kinds.get("igemm") + pairs + 3 * blocks == 56, (pairs, blocks, kinds)
     assert kinds.get("direct") == 1 and kinds.get("conv1x1", 0) + heads == 6, kinds
-    assert kinds.get("maxpool") == 1 and kinds.get("resize") == 2, kinds
+    ups = sum(L["kernel"].endswith("_up") for L in ls)
+    assert kinds.get("maxpool") == 1 and kinds.get("resize", 0) + ups == 2, kinds
     assert "copy" not in kinds and "elementwise" not in kinds, kinds
     ms = rt.run_profiled()
     assert len(ms) == len(ls) and np.all(ms > 0)
