@@ -84,9 +84,10 @@ struct IgemmArgs {
                            // -3: the wide-tile kernel (c_in % 128 == 0); -4: the band-tile
                            // kernel (tile_pb: its band height in rows)
   int band_rows;           // set by the launcher for the band-tile kernel
-  // EPI_QU8: a nearest 2x upsample of the output written as well (the
-  // resize folded into its producer): every output pixel's bytes also at
-  // its four pixels of this view, (n, 2 ho, 2 wo, cout); null = none
+  // EPI_QU8 (table or plain requantize epilogues) and EPI_F16: a nearest
+  // 2x upsample of the output written as well (the resize folded into its
+  // producer): every output pixel's values also at its four pixels of this
+  // view, (n, 2 ho, 2 wo, cout); null = none
   void* y_up;
   int up_pix_stride, up_c_off;
   int x_bytes;             // set by the launcher: bytes of the input view's buffer (< 2^31)

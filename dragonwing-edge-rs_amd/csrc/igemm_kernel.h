@@ -210,8 +210,23 @@ __device__ __forceinline__ void epilogue4(const IgemmArgs& a, const EpiLds& e, c
       p01 = p01 + __builtin_bit_cast(h16x2, rres.x);
       p23 = p23 + __builtin_bit_cast(h16x2, rres.y);
     }
-    *reinterpret_cast<uint2*>((uint16_t*)a.y + yo) =
-        make_uint2(__builtin_bit_cast(uint32_t, p01), __builtin_bit_cast(uint32_t, p23));
+    const uint2 out = make_uint2(__builtin_bit_cast(uint32_t, p01), __builtin_bit_cast(uint32_t, p23));
+    *reinterpret_cast<uint2*>((uint16_t*)a.y + yo) = out;
+    if (a.y_up) {
+      // the nearest 2x upsample: the same values at the pixel's four pixels
+      const int hw = a.ho * a.wo;
+      const int nn = div_small(p, hw, a.r_hwo);
+      const int r = p - nn * hw;
+      const int oh = div_small(r, a.wo, a.r_wo);
+      const int ow = r - oh * a.wo;
+      uint16_t* u = (uint16_t*)a.y_up +
+                    ((size_t)(nn * 2 * a.ho + 2 * oh) * (2 * a.wo) + 2 * ow) * a.up_pix_stride + a.up_c_off + ch;
+      const size_t upr = (size_t)2 * a.wo * a.up_pix_stride;
+      *reinterpret_cast<uint2*>(u) = out;
+      *reinterpret_cast<uint2*>(u + a.up_pix_stride) = out;
+      *reinterpret_cast<uint2*>(u + upr) = out;
+      *reinterpret_cast<uint2*>(u + upr + a.up_pix_stride) = out;
+    }
   }
 }
 

@@ -401,9 +401,10 @@ void launch_igemm(hipStream_t st, const IgemmArgs& a_in, int esize) {
   a.r_bytes = (int)rb;
   a.tile_tpw = t.tpw;
   a.band_rows = t.tpw == -4 ? t.pb : 0;
-  if (a.y_up && (esize != 1 || a.epi != EPI_QU8 || a.h_wfrag || (a.res && !a.lut) || a.up_pix_stride % 4 != 0 ||
-                 a.up_c_off % 4 != 0))
-    fail(-2, "igemm: an upsampled copy needs a u8 table or requantize epilogue and 4-byte aligned views");
+  if (a.y_up && (esize == 1 ? (a.epi != EPI_QU8 || a.h_wfrag || (a.res && !a.lut) || a.up_pix_stride % 4 != 0 ||
+                                a.up_c_off % 4 != 0)
+                             : (a.epi != EPI_F16 || a.up_pix_stride % 4 != 0 || a.up_c_off % 4 != 0)))
+    fail(-2, "igemm: an upsampled copy needs a u8 table, requantize or f16 epilogue and aligned views");
   bool ok;
   if (esize == 1 && a.h_wfrag) {
     if (a.epi != EPI_QU8 || !a.lut || a.res || !head_tile_ok(a, t))

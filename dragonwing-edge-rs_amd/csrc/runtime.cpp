@@ -1779,6 +1779,8 @@ void Runtime::emit_conv(const Group& gr) {
       L.bytes += r.bytes();
     }
     L.bytes += (double)x.bytes() + W.data.size() + y.pixels() * co * 2.0;
+    L.t_in = gr.in;
+    L.t_out = gr.out;
     DW_HIP(hipStreamSynchronize(be->stream));
     push_igemm(L, a, 2);
     return;
@@ -2259,9 +2261,9 @@ void Runtime::fuse_c2f() {
   if (log) fclose(log);
 }
 
-// A nearest 2x upsample (resize) of a u8 tensor folded into the implicit
-// GEMM that writes that tensor: its epilogue stores every output pixel's
-// bytes at the pixel's four pixels of the resize's output view as well
+// A nearest 2x upsample (resize) of a u8 or f16 tensor folded into the
+// implicit GEMM that writes that tensor: its epilogue stores every output
+// pixel's values at the pixel's four pixels of the resize's output view as well
 // (igemm_store, IgemmArgs::y_up), and the resize's launch goes.  The bytes
 // are the resize's.  Timed against the two launches and kept only if
 // faster; DW_RESIZE_FUSE=1 keeps every candidate, =0 none;
@@ -2294,19 +2296,21 @@ void Runtime::fuse_resize() {
   };
   for (size_t j = 0; j < launches.size(); ++j) {
     Launch& R = launches[j];
-    if (!R.ra || R.rdtype != U8) continue;
+    if (!R.ra || (R.rdtype != U8 && R.rdtype != F16)) continue;
     if (keep && !listed(keep, R.op)) continue;
     const ResizeArgs& ra = *R.ra;
     if (ra.ho != 2 * ra.h || ra.wo != 2 * ra.w || ra.y.pix_stride % 4 != 0 || ra.y.c_off % 4 != 0) continue;
+    const int es = R.rdtype == U8 ? 1 : 2;
     // the launch that writes the resize's input
     int pi = -1;
     for (int i = (int)j - 1; i >= 0 && pi < 0; --i)
       if (launches[i].t_out == R.t_in) pi = i;
     if (pi < 0) continue;
     Launch& L = launches[pi];
-    if (!L.ig || L.esize != 1) continue;
+    if (!L.ig || L.esize != es) continue;
     const IgemmArgs& a = *L.ig;
-    if (a.epi != EPI_QU8 || a.h_wfrag || (a.res && !a.lut) || a.y_up) continue;
+    if (es == 1 ? (a.epi != EPI_QU8 || a.h_wfrag || (a.res && !a.lut)) : a.epi != EPI_F16) continue;
+    if (a.y_up) continue;
     if (a.y != ra.x.base || a.y_pix_stride != ra.x.pix_stride || a.y_c_off != ra.x.c_off || a.cout != ra.c ||
         a.n != ra.n || a.ho != ra.h || a.wo != ra.w)
       continue;
@@ -2325,14 +2329,14 @@ void Runtime::fuse_resize() {
     f.up_pix_stride = ra.y.pix_stride;
     f.up_c_off = ra.y.c_off;
     if (tuned) {
-      const float both = time4([&a](hipStream_t s) { launch_igemm(s, a, 1); }) + time4(R.fn);
-      const float one = time4([&f](hipStream_t s) { launch_igemm(s, f, 1); });
+      const float both = time4([&a, es](hipStream_t s) { launch_igemm(s, a, es); }) + time4(R.fn);
+      const float one = time4([&f, es](hipStream_t s) { launch_igemm(s, f, es); });
       if (!force && one >= both) continue;
     }
     *L.ig = f;
-    L.kernel = igemm_tile_name(f, 1);
+    L.kernel = igemm_tile_name(f, es);
     L.op += "+" + R.op;
-    L.bytes += (double)R.bytes - (double)ra.n * ra.h * ra.w * ra.c;  // the resize's read goes
+    L.bytes += (double)R.bytes - (double)ra.n * ra.h * ra.w * ra.c * es;  // the resize's read goes
     L.writes.insert(L.writes.end(), R.writes.begin(), R.writes.end());
     L.tuned_ms = 0;
     launches.erase(launches.begin() + (long)j);

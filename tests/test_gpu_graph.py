@@ -377,6 +377,27 @@ def test_int8_benchmark_graph_resize_fused_same_bytes(backend, monkeypatch):
         np.testing.assert_array_equal(a, b, err_msg=o)
 
 
+@pytest.mark.parametrize("size,batch", [(320, 1), (640, 32)])
+def test_f16_graph_resize_fused_same_bytes(backend, monkeypatch, size, batch):
+    # The fp16 graph's upsamples written by the epilogues of the convs that
+    # produce their inputs (DW_RESIZE_FUSE=1) and as separate launches (=0):
+    # the same f16 values.
+    g, info = yolo.f16_graph(batch=batch, size=size)
+    x = yolo.input_images(batch, size)
+    outs = {}
+    for mode in ("0", "1"):
+        monkeypatch.setenv("DW_RESIZE_FUSE", mode)
+        rt = HipGraphRuntime(g, backend)
+        n = sum(L["kernel"] == "resize_nearest" for L in rt.launches())
+        print(f"{size} DW_RESIZE_FUSE={mode}: {n} resize launches", flush=True)
+        assert n == (2 if mode == "0" else 0), n
+        rt.set_input_f32(info["input"], x)
+        rt.run()
+        outs[mode] = gpu_outputs(rt, info)
+    for o, a, b in zip(info["outputs"], outs["0"], outs["1"]):
+        np.testing.assert_array_equal(a, b, err_msg=o)
+
+
 @pytest.mark.parametrize("tile", ["64,10,-4", "80,10,-4"])
 def test_int8_graph_band_head_same_bytes(backend, monkeypatch, tile):
     # The detect heads' fused u8 -> f16 1x1 on the band-tile kernel: the same
