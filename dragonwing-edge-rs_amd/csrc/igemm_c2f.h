@@ -6,8 +6,8 @@
 // In separate launches y, t and z go through HBM and four launches pay
 // their fixed costs; here only x is read and only out is written.
 //
-// A workgroup of 8 waves owns R whole rows of one image (R tuned, a divisor
-// of the height).  LDS holds all four weight sets and epilogue blocks and
+// A workgroup of 16 waves owns R whole rows of one image (R tuned, a
+// divisor of the height).  LDS holds all four weight sets and epilogue blocks and
 // three tiles:
 //  * Y1: y1 over rows r0 - 2 .. r0 + R + 1 with a one-pixel column halo, in
 //    the operand form of m.cv1 (u8 xor 0x80; columns beside the image and
@@ -37,7 +37,7 @@ struct C2fArgs {
   int rows;
 };
 
-constexpr int kC2fWaves = 8;
+constexpr int kC2fWaves = 16;
 constexpr int kC2fThreads = 64 * kC2fWaves;
 
 // LDS pixel stride of the 3x3 tiles in 16-byte units (the pair kernel's)
@@ -79,9 +79,12 @@ __host__ __device__ inline C2fLayout c2f_layout(int c, int c2, int ks0, int ks1,
   return L;
 }
 
-// 16-pixel blocks a wave takes at a time in each phase
-__host__ __device__ constexpr int c2f_pbc0(int cb) { return cb == 1 ? 8 : 4; }
-__host__ __device__ constexpr int c2f_pbc(int cb) { return cb == 1 ? 8 : 4; }
+// 16-pixel blocks a wave takes at a time in each phase: within 128 VGPRs, so
+// that 16 waves (four a SIMD) hide each other's LDS and table latencies in
+// the VALU-bound epilogues (b2's block: 55.9 us with 8 waves, 47.9 with 12,
+// 44.3 with 16)
+__host__ __device__ constexpr int c2f_pbc0(int cb, int ks0) { return cb == 1 ? (ks0 == 1 ? 4 : 3) : 2; }
+__host__ __device__ constexpr int c2f_pbc(int cb) { return cb == 1 ? 5 : 3; }
 
 // CB: c / 16 (1 or 2); CBD: c2 / 16 (2 CB: c2 = 2c); KS0: cv1's k-steps
 // (c1 / 64 rounded up); RES: the bottleneck's shortcut.
@@ -89,7 +92,7 @@ template <int CB, int CBD, int KS0, bool RES>
 __global__ __launch_bounds__(kC2fThreads) void igemm_c2f_kernel(const C2fArgs p) {
   constexpr int C = CB * 16;
   constexpr int CBA = 2 * CB;  // cv1's output blocks
-  constexpr int PBC0 = c2f_pbc0(CB);
+  constexpr int PBC0 = c2f_pbc0(CB, KS0);
   constexpr int PBC = c2f_pbc(CB);
   constexpr int CU = C / 16;
   constexpr int SU = c2f_su(C);
