@@ -81,8 +81,8 @@ struct IgemmArgs {
   int tile_bc, tile_pb;    // tile choice (channels, 16-pixel blocks per wave); 0 = heuristic
   int tile_tpw;            // > 0: persistent kernel, pixel tiles per workgroup (small K only);
                            // -1: the streamed-weight kernel (long K); -2: the row-tile kernel;
-                           // -3: the wide-tile kernel (c_in % 128 == 0); -4: the band-tile
-                           // kernel (tile_pb: its band height in rows)
+                           // -3: the wide-tile kernel (c_in % 128 == 0); -4 / -5: the
+                           // band-tile kernel with 8 / 16 waves (tile_pb: its band height)
   int band_rows;           // set by the launcher for the band-tile kernel
   // EPI_QU8 (table or plain requantize epilogues) and EPI_F16: a nearest
   // 2x upsample of the output written as well (the resize folded into its

@@ -1,5 +1,5 @@
 // Band-tile implicit GEMM for 3x3 convolutions (stride 1, padding 1, int8
-// or fp16): one workgroup of 8 waves owns R whole output rows of one image
+// or fp16): one workgroup of 8 or 16 waves owns R whole output rows of one image
 // (R chosen by the graph runtime's tuner, a divisor of the height) and BC
 // output channels, so a layer runs as one round of workgroups, about one a
 // CU, whatever its width.
@@ -13,7 +13,7 @@
 // int8 u8 xor 0x80 or the padding pattern, fp16 as they are), and then each
 // wave walks its own contiguous range of the band's 16-pixel blocks, PBC
 // blocks at a time, both operands read from LDS (the next k-step's
-// fragments while this one's MFMAs run).  The ranges of the 8 waves differ
+// fragments while this one's MFMAs run).  The ranges of the waves differ
 // by at most one block; blocks past a range's end in its last chunk are
 // skipped (wave-uniform) and never stored.  Each wave has its own LDS rows
 // for the epilogue's regrouping, so a wave's epilogue overlaps the other
@@ -23,7 +23,7 @@
 // k-slice offsets, the weights (fragment order, [k-step][block][64 lanes x
 // 16 B]), the input tile ((R + 2) x (W + 2) pixels of SU 16-byte units, SU =
 // c_in * esize / 16 made odd: 8 consecutive pixels' units fall in 8
-// distinct bank groups), the 8 waves' regroup rows.
+// distinct bank groups), the waves' regroup rows.
 //
 // The per-output arithmetic and the epilogues are igemm_kernel's
 // (igemm_store), and integer sums do not depend on the k-order, so int8
@@ -41,15 +41,16 @@ bool igemm_launch_band_f16(hipStream_t st, const IgemmArgs& a, const TileCfg& t)
 
 namespace ig {
 
-constexpr int kBandWaves = 8;
-constexpr int kBandThreads = 64 * kBandWaves;
-constexpr int kBandFill = 16;  // input units each thread loads at start-up (at most)
+constexpr int kBandFill = 16;  // input units each thread of an 8-wave workgroup loads at start-up (at most)
 
-// 16-pixel blocks per chunk (accumulators CB x PBC): for 64-channel tiles
-// a wave's whole range (6 or 7 blocks on the large maps) in one pass of the
-// k-loop; 80-channel tiles measured fastest at 4 (6 was slower, 7 spills)
-__host__ __device__ constexpr int band_pbc(int cb) {
-  return cb <= 2 ? 8 : (cb <= 4 ? 7 : (cb == 5 ? 4 : 2));
+// 16-pixel blocks per chunk (accumulators CB x PBC) for NW waves: with 8
+// waves (256 VGPRs) 64-channel tiles take a wave's whole range (6 or 7
+// blocks on the large maps) in one pass of the k-loop, 80-channel tiles
+// measured fastest at 4 (6 was slower, 7 spills); with 16 waves (four a
+// SIMD, 128 VGPRs) the chunks are what fits without spilling
+__host__ __device__ constexpr int band_pbc(int cb, int nw) {
+  return nw == 8 ? (cb <= 2 ? 8 : (cb <= 4 ? 7 : (cb == 5 ? 4 : 2)))
+                 : (cb == 1 ? 6 : (cb == 2 ? 4 : (cb <= 5 ? 2 : 1)));
 }
 __host__ __device__ constexpr int band_su(int cu) { return cu | 1; }
 __host__ __device__ constexpr int band_tab_off(int bc) { return 256 + 8 * bc; }
@@ -59,14 +60,17 @@ __host__ __device__ constexpr int band_tile_bytes(int rows, int w, int cu) { ret
 __host__ __device__ constexpr int band_xp_off(int bc, int ks, int rows, int w, int cu) {
   return band_x_off(bc, ks) + band_tile_bytes(rows, w, cu);
 }
-inline size_t band_lds_bytes(int bc, int ks, int rows, int w, int cu) {
-  return (size_t)band_xp_off(bc, ks, rows, w, cu) + (size_t)kBandWaves * 16 * xpose_row(bc);
+inline size_t band_lds_bytes(int bc, int ks, int rows, int w, int cu, int nw) {
+  return (size_t)band_xp_off(bc, ks, rows, w, cu) + (size_t)nw * 16 * xpose_row(bc);
 }
 
-template <int ESZ, int BC, int EPV>
-__global__ __launch_bounds__(kBandThreads) void igemm_band_kernel(const IgemmArgs a) {
+template <int ESZ, int BC, int EPV, int NW>
+__global__ __launch_bounds__(64 * NW) void igemm_band_kernel(const IgemmArgs a) {
   constexpr int CB = BC / 16;
-  constexpr int PBC = band_pbc(CB);
+  constexpr int PBC = band_pbc(CB, NW);
+  constexpr int kBandWaves = NW;
+  constexpr int kBandThreads = 64 * NW;
+  constexpr int FILL = kBandFill * 8 / NW;  // input units a thread loads at start-up (at most)
   constexpr bool FAST = EPV != EPV_GENERIC;
   static_assert(!FAST || ESZ == 1, "specialised epilogues are int8");
   using acc_t = typename std::conditional<ESZ == 1, v4i, v4f>::type;
@@ -143,11 +147,11 @@ __global__ __launch_bounds__(kBandThreads) void igemm_band_kernel(const IgemmArg
   const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, a.x_bytes, 0x00020000);
   const int units = (R + 2) * TW * CU;
   const float r_cu = 1.0f / (float)CU, r_tw = 1.0f / (float)TW;
-  u32x4 xv[kBandFill];
-  int xdst[kBandFill];  // LDS offset of the unit, or -1 for none
-  bool xin[kBandFill];
+  u32x4 xv[FILL];
+  int xdst[FILL];  // LDS offset of the unit, or -1 for none
+  bool xin[FILL];
 #pragma unroll
-  for (int i = 0; i < kBandFill; ++i) {
+  for (int i = 0; i < FILL; ++i) {
     const int u = tid + i * kBandThreads;
     xdst[i] = -1;
     xin[i] = false;
@@ -182,7 +186,7 @@ __global__ __launch_bounds__(kBandThreads) void igemm_band_kernel(const IgemmArg
   // everything above has landed (direct loads included); write the tile
   __builtin_amdgcn_s_waitcnt(0);
 #pragma unroll
-  for (int i = 0; i < kBandFill; ++i) {
+  for (int i = 0; i < FILL; ++i) {
     if (xdst[i] >= 0) {
       if constexpr (ESZ == 1) {
         const uint32_t key = xin[i] ? a.xxor : a.xpad;
@@ -261,23 +265,32 @@ __global__ __launch_bounds__(kBandThreads) void igemm_band_kernel(const IgemmArg
   }
 }
 
-template <int ESZ, int BC, int EPV>
+template <int ESZ, int BC, int EPV, int NW>
 void launch_band_bc(hipStream_t st, const IgemmArgs& a, const TileCfg& t) {
   const int rows = a.band_rows;
   const dim3 grid((unsigned)(a.n * (a.h / rows) * (a.cout_pad / t.bc)));
-  const size_t lds = band_lds_bytes(t.bc, a.ksteps, rows, a.w, a.cin * ESZ / 16);
-  hipLaunchKernelGGL((igemm_band_kernel<ESZ, BC, EPV>), grid, dim3(kBandThreads), lds, st, a);
+  const size_t lds = band_lds_bytes(t.bc, a.ksteps, rows, a.w, a.cin * ESZ / 16, NW);
+  hipLaunchKernelGGL((igemm_band_kernel<ESZ, BC, EPV, NW>), grid, dim3(64 * NW), lds, st, a);
 }
 
+// t.tpw: -4 the 8-wave form, -5 the 16-wave form
 template <int ESZ, int EPV>
 bool launch_band_tiles(hipStream_t st, const IgemmArgs& a, const TileCfg& t) {
+#define DW_BAND(BC_)                                                              \
+  case BC_:                                                                       \
+    if (t.tpw == -5)                                                              \
+      launch_band_bc<ESZ, BC_, EPV, 16>(st, a, t);                                \
+    else                                                                          \
+      launch_band_bc<ESZ, BC_, EPV, 8>(st, a, t);                                 \
+    return true;
   switch (t.bc) {
-    case 128: launch_band_bc<ESZ, 128, EPV>(st, a, t); return true;
-    case 80: launch_band_bc<ESZ, 80, EPV>(st, a, t); return true;
-    case 64: launch_band_bc<ESZ, 64, EPV>(st, a, t); return true;
-    case 32: launch_band_bc<ESZ, 32, EPV>(st, a, t); return true;
-    case 16: launch_band_bc<ESZ, 16, EPV>(st, a, t); return true;
+    DW_BAND(128)
+    DW_BAND(80)
+    DW_BAND(64)
+    DW_BAND(32)
+    DW_BAND(16)
   }
+#undef DW_BAND
   return false;
 }
 

@@ -142,34 +142,41 @@ TileCfg make_wide_tile(const IgemmArgs& a, int bc) {
   return t;
 }
 
-// The band-tile kernel (tpw = -4, pb = its band height R): 3x3, stride 1,
-// padding 1, R whole rows (R divides H) of at least one 16-pixel block per
-// wave, the input tile within the start-up loads, everything within LDS.
-bool band_ok(const IgemmArgs& a, int bc, int rows) {
+// The band-tile kernel (tpw = -4: 8 waves, -5: 16 waves; pb = its band
+// height R): 3x3, stride 1, padding 1, R whole rows (R divides H) of at
+// least one 16-pixel block per wave, the input tile within the start-up
+// loads, everything within LDS.
+int band_waves(int tpw) { return tpw == -5 ? 16 : 8; }
+
+bool band_ok(const IgemmArgs& a, int bc, int rows, int tpw = -4) {
   const int es = a.epi == EPI_F16 ? 2 : 1;
+  const int nw = band_waves(tpw);
   if (a.kh != 3 || a.kw != 3 || a.sh != 1 || a.sw != 1 || a.pt != 1 || a.pl != 1) return false;
   if (a.ho != a.h || a.wo != a.w || (a.cin * es) % 16 != 0 || a.w <= 0) return false;
   if (!(bc == 128 || bc == 80 || bc == 64 || bc == 32 || bc == 16) || a.cout_pad % bc != 0) return false;
-  if (rows < 1 || a.h % rows != 0 || rows * a.w < 16 * ig::kBandWaves) return false;
+  // 16 waves over 64 channels: only the u8 requantize and table epilogues
+  // without a residual fit 128 VGPRs
+  if (nw == 16 && bc > 64 && !(es == 1 && a.epi == EPI_QU8 && !a.res && !a.h_wfrag)) return false;
+  if (rows < 1 || a.h % rows != 0 || rows * a.w < 16 * nw) return false;
   const int cu = a.cin * es / 16;
-  if ((rows + 2) * (a.w + 2) * cu > ig::kBandFill * ig::kBandThreads) return false;
-  return ig::band_lds_bytes(bc, a.ksteps, rows, a.w, cu) <= 160 * 1024;
+  if ((rows + 2) * (a.w + 2) * cu > ig::kBandFill * 512) return false;
+  return ig::band_lds_bytes(bc, a.ksteps, rows, a.w, cu, nw) <= 160 * 1024;
 }
 
-TileCfg make_band_tile(const IgemmArgs& a, int bc, int rows) {
+TileCfg make_band_tile(const IgemmArgs& a, int bc, int rows, int tpw = -4) {
   TileCfg t = make_tile(a, bc, 4);
   t.pb = rows;
   t.kchunk = a.ksteps;
-  t.tpw = -4;
+  t.tpw = tpw;
   return t;
 }
 
-// Band heights worth timing for a channel tile: those that give between
-// 96 and 768 workgroups (about one a CU up to three), at most 5.
-int band_heights(const IgemmArgs& a, int bc, int* rows, int max) {
+// Band heights worth timing for a channel tile and wave count: those that
+// give between 96 and 768 workgroups (about one a CU up to three), at most 5.
+int band_heights(const IgemmArgs& a, int bc, int tpw, int* rows, int max) {
   int n = 0;
   for (int r = 1; r <= a.h && n < max; ++r) {
-    if (!band_ok(a, bc, r)) continue;
+    if (!band_ok(a, bc, r, tpw)) continue;
     const long wgs = (long)a.n * (a.h / r) * (a.cout_pad / bc);
     if (wgs >= 96 && wgs <= 768) rows[n++] = r;
   }
@@ -234,7 +241,7 @@ TileCfg pick_any(const IgemmArgs& a) {
     if (nv == 3 && v2 == -1 && st_ok(a, v0, v1)) return make_st_tile(a, v0, v1);
     if (nv == 3 && v2 == -2 && rows_ok(a, v0)) return make_rows_tile(a, v0);
     if (nv == 3 && v2 == -3 && wide_ok(a, v0)) return make_wide_tile(a, v0);
-    if (nv == 3 && v2 == -4 && band_ok(a, v0, v1)) return make_band_tile(a, v0, v1);
+    if (nv == 3 && (v2 == -4 || v2 == -5) && band_ok(a, v0, v1, v2)) return make_band_tile(a, v0, v1, v2);
     if (nv >= 2 && tile_ok(a, v0, v1)) return make_tile(a, v0, v1);
     if (nv == 1 && tile_ok(a, channel_tile(a.cout), v0)) return make_tile(a, channel_tile(a.cout), v0);
   }
@@ -242,7 +249,8 @@ TileCfg pick_any(const IgemmArgs& a) {
   if (a.tile_bc && a.tile_tpw == -1 && st_ok(a, a.tile_bc, a.tile_pb)) return make_st_tile(a, a.tile_bc, a.tile_pb);
   if (a.tile_bc && a.tile_tpw == -2 && rows_ok(a, a.tile_bc)) return make_rows_tile(a, a.tile_bc);
   if (a.tile_bc && a.tile_tpw == -3 && wide_ok(a, a.tile_bc)) return make_wide_tile(a, a.tile_bc);
-  if (a.tile_bc && a.tile_tpw == -4 && band_ok(a, a.tile_bc, a.tile_pb)) return make_band_tile(a, a.tile_bc, a.tile_pb);
+  if (a.tile_bc && (a.tile_tpw == -4 || a.tile_tpw == -5) && band_ok(a, a.tile_bc, a.tile_pb, a.tile_tpw))
+    return make_band_tile(a, a.tile_bc, a.tile_pb, a.tile_tpw);
   if (a.tile_bc && tile_ok(a, a.tile_bc, a.tile_pb)) return make_tile(a, a.tile_bc, a.tile_pb);
   const int bc = channel_tile(a.cout);
   const int ctiles = a.cout_pad / bc;
@@ -282,7 +290,7 @@ int igemm_candidates(const IgemmArgs& a, int* bc, int* pb, int* tpw, int max) {
       ++n;
     }
     int rows[8];
-    const int nr = band_heights(a, a.cout_pad, rows, 8);
+    const int nr = band_heights(a, a.cout_pad, -4, rows, 8);
     for (int i = 0; i < nr && n < max; ++i)
       if (head_tile_ok(a, make_band_tile(a, a.cout_pad, rows[i]))) {
         bc[n] = a.cout_pad;
@@ -292,22 +300,23 @@ int igemm_candidates(const IgemmArgs& a, int* bc, int* pb, int* tpw, int max) {
       }
     return n;
   }
-  // band tiles: the widest channel tile, and 64 channels when that splits
-  // a wider layer in two or more
+  // band tiles (8 and 16 waves): the widest channel tile, and 64 channels
+  // when that splits a wider layer in two or more
   {
     const int bw = std::min(a.cout_pad, 128);
-    for (int j = 0; j < 2; ++j) {
-      const int b = j == 0 ? bw : 64;
-      if (j == 1 && (bw <= 64 || a.cout_pad % 64 != 0)) continue;
-      int rows[8];
-      const int nr = band_heights(a, b, rows, 8);
-      for (int i = 0; i < nr && n < max; ++i) {
-        bc[n] = b;
-        pb[n] = rows[i];
-        tpw[n] = -4;
-        ++n;
+    for (int tw : {-4, -5})
+      for (int j = 0; j < 2; ++j) {
+        const int b = j == 0 ? bw : 64;
+        if (j == 1 && (bw <= 64 || a.cout_pad % 64 != 0)) continue;
+        int rows[8];
+        const int nr = band_heights(a, b, tw, rows, 8);
+        for (int i = 0; i < nr && n < max; ++i) {
+          bc[n] = b;
+          pb[n] = rows[i];
+          tpw[n] = tw;
+          ++n;
+        }
       }
-    }
   }
   for (int b : {256, 128, 64})
     if (n < max && wide_ok(a, b)) {
@@ -362,6 +371,8 @@ const char* igemm_tile_name(const IgemmArgs& a, int esize) {
     snprintf(buf, sizeof buf, "igemm_%s_c%d_wide", esize == 1 ? "i8" : "f16", t.bc);
   else if (t.tpw == -4)
     snprintf(buf, sizeof buf, "igemm_%s_c%d_band%d", esize == 1 ? "i8" : "f16", t.bc, t.pb);
+  else if (t.tpw == -5)
+    snprintf(buf, sizeof buf, "igemm_%s_c%d_band%dw16", esize == 1 ? "i8" : "f16", t.bc, t.pb);
   else
     snprintf(buf, sizeof buf, "igemm_%s_c%d_p%d", esize == 1 ? "i8" : "f16", t.bc, 64 * t.pb);
   if (a.h_wfrag) strncat(buf, "_head", sizeof buf - strlen(buf) - 1);
@@ -383,7 +394,8 @@ void launch_igemm(hipStream_t st, const IgemmArgs& a_in, int esize) {
                      : t.tpw == -1 ? ig::st_lds_bytes(t.bc, a.ksteps, t.pd)
                      : t.tpw == -2 ? ig::rows_lds_bytes(t.bc, a.ksteps, a.w, a.cin, esize)
                      : t.tpw == -3 ? ig::wide_lds_bytes(t.bc, a.ksteps)
-                     : t.tpw == -4 ? ig::band_lds_bytes(t.bc, a.ksteps, t.pb, a.w, a.cin * esize / 16)
+                     : t.tpw == -4 || t.tpw == -5
+                         ? ig::band_lds_bytes(t.bc, a.ksteps, t.pb, a.w, a.cin * esize / 16, band_waves(t.tpw))
                                    : ig::lds_bytes(t, a.ksteps);
   if (lds > 160 * 1024) fail(-2, "igemm: k-slice table does not fit LDS");
   if ((long long)a.ho * a.wo >= (1ll << 23)) fail(-2, "igemm: more than 2^23 output pixels per image");
@@ -400,7 +412,7 @@ void launch_igemm(hipStream_t st, const IgemmArgs& a_in, int esize) {
   a.y_bytes = (int)yb;
   a.r_bytes = (int)rb;
   a.tile_tpw = t.tpw;
-  a.band_rows = t.tpw == -4 ? t.pb : 0;
+  a.band_rows = t.tpw == -4 || t.tpw == -5 ? t.pb : 0;
   if (a.y_up && (esize == 1 ? (a.epi != EPI_QU8 || a.h_wfrag || (a.res && !a.lut) || a.up_pix_stride % 4 != 0 ||
                                 a.up_c_off % 4 != 0)
                              : (a.epi != EPI_F16 || a.up_pix_stride % 4 != 0 || a.up_c_off % 4 != 0)))
@@ -421,7 +433,7 @@ void launch_igemm(hipStream_t st, const IgemmArgs& a_in, int esize) {
       ok = ab ? igemm_launch_rows_i8_a(st, a, t, epv) : igemm_launch_rows_i8_b(st, a, t, epv);
     else if (t.tpw == -3)
       ok = ab ? igemm_launch_wide_i8_a(st, a, t, epv) : igemm_launch_wide_i8_b(st, a, t, epv);
-    else if (t.tpw == -4)
+    else if (t.tpw == -4 || t.tpw == -5)
       ok = ab ? igemm_launch_band_i8_a(st, a, t, epv) : igemm_launch_band_i8_b(st, a, t, epv);
     else
       ok = ab ? igemm_launch_i8_a(st, a, t, epv) : igemm_launch_i8_b(st, a, t, epv);
@@ -430,7 +442,7 @@ void launch_igemm(hipStream_t st, const IgemmArgs& a_in, int esize) {
          : t.tpw == -1 ? igemm_launch_st_f16(st, a, t)
          : t.tpw == -2 ? igemm_launch_rows_f16(st, a, t)
          : t.tpw == -3 ? igemm_launch_wide_f16(st, a, t)
-         : t.tpw == -4 ? igemm_launch_band_f16(st, a, t)
+         : t.tpw == -4 || t.tpw == -5 ? igemm_launch_band_f16(st, a, t)
                        : igemm_launch_f16(st, a, t);
   }
   if (!ok) fail(-2, "igemm: no kernel for tile");

@@ -30,11 +30,11 @@ bool igemm_launch_head_i8(hipStream_t st, const IgemmArgs& a, const TileCfg& t) 
   }
   if (t.tpw == -4) {
     if (t.bc == 64) {
-      ig::launch_band_bc<1, 64, EPV_QU8_LUT_HEAD>(st, a, t);
+      ig::launch_band_bc<1, 64, EPV_QU8_LUT_HEAD, 8>(st, a, t);
       return true;
     }
     if (t.bc == 80) {
-      ig::launch_band_bc<1, 80, EPV_QU8_LUT_HEAD>(st, a, t);
+      ig::launch_band_bc<1, 80, EPV_QU8_LUT_HEAD, 8>(st, a, t);
       return true;
     }
   }

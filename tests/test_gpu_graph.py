@@ -264,7 +264,8 @@ def test_int8_graph_row_tiles_bit_exact(backend, monkeypatch):
         np.testing.assert_array_equal(gv, ref[o], err_msg=o)
 
 
-@pytest.mark.parametrize("tile", ["16,10,-4", "32,10,-4", "64,5,-4", "64,10,-4", "80,10,-4"])
+@pytest.mark.parametrize("tile", ["16,10,-4", "32,10,-4", "64,5,-4", "64,10,-4", "80,10,-4", "16,10,-5", "32,10,-5",
+                                  "64,10,-5", "80,10,-5"])
 def test_int8_graph_band_tiles_bit_exact(backend, monkeypatch, tile):
     # 320x320 input: the stride-1 3x3 layers the band-tile kernel accepts for
     # the forced channel tile and band height (C2f bottlenecks with the table

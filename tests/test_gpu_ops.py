@@ -306,27 +306,29 @@ def test_qlinearconv_row_tiles_bit_exact(backend, geom, monkeypatch):
         np.testing.assert_array_equal(run_qconv(backend, c, s, p), ref, err_msg=f"tile {bc},4,-2")
 
 
-def band_tiles(h, w, ci, co, esize=1):
-    """The band-tile kernel's (channel tile, band height) pairs for a 3x3
-    stride-1 conv on an h x w map: channel tiles of 128, 80, 64, 32 or 16
-    that divide the padded c_out, heights that divide h with at least one
-    16-pixel block per wave (8 waves), the input tile within the start-up
-    loads (16 units a thread) and everything within the 160 KB of LDS."""
+def band_tiles(h, w, ci, co, esize=1, waves=8):
+    """The band-tile kernel's (channel tile, band height, tile code) triples
+    for a 3x3 stride-1 conv on an h x w map with `waves` waves (8: code -4,
+    16: code -5): channel tiles of 128, 80, 64, 32 or 16 that divide the
+    padded c_out (16 waves: at most 64 unless the epilogue is the plain u8
+    requantize), heights that divide h with at least one 16-pixel block per
+    wave, the input tile within the start-up loads (8192 units) and
+    everything within the 160 KB of LDS."""
     top = channel_tile(co)
     pad = -(-co // top) * top
     cu = ci * esize // 16
     ks = -(-9 * ci * esize // 64)
     out = []
     for bc in (128, 80, 64, 32, 16):
-        if pad % bc:
+        if pad % bc or (waves == 16 and bc > 64 and esize != 1):
             continue
         for rows in range(1, h + 1):
-            if h % rows or rows * w < 128 or (rows + 2) * (w + 2) * cu > 16 * 512:
+            if h % rows or rows * w < 16 * waves or (rows + 2) * (w + 2) * cu > 16 * 512:
                 continue
             w_off = -(-(256 + 8 * bc + ks * 16) // 16) * 16
-            lds = w_off + ks * bc * 64 + (rows + 2) * (w + 2) * (cu | 1) * 16 + 8 * 16 * (bc + 16)
+            lds = w_off + ks * bc * 64 + (rows + 2) * (w + 2) * (cu | 1) * 16 + waves * 16 * (bc + 16)
             if lds <= 160 * 1024:
-                out.append((bc, rows))
+                out.append((bc, rows, -4 if waves == 8 else -5))
     return out
 
 
@@ -346,11 +348,11 @@ def test_qlinearconv_band_tiles_bit_exact(backend, geom, x_zp, monkeypatch):
              bias=r.integers((co,), -4096, 4096).astype(np.int32),
              w_scales=r.log_uniform((co,), 1e-3, 1e-2), x_scale=0.02, x_zp=x_zp, y_scale=0.05, y_zp=133)
     ref = oracle_qconv(c, 1, 1)
-    tiles = band_tiles(h, w, ci, co)
+    tiles = band_tiles(h, w, ci, co) + band_tiles(h, w, ci, co, waves=16)
     assert tiles
-    for bc, rows in tiles:
-        monkeypatch.setenv("DW_IGEMM_TILE", f"{bc},{rows},-4")
-        np.testing.assert_array_equal(run_qconv(backend, c, 1, 1), ref, err_msg=f"tile {bc},{rows},-4")
+    for bc, rows, code in tiles:
+        monkeypatch.setenv("DW_IGEMM_TILE", f"{bc},{rows},{code}")
+        np.testing.assert_array_equal(run_qconv(backend, c, 1, 1), ref, err_msg=f"tile {bc},{rows},{code}")
 
 
 def wide_tiles(co):
@@ -613,12 +615,12 @@ def test_conv_f16_band_tiles_identical(backend, monkeypatch, geom):
     monkeypatch.setenv("DW_IGEMM_TILE", "16,4")
     first = run_conv_f16(backend, xh, kh_, bh, 1, 1, ops.ACT_SILU, exact=False)
     assert rel_err(f16v(first), f16v(ref)) <= 1e-2
-    tiles = band_tiles(h, w, ci, co, esize=2)
+    tiles = band_tiles(h, w, ci, co, esize=2) + band_tiles(h, w, ci, co, esize=2, waves=16)
     assert tiles
-    for bc, rows in tiles:
-        monkeypatch.setenv("DW_IGEMM_TILE", f"{bc},{rows},-4")
+    for bc, rows, code in tiles:
+        monkeypatch.setenv("DW_IGEMM_TILE", f"{bc},{rows},{code}")
         got = run_conv_f16(backend, xh, kh_, bh, 1, 1, ops.ACT_SILU, exact=False)
-        np.testing.assert_array_equal(got, first, err_msg=f"tile {bc},{rows},-4")
+        np.testing.assert_array_equal(got, first, err_msg=f"tile {bc},{rows},{code}")
 
 
 @pytest.mark.parametrize("geom", [(2, 11, 9, 64, 128, 3, 1, 1), (2, 20, 18, 128, 64, 3, 2, 1),
