@@ -237,11 +237,12 @@ void launch_igemm(hipStream_t st, const IgemmArgs& a, int esize);
 // Two chained 3x3 QLinearConvs (c -> c -> c, c = 16, 32 or 64, stride 1,
 // padding 1; a1 writes what a2 reads, a2's residual is a1's input or none)
 // in one launch, the intermediate in LDS, `rows` output rows per workgroup
-// (k_igemm_pair.hip).  igemm_pair_rows lists the valid band heights.
+// of 4 or 16 waves (k_igemm_pair.hip).  igemm_pair_rows lists the valid band
+// heights.
 bool igemm_pair_ok(const IgemmArgs& a1, const IgemmArgs& a2, int rows);
 int igemm_pair_rows(const IgemmArgs& a1, const IgemmArgs& a2, int* rows, int max);
 bool igemm_pair_lds_two_per_cu(const IgemmArgs& a1, int rows);  // LDS of the band <= 80 KB
-void launch_igemm_pair(hipStream_t st, const IgemmArgs& a1, const IgemmArgs& a2, int rows);
+void launch_igemm_pair(hipStream_t st, const IgemmArgs& a1, const IgemmArgs& a2, int rows, int waves = 4);
 // A whole int8 C2f block with one bottleneck (k_igemm_c2f.hip): cv1 (1x1,
 // c1 -> 2c), the bottleneck's two 3x3 convs (c -> c, the second with the
 // shortcut or not) and cv2 (1x1, 3c -> 2c) in one launch, c = 16 or 32,

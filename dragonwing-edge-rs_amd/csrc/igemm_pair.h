@@ -56,18 +56,24 @@ __host__ __device__ constexpr int pair_m_off(int c, int ks, int w, int rows) {
 __host__ __device__ constexpr int pair_lds_bytes(int c, int ks, int w, int rows) {
   return pair_m_off(c, ks, w, rows) + (rows + 2) * (w + 2) * pair_su(c) * 16;
 }
-constexpr int kPairFill = 8;  // input units each thread loads at start-up (at most)
-// 16-pixel blocks a wave computes at a time (accumulators CB x PBC)
-__host__ __device__ constexpr int pair_pbc(int cb) { return cb == 1 ? 8 : (cb == 2 ? 6 : 5); }
+constexpr int kPairFill = 8;  // input units each thread of a 4-wave workgroup loads at start-up (at most)
+// 16-pixel blocks a wave computes at a time (accumulators CB x PBC): 4
+// waves take 128 VGPRs (256 for 64 channels, one workgroup a CU), 16 waves
+// (four a SIMD) 128
+__host__ __device__ constexpr int pair_pbc(int cb, int nw, bool res) {
+  return nw == 4 ? (cb == 1 ? 8 : (cb == 2 ? 6 : 5)) : (cb == 1 ? 4 : (cb == 2 ? 3 : (res ? 1 : 2)));
+}
 
 // CB: 16-channel blocks (c / 16); RES: the second epilogue adds the block
-// input.  Both phases walk their 16-pixel blocks PBC at a time per wave
-// (blocks wave * PBC + 4 * PBC * j ..), so any band height fits the
-// registers.
-template <int CB, bool RES>
-__global__ __launch_bounds__(256, CB <= 2 ? 2 : 1) void igemm_pair_kernel(const PairArgs p) {
+// input; NW: waves (4 or 16).  Both phases walk their 16-pixel blocks PBC at
+// a time per wave (blocks wave * PBC + NW * PBC * j ..), so any band height
+// fits the registers.
+template <int CB, bool RES, int NW>
+__global__ __launch_bounds__(64 * NW, NW == 4 ? (CB <= 2 ? 2 : 1) : 1) void igemm_pair_kernel(const PairArgs p) {
   constexpr int C = CB * 16;
-  constexpr int PBC = pair_pbc(CB);
+  constexpr int PBC = pair_pbc(CB, NW, RES);
+  constexpr int NT = 64 * NW;
+  constexpr int FILL = kPairFill * 4 / NW;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const IgemmArgs& a1 = p.a1;
   const IgemmArgs& a2 = p.a2;
@@ -79,7 +85,7 @@ __global__ __launch_bounds__(256, CB <= 2 ? 2 : 1) void igemm_pair_kernel(const 
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
   // XCD-aware tile order, as igemm_kernel: tile = (image, band)
   const int nwg = gridDim.x;
@@ -107,7 +113,7 @@ __global__ __launch_bounds__(256, CB <= 2 ? 2 : 1) void igemm_pair_kernel(const 
   const int frag_lane = ((lane & 15) * 64 + (lane >> 4) * 16);
   {
     const int nfr = KS * CB;
-    for (int f = wave; f < 2 * nfr; f += 4) {
+    for (int f = wave; f < 2 * nfr; f += NW) {
       const int second = f >= nfr;
       const int ff = f - second * nfr;
       const int sl = ff / CB, cb = ff - sl * CB;
@@ -143,12 +149,12 @@ __global__ __launch_bounds__(256, CB <= 2 ? 2 : 1) void igemm_pair_kernel(const 
   const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc((void*)a1.x, (short)0, a1.x_bytes, 0x00020000);
   const int units = (R + 4) * TW * CU;
   const float r_tw = 1.0f / (float)TW;
-  u32x4 xv[kPairFill];
-  int xdst[kPairFill];  // LDS offset of the unit, or -1 for none
-  bool xin[kPairFill];
+  u32x4 xv[FILL];
+  int xdst[FILL];  // LDS offset of the unit, or -1 for none
+  bool xin[FILL];
 #pragma unroll
-  for (int i = 0; i < kPairFill; ++i) {
-    const int u = tid + i * 256;
+  for (int i = 0; i < FILL; ++i) {
+    const int u = tid + i * NT;
     xdst[i] = -1;
     xin[i] = false;
     if (u < units) {
@@ -166,7 +172,7 @@ __global__ __launch_bounds__(256, CB <= 2 ? 2 : 1) void igemm_pair_kernel(const 
 
   // ---- k-slice offsets (shared by both convs: same tile geometry and
   // channel count): slice s of k-step q is 16 input channels of one tap
-  for (int e = tid; e < KS * 4; e += 256) {
+  for (int e = tid; e < KS * 4; e += NT) {
     const int k = e * 16;
     int off = 0;
     if (k < 9 * C) {
@@ -183,7 +189,7 @@ __global__ __launch_bounds__(256, CB <= 2 ? 2 : 1) void igemm_pair_kernel(const 
   {
     const u32x4 pad2 = u32x4{a2.xpad, a2.xpad, a2.xpad, a2.xpad};
     const int mun = (R + 2) * TW * CU;
-    for (int u = tid; u < mun; u += 256) {
+    for (int u = tid; u < mun; u += NT) {
       const int ip = u / CU;
       const int cu = u - ip * CU;
       const int tr = div_small(ip, TW, r_tw), tc = ip - tr * TW;
@@ -196,7 +202,7 @@ __global__ __launch_bounds__(256, CB <= 2 ? 2 : 1) void igemm_pair_kernel(const 
   // everything above has landed (direct loads included); write the tile
   __builtin_amdgcn_s_waitcnt(0);
 #pragma unroll
-  for (int i = 0; i < kPairFill; ++i) {
+  for (int i = 0; i < FILL; ++i) {
     if (xdst[i] >= 0) {
       const uint32_t key = xin[i] ? a1.xxor : a1.xpad;
       *reinterpret_cast<u32x4*>(s_x + xdst[i]) = xv[i] ^ key;
@@ -246,7 +252,7 @@ __global__ __launch_bounds__(256, CB <= 2 ? 2 : 1) void igemm_pair_kernel(const 
     const int qbase = 0x4B400000 - a1.y_zp;
     const float qlo = 12582912.0f - (float)a1.y_zp, qhi = qlo + 255.0f;
     const __attribute__((address_space(3))) uint8_t* lut3 = (const __attribute__((address_space(3))) uint8_t*)s_lut1;
-    for (int b0 = wave * PBC; b0 < nb; b0 += 4 * PBC) {
+    for (int b0 = wave * PBC; b0 < nb; b0 += NW * PBC) {
       int pbase[PBC], poff[PBC];  // window in the input tile; result in the intermediate tile (-1: none)
 #pragma unroll
       for (int pb = 0; pb < PBC; ++pb) {
@@ -296,7 +302,7 @@ __global__ __launch_bounds__(256, CB <= 2 ? 2 : 1) void igemm_pair_kernel(const 
     const int qbase = 0x4B400000 - a2.y_zp;
     const float qlo = 12582912.0f - (float)a2.y_zp, qhi = qlo + 255.0f;
     const __attribute__((address_space(3))) uint8_t* lut3 = (const __attribute__((address_space(3))) uint8_t*)s_lut2;
-    for (int b0 = wave * PBC; b0 < nb; b0 += 4 * PBC) {
+    for (int b0 = wave * PBC; b0 < nb; b0 += NW * PBC) {
       int pbase[PBC], pixel[PBC], xres[PBC];  // window; output pixel (-1: none); the residual's unit
 #pragma unroll
       for (int pb = 0; pb < PBC; ++pb) {

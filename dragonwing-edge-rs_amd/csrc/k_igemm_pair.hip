@@ -52,8 +52,9 @@ bool igemm_pair_lds_two_per_cu(const IgemmArgs& a1, int rows) {
   return ig::pair_lds_bytes(a1.cin, a1.ksteps, a1.w, rows) <= 80 * 1024;
 }
 
-void launch_igemm_pair(hipStream_t st, const IgemmArgs& a1_in, const IgemmArgs& a2_in, int rows) {
+void launch_igemm_pair(hipStream_t st, const IgemmArgs& a1_in, const IgemmArgs& a2_in, int rows, int waves) {
   if (!igemm_pair_ok(a1_in, a2_in, rows)) fail(-2, "igemm pair: unsupported shapes, views or band height");
+  if (waves != 4 && waves != 16) fail(-2, "igemm pair: 4 or 16 waves");
   ig::PairArgs p;
   p.a1 = a1_in;
   p.a2 = a2_in;
@@ -64,14 +65,18 @@ void launch_igemm_pair(hipStream_t st, const IgemmArgs& a1_in, const IgemmArgs& 
   const dim3 grid((unsigned)(p.a1.n * (h / rows)));
   const size_t lds = (size_t)ig::pair_lds_bytes(c, p.a1.ksteps, w, rows);
   const bool res = p.a2.res != nullptr;
-#define DW_P(CB_)                                                                                    \
-  if (c == 16 * (CB_)) {                                                                            \
-    if (res)                                                                                        \
-      hipLaunchKernelGGL((ig::igemm_pair_kernel<CB_, true>), grid, dim3(256), lds, st, p);         \
-    else                                                                                            \
-      hipLaunchKernelGGL((ig::igemm_pair_kernel<CB_, false>), grid, dim3(256), lds, st, p);        \
-    DW_HIP(hipGetLastError());                                                                      \
-    return;                                                                                         \
+#define DW_P(CB_)                                                                                       \
+  if (c == 16 * (CB_)) {                                                                               \
+    if (res && waves == 16)                                                                            \
+      hipLaunchKernelGGL((ig::igemm_pair_kernel<CB_, true, 16>), grid, dim3(1024), lds, st, p);       \
+    else if (res)                                                                                      \
+      hipLaunchKernelGGL((ig::igemm_pair_kernel<CB_, true, 4>), grid, dim3(256), lds, st, p);         \
+    else if (waves == 16)                                                                              \
+      hipLaunchKernelGGL((ig::igemm_pair_kernel<CB_, false, 16>), grid, dim3(1024), lds, st, p);      \
+    else                                                                                               \
+      hipLaunchKernelGGL((ig::igemm_pair_kernel<CB_, false, 4>), grid, dim3(256), lds, st, p);        \
+    DW_HIP(hipGetLastError());                                                                         \
+    return;                                                                                            \
   }
   DW_P(1) DW_P(2) DW_P(4)
 #undef DW_P

@@ -2069,9 +2069,11 @@ bool listed(const char* csv, const std::string& ops) {
 // two tuned launches.  DW_PAIR=1 keeps every candidate pair, DW_PAIR=0
 // none; untuned plans (DW_AUTOTUNE=0, DW_IGEMM_TILE) keep none unless
 // DW_PAIR=1, which then takes the tallest band that leaves two workgroups
-// a CU their LDS (or the tallest).  DW_PAIR_ROWS=<r> forces band height r
-// wherever it is valid (tests); DW_PAIR_KEEP=<op,op,..> keeps exactly the
-// pairs whose first conv is listed (another process reproducing a plan).
+// a CU their LDS (or the tallest).  Each height is timed in both
+// workgroup forms (4 waves, and 16 waves with smaller register chunks).
+// DW_PAIR_ROWS=<r> forces band height r wherever it is valid (tests),
+// DW_PAIR_WAVES=4|16 forces the form; DW_PAIR_KEEP=<op,op,..> keeps exactly
+// the pairs whose first conv is listed (another process reproducing a plan).
 void Runtime::fuse_pairs() {
   const char* env = getenv("DW_PAIR");
   if (env && env[0] == '0') return;
@@ -2086,16 +2088,18 @@ void Runtime::fuse_pairs() {
       for (auto& i : op.in) k += i == t;
     return k;
   };
+  FILE* log = nullptr;
+  if (const char* lp = getenv("DW_AUTOTUNE_LOG")) log = fopen(lp, "a");
   hipStream_t st = be->stream;
   hipEvent_t e0 = nullptr, e1 = nullptr;
   DW_HIP(hipEventCreate(&e0));
   DW_HIP(hipEventCreate(&e1));
-  auto time4 = [&](const IgemmArgs& a1, const IgemmArgs& a2, int rows) {
-    launch_igemm_pair(st, a1, a2, rows);
+  auto time4 = [&](const IgemmArgs& a1, const IgemmArgs& a2, int rows, int waves) {
+    launch_igemm_pair(st, a1, a2, rows, waves);
     float t_min = 1e30f;
     for (int r = 0; r < 3; ++r) {
       DW_HIP(hipEventRecord(e0, st));
-      for (int k = 0; k < 4; ++k) launch_igemm_pair(st, a1, a2, rows);
+      for (int k = 0; k < 4; ++k) launch_igemm_pair(st, a1, a2, rows, waves);
       DW_HIP(hipEventRecord(e1, st));
       DW_HIP(hipEventSynchronize(e1));
       float ms = 0;
@@ -2114,17 +2118,22 @@ void Runtime::fuse_pairs() {
     int cand[16];
     const int nc = igemm_pair_rows(*L1.ig, *L2.ig, cand, 16);
     if (nc == 0) continue;
-    int rows = cand[0];
+    int rows = cand[0], waves = 4;
     if (tuned) {
       if (L1.tuned_ms <= 0 || L2.tuned_ms <= 0) continue;
       float best = 1e30f;
-      for (int k = 0; k < nc; ++k) {
-        const float t = time4(*L1.ig, *L2.ig, cand[k]);
-        if (t < best) {
-          best = t;
-          rows = cand[k];
+      for (int k = 0; k < nc; ++k)
+        for (int wv : {4, 16}) {
+          const float t = time4(*L1.ig, *L2.ig, cand[k], wv);
+          if (log)
+            fprintf(log, "%s\tigemm_i8_pair_c%d_r%d_w%d\t%.2f\n", L1.op.c_str(), L1.ig->cin, cand[k], wv, t * 1e3f / 4);
+          if (t < best) {
+            best = t;
+            rows = cand[k];
+            waves = wv;
+          }
         }
-      }
+      if (log) fprintf(log, "%s\ttwo launches\t%.2f\n", L1.op.c_str(), (L1.tuned_ms + L2.tuned_ms) * 1e3f / 4);
       if (!force && best >= L1.tuned_ms + L2.tuned_ms) continue;
     } else {
       for (int k = 0; k < nc; ++k)
@@ -2138,13 +2147,14 @@ void Runtime::fuse_pairs() {
       if (igemm_pair_ok(*L1.ig, *L2.ig, r)) rows = r;
     }
     Launch P;
-    P.kernel = "igemm_i8_pair_c" + std::to_string(L1.ig->cin);
+    if (const char* fw = getenv("DW_PAIR_WAVES")) waves = atoi(fw) == 16 ? 16 : 4;
+    P.kernel = "igemm_i8_pair_c" + std::to_string(L1.ig->cin) + (waves == 16 ? "_w16" : "");
     P.op = L1.op + "+" + L2.op;
     P.work = L1.work + L2.work;
     // the intermediate neither written nor read back
     P.bytes = L1.bytes + L2.bytes - 2.0 * (double)T(L1.t_out).pixels() * T(L1.t_out).c;
     auto a1 = L1.ig, a2 = L2.ig;
-    P.fn = [a1, a2, rows](hipStream_t s) { launch_igemm_pair(s, *a1, *a2, rows); };
+    P.fn = [a1, a2, rows, waves](hipStream_t s) { launch_igemm_pair(s, *a1, *a2, rows, waves); };
     P.esize = 1;
     P.group = L1.group;
     P.reads = L1.reads;
@@ -2156,6 +2166,7 @@ void Runtime::fuse_pairs() {
     launches[i] = P;
     launches.erase(launches.begin() + (long)i + 1);
   }
+  if (log) fclose(log);
   (void)hipEventDestroy(e0);
   (void)hipEventDestroy(e1);
 }

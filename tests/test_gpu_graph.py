@@ -595,7 +595,7 @@ def test_int8_graph_pairs_bit_exact(backend, monkeypatch):
     monkeypatch.setenv("DW_PAIR", "1")  # every candidate pair, whatever the timing
     monkeypatch.setenv("DW_C2F", "0")  # the one-bottleneck blocks as pairs too
     rt = HipGraphRuntime(g, backend, exact_u8_f16=True)
-    pairs = sorted(L["kernel"] for L in rt.launches() if L["kernel"].startswith("igemm_i8_pair"))
+    pairs = sorted(L["kernel"].replace("_w16", "") for L in rt.launches() if L["kernel"].startswith("igemm_i8_pair"))
     assert pairs == ["igemm_i8_pair_c16"] + ["igemm_i8_pair_c32"] * 3 + ["igemm_i8_pair_c64"] * 5, pairs
     rt.set_input_f32(info["input"], x)
     rt.run()
@@ -613,6 +613,15 @@ def test_int8_graph_pairs_bit_exact(backend, monkeypatch):
         for o, gv, gr in zip(info["outputs"], got, gpu_outputs(rtr, info)):
             np.testing.assert_array_equal(gv, gr, err_msg=f"{o} rows {rows}")
     monkeypatch.delenv("DW_PAIR_ROWS")
+    # the 16-wave form of every pair
+    monkeypatch.setenv("DW_PAIR_WAVES", "16")
+    rtw = HipGraphRuntime(g, backend, exact_u8_f16=True)
+    assert all(L["kernel"].endswith("_w16") for L in rtw.launches() if L["kernel"].startswith("igemm_i8_pair"))
+    rtw.set_input_f32(info["input"], x)
+    rtw.run()
+    for o, gv, gw in zip(info["outputs"], got, gpu_outputs(rtw, info)):
+        np.testing.assert_array_equal(gv, gw, err_msg=f"{o} 16 waves")
+    monkeypatch.delenv("DW_PAIR_WAVES")
     monkeypatch.setenv("DW_PAIR", "0")
     rt0 = HipGraphRuntime(g, backend, exact_u8_f16=True)
     assert not any(L["kernel"].startswith("igemm_i8_pair") for L in rt0.launches())
@@ -702,7 +711,7 @@ def check_int8_batch_bit_exact(g, info, x, backend, graph1, monkeypatch):
     # the eight C2f bottlenecks of 16, 32 and 64 channels (with and without
     # the shortcut) and the stride-8 head's first two box convs run as
     # chained pairs
-    pairs = [L["kernel"] for L in rt.launches() if L["kernel"].startswith("igemm_i8_pair")]
+    pairs = [L["kernel"].replace("_w16", "") for L in rt.launches() if L["kernel"].startswith("igemm_i8_pair")]
     assert sorted(pairs) == sorted(["igemm_i8_pair_c16"] + ["igemm_i8_pair_c32"] * 3 + ["igemm_i8_pair_c64"] * 5), pairs
     rt.set_input_f32(info["input"], x)
     rt.run()
