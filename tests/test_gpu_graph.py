@@ -888,3 +888,71 @@ def test_f16_stem_mfma_vs_oracle(backend, ci, k, s, p, co, n, h, w, act):
     rt.set_input_nchw_f32("x", xn)
     rt.run()
     assert rt.get_output_bytes(out).view(np.uint16).reshape(n, ho, wo, co).tobytes() == got.tobytes()
+
+
+def stem_u8_graph(n, h, w, co, seed):
+    """A three-channel 3x3 stride-2 stem kept fp16 (f16 weights) whose
+    result is quantized to u8 and run through the SiLU table, as the INT8
+    graph's first layer; weights large enough that f16 subnormal inputs
+    reach the output bytes."""
+    from dragonwing_edge_rs_amd.graph import GRAPH_F32, Graph
+
+    r = np.random.default_rng(seed)
+    g = Graph(GRAPH_F32)
+    g.add_tensor("x", (n, h, w, 3))
+    g.add_initializer("w", r.normal(0, 500.0, (3, 3, 3, co)).astype(np.float32))
+    g.add_initializer("b", r.normal(0, 0.5, co).astype(np.float32))
+    ho, wo = (h - 1) // 2 + 1, (w - 1) // 2 + 1
+    for t in ("s", "sg", "act"):
+        g.add_tensor(t, (n, ho, wo, co))
+    g.add_op("stem", "Conv", ["x", "w", "b"], ["s"], kernel_shape=(3, 3), strides=(2, 2), pads=(1, 1, 1, 1))
+    g.add_op("sig", "Sigmoid", ["s"], ["sg"])
+    g.add_op("mul", "Mul", ["s", "sg"], ["act"])
+    g.set_io(["x"], ["act"])
+    g.set_activation_range("x", -1e-3, 1e-3)
+    g.set_activation_range("s", -4.0, 4.0)
+    g.set_activation_range("sg", 0.0, 1.0)
+    g.set_activation_range("act", -0.3, 4.0)
+    g.quantize_qdq(["stem"])
+    return g, (n, ho, wo, co)
+
+
+def stem_u8_inputs(n, h, w, seed):
+    """f16 inputs of magnitude <= 1e-3; image 0 entirely f16 subnormals (every
+    wave on the reference's half-value decode), the others with one
+    subnormal in every eighth row and a block of zeros at the corner."""
+    r = np.random.default_rng(seed)
+    xb = synth.f16_bits(r.uniform(-1e-3, 1e-3, (n, h, w, 3)).astype(np.float32))
+    xb[0] = r.integers(1, 0x400, (h, w, 3)).astype(np.uint16) | (r.integers(0, 2, (h, w, 3)).astype(np.uint16) << 15)
+    for i in range(1, n):
+        for row in r.choice(h, size=max(1, h // 8), replace=False):
+            xb[i, row, r.integers(0, w), r.integers(0, 3)] = np.uint16(r.integers(1, 0x400))
+        xb[i, : h // 4, : w // 4] = 0
+    return xb
+
+
+@pytest.mark.parametrize("n,h,w,co", [
+    (2, 16, 32, 16),    # one partial workgroup
+    (3, 64, 96, 32),    # two 16-channel chunks, many waves
+    (2, 18, 36, 16),    # rows of ragged 256-pixel blocks
+])
+def test_int8_stem_subnormal_inputs_bit_exact(backend, n, h, w, co):
+    # the INT8 graph's fp16 stem with a u8 output (conv, QuantizeLinear, the
+    # SiLU table in one launch) on inputs whose f16 subnormals reach the output
+    # bytes: the reference's half-value decode, zero blocks and the padded
+    # borders give the oracle's bytes
+    g, shp = stem_u8_graph(n, h, w, co, seed=7 + co)
+    xb = stem_u8_inputs(n, h, w, seed=8 + h)
+    ref = oracle_run(g, {"x": xb})["act"]
+    # the test is sensitive to the decode: IEEE-widened subnormals (the
+    # reference decode of twice the value) change the output bytes
+    sub = ((xb & 0x7C00) == 0) & ((xb & 0x3FF) != 0) & ((xb & 0x3FF) < 0x200)
+    x2 = xb.copy()
+    x2[sub] = ((xb[sub] & 0x3FF) * 2) | (xb[sub] & 0x8000)
+    assert np.mean(oracle_run(g, {"x": x2})["act"] != ref) > 0.01
+    rt = HipGraphRuntime(g, backend)
+    assert [L["kernel"] for L in rt.launches()] == ["direct_conv"]
+    rt.set_input_bytes("x", xb)
+    rt.run()
+    np.testing.assert_array_equal(rt.get_output_bytes("act").reshape(shp), ref)
+    assert len(np.unique(ref)) > 50
