@@ -309,13 +309,14 @@ def read_counter_csv(d: Path):
 
 def plan_env(launches):
     """The timed plan choices of a runtime (which fused C2f blocks, chained
-    pairs, fused head 1x1s and folded upsamples it kept), as the
+    pairs, fused head 1x1s, folded upsamples and sibling GEMMs it kept), as the
     environment that makes another process build the same launch list."""
     first = lambda L: L["ops"].split("+")[0]
     return {"DW_PAIR_KEEP": ",".join(first(L) for L in launches if L["kernel"].startswith("igemm_i8_pair")),
             "DW_HEAD_KEEP": ",".join(first(L) for L in launches if L["kernel"].endswith("_head")),
             "DW_C2F_KEEP": ",".join(first(L) for L in launches if L["kernel"].startswith("igemm_i8_c2f")),
-            "DW_RESIZE_KEEP": ",".join(L["ops"].split("+")[-1] for L in launches if L["kernel"].endswith("_up"))}
+            "DW_RESIZE_KEEP": ",".join(L["ops"].split("+")[-1] for L in launches if L["kernel"].endswith("_up")),
+            "DW_SIB_KEEP": ",".join(first(L) for L in launches if L["kernel"].endswith("_sib"))}
 
 
 def measure_traffic(workload: str, launches, timeout: float = 240.0):

@@ -132,7 +132,7 @@ __global__ __launch_bounds__(64 * NW) void igemm_band_kernel(const IgemmArgs a) 
       __builtin_amdgcn_global_load_lds((const void*)(a.mscale + c0 + lane * 4),
                                        (__attribute__((address_space(3))) void*)s_ms, 16, 0, 0);
     if (wave == 2 && a.lut && lane < 16)
-      __builtin_amdgcn_global_load_lds((const void*)(a.lut + lane * 16),
+      __builtin_amdgcn_global_load_lds((const void*)(tile_lut(a, c0) + lane * 16),
                                        (__attribute__((address_space(3))) void*)s_lut, 16, 0, 0);
   } else if (a.epi == EPI_F16 && a.bias_h) {
     ep.bias_h = reinterpret_cast<const uint16_t*>(s_bias);

@@ -283,6 +283,11 @@ __device__ __forceinline__ void pixel_setup(const IgemmArgs& a, int p0, int lane
   }
 }
 
+// The table of channel tile c0: a sibling GEMM's second conv has its own.
+__device__ __forceinline__ const uint8_t* tile_lut(const IgemmArgs& a, int c0) {
+  return (a.y2 && c0 >= a.split) ? a.lut2 : a.lut;
+}
+
 // LDS rows the int8 epilogue uses to regroup results (per wave: 16 pixels
 // x (BC + 16) bytes; the 16-byte pad puts the 64 lanes' 4-byte writes in 64
 // distinct banks).
@@ -381,9 +386,15 @@ __device__ __forceinline__ void igemm_store(const IgemmArgs& a, const EpiLds& ep
   if constexpr (EPV == EPV_QU8_LUT_HEAD) {
     igemm_store_head<BC, PB>(a, acc, p0, lane, s_ms, s_lut, xp, plim);
   } else if constexpr (FAST) {
+    // the output view of this channel tile: a sibling GEMM's second conv
+    // (c0 >= split) writes its own tensor, channel c0 - split of it
+    const bool g2 = a.y2 != nullptr && c0 >= a.split;
+    uint8_t* const ybase = (uint8_t*)(g2 ? a.y2 : a.y);
+    const int ypix = g2 ? a.y2_pix_stride : a.y_pix_stride;
+    const int ycoff = g2 ? a.y2_c_off - a.split : a.y_c_off;
     const bool full = c0 + BC <= a.cout;
-    const bool wide = CB >= 2 && xp != nullptr && full && (a.y_pix_stride & 15) == 0 &&
-                      ((a.y_c_off + c0) & 15) == 0 && (((uintptr_t)a.y) & 15) == 0 &&
+    const bool wide = CB >= 2 && xp != nullptr && full && (ypix & 15) == 0 &&
+                      ((ycoff + c0) & 15) == 0 && (((uintptr_t)ybase) & 15) == 0 &&
                       (!a.y_up || ((a.up_pix_stride & 15) == 0 && ((a.up_c_off + c0) & 15) == 0 &&
                                    (((uintptr_t)a.y_up) & 15) == 0));
     uint8_t* const xrow = wide ? xp + (lane & 15) * xpose_row(BC) : nullptr;
@@ -397,7 +408,7 @@ __device__ __forceinline__ void igemm_store(const IgemmArgs& a, const EpiLds& ep
     for (int pb = 0; pb < PB; ++pb) {
       const int p = p0 + pb * 16 + (lane & 15);
       if (p >= plim) continue;
-      uint8_t* yrow = (uint8_t*)a.y + (size_t)p * a.y_pix_stride + a.y_c_off + c0 + cq;
+      uint8_t* yrow = ybase + (size_t)p * ypix + ycoff + c0 + cq;
       // the pixel's top-left pixel in the upsampled view, if any
       size_t up = 0;
       if (a.y_up) {
@@ -605,7 +616,7 @@ __global__ __launch_bounds__(256) void igemm_kernel(const IgemmArgs a) {
       __builtin_amdgcn_global_load_lds((const void*)(a.mscale + c0 + lane * 4),
                                        (__attribute__((address_space(3))) void*)s_ms, 16, 0, 0);
     if (wave == 2 && a.lut && lane < 16)
-      __builtin_amdgcn_global_load_lds((const void*)(a.lut + lane * 16),
+      __builtin_amdgcn_global_load_lds((const void*)(tile_lut(a, c0) + lane * 16),
                                        (__attribute__((address_space(3))) void*)s_lut, 16, 0, 0);
   } else if (a.epi == EPI_F16 && a.bias_h) {
     if (wave == 0 && lane < nvalid / 2)

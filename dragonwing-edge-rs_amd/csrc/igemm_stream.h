@@ -111,7 +111,7 @@ __global__ __launch_bounds__(256) void igemm_stream_kernel(const IgemmArgs a) {
         epi_src = reinterpret_cast<const uint8_t*>(a.mscale + c0 + lane * 4);
         epi_dst = s_ms + lane * 16;
       } else if (wave == 2 && a.lut && lane < 16) {
-        epi_src = a.lut + lane * 16;
+        epi_src = tile_lut(a, c0) + lane * 16;
         epi_dst = s_lut + lane * 16;
       }
     }

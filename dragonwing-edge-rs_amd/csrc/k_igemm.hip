@@ -273,6 +273,12 @@ int epilogue_variant(const IgemmArgs& a, int esize) {
 
 int igemm_channel_tile(int cout) { return channel_tile(cout); }
 
+bool igemm_sibling_tile_ok(const IgemmArgs& a, int bc, int tpw, int esize) {
+  return esize == 1 && a.epi == EPI_QU8 && a.lut && a.lut2 && !a.res && !a.y_up && !a.h_wfrag &&
+         (tpw == 0 || tpw == -1 || tpw == -4 || tpw == -5) && bc > 0 && a.split > 0 && a.split % bc == 0 &&
+         a.split < a.cout && a.y2_pix_stride % 4 == 0 && a.y2_c_off % 4 == 0;
+}
+
 int igemm_candidates(const IgemmArgs& a, int* bc, int* pb, int* tpw, int max) {
   int n = 0;
   if (a.h_wfrag) {
@@ -300,14 +306,15 @@ int igemm_candidates(const IgemmArgs& a, int* bc, int* pb, int* tpw, int max) {
       }
     return n;
   }
-  // band tiles (8 and 16 waves): the widest channel tile, and 64 channels
-  // when that splits a wider layer in two or more
+  // band tiles (8 and 16 waves): the widest channel tile, and 64 or 80
+  // channels when that splits a wider layer in two or more (80: a sibling
+  // GEMM whose first conv has 80 channels)
   {
     const int bw = std::min(a.cout_pad, 128);
     for (int tw : {-4, -5})
-      for (int j = 0; j < 2; ++j) {
-        const int b = j == 0 ? bw : 64;
-        if (j == 1 && (bw <= 64 || a.cout_pad % 64 != 0)) continue;
+      for (int j = 0; j < 3; ++j) {
+        const int b = j == 0 ? bw : (j == 1 ? 64 : 80);
+        if (j > 0 && (bw <= b || a.cout_pad % b != 0)) continue;
         int rows[8];
         const int nr = band_heights(a, b, tw, rows, 8);
         for (int i = 0; i < nr && n < max; ++i) {
@@ -377,6 +384,7 @@ const char* igemm_tile_name(const IgemmArgs& a, int esize) {
     snprintf(buf, sizeof buf, "igemm_%s_c%d_p%d", esize == 1 ? "i8" : "f16", t.bc, 64 * t.pb);
   if (a.h_wfrag) strncat(buf, "_head", sizeof buf - strlen(buf) - 1);
   if (a.y_up) strncat(buf, "_up", sizeof buf - strlen(buf) - 1);
+  if (a.y2) strncat(buf, "_sib", sizeof buf - strlen(buf) - 1);
   return buf;
 }
 
@@ -417,6 +425,11 @@ void launch_igemm(hipStream_t st, const IgemmArgs& a_in, int esize) {
                                 a.up_c_off % 4 != 0)
                              : (a.epi != EPI_F16 || a.up_pix_stride % 4 != 0 || a.up_c_off % 4 != 0)))
     fail(-2, "igemm: an upsampled copy needs a u8 table, requantize or f16 epilogue and aligned views");
+  // a sibling GEMM: a kernel whose workgroup keeps one channel tile and
+  // stores through igemm_store (staged, streamed-weight, band), the table
+  // epilogue, and tiles that do not straddle the split
+  if (a.y2 && !igemm_sibling_tile_ok(a, t.bc, t.tpw, esize))
+    fail(-2, "igemm: a sibling GEMM needs the table epilogue and a staged, streamed or band tile within one conv");
   bool ok;
   if (esize == 1 && a.h_wfrag) {
     if (a.epi != EPI_QU8 || !a.lut || a.res || !head_tile_ok(a, t))

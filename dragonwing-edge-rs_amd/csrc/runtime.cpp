@@ -237,6 +237,7 @@ struct Runtime {
   float time_graph();
   void fuse_c2f();
   void fuse_resize();
+  void fuse_siblings();
   void enqueue(hipStream_t st);
   void run();
 };
@@ -410,6 +411,7 @@ void Runtime::build(Backend* b, const GraphIR& graph, bool stats_mode) {
     fuse_pairs();
     fuse_heads();
     fuse_resize();
+    fuse_siblings();
   }
   // streams: the schedule over 4 streams, or one stream, whichever runs the
   // whole graph faster (the cross-stream waits cost more than the overlap
@@ -2165,6 +2167,158 @@ void Runtime::fuse_pairs() {
     P.t_out = L2.t_out;
     launches[i] = P;
     launches.erase(launches.begin() + (long)i + 1);
+  }
+  if (log) fclose(log);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+}
+
+// Sibling QLinearConvs in one launch: two convs that read the same input
+// view with the same geometry, each with the table epilogue and no residual
+// (the box0 and cls0 convs of a detect scale), as one GEMM over both channel
+// sets: the second conv's channels after the first's (packed weights, bias'
+// and multipliers concatenated on the device), each channel tile writing its
+// own conv's output view with its own table.  Every output is computed as
+// its own conv computes it, so the bytes are the two launches'.  Both orders
+// and every staged, streamed-weight and band tile whose channel tiles do not
+// straddle the first conv's channels are timed; the fastest is kept if it
+// beats the two tuned launches.  DW_SIB=0 fuses none, =1 every candidate;
+// DW_SIB_KEEP=<op,op,..> keeps exactly the pairs whose first conv is listed.
+void Runtime::fuse_siblings() {
+  const char* env = getenv("DW_SIB");
+  if (env && env[0] == '0') return;
+  const char* keep = getenv("DW_SIB_KEEP");
+  const bool force = (env && env[0] == '1') || keep;
+  const char* tune_env = getenv("DW_AUTOTUNE");
+  const bool tuned = !((tune_env && tune_env[0] == '0') || getenv("DW_IGEMM_TILE"));
+  if (!force && !tuned) return;
+  FILE* log = nullptr;
+  if (const char* lp = getenv("DW_AUTOTUNE_LOG")) log = fopen(lp, "a");
+  hipStream_t st = be->stream;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  DW_HIP(hipEventCreate(&e0));
+  DW_HIP(hipEventCreate(&e1));
+  auto alone = [](const IgemmArgs& a) {
+    return a.epi == EPI_QU8 && a.lut && a.bias_i && a.mscale && !a.res && !a.y_up && !a.h_wfrag && !a.y2 &&
+           a.cout % 16 == 0;
+  };
+  auto same_input = [](const IgemmArgs& a, const IgemmArgs& b) {
+    return a.x == b.x && a.x_pix_stride == b.x_pix_stride && a.x_c_off == b.x_c_off && a.n == b.n && a.h == b.h &&
+           a.w == b.w && a.cin == b.cin && a.kh == b.kh && a.kw == b.kw && a.sh == b.sh && a.sw == b.sw &&
+           a.pt == b.pt && a.pl == b.pl && a.ho == b.ho && a.wo == b.wo && a.ksteps == b.ksteps &&
+           a.xpad == b.xpad && a.xxor == b.xxor && a.y_zp == b.y_zp;
+  };
+  auto time4 = [&](const IgemmArgs& a) {
+    launch_igemm(st, a, 1);
+    float t_min = 1e30f;
+    for (int r = 0; r < 3; ++r) {
+      DW_HIP(hipEventRecord(e0, st));
+      for (int k = 0; k < 4; ++k) launch_igemm(st, a, 1);
+      DW_HIP(hipEventRecord(e1, st));
+      DW_HIP(hipEventSynchronize(e1));
+      float ms = 0;
+      DW_HIP(hipEventElapsedTime(&ms, e0, e1));
+      t_min = std::min(t_min, ms);
+    }
+    return t_min;
+  };
+  // F's channels, then S's, at channel tile width bc: the combined
+  // arguments (packed weights zero-padded to a whole tile)
+  auto combine = [&](const IgemmArgs& F, const IgemmArgs& S, int bc) {
+    IgemmArgs C = F;
+    C.cout = F.cout + S.cout;
+    C.split = F.cout;
+    C.cout_pad = (C.cout + bc - 1) / bc * bc;
+    const size_t row = 64, ks = (size_t)F.ksteps;
+    uint8_t* wpk = (uint8_t*)dalloc(ks * C.cout_pad * row);
+    DW_HIP(hipMemsetAsync(wpk, 0, ks * C.cout_pad * row, st));
+    DW_HIP(hipMemcpy2DAsync(wpk, C.cout_pad * row, F.wpk, F.cout_pad * row, F.cout * row, ks,
+                            hipMemcpyDeviceToDevice, st));
+    DW_HIP(hipMemcpy2DAsync(wpk + F.cout * row, C.cout_pad * row, S.wpk, S.cout_pad * row, S.cout * row, ks,
+                            hipMemcpyDeviceToDevice, st));
+    int* bias = (int*)dalloc(C.cout_pad * sizeof(int));
+    float* ms = (float*)dalloc(C.cout_pad * sizeof(float));
+    DW_HIP(hipMemcpyAsync(bias, F.bias_i, F.cout * sizeof(int), hipMemcpyDeviceToDevice, st));
+    DW_HIP(hipMemcpyAsync(bias + F.cout, S.bias_i, S.cout * sizeof(int), hipMemcpyDeviceToDevice, st));
+    DW_HIP(hipMemcpyAsync(ms, F.mscale, F.cout * sizeof(float), hipMemcpyDeviceToDevice, st));
+    DW_HIP(hipMemcpyAsync(ms + F.cout, S.mscale, S.cout * sizeof(float), hipMemcpyDeviceToDevice, st));
+    DW_HIP(hipStreamSynchronize(st));
+    C.wpk = wpk;
+    C.bias_i = bias;
+    C.mscale = ms;
+    C.y2 = S.y;
+    C.y2_pix_stride = S.y_pix_stride;
+    C.y2_c_off = S.y_c_off;
+    C.lut2 = S.lut;
+    C.tile_bc = C.tile_pb = C.tile_tpw = 0;
+    return C;
+  };
+  for (size_t i = 0; i < launches.size(); ++i) {
+    for (size_t j = i + 1; j < launches.size(); ++j) {
+      Launch& LA = launches[i];
+      Launch& LB = launches[j];
+      if (!LA.ig || !LB.ig || LA.esize != 1 || LB.esize != 1) continue;
+      const IgemmArgs A = *LA.ig, B = *LB.ig;
+      if (!alone(A) || !alone(B) || !same_input(A, B)) continue;
+      if (!tuned && !force) continue;
+      if (tuned && (LA.tuned_ms <= 0 || LB.tuned_ms <= 0)) continue;
+      float best = 1e30f;
+      IgemmArgs bestC{};
+      bool first_a = true;
+      for (int order = 0; order < 2; ++order) {
+        const IgemmArgs& F = order == 0 ? A : B;
+        const IgemmArgs& S = order == 0 ? B : A;
+        const Launch& LF = order == 0 ? LA : LB;
+        if (keep && !listed(keep, LF.op)) continue;
+        for (int bw : {128, 96, 80, 64, 48, 32, 16}) {
+          if (F.cout % bw != 0) continue;
+          IgemmArgs C = combine(F, S, bw);
+          int bc[64], pb[64], tpw[64];
+          const int n = igemm_candidates(C, bc, pb, tpw, 64);
+          for (int k = 0; k < n; ++k) {
+            if (bc[k] != bw || !igemm_sibling_tile_ok(C, bc[k], tpw[k], 1)) continue;
+            C.tile_bc = bc[k];
+            C.tile_pb = pb[k];
+            C.tile_tpw = tpw[k];
+            const float t = tuned ? time4(C) : 0.0f;
+            if (log)
+              fprintf(log, "%s+%s\t%s\t%.2f\n", LF.op.c_str(), (order == 0 ? LB : LA).op.c_str(),
+                      igemm_tile_name(C, 1), t * 1e3f / 4);
+            if (t < best) {
+              best = t;
+              bestC = C;
+              first_a = order == 0;
+            }
+          }
+        }
+      }
+      if (best >= 1e30f) continue;
+      if (log) fprintf(log, "%s+%s\ttwo launches\t%.2f\n", LA.op.c_str(), LB.op.c_str(),
+                       (LA.tuned_ms + LB.tuned_ms) * 1e3f / 4);
+      if (!force && best >= LA.tuned_ms + LB.tuned_ms) continue;
+      const Launch& LF = first_a ? LA : LB;
+      const Launch& LS = first_a ? LB : LA;
+      Launch P;
+      P.ig = std::make_shared<IgemmArgs>(bestC);
+      P.kernel = igemm_tile_name(bestC, 1);
+      P.op = LF.op + "+" + LS.op;
+      P.work = LA.work + LB.work;
+      // the input read once
+      P.bytes = LA.bytes + LB.bytes - (double)A.n * A.h * A.w * A.cin;
+      auto ig = P.ig;
+      P.fn = [ig](hipStream_t s) { launch_igemm(s, *ig, 1); };
+      P.esize = 1;
+      P.group = LA.group;
+      P.reads = LA.reads;
+      P.reads.insert(P.reads.end(), LB.reads.begin(), LB.reads.end());
+      P.writes = LA.writes;
+      P.writes.insert(P.writes.end(), LB.writes.begin(), LB.writes.end());
+      P.t_in = LA.t_in;
+      P.tuned_ms = best;
+      launches[i] = P;
+      launches.erase(launches.begin() + (long)j);
+      break;
+    }
   }
   if (log) fclose(log);
   (void)hipEventDestroy(e0);

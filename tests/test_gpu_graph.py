@@ -570,11 +570,13 @@ def test_int8_graph_launch_plan(backend, int8_small):
     # the six fp16 head 1x1 convs on the fp16 matrix cores (each in its own
     # launch or inside its 3x3's, "_head"), one SPPF cascade, two resizes
     # (each in its own launch or written by the conv before it, "_up"), no
-    # copies or elementwise.
+    # copies or elementwise; a detect scale's box0 and cls0 as one GEMM
+    # ("_sib") where the tuner finds that faster.
     pairs = sum(L["kernel"].startswith("igemm_i8_pair") for L in ls)
     blocks = sum(L["kernel"].startswith("igemm_i8_c2f") for L in ls)
     heads = sum(L["kernel"].endswith("_head") for L in ls)
-    assert kinds.get("igemm") + pairs + 3 * blocks == 56, (pairs, blocks, kinds)
+    sibs = sum(L["kernel"].endswith("_sib") for L in ls)
+    assert kinds.get("igemm") + pairs + 3 * blocks + sibs == 56, (pairs, blocks, sibs, kinds)
     assert kinds.get("direct") == 1 and kinds.get("conv1x1", 0) + heads == 6, kinds
     ups = sum(L["kernel"].endswith("_up") for L in ls)
     assert kinds.get("maxpool") == 1 and kinds.get("resize", 0) + ups == 2, kinds
@@ -888,6 +890,55 @@ def test_f16_stem_mfma_vs_oracle(backend, ci, k, s, p, co, n, h, w, act):
     rt.set_input_nchw_f32("x", xn)
     rt.run()
     assert rt.get_output_bytes(out).view(np.uint16).reshape(n, ho, wo, co).tobytes() == got.tobytes()
+
+
+def test_int8_graph_siblings_bit_exact(backend, int8_small, monkeypatch):
+    # each detect scale's box0 and cls0 QLinearConvs (same input) as one GEMM
+    # over both channel sets, every channel tile writing its own conv's
+    # output with its own table: forced for all three scales, the oracle's
+    # bytes, and the bytes of the unfused plan
+    g, info = int8_small
+    x = yolo.input_images(2, 96)
+    monkeypatch.setenv("DW_PAIR", "0")  # det0's box0 may otherwise chain with box1
+    monkeypatch.setenv("DW_SIB", "1")
+    rt = HipGraphRuntime(g, backend, exact_u8_f16=True)
+    sib = [L for L in rt.launches() if L["kernel"].endswith("_sib")]
+    assert len(sib) == 3, [L["kernel"] for L in rt.launches()]
+    assert all("box0" in L["ops"] and "cls0" in L["ops"] for L in sib), [L["ops"] for L in sib]
+    rt.set_input_f32(info["input"], x)
+    rt.run()
+    got = gpu_outputs(rt, info)
+    ref = oracle_run(g, {info["input"]: synth.f16_bits(x)})
+    for o, gv in zip(info["outputs"], got):
+        np.testing.assert_array_equal(gv, ref[o], err_msg=o)
+    monkeypatch.setenv("DW_SIB", "0")
+    rt0 = HipGraphRuntime(g, backend, exact_u8_f16=True)
+    assert not any(L["kernel"].endswith("_sib") for L in rt0.launches())
+    rt0.set_input_f32(info["input"], x)
+    rt0.run()
+    for o, gv, g0 in zip(info["outputs"], got, gpu_outputs(rt0, info)):
+        assert gv.tobytes() == g0.tobytes(), o
+
+
+def test_int8_benchmark_graph_siblings_same_bytes(backend, monkeypatch):
+    # the benchmark's 640 x 640 batch-32 graph with every sibling pair fused
+    # and with none: the same bytes on every output
+    from dragonwing_edge_rs_amd import workloads
+
+    g, inputs, outs, work, extra = workloads.yolov8n_int8(backend)
+    monkeypatch.setenv("DW_PAIR", "0")  # det0's box0 may otherwise chain with box1
+    res = []
+    for v in ("1", "0"):
+        monkeypatch.setenv("DW_SIB", v)
+        rt = HipGraphRuntime(g, backend)
+        n = sum(L["kernel"].endswith("_sib") for L in rt.launches())
+        assert n == (3 if v == "1" else 0), n
+        for k, val in inputs.items():
+            rt.set_input_bytes(k, val)
+        rt.run()
+        res.append([rt.get_output_bytes(o).tobytes() for o in outs])
+        del rt
+    assert res[0] == res[1]
 
 
 def stem_u8_graph(n, h, w, co, seed):
