@@ -52,7 +52,7 @@ def kernel_bound(kernel: str):
         return PEAKS["int8"]
     if kernel.startswith("igemm_f16"):
         return PEAKS["f16"]
-    if kernel.startswith("direct_conv"):
+    if kernel.startswith("direct_conv") or kernel.startswith("stem_pad"):
         return PEAKS["f32"]
     return PEAKS["hbm"]  # the u8 -> f16 1x1 convs (conv1x1_u8_f16) are HBM-bound
 
@@ -74,8 +74,8 @@ def conv_rooflines(launches, ms):
     rows = []
     for L, t in zip(launches, ms):
         k = L["kernel"]
-        if not (k.startswith("igemm") or k.startswith("direct_conv") or k.startswith("dwconv") or
-                k.startswith("conv1x1")):
+        if not (k.startswith("igemm") or k.startswith("direct_conv") or k.startswith("stem_pad") or
+                k.startswith("dwconv") or k.startswith("conv1x1")):
             continue
         t_mfma = L["work"] / (arith_peak(k) * 1e12) if not k.startswith("dwconv") else 0.0
         t_hbm = L["bytes"] / (PEAKS["hbm"][1] * 1e9)

@@ -149,6 +149,8 @@ struct DirectArgs {
                            // [c_out / 4][kh * kw * c_in][4], for the tiled kernel
   const float* wq16;       // optional (1x1, c_out % 16 == 0): the weights as [c_out / 16][c_in][16],
                            // for the 1x1 kernel's 16-channel groups
+  int w_finite;            // 1: every weight is finite (the host that holds them checked), so an
+                           // out-of-image tap may be accumulated as +0 instead of skipped
 };
 
 // 1x1 convolution (stride 1, no padding) with u8 input dequantized to f16,
@@ -274,6 +276,10 @@ int igemm_candidates(const IgemmArgs& a, int* bc, int* pb, int* tpw, int max);
 bool igemm_sibling_tile_ok(const IgemmArgs& a, int bc, int tpw, int esize);
 
 void launch_direct_conv(hipStream_t st, const DirectArgs& a);
+// true if launch_direct_conv runs a on the padded-window stem kernel (3x3,
+// stride 2, pad 1, three dense f16 channels in, u8 out, finite weights;
+// DW_STEM_PAD=0 turns it off)
+bool stem_pad_ok(const DirectArgs& a);
 bool conv1x1_u8_f16_supported(int cin, int cout);
 void launch_strided_copy(hipStream_t st, const StridedCopyArgs& a);
 void launch_broadcast_binary(hipStream_t st, const BinaryArgs& a);

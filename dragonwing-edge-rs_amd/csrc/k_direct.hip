@@ -413,6 +413,110 @@ __global__ __launch_bounds__(256) void conv_small_kernel(const DirectArgs a) {
     dx::store_outputs_t<2, OC, FE>(a, acc, oc0, (uint8_t*)a.y + yo, s_lut);
 }
 
+// The INT8 graph's stem (3x3, stride 2, pad 1, three dense f16 channels in,
+// u8 out through QuantizeLinear and the activation table): one output pixel x
+// 16 channels a thread, as conv_small_kernel, with less work per output:
+//  * no per-tap skip: an out-of-image tap is accumulated as +0.  The
+//    running sum starts at +0; fma(+0, w, acc) is acc for a finite weight w
+//    unless acc is a zero, where only the zero's sign may change, and no u8
+//    output depends on a zero's sign (a later nonzero term replaces it; a
+//    final +0 or -0 rounds to an f16 zero and quantizes to the zero point's
+//    byte).  The rows above the image load as zeros (buffer loads out of
+//    range), and the column left of the image is cleared in registers.  The
+//    host sets w_finite after checking the weights;
+//  * the input values stay packed, two halves a register, and enter each
+//    FMA as its f16 operand (v_fma_mix widens exactly, at the issue rate of
+//    the SGPR-operand FMA it replaces), unless a lane of the wave holds an
+//    f16 subnormal among them (checked on the packed registers): that wave
+//    widens every value with the reference decode (half a subnormal's IEEE
+//    value) first.
+// The FMA chain of every output is the reference's: taps in (kh, kw) order,
+// channels in order, one fmaf each (ops.rs:1356-1436).
+template <bool FE, bool SUB>
+__device__ __forceinline__ void stem_pad_accumulate(const uint32_t (&dw)[3][5], const wrow_t wbase, int cout,
+                                                    float (&acc)[16]) {
+#pragma unroll
+  for (int kh = 0; kh < 3; ++kh)
+#pragma unroll
+    for (int kw = 0; kw < 3; ++kw)
+#pragma unroll
+      for (int ic = 0; ic < 3; ++ic) {
+        const int hi = 1 + kw * 3 + ic;  // half index in the row's 20 loaded bytes (PAR 1)
+        const uint16_t hb = (uint16_t)(dw[kh][hi >> 1] >> (16 * (hi & 1)));
+        const float xv = SUB ? h2f(hb) : h2f_ieee(hb);
+        const wrow_t wr = wbase + (size_t)((kh * 3 + kw) * 3 + ic) * cout;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc[j] = fmaf(xv, wr[j], acc[j]);
+      }
+}
+
+template <bool FE>
+__global__ __launch_bounds__(256) void stem_pad_u8_kernel(const DirectArgs a) {
+  __shared__ uint8_t s_lut[256];
+  if (a.lut) s_lut[threadIdx.x] = a.lut[threadIdx.x];
+  __syncthreads();
+  const int p = blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= a.m) return;
+  const int oc0 = blockIdx.y * 16;
+  const int hw = a.ho * a.wo;
+  const int nn = p / hw;
+  const int rem = p - nn * hw;
+  const int oh = rem / a.wo;
+  const int ow = rem - oh * a.wo;
+  const int ih0 = 2 * oh - 1, iw0 = 2 * ow - 1;
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, a.x_bytes, 0x00020000);
+  // each window row: 9 halves from half index 3 iw0 of the image row, which
+  // is odd: five 4-byte loads from the boundary one half below it
+  uint32_t dw[3][5];
+#pragma unroll
+  for (int kh = 0; kh < 3; ++kh) {
+    const int ih = ih0 + kh;
+    const bool rv = (unsigned)ih < (unsigned)a.h;
+    const int off = rv ? (((nn * a.h + ih) * a.w + iw0) * 3 - 1) * 2 : (int)0x80000000;
+#pragma unroll
+    for (int i = 0; i < 5; ++i) {
+      const int o = off + 4 * i;
+      dw[kh][i] = __builtin_amdgcn_raw_buffer_load_b32(xr, o < 0 ? (int)0x80000000 : o, 0, 0);
+    }
+  }
+  if (ow == 0) {
+    // the column left of the image (halves 1..3: dword 0's high half and
+    // dword 1) holds the previous image row's last pixel: zeros
+#pragma unroll
+    for (int kh = 0; kh < 3; ++kh) {
+      dw[kh][0] &= 0xffffu;
+      dw[kh][1] = 0;
+    }
+  }
+  // any f16 subnormal among the loaded halves, in the wave:
+  // (2|h| - 2) mod 2^16 < 0x7fe
+  typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+  uint32_t mn = 0xffffffffu;
+  {
+    const uint32_t two = 0x00020002u, m2 = 0xfffefffeu;
+#pragma unroll
+    for (int kh = 0; kh < 3; ++kh)
+#pragma unroll
+      for (int i = 0; i < 5; ++i) {
+        uint32_t tv;
+        asm("v_pk_mad_u16 %0, %1, %2, %3" : "=v"(tv) : "v"(dw[kh][i]), "v"(two), "s"(m2));
+        mn = __builtin_bit_cast(uint32_t, __builtin_elementwise_min(__builtin_bit_cast(us2, mn),
+                                                                    __builtin_bit_cast(us2, tv)));
+      }
+  }
+  const bool sub = __any((mn & 0xffffu) < 0x7feu || (mn >> 16) < 0x7feu);
+  const wrow_t wbase = (wrow_t)(a.wf + oc0);
+  float acc[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
+  if (sub)
+    stem_pad_accumulate<FE, true>(dw, wbase, a.cout, acc);
+  else
+    stem_pad_accumulate<FE, false>(dw, wbase, a.cout, acc);
+  const size_t yo = (size_t)p * a.y_pix_stride + a.y_c_off + oc0;
+  dx::store_outputs_t<2, 16, FE>(a, acc, oc0, (uint8_t*)a.y + yo, s_lut);
+}
+
 // Depthwise 3x3 over f16 NHWC.  A thread owns 4 channels of a block of
 // ROWS x SEG outputs; it loads the block's input window (NR rows of NC
 // columns, 8 bytes each) up front with buffer loads (a load outside the
@@ -702,6 +806,15 @@ __global__ __launch_bounds__(256) void dwconv_kernel(const DwArgs a) {
 
 }  // namespace
 
+bool stem_pad_ok(const DirectArgs& a) {
+  const char* e = getenv("DW_STEM_PAD");
+  if (e && e[0] == '0') return false;
+  return a.kh == 3 && a.kw == 3 && a.cin == 3 && a.cout % 16 == 0 && a.in_kind == 1 && a.out_kind == 2 &&
+         a.w_finite && a.sh == 2 && a.sw == 2 && a.pt == 1 && a.pl == 1 && a.h % 2 == 0 && a.w % 2 == 0 &&
+         a.ho == a.h / 2 && a.wo == a.w / 2 && a.x_pix_stride == 3 && a.x_c_off == 0 && (uintptr_t)a.x % 4 == 0 &&
+         (long long)a.n * a.h * a.w * 6 + 16 < (1ll << 31);
+}
+
 void launch_direct_conv(hipStream_t st, const DirectArgs& a_in) {
   if (launch_conv1x1_exact(st, a_in)) return;
   DirectArgs a = a_in;
@@ -716,6 +829,17 @@ void launch_direct_conv(hipStream_t st, const DirectArgs& a_in) {
     };
     a.vec_out = aligned(16) ? 16 : (aligned(4) ? 4 : 1);
     const dim3 grid((a.m + 255) / 256, a.cout / 16);
+    if (stem_pad_ok(a)) {
+      a.x_bytes = (int)((long long)a.n * a.h * a.w * 6);
+      if (a.m > 0) {
+        if (a.fast_epi)
+          hipLaunchKernelGGL((stem_pad_u8_kernel<true>), grid, dim3(256), 0, st, a);
+        else
+          hipLaunchKernelGGL((stem_pad_u8_kernel<false>), grid, dim3(256), 0, st, a);
+        DW_HIP(hipGetLastError());
+      }
+      return;
+    }
     // row loads: dense f16 rows of even width, 4-byte aligned base, even
     // column stride (every output's first input pixel index then has the
     // parity of the left pad, so the loads start on 4-byte boundaries)

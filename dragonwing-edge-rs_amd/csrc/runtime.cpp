@@ -1903,6 +1903,14 @@ void Runtime::emit_conv(const Group& gr) {
     fail(DW_ERR_UNSUPPORTED, "runtime: conv weight dtype");
   }
   if (!a.wf) a.wf = (const float*)upload(wf.data(), wf.size() * 4);
+  {
+    bool fin = true;
+    if (W.dtype == DW_DTYPE_F32)
+      for (size_t i = 0; i < wf.size() && fin; ++i) fin = std::isfinite(wf[i]);
+    else
+      for (size_t i = 0; i < W.numel() && fin; ++i) fin = (((const uint16_t*)W.data.data())[i] & 0x7c00) != 0x7c00;
+    a.w_finite = fin ? 1 : 0;
+  }
   if (kh == 1 && kw == 1 && co % 16 == 0 && (W.dtype == DW_DTYPE_F32 || W.dtype == DW_DTYPE_F16)) {
     // the 1x1 kernel's layout: [co / 16][ci][16] (each 16-channel group's
     // weight rows contiguous)
@@ -1960,7 +1968,7 @@ void Runtime::emit_conv(const Group& gr) {
     if (const char* e = getenv("DW_QUANT_CORRECTED"))
       if (atoi(e) != 0) a.out_plain = 0;
   }
-  L.kernel = "direct_conv";
+  L.kernel = stem_pad_ok(a) ? "stem_pad_u8" : "direct_conv";
   L.bytes += (double)x.bytes() + W.numel() * 4.0 + (double)y.bytes();
   L.da = std::make_shared<DirectArgs>(a);
   L.fn = [da = L.da](hipStream_t st) { launch_direct_conv(st, *da); };
@@ -2259,6 +2267,9 @@ void Runtime::fuse_siblings() {
       Launch& LB = launches[j];
       if (!LA.ig || !LB.ig || LA.esize != 1 || LB.esize != 1) continue;
       const IgemmArgs A = *LA.ig, B = *LB.ig;
+      // the same input tensor (not only the same bytes: activations that
+      // are never live together share arena bytes)
+      if (LA.t_in.empty() || LA.t_in != LB.t_in) continue;
       if (!alone(A) || !alone(B) || !same_input(A, B)) continue;
       if (!tuned && !force) continue;
       if (tuned && (LA.tuned_ms <= 0 || LB.tuned_ms <= 0)) continue;
