@@ -110,6 +110,13 @@ struct IgemmArgs {
   void* y2;
   int y2_pix_stride, y2_c_off, split;
   const uint8_t* lut2;
+  // EPI_QU8 with a table and a residual: the QLinearAdd's two scaled
+  // operands as tables, [q] = f32((lut[q] - za) * ra) for the table input q,
+  // [256 + b] = f32((b - zb) * rb), the products qadd_u8 rounds; set by the
+  // host when every sum of two entries stays below 2^21 in magnitude (the
+  // rounding add then rounds to the nearest even integer, as rintf does).
+  // Null: qadd_u8.  Used by the chained-pair and C2f kernels.
+  const float* rtab;
 };
 
 // Arguments of the direct convolution with the reference accumulation order.

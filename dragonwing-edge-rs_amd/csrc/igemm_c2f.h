@@ -49,7 +49,7 @@ __host__ __device__ constexpr int c2f_zrow(int c) { return c + 16; }
 // [multipliers 4 cout], the 3x3 k-slice table, the four weight sets
 // (fragment order), Y1, T, Y0, the 8 waves' z rows.
 struct C2fLayout {
-  int epi[4], tab, w[4], y1, t, y0, zr, total;
+  int epi[4], tab, w[4], y1, t, y0, zr, rt, total;
 };
 __host__ __device__ inline C2fLayout c2f_layout(int c, int c2, int ks0, int ks1, int ks3, int w, int rows) {
   C2fLayout L{};
@@ -75,6 +75,8 @@ __host__ __device__ inline C2fLayout c2f_layout(int c, int c2, int ks0, int ks1,
   off += rows * w * c;
   L.zr = off;
   off += kC2fWaves * 16 * c2f_zrow(c);
+  L.rt = off;  // m.cv2's QLinearAdd tables (IgemmArgs::rtab, 2 KB)
+  off += 2048;
   L.total = off;
   return L;
 }
@@ -166,6 +168,13 @@ __global__ __launch_bounds__(kC2fThreads) void igemm_c2f_kernel(const C2fArgs p)
   if (wave == 5) load_lut(a1, smem + L.epi[1]);
   if (wave == 6) load_lut(a2, smem + L.epi[2]);
   if (wave == 7) load_lut(a3, smem + L.epi[3]);
+  // the QLinearAdd tables: 2 KB, two loads of 64 lanes from lane 0 up
+  if (RES && a2.rtab && wave == 8) {
+    __builtin_amdgcn_global_load_lds((const void*)(a2.rtab + lane * 4),
+                                     (__attribute__((address_space(3))) void*)(smem + L.rt), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((const void*)(a2.rtab + 256 + lane * 4),
+                                     (__attribute__((address_space(3))) void*)(smem + L.rt + 1024), 16, 0, 0);
+  }
 
   // ---- the 3x3 convs' k-slice offsets (same tile geometry and channels)
   for (int e = tid; e < KS1 * 4; e += kC2fThreads) {
@@ -438,8 +447,13 @@ __global__ __launch_bounds__(kC2fThreads) void igemm_c2f_kernel(const C2fArgs p)
 #pragma unroll
           for (int rr = 0; rr < 4; ++rr) {
             const int qb = requant_bits(acc[cb][pb][rr], ms4[rr], qlo2, qhi2);
-            int qi = lut2[(uint32_t)qb - (uint32_t)qbase2];
-            if constexpr (RES) qi = qadd_u8(qi, (rres >> (8 * rr)) & 0xff, a2);
+            int qi;
+            if (RES && a2.rtab) {
+              qi = qadd_u8_tab((lds_f32p)(smem + L.rt), qb - qbase2, (rres >> (8 * rr)) & 0xff, a2.zy);
+            } else {
+              qi = lut2[(uint32_t)qb - (uint32_t)qbase2];
+              if constexpr (RES) qi = qadd_u8(qi, (rres >> (8 * rr)) & 0xff, a2);
+            }
             out |= (uint32_t)qi << (8 * rr);
           }
           *reinterpret_cast<uint32_t*>(zrow + cb * 16 + cq) = out ^ a3.xxor;

@@ -149,6 +149,20 @@ __device__ __forceinline__ int qadd_u8(int qa, int rb, const IgemmArgs& a) {
   return (int)__builtin_amdgcn_fmed3f(g, 0.0f, 255.0f);
 }
 
+// qadd_u8 of the table output of requant byte qt and the residual rb from
+// the tables of IgemmArgs::rtab in LDS (rt: its 512 floats): the sum of the
+// two rounded products, rounded to the nearest even integer by adding
+// 1.5 * 2^23 (exact while the sum is below 2^22 in magnitude), the zero
+// point and the clamp to 0..255 in one med3 of the biased value, as
+// requant_bits does.
+typedef const __attribute__((address_space(3))) float* lds_f32p;
+__device__ __forceinline__ int qadd_u8_tab(lds_f32p rt, int qt, int rb, int zy) {
+  const float s = rt[qt] + rt[256 + rb];
+  const float lo = 12582912.0f - (float)zy;
+  const float t = __builtin_amdgcn_fmed3f(s + 12582912.0f, lo, lo + 255.0f);
+  return __builtin_bit_cast(int, t) - (0x4B400000 - zy);
+}
+
 // Generic epilogue for one 16x16 block: this lane holds channels ch..ch+3
 // of pixel p (channel cl..cl+3 of the tile).
 template <int ESZ, typename AccT>

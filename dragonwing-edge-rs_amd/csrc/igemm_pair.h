@@ -53,8 +53,12 @@ __host__ __device__ constexpr int pair_x_off(int c, int ks) { return pair_w_off(
 __host__ __device__ constexpr int pair_m_off(int c, int ks, int w, int rows) {
   return pair_x_off(c, ks) + (rows + 4) * (w + 2) * pair_su(c) * 16;
 }
-__host__ __device__ constexpr int pair_lds_bytes(int c, int ks, int w, int rows) {
+// and the second conv's QLinearAdd tables (IgemmArgs::rtab, 2 KB)
+__host__ __device__ constexpr int pair_rt_off(int c, int ks, int w, int rows) {
   return pair_m_off(c, ks, w, rows) + (rows + 2) * (w + 2) * pair_su(c) * 16;
+}
+__host__ __device__ constexpr int pair_lds_bytes(int c, int ks, int w, int rows) {
+  return pair_rt_off(c, ks, w, rows) + 2048;
 }
 constexpr int kPairFill = 8;  // input units each thread of a 4-wave workgroup loads at start-up (at most)
 // 16-pixel blocks a wave computes at a time (accumulators CB x PBC): 4
@@ -108,6 +112,7 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? (CB <= 2 ? 2 : 1) : 1) void igem
   uint8_t* const s_w2 = s_w1 + KS * C * 64;
   uint8_t* const s_x = smem + pair_x_off(C, KS);
   uint8_t* const s_m = smem + pair_m_off(C, KS, W, R);
+  const lds_f32p s_rt = (lds_f32p)(smem + pair_rt_off(C, KS, W, R));
 
   // ---- both weight sets (fragment order) and both epilogue blocks, direct to LDS
   const int frag_lane = ((lane & 15) * 64 + (lane >> 4) * 16);
@@ -141,6 +146,14 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? (CB <= 2 ? 2 : 1) : 1) void igem
                                      16, 0, 0);
     __builtin_amdgcn_global_load_lds((const void*)(a2.lut + lane * 16), (__attribute__((address_space(3))) void*)s_lut2,
                                      16, 0, 0);
+  }
+  // the QLinearAdd tables: 2 KB, two loads of 64 lanes from lane 0 up
+  if (RES && a2.rtab && wave == 3) {
+    __builtin_amdgcn_global_load_lds((const void*)(a2.rtab + lane * 4),
+                                     (__attribute__((address_space(3))) void*)(smem + pair_rt_off(C, KS, W, R)), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((const void*)(a2.rtab + 256 + lane * 4),
+                                     (__attribute__((address_space(3))) void*)(smem + pair_rt_off(C, KS, W, R) + 1024), 16,
+                                     0, 0);
   }
 
   // ---- input tile: rows r0 - 2 .. r0 + R + 1, columns -1 .. W, raw
@@ -335,8 +348,13 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? (CB <= 2 ? 2 : 1) : 1) void igem
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int qb = requant_bits(acc[cb][pb][r], ms4[r], qlo, qhi);
-            int qi = lut3[(uint32_t)qb - (uint32_t)qbase];
-            if constexpr (RES) qi = qadd_u8(qi, (rres >> (8 * r)) & 0xff, a2);
+            int qi;
+            if (RES && a2.rtab) {
+              qi = qadd_u8_tab(s_rt, qb - qbase, (rres >> (8 * r)) & 0xff, a2.zy);
+            } else {
+              qi = lut3[(uint32_t)qb - (uint32_t)qbase];
+              if constexpr (RES) qi = qadd_u8(qi, (rres >> (8 * r)) & 0xff, a2);
+            }
             out |= (uint32_t)qi << (8 * r);
           }
           uint8_t* yrow = (uint8_t*)a2.y + (size_t)pixel[pb] * a2.y_pix_stride + a2.y_c_off + cb * 16 + cq;

@@ -2033,9 +2033,9 @@ void Runtime::emit_qconv(const Group& gr) {
   L.op = join_names(g, gr.ops);
   L.work = 2.0 * (double)y.pixels() * co * kh * kw * ci;
   L.bytes = (double)x.bytes() + W.data.size() + (double)y.pixels() * co;
+  uint8_t lut[256];
   if (gr.lut) {
     const RtTensor& lo = T(gr.lut_out);
-    uint8_t lut[256];
     build_silu_lut(lut, pre.scale, pre.zp, lo.scale, lo.zp);
     a.lut = (const uint8_t*)upload(lut, 256);
   }
@@ -2053,6 +2053,23 @@ void Runtime::emit_qconv(const Group& gr) {
     a.zb = r.zp;
     a.zy = y.zp;
     L.bytes += r.bytes();
+    // the QLinearAdd's rounded products as tables (the kernels that take
+    // them add two entries instead of converting and multiplying): the same
+    // f32 products qadd_u8 forms, kept when every sum of two entries stays
+    // below 2^21 in magnitude; DW_QADD_TABLES=0 keeps qadd_u8
+    const char* qt = getenv("DW_QADD_TABLES");
+    if (gr.lut && !(qt && qt[0] == '0')) {
+      float rt[512];
+      float ma = 0.0f, mb = 0.0f;
+      for (int q = 0; q < 256; ++q) {
+        rt[q] = (float)((int)lut[q] - a.za) * a.ra;
+        rt[256 + q] = (float)(q - a.zb) * a.rb;
+        ma = std::max(ma, std::fabs(rt[q]));
+        mb = std::max(mb, std::fabs(rt[256 + q]));
+      }
+      if (std::isfinite(ma) && std::isfinite(mb) && ma + mb < 2097152.0f)
+        a.rtab = (const float*)upload(rt, sizeof rt);
+    }
   }
   DW_HIP(hipStreamSynchronize(be->stream));
   L.t_in = gr.in;
