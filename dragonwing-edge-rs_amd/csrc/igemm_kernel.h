@@ -303,9 +303,11 @@ __device__ __forceinline__ const uint8_t* tile_lut(const IgemmArgs& a, int c0) {
 }
 
 // LDS rows the int8 epilogue uses to regroup results (per wave: 16 pixels
-// x (BC + 16) bytes; the 16-byte pad puts the 64 lanes' 4-byte writes in 64
-// distinct banks).
-__host__ __device__ constexpr int xpose_row(int bc) { return bc + 16; }
+// x xpose_row(BC) bytes).  A row of d dwords puts the 64 lanes' 4-byte writes
+// (16 pixels x 4 channel quads, dwords d * i + j) in 64 distinct banks when
+// d = 4 (mod 8): BC + 16 bytes for BC a multiple of 32, BC bytes otherwise
+// (48, 80).
+__host__ __device__ constexpr int xpose_row(int bc) { return bc % 32 == 0 ? bc + 16 : bc; }
 __host__ __device__ constexpr int xpose_bytes(int bc) { return 4 * 16 * xpose_row(bc); }
 
 // EPV_QU8_LUT_HEAD: the tile holds every channel of its pixels (BC >= the
