@@ -102,11 +102,11 @@ struct IgemmArgs {
   int h_cout, h_y_pix_stride, h_y_c_off, h_act;
   float h_scale;            // the u8 results' quantization (the 1x1's input)
   int h_zp;
-  // Two sibling QLinearConvs (same input, same geometry) as one GEMM: the
-  // channels from `split` on are the second conv's (its weights, bias' and
+  // Two sibling convs (same input, same geometry) as one GEMM: the channels
+  // from `split` on are the second conv's (its weights, bias' and
   // multipliers follow the first's), stored to their own output view y2
-  // with their own table lut2; every channel tile lies wholly on one side
-  // (split % channel tile == 0).  y2 null: one conv.
+  // (u8: with their own table lut2); every channel tile lies wholly on one
+  // side (split % channel tile == 0).  y2 null: one conv.
   void* y2;
   int y2_pix_stride, y2_c_off, split;
   const uint8_t* lut2;
@@ -279,7 +279,8 @@ int igemm_channel_tile(int cout);
 // wave); returns how many were written (at most `max`).
 int igemm_candidates(const IgemmArgs& a, int* bc, int* pb, int* tpw, int max);
 // whether a sibling GEMM (a.y2 set) may run on channel tile bc of kernel
-// family tpw (staged 0, streamed -1, band -4 / -5)
+// family tpw (int8: staged 0, streamed -1, band -4 / -5; fp16: every family
+// but the persistent small-K kernel)
 bool igemm_sibling_tile_ok(const IgemmArgs& a, int bc, int tpw, int esize);
 
 void launch_direct_conv(hipStream_t st, const DirectArgs& a);

@@ -225,7 +225,10 @@ __device__ __forceinline__ void epilogue4(const IgemmArgs& a, const EpiLds& e, c
       p23 = p23 + __builtin_bit_cast(h16x2, rres.y);
     }
     const uint2 out = make_uint2(__builtin_bit_cast(uint32_t, p01), __builtin_bit_cast(uint32_t, p23));
-    *reinterpret_cast<uint2*>((uint16_t*)a.y + yo) = out;
+    if (a.y2 && ch >= a.split)  // a sibling GEMM's second conv: its own output view
+      *reinterpret_cast<uint2*>((uint16_t*)a.y2 + (size_t)p * a.y2_pix_stride + a.y2_c_off + (ch - a.split)) = out;
+    else
+      *reinterpret_cast<uint2*>((uint16_t*)a.y + yo) = out;
     if (a.y_up) {
       // the nearest 2x upsample: the same values at the pixel's four pixels
       const int hw = a.ho * a.wo;

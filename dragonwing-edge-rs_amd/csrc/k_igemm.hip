@@ -274,9 +274,13 @@ int epilogue_variant(const IgemmArgs& a, int esize) {
 int igemm_channel_tile(int cout) { return channel_tile(cout); }
 
 bool igemm_sibling_tile_ok(const IgemmArgs& a, int bc, int tpw, int esize) {
-  return esize == 1 && a.epi == EPI_QU8 && a.lut && a.lut2 && !a.res && !a.y_up && !a.h_wfrag &&
-         (tpw == 0 || tpw == -1 || tpw == -4 || tpw == -5) && bc > 0 && a.split > 0 && a.split % bc == 0 &&
-         a.split < a.cout && a.y2_pix_stride % 4 == 0 && a.y2_c_off % 4 == 0;
+  const bool common = !a.res && !a.y_up && !a.h_wfrag && bc > 0 && a.split > 0 && a.split % bc == 0 &&
+                      a.split < a.cout && a.y2_pix_stride % 4 == 0 && a.y2_c_off % 4 == 0;
+  if (esize == 1)  // the u8 table epilogue (its table staged per channel tile)
+    return common && a.epi == EPI_QU8 && a.lut && a.lut2 && (tpw == 0 || tpw == -1 || tpw == -4 || tpw == -5);
+  // fp16: the generic epilogue chooses the view per four channels; every
+  // kernel storing through igemm_store (not the persistent small-K kernel)
+  return common && esize == 2 && a.epi == EPI_F16 && tpw <= 0;
 }
 
 int igemm_candidates(const IgemmArgs& a, int* bc, int* pb, int* tpw, int max) {

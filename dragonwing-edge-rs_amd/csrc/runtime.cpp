@@ -134,6 +134,14 @@ struct Runtime {
   size_t act_bytes = 0;           // the activation arena
   size_t act_bytes_unshared = 0;  // what the roots would take without reuse
   std::vector<Launch> launches;
+  // the sibling fusions in the order made: the fused launch's position, the
+  // two launches it replaced and the second one's former position (undone
+  // last first, they restore the list)
+  struct SibUndo {
+    size_t pos, jpos;
+    Launch a, b;
+  };
+  std::vector<SibUndo> sib_undo;
   std::vector<std::string> info;
   bool capture = false;
   hipGraph_t hgraph = nullptr;
@@ -432,6 +440,30 @@ void Runtime::build(Backend* b, const GraphIR& graph, bool stats_mode) {
     if (const char* lp = getenv("DW_AUTOTUNE_LOG"))
       if (FILE* log = fopen(lp, "a")) {
         fprintf(log, "graph\t%d streams\t%.2f\ngraph\t1 stream\t%.2f\n", ns, t_multi * 1e3f, t_one * 1e3f);
+        fclose(log);
+      }
+  }
+  // sibling GEMMs were kept by timing each alone; on several streams the two
+  // convs they replace may already run concurrently, so the whole graph is
+  // timed with them and without them (on the chosen stream count), and the
+  // faster list kept
+  if (!sib_undo.empty() && !stats && tuned) {
+    const int nsel = nstreams;
+    const float t_sib = time_graph();
+    std::vector<Launch> fused = launches;
+    for (auto it = sib_undo.rbegin(); it != sib_undo.rend(); ++it) {
+      launches[it->pos] = it->a;
+      launches.insert(launches.begin() + (long)it->jpos, it->b);
+    }
+    plan_streams(nsel);
+    const float t_apart = time_graph();
+    if (t_sib <= t_apart) {
+      launches = fused;
+      plan_streams(nsel);
+    }
+    if (const char* lp = getenv("DW_AUTOTUNE_LOG"))
+      if (FILE* log = fopen(lp, "a")) {
+        fprintf(log, "graph\tsibling GEMMs\t%.2f\ngraph\tsiblings apart\t%.2f\n", t_sib * 1e3f, t_apart * 1e3f);
         fclose(log);
       }
   }
@@ -2198,12 +2230,13 @@ void Runtime::fuse_pairs() {
   (void)hipEventDestroy(e1);
 }
 
-// Sibling QLinearConvs in one launch: two convs that read the same input
-// view with the same geometry, each with the table epilogue and no residual
-// (the box0 and cls0 convs of a detect scale), as one GEMM over both channel
-// sets: the second conv's channels after the first's (packed weights, bias'
-// and multipliers concatenated on the device), each channel tile writing its
-// own conv's output view with its own table.  Every output is computed as
+// Sibling convs in one launch: two convs that read the same input tensor
+// with the same geometry, each with the u8 table epilogue (QLinearConv) or
+// the same f16 epilogue (fp16 Conv) and no residual (the box0 and cls0 convs
+// of a detect scale), as one GEMM over both channel sets: the second conv's
+// channels after the first's (packed weights, bias' and multipliers
+// concatenated on the device), each channel tile writing its own conv's
+// output view (u8: with its own table).  Every output is computed as
 // its own conv computes it, so the bytes are the two launches'.  Both orders
 // and every staged, streamed-weight and band tile whose channel tiles do not
 // straddle the first conv's channels are timed; the fastest is kept if it
@@ -2223,9 +2256,12 @@ void Runtime::fuse_siblings() {
   hipEvent_t e0 = nullptr, e1 = nullptr;
   DW_HIP(hipEventCreate(&e0));
   DW_HIP(hipEventCreate(&e1));
-  auto alone = [](const IgemmArgs& a) {
-    return a.epi == EPI_QU8 && a.lut && a.bias_i && a.mscale && !a.res && !a.y_up && !a.h_wfrag && !a.y2 &&
-           a.cout % 16 == 0;
+  // u8: the table epilogue; fp16: the f16 epilogue with its bias (the two
+  // convs' activations compared below)
+  auto alone = [](const IgemmArgs& a, int esize) {
+    const bool base = !a.res && !a.y_up && !a.h_wfrag && !a.y2 && a.cout % 16 == 0;
+    return esize == 1 ? base && a.epi == EPI_QU8 && a.lut && a.bias_i && a.mscale
+                      : base && a.epi == EPI_F16 && a.bias_h;
   };
   auto same_input = [](const IgemmArgs& a, const IgemmArgs& b) {
     return a.x == b.x && a.x_pix_stride == b.x_pix_stride && a.x_c_off == b.x_c_off && a.n == b.n && a.h == b.h &&
@@ -2233,12 +2269,12 @@ void Runtime::fuse_siblings() {
            a.pt == b.pt && a.pl == b.pl && a.ho == b.ho && a.wo == b.wo && a.ksteps == b.ksteps &&
            a.xpad == b.xpad && a.xxor == b.xxor && a.y_zp == b.y_zp;
   };
-  auto time4 = [&](const IgemmArgs& a) {
-    launch_igemm(st, a, 1);
+  auto time4 = [&](const IgemmArgs& a, int esize) {
+    launch_igemm(st, a, esize);
     float t_min = 1e30f;
     for (int r = 0; r < 3; ++r) {
       DW_HIP(hipEventRecord(e0, st));
-      for (int k = 0; k < 4; ++k) launch_igemm(st, a, 1);
+      for (int k = 0; k < 4; ++k) launch_igemm(st, a, esize);
       DW_HIP(hipEventRecord(e1, st));
       DW_HIP(hipEventSynchronize(e1));
       float ms = 0;
@@ -2249,7 +2285,7 @@ void Runtime::fuse_siblings() {
   };
   // F's channels, then S's, at channel tile width bc: the combined
   // arguments (packed weights zero-padded to a whole tile)
-  auto combine = [&](const IgemmArgs& F, const IgemmArgs& S, int bc) {
+  auto combine = [&](const IgemmArgs& F, const IgemmArgs& S, int bc, int esize) {
     IgemmArgs C = F;
     C.cout = F.cout + S.cout;
     C.split = F.cout;
@@ -2261,16 +2297,23 @@ void Runtime::fuse_siblings() {
                             hipMemcpyDeviceToDevice, st));
     DW_HIP(hipMemcpy2DAsync(wpk + F.cout * row, C.cout_pad * row, S.wpk, S.cout_pad * row, S.cout * row, ks,
                             hipMemcpyDeviceToDevice, st));
-    int* bias = (int*)dalloc(C.cout_pad * sizeof(int));
-    float* ms = (float*)dalloc(C.cout_pad * sizeof(float));
-    DW_HIP(hipMemcpyAsync(bias, F.bias_i, F.cout * sizeof(int), hipMemcpyDeviceToDevice, st));
-    DW_HIP(hipMemcpyAsync(bias + F.cout, S.bias_i, S.cout * sizeof(int), hipMemcpyDeviceToDevice, st));
-    DW_HIP(hipMemcpyAsync(ms, F.mscale, F.cout * sizeof(float), hipMemcpyDeviceToDevice, st));
-    DW_HIP(hipMemcpyAsync(ms + F.cout, S.mscale, S.cout * sizeof(float), hipMemcpyDeviceToDevice, st));
+    if (esize == 1) {
+      int* bias = (int*)dalloc(C.cout_pad * sizeof(int));
+      float* ms = (float*)dalloc(C.cout_pad * sizeof(float));
+      DW_HIP(hipMemcpyAsync(bias, F.bias_i, F.cout * sizeof(int), hipMemcpyDeviceToDevice, st));
+      DW_HIP(hipMemcpyAsync(bias + F.cout, S.bias_i, S.cout * sizeof(int), hipMemcpyDeviceToDevice, st));
+      DW_HIP(hipMemcpyAsync(ms, F.mscale, F.cout * sizeof(float), hipMemcpyDeviceToDevice, st));
+      DW_HIP(hipMemcpyAsync(ms + F.cout, S.mscale, S.cout * sizeof(float), hipMemcpyDeviceToDevice, st));
+      C.bias_i = bias;
+      C.mscale = ms;
+    } else {
+      uint16_t* bh = (uint16_t*)dalloc(C.cout_pad * sizeof(uint16_t));
+      DW_HIP(hipMemcpyAsync(bh, F.bias_h, F.cout * sizeof(uint16_t), hipMemcpyDeviceToDevice, st));
+      DW_HIP(hipMemcpyAsync(bh + F.cout, S.bias_h, S.cout * sizeof(uint16_t), hipMemcpyDeviceToDevice, st));
+      C.bias_h = bh;
+    }
     DW_HIP(hipStreamSynchronize(st));
     C.wpk = wpk;
-    C.bias_i = bias;
-    C.mscale = ms;
     C.y2 = S.y;
     C.y2_pix_stride = S.y_pix_stride;
     C.y2_c_off = S.y_c_off;
@@ -2282,12 +2325,13 @@ void Runtime::fuse_siblings() {
     for (size_t j = i + 1; j < launches.size(); ++j) {
       Launch& LA = launches[i];
       Launch& LB = launches[j];
-      if (!LA.ig || !LB.ig || LA.esize != 1 || LB.esize != 1) continue;
+      const int es = LA.esize;
+      if (!LA.ig || !LB.ig || (es != 1 && es != 2) || LB.esize != es) continue;
       const IgemmArgs A = *LA.ig, B = *LB.ig;
       // the same input tensor (not only the same bytes: activations that
       // are never live together share arena bytes)
       if (LA.t_in.empty() || LA.t_in != LB.t_in) continue;
-      if (!alone(A) || !alone(B) || !same_input(A, B)) continue;
+      if (!alone(A, es) || !alone(B, es) || !same_input(A, B) || A.act != B.act) continue;
       if (!tuned && !force) continue;
       if (tuned && (LA.tuned_ms <= 0 || LB.tuned_ms <= 0)) continue;
       float best = 1e30f;
@@ -2300,18 +2344,18 @@ void Runtime::fuse_siblings() {
         if (keep && !listed(keep, LF.op)) continue;
         for (int bw : {128, 96, 80, 64, 48, 32, 16}) {
           if (F.cout % bw != 0) continue;
-          IgemmArgs C = combine(F, S, bw);
+          IgemmArgs C = combine(F, S, bw, es);
           int bc[64], pb[64], tpw[64];
           const int n = igemm_candidates(C, bc, pb, tpw, 64);
           for (int k = 0; k < n; ++k) {
-            if (bc[k] != bw || !igemm_sibling_tile_ok(C, bc[k], tpw[k], 1)) continue;
+            if (bc[k] != bw || !igemm_sibling_tile_ok(C, bc[k], tpw[k], es)) continue;
             C.tile_bc = bc[k];
             C.tile_pb = pb[k];
             C.tile_tpw = tpw[k];
-            const float t = tuned ? time4(C) : 0.0f;
+            const float t = tuned ? time4(C, es) : 0.0f;
             if (log)
               fprintf(log, "%s+%s\t%s\t%.2f\n", LF.op.c_str(), (order == 0 ? LB : LA).op.c_str(),
-                      igemm_tile_name(C, 1), t * 1e3f / 4);
+                      igemm_tile_name(C, es), t * 1e3f / 4);
             if (t < best) {
               best = t;
               bestC = C;
@@ -2328,14 +2372,14 @@ void Runtime::fuse_siblings() {
       const Launch& LS = first_a ? LB : LA;
       Launch P;
       P.ig = std::make_shared<IgemmArgs>(bestC);
-      P.kernel = igemm_tile_name(bestC, 1);
+      P.kernel = igemm_tile_name(bestC, es);
       P.op = LF.op + "+" + LS.op;
       P.work = LA.work + LB.work;
       // the input read once
-      P.bytes = LA.bytes + LB.bytes - (double)A.n * A.h * A.w * A.cin;
+      P.bytes = LA.bytes + LB.bytes - (double)A.n * A.h * A.w * A.cin * es;
       auto ig = P.ig;
-      P.fn = [ig](hipStream_t s) { launch_igemm(s, *ig, 1); };
-      P.esize = 1;
+      P.fn = [ig, es](hipStream_t s) { launch_igemm(s, *ig, es); };
+      P.esize = es;
       P.group = LA.group;
       P.reads = LA.reads;
       P.reads.insert(P.reads.end(), LB.reads.begin(), LB.reads.end());
@@ -2343,6 +2387,7 @@ void Runtime::fuse_siblings() {
       P.writes.insert(P.writes.end(), LB.writes.begin(), LB.writes.end());
       P.t_in = LA.t_in;
       P.tuned_ms = best;
+      if (!force) sib_undo.push_back({i, j, LA, LB});
       launches[i] = P;
       launches.erase(launches.begin() + (long)j);
       break;

@@ -923,6 +923,34 @@ def test_int8_graph_siblings_bit_exact(backend, int8_small, monkeypatch):
         assert gv.tobytes() == g0.tobytes(), o
 
 
+@pytest.mark.parametrize("size,batch", [(96, 2), (640, 32)])
+def test_f16_graph_siblings_same_bytes(backend, monkeypatch, size, batch):
+    # The fp16 graph's box0 and cls0 of each detect scale as one GEMM
+    # (DW_SIB=1) and as two launches (=0): every output is summed over K in
+    # the same k-step order either way, so the same f16 values; within the
+    # fp16 tolerance of the oracle at the small size.
+    g, info = yolo.f16_graph(batch=batch, size=size)
+    x = yolo.input_images(batch, size)
+    outs = {}
+    for mode in ("0", "1"):
+        monkeypatch.setenv("DW_SIB", mode)
+        rt = HipGraphRuntime(g, backend)
+        sib = [L["ops"] for L in rt.launches() if L["kernel"].endswith("_sib")]
+        print(f"{size} DW_SIB={mode}: {len(sib)} sibling launches", flush=True)
+        assert len(sib) == (3 if mode == "1" else 0), sib
+        assert all("box0" in o and "cls0" in o for o in sib), sib
+        rt.set_input_f32(info["input"], x)
+        rt.run()
+        outs[mode] = gpu_outputs(rt, info)
+        del rt
+    for o, a, b in zip(info["outputs"], outs["0"], outs["1"]):
+        np.testing.assert_array_equal(a, b, err_msg=o)
+    if size == 96:
+        ref = oracle_run(g, {info["input"]: synth.f16_bits(x)})
+        for o, gv in zip(info["outputs"], outs["1"]):
+            assert rel_err(oracle.f16_to_f32(gv), oracle.f16_to_f32(ref[o])) <= 1e-2, o
+
+
 def test_int8_benchmark_graph_siblings_same_bytes(backend, monkeypatch):
     # the benchmark's 640 x 640 batch-32 graph with every sibling pair fused
     # and with none: the same bytes on every output
