@@ -1,5 +1,5 @@
-// Band-tile implicit GEMM for 3x3 convolutions (stride 1, padding 1, int8
-// or fp16): one workgroup of 8 or 16 waves owns R whole output rows of one image
+// Band-tile implicit GEMM for 3x3 convolutions (stride 1 or 2, padding 1,
+// int8 or fp16): one workgroup of 8 or 16 waves owns R whole output rows of one image
 // (R chosen by the graph runtime's tuner, a divisor of the height) and BC
 // output channels, so a layer runs as one round of workgroups, about one a
 // CU, whatever its width.
@@ -21,9 +21,10 @@
 //
 // LDS layout: epilogue data [table 256][bias' 4 BC][multipliers 4 BC], the
 // k-slice offsets, the weights (fragment order, [k-step][block][64 lanes x
-// 16 B]), the input tile ((R + 2) x (W + 2) pixels of SU 16-byte units, SU =
-// c_in * esize / 16 made odd: 8 consecutive pixels' units fall in 8
-// distinct bank groups), the waves' regroup rows.
+// 16 B]), the input tile (S (R - 1) + 3 rows of S (W - 1) + 3 pixels for
+// output rows W wide at stride S, pixels of SU 16-byte units, SU = c_in *
+// esize / 16 made odd: 8 consecutive pixels' units fall in 8 distinct bank
+// groups), the waves' regroup rows.
 //
 // The per-output arithmetic and the epilogues are igemm_kernel's
 // (igemm_store), and integer sums do not depend on the k-order, so int8
@@ -56,12 +57,18 @@ __host__ __device__ constexpr int band_su(int cu) { return cu | 1; }
 __host__ __device__ constexpr int band_tab_off(int bc) { return 256 + 8 * bc; }
 __host__ __device__ constexpr int band_w_off(int bc, int ks) { return (band_tab_off(bc) + ks * 16 + 15) / 16 * 16; }
 __host__ __device__ constexpr int band_x_off(int bc, int ks) { return band_w_off(bc, ks) + ks * bc * 64; }
-__host__ __device__ constexpr int band_tile_bytes(int rows, int w, int cu) { return (rows + 2) * (w + 2) * band_su(cu) * 16; }
-__host__ __device__ constexpr int band_xp_off(int bc, int ks, int rows, int w, int cu) {
-  return band_x_off(bc, ks) + band_tile_bytes(rows, w, cu);
+// input tile of a band of `rows` output rows `wo` pixels wide at stride s
+// (1 or 2): s (rows - 1) + 3 input rows of s (wo - 1) + 3 columns
+__host__ __device__ constexpr int band_tile_rows(int rows, int s) { return s * (rows - 1) + 3; }
+__host__ __device__ constexpr int band_tile_w(int wo, int s) { return s * (wo - 1) + 3; }
+__host__ __device__ constexpr int band_tile_bytes(int rows, int wo, int cu, int s) {
+  return band_tile_rows(rows, s) * band_tile_w(wo, s) * band_su(cu) * 16;
 }
-inline size_t band_lds_bytes(int bc, int ks, int rows, int w, int cu, int nw) {
-  return (size_t)band_xp_off(bc, ks, rows, w, cu) + (size_t)nw * 16 * xpose_row(bc);
+__host__ __device__ constexpr int band_xp_off(int bc, int ks, int rows, int wo, int cu, int s) {
+  return band_x_off(bc, ks) + band_tile_bytes(rows, wo, cu, s);
+}
+inline size_t band_lds_bytes(int bc, int ks, int rows, int wo, int cu, int nw, int s) {
+  return (size_t)band_xp_off(bc, ks, rows, wo, cu, s) + (size_t)nw * 16 * xpose_row(bc);
 }
 
 template <int ESZ, int BC, int EPV, int NW>
@@ -77,8 +84,10 @@ __global__ __launch_bounds__(64 * NW) void igemm_band_kernel(const IgemmArgs a) 
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
   const int KSTEPS = a.ksteps, COUTP = a.cout_pad, CIN = a.cin;
-  const int W = a.w, H = a.h, R = a.band_rows;
-  const int TW = W + 2;
+  const int W = a.wo, H = a.ho, R = a.band_rows;  // output map and band height
+  const int S = a.sh;                             // stride, 1 or 2 (both axes)
+  const int TW = band_tile_w(W, S);
+  const int TE = (TW + 1) >> 1;  // stride 2: the tile's even columns, stored first
   const int CU = CIN * ESZ / 16;  // 16-byte units per pixel
   const int SU = band_su(CU);
 
@@ -106,7 +115,7 @@ __global__ __launch_bounds__(64 * NW) void igemm_band_kernel(const IgemmArgs a) 
   int* const s_tab = reinterpret_cast<int*>(smem + band_tab_off(BC));
   uint8_t* const s_w = smem + band_w_off(BC, KSTEPS);
   uint8_t* const s_x = smem + band_x_off(BC, KSTEPS);
-  uint8_t* const s_xp = smem + band_xp_off(BC, KSTEPS, R, W, CU);
+  uint8_t* const s_xp = smem + band_xp_off(BC, KSTEPS, R, W, CU, S);
 
   // ---- weights (all of K, fragment order) and epilogue data, direct to LDS
   const int frag_lane = ((lane & 15) * 64 + (lane >> 4) * 16);
@@ -141,11 +150,14 @@ __global__ __launch_bounds__(64 * NW) void igemm_band_kernel(const IgemmArgs a) 
                                        (__attribute__((address_space(3))) void*)s_bias, 4, 0, 0);
   }
 
-  // ---- input tile: rows r0 - 1 .. r0 + R, columns -1 .. W, raw 16-byte
-  // units (out-of-image units: out-of-range loads, which return zero), all
-  // in flight together
+  // ---- input tile: input rows S r0 - 1 .. S (r0 + R - 1) + 1, columns
+  // -1 .. S (W - 1) + 1, raw 16-byte units (out-of-image units: out-of-range
+  // loads, which return zero), all in flight together.  At stride 2 a row
+  // keeps its even columns first, then its odd ones, so the pixels a tap
+  // reads for consecutive output pixels stay one pixel (SU units) apart.
+  const int IH = a.h, IW = a.w;
   const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, a.x_bytes, 0x00020000);
-  const int units = (R + 2) * TW * CU;
+  const int units = band_tile_rows(R, S) * TW * CU;
   const float r_cu = 1.0f / (float)CU, r_tw = 1.0f / (float)TW;
   u32x4 xv[FILL];
   int xdst[FILL];  // LDS offset of the unit, or -1 for none
@@ -159,12 +171,13 @@ __global__ __launch_bounds__(64 * NW) void igemm_band_kernel(const IgemmArgs a) 
       const int ip = div_small(u, CU, r_cu);
       const int cu = u - ip * CU;
       const int tr = div_small(ip, TW, r_tw), tc = ip - tr * TW;
-      const int ih = r0 - 1 + tr, iw = tc - 1;
-      const bool ok = (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W;
+      const int ih = S * r0 - 1 + tr, iw = tc - 1;
+      const bool ok = (unsigned)ih < (unsigned)IH && (unsigned)iw < (unsigned)IW;
       // byte offset: the view's element offset times the element size
-      const int off = ok ? ((((n * H + ih) * W + iw) * a.x_pix_stride + a.x_c_off) * ESZ + cu * 16) : (int)0x80000000;
+      const int off = ok ? ((((n * IH + ih) * IW + iw) * a.x_pix_stride + a.x_c_off) * ESZ + cu * 16) : (int)0x80000000;
       xv[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrsrc, off, 0, 0));
-      xdst[i] = (ip * SU + cu) * 16;
+      const int pos = S == 1 ? tc : ((tc & 1) ? TE + (tc >> 1) : (tc >> 1));
+      xdst[i] = ((tr * TW + pos) * SU + cu) * 16;
       xin[i] = ok;
     }
   }
@@ -178,7 +191,8 @@ __global__ __launch_bounds__(64 * NW) void igemm_band_kernel(const IgemmArgs a) 
     if (k < 9 * CIN) {
       const int tap = k / CIN, ci = k - (k / CIN) * CIN;
       const int kh = tap / 3, kw = tap - (tap / 3) * 3;
-      off = ((kh * TW + kw) * SU + ci * ESZ / 16) * 16;
+      const int kc = S == 1 ? kw : ((kw & 1) ? TE : (kw >> 1));  // column position from the pixel's
+      off = ((kh * TW + kc) * SU + ci * ESZ / 16) * 16;
     }
     s_tab[e] = off;
   }
@@ -216,7 +230,7 @@ __global__ __launch_bounds__(64 * NW) void igemm_band_kernel(const IgemmArgs a) 
       const int pl = (b0 + pb) * 16 + (lane & 15);
       const int q = (pb < nvb && pl < np) ? pl : 0;
       const int r = div_small(q, W, a.r_wo), c = q - r * W;
-      pbase[pb] = (r * TW + c) * SU * 16;
+      pbase[pb] = (S * r * TW + c) * SU * 16;
     }
     acc_t acc[CB][PBC];
 #pragma unroll
@@ -268,8 +282,8 @@ __global__ __launch_bounds__(64 * NW) void igemm_band_kernel(const IgemmArgs a) 
 template <int ESZ, int BC, int EPV, int NW>
 void launch_band_bc(hipStream_t st, const IgemmArgs& a, const TileCfg& t) {
   const int rows = a.band_rows;
-  const dim3 grid((unsigned)(a.n * (a.h / rows) * (a.cout_pad / t.bc)));
-  const size_t lds = band_lds_bytes(t.bc, a.ksteps, rows, a.w, a.cin * ESZ / 16, NW);
+  const dim3 grid((unsigned)(a.n * (a.ho / rows) * (a.cout_pad / t.bc)));
+  const size_t lds = band_lds_bytes(t.bc, a.ksteps, rows, a.wo, a.cin * ESZ / 16, NW, a.sh);
   hipLaunchKernelGGL((igemm_band_kernel<ESZ, BC, EPV, NW>), grid, dim3(64 * NW), lds, st, a);
 }
 

@@ -143,24 +143,29 @@ TileCfg make_wide_tile(const IgemmArgs& a, int bc) {
 }
 
 // The band-tile kernel (tpw = -4: 8 waves, -5: 16 waves; pb = its band
-// height R): 3x3, stride 1, padding 1, R whole rows (R divides H) of at
-// least one 16-pixel block per wave, the input tile within the start-up
-// loads, everything within LDS.
+// height R): 3x3, stride 1 or 2 on both axes, padding 1 (the output map
+// (h - 1) / s + 1 by (w - 1) / s + 1), R whole output rows (R divides the
+// output height) of at least one 16-pixel block per wave, the input tile
+// within the start-up loads, everything within LDS.
 int band_waves(int tpw) { return tpw == -5 ? 16 : 8; }
 
 bool band_ok(const IgemmArgs& a, int bc, int rows, int tpw = -4) {
   const int es = a.epi == EPI_F16 ? 2 : 1;
   const int nw = band_waves(tpw);
-  if (a.kh != 3 || a.kw != 3 || a.sh != 1 || a.sw != 1 || a.pt != 1 || a.pl != 1) return false;
-  if (a.ho != a.h || a.wo != a.w || (a.cin * es) % 16 != 0 || a.w <= 0) return false;
+  const int s = a.sh;
+  // DW_BAND_S2=0: no stride-2 band tiles (plan comparisons)
+  static const bool s2_on = !(getenv("DW_BAND_S2") && atoi(getenv("DW_BAND_S2")) == 0);
+  if (a.kh != 3 || a.kw != 3 || !(s == 1 || (s == 2 && s2_on)) || a.sw != s || a.pt != 1 || a.pl != 1) return false;
+  if (a.h <= 0 || a.w <= 0 || a.ho != (a.h - 1) / s + 1 || a.wo != (a.w - 1) / s + 1) return false;
+  if ((a.cin * es) % 16 != 0) return false;
   if (!(bc == 128 || bc == 80 || bc == 64 || bc == 32 || bc == 16) || a.cout_pad % bc != 0) return false;
   // 16 waves over 64 channels: only the u8 requantize and table epilogues
   // without a residual fit 128 VGPRs
   if (nw == 16 && bc > 64 && !(es == 1 && a.epi == EPI_QU8 && !a.res && !a.h_wfrag)) return false;
-  if (rows < 1 || a.h % rows != 0 || rows * a.w < 16 * nw) return false;
+  if (rows < 1 || a.ho % rows != 0 || rows * a.wo < 16 * nw) return false;
   const int cu = a.cin * es / 16;
-  if ((rows + 2) * (a.w + 2) * cu > ig::kBandFill * 512) return false;
-  return ig::band_lds_bytes(bc, a.ksteps, rows, a.w, cu, nw) <= 160 * 1024;
+  if ((long)ig::band_tile_rows(rows, s) * ig::band_tile_w(a.wo, s) * cu > ig::kBandFill * 512) return false;
+  return ig::band_lds_bytes(bc, a.ksteps, rows, a.wo, cu, nw, s) <= 160 * 1024;
 }
 
 TileCfg make_band_tile(const IgemmArgs& a, int bc, int rows, int tpw = -4) {
@@ -175,9 +180,9 @@ TileCfg make_band_tile(const IgemmArgs& a, int bc, int rows, int tpw = -4) {
 // give between 96 and 768 workgroups (about one a CU up to three), at most 5.
 int band_heights(const IgemmArgs& a, int bc, int tpw, int* rows, int max) {
   int n = 0;
-  for (int r = 1; r <= a.h && n < max; ++r) {
+  for (int r = 1; r <= a.ho && n < max; ++r) {
     if (!band_ok(a, bc, r, tpw)) continue;
-    const long wgs = (long)a.n * (a.h / r) * (a.cout_pad / bc);
+    const long wgs = (long)a.n * (a.ho / r) * (a.cout_pad / bc);
     if (wgs >= 96 && wgs <= 768) rows[n++] = r;
   }
   return n;
@@ -407,7 +412,7 @@ void launch_igemm(hipStream_t st, const IgemmArgs& a_in, int esize) {
                      : t.tpw == -2 ? ig::rows_lds_bytes(t.bc, a.ksteps, a.w, a.cin, esize)
                      : t.tpw == -3 ? ig::wide_lds_bytes(t.bc, a.ksteps)
                      : t.tpw == -4 || t.tpw == -5
-                         ? ig::band_lds_bytes(t.bc, a.ksteps, t.pb, a.w, a.cin * esize / 16, band_waves(t.tpw))
+                         ? ig::band_lds_bytes(t.bc, a.ksteps, t.pb, a.wo, a.cin * esize / 16, band_waves(t.tpw), a.sh)
                                    : ig::lds_bytes(t, a.ksteps);
   if (lds > 160 * 1024) fail(-2, "igemm: k-slice table does not fit LDS");
   if ((long long)a.ho * a.wo >= (1ll << 23)) fail(-2, "igemm: more than 2^23 output pixels per image");

@@ -306,27 +306,31 @@ def test_qlinearconv_row_tiles_bit_exact(backend, geom, monkeypatch):
         np.testing.assert_array_equal(run_qconv(backend, c, s, p), ref, err_msg=f"tile {bc},4,-2")
 
 
-def band_tiles(h, w, ci, co, esize=1, waves=8):
+def band_tiles(h, w, ci, co, esize=1, waves=8, stride=1):
     """The band-tile kernel's (channel tile, band height, tile code) triples
-    for a 3x3 stride-1 conv on an h x w map with `waves` waves (8: code -4,
-    16: code -5): channel tiles of 128, 80, 64, 32 or 16 that divide the
-    padded c_out (16 waves: at most 64 unless the epilogue is the plain u8
-    requantize), heights that divide h with at least one 16-pixel block per
-    wave, the input tile within the start-up loads (8192 units) and
-    everything within the 160 KB of LDS."""
+    for a 3x3 padding-1 conv of stride 1 or 2 on an h x w map with `waves`
+    waves (8: code -4, 16: code -5): channel tiles of 128, 80, 64, 32 or 16
+    that divide the padded c_out (16 waves: at most 64 unless the epilogue
+    is the plain u8 requantize), heights that divide the output height with
+    at least one 16-pixel block per wave, the input tile (s (rows - 1) + 3
+    rows of s (wo - 1) + 3 pixels) within the start-up loads (8192 units)
+    and everything within the 160 KB of LDS."""
     top = channel_tile(co)
     pad = -(-co // top) * top
     cu = ci * esize // 16
     ks = -(-9 * ci * esize // 64)
+    ho, wo = (h - 1) // stride + 1, (w - 1) // stride + 1
+    tw = stride * (wo - 1) + 3
     out = []
     for bc in (128, 80, 64, 32, 16):
         if pad % bc or (waves == 16 and bc > 64 and esize != 1):
             continue
-        for rows in range(1, h + 1):
-            if h % rows or rows * w < 16 * waves or (rows + 2) * (w + 2) * cu > 16 * 512:
+        for rows in range(1, ho + 1):
+            tr = stride * (rows - 1) + 3
+            if ho % rows or rows * wo < 16 * waves or tr * tw * cu > 16 * 512:
                 continue
             w_off = -(-(256 + 8 * bc + ks * 16) // 16) * 16
-            lds = w_off + ks * bc * 64 + (rows + 2) * (w + 2) * (cu | 1) * 16 + waves * 16 * (bc + 16)
+            lds = w_off + ks * bc * 64 + tr * tw * (cu | 1) * 16 + waves * 16 * (bc + 16 if bc % 32 == 0 else bc)
             if lds <= 160 * 1024:
                 out.append((bc, rows, -4 if waves == 8 else -5))
     return out
@@ -353,6 +357,28 @@ def test_qlinearconv_band_tiles_bit_exact(backend, geom, x_zp, monkeypatch):
     for bc, rows, code in tiles:
         monkeypatch.setenv("DW_IGEMM_TILE", f"{bc},{rows},{code}")
         np.testing.assert_array_equal(run_qconv(backend, c, 1, 1), ref, err_msg=f"tile {bc},{rows},{code}")
+
+
+@pytest.mark.parametrize("geom,x_zp", [((2, 24, 64, 64, 128), 119), ((1, 31, 63, 32, 64), 128),
+                                       ((1, 36, 48, 64, 80), 7), ((2, 18, 30, 128, 64), 140)])
+def test_qlinearconv_band_tiles_stride2_bit_exact(backend, geom, x_zp, monkeypatch):
+    # The band-tile kernel at stride 2 (2 R + 1 input rows per band, each
+    # row's even columns stored before its odd ones): every channel tile and
+    # band height it accepts, odd input sizes (the last output row and
+    # column read one padding row and column), zero points other than 128.
+    n, h, w, ci, co = geom
+    r = synth.Rng(synth.seed_for(1700 + sum(geom)))
+    c = dict(x=r.integers((n, h, w, ci), 0, 255).astype(np.uint8),
+             w=r.integers((3, 3, ci, co), -127, 127).astype(np.int8),
+             bias=r.integers((co,), -4096, 4096).astype(np.int32),
+             w_scales=r.log_uniform((co,), 1e-3, 1e-2), x_scale=0.02, x_zp=x_zp, y_scale=0.05, y_zp=133)
+    ref = oracle_qconv(c, 2, 1)
+    tiles = band_tiles(h, w, ci, co, stride=2) + band_tiles(h, w, ci, co, waves=16, stride=2)
+    assert tiles
+    print(f"{geom}: {len(tiles)} band tiles", flush=True)
+    for bc, rows, code in tiles:
+        monkeypatch.setenv("DW_IGEMM_TILE", f"{bc},{rows},{code}")
+        np.testing.assert_array_equal(run_qconv(backend, c, 2, 1), ref, err_msg=f"tile {bc},{rows},{code}")
 
 
 def wide_tiles(co):
@@ -620,6 +646,27 @@ def test_conv_f16_band_tiles_identical(backend, monkeypatch, geom):
     for bc, rows, code in tiles:
         monkeypatch.setenv("DW_IGEMM_TILE", f"{bc},{rows},{code}")
         got = run_conv_f16(backend, xh, kh_, bh, 1, 1, ops.ACT_SILU, exact=False)
+        np.testing.assert_array_equal(got, first, err_msg=f"tile {bc},{rows},{code}")
+
+
+@pytest.mark.parametrize("geom", [(2, 20, 40, 32, 64), (1, 31, 47, 16, 32)])
+def test_conv_f16_band_tiles_stride2_identical(backend, monkeypatch, geom):
+    # The fp16 band-tile kernel at stride 2 sums the staged kernel's k-steps
+    # in its order: identical results, odd input sizes included.
+    n, h, w, ci, co = geom
+    r = synth.Rng(synth.seed_for(1800 + sum(geom)))
+    xh = synth.f16_bits(r.normal((n, h, w, ci), 0.0, 1.0))
+    kh_ = synth.f16_bits(r.normal((3, 3, ci, co), 0.0, (1.0 / (9 * ci)) ** 0.5))
+    bh = synth.f16_bits(r.normal((co,), 0.0, 0.1))
+    ref = oracle_conv_f16(xh, kh_, bh, 2, 1, ops.ACT_SILU)
+    monkeypatch.setenv("DW_IGEMM_TILE", "16,4")
+    first = run_conv_f16(backend, xh, kh_, bh, 2, 1, ops.ACT_SILU, exact=False)
+    assert rel_err(f16v(first), f16v(ref)) <= 1e-2
+    tiles = band_tiles(h, w, ci, co, esize=2, stride=2) + band_tiles(h, w, ci, co, esize=2, waves=16, stride=2)
+    assert tiles
+    for bc, rows, code in tiles:
+        monkeypatch.setenv("DW_IGEMM_TILE", f"{bc},{rows},{code}")
+        got = run_conv_f16(backend, xh, kh_, bh, 2, 1, ops.ACT_SILU, exact=False)
         np.testing.assert_array_equal(got, first, err_msg=f"tile {bc},{rows},{code}")
 
 
