@@ -225,10 +225,14 @@ __device__ __forceinline__ void epilogue4(const IgemmArgs& a, const EpiLds& e, c
       p23 = p23 + __builtin_bit_cast(h16x2, rres.y);
     }
     const uint2 out = make_uint2(__builtin_bit_cast(uint32_t, p01), __builtin_bit_cast(uint32_t, p23));
-    if (a.y2 && ch >= a.split)  // a sibling GEMM's second conv: its own output view
-      *reinterpret_cast<uint2*>((uint16_t*)a.y2 + (size_t)p * a.y2_pix_stride + a.y2_c_off + (ch - a.split)) = out;
-    else
-      *reinterpret_cast<uint2*>((uint16_t*)a.y + yo) = out;
+    // a sibling GEMM's second conv stores to its own output view; a channel
+    // tile lies wholly on one side of the split, so the choice is made once
+    // per tile (scalar selects, one store)
+    const bool g2 = a.y2 && __builtin_amdgcn_readfirstlane(ch - cl) >= a.split;
+    uint16_t* const ybase = (uint16_t*)(g2 ? a.y2 : a.y);
+    const int ypix = g2 ? a.y2_pix_stride : a.y_pix_stride;
+    const int ycoff = g2 ? a.y2_c_off - a.split : a.y_c_off;
+    *reinterpret_cast<uint2*>(ybase + (size_t)p * ypix + ycoff + ch) = out;
     if (a.y_up) {
       // the nearest 2x upsample: the same values at the pixel's four pixels
       const int hw = a.ho * a.wo;
