@@ -71,8 +71,9 @@ inline size_t band_lds_bytes(int bc, int ks, int rows, int wo, int cu, int nw, i
   return (size_t)band_xp_off(bc, ks, rows, wo, cu, s) + (size_t)nw * 16 * xpose_row(bc);
 }
 
-template <int ESZ, int BC, int EPV, int NW>
+template <int ESZ, int BC, int EPV, int NW, int S>
 __global__ __launch_bounds__(64 * NW) void igemm_band_kernel(const IgemmArgs a) {
+  static_assert(S == 1 || S == 2, "stride 1 or 2 (both axes)");
   constexpr int CB = BC / 16;
   constexpr int PBC = band_pbc(CB, NW);
   constexpr int kBandWaves = NW;
@@ -85,7 +86,6 @@ __global__ __launch_bounds__(64 * NW) void igemm_band_kernel(const IgemmArgs a) 
 
   const int KSTEPS = a.ksteps, COUTP = a.cout_pad, CIN = a.cin;
   const int W = a.wo, H = a.ho, R = a.band_rows;  // output map and band height
-  const int S = a.sh;                             // stride, 1 or 2 (both axes)
   const int TW = band_tile_w(W, S);
   const int TE = (TW + 1) >> 1;  // stride 2: the tile's even columns, stored first
   const int CU = CIN * ESZ / 16;  // 16-byte units per pixel
@@ -284,7 +284,11 @@ void launch_band_bc(hipStream_t st, const IgemmArgs& a, const TileCfg& t) {
   const int rows = a.band_rows;
   const dim3 grid((unsigned)(a.n * (a.ho / rows) * (a.cout_pad / t.bc)));
   const size_t lds = band_lds_bytes(t.bc, a.ksteps, rows, a.wo, a.cin * ESZ / 16, NW, a.sh);
-  hipLaunchKernelGGL((igemm_band_kernel<ESZ, BC, EPV, NW>), grid, dim3(64 * NW), lds, st, a);
+  // the stride is a template argument: the stride-1 code has no stride-2 terms
+  if (a.sh == 2)
+    hipLaunchKernelGGL((igemm_band_kernel<ESZ, BC, EPV, NW, 2>), grid, dim3(64 * NW), lds, st, a);
+  else
+    hipLaunchKernelGGL((igemm_band_kernel<ESZ, BC, EPV, NW, 1>), grid, dim3(64 * NW), lds, st, a);
 }
 
 // t.tpw: -4 the 8-wave form, -5 the 16-wave form
